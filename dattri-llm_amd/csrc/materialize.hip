@@ -1,0 +1,297 @@
+// K2c: per-sample weight gradient of a linear layer on gfx950 MFMA.
+//
+//   dW[b, o, k] = sum_t g[b, t, o] * a[b, t, k]          (b < B, o < D, k < K)
+//   dW[b, o, K] = sum_t g[b, t, o]                        (only with has_bias)
+//
+// Follows materialize_factors for linear layers,
+// dattri_llm/gradient/ops/materialize.py:114-116 (torch.bmm(g^T, a) flattened
+// to (B, out*in), index o*K + i), with the bias folded as the ones column of
+// preprocess.py:436-437 (so the layout is (B, D, K+1)).
+//
+// Both operands contract over the token axis, which is the slow (row) axis of
+// the row-major captures.  Each stage therefore loads 8x8 (bf16/f16) or 4x4
+// (fp32) blocks with 16-byte row loads, transposes them in registers and
+// stores them into LDS token-contiguous, so the MFMA fragment reads are single
+// 16-byte LDS reads.  A workgroup owns a 128 (o) x 128 (k) output tile of one
+// sample; the fp32 accumulators are converted to the output dtype and staged
+// through LDS so the tile leaves as coalesced 16-byte row stores.
+#include "common.h"
+
+namespace da {
+namespace {
+
+constexpr int kBM = 128;                 // output rows (o) per tile
+constexpr int kBN = 128;                 // output cols (k) per tile
+constexpr int kRowBytes = 128;           // token bytes per LDS row and stage
+constexpr int kLdsRow = kRowBytes + 16;  // padded LDS row
+constexpr int kThreads = 256;
+constexpr int kGroup = 8;
+constexpr int kStageBytes = (kBM + kBN) * kLdsRow;
+
+struct MatArgs {
+  const char* a;
+  const char* g;
+  int64_t batch, tokens, k, d;               // k, d: element widths of a, g
+  int64_t a_bstride, a_tstride;              // bytes
+  int64_t g_bstride, g_tstride;              // bytes
+  char* out;
+  int64_t out_bstride, out_rstride;          // elements
+  int64_t tiles_m, tiles_n;                  // per sample
+};
+
+// Transpose a VEC x VEC block held as VEC rows of one 16-byte chunk each.
+template <int DT>
+__device__ __forceinline__ void transpose_block(const u32x4 (&in)[Elem<DT>::kVec],
+                                                u32x4 (&out)[Elem<DT>::kVec]) {
+  if constexpr (DT == DA_F32) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) out[c] = u32x4{in[0][c], in[1][c], in[2][c], in[3][c]};
+  } else {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int w = c >> 1;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t lo = in[2 * p][w], hi = in[2 * p + 1][w];
+        out[c][p] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+      }
+    }
+  }
+}
+
+template <int DT, int OT, bool kAlignedOut>
+__global__ __launch_bounds__(kThreads, 2) void materialize_tiles(MatArgs m) {
+  constexpr int VEC = Elem<DT>::kVec;           // elements per 16-byte chunk
+  constexpr int ES = Elem<DT>::kBytes;
+  constexpr int TS = kRowBytes / ES;            // tokens per stage
+  constexpr int BLK_T = TS / VEC;               // token blocks per stage
+  constexpr int BLK_C = kBM / VEC;              // column blocks per operand tile
+  constexpr int BLOCKS = BLK_T * BLK_C;         // blocks per operand per stage
+  constexpr int PER_THREAD = BLOCKS / (kThreads / 2);
+  static_assert(PER_THREAD >= 1 && BLOCKS % (kThreads / 2) == 0, "stage/block mismatch");
+
+  __shared__ __attribute__((aligned(16))) char smem[2 * kStageBytes];
+
+  const int64_t ntiles = (int64_t)gridDim.x;
+  const int64_t logical = xcd_remap(blockIdx.x, ntiles);
+  const int64_t per_sample = m.tiles_m * m.tiles_n;
+  const int64_t b = logical / per_sample;
+  const int64_t rem = logical - b * per_sample;
+  // swizzle inside the sample: groups of kGroup row tiles sweep the columns
+  const int64_t per_group = (int64_t)kGroup * m.tiles_n;
+  const int64_t group = rem / per_group;
+  const int64_t first = group * kGroup;
+  const int64_t gsize = min(m.tiles_m - first, (int64_t)kGroup);
+  const int64_t in_group = rem - group * per_group;
+  const int64_t tm = first + in_group % gsize;
+  const int64_t tn = in_group / gsize;
+  const int64_t o0 = tm * kBM, k0 = tn * kBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // This thread stages operand `side` (0: g -> rows o, 1: a -> rows k).
+  const int side = tid / (kThreads / 2);
+  const int tsub = tid % (kThreads / 2);
+  const char* src = side == 0 ? m.g + b * m.g_bstride : m.a + b * m.a_bstride;
+  const int64_t tstride = side == 0 ? m.g_tstride : m.a_tstride;
+  const int64_t width = side == 0 ? m.d : m.k;
+  const int64_t c0 = side == 0 ? o0 : k0;
+
+  u32x4 blk[PER_THREAD][VEC];
+  auto gload = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int bi = tsub + q * (kThreads / 2);
+      const int bt = bi / BLK_C, bc = bi % BLK_C;
+      const int64_t col = c0 + (int64_t)bc * VEC;
+      const bool cin = col < width;
+#pragma unroll
+      for (int r = 0; r < VEC; ++r) {
+        const int64_t t = (int64_t)st * TS + bt * VEC + r;
+        blk[q][r] = (cin && t < m.tokens) ? ld16(src + t * tstride + col * ES) : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    char* base = smem + buf * kStageBytes + (side == 0 ? 0 : kBM * kLdsRow);
+#pragma unroll
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int bi = tsub + q * (kThreads / 2);
+      const int bt = bi / BLK_C, bc = bi % BLK_C;
+      u32x4 tr[VEC];
+      transpose_block<DT>(blk[q], tr);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) st16(base + (bc * VEC + c) * kLdsRow + bt * 16, tr[c]);
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
+
+  const int nst = (int)((m.tokens + TS - 1) / TS);
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int frow = lane & 31, fhalf = lane >> 5;
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) gload(st + 1);
+    const char* base = smem + buf * kStageBytes;
+#pragma unroll
+    for (int kg = 0; kg < kRowBytes / 32; ++kg) {
+      u32x4 fa[2], fb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        fa[x] = ld16(base + (64 * wm + 32 * x + frow) * kLdsRow + 32 * kg + 16 * fhalf);
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        fb[y] = ld16(base + (kBM + 64 * wn + 32 * y + frow) * kLdsRow + 32 * kg + 16 * fhalf);
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) Mfma32<DT>::mma(acc[x][y], fa[x], fb[y]);
+    }
+    if (st + 1 < nst) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: each wave stages its 64x64 output block (output dtype) in LDS,
+  // then writes whole rows.  The loop above ended with a barrier, so the
+  // stage buffers are free.
+  constexpr int OS = Elem<OT>::kBytes;
+  constexpr int ROWB = 64 * OS;                   // bytes of one staged row
+  char* wbuf = smem + wave * (64 * ROWB);
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * x + acc_row(r, lane), col = 32 * y + acc_col(lane);
+        Elem<OT>::store(wbuf, (int64_t)row * 64 + col, acc[x][y][r]);
+      }
+  __syncthreads();
+  const int64_t orow0 = o0 + 64 * wm, ocol0 = k0 + 64 * wn;
+  char* obase = m.out + (b * m.out_bstride) * OS;
+  if constexpr (kAlignedOut) {
+    constexpr int CH = ROWB / 16;                 // 16-byte chunks per row
+    constexpr int ROWS_PER_PASS = 64 / CH;
+#pragma unroll
+    for (int pass = 0; pass < 64 / ROWS_PER_PASS; ++pass) {
+      const int row = pass * ROWS_PER_PASS + lane / CH, ch = lane % CH;
+      const int64_t orow = orow0 + row;
+      const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
+      if (orow < m.d && ocol < m.k)
+        st16(obase + (orow * m.out_rstride + ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
+    }
+  } else {
+    for (int e = lane; e < 64 * 64; e += 64) {
+      const int row = e >> 6, col = e & 63;
+      const int64_t orow = orow0 + row, ocol = ocol0 + col;
+      if (orow < m.d && ocol < m.k) {
+        if constexpr (OS == 4)
+          ((uint32_t*)obase)[orow * m.out_rstride + ocol] = ((const uint32_t*)wbuf)[e];
+        else
+          ((uint16_t*)obase)[orow * m.out_rstride + ocol] = ((const uint16_t*)wbuf)[e];
+      }
+    }
+  }
+}
+
+// Bias column dW[b, o, K] = sum_t g[b, t, o]: one thread per (b, o).
+template <int DT, int OT>
+__global__ void bias_column(const char* g, int64_t batch, int64_t tokens, int64_t d,
+                            int64_t g_bstride, int64_t g_tstride, char* out, int64_t out_bstride,
+                            int64_t out_rstride, int64_t kcol) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (o >= d) return;
+  const char* src = g + b * g_bstride;
+  float s = 0.f;
+  for (int64_t t = 0; t < tokens; ++t) s += Elem<DT>::load(src + t * g_tstride, o);
+  Elem<OT>::store(out, b * out_bstride + o * out_rstride + kcol, s);
+}
+
+template <int DT, int OT>
+int launch(const MatArgs& m, int has_bias, hipStream_t st) {
+  const int64_t ntiles = m.batch * m.tiles_m * m.tiles_n;
+  if (ntiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_materialize_linear: too many tiles");
+  const bool aligned = ((m.out_rstride * Elem<OT>::kBytes) % 16 == 0) &&
+                       ((m.out_bstride * Elem<OT>::kBytes) % 16 == 0) && (((uintptr_t)m.out & 15) == 0);
+  if (ntiles > 0) {
+    if (aligned)
+      materialize_tiles<DT, OT, true><<<(unsigned)ntiles, kThreads, 0, st>>>(m);
+    else
+      materialize_tiles<DT, OT, false><<<(unsigned)ntiles, kThreads, 0, st>>>(m);
+    int rc = check_launch("da_materialize_linear(tiles)");
+    if (rc) return rc;
+  }
+  if (has_bias) {
+    dim3 grid((unsigned)((m.d + 255) / 256), (unsigned)m.batch);
+    bias_column<DT, OT><<<grid, 256, 0, st>>>(m.g, m.batch, m.tokens, m.d, m.g_bstride, m.g_tstride,
+                                              m.out, m.out_bstride, m.out_rstride, m.k);
+    return check_launch("da_materialize_linear(bias)");
+  }
+  return DA_OK;
+}
+
+}  // namespace
+}  // namespace da
+
+extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch,
+                                     int64_t tokens, int64_t K, int64_t D, int64_t a_bstride,
+                                     int64_t a_tstride, int64_t g_bstride, int64_t g_tstride,
+                                     int has_bias, void* out, int out_dtype, int64_t out_bstride,
+                                     int64_t out_rstride, void* stream) {
+  using namespace da;
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype))
+    return set_error(DA_ERR_INVALID, "da_materialize_linear: bad dtype");
+  if (batch < 0 || tokens < 0 || K < 0 || D < 0)
+    return set_error(DA_ERR_INVALID, "da_materialize_linear: negative size");
+  if (batch == 0 || K == 0 || D == 0) return DA_OK;
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if ((K * es) % 16 || (D * es) % 16)
+    return set_error(DA_ERR_INVALID, "da_materialize_linear: K and D must be multiples of %lld",
+                     (long long)(16 / es));
+  if (!a || !g || !out) return set_error(DA_ERR_INVALID, "da_materialize_linear: NULL pointer");
+  if (((uintptr_t)a | (uintptr_t)g) & 15)
+    return set_error(DA_ERR_INVALID, "da_materialize_linear: inputs must be 16-byte aligned");
+  if (((a_bstride * es) | (a_tstride * es) | (g_bstride * es) | (g_tstride * es)) % 16)
+    return set_error(DA_ERR_INVALID, "da_materialize_linear: strides must be multiples of 16 bytes");
+  if (out_rstride < K + (has_bias ? 1 : 0))
+    return set_error(DA_ERR_INVALID, "da_materialize_linear: out row stride too small");
+  if (tokens == 0) return set_error(DA_ERR_INVALID, "da_materialize_linear: tokens must be >= 1");
+  MatArgs m;
+  m.a = (const char*)a;
+  m.g = (const char*)g;
+  m.batch = batch;
+  m.tokens = tokens;
+  m.k = K;
+  m.d = D;
+  m.a_bstride = a_bstride * es;
+  m.a_tstride = a_tstride * es;
+  m.g_bstride = g_bstride * es;
+  m.g_tstride = g_tstride * es;
+  m.out = (char*)out;
+  m.out_bstride = out_bstride;
+  m.out_rstride = out_rstride;
+  m.tiles_m = (D + kBM - 1) / kBM;
+  m.tiles_n = (K + kBN - 1) / kBN;
+  hipStream_t st = (hipStream_t)stream;
+#define DA_MAT_CASE(DT)                                                         \
+  switch (out_dtype) {                                                          \
+    case DA_F32: return launch<DT, DA_F32>(m, has_bias, st);                    \
+    case DA_BF16: return launch<DT, DA_BF16>(m, has_bias, st);                  \
+    default: return launch<DT, DA_F16>(m, has_bias, st);                        \
+  }
+  switch (dtype) {
+    case DA_BF16: DA_MAT_CASE(DA_BF16)
+    case DA_F16: DA_MAT_CASE(DA_F16)
+    default: DA_MAT_CASE(DA_F32)
+  }
+#undef DA_MAT_CASE
+}

@@ -1,0 +1,356 @@
+"""numpy restatement of dattri-llm's gradient-scoring ops (TEST INFRASTRUCTURE ONLY).
+
+Reference: TRAIS-Lab/dattri-llm 0.1.0, paths relative to its repository root.
+Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+
+Each function below says which reference lines it restates and how it is
+pinned (tests/test_oracle.py):
+
+=============================  =============================================  ===========================================
+function                       reference                                      pinned by
+=============================  =============================================  ===========================================
+cross_gram_factorized          gradient/ops/dot.py:115-118                    brute-force loops; torch autograd per-sample
+                                                                              grads (linear layer, with bias)
+cross_gram_materialized        gradient/ops/dot.py:110-114                    equals the factorized form; autograd
+cross_gram                     gradient/ops/dot.py:36-118 (linear, norm)      the two above + norm branch vs autograd
+materialize_linear             gradient/ops/materialize.py:114-116,           torch autograd weight.grad (+ bias.grad)
+                               preprocess.py:436-437                          flattened o*K+i layout
+rms_x_hat / layer_norm_x_hat   gradient/ops/norm.py:25-41, :10-22             torch.nn.functional.rms_norm / layer_norm
+                                                                              (eps=None -> machine eps special case)
+norm_weight_grad               materialize.py:96-98 + preprocess.py:366-384   autograd of nn.RMSNorm / nn.LayerNorm
+                               + norm.py:95-110
+project                        gradient/ops/projection.py:363-370            ones-column identity: addmm(bias) ==
+                                                                              cat([x,1]) @ P
+project_outer                  hooks/hooks.py:631-648, projection.py:423-489  Kronecker identity
+                                                                              vec(P_out^T dW P_in) vs materialize_linear
+score_gemm                     gradient/ops/dot.py:114, :505, :599-604        brute-force loops
+cost rules                     dot.py:728-753, projection.py:846-899          the reference's own known-answer tables
+moe_router_topk                transformers MixtralTopKRouter.forward         torch.topk(torch.softmax(x.float()))
+                               (installed transformers, a library routine)
+moe_segments                   hooks/override_layers/fused_experts.py:219-228 torch.where(one_hot(idx).permute(2,1,0)[e])
+moe_regroup_dense              hooks/routing.py:71-86                         explicit scatter check
+moe_segment_ghost              dense-with-zeros cross_gram (routing.py:17-23) equals cross_gram on the regrouped
+                                                                              zero-filled (B, T, d) factors
+=============================  =============================================  ===========================================
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "cross_gram",
+    "cross_gram_factorized",
+    "cross_gram_materialized",
+    "layer_norm_x_hat",
+    "materialize_linear",
+    "maybe_materialize_projected",
+    "maybe_use_materialized_gram",
+    "maybe_use_materialized_norm",
+    "moe_regroup_dense",
+    "moe_router_topk",
+    "moe_segment_ghost",
+    "moe_segments",
+    "norm_weight_grad",
+    "preprocess",
+    "project",
+    "project_outer",
+    "rms_x_hat",
+    "score_gemm",
+    "should_materialize",
+    "BF16_EPS",
+    "F32_EPS",
+    "F16_EPS",
+    "bf16_round",
+]
+
+# torch.finfo(dtype).eps, the RMSNorm eps=None special case (norm.py:38-39).
+F32_EPS = float(np.finfo(np.float32).eps)  # 2**-23
+F16_EPS = float(np.finfo(np.float16).eps)  # 2**-10
+BF16_EPS = 2.0**-7
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bfloat16 (round-to-nearest-even), returned as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def _with_ones(a: np.ndarray) -> np.ndarray:
+    """Linear bias fold: append a ones column (preprocess.py:436-437)."""
+    return np.concatenate([a, np.ones(a.shape[:-1] + (1,), dtype=a.dtype)], axis=-1)
+
+
+def _to_3d(x: np.ndarray) -> np.ndarray:
+    """(B, D) -> (B, 1, D) (preprocess.py:447-455)."""
+    return x[:, None, :] if x.ndim == 2 else x
+
+
+# ---------------------------------------------------------------------------
+# cross-gram
+# ---------------------------------------------------------------------------
+
+
+def cross_gram_factorized(a1, g1, a2, g2, bias: bool = False) -> np.ndarray:
+    """Ghost route of cross_gram (dot.py:115-118): K_a = A1 A2^T, K_g = G1 G2^T
+    over the flattened (B*S) rows, Hadamard product summed per sample block.
+    ``bias`` folds a ones column into both activations first."""
+    a1, g1, a2, g2 = (_to_3d(x) for x in (a1, g1, a2, g2))
+    if bias:
+        a1, a2 = _with_ones(a1), _with_ones(a2)
+    b1, s1, k = a1.shape
+    b2, s2, _ = a2.shape
+    d = g1.shape[-1]
+    ka = a1.reshape(b1 * s1, k) @ a2.reshape(b2 * s2, k).T
+    kg = g1.reshape(b1 * s1, d) @ g2.reshape(b2 * s2, d).T
+    return (ka * kg).reshape(b1, s1, b2, s2).sum(axis=(1, 3))
+
+
+def cross_gram_materialized(a1, g1, a2, g2, bias: bool = False) -> np.ndarray:
+    """Materialized route of cross_gram (dot.py:110-114): per-sample
+    ``bmm(a^T, g)`` flattened, then one GEMM."""
+    a1, g1, a2, g2 = (_to_3d(x) for x in (a1, g1, a2, g2))
+    if bias:
+        a1, a2 = _with_ones(a1), _with_ones(a2)
+    m1 = np.matmul(a1.transpose(0, 2, 1), g1).reshape(a1.shape[0], -1)
+    m2 = np.matmul(a2.transpose(0, 2, 1), g2).reshape(a2.shape[0], -1)
+    return m1 @ m2.T
+
+
+def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto", bias: bool = False):
+    """cross_gram (dot.py:36-118) on preprocessed factors, for the linear and
+    norm families.  Norm layers contract positions first (dot.py:80-86)."""
+    if layer_type in NORM_TYPES:
+        grad1 = (_to_3d(a1) * _to_3d(g1)).sum(axis=1)
+        grad2 = (_to_3d(a2) * _to_3d(g2)).sum(axis=1)
+        return grad1 @ grad2.T
+    a1_3, a2_3 = _to_3d(a1), _to_3d(a2)
+    b1, s, k = a1_3.shape
+    d = _to_3d(g1).shape[-1]
+    if mode == "auto":
+        mode = (
+            "materialized"
+            if maybe_use_materialized_gram(b1, a2_3.shape[0], s, k + int(bias), d)
+            else "factorized"
+        )
+    if mode == "materialized":
+        return cross_gram_materialized(a1, g1, a2, g2, bias)
+    return cross_gram_factorized(a1, g1, a2, g2, bias)
+
+
+# ---------------------------------------------------------------------------
+# materialization and norm preprocessing
+# ---------------------------------------------------------------------------
+
+
+def materialize_linear(a, g, bias: bool = False) -> np.ndarray:
+    """Per-sample weight gradient of a linear layer, ``bmm(g^T, a)`` flattened
+    to (B, D*K) with index o*K + i (materialize.py:114-116); with ``bias`` the
+    activation carries the ones column so the layout is (B, D*(K+1))."""
+    a, g = _to_3d(a), _to_3d(g)
+    if bias:
+        a = _with_ones(a)
+    return np.matmul(g.transpose(0, 2, 1), a).reshape(a.shape[0], -1)
+
+
+NORM_TYPES = frozenset(
+    {
+        "nn.LayerNorm",
+        "nn.RMSNorm",
+        "nn.GroupNorm",
+        "nn.InstanceNorm1d",
+        "nn.InstanceNorm2d",
+        "nn.InstanceNorm3d",
+    }
+)
+
+
+def rms_x_hat(x, eps) -> np.ndarray:
+    """x * rsqrt(mean(x^2) + eps) over the last axis (norm.py:25-41)."""
+    mean_sq = (x * x).mean(axis=-1, keepdims=True)
+    return x / np.sqrt(mean_sq + eps)
+
+
+def layer_norm_x_hat(x, eps) -> np.ndarray:
+    """(x - mu) / sqrt(var + eps), biased variance, last axis (norm.py:10-22)."""
+    mu = x.mean(axis=-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps)
+
+
+def preprocess(a, g, layer_type: str, module_kwargs: dict | None, include_bias: bool = True):
+    """preprocess_factors (preprocess.py:301-439) for linear, RMSNorm and
+    LayerNorm over the last axis.  ``module_kwargs['eps'] is None`` must be
+    resolved by the caller to the raw activation dtype's machine eps."""
+    if module_kwargs is None:
+        return a, g
+    has_bias = module_kwargs["has_bias"] and include_bias
+    if layer_type in ("nn.RMSNorm", "nn.LayerNorm"):
+        fn = rms_x_hat if layer_type == "nn.RMSNorm" else layer_norm_x_hat
+        x_hat = fn(a, module_kwargs["eps"])
+        if has_bias:  # norm.py:95-110
+            return (
+                np.concatenate([x_hat, np.ones_like(x_hat)], axis=-1),
+                np.concatenate([g, g], axis=-1),
+            )
+        return x_hat, g
+    if layer_type in LINEAR_TYPES and has_bias:
+        return _with_ones(a), g
+    return a, g
+
+
+LINEAR_TYPES = frozenset(
+    {
+        "nn.Linear",
+        "nn.Bilinear",
+        "nn.NonDynamicallyQuantizableLinear",
+        "transformers.pytorch_utils.Conv1D",
+    }
+)
+
+
+def norm_weight_grad(x, g, layer_type: str, eps: float, has_bias: bool = False) -> np.ndarray:
+    """Per-sample norm weight gradient: preprocess then ``(a*g).sum(1)``
+    (materialize.py:96-98).  Returns (B, d), or (B, 2d) = [dgamma, dbeta]."""
+    a, gg = preprocess(x, g, layer_type, {"has_bias": has_bias, "eps": eps})
+    return (_to_3d(a) * _to_3d(gg)).sum(axis=1)
+
+
+# ---------------------------------------------------------------------------
+# projection
+# ---------------------------------------------------------------------------
+
+
+def project(x, matrix, bias_row=None) -> np.ndarray:
+    """ProjectionMatrix.__call__ (projection.py:363-370): ``x @ P`` over the
+    last axis, plus the bias row broadcast when the layer has a bias."""
+    flat = x.reshape(-1, x.shape[-1])
+    out = flat @ matrix
+    if bias_row is not None:
+        out = out + bias_row[None, :]
+    return out.reshape(*x.shape[:-1], matrix.shape[1])
+
+
+def project_outer(a, g, p_in, p_out, bias: bool = False) -> np.ndarray:
+    """Capture-time LoGRA projection then materialization
+    (hooks.py:631-648): a_p = a @ P_in (+ bias row, P_in is (K+1, k_a) when
+    ``bias``), g_p = g @ P_out, result ``bmm(g_p^T, a_p)`` flattened to
+    (B, k_g*k_a) with index o*k_a + i."""
+    if bias:
+        a_p = project(a, p_in[:-1], p_in[-1])
+    else:
+        a_p = project(a, p_in)
+    g_p = project(g, p_out)
+    return materialize_linear(a_p, g_p)
+
+
+# ---------------------------------------------------------------------------
+# score GEMM
+# ---------------------------------------------------------------------------
+
+
+def score_gemm(m1_list, m2_list) -> np.ndarray:
+    """Dense-side layer products summed over layers (dot.py:114, :505,
+    :599-604): sum_L M1_L @ M2_L^T."""
+    total = None
+    for m1, m2 in zip(m1_list, m2_list, strict=True):
+        part = m1.reshape(m1.shape[0], -1) @ m2.reshape(m2.shape[0], -1).T
+        total = part if total is None else total + part
+    return total
+
+
+# ---------------------------------------------------------------------------
+# cost rules (exact restatements; pinned by the reference's known-answer tests)
+# ---------------------------------------------------------------------------
+
+
+def maybe_use_materialized_gram(b1, b2, s, k, d, kappa: float = 1.0) -> bool:
+    """dot.py:728-745."""
+    cost_f = b1 * b2 * s * s * (d + k)
+    cost_m = (b1 + b2) * s * d * k + b1 * b2 * d * k
+    return kappa * cost_f >= cost_m
+
+
+def maybe_use_materialized_norm(s, k, d) -> bool:
+    """dot.py:748-753."""
+    return s * (d + k) >= d * k
+
+
+def maybe_materialize_projected(seq_len, k_a, k_g, kappa: float = 1.0) -> bool:
+    """projection.py:846-874."""
+    denom = k_a + k_g
+    if denom <= 0:
+        return False
+    return seq_len >= kappa * (k_a * k_g) / denom
+
+
+def should_materialize(capture_style, seq_len, k_a, k_g) -> bool:
+    """projection.py:877-899."""
+    if capture_style == "factorized":
+        return False
+    if capture_style == "materialized":
+        return True
+    if capture_style != "auto":
+        raise ValueError(f"capture_style must be one of ('factorized', 'materialized', 'auto'), got {capture_style!r}.")
+    return maybe_materialize_projected(seq_len, k_a, k_g)
+
+
+# ---------------------------------------------------------------------------
+# MoE routing
+# ---------------------------------------------------------------------------
+
+
+def _softmax_f32(logits: np.ndarray) -> np.ndarray:
+    x = logits.astype(np.float32)
+    m = x.max(axis=-1, keepdims=True)
+    e = np.exp(x - m, dtype=np.float32)
+    return e / e.sum(axis=-1, keepdims=True, dtype=np.float32)
+
+
+def moe_router_topk(logits, k: int):
+    """Mixtral top-k router (transformers MixtralTopKRouter.forward): top-k of
+    softmax(logits.float()), weights renormalised over the k.  Indices are
+    ordered by descending probability, ties broken toward the lower expert
+    index.  Returns (weights (N,k) float32, indices (N,k) int64)."""
+    probs = _softmax_f32(np.asarray(logits))
+    n, e = probs.shape
+    # stable sort on (-prob) keeps the lower index first among equal values
+    order = np.argsort(-probs, axis=-1, kind="stable")[:, :k]
+    top = np.take_along_axis(probs, order, axis=-1)
+    weights = top / top.sum(axis=-1, keepdims=True, dtype=np.float32)
+    return weights.astype(np.float32), order.astype(np.int64)
+
+
+def moe_segments(top_idx, n_experts: int):
+    """Per-expert routed rows in the reference loop's order
+    (fused_experts.py:219-228): ``torch.where(one_hot(idx).permute(2,1,0)[e])``
+    enumerates (top_k_pos, token_idx) slot-major, token ascending.
+    Returns a list of (top_k_pos, token_idx) int64 arrays, one per expert."""
+    top_idx = np.asarray(top_idx)
+    out = []
+    for e in range(n_experts):
+        mask = (top_idx == e).T  # (k, tokens): mask[pos, token]
+        pos, tok = np.nonzero(mask)  # row-major: pos-major, token ascending
+        out.append((pos.astype(np.int64), tok.astype(np.int64)))
+    return out
+
+
+def moe_regroup_dense(rows, token_idx, batch: int, tokens: int) -> np.ndarray:
+    """RowLayout.regroup (routing.py:71-86): scatter routed rows back to a
+    zero-filled (B, T, d) tensor at their (sample, position)."""
+    out = np.zeros((batch, tokens) + rows.shape[1:], dtype=rows.dtype)
+    tok = np.asarray(token_idx)
+    out[tok // tokens, tok % tokens] = rows
+    return out
+
+
+def moe_segment_ghost(a1, g1, tok1, a2, g2, tok2, batch1, batch2, tokens1, tokens2, bias=False):
+    """One expert's factorized cross-gram under the reference's layout:
+    regroup both sides' routed rows to zero-filled (B, T, d) factors
+    (routing.py:71-86) and apply the ghost route (dot.py:115-118)."""
+    A1 = moe_regroup_dense(a1, tok1, batch1, tokens1)
+    G1 = moe_regroup_dense(g1, tok1, batch1, tokens1)
+    A2 = moe_regroup_dense(a2, tok2, batch2, tokens2)
+    G2 = moe_regroup_dense(g2, tok2, batch2, tokens2)
+    return cross_gram_factorized(A1, G1, A2, G2, bias)
