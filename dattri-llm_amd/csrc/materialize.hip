@@ -220,7 +220,9 @@ template <int DT, int OT>
 int launch(const MatArgs& m, int has_bias, hipStream_t st) {
   const int64_t ntiles = m.batch * m.tiles_m * m.tiles_n;
   if (ntiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_materialize_linear: too many tiles");
-  const bool aligned = ((m.out_rstride * Elem<OT>::kBytes) % 16 == 0) &&
+  // 16-byte output stores need whole output chunks inside every row.
+  const bool aligned = (m.k % (16 / Elem<OT>::kBytes) == 0) &&
+                       ((m.out_rstride * Elem<OT>::kBytes) % 16 == 0) &&
                        ((m.out_bstride * Elem<OT>::kBytes) % 16 == 0) && (((uintptr_t)m.out & 15) == 0);
   if (ntiles > 0) {
     if (aligned)

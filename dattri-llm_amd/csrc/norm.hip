@@ -1,0 +1,385 @@
+// K3b: per-sample weight gradient of token norm layers (RMSNorm, LayerNorm).
+//
+//   x_hat[b,t,:] = x * rsqrt(mean(x^2) + eps)                 (RMSNorm)
+//                = (x - mean) * rsqrt(var + eps)              (LayerNorm, biased var)
+//   dgamma[b,:]  = sum_t x_hat[b,t,:] * g[b,t,:]
+//   dbeta[b,:]   = sum_t g[b,t,:]                             (has_bias: out is [dgamma, dbeta])
+//
+// Follows preprocess_factors' norm branches, dattri_llm/gradient/ops/preprocess.py:366-384,
+// with _compute_rms_x_hat / _compute_layer_norm_x_hat (gradient/ops/norm.py:25-41,
+// :10-22), the bias augmentation of norm.py:95-110, and the token contraction of
+// materialize_factors, gradient/ops/materialize.py:96-98.  The reference makes
+// 3-4 elementwise passes plus a concatenation; here one pass reads x and g once.
+//
+// One wave owns one token row at a time: the row lives in registers
+// (kQ 16-byte chunks per lane), the mean square is a wave reduction, and the
+// wave accumulates x_hat*g (and g) for its lanes' features across the rows it
+// visits.  The four waves of a workgroup combine through LDS and write one fp32
+// partial per (sample, token chunk); a second kernel sums the chunks in order.
+#include "common.h"
+
+namespace da {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kRowsPerWG = 32;  // token rows per workgroup
+
+struct NormArgs {
+  const char* x;
+  const char* g;
+  int64_t batch, tokens, d;
+  int64_t x_bstride, x_tstride, g_bstride, g_tstride;  // bytes
+  int kind;                                            // 0 RMSNorm, 1 LayerNorm
+  float eps;
+  int has_bias;
+  int64_t chunks;                                      // token chunks per sample
+  float* partial;                                      // [batch][chunks][(1+bias)*d]
+};
+
+template <int DT>
+__device__ __forceinline__ float elem_of(const u32x4& v, int e) {
+  if constexpr (DT == DA_F32) return __uint_as_float(v[e]);
+  else return Elem<DT>::from_bits((e & 1) ? (v[e >> 1] >> 16) : (v[e >> 1] & 0xffffu));
+}
+
+template <int DT, int kQ, bool kBias>
+__global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
+  constexpr int VEC = Elem<DT>::kVec;
+  extern __shared__ float lds[];  // (1+bias) * d floats: one wave's sums at a time
+
+  const int64_t b = blockIdx.y, chunk = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t nchunk16 = a.d / VEC;  // 16-byte chunks per row
+  const float inv_d = 1.f / (float)a.d;
+
+  float dg[kQ][VEC], db[kBias ? kQ : 1][VEC];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dg[q][e] = 0.f;
+#pragma unroll
+  for (int q = 0; q < (kBias ? kQ : 1); ++q)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) db[q][e] = 0.f;
+
+  const int64_t t_begin = chunk * kRowsPerWG;
+  const int64_t t_end = min(t_begin + kRowsPerWG, a.tokens);
+  for (int64_t t = t_begin + wave; t < t_end; t += kWaves) {
+    const char* xr = a.x + b * a.x_bstride + t * a.x_tstride;
+    const char* gr = a.g + b * a.g_bstride + t * a.g_tstride;
+    u32x4 vx[kQ], vg[kQ];  // the row stays packed; unpacked on use
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int64_t c = lane + (int64_t)q * kWave;
+      const bool in = c < nchunk16;
+      vx[q] = in ? ld16(xr + c * 16) : u32x4{0, 0, 0, 0};
+      vg[q] = in ? ld16(gr + c * 16) : u32x4{0, 0, 0, 0};
+    }
+    float mean = 0.f;
+    if (a.kind == 1) {
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += elem_of<DT>(vx[q], e);
+      mean = wave_sum(s) * inv_d;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const bool in = lane + (int64_t)q * kWave < nchunk16;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float c = in ? elem_of<DT>(vx[q], e) - mean : 0.f;
+        ss += c * c;
+      }
+    }
+    const float rstd = 1.f / sqrtf(wave_sum(ss) * inv_d + a.eps);
+    // Re-read the packed row rather than keeping kQ*VEC unpacked floats live
+    // across the reductions (halves register pressure, doubles occupancy).
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) asm volatile("" : "+v"(vx[q]));
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float gv = elem_of<DT>(vg[q], e);
+        dg[q][e] += (elem_of<DT>(vx[q], e) - mean) * rstd * gv;
+        if constexpr (kBias) db[q][e] += gv;
+      }
+  }
+
+  // Combine waves one at a time through LDS (one wave's sums fit), then wave 0
+  // writes the workgroup's partial.
+  const int64_t width = (1 + a.has_bias) * a.d;
+  for (int w = 1; w < kWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) {
+        const int64_t c = lane + (int64_t)q * kWave;
+        if (c < nchunk16)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            lds[c * VEC + e] = dg[q][e];
+            if constexpr (kBias) lds[a.d + c * VEC + e] = db[q][e];
+          }
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) {
+        const int64_t c = lane + (int64_t)q * kWave;
+        if (c < nchunk16)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            dg[q][e] += lds[c * VEC + e];
+            if constexpr (kBias) db[q][e] += lds[a.d + c * VEC + e];
+          }
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+    float* dst = a.partial + (b * a.chunks + chunk) * width;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int64_t c = lane + (int64_t)q * kWave;
+      if (c < nchunk16)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          dst[c * VEC + e] = dg[q][e];
+          if constexpr (kBias) dst[a.d + c * VEC + e] = db[q][e];
+        }
+    }
+  }
+}
+
+template <int OT>
+__global__ void norm_grad_reduce(const float* __restrict__ partial, int64_t batch, int64_t chunks,
+                                 int64_t width, char* out, int64_t out_bstride) {
+  const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (f >= width) return;
+  const float* p = partial + b * chunks * width + f;
+  float s = 0.f;
+  for (int64_t c = 0; c < chunks; ++c) s += p[c * width];
+  Elem<OT>::store(out, b * out_bstride + f, s);
+}
+
+// x_hat rows for the preprocess API: one wave per row, same math as above.
+template <int DT, int OT, int kQ>
+__global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_t rows, int64_t d,
+                                                           int64_t x_rstride, int kind, float eps,
+                                                           char* out, int64_t out_rstride) {
+  constexpr int VEC = Elem<DT>::kVec;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t nchunk16 = d / VEC;
+  const float inv_d = 1.f / (float)d;
+  float xv[kQ][VEC];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const int64_t c = lane + (int64_t)q * kWave;
+    const u32x4 v = c < nchunk16 ? ld16(x + row * x_rstride + c * 16) : u32x4{0, 0, 0, 0};
+    unpack16<DT>(v, xv[q]);
+  }
+  float mean = 0.f;
+  if (kind == 1) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += xv[q][e];
+    mean = wave_sum(s) * inv_d;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const bool in = lane + (int64_t)q * kWave < nchunk16;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float c = in ? xv[q][e] - mean : 0.f;
+      ss += c * c;
+    }
+  }
+  const float rstd = 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const int64_t c = lane + (int64_t)q * kWave;
+    if (c < nchunk16)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        Elem<OT>::store(out, row * out_rstride + c * VEC + e, (xv[q][e] - mean) * rstd);
+  }
+}
+
+int pick_q(int64_t d, int64_t vec) {
+  const int64_t per_lane = (d / vec + kWave - 1) / kWave;
+  if (per_lane <= 1) return 1;
+  if (per_lane <= 2) return 2;
+  if (per_lane <= 4) return 4;
+  if (per_lane <= 8) return 8;
+  if (per_lane <= 16) return 16;
+  return -1;
+}
+
+template <int DT, int OT>
+int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t st) {
+  const int64_t width = (1 + a.has_bias) * a.d;
+  const size_t lds = (size_t)width * sizeof(float);
+  dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
+#define DA_NORM_Q(Q)                                              \
+  if (a.has_bias)                                                 \
+    norm_grad_chunks<DT, Q, true><<<grid, kThreads, lds, st>>>(a); \
+  else                                                            \
+    norm_grad_chunks<DT, Q, false><<<grid, kThreads, lds, st>>>(a)
+  switch (q) {
+    case 1: DA_NORM_Q(1); break;
+    case 2: DA_NORM_Q(2); break;
+    case 4: DA_NORM_Q(4); break;
+    case 8: DA_NORM_Q(8); break;
+    default: DA_NORM_Q(16); break;
+  }
+#undef DA_NORM_Q
+  int rc = check_launch("da_norm_weight_grad(chunks)");
+  if (rc) return rc;
+  dim3 g2((unsigned)((width + 255) / 256), (unsigned)a.batch);
+  norm_grad_reduce<OT><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, (char*)out,
+                                           out_bstride);
+  return check_launch("da_norm_weight_grad(reduce)");
+}
+
+template <int DT, int OT>
+int launch_xhat(const void* x, int64_t rows, int64_t d, int64_t x_rstride, int kind, float eps,
+                void* out, int64_t out_rstride, int q, hipStream_t st) {
+  const unsigned blocks = (unsigned)((rows + kWaves - 1) / kWaves);
+  const int64_t xs = x_rstride * Elem<DT>::kBytes;
+#define DA_XHAT_Q(Q)                                                                       \
+  norm_xhat_rows<DT, OT, Q><<<blocks, kThreads, 0, st>>>((const char*)x, rows, d, xs, kind, \
+                                                         eps, (char*)out, out_rstride)
+  switch (q) {
+    case 1: DA_XHAT_Q(1); break;
+    case 2: DA_XHAT_Q(2); break;
+    case 4: DA_XHAT_Q(4); break;
+    case 8: DA_XHAT_Q(8); break;
+    default: DA_XHAT_Q(16); break;
+  }
+#undef DA_XHAT_Q
+  return check_launch("da_norm_xhat");
+}
+
+int check_common(const char* who, int dtype, int out_dtype, int64_t d, int kind, int* q) {
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype))
+    return set_error(DA_ERR_INVALID, "%s: bad dtype", who);
+  if (kind != 0 && kind != 1) return set_error(DA_ERR_INVALID, "%s: kind must be 0 (RMSNorm) or 1 (LayerNorm)", who);
+  const int64_t vec = 16 / (int64_t)elem_bytes(dtype);
+  if (d <= 0 || d % vec)
+    return set_error(DA_ERR_INVALID, "%s: d=%lld must be a positive multiple of %lld", who,
+                     (long long)d, (long long)vec);
+  *q = pick_q(d, vec);
+  if (*q < 0)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: d=%lld exceeds %lld features per row", who,
+                     (long long)d, (long long)(vec * kWave * 16));
+  return DA_OK;
+}
+
+}  // namespace
+}  // namespace da
+
+extern "C" {
+
+int da_norm_weight_grad_workspace(int64_t batch, int64_t tokens, int64_t d, int has_bias,
+                                  size_t* bytes) {
+  if (batch < 0 || tokens < 0 || d < 0 || !bytes)
+    return da::set_error(DA_ERR_INVALID, "da_norm_weight_grad_workspace: bad arguments");
+  const int64_t chunks = (tokens + da::kRowsPerWG - 1) / da::kRowsPerWG;
+  *bytes = (size_t)(batch * chunks * (1 + (has_bias ? 1 : 0)) * d) * sizeof(float);
+  return DA_OK;
+}
+
+int da_norm_weight_grad(const void* x, const void* g, int dtype, int64_t batch, int64_t tokens,
+                        int64_t d, int64_t x_bstride, int64_t x_tstride, int64_t g_bstride,
+                        int64_t g_tstride, int kind, float eps, int has_bias, void* out,
+                        int out_dtype, int64_t out_bstride, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  using namespace da;
+  int q;
+  int rc = check_common("da_norm_weight_grad", dtype, out_dtype, d, kind, &q);
+  if (rc) return rc;
+  if (batch < 0 || tokens < 0) return set_error(DA_ERR_INVALID, "da_norm_weight_grad: negative size");
+  if (batch == 0) return DA_OK;
+  if (tokens == 0) return set_error(DA_ERR_INVALID, "da_norm_weight_grad: tokens must be >= 1");
+  if (!x || !g || !out) return set_error(DA_ERR_INVALID, "da_norm_weight_grad: NULL pointer");
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if (((uintptr_t)x | (uintptr_t)g) & 15 ||
+      ((x_bstride * es) | (x_tstride * es) | (g_bstride * es) | (g_tstride * es)) % 16)
+    return set_error(DA_ERR_INVALID, "da_norm_weight_grad: rows must be 16-byte aligned");
+  const int bias = has_bias ? 1 : 0;
+  if (out_bstride < (1 + bias) * d)
+    return set_error(DA_ERR_INVALID, "da_norm_weight_grad: out batch stride too small");
+  size_t need = 0;
+  da_norm_weight_grad_workspace(batch, tokens, d, bias, &need);
+  if (!workspace || workspace_bytes < need)
+    return set_error(DA_ERR_WORKSPACE, "da_norm_weight_grad: workspace needs %zu bytes", need);
+  NormArgs a;
+  a.x = (const char*)x;
+  a.g = (const char*)g;
+  a.batch = batch;
+  a.tokens = tokens;
+  a.d = d;
+  a.x_bstride = x_bstride * es;
+  a.x_tstride = x_tstride * es;
+  a.g_bstride = g_bstride * es;
+  a.g_tstride = g_tstride * es;
+  a.kind = kind;
+  a.eps = eps;
+  a.has_bias = bias;
+  a.chunks = (tokens + kRowsPerWG - 1) / kRowsPerWG;
+  a.partial = (float*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+#define DA_NG(DT)                                                                  \
+  switch (out_dtype) {                                                             \
+    case DA_F32: return launch_grad<DT, DA_F32>(a, q, out, out_bstride, st);       \
+    case DA_BF16: return launch_grad<DT, DA_BF16>(a, q, out, out_bstride, st);     \
+    default: return launch_grad<DT, DA_F16>(a, q, out, out_bstride, st);           \
+  }
+  switch (dtype) {
+    case DA_BF16: DA_NG(DA_BF16)
+    case DA_F16: DA_NG(DA_F16)
+    default: DA_NG(DA_F32)
+  }
+#undef DA_NG
+}
+
+int da_norm_xhat(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rstride, int kind,
+                 float eps, void* out, int out_dtype, int64_t out_rstride, void* stream) {
+  using namespace da;
+  int q;
+  int rc = check_common("da_norm_xhat", dtype, out_dtype, d, kind, &q);
+  if (rc) return rc;
+  if (rows < 0) return set_error(DA_ERR_INVALID, "da_norm_xhat: negative rows");
+  if (rows == 0) return DA_OK;
+  if (!x || !out) return set_error(DA_ERR_INVALID, "da_norm_xhat: NULL pointer");
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if (((uintptr_t)x & 15) || (x_rstride * es) % 16)
+    return set_error(DA_ERR_INVALID, "da_norm_xhat: rows must be 16-byte aligned");
+  if (out_rstride < d) return set_error(DA_ERR_INVALID, "da_norm_xhat: out row stride too small");
+  hipStream_t st = (hipStream_t)stream;
+#define DA_XH(DT)                                                                                 \
+  switch (out_dtype) {                                                                            \
+    case DA_F32: return launch_xhat<DT, DA_F32>(x, rows, d, x_rstride, kind, eps, out, out_rstride, q, st);   \
+    case DA_BF16: return launch_xhat<DT, DA_BF16>(x, rows, d, x_rstride, kind, eps, out, out_rstride, q, st); \
+    default: return launch_xhat<DT, DA_F16>(x, rows, d, x_rstride, kind, eps, out, out_rstride, q, st);       \
+  }
+  switch (dtype) {
+    case DA_BF16: DA_XH(DA_BF16)
+    case DA_F16: DA_XH(DA_F16)
+    default: DA_XH(DA_F32)
+  }
+#undef DA_XH
+}
+
+}  // extern "C"

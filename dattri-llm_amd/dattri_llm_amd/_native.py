@@ -63,6 +63,43 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "da_ghost_gram": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, _P, _I64, _I32, _P, _SZ, _P]),
 }
 
+class DenseLayer(ctypes.Structure):
+    """Mirror of ``da_dense_layer`` (include/dattri_amd.h)."""
+
+    _fields_ = [
+        ("m1", ctypes.c_void_p),
+        ("m2", ctypes.c_void_p),
+        ("width", ctypes.c_int64),
+        ("ld1", ctypes.c_int64),
+        ("ld2", ctypes.c_int64),
+    ]
+
+
+_LAYERS = ctypes.POINTER(DenseLayer)
+SIGNATURES.update(
+    {
+        "da_materialize_linear": (
+            _I32,
+            [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _I32, _I64, _I64, _P],
+        ),
+        "da_score_gemm_workspace": (_I32, [_I64, _I64, _LAYERS, _I32, _I32, ctypes.POINTER(_SZ)]),
+        "da_score_gemm": (
+            _I32,
+            [_I64, _I64, _LAYERS, _I32, _I32, _P, _I64, _I64, _I32, _P, _SZ, _P],
+        ),
+        "da_norm_weight_grad_workspace": (_I32, [_I64, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
+        "da_norm_weight_grad": (
+            _I32,
+            [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, ctypes.c_float, _I32,
+             _P, _I32, _I64, _P, _SZ, _P],
+        ),
+        "da_norm_xhat": (
+            _I32,
+            [_P, _I32, _I64, _I64, _I64, _I32, ctypes.c_float, _P, _I32, _I64, _P],
+        ),
+    }
+)
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 

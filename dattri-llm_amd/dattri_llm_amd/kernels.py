@@ -118,6 +118,192 @@ def ghost_gram(
     return out
 
 
+def materialize_linear(
+    a: torch.Tensor,
+    g: torch.Tensor,
+    *,
+    bias: bool = False,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """Per-sample linear weight gradient ``(B, D*(K+bias))``, index o*(K+bias)+k."""
+    dev = nat.require_device(a, g)
+    if a.dim() != 3 or g.dim() != 3 or a.shape[:2] != g.shape[:2]:
+        raise ValueError("materialize_linear expects a (B, T, K) and g (B, T, D)")
+    if a.dtype != g.dtype:
+        raise ValueError("materialize_linear factors must share one dtype")
+    out_dtype = out_dtype or a.dtype
+    b, t, k = a.shape
+    d = g.shape[-1]
+    kb = k + int(bias)
+    out = torch.empty(b, d * kb, dtype=out_dtype, device=dev)
+    if b == 0 or d == 0 or kb == 0:
+        return out
+    if t == 0:
+        return out.zero_()
+    vec = _chunk_elems(a.dtype)
+    kp = -(-k // vec) * vec
+    dp = -(-d // vec) * vec
+    if kp != k or dp != d:
+        # padded widths: compute into a padded buffer, then drop the padding
+        full = materialize_linear(prepare_rows(a, kp), prepare_rows(g, dp), out_dtype=out_dtype)
+        full = full.view(b, dp, kp)[:, :d, :k]
+        out.view(b, d, kb)[:, :, :k] = full
+        if bias:
+            out.view(b, d, kb)[:, :, k] = _column_sums(g, out_dtype)
+        return out
+    a, g = prepare_rows(a, k), prepare_rows(g, d)
+    nat.check(
+        nat.load().da_materialize_linear(
+            a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d,
+            a.stride(0), a.stride(1), g.stride(0), g.stride(1), int(bias),
+            out.data_ptr(), nat.dtype_code(out_dtype), d * kb, kb, nat.stream_ptr(dev),
+        ),
+        "materialize_linear",
+    )
+    return out
+
+
+def _column_sums(g: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """sum_t g[b, t, :] through the materialize kernel with a ones activation."""
+    b, t, _ = g.shape
+    vec = _chunk_elems(g.dtype)
+    ones = torch.zeros(b, t, vec, dtype=g.dtype, device=g.device)
+    ones[..., 0] = 1
+    dp = -(-g.shape[-1] // vec) * vec
+    m = materialize_linear(ones, prepare_rows(g, dp), out_dtype=out_dtype)
+    return m.view(b, dp, vec)[:, : g.shape[-1], 0]
+
+
+def score_gemm(
+    pairs: list[tuple[torch.Tensor, torch.Tensor]],
+    *,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """``sum_L m1_L @ m2_L.T`` over dense layer pairs, fp32 ``(B1, B2)``.
+
+    Each ``m*`` is (B, width...) and is flattened to (B, width); all pairs
+    share one dtype.  The side with fewer rows is put on the kernel's 32-row
+    side (the result is written transposed through the output strides).
+    """
+    if not pairs:
+        raise ValueError("score_gemm needs at least one layer pair")
+    flat = [(m1.reshape(m1.shape[0], -1), m2.reshape(m2.shape[0], -1)) for m1, m2 in pairs]
+    dev = nat.require_device(*[t for p in flat for t in p])
+    dtype = flat[0][0].dtype
+    b1, b2 = flat[0][0].shape[0], flat[0][1].shape[0]
+    for m1, m2 in flat:
+        if m1.dtype != dtype or m2.dtype != dtype:
+            raise ValueError("score_gemm layers must share one dtype")
+        if m1.shape[0] != b1 or m2.shape[0] != b2 or m1.shape[1] != m2.shape[1]:
+            raise ValueError("score_gemm layer shapes disagree")
+    if out is None:
+        out = torch.empty(b1, b2, dtype=torch.float32, device=dev)
+        accumulate = False
+    elif out.dtype != torch.float32 or tuple(out.shape) != (b1, b2):
+        raise ValueError("out must be float32 (B1, B2)")
+    vec = _chunk_elems(dtype)
+    swap = b1 > b2
+    layers = []
+    keep = []
+    for m1, m2 in flat:
+        w = -(-m1.shape[1] // vec) * vec
+        m1, m2 = prepare_rows(m1, w), prepare_rows(m2, w)
+        keep += [m1, m2]
+        if swap:
+            m1, m2 = m2, m1
+        layers.append(nat.DenseLayer(m1.data_ptr(), m2.data_ptr(), w, m1.stride(0), m2.stride(0)))
+    n1, n2 = (b2, b1) if swap else (b1, b2)
+    ld_row, ld_col = (out.stride(1), out.stride(0)) if swap else (out.stride(0), out.stride(1))
+    lib = nat.load()
+    code = nat.dtype_code(dtype)
+    for start in range(0, len(layers), 32):
+        group = layers[start : start + 32]
+        arr = (nat.DenseLayer * len(group))(*group)
+        nbytes = ctypes.c_size_t(0)
+        nat.check(lib.da_score_gemm_workspace(n1, n2, arr, len(group), code, ctypes.byref(nbytes)), "score_gemm")
+        ws = nat.workspace(nbytes.value, dev)
+        nat.check(
+            lib.da_score_gemm(n1, n2, arr, len(group), code, out.data_ptr(), ld_row, ld_col,
+                              int(accumulate or start > 0), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
+            "score_gemm",
+        )
+    del keep
+    return out
+
+
+NORM_KIND = {"nn.RMSNorm": 0, "nn.LayerNorm": 1}
+
+
+def norm_weight_grad(
+    x: torch.Tensor,
+    g: torch.Tensor,
+    *,
+    kind: int,
+    eps: float,
+    bias: bool = False,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """Per-sample norm weight gradient (B, d) -- or (B, 2d) = [dgamma, dbeta]."""
+    dev = nat.require_device(x, g)
+    if x.dim() != 3 or x.shape != g.shape:
+        raise ValueError("norm_weight_grad expects x and g of one (B, T, d) shape")
+    if x.dtype != g.dtype:
+        raise ValueError("norm_weight_grad factors must share one dtype")
+    out_dtype = out_dtype or x.dtype
+    b, t, d = x.shape
+    width = d * (1 + int(bias))
+    out = torch.empty(b, width, dtype=out_dtype, device=dev)
+    if b == 0:
+        return out
+    if t == 0:
+        return out.zero_()
+    if d % _chunk_elems(x.dtype) or not (_aligned(x) and _aligned(g)):
+        x, g = x.contiguous(), g.contiguous()
+        if d % _chunk_elems(x.dtype) or not (_aligned(x) and _aligned(g)):
+            raise NotImplementedError(
+                f"norm_weight_grad: width {d} is not a multiple of {_chunk_elems(x.dtype)} elements"
+            )
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_norm_weight_grad_workspace(b, t, d, int(bias), ctypes.byref(nbytes)), "norm_weight_grad")
+    ws = nat.workspace(nbytes.value, dev)
+    nat.check(
+        lib.da_norm_weight_grad(
+            x.data_ptr(), g.data_ptr(), nat.dtype_code(x.dtype), b, t, d,
+            x.stride(0), x.stride(1), g.stride(0), g.stride(1), int(kind), float(eps), int(bias),
+            out.data_ptr(), nat.dtype_code(out_dtype), width, ws.data_ptr(), ws.numel(),
+            nat.stream_ptr(dev),
+        ),
+        "norm_weight_grad",
+    )
+    return out
+
+
+def norm_xhat(x: torch.Tensor, *, kind: int, eps: float, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Normalised rows of a token norm layer over the last axis."""
+    dev = nat.require_device(x)
+    out_dtype = out_dtype or x.dtype
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    out = torch.empty(*x.shape, dtype=out_dtype, device=dev)
+    if rows == 0:
+        return out
+    flat = x.reshape(rows, d)
+    if d % _chunk_elems(x.dtype) or not _aligned(flat):
+        flat = flat.contiguous()
+        if d % _chunk_elems(x.dtype) or not _aligned(flat):
+            raise NotImplementedError(f"norm_xhat: width {d} is not a multiple of {_chunk_elems(x.dtype)}")
+    nat.check(
+        nat.load().da_norm_xhat(
+            flat.data_ptr(), nat.dtype_code(x.dtype), rows, d, flat.stride(0), int(kind), float(eps),
+            out.data_ptr(), nat.dtype_code(out_dtype), d, nat.stream_ptr(dev),
+        ),
+        "norm_xhat",
+    )
+    return out
+
+
 def selftest_mfma(dtype: torch.dtype, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """Raw accumulator dump of one 32x32 MFMA (see da_selftest_mfma)."""
     dev = nat.require_device(a, b)

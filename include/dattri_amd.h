@@ -97,6 +97,82 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
                   size_t workspace_bytes, void* stream);
 
 /*
+ * Per-sample weight gradient of a linear layer (materialized route):
+ *
+ *   out[b*out_bstride + o*out_rstride + k] = sum_t g[b,t,o] * a[b,t,k]   (k < K)
+ *   out[b*out_bstride + o*out_rstride + K] = sum_t g[b,t,o]              (has_bias)
+ *
+ * a is (B, T, K), g is (B, T, D) with element strides (bstride, tstride) and
+ * unit feature stride; out is written in out_dtype (fp32 accumulation).
+ * Replaces materialize_factors for linear layers,
+ * dattri_llm/gradient/ops/materialize.py:114-116 (bmm(g^T, a) flattened to
+ * (B, out*in)), with the bias column of preprocess.py:436-437.
+ */
+int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens,
+                          int64_t K, int64_t D, int64_t a_bstride, int64_t a_tstride,
+                          int64_t g_bstride, int64_t g_tstride, int has_bias, void* out,
+                          int out_dtype, int64_t out_bstride, int64_t out_rstride, void* stream);
+
+/*
+ * One dense layer of a score GEMM: m1 is (B1, width), m2 is (B2, width), row
+ * strides ld1/ld2 in elements, unit column stride.
+ */
+typedef struct da_dense_layer {
+  const void* m1;
+  const void* m2;
+  int64_t width;
+  int64_t ld1;
+  int64_t ld2;
+} da_dense_layer;
+
+/*
+ * Multi-layer score GEMM (dense route), fp32 accumulation:
+ *
+ *   out[i*ld_row + j*ld_col] (+)= sum_L sum_c m1_L[i,c] * m2_L[j,c]
+ *
+ * All layers share one dtype; at most 32 layers per call.  Deterministic
+ * (fixed-order split-K reduction through the workspace).
+ * Replaces the dense products of cross_gram / cross_dot,
+ * dattri_llm/gradient/ops/dot.py:114 and :501-505, and the layer sum of
+ * layerwise_cross_dot, dot.py:599-604.
+ */
+int da_score_gemm_workspace(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers,
+                            int dtype, size_t* bytes);
+int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
+                  float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/*
+ * Per-sample weight gradient of a token norm layer (kind 0 = RMSNorm,
+ * 1 = LayerNorm), one pass over x and g:
+ *
+ *   x_hat = x * rsqrt(mean(x^2) + eps)  |  (x - mean) * rsqrt(var + eps)
+ *   out[b*out_bstride + f]     = sum_t x_hat[b,t,f] * g[b,t,f]      (f < d)
+ *   out[b*out_bstride + d + f] = sum_t g[b,t,f]                     (has_bias)
+ *
+ * eps is the caller's resolved epsilon (the reference's eps=None means the
+ * activation dtype's machine epsilon, gradient/ops/norm.py:38-39).
+ * Replaces preprocess_factors' norm branches (dattri_llm/gradient/ops/preprocess.py:366-384,
+ * norm.py:25-41, :95-110) followed by materialize_factors' token sum
+ * (materialize.py:96-98).
+ */
+int da_norm_weight_grad_workspace(int64_t batch, int64_t tokens, int64_t d, int has_bias,
+                                  size_t* bytes);
+int da_norm_weight_grad(const void* x, const void* g, int dtype, int64_t batch, int64_t tokens,
+                        int64_t d, int64_t x_bstride, int64_t x_tstride, int64_t g_bstride,
+                        int64_t g_tstride, int kind, float eps, int has_bias, void* out,
+                        int out_dtype, int64_t out_bstride, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
+ * Normalised rows x_hat of a token norm layer (the activation factor
+ * preprocess_factors returns, dattri_llm/gradient/ops/norm.py:10-41):
+ * x is (rows, d) with row stride x_rstride, out (rows, d) in out_dtype.
+ */
+int da_norm_xhat(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rstride, int kind,
+                 float eps, void* out, int out_dtype, int64_t out_rstride, void* stream);
+
+/*
  * Lane-layout self test of the 32x32 MFMA convention every kernel relies on:
  * a (32 x k) and b (32 x k) row-major (k = 16 for bf16/f16, 8 for f32, i.e.
  * one 16-byte chunk per lane), out receives 64 lanes x 16 accumulator values

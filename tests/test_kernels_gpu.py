@@ -1,0 +1,136 @@
+"""GPU parity of the materialize, score-GEMM and norm kernels against the oracle.
+
+Bar: normwise relative error <= 1e-2 for bf16/fp16 inputs (fp32 accumulation),
+<= 1e-3 for fp32 inputs; the oracle runs in float64 on the same rounded inputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 1e-2, torch.float16: 1e-2, torch.float32: 1e-3}
+
+
+def _rand(gen, *shape, dtype, scale=None):
+    x = torch.randn(*shape, generator=gen)
+    if scale is not None:
+        x = x * scale
+    return x.to(dtype)
+
+
+def _np(x):
+    return x.double().cpu().numpy()
+
+
+MAT_CASES = [
+    # (b, t, k, d, bias)
+    (2, 64, 128, 128, False),
+    (3, 100, 72, 200, True),      # ragged T, partial tiles, bias column
+    (1, 1, 8, 8, False),
+    (2, 130, 256, 136, True),
+    (4, 33, 100, 60, False),      # widths not multiples of 8 -> padded path
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+@pytest.mark.parametrize("case", MAT_CASES)
+def test_materialize_linear(device, dtype, out_dtype, case):
+    from dattri_llm_amd import kernels
+
+    b, t, k, d, bias = case
+    gen = torch.Generator().manual_seed(sum(case))
+    a = _rand(gen, b, t, k, dtype=dtype)
+    g = _rand(gen, b, t, d, dtype=dtype)
+    print(f"materialize case={case} dtype={dtype} out={out_dtype}", flush=True)
+    got = kernels.materialize_linear(a.to(device), g.to(device), bias=bias, out_dtype=out_dtype)
+    ref = oracle.materialize_linear(_np(a), _np(g), bias=bias)
+    assert got.shape == ref.shape
+    assert got.dtype == (out_dtype or dtype)
+    assert rel_err(got.float().cpu().numpy(), ref) <= TOL[dtype]
+
+
+def test_materialize_linear_strided(device):
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(5)
+    a = _rand(gen, 40, 3, 64, dtype=torch.bfloat16)  # (T, B, K) sequence-first
+    g = _rand(gen, 40, 3, 32, dtype=torch.bfloat16)
+    got = kernels.materialize_linear(a.to(device).transpose(0, 1), g.to(device).transpose(0, 1))
+    ref = oracle.materialize_linear(_np(a.transpose(0, 1)), _np(g.transpose(0, 1)))
+    assert rel_err(got.float().cpu().numpy(), ref) <= 1e-2
+
+
+SCORE_CASES = [
+    # (b1, b2, widths)
+    (8, 64, [4096, 1024, 136]),
+    (3, 5, [64]),
+    (70, 20, [520, 8, 2000]),        # b1 > b2 -> transposed launch; b1 > 32
+    (1, 1, [8]),
+    (33, 130, [4104]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", SCORE_CASES)
+def test_score_gemm(device, dtype, case):
+    from dattri_llm_amd import kernels
+
+    b1, b2, widths = case
+    gen = torch.Generator().manual_seed(b1 * 7 + b2)
+    pairs = [(_rand(gen, b1, w, dtype=dtype), _rand(gen, b2, w, dtype=dtype)) for w in widths]
+    print(f"score_gemm case={case} dtype={dtype}", flush=True)
+    got = kernels.score_gemm([(m1.to(device), m2.to(device)) for m1, m2 in pairs])
+    ref = oracle.score_gemm([_np(m1) for m1, _ in pairs], [_np(m2) for _, m2 in pairs])
+    assert got.shape == (b1, b2)
+    assert rel_err(got.cpu().numpy(), ref) <= TOL[dtype]
+    # accumulate into an existing result
+    kernels.score_gemm([(m1.to(device), m2.to(device)) for m1, m2 in pairs], out=got, accumulate=True)
+    assert rel_err(got.cpu().numpy(), 2 * ref) <= TOL[dtype]
+
+
+NORM_CASES = [
+    # (b, t, d, layer_type, bias, eps)
+    (2, 70, 4096, "nn.RMSNorm", False, 1e-6),
+    (3, 33, 128, "nn.RMSNorm", False, None),      # eps=None -> dtype machine eps
+    (2, 64, 136, "nn.LayerNorm", True, 1e-5),
+    (4, 1, 64, "nn.LayerNorm", False, 1e-5),
+    (1, 300, 1024, "nn.RMSNorm", False, 1e-5),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", NORM_CASES)
+def test_norm_weight_grad(device, dtype, case):
+    from dattri_llm_amd import kernels
+
+    b, t, d, lt, bias, eps = case
+    eps_v = torch.finfo(dtype).eps if eps is None else eps
+    gen = torch.Generator().manual_seed(b + t + d)
+    x = _rand(gen, b, t, d, dtype=dtype)
+    g = _rand(gen, b, t, d, dtype=dtype)
+    print(f"norm case={case} dtype={dtype}", flush=True)
+    got = kernels.norm_weight_grad(x.to(device), g.to(device), kind=kernels.NORM_KIND[lt],
+                                   eps=eps_v, bias=bias, out_dtype=torch.float32)
+    ref = oracle.norm_weight_grad(_np(x), _np(g), lt, eps_v, bias)
+    assert got.shape == ref.shape
+    assert rel_err(got.cpu().numpy(), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("lt", ["nn.RMSNorm", "nn.LayerNorm"])
+def test_norm_xhat(device, dtype, lt):
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(3)
+    x = _rand(gen, 3, 17, 256, dtype=dtype, scale=3.0)
+    fn = oracle.rms_x_hat if lt == "nn.RMSNorm" else oracle.layer_norm_x_hat
+    got = kernels.norm_xhat(x.to(device), kind=kernels.NORM_KIND[lt], eps=1e-5, out_dtype=torch.float32)
+    assert rel_err(got.cpu().numpy(), fn(_np(x), 1e-5)) <= TOL[dtype]
