@@ -1,0 +1,392 @@
+#!/usr/bin/env python
+"""Pair-score throughput of the gradient-scoring path on one MI355X.
+
+Default workload (the headline metric): a Llama-3-8B-shaped decoder block
+(d 4096, 32 q / 8 kv heads -> q/k/v/o 4096->4096/1024/1024/4096, SwiGLU FFN
+14336, two RMSNorm(4096)), bf16, with the factors its 7 linears and 2 norms
+capture for 8 train sequences x 2048 tokens and 64 query sequences x 512
+tokens.  The reference's cost rule routes every layer of this block to the
+materialized form, so -- as in dattri-llm's scoring loop (the query block is
+routed to dense once, then every train block is materialized and scored
+against it) -- one step is one train block:
+
+    RMSNorm per-sample weight grads  (norm kernel, x2)
+    per-sample dW of the 7 linears   (materialize kernel, x7)
+    one multi-layer score GEMM       (score kernel: 9 layers, 8 x 64)
+
+Inputs are synthetic (seeded on the device) and already resident in HBM; the
+query-side preparation (64 queries materialized once) runs before the timed
+region and is reported as ``query_prep_ms``.
+
+Prints ONE JSON line.  ``--workload ghost`` instead times the fused ghost
+cross-gram at 256 train x 64 query samples, T=512, d_in=d_out=4096.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "dattri-llm_amd"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "train×query pair-scores/sec (Llama-8B-shaped block, bf16); MFMA util % of peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+D_MODEL, D_KV, D_FFN = 4096, 1024, 14336
+# (layer, activation factor, d_in, d_out)
+LINEARS = [
+    ("q_proj", "attn_in", D_MODEL, D_MODEL),
+    ("k_proj", "attn_in", D_MODEL, D_KV),
+    ("v_proj", "attn_in", D_MODEL, D_KV),
+    ("o_proj", "o_in", D_MODEL, D_MODEL),
+    ("gate_proj", "mlp_in", D_MODEL, D_FFN),
+    ("up_proj", "mlp_in", D_MODEL, D_FFN),
+    ("down_proj", "down_in", D_FFN, D_MODEL),
+]
+NORMS = [("input_layernorm", D_MODEL), ("post_attention_layernorm", D_MODEL)]
+ACT_WIDTH = {"attn_in": D_MODEL, "o_in": D_MODEL, "mlp_in": D_MODEL, "down_in": D_FFN}
+RMS_EPS = 1e-5
+
+
+def _randn(shape, gen, dtype, scale=1.0):
+    import torch
+
+    x = torch.empty(shape, dtype=torch.float32, device="cuda")
+    x.normal_(0.0, scale, generator=gen)
+    return x.to(dtype)
+
+
+def make_block(batch: int, tokens: int, seed: int):
+    """Synthetic captures of one block: shared activation factors per input,
+    one output-gradient factor per layer, norm inputs and gradients."""
+    import torch
+
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    bf = torch.bfloat16
+    acts = {k: _randn((batch, tokens, w), gen, bf) for k, w in ACT_WIDTH.items()}
+    grads = {n: _randn((batch, tokens, dout), gen, bf, dout**-0.5) for n, _a, _i, dout in LINEARS}
+    norms = {n: (_randn((batch, tokens, d), gen, bf), _randn((batch, tokens, d), gen, bf, d**-0.5))
+             for n, d in NORMS}
+    return acts, grads, norms
+
+
+def dense_block(acts, grads, norms, timers=None):
+    """Per-sample dense gradients of every layer (the materialized route)."""
+    import torch
+
+    from dattri_llm_amd import kernels
+
+    out = {}
+    for name, d in NORMS:
+        x, g = norms[name]
+        ev = _ev(timers, "norm_weight_grad")
+        out[name] = kernels.norm_weight_grad(x, g, kind=0, eps=RMS_EPS, out_dtype=torch.bfloat16)
+        _ev_end(ev)
+    for name, act, _din, _dout in LINEARS:
+        ev = _ev(timers, f"materialize:{name}")
+        out[name] = kernels.materialize_linear(acts[act], grads[name])
+        _ev_end(ev)
+    return out
+
+
+def _ev(timers, key):
+    if timers is None:
+        return None
+    import torch
+
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    timers.setdefault(key, []).append((s, e))
+    return e
+
+
+def _ev_end(e):
+    if e is not None:
+        e.record()
+
+
+def _mean_ms(timers, key):
+    pairs = timers.get(key, [])
+    return sum(s.elapsed_time(e) for s, e in pairs) / max(len(pairs), 1)
+
+
+def cpu_info():
+    cores = len(os.sched_getaffinity(0))
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, model
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        info = [p for p in threadpool_info() if p.get("user_api") == "blas"]
+        if info:
+            return int(info[0]["num_threads"])
+    except Exception:  # noqa: BLE001
+        pass
+    return int(os.environ.get("OMP_NUM_THREADS", "1"))
+
+
+# ---------------------------------------------------------------------------
+# Llama block (headline)
+# ---------------------------------------------------------------------------
+
+
+def bench_block(args):
+    import torch
+
+    from dattri_llm_amd import kernels
+
+    n_train, t_train, n_query, t_query = 8, 2048, 64, 512
+    acts, grads, norms = make_block(n_train, t_train, seed=0)
+    q_acts, q_grads, q_norms = make_block(n_query, t_query, seed=1)
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    q_dense = dense_block(q_acts, q_grads, q_norms)
+    torch.cuda.synchronize()
+    query_prep_ms = (time.perf_counter() - t0) * 1e3
+    del q_acts, q_grads, q_norms
+    names = [n for n, _ in NORMS] + [n for n, *_ in LINEARS]
+    scores = torch.empty(n_train, n_query, dtype=torch.float32, device="cuda")
+
+    def step(timers=None):
+        tr = dense_block(acts, grads, norms, timers)
+        ev = _ev(timers, "score_gemm")
+        kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=scores)
+        _ev_end(ev)
+        return scores
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timers)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Algorithmic work.
+    dk = {n: din * dout for n, _a, din, dout in LINEARS}
+    width = sum(dk.values()) + sum(d for _, d in NORMS)
+    mat_flops = {n: 2.0 * n_train * t_train * v for n, v in dk.items()}
+    score_bytes = (n_train + n_query) * width * 2.0
+    kern = {}
+    for n, *_ in LINEARS:
+        t = _mean_ms(timers, f"materialize:{n}")
+        kern[f"materialize:{n}"] = {"ms": round(t, 4), "tflops": round(mat_flops[n] / t / 1e9, 1)}
+    t_score = _mean_ms(timers, "score_gemm")
+    kern["score_gemm"] = {"ms": round(t_score, 4), "gbs": round(score_bytes / t_score / 1e6, 1)}
+    t_norm = _mean_ms(timers, "norm_weight_grad")
+    norm_bytes = 2.0 * n_train * t_train * D_MODEL * 2
+    kern["norm_weight_grad"] = {"ms": round(t_norm, 4), "gbs": round(norm_bytes / t_norm / 1e6, 1)}
+    t_mat = sum(_mean_ms(timers, f"materialize:{n}") for n, *_ in LINEARS)
+    mfma_util = sum(mat_flops.values()) / (t_mat * 1e9) / PEAK_BF16_TFLOPS
+
+    # Dominant kernel: the one taking most of the step.
+    big = max(((k, v["ms"] * (2 if k == "norm_weight_grad" else 1)) for k, v in kern.items()), key=lambda kv: kv[1])[0]
+    if big == "score_gemm":
+        roof = {"bound": "hbm", "kernel": "score_gemm_chunks", "achieved": kern[big]["gbs"],
+                "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(kern[big]["gbs"] / PEAK_HBM_GBS, 4), "traffic": None}
+    else:
+        roof = {"bound": "mfma", "kernel": "materialize_tiles (" + big.split(":")[-1] + ")",
+                "achieved": kern[big]["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(kern[big]["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None}
+
+    pairs = n_train * n_query
+    result = {
+        "metric": METRIC,
+        "value": round(pairs / (ms / 1e3), 1),
+        "unit": "pair-scores/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "llama3-8b-block: 8 train x 2048 tok vs 64 query x 512 tok, "
+                        "7 linears + 2 RMSNorm, materialized route",
+            "train_block": [n_train, t_train],
+            "query_block": [n_query, t_query],
+            "score_width_per_sample": width,
+        },
+        "mfma_util": round(mfma_util, 4),
+        "query_prep_ms": round(query_prep_ms, 2),
+        "roofline": roof,
+        "kernels": kern,
+    }
+    if args.cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_block(n_query_total=n_query, n_train_total=n_train)
+    return result
+
+
+def cpu_baseline_block(n_query_total: int, n_train_total: int):
+    """The oracle (numpy fp32) on a bounded sample of the same step: the full
+    8-sample train block (T=2048, all 9 layers) materialized and scored, as one
+    GEMM per layer like the reference's loop, against 16 of the 64 cached dense
+    queries; the score part is scaled to 64 queries (it streams the query
+    matrix, so its time is linear in the query count)."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0)
+    f32 = np.float32
+
+    def block(b, t):
+        acts = {k: rng.standard_normal((b, t, w), dtype=f32) for k, w in ACT_WIDTH.items()}
+        grads = {n: rng.standard_normal((b, t, dout), dtype=f32) * f32(dout**-0.5) for n, _a, _i, dout in LINEARS}
+        norms = {n: (rng.standard_normal((b, t, d), dtype=f32), rng.standard_normal((b, t, d), dtype=f32))
+                 for n, d in NORMS}
+        return acts, grads, norms
+
+    def dense(acts, grads, norms):
+        out = {}
+        for n, _d in NORMS:
+            out[n] = oracle.norm_weight_grad(norms[n][0], norms[n][1], "nn.RMSNorm", RMS_EPS)
+        for n, a, _i, _o in LINEARS:
+            out[n] = oracle.materialize_linear(acts[a], grads[n])
+        return out
+
+    nq = 16
+    q_dense = dense(*block(nq, 512))
+    tr = block(n_train_total, 2048)
+    names = list(q_dense)
+    best_mat = best_score = float("inf")
+    for _ in range(2):
+        t0 = time.perf_counter()
+        tr_dense = dense(*tr)
+        best_mat = min(best_mat, time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        oracle.score_gemm([tr_dense[n] for n in names], [q_dense[n] for n in names])
+        best_score = min(best_score, time.perf_counter() - t0)
+        del tr_dense
+    step_s = best_mat + (n_query_total / nq) * best_score
+    cores, model = cpu_info()
+    return {
+        "value": round(n_train_total * n_query_total / step_s, 3),
+        "unit": "pair-scores/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": f"numpy fp32 oracle: the 8-sample train block (T=2048, 7 linears + 2 RMSNorm) "
+                  f"materialized ({best_mat:.2f} s) and scored vs 16 dense queries ({best_score:.2f} s), "
+                  f"best of 2; score time scaled x{n_query_total // nq} to 64 queries -> step "
+                  f"{step_s:.2f} s; host {model}, {cores} cores visible",
+    }
+
+
+# ---------------------------------------------------------------------------
+# ghost cross-gram (factorized route)
+# ---------------------------------------------------------------------------
+
+
+def bench_ghost(args):
+    import torch
+
+    from dattri_llm_amd import kernels
+
+    n1, n2, t, d = 256, 64, 512, 4096
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    bf = torch.bfloat16
+    a1 = _randn((n1, t, d), gen, bf, d**-0.5)
+    g1 = _randn((n1, t, d), gen, bf, d**-0.5)
+    a2 = _randn((n2, t, d), gen, bf, d**-0.5)
+    g2 = _randn((n2, t, d), gen, bf, d**-0.5)
+    out = torch.empty(n1, n2, dtype=torch.float32, device="cuda")
+    for _ in range(args.warmup):
+        kernels.ghost_gram(a1, g1, a2, g2, out=out)
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ev = _ev(timers, "ghost")
+        kernels.ghost_gram(a1, g1, a2, g2, out=out)
+        _ev_end(ev)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    flops = 2.0 * n1 * n2 * t * t * (d + d)
+    t_k = _mean_ms(timers, "ghost")
+    tflops = flops / t_k / 1e9
+    result = {
+        "metric": "ghost cross-gram pair-scores/sec (256x64 pairs, T=512, d=4096, bf16)",
+        "value": round(n1 * n2 / (ms / 1e3), 1),
+        "unit": "pair-scores/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "ghost cross-gram 256 train x 64 query, T=512, d_in=d_out=4096"},
+        "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles", "achieved": round(tflops, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import oracle
+
+        rng = np.random.default_rng(0)
+        s = [rng.standard_normal((n, t, d), dtype=np.float32) for n in (8, 8, 4, 4)]
+        t0 = time.perf_counter()
+        oracle.cross_gram_factorized(s[0], s[1], s[2], s[3])
+        dt = time.perf_counter() - t0
+        cores, model = cpu_info()
+        result["cpu_baseline"] = {"value": round(32 / dt, 3), "unit": "pair-scores/s",
+                                  "cores": blas_threads(), "kind": "port",
+                                  "sample": f"numpy fp32 oracle, 8 train x 4 query at T=512, d=4096 "
+                                            f"({dt:.2f} s); host {model}, {cores} cores visible"}
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["block", "ghost"], default="block")
+    ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the scoring path shards train rows; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    result = bench_block(args) if args.workload == "block" else bench_ghost(args)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -36,13 +36,14 @@ int zero_f32_2d(float* out, int64_t rows, int64_t cols, int64_t ld, hipStream_t 
   return check_launch("zero_f32_2d");
 }
 
-// One wave computes C = A . B^T for a single 32x32 block with the library's
+// One wave computes C = A . B^T for a single MFMA block with the library's
 // operand convention and dumps the accumulator registers verbatim.
+// shape 32: 32x32 block, A/B are 32 rows x 32 bytes (one chunk per lane half).
+// shape 16: 16x16 block, A/B are 16 rows x 64 bytes (one chunk per lane quarter).
 template <int DT>
-__global__ __launch_bounds__(64) void selftest_mfma_kernel(const char* a, const char* b, float* out) {
+__global__ __launch_bounds__(64) void selftest_mfma32_kernel(const char* a, const char* b, float* out) {
   const int lane = threadIdx.x;
   const int row = lane & 31, half = lane >> 5;
-  // A and B are (32 x 2 chunks) of 16 bytes: row stride 32 bytes.
   const u32x4 va = ld16(a + row * 32 + half * 16);
   const u32x4 vb = ld16(b + row * 32 + half * 16);
   f32x16 acc = {};
@@ -51,30 +52,42 @@ __global__ __launch_bounds__(64) void selftest_mfma_kernel(const char* a, const 
   for (int r = 0; r < 16; ++r) out[lane * 16 + r] = acc[r];
 }
 
+template <int DT>
+__global__ __launch_bounds__(64) void selftest_mfma16_kernel(const char* a, const char* b, float* out) {
+  const int lane = threadIdx.x;
+  const int row = lane & 15, quarter = lane >> 4;
+  const u32x4 va = ld16(a + row * 64 + quarter * 16);
+  const u32x4 vb = ld16(b + row * 64 + quarter * 16);
+  f32x4 acc = {};
+  Mfma16<DT>::mma(acc, va, vb);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[lane * 4 + r] = acc[r];
+}
+
 }  // namespace da
 
 extern "C" {
 
-int da_abi_version(void) { return 1; }
+int da_abi_version(void) { return 2; }
 
 const char* da_last_error(void) { return da::g_error; }
 
-int da_selftest_mfma(int dtype, const void* a, const void* b, float* out, void* stream) {
+int da_selftest_mfma(int dtype, int shape, const void* a, const void* b, float* out, void* stream) {
   if (!a || !b || !out) return da::set_error(DA_ERR_INVALID, "da_selftest_mfma: null pointer");
+  if (shape != 16 && shape != 32) return da::set_error(DA_ERR_INVALID, "da_selftest_mfma: shape must be 16 or 32");
+  if (!da::valid_dtype(dtype)) return da::set_error(DA_ERR_INVALID, "da_selftest_mfma: bad dtype %d", dtype);
   hipStream_t s = (hipStream_t)stream;
+#define DA_ST(DT)                                                                                   \
+  if (shape == 32)                                                                                  \
+    da::selftest_mfma32_kernel<DT><<<1, 64, 0, s>>>((const char*)a, (const char*)b, out);          \
+  else                                                                                              \
+    da::selftest_mfma16_kernel<DT><<<1, 64, 0, s>>>((const char*)a, (const char*)b, out);
   switch (dtype) {
-    case DA_BF16:
-      da::selftest_mfma_kernel<DA_BF16><<<1, 64, 0, s>>>((const char*)a, (const char*)b, out);
-      break;
-    case DA_F16:
-      da::selftest_mfma_kernel<DA_F16><<<1, 64, 0, s>>>((const char*)a, (const char*)b, out);
-      break;
-    case DA_F32:
-      da::selftest_mfma_kernel<DA_F32><<<1, 64, 0, s>>>((const char*)a, (const char*)b, out);
-      break;
-    default:
-      return da::set_error(DA_ERR_INVALID, "da_selftest_mfma: bad dtype %d", dtype);
+    case DA_BF16: DA_ST(DA_BF16) break;
+    case DA_F16: DA_ST(DA_F16) break;
+    default: DA_ST(DA_F32) break;
   }
+#undef DA_ST
   return da::check_launch("da_selftest_mfma");
 }
 

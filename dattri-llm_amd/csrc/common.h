@@ -131,6 +131,38 @@ template <> struct Mfma32<DA_F32> {
   }
 };
 
+// ---------------------------------------------------------------------------
+// 16x16 MFMA (v_mfma_f32_16x16x32_{bf16,f16}, v_mfma_f32_16x16x4_f32).
+//
+// Lane l supplies row (l % 16) of A / column (l % 16) of B; its 16-byte chunk
+// holds the k-elements [kb + kVec*(l/16), ... + kVec) (fp32: four MFMAs, one
+// element each).  Accumulator: acc[r] of lane l holds C[4*(l/16) + r][l % 16]
+// (checked by da_selftest_mfma).
+// ---------------------------------------------------------------------------
+template <int DT> struct Mfma16;
+template <> struct Mfma16<DA_BF16> {
+  __device__ static __forceinline__ void mma(f32x4& acc, u32x4 a, u32x4 b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<DA_F16> {
+  __device__ static __forceinline__ void mma(f32x4& acc, u32x4 a, u32x4 b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<DA_F32> {
+  __device__ static __forceinline__ void mma(f32x4& acc, u32x4 a, u32x4 b) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[s]), __uint_as_float(b[s]), acc,
+                                                 0, 0, 0);
+  }
+};
+__device__ __forceinline__ int acc16_row(int r, int lane) { return 4 * (lane >> 4) + r; }
+__device__ __forceinline__ int acc16_col(int lane) { return lane & 15; }
+
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 __device__ __forceinline__ int acc_col(int lane) { return lane & 31; }
 

@@ -1,0 +1,208 @@
+// K3c: MoE routing and expert segmentation (integer work, bit-exact).
+//
+//   da_moe_topk:       top-k of softmax(logits) per token, weights renormalised
+//                      over the k, indices by descending probability with ties
+//                      going to the lower expert index -- the router of
+//                      transformers' MixtralTopKRouter.forward
+//                      (softmax(logits.float()) -> topk -> / sum), as consumed by
+//                      dattri_llm/gradient/hooks/override_layers/fused_experts.py:210-237.
+//   da_counting_sort:  stable counting sort of int32 keys into bins.  With the
+//                      top-k indices read slot-major (key[p] = idx[p % N][p / N])
+//                      the sorted order is exactly the reference loop's
+//                      torch.where(one_hot(idx).permute(2,1,0)[e]) enumeration,
+//                      fused_experts.py:219-228 (slot-major, token ascending),
+//                      and the bin offsets are the expert segments.  With
+//                      key = token // T it groups an expert's rows by sample for
+//                      the segmented ghost product (the dense-with-zeros regroup
+//                      of hooks/routing.py:71-86, without the zeros).
+//
+// Both are tiny next to the expert GEMMs; they exist so the routing never
+// leaves the device and never depends on a library sort's tie order.
+#include "common.h"
+
+namespace da {
+namespace {
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopK = 16;
+constexpr int kMaxBins = 8192;
+
+template <int DT>
+__global__ void moe_topk_kernel(const char* logits, int64_t n, int e, int k, int64_t rstride,
+                                float* weights, int64_t* index) {
+  const int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tok >= n) return;
+  const char* row = logits + tok * rstride * Elem<DT>::kBytes;
+  float mx = -INFINITY;
+  for (int x = 0; x < e; ++x) mx = fmaxf(mx, Elem<DT>::load(row, x));
+  float sum = 0.f;
+  for (int x = 0; x < e; ++x) sum += expf(Elem<DT>::load(row, x) - mx);
+  // Selection by repeated arg-max over the probabilities; strict '>' keeps the
+  // lower index on ties.  `taken` marks chosen experts (e <= 256).
+  uint32_t taken[kMaxExperts / 32];
+#pragma unroll
+  for (int w = 0; w < kMaxExperts / 32; ++w) taken[w] = 0u;
+  float top[kMaxTopK];
+  int64_t idx[kMaxTopK];
+  float tsum = 0.f;
+  for (int s = 0; s < k; ++s) {
+    float best = -1.f;
+    int bi = -1;
+    for (int x = 0; x < e; ++x) {
+      if (taken[x >> 5] & (1u << (x & 31))) continue;
+      const float p = expf(Elem<DT>::load(row, x) - mx) / sum;
+      if (p > best) {
+        best = p;
+        bi = x;
+      }
+    }
+    if (bi < 0) {  // remaining probabilities are NaN: take the lowest free index
+      for (int x = e - 1; x >= 0; --x)
+        if (!(taken[x >> 5] & (1u << (x & 31)))) bi = x;
+    }
+    taken[bi >> 5] |= 1u << (bi & 31);
+    top[s] = best;
+    idx[s] = bi;
+    tsum += best;
+  }
+  for (int s = 0; s < k; ++s) {
+    weights[tok * k + s] = top[s] / tsum;
+    index[tok * k + s] = idx[s];
+  }
+}
+
+// keys are read either directly (slot_major == 0: key[p] = keys[p]) or as the
+// slot-major view of an (n/k, k) int64 index matrix (slot_major == 1).
+struct SortArgs {
+  const int32_t* keys32;
+  const int64_t* keys64;  // (rows, k) row-major when slot_major
+  int64_t n, rows, k;
+  int slot_major;
+  int bins;
+  int32_t* offsets;       // bins + 1
+  int32_t* perm;          // n
+  int64_t key_div;        // key = raw / key_div (1 = identity)
+};
+
+__device__ __forceinline__ int64_t sort_key(const SortArgs& a, int64_t p) {
+  int64_t raw;
+  if (a.slot_major) {
+    const int64_t slot = p / a.rows, r = p - slot * a.rows;
+    raw = a.keys64[r * a.k + slot];
+  } else {
+    raw = a.keys32 ? (int64_t)a.keys32[p] : a.keys64[p];
+  }
+  return a.key_div > 1 ? (raw >= 0 ? raw / a.key_div : -1) : raw;
+}
+
+// One workgroup: histogram (LDS atomics; counts are order independent), exclusive
+// scan, then wave 0 scatters in input order, 64 entries at a time, ranking equal
+// keys inside the wave with shuffles -- a stable sort.  Keys outside [0, bins)
+// are skipped; offsets[bins] is the number of entries kept.
+__global__ __launch_bounds__(256) void counting_sort_kernel(SortArgs a) {
+  __shared__ int32_t cnt[kMaxBins];
+  const int tid = threadIdx.x;
+  for (int b = tid; b < a.bins; b += 256) cnt[b] = 0;
+  __syncthreads();
+  for (int64_t p = tid; p < a.n; p += 256) {
+    const int64_t key = sort_key(a, p);
+    if (key >= 0 && key < a.bins) atomicAdd(&cnt[key], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t run = 0;
+    for (int b = 0; b < a.bins; ++b) {
+      const int32_t c = cnt[b];
+      a.offsets[b] = run;
+      cnt[b] = run;  // becomes the next free slot of bin b
+      run += c;
+    }
+    a.offsets[a.bins] = run;
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+  const int lane = tid;
+  for (int64_t base = 0; base < a.n; base += 64) {
+    const int64_t p = base + lane;
+    const int64_t key = p < a.n ? sort_key(a, p) : -1;
+    const bool ok = key >= 0 && key < a.bins;
+    int rank = 0, total = 0;
+    for (int src = 0; src < 64; ++src) {
+      const int64_t other = __shfl(key, src, 64);
+      if (ok && other == key) {
+        total += 1;
+        if (src < lane) rank += 1;
+      }
+    }
+    int32_t slot = 0;
+    if (ok) slot = cnt[key] + rank;
+    // every lane has read cnt[] before the last lane of each key group bumps it
+    __builtin_amdgcn_wave_barrier();
+    if (ok) {
+      a.perm[slot] = (int32_t)p;
+      if (rank == total - 1) cnt[key] = slot + 1;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+}  // namespace
+}  // namespace da
+
+extern "C" {
+
+int da_moe_topk(const void* logits, int dtype, int64_t n_tokens, int n_experts, int k,
+                int64_t row_stride, float* weights, int64_t* index, void* stream) {
+  using namespace da;
+  const char* who = "da_moe_topk";
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype", who);
+  if (n_tokens < 0) return set_error(DA_ERR_INVALID, "%s: negative token count", who);
+  if (n_experts < 1 || n_experts > kMaxExperts)
+    return set_error(DA_ERR_INVALID, "%s: n_experts must be in [1, %d]", who, kMaxExperts);
+  if (k < 1 || k > n_experts || k > kMaxTopK)
+    return set_error(DA_ERR_INVALID, "%s: k must be in [1, min(n_experts, %d)]", who, kMaxTopK);
+  if (row_stride < n_experts) return set_error(DA_ERR_INVALID, "%s: row stride < n_experts", who);
+  if (n_tokens == 0) return DA_OK;
+  if (!logits || !weights || !index) return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  const unsigned blocks = (unsigned)((n_tokens + 255) / 256);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case DA_BF16: moe_topk_kernel<DA_BF16><<<blocks, 256, 0, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
+    case DA_F16: moe_topk_kernel<DA_F16><<<blocks, 256, 0, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
+    default: moe_topk_kernel<DA_F32><<<blocks, 256, 0, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
+  }
+  return check_launch(who);
+}
+
+int da_counting_sort(const int32_t* keys32, const int64_t* keys64, int64_t n, int64_t rows,
+                     int64_t k, int slot_major, int64_t key_div, int bins, int32_t* offsets,
+                     int32_t* perm, void* stream) {
+  using namespace da;
+  const char* who = "da_counting_sort";
+  if (n < 0 || bins < 1 || bins > kMaxBins)
+    return set_error(DA_ERR_INVALID, "%s: need n >= 0 and 1 <= bins <= %d", who, kMaxBins);
+  if (n > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: at most 2^31-1 entries", who);
+  if (key_div < 1) return set_error(DA_ERR_INVALID, "%s: key_div must be >= 1", who);
+  if (slot_major) {
+    if (!keys64 || rows < 1 || k < 1 || rows * k != n)
+      return set_error(DA_ERR_INVALID, "%s: slot-major keys need an int64 (rows, k) matrix with rows*k == n", who);
+  } else if (n > 0 && !keys32 && !keys64) {
+    return set_error(DA_ERR_INVALID, "%s: no keys", who);
+  }
+  if (!offsets || (n > 0 && !perm)) return set_error(DA_ERR_INVALID, "%s: NULL output", who);
+  SortArgs a;
+  a.keys32 = keys32;
+  a.keys64 = keys64;
+  a.n = n;
+  a.rows = rows;
+  a.k = k;
+  a.slot_major = slot_major;
+  a.bins = bins;
+  a.offsets = offsets;
+  a.perm = perm;
+  a.key_div = key_div;
+  counting_sort_kernel<<<1, 256, 0, (hipStream_t)stream>>>(a);
+  return check_launch(who);
+}
+
+}  // extern "C"

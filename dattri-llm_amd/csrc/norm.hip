@@ -30,7 +30,7 @@ struct NormArgs {
   const char* g;
   int64_t batch, tokens, d;
   int64_t x_bstride, x_tstride, g_bstride, g_tstride;  // bytes
-  int kind;                                            // 0 RMSNorm, 1 LayerNorm
+  int kind;                                            // 0 RMSNorm, 1 LayerNorm, 2 as given
   float eps;
   int has_bias;
   int64_t chunks;                                      // token chunks per sample
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
         ss += c * c;
       }
     }
-    const float rstd = 1.f / sqrtf(wave_sum(ss) * inv_d + a.eps);
+    const float rstd = a.kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + a.eps);
     // Re-read the packed row rather than keeping kQ*VEC unpacked floats live
     // across the reductions (halves register pressure, doubles occupancy).
 #pragma unroll
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_
       ss += c * c;
     }
   }
-  const float rstd = 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
+  const float rstd = kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
 #pragma unroll
   for (int q = 0; q < kQ; ++q) {
     const int64_t c = lane + (int64_t)q * kWave;
@@ -274,7 +274,8 @@ int launch_xhat(const void* x, int64_t rows, int64_t d, int64_t x_rstride, int k
 int check_common(const char* who, int dtype, int out_dtype, int64_t d, int kind, int* q) {
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype))
     return set_error(DA_ERR_INVALID, "%s: bad dtype", who);
-  if (kind != 0 && kind != 1) return set_error(DA_ERR_INVALID, "%s: kind must be 0 (RMSNorm) or 1 (LayerNorm)", who);
+  if (kind < 0 || kind > 2)
+    return set_error(DA_ERR_INVALID, "%s: kind must be 0 (RMSNorm), 1 (LayerNorm) or 2 (normalised)", who);
   const int64_t vec = 16 / (int64_t)elem_bytes(dtype);
   if (d <= 0 || d % vec)
     return set_error(DA_ERR_INVALID, "%s: d=%lld must be a positive multiple of %lld", who,

@@ -1,0 +1,340 @@
+// K2: random projection of factor rows, and the fused capture-time projection
+// + per-sample outer-product sum (LoGRA-style, double-sided).
+//
+//   project_rows:  out[r, c] = sum_j x[r, j] * P[j, c] (+ bias[c])
+//     follows ProjectionMatrix.__call__, dattri_llm/gradient/ops/projection.py:363-370
+//     (flat @ P, or addmm(bias_row, flat, P)).
+//
+//   project_outer: M[b, o, i] = sum_t (g[b,t,:] P_out)[o] * (a[b,t,:] P_in (+ bias_in))[i]
+//     follows the capture path of hooks.py:631-648: project the activation with
+//     proj_seed+1 and the gradient with proj_seed (projection.py:437-440,
+//     :476-488), then materialize_factors(a_p, g_p, "nn.Linear"), i.e.
+//     bmm(g_p^T, a_p) flattened to (B, k_g*k_a) (materialize.py:114-116).
+//
+// Both are bound by streaming the factor rows from HBM (the projected widths
+// are <= 64, so every input byte meets at most 2*64 flops).  A workgroup owns
+// 64 rows (4 waves x 16) and up to 64 projected columns; each wave feeds its
+// rows straight from HBM into 16x16x32 MFMAs (four lanes per row, 64
+// contiguous bytes per load instruction, prefetched one stage ahead), while
+// the transposed projection matrix P^T -- tiny, L2-resident and shared by
+// the four waves -- is staged through double-buffered LDS.  The fused kernel
+// runs the activation and gradient projections back to back for one 64-token
+// chunk of one sample, parks both (64 x 64 fp32) in LDS and contracts them over
+// the chunk's tokens; chunk partials are summed in a fixed order.
+#include "common.h"
+
+namespace da {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRows = 64;                 // rows per workgroup (4 waves x 16)
+constexpr int kCols = 64;                 // projected columns per workgroup
+constexpr int kStage = 256;               // bytes of feature width per stage
+constexpr int kPtRow = kStage + 16;       // padded LDS row of P^T
+constexpr int kPtBytes = kCols * kPtRow;  // one LDS stage of P^T
+
+// acc[cb][e] += sum over the width of x[row(lane,e)] * pt[16*cb + col(lane)],
+// rows = this wave's 16 rows.  xrow: this lane's row (nullptr = zero row).
+template <int DT>
+__device__ __forceinline__ void project_tile(const char* xrow, int64_t wbytes, const char* pt,
+                                             int64_t pt_rstride, int ncols, char* lds,
+                                             f32x4 (&acc)[4], int tid, int lane) {
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int q = lane >> 4, r = lane & 15;
+  const int prow = tid >> 4, pch = tid & 15;  // P^T staging: 16 rows x 16 chunks per pass
+  const int nk = (int)((wbytes + kStage - 1) / kStage);
+  u32x4 xv[4], pv[4];
+
+  auto load_x = [&](int kt) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int64_t off = (int64_t)kt * kStage + 64 * st + 16 * q;
+      xv[st] = (xrow && off < wbytes) ? ld16(xrow + off) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto load_p = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int c = prow + 16 * p;
+      const int64_t off = (int64_t)kt * kStage + 16 * pch;
+      pv[p] = (c < ncols && off < wbytes) ? ld16(pt + c * pt_rstride + off) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_p = [&](int buf) {
+    char* base = lds + buf * kPtBytes;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) st16(base + (prow + 16 * p) * kPtRow + 16 * pch, pv[p]);
+  };
+
+  load_p(0);
+  store_p(0);
+  load_x(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    u32x4 cur[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) cur[st] = xv[st];
+    if (kt + 1 < nk) {
+      load_x(kt + 1);
+      load_p(kt + 1);
+    }
+    const char* base = lds + (kt & 1) * kPtBytes;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const u32x4 b = ld16(base + (16 * cb + r) * kPtRow + 64 * st + 16 * q);
+        Mfma16<DT>::mma(acc[cb], cur[st], b);
+      }
+    if (kt + 1 < nk) store_p((kt + 1) & 1);
+    __syncthreads();
+  }
+}
+
+struct RowsArgs {
+  const char* x;
+  int64_t rows, wbytes, x_rstride;  // bytes
+  const char* pt;
+  int64_t pt_rstride;               // bytes
+  int64_t k;
+  const float* bias;                // k floats or nullptr
+  char* out;
+  int64_t out_rstride;              // elements
+};
+
+template <int DT, int OT>
+__global__ __launch_bounds__(kThreads) void project_rows_kernel(RowsArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kPtBytes];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * kRows;
+  const int64_t c0 = (int64_t)blockIdx.y * kCols;
+  const int64_t row = r0 + 16 * wave + (lane & 15);
+  const char* xrow = row < a.rows ? a.x + row * a.x_rstride : nullptr;
+  const int ncols = (int)min((int64_t)kCols, a.k - c0);
+  f32x4 acc[4];
+  project_tile<DT>(xrow, a.wbytes, a.pt + c0 * a.pt_rstride, a.pt_rstride, ncols, lds, acc, tid, lane);
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t orow = r0 + 16 * wave + acc16_row(e, lane);
+      const int64_t ocol = c0 + 16 * cb + acc16_col(lane);
+      if (orow < a.rows && ocol < a.k)
+        Elem<OT>::store(a.out, orow * a.out_rstride + ocol, acc[cb][e] + (a.bias ? a.bias[ocol] : 0.f));
+    }
+}
+
+struct OuterArgs {
+  const char* a;
+  const char* g;
+  int64_t batch, tokens;
+  int64_t a_bstride, a_tstride, g_bstride, g_tstride;  // bytes
+  int64_t abytes, gbytes;                              // row widths in bytes
+  const char* pin_t;                                   // (ka, K) transposed P_in
+  const char* pout_t;                                  // (kg, D) transposed P_out
+  int64_t pin_rstride, pout_rstride;                   // bytes
+  int ka, kg;
+  const float* bias_in;                                // ka floats or nullptr
+  int64_t chunks;                                      // 64-token chunks per sample
+  float* partial;                                      // [batch][chunks][kg][ka]
+};
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void project_outer_kernel(OuterArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * kPtBytes];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.x / a.chunks, chunk = blockIdx.x % a.chunks;
+  const int64_t t = chunk * kRows + 16 * wave + (lane & 15);
+  const bool valid = t < a.tokens;
+  const char* arow = valid ? a.a + b * a.a_bstride + t * a.a_tstride : nullptr;
+  const char* grow = valid ? a.g + b * a.g_bstride + t * a.g_tstride : nullptr;
+
+  f32x4 pa[4], pg[4];
+  project_tile<DT>(arow, a.abytes, a.pin_t, a.pin_rstride, a.ka, lds, pa, tid, lane);
+  project_tile<DT>(grow, a.gbytes, a.pout_t, a.pout_rstride, a.kg, lds, pg, tid, lane);
+
+  // Park both projected chunks (tokens x 64, fp32) in LDS; the stage buffers
+  // are free (project_tile ends with a barrier).
+  float* ap = (float*)lds;        // [64 tokens][64]
+  float* gp = ap + kRows * kCols;  // [64 tokens][64]
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = 16 * wave + acc16_row(e, lane);
+      const int col = 16 * cb + acc16_col(lane);
+      const bool tv = chunk * kRows + tok < a.tokens;
+      const float bias = (a.bias_in && col < a.ka && tv) ? a.bias_in[col] : 0.f;
+      ap[tok * kCols + col] = pa[cb][e] + bias;
+      gp[tok * kCols + col] = pg[cb][e];
+    }
+  __syncthreads();
+  // M[o][i] = sum_tok gp[tok][o] * ap[tok][i]: thread -> one o, 16 consecutive i.
+  const int o = tid >> 2, i0 = (tid & 3) * 16;
+  float m[16];
+#pragma unroll
+  for (int x = 0; x < 16; ++x) m[x] = 0.f;
+  for (int tok = 0; tok < kRows; ++tok) {
+    const float gv = gp[tok * kCols + o];
+    const float* arow_l = ap + tok * kCols + i0;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) m[x] += gv * arow_l[x];
+  }
+  if (o < a.kg) {
+    float* dst = a.partial + ((b * a.chunks + chunk) * a.kg + o) * a.ka;
+#pragma unroll
+    for (int x = 0; x < 16; ++x)
+      if (i0 + x < a.ka) dst[i0 + x] = m[x];
+  }
+}
+
+template <int OT>
+__global__ void project_outer_reduce(const float* __restrict__ partial, int64_t batch, int64_t chunks,
+                                     int64_t width, char* out, int64_t out_bstride) {
+  const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (f >= width) return;
+  float s = 0.f;
+  for (int64_t c = 0; c < chunks; ++c) s += partial[(b * chunks + c) * width + f];
+  Elem<OT>::store(out, b * out_bstride + f, s);
+}
+
+int check_rows(const void* p, int64_t rstride_bytes, const char* who, const char* what) {
+  if (((uintptr_t)p & 15) || (rstride_bytes % 16))
+    return set_error(DA_ERR_INVALID, "%s: %s rows must be 16-byte aligned", who, what);
+  return DA_OK;
+}
+
+}  // namespace
+}  // namespace da
+
+extern "C" {
+
+int da_project_rows(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rstride,
+                    const void* pt, int64_t k, int64_t pt_rstride, const float* bias, void* out,
+                    int out_dtype, int64_t out_rstride, void* stream) {
+  using namespace da;
+  const char* who = "da_project_rows";
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype", who);
+  if (rows < 0 || d < 0 || k < 0) return set_error(DA_ERR_INVALID, "%s: negative size", who);
+  if (rows == 0 || k == 0) return DA_OK;
+  if (!x || !pt || !out) return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if ((d * es) % 16) return set_error(DA_ERR_INVALID, "%s: d must be a multiple of %lld", who, (long long)(16 / es));
+  if (out_rstride < k) return set_error(DA_ERR_INVALID, "%s: out row stride < k", who);
+  int rc = check_rows(x, x_rstride * es, who, "x");
+  if (rc) return rc;
+  rc = check_rows(pt, pt_rstride * es, who, "P^T");
+  if (rc) return rc;
+  RowsArgs a;
+  a.x = (const char*)x;
+  a.rows = rows;
+  a.wbytes = d * es;
+  a.x_rstride = x_rstride * es;
+  a.pt = (const char*)pt;
+  a.pt_rstride = pt_rstride * es;
+  a.k = k;
+  a.bias = bias;
+  a.out = (char*)out;
+  a.out_rstride = out_rstride;
+  const int64_t gx = (rows + kRows - 1) / kRows, gy = (k + kCols - 1) / kCols;
+  if (gx > 0x7fffffffLL || gy > 65535) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+  dim3 grid((unsigned)gx, (unsigned)gy);
+  hipStream_t st = (hipStream_t)stream;
+#define DA_PR(DT)                                                                           \
+  switch (out_dtype) {                                                                      \
+    case DA_F32: project_rows_kernel<DT, DA_F32><<<grid, kThreads, 0, st>>>(a); break;      \
+    case DA_BF16: project_rows_kernel<DT, DA_BF16><<<grid, kThreads, 0, st>>>(a); break;    \
+    default: project_rows_kernel<DT, DA_F16><<<grid, kThreads, 0, st>>>(a); break;          \
+  }
+  switch (dtype) {
+    case DA_BF16: DA_PR(DA_BF16) break;
+    case DA_F16: DA_PR(DA_F16) break;
+    default: DA_PR(DA_F32) break;
+  }
+#undef DA_PR
+  return check_launch(who);
+}
+
+int da_project_outer_workspace(int64_t batch, int64_t tokens, int64_t ka, int64_t kg, size_t* bytes) {
+  if (batch < 0 || tokens < 0 || ka < 0 || kg < 0 || !bytes)
+    return da::set_error(DA_ERR_INVALID, "da_project_outer_workspace: bad arguments");
+  const int64_t chunks = (tokens + da::kRows - 1) / da::kRows;
+  *bytes = (size_t)(batch * chunks * ka * kg) * sizeof(float);
+  return DA_OK;
+}
+
+int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens, int64_t K,
+                     int64_t D, int64_t a_bstride, int64_t a_tstride, int64_t g_bstride,
+                     int64_t g_tstride, const void* pin_t, int64_t ka, int64_t pin_rstride,
+                     const float* bias_in, const void* pout_t, int64_t kg, int64_t pout_rstride,
+                     void* out, int out_dtype, int64_t out_bstride, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  using namespace da;
+  const char* who = "da_project_outer";
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype", who);
+  if (batch < 0 || tokens < 0 || K < 0 || D < 0 || ka < 0 || kg < 0)
+    return set_error(DA_ERR_INVALID, "%s: negative size", who);
+  if (ka > kCols || kg > kCols)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: projected widths above %d (got %lld, %lld)", who, kCols,
+                     (long long)ka, (long long)kg);
+  if (batch == 0 || ka == 0 || kg == 0) return DA_OK;
+  if (tokens == 0) return set_error(DA_ERR_INVALID, "%s: tokens must be >= 1", who);
+  if (!a || !g || !pin_t || !pout_t || !out) return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if ((K * es) % 16 || (D * es) % 16)
+    return set_error(DA_ERR_INVALID, "%s: K and D must be multiples of %lld", who, (long long)(16 / es));
+  if (((a_bstride * es) | (a_tstride * es) | (g_bstride * es) | (g_tstride * es)) % 16 ||
+      (((uintptr_t)a | (uintptr_t)g) & 15))
+    return set_error(DA_ERR_INVALID, "%s: factor rows must be 16-byte aligned", who);
+  int rc = check_rows(pin_t, pin_rstride * es, who, "P_in^T");
+  if (rc) return rc;
+  rc = check_rows(pout_t, pout_rstride * es, who, "P_out^T");
+  if (rc) return rc;
+  if (out_bstride < ka * kg) return set_error(DA_ERR_INVALID, "%s: out batch stride < kg*ka", who);
+  size_t need = 0;
+  da_project_outer_workspace(batch, tokens, ka, kg, &need);
+  if (!workspace || workspace_bytes < need)
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace needs %zu bytes", who, need);
+  OuterArgs o;
+  o.a = (const char*)a;
+  o.g = (const char*)g;
+  o.batch = batch;
+  o.tokens = tokens;
+  o.a_bstride = a_bstride * es;
+  o.a_tstride = a_tstride * es;
+  o.g_bstride = g_bstride * es;
+  o.g_tstride = g_tstride * es;
+  o.abytes = K * es;
+  o.gbytes = D * es;
+  o.pin_t = (const char*)pin_t;
+  o.pout_t = (const char*)pout_t;
+  o.pin_rstride = pin_rstride * es;
+  o.pout_rstride = pout_rstride * es;
+  o.ka = (int)ka;
+  o.kg = (int)kg;
+  o.bias_in = bias_in;
+  o.chunks = (tokens + kRows - 1) / kRows;
+  o.partial = (float*)workspace;
+  const int64_t blocks = batch * o.chunks;
+  if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case DA_BF16: project_outer_kernel<DA_BF16><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+    case DA_F16: project_outer_kernel<DA_F16><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+    default: project_outer_kernel<DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+  }
+  rc = check_launch("da_project_outer(chunks)");
+  if (rc) return rc;
+  const int64_t width = ka * kg;
+  dim3 g2((unsigned)((width + 255) / 256), (unsigned)batch);
+  switch (out_dtype) {
+    case DA_F32: project_outer_reduce<DA_F32><<<g2, 256, 0, st>>>(o.partial, batch, o.chunks, width, (char*)out, out_bstride); break;
+    case DA_BF16: project_outer_reduce<DA_BF16><<<g2, 256, 0, st>>>(o.partial, batch, o.chunks, width, (char*)out, out_bstride); break;
+    default: project_outer_reduce<DA_F16><<<g2, 256, 0, st>>>(o.partial, batch, o.chunks, width, (char*)out, out_bstride); break;
+  }
+  return check_launch("da_project_outer(reduce)");
+}
+
+}  // extern "C"

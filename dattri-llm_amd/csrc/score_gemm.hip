@@ -9,12 +9,14 @@
 //
 // The product is skinny (B1, B2 in the tens, widths up to 10^8) and bound by
 // streaming both operands from HBM once.  The flattened width of every layer
-// is cut into chunks; a workgroup owns one chunk of one layer for a 32-row x
-// 64-row (side-1 x side-2) output tile.  Each lane loads 16-byte pieces of a
-// 128-byte run of its row straight into MFMA operand registers (no LDS: every
-// element is used by exactly one MFMA of the tile), the four waves split the
-// chunk, combine through LDS, and write one fp32 partial tile; a second kernel
-// sums the partials of each output in a fixed order.
+// is cut into chunks; a workgroup owns one chunk of one layer for a 16-row x
+// 64-row (side-1 x side-2) output tile and runs 16x16x32 MFMAs straight from
+// registers (every element is used by exactly one MFMA of the tile, so there
+// is nothing to share through LDS).  In a 16x16 MFMA four lanes serve one
+// row; they read 64 contiguous bytes of it per load instruction, and the same
+// element-to-k assignment is used on both sides, so the sum is exact in any
+// order.  The four waves split the chunk, combine through LDS and write one
+// fp32 partial tile; a second kernel sums the partials in a fixed order.
 #include "common.h"
 
 namespace da {
@@ -22,9 +24,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxLayers = 32;
-constexpr int kTileM = 32;  // side-1 rows per workgroup
-constexpr int kTileN = 64;  // side-2 rows per workgroup
-constexpr int kRun = 128;   // bytes of one row a lane reads per step group (8 x 16 B)
+constexpr int kTileM = 16;   // side-1 rows per workgroup
+constexpr int kTileN = 64;   // side-2 rows per workgroup (4 MFMA blocks)
+constexpr int kStep = 256;   // bytes of width per row and wave iteration
+constexpr int kUnit = 4 * kStep;  // chunk granularity: one iteration of every wave
 
 struct LayerDev {
   const char* m1;
@@ -37,11 +40,11 @@ struct LayerDev {
 struct ScoreArgs {
   LayerDev layers[kMaxLayers];
   int n_layers;
-  int64_t chunk_bytes;  // bytes of width per chunk (multiple of 4 * 2 * kRun)
+  int64_t chunk_bytes;  // bytes of width per chunk (multiple of kUnit)
   int64_t n_chunks;
   int64_t b1, b2;
   int64_t tiles_n;      // ceil(b2 / kTileN)
-  float* partial;       // [n_chunks][b1][b2]
+  float* partial;       // [b1][b2][n_chunks]
 };
 
 template <int DT>
@@ -57,78 +60,82 @@ __global__ __launch_bounds__(kThreads) void score_gemm_chunks(ScoreArgs s) {
   const int64_t c1 = min(c0 + s.chunk_bytes, L.bytes);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 31, h = lane >> 5;
-  // Side-1 row (one 32-row block) and side-2 rows (two 32-row blocks) of this lane.
+  const int r = lane & 15, q = lane >> 4;
   const int64_t i = tm * kTileM + r;
-  const int64_t j0 = tn * kTileN + r, j1 = j0 + 32;
   const char* p1 = i < s.b1 ? L.m1 + i * L.ld1 : nullptr;
-  const char* q0 = j0 < s.b2 ? L.m2 + j0 * L.ld2 : nullptr;
-  const char* q1 = j1 < s.b2 ? L.m2 + j1 * L.ld2 : nullptr;
+  const char* p2[4];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const int64_t j = tn * kTileN + 16 * blk + r;
+    p2[blk] = j < s.b2 ? L.m2 + j * L.ld2 : nullptr;
+  }
 
-  f32x16 acc0 = {}, acc1 = {};
-  // The chunk is split into 4 quarter ranges, one per wave; each wave walks its
-  // range in groups of 2 * kRun bytes: lane half h reads the run at
-  // base + h * kRun, 16 bytes per MFMA step (same k-permutation on both sides).
+  f32x4 acc[4] = {};
   const int64_t span = c1 - c0;
-  const int64_t quarter = ((span + 4 * 2 * kRun - 1) / (4 * 2 * kRun)) * (2 * kRun);
+  const int64_t quarter = ((span + kUnit - 1) / kUnit) * kStep;
   const int64_t w0 = c0 + wave * quarter;
   const int64_t w1 = min(w0 + quarter, c1);
-  for (int64_t base = w0; base < w1; base += 2 * kRun) {
-    const int64_t run = base + h * kRun;
-    u32x4 va[8], vb0[8], vb1[8];
+  for (int64_t base = w0; base < w1; base += kStep) {
+    // MFMA step st reads bytes [base + 64*st + 16*q, +16) of the lane's row.
+    u32x4 va[4], vb[4][4];
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const int64_t off = run + 16 * st;
+    for (int st = 0; st < 4; ++st) {
+      const int64_t off = base + 64 * st + 16 * q;
       const bool in = off < w1;
       va[st] = (p1 && in) ? ld16(p1 + off) : u32x4{0, 0, 0, 0};
-      vb0[st] = (q0 && in) ? ld16(q0 + off) : u32x4{0, 0, 0, 0};
-      vb1[st] = (q1 && in) ? ld16(q1 + off) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+        vb[blk][st] = (p2[blk] && in) ? ld16(p2[blk] + off) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      Mfma32<DT>::mma(acc0, va[st], vb0[st]);
-      Mfma32<DT>::mma(acc1, va[st], vb1[st]);
-    }
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) Mfma16<DT>::mma(acc[blk], va[st], vb[blk][st]);
   }
 
   // Combine the four waves' tiles: waves 1..3 park theirs in LDS, wave 0 sums.
   if (wave > 0) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int row = acc_row(q, lane), col = acc_col(lane);
-      red[wave - 1][row * kTileN + col] = acc0[q];
-      red[wave - 1][row * kTileN + 32 + col] = acc1[q];
-    }
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        red[wave - 1][acc16_row(e, lane) * kTileN + 16 * blk + acc16_col(lane)] = acc[blk][e];
   }
   __syncthreads();
   if (wave == 0) {
-    float* dst = s.partial + chunk * s.b1 * s.b2;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int row = acc_row(q, lane), col = acc_col(lane);
-      const int64_t oi = tm * kTileM + row;
-      const int e0 = row * kTileN + col, e1 = e0 + 32;
-      const float v0 = acc0[q] + red[0][e0] + red[1][e0] + red[2][e0];
-      const float v1 = acc1[q] + red[0][e1] + red[1][e1] + red[2][e1];
-      const int64_t oj0 = tn * kTileN + col, oj1 = oj0 + 32;
-      if (oi < s.b1) {
-        if (oj0 < s.b2) dst[oi * s.b2 + oj0] = v0;
-        if (oj1 < s.b2) dst[oi * s.b2 + oj1] = v1;
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = acc16_row(e, lane), col = 16 * blk + acc16_col(lane);
+        const int x = row * kTileN + col;
+        const float v = acc[blk][e] + red[0][x] + red[1][x] + red[2][x];
+        const int64_t oi = tm * kTileM + row, oj = tn * kTileN + col;
+        if (oi < s.b1 && oj < s.b2) s.partial[(oi * s.b2 + oj) * s.n_chunks + chunk] = v;
       }
-    }
   }
 }
 
-__global__ void score_gemm_reduce(const float* __restrict__ partial, int64_t n_chunks, int64_t b1,
-                                  int64_t b2, float* __restrict__ out, int64_t ld_row,
-                                  int64_t ld_col, int accumulate) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= b1 * b2) return;
-  const int64_t i = idx / b2, j = idx - i * b2;
-  float s = 0.f;
-  for (int64_t c = 0; c < n_chunks; ++c) s += partial[c * b1 * b2 + idx];
-  float* o = out + i * ld_row + j * ld_col;
-  *o = accumulate ? *o + s : s;
+// One workgroup per output: its n_chunks partials are contiguous; each thread
+// sums a fixed strided subset, then a fixed tree combines the threads.
+__global__ __launch_bounds__(256) void score_gemm_reduce(const float* __restrict__ partial,
+                                                         int64_t n_chunks, int64_t b1, int64_t b2,
+                                                         float* __restrict__ out, int64_t ld_row,
+                                                         int64_t ld_col, int accumulate) {
+  __shared__ float red[4];
+  const int64_t idx = blockIdx.x;
+  const float* p = partial + idx * n_chunks;
+  float v = 0.f;
+  for (int64_t c = threadIdx.x; c < n_chunks; c += 256) v += p[c];
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float sum = (red[0] + red[1]) + (red[2] + red[3]);
+    const int64_t i = idx / b2, j = idx - i * b2;
+    float* o = out + i * ld_row + j * ld_col;
+    *o = accumulate ? *o + sum : sum;
+  }
 }
 
 struct Plan {
@@ -157,8 +164,8 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
     total += L.width * es;
   }
   // Aim for ~4096 chunks over all layers (16 waves per CU), at least one
-  // 4-wave step group (4 * 2 * kRun bytes) per chunk.
-  const int64_t unit = 4 * 2 * kRun;
+  // iteration of every wave (kUnit bytes) per chunk.
+  const int64_t unit = kUnit;
   int64_t cb = (total / 4096 + unit - 1) / unit * unit;
   if (cb < unit) cb = unit;
   p->chunk_bytes = cb;
@@ -234,7 +241,8 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
   rc = check_launch("da_score_gemm(chunks)");
   if (rc) return rc;
   const int64_t n = b1 * b2;
-  score_gemm_reduce<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
+  if (n > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_score_gemm: too many outputs");
+  score_gemm_reduce<<<(unsigned)n, 256, 0, st>>>(
       (const float*)workspace, p.n_chunks, b1, b2, out, ld_row, ld_col, accumulate);
   return check_launch("da_score_gemm(reduce)");
 }

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdattri_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DA_F32, DA_F16, DA_BF16 = 0, 1, 2
 DA_OK, DA_ERR_INVALID, DA_ERR_UNSUPPORTED, DA_ERR_HIP, DA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -58,7 +58,7 @@ _SIDE = ctypes.POINTER(FactorSide)
 SIGNATURES: dict[str, tuple[object, list]] = {
     "da_abi_version": (_I32, []),
     "da_last_error": (ctypes.c_char_p, []),
-    "da_selftest_mfma": (_I32, [_I32, _P, _P, _P, _P]),
+    "da_selftest_mfma": (_I32, [_I32, _I32, _P, _P, _P, _P]),
     "da_ghost_gram_workspace": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
     "da_ghost_gram": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, _P, _I64, _I32, _P, _SZ, _P]),
 }
@@ -97,6 +97,24 @@ SIGNATURES.update(
             _I32,
             [_P, _I32, _I64, _I64, _I64, _I32, ctypes.c_float, _P, _I32, _I64, _P],
         ),
+    }
+)
+
+_FP = ctypes.POINTER(ctypes.c_float)
+SIGNATURES.update(
+    {
+        "da_project_rows": (
+            _I32,
+            [_P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I32, _I64, _P],
+        ),
+        "da_project_outer_workspace": (_I32, [_I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)]),
+        "da_project_outer": (
+            _I32,
+            [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _P,
+             _I64, _I64, _P, _I32, _I64, _P, _SZ, _P],
+        ),
+        "da_moe_topk": (_I32, [_P, _I32, _I64, _I32, _I32, _I64, _P, _P, _P]),
+        "da_counting_sort": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _I64, _I32, _P, _P, _P]),
     }
 )
 

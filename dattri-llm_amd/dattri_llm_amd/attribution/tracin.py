@@ -1,0 +1,109 @@
+"""TracIn / GradCos on the MI355X scoring path.
+
+The scoring half of ``dattri_llm/attribution/algorithm/tracin.py`` and
+``attribution/base.py``: the inner product is the layerwise cross-gram
+(base.py:657-675, tracin.py:92-108), GradCos divides by whole-model gradient
+norms (tracin.py:125-148), and the query block is routed once before scoring
+(``_route_test_rep``, base.py:586-655): layers the cost rule prefers dense are
+materialized (largest flop saving first, under a byte budget), norm layers are
+materialized, and the remaining factorized layers are finalized.
+"""
+
+from __future__ import annotations
+
+from typing import ClassVar
+
+import torch
+
+from dattri_llm_amd.attribution.score import AttributionScore
+from dattri_llm_amd.attribution.utils import finalize_factors, score_sources
+from dattri_llm_amd.gradient import ops
+from dattri_llm_amd.gradient.gradient import Factorized, Gradient
+from dattri_llm_amd.utils.cache import CacheBudget
+
+
+class TracInAttributor:
+    """Gradient-dot (TracIn) or cosine (GradCos) attribution over gradient sources.
+
+    Args:
+        train_batch_size: train samples per scoring block (the reference's
+            ``per_device_train_batch_size``), used by the query routing rule.
+        device: where scoring runs.
+        cache_budget: budget factory ``device -> CacheBudget`` for the dense query cache.
+    """
+
+    algorithm: ClassVar[str] = "TracIn"
+
+    def __init__(self, train_batch_size: int = 1, device="cuda", *, cache_budget=None) -> None:
+        self.train_batch_size = train_batch_size
+        self.device = torch.device(device)
+        self._budget = cache_budget or (lambda dev: CacheBudget(dev))
+        self._metric = "dot"
+
+    def _set_metric(self, normalized_grad: bool) -> None:
+        self._metric = "cosine" if normalized_grad else "dot"
+        self.algorithm = "GradCos" if normalized_grad else "TracIn"
+
+    def route_test_rep(self, test_rep: Gradient) -> Gradient:
+        """The query routing of base.py:586-655."""
+        b_train = self.train_batch_size or 1
+        candidates = []
+        for name in test_rep.layer_names:
+            value = test_rep.data[name]
+            if not isinstance(value, Factorized):
+                continue
+            lt = test_rep.layer_types[name]
+            if not (ops.is_linear(lt) or ops.is_conv(lt) or ops.is_conv_transpose(lt)):
+                candidates.append((float("inf"), name))
+                continue
+            b_test, s, k, d = ops.effective_dims(value, lt)
+            if ops.maybe_use_materialized_gram(b_train, b_test, s, k, d):
+                cost_f = b_train * b_test * s * s * (d + k)
+                cost_m = (b_train + b_test) * s * d * k + b_train * b_test * d * k
+                candidates.append((cost_f - cost_m, name))
+        budget = self._budget(test_rep.device)
+        held = 0
+        dense = []
+        for _saving, name in sorted(candidates, reverse=True):
+            layer = test_rep.select_layers([name])
+            growth = max(layer.materialized_nbytes - layer.nbytes, 0)
+            if budget.fits(growth, held):
+                dense.append(name)
+                held += growth
+        if dense:
+            test_rep = test_rep.map_layers(lambda _n, v, t: ops.materialize(v, t), layers=dense, consume=True)
+        return finalize_factors(test_rep, budget=budget, held=held)
+
+    def inner_product(self, train_rep: Gradient, test_rep: Gradient, *, dense_cache=None) -> torch.Tensor:
+        if not any(name in test_rep.data for name in train_rep.data):
+            return torch.zeros(train_rep.batch_size, test_rep.batch_size, device=self.device)
+        dot = ops.layerwise_cross_dot(train_rep, test_rep, dense_cache=dense_cache)
+        if self._metric == "dot":
+            return dot
+        shared = [n for n in train_rep.data if n in test_rep.data]
+        n_tr = self._norm(train_rep, shared, dense_cache)
+        n_te = self._norm(test_rep, shared, None)
+        return dot / (n_tr[:, None] * n_te[None, :] + 1e-8)
+
+    @staticmethod
+    def _norm(rep: Gradient, layers, dense_cache) -> torch.Tensor:
+        total = torch.zeros(rep.batch_size, device=rep.device)
+        for name in layers:
+            value = rep.data[name]
+            if dense_cache is not None and name in dense_cache:
+                value = dense_cache.get(name)
+            sq = ops.grad_norm_sq(value, rep.layer_types[name]).to(total.dtype)
+            total += sq.expand(rep.batch_size) if sq.shape[0] == 1 else sq
+        return total.clamp_min(0).sqrt()
+
+    def attribute_sources(self, train_source, test_source, *, normalized_grad: bool = False,
+                          batch_size: int | None = None) -> AttributionScore:
+        """Score two ``(step, Gradient, hashes)`` sources (base.py:704-770)."""
+        self._set_metric(normalized_grad)
+        scores, row_ids, row_steps, test_ids, _ = score_sources(
+            train_source, test_source, self.device, inner_product=self.inner_product,
+            transform_test=self.route_test_rep, batch_size=batch_size or self.train_batch_size,
+        )
+        return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
+                                algorithm=self.algorithm,
+                                algorithm_meta={"normalized_grad": normalized_grad}, layer_name=None)

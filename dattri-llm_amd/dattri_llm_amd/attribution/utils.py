@@ -1,0 +1,151 @@
+"""The inner-product scoring loop over gradient sources.
+
+Mirrors ``dattri_llm/attribution/utils.py`` (``finalize_factors`` :180-236,
+``score_sources`` :239-440) and ``rebatch_blocks``
+(``dattri_llm/gradient/streaming.py:197-268``).  Sources are iterables of
+``(step, Gradient, hashes)`` blocks -- the reference's ``GradientSource``
+protocol -- so its ``GradientStreamer`` / ``DiskGradientSource`` plug in
+unchanged.  Scores are accumulated on the device in fp32 and copied to the
+host once per train block (the reference syncs once per train x test block
+pair).
+"""
+
+from __future__ import annotations
+
+from typing import TYPE_CHECKING
+
+import torch
+
+from dattri_llm_amd.gradient import ops
+from dattri_llm_amd.gradient.gradient import Factorized, Gradient
+from dattri_llm_amd.utils.cache import CacheBudget, TensorCache
+
+if TYPE_CHECKING:
+    from collections.abc import Callable, Iterable, Iterator
+
+
+def finalize_factors(rep: Gradient, *, budget: CacheBudget | None = None, held: int = 0) -> Gradient:
+    """Preprocess every raw factorized layer once (utils.py:180-236).
+
+    Linear layers need no rewrite here: their bias column is applied inside
+    the kernels (an implicit ones column), so the raw capture *is* the final
+    form and keeping ``module_kwargs`` costs nothing.  Token-norm layers are
+    replaced by their final factors (x_hat, with the bias block) exactly as
+    the reference does, under the same budget rule."""
+    names = [
+        n for n, v in rep.data.items()
+        if isinstance(v, Factorized) and v.module_kwargs is not None and ops.is_norm(rep.layer_types[n])
+    ]
+    if not names:
+        return rep
+    charged = held
+
+    def finalize(_name, value: Factorized, layer_type):
+        nonlocal charged
+        a, g = ops.preprocess_factorized(value, layer_type)
+        final = Factorized(activation=a, pre_activation_grad=g, module_kwargs=None)
+        growth = max(final.nbytes - value.nbytes, 0)
+        if budget is not None and not budget.fits(growth, charged):
+            return value
+        charged += growth
+        return final
+
+    return rep.map_layers(finalize, layers=names, consume=True)
+
+
+def rebatch_blocks(source: Iterable, batch_size: int) -> Iterator[tuple[list[int], Gradient, list[str]]]:
+    """Re-batch dense blocks into ``batch_size``-sample batches; factorized
+    blocks pass one at a time (streaming.py:197-268)."""
+    if batch_size < 1:
+        raise ValueError(f"batch_size must be >= 1, got {batch_size}.")
+    pending: dict[str, list[torch.Tensor]] = {}
+    ids: list[str] = []
+    steps: list[int] = []
+    count = 0
+    meta = None
+
+    def build():
+        nonlocal pending, ids, steps, count
+        data = {n: t[0] if len(t) == 1 else torch.cat(t, dim=0) for n, t in pending.items()}
+        rep, lt, ix = meta
+        batch = (steps, Gradient(rep, data, lt, ix, validate_on_init=False), ids)
+        pending, ids, steps, count = {}, [], [], 0
+        return batch
+
+    for step, block, hashes in source:
+        if not all(isinstance(v, torch.Tensor) for v in block.data.values()):
+            if count:
+                yield build()
+            yield [step] * block.batch_size, block, list(hashes)
+            continue
+        meta = (block.representation, block.layer_types, block.indexing)
+        for name, tensor in block.data.items():
+            pending.setdefault(name, []).append(tensor)
+        ids.extend(hashes)
+        steps.extend([step] * block.batch_size)
+        count += block.batch_size
+        if count >= batch_size:
+            yield build()
+    if count:
+        yield build()
+
+
+def _merge_dense_test(cached: list) -> list:
+    """Stack all-dense cached test reps into one block (utils.py:159-177)."""
+    if len(cached) < 2:
+        return cached
+    stream = ((0, rep, cols) for rep, cols in cached)
+    merged = list(rebatch_blocks(stream, batch_size=sum(len(c) for _, c in cached)))
+    return [(rep, cols) for _s, rep, cols in merged]
+
+
+def score_sources(
+    train_source: Iterable,
+    test_source: Iterable,
+    device,
+    *,
+    inner_product: Callable,
+    transform_train: Callable | None = None,
+    transform_test: Callable | None = None,
+    batch_size: int = 1,
+    cache_budget: CacheBudget | None = None,
+):
+    """Score every train block against every cached test block
+    (utils.py:239-440, instance granularity, cached test side).
+
+    Returns ``(scores (rows, num_test) fp32 CPU, row_train_ids, row_steps, test_ids, None)``."""
+    transform_train = transform_train or (lambda g: g)
+    transform_test = transform_test or (lambda g: g)
+    budget = cache_budget if cache_budget is not None else CacheBudget(device)
+    test_ids: list[str] = []
+    index: dict[str, int] = {}
+    cached = []
+    for _step, test_g, hashes in test_source:
+        cols = []
+        for h in hashes:
+            if h not in index:
+                index[h] = len(test_ids)
+                test_ids.append(h)
+            cols.append(index[h])
+        cached.append((transform_test(test_g.to(device)), cols))
+    cached = _merge_dense_test(cached)
+    num_test = len(test_ids)
+    reuse = len(cached) > 1
+    chunks, row_ids, row_steps = [], [], []
+    for steps, train_g, ids in rebatch_blocks(train_source, batch_size):
+        train_rep = transform_train(train_g.to(device))
+        row = torch.zeros(train_rep.batch_size, num_test, dtype=torch.float32, device=device)
+        cache = TensorCache("memory", budget=budget) if reuse else None
+        for test_rep, cols in cached:
+            block = inner_product(train_rep, test_rep, dense_cache=cache).to(torch.float32)
+            if cols and cols == list(range(cols[0], cols[0] + len(cols))):
+                row[:, cols[0]:cols[0] + len(cols)] = block
+            else:
+                row[:, torch.tensor(cols, device=device)] = block
+        if cache is not None:
+            cache.clear()
+        chunks.append(row.cpu())
+        row_ids.extend(ids)
+        row_steps.extend(steps)
+    scores = torch.cat(chunks, dim=0) if chunks else torch.zeros(0, num_test)
+    return scores, row_ids, row_steps, test_ids, None

@@ -1,0 +1,6 @@
+"""Gradient data model and ops (the reference's ``dattri_llm.gradient`` surface on this path)."""
+
+from dattri_llm_amd.gradient import ops
+from dattri_llm_amd.gradient.gradient import Factorized, Gradient, GradientRecord
+
+__all__ = ["Factorized", "Gradient", "GradientRecord", "ops"]

@@ -1,0 +1,84 @@
+"""Layer-type-aware gradient operations on the MI355X kernels.
+
+Same public names and signatures as ``dattri_llm.gradient.ops`` for the
+scoring path (``dattri_llm/gradient/ops/__init__.py:123``): ``_factors``
+functions take raw batch-first ``(activation, pre_activation_grad)``
+tensors, the unsuffixed ones take :class:`Factorized` (or dense tensors).
+"""
+
+from dattri_llm_amd.gradient.ops import cost, dtypes, moe
+from dattri_llm_amd.gradient.ops.cost import CostModel, calibrate, get_routing_policy, set_routing_policy
+from dattri_llm_amd.gradient.ops.dot import (
+    cross_dot,
+    cross_dot_factors,
+    cross_gram,
+    dot,
+    dot_factors,
+    effective_dims,
+    grad_norm_sq,
+    grad_norm_sq_factors,
+    layerwise_cross_dot,
+    layerwise_cross_dot_per_token,
+    maybe_use_materialized_gram,
+    maybe_use_materialized_norm,
+    pairwise_dot,
+    pairwise_dot_factors,
+)
+from dattri_llm_amd.gradient.ops.dtypes import as_float, compute_dtype, get_compute_dtype, set_compute_dtype
+from dattri_llm_amd.gradient.ops.materialize import materialize, materialize_factors
+from dattri_llm_amd.gradient.ops.preprocess import (
+    extract_module_kwargs,
+    preprocess_factorized,
+    preprocess_factors,
+    to_3d,
+)
+from dattri_llm_amd.gradient.ops.projection import (
+    CAPTURE_STYLES,
+    MASK_KEYS,
+    PROJECTION_STYLES,
+    DattriProjector,
+    ProjectionMatrix,
+    apply_projection,
+    capture_projected,
+    gaussian_projector,
+    maybe_materialize_projected,
+    project_activation,
+    project_factorized,
+    project_factors,
+    project_gradient,
+    project_layer,
+    project_outer_factors,
+    should_materialize,
+)
+from dattri_llm_amd.gradient.ops.types import (
+    ALL_LAYER_TYPES,
+    CONV_TRANSPOSE_TYPES,
+    CONV_TYPES,
+    EMBEDDING_TYPES,
+    LINEAR_TYPES,
+    NORM_TYPES,
+    PARAM_GRAD_TYPES,
+    canonical_class_name,
+    is_conv,
+    is_conv_transpose,
+    is_embedding,
+    is_kfac_eligible,
+    is_linear,
+    is_norm,
+)
+
+__all__ = [
+    "ALL_LAYER_TYPES", "CAPTURE_STYLES", "CONV_TRANSPOSE_TYPES", "CONV_TYPES", "EMBEDDING_TYPES",
+    "LINEAR_TYPES", "MASK_KEYS", "NORM_TYPES", "PARAM_GRAD_TYPES", "PROJECTION_STYLES", "CostModel",
+    "DattriProjector", "ProjectionMatrix", "apply_projection", "as_float", "calibrate",
+    "canonical_class_name", "capture_projected", "compute_dtype", "cost", "cross_dot",
+    "cross_dot_factors", "cross_gram", "dot", "dot_factors", "dtypes", "effective_dims",
+    "extract_module_kwargs", "gaussian_projector", "get_compute_dtype", "get_routing_policy",
+    "grad_norm_sq", "grad_norm_sq_factors", "is_conv", "is_conv_transpose", "is_embedding",
+    "is_kfac_eligible", "is_linear", "is_norm", "layerwise_cross_dot", "layerwise_cross_dot_per_token",
+    "materialize", "materialize_factors", "maybe_materialize_projected", "maybe_use_materialized_gram",
+    "maybe_use_materialized_norm", "moe", "pairwise_dot", "pairwise_dot_factors", "preprocess_factorized",
+    "preprocess_factors", "project_activation", "project_factorized", "project_factors",
+    "project_gradient", "project_layer", "project_outer_factors", "set_compute_dtype",
+    "set_routing_policy", "should_materialize", "to_3d",
+]

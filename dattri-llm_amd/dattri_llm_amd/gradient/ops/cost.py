@@ -1,0 +1,132 @@
+"""Factorized-vs-materialized routing, re-calibrated to measured MI355X rates.
+
+The reference routes on flop counts alone (``dattri_llm/gradient/ops/dot.py:728-753``):
+materialize iff ``kappa * B1*B2*S^2*(D+K) >= (B1+B2)*S*D*K + B1*B2*D*K``.  On
+MI355X the two routes run on kernels with very different efficiencies -- the
+ghost route is one MFMA-bound kernel, the materialized route is an MFMA-bound
+dW kernel plus an HBM-bound score GEMM that streams every dense row -- so the
+time model prices each term at the rate its kernel actually achieves:
+
+    t_F = 2*B1*B2*S1*S2*(K+D) / R_ghost                               + 1 launch
+    t_M = 2*(B1*S1 + B2*S2)*D*K / R_mat
+          + (B1+B2)*D*K*e / R_stream   (dW written once and read once)  + 3 launches
+
+with ``e`` the element size.  The rates come from :func:`calibrate` (timed
+kernels on the current GPU) or the committed MI355X measurement.
+
+``set_routing_policy("calibrated")`` makes ``maybe_use_materialized_gram`` use
+this model; the default ``"flops"`` keeps the reference's rule bit-for-bit
+(its known-answer tests pin it).  Both routes are exact, so the policy changes
+speed, never scores.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+from dataclasses import asdict, dataclass
+
+_POLICIES = ("flops", "calibrated")
+_policy = "flops"
+_model = None
+RATES_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "mi355x_rates.json")
+
+
+def set_routing_policy(policy: str) -> str:
+    """Select ``"flops"`` (the reference rule) or ``"calibrated"``; returns the previous one."""
+    global _policy  # noqa: PLW0603
+    if policy not in _POLICIES:
+        raise ValueError(f"routing policy must be one of {_POLICIES}, got {policy!r}")
+    previous, _policy = _policy, policy
+    return previous
+
+
+def get_routing_policy() -> str:
+    return _policy
+
+
+@dataclass(frozen=True)
+class CostModel:
+    """Measured rates of the three kernels of the two routes."""
+
+    ghost_tflops: float
+    materialize_tflops: float
+    stream_gbs: float
+    launch_us: float = 8.0
+    elem_bytes: int = 2
+    source: str = ""
+
+    def time_factorized(self, b1, b2, s1, s2, k, d) -> float:
+        flops = 2.0 * b1 * b2 * s1 * s2 * (k + d)
+        return flops / (self.ghost_tflops * 1e12) + self.launch_us * 1e-6
+
+    def time_materialized(self, b1, b2, s1, s2, k, d) -> float:
+        flops = 2.0 * (b1 * s1 + b2 * s2) * d * k
+        stream = 2.0 * (b1 + b2) * d * k * self.elem_bytes
+        return (flops / (self.materialize_tflops * 1e12) + stream / (self.stream_gbs * 1e9)
+                + 3 * self.launch_us * 1e-6)
+
+    def prefers_materialized(self, b1, b2, s1, s2, k, d, kappa: float = 1.0) -> bool:
+        return kappa * self.time_factorized(b1, b2, s1, s2, k, d) >= self.time_materialized(b1, b2, s1, s2, k, d)
+
+    def save(self, path: str = RATES_FILE) -> None:
+        with open(path, "w") as f:
+            json.dump(asdict(self), f, indent=2)
+            f.write("\n")
+
+
+def calibrated_model() -> CostModel:
+    """The active calibrated model (loaded from the committed rates file)."""
+    global _model  # noqa: PLW0603
+    if _model is None:
+        with open(RATES_FILE) as f:
+            _model = CostModel(**json.load(f))
+    return _model
+
+
+def use_model(model: CostModel) -> None:
+    """Install a freshly calibrated model for this process."""
+    global _model  # noqa: PLW0603
+    _model = model
+
+
+def calibrate(device=None, repeats: int = 3) -> CostModel:
+    """Time the three kernels on the current GPU at mid-size shapes and return
+    the rates (TFLOP/s for the MFMA kernels, GB/s for the score stream)."""
+    import torch
+
+    from dattri_llm_amd import kernels
+
+    dev = torch.device(device or "cuda")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).to(bf)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize(dev)
+        best = float("inf")
+        for _ in range(repeats):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize(dev)
+            best = min(best, s.elapsed_time(e) * 1e-3)
+        return best
+
+    b, t, k = 32, 512, 4096
+    a1, g1 = rnd(b, t, k), rnd(b, t, k)
+    a2, g2 = rnd(8, t, k), rnd(8, t, k)
+    t_ghost = timed(lambda: kernels.ghost_gram(a1, g1, a2, g2))
+    ghost = 2.0 * b * 8 * t * t * 2 * k / t_ghost / 1e12
+    t_mat = timed(lambda: kernels.materialize_linear(a1[:8], g1[:8]))
+    mat = 2.0 * 8 * t * k * k / t_mat / 1e12
+    m1 = rnd(8, k * k)
+    m2 = rnd(64, k * k)
+    t_score = timed(lambda: kernels.score_gemm([(m1, m2)]))
+    stream = (8 + 64) * k * k * 2 / t_score / 1e9
+    name = torch.cuda.get_device_name(dev)
+    return CostModel(round(ghost, 1), round(mat, 1), round(stream, 1), source=f"calibrate() on {name}")

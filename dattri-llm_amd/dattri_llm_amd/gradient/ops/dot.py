@@ -1,0 +1,354 @@
+"""Gradient inner products on the MI355X kernels.
+
+Mirrors ``dattri_llm/gradient/ops/dot.py``:
+
+* :func:`cross_gram` (dot.py:36-118) -- per-layer ``K[i, j] = <dW1_i, dW2_j>``;
+  the factorized route is the fused ghost kernel (``da_ghost_gram``), the
+  materialized route is the dW kernel on both sides plus the score GEMM, the
+  norm route is the fused norm-gradient kernel plus the score GEMM.
+* :func:`cross_dot` / :func:`cross_dot_factors` (dot.py:121-146, :478-517) --
+  raw captures are preprocessed *inside* the kernels (implicit bias column,
+  x_hat in registers) instead of by concatenation copies.
+* :func:`layerwise_cross_dot` (dot.py:532-604) -- all dense layer pairs of a
+  block go through ONE multi-layer score-GEMM launch and factorized pairs
+  accumulate into the same fp32 total.
+* the routing rules (dot.py:686-753), looked up through this module's globals
+  so the reference's ``pin_route`` monkeypatching still steers ``cross_gram``.
+
+Every product accumulates in fp32; results are returned in the resolved
+compute dtype (the reference's contract).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import TYPE_CHECKING
+
+import torch
+
+from dattri_llm_amd import kernels
+from dattri_llm_amd.gradient.ops import cost, dtypes
+from dattri_llm_amd.gradient.ops.materialize import (
+    linear_dense,
+    materialize,
+    norm_grad_from_final,
+    norm_grad_from_raw,
+)
+from dattri_llm_amd.gradient.ops.preprocess import final_linear, to_3d
+from dattri_llm_amd.gradient.ops.types import (
+    PARAM_GRAD_TYPES,
+    TOKEN_NORM_TYPES,
+    is_conv,
+    is_conv_transpose,
+    is_embedding,
+    is_linear,
+    is_norm,
+    require_supported,
+)
+
+if TYPE_CHECKING:
+    from collections.abc import Iterable
+
+
+def _kernel_operands(*tensors):
+    aligned = dtypes.align(*tensors)
+    out_dtype = aligned[0].dtype
+    kd = dtypes.kernel_dtype(out_dtype)
+    return tuple(t.to(kd) for t in aligned), out_dtype
+
+
+def _dense_gram(m1: torch.Tensor, m2: torch.Tensor, out=None, accumulate=False) -> torch.Tensor:
+    """fp32 ``m1 @ m2.T`` of two dense (B, d) blocks via the score kernel."""
+    (m1, m2), _ = _kernel_operands(m1.reshape(m1.shape[0], -1), m2.reshape(m2.shape[0], -1))
+    return kernels.score_gemm([(m1, m2)], out=out, accumulate=accumulate)
+
+
+def _route(b1: int, b2: int, s: int, k: int, d: int) -> str:
+    # looked up through module globals (pin_route contract, run_ours.py:61-86)
+    return "materialized" if maybe_use_materialized_gram(b1, b2, s, k, d) else "factorized"
+
+
+def _linear_gram32(a1, g1, bias1, a2, g2, bias2, mode, out=None, accumulate=False):
+    """fp32 (B1, B2) cross-gram of linear factors with implicit bias columns."""
+    if bias1 != bias2:
+        raise ValueError("the two sides disagree on the bias column")
+    (a1, g1, a2, g2), _ = _kernel_operands(to_3d(a1), to_3d(g1), to_3d(a2), to_3d(g2))
+    if a1.shape[-1] != a2.shape[-1] or g1.shape[-1] != g2.shape[-1]:
+        raise ValueError("the two sides disagree on the layer widths")
+    b1, s, k = a1.shape
+    b2 = a2.shape[0]
+    d = g1.shape[-1]
+    if mode == "auto":
+        mode = _route(b1, b2, s, k + int(bias1), d)
+    if mode == "materialized":
+        m1 = kernels.materialize_linear(a1, g1, bias=bias1)
+        m2 = kernels.materialize_linear(a2, g2, bias=bias2)
+        return kernels.score_gemm([(m1, m2)], out=out, accumulate=accumulate)
+    if mode != "factorized":
+        raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
+    return kernels.ghost_gram(a1, g1, a2, g2, bias=bias1, out=out, accumulate=accumulate)
+
+
+def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Tensor:
+    """Cross-gram ``K[i, j] = <dW1_i, dW2_j>`` on already-preprocessed factors
+    (dot.py:36-118)."""
+    if is_embedding(layer_type):
+        require_supported(layer_type, "cross_gram")
+    out_dtype = dtypes.resolve(a1, g1, a2, g2)
+    if is_norm(layer_type):
+        if layer_type not in TOKEN_NORM_TYPES:
+            require_supported(layer_type, "cross_gram")
+        return _dense_gram(norm_grad_from_final(a1, g1), norm_grad_from_final(a2, g2)).to(out_dtype)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, "cross_gram")
+    if to_3d(a1).ndim == 4:
+        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
+    return _linear_gram32(a1, g1, False, a2, g2, False, mode).to(out_dtype)
+
+
+def _side(a, g, layer_type, module_kwargs, include_bias):
+    """('norm', (B, d) dense) | ('linear', (a, g, bias)) for one raw side."""
+    if layer_type in TOKEN_NORM_TYPES:
+        if module_kwargs is not None:
+            return "norm", norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
+        return "norm", norm_grad_from_final(a, g)
+    if not is_linear(layer_type):
+        require_supported(layer_type, "cross_dot")
+    return "linear", final_linear(a, g, layer_type, module_kwargs, include_bias)
+
+
+def _cross_factors32(a1, g1, a2, g2, layer_type, mk1, mk2, include_bias, mode, out=None, accumulate=False):
+    kind, s1 = _side(a1, g1, layer_type, mk1, include_bias)
+    _, s2 = _side(a2, g2, layer_type, mk2, include_bias)
+    if kind == "norm":
+        return _dense_gram(s1, s2, out=out, accumulate=accumulate)
+    return _linear_gram32(*s1, *s2, mode, out=out, accumulate=accumulate)
+
+
+def cross_dot_factors(a1, g1, a2, g2, layer_type: str, module_kwargs1: dict | None = None,
+                      module_kwargs2: dict | None = None, include_bias: bool = True,
+                      mode: str = "auto") -> torch.Tensor:
+    """(B1, B2) cross-gram of two raw factor pairs (dot.py:121-146)."""
+    out_dtype = dtypes.resolve(a1, g1, a2, g2)
+    return _cross_factors32(a1, g1, a2, g2, layer_type, module_kwargs1, module_kwargs2,
+                            include_bias, mode).to(out_dtype)
+
+
+def pairwise_dot_factors(a, g, layer_type: str, module_kwargs: dict | None = None,
+                         include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
+    """(B, B) pairwise Gram of one block (dot.py:149-163)."""
+    return cross_dot_factors(a, g, a, g, layer_type, module_kwargs, module_kwargs, include_bias, mode)
+
+
+def dot_factors(a1, g1, a2, g2, layer_type: str, module_kwargs1: dict | None = None,
+                module_kwargs2: dict | None = None, include_bias: bool = True) -> torch.Tensor:
+    """(B,) per-sample dots ``<dW1_i, dW2_i>`` (dot.py:307-357)."""
+    out_dtype = dtypes.resolve(a1, g1, a2, g2)
+    b = a1.shape[0]
+    if g2.shape[0] != b:
+        raise ValueError("dot_factors needs two blocks of one batch size")
+    kind, s1 = _side(a1, g1, layer_type, module_kwargs1, include_bias)
+    _, s2 = _side(a2, g2, layer_type, module_kwargs2, include_bias)
+    out = torch.empty(b, dtype=torch.float32, device=a1.device)
+    for i in range(b):
+        if kind == "norm":
+            out[i] = _dense_gram(s1[i : i + 1], s2[i : i + 1])[0, 0]
+        else:
+            x1, y1, bias1 = s1
+            x2, y2, bias2 = s2
+            out[i] = _linear_gram32(to_3d(x1)[i : i + 1], to_3d(y1)[i : i + 1], bias1,
+                                    to_3d(x2)[i : i + 1], to_3d(y2)[i : i + 1], bias2, "factorized")[0, 0]
+    return out.to(out_dtype)
+
+
+def _diag_gram(m: torch.Tensor) -> torch.Tensor:
+    """fp32 squared row norms of a dense (B, d) block."""
+    out = torch.empty(m.shape[0], dtype=torch.float32, device=m.device)
+    for i in range(m.shape[0]):
+        _dense_gram(m[i : i + 1], m[i : i + 1], out=out[i : i + 1].view(1, 1))
+    return out
+
+
+def grad_norm_sq_factors(a, g, layer_type: str, module_kwargs: dict | None = None,
+                         include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
+    """(B,) squared per-sample gradient norms (dot.py:365-411)."""
+    out_dtype = dtypes.resolve(a, g)
+    kind, side = _side(a, g, layer_type, module_kwargs, include_bias)
+    if kind == "norm":
+        return _diag_gram(side).to(out_dtype)
+    x, y, bias = side
+    x3, y3 = to_3d(x), to_3d(y)
+    s, k, d = x3.shape[1], x3.shape[-1] + int(bias), y3.shape[-1]
+    if mode == "auto":
+        mode = "materialized" if maybe_use_materialized_norm(s, k, d) else "factorized"
+    if mode == "materialized":
+        return _diag_gram(linear_dense(x3, y3, bias)).to(out_dtype)
+    out = torch.empty(x3.shape[0], dtype=torch.float32, device=x3.device)
+    for i in range(x3.shape[0]):
+        _linear_gram32(x3[i : i + 1], y3[i : i + 1], bias, x3[i : i + 1], y3[i : i + 1], bias,
+                       "factorized", out=out[i : i + 1].view(1, 1))
+    return out.to(out_dtype)
+
+
+def grad_norm_sq(f, layer_type: str, include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
+    """(B,) squared norms of one layer, whatever its form (dot.py:414-437)."""
+    if isinstance(f, torch.Tensor):
+        flat = f.reshape(f.shape[0], -1)
+        return _diag_gram(flat).to(dtypes.resolve(flat))
+    bf = f.as_batch_first()
+    return grad_norm_sq_factors(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
+                                include_bias, mode)
+
+
+def pairwise_dot(f, layer_type: str, include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
+    bf = f.as_batch_first()
+    return pairwise_dot_factors(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
+                                include_bias, mode)
+
+
+def dot(f1, f2, layer_type: str, include_bias: bool = True) -> torch.Tensor:
+    b1, b2 = f1.as_batch_first(), f2.as_batch_first()
+    return dot_factors(b1.activation, b1.pre_activation_grad, b2.activation, b2.pre_activation_grad,
+                       layer_type, b1.module_kwargs, b2.module_kwargs, include_bias)
+
+
+def _cross_dot32(f1, f2, layer_type, include_bias=True, mode="auto", out=None, accumulate=False):
+    if isinstance(f1, torch.Tensor) or isinstance(f2, torch.Tensor):
+        m1 = materialize(f1, layer_type, include_bias)
+        m2 = materialize(f2, layer_type, include_bias)
+        return _dense_gram(m1, m2, out=out, accumulate=accumulate)
+    b1, b2 = f1.as_batch_first(), f2.as_batch_first()
+    return _cross_factors32(b1.activation, b1.pre_activation_grad, b2.activation, b2.pre_activation_grad,
+                            layer_type, b1.module_kwargs, b2.module_kwargs, include_bias, mode,
+                            out=out, accumulate=accumulate)
+
+
+def _payload_dtype(f) -> torch.dtype:
+    if isinstance(f, torch.Tensor):
+        return dtypes.resolve(f)
+    return dtypes.resolve(f.activation, f.pre_activation_grad)
+
+
+def cross_dot(f1, f2, layer_type: str, include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
+    """(B1, B2) cross-gram of one layer in whatever form each side holds
+    (dot.py:478-517)."""
+    out_dtype = torch.promote_types(_payload_dtype(f1), _payload_dtype(f2)) \
+        if dtypes.get_compute_dtype() == "auto" else dtypes.resolve(torch.empty(0))
+    return _cross_dot32(f1, f2, layer_type, include_bias, mode).to(out_dtype)
+
+
+def _expand_broadcast(m: torch.Tensor, b1: int, b2: int) -> torch.Tensor:
+    return m.expand(b1 if m.shape[0] == 1 else m.shape[0], b2 if m.shape[1] == 1 else m.shape[1])
+
+
+def _batch(f) -> int:
+    if isinstance(f, torch.Tensor):
+        return f.shape[0]
+    return f.activation.shape[0 if f.batch_first else 1]
+
+
+def layerwise_cross_dot(train, test, *, layers: Iterable[str] | None = None, mode: str = "auto",
+                        dense_cache=None, reduce: str = "sum"):
+    """Layer-by-layer cross-gram of two gradient blocks, summed over layers
+    (dot.py:532-604)."""
+    if reduce not in {"sum", "none"}:
+        raise ValueError("reduce must be 'sum' or 'none'")
+    names = list(train.data) if layers is None else list(layers)
+    pairs = []  # (name, layer_type, train payload, test payload)
+    for name in names:
+        if name not in train.data or name not in test.data:
+            continue
+        layer_type = train.layer_types[name]
+        if layer_type == PARAM_GRAD_TYPES:
+            continue
+        tr, te = train.data[name], test.data[name]
+        if isinstance(te, torch.Tensor) and not isinstance(tr, torch.Tensor):
+            tr = (dense_cache.get_or_compute(name, lambda tr=tr, lt=layer_type: materialize(tr, lt))
+                  if dense_cache is not None else materialize(tr, layer_type))
+        pairs.append((name, layer_type, tr, te))
+    if reduce == "none":
+        return {n: cross_dot(tr, te, lt, mode=mode) for n, lt, tr, te in pairs}
+    if not pairs:
+        raise ValueError("No shared layers between the two gradient blocks.")
+    b_tr, b_te = train.batch_size, test.batch_size
+    out_dtype = None
+    for _n, _lt, tr, te in pairs:
+        d = torch.promote_types(_payload_dtype(tr), _payload_dtype(te))
+        out_dtype = d if out_dtype is None else torch.promote_types(out_dtype, d)
+    if dtypes.get_compute_dtype() != "auto":
+        out_dtype = dtypes.resolve(torch.empty(0))
+    device = next(p.device if isinstance(p, torch.Tensor) else p.activation.device
+                  for _n, _lt, tr, _te in pairs for p in (tr,))
+    total = torch.zeros(b_tr, b_te, dtype=torch.float32, device=device)
+    # Dense x dense pairs of full batch: one multi-layer score GEMM per dtype.
+    dense_groups: dict[torch.dtype, list] = {}
+    rest = []
+    for name, lt, tr, te in pairs:
+        full = _batch(tr) == b_tr and _batch(te) == b_te
+        if full and isinstance(tr, torch.Tensor) and isinstance(te, torch.Tensor):
+            (m1, m2), _ = _kernel_operands(tr.reshape(b_tr, -1), te.reshape(b_te, -1))
+            dense_groups.setdefault(m1.dtype, []).append((m1, m2))
+        else:
+            rest.append((name, lt, tr, te, full))
+    for group in dense_groups.values():
+        kernels.score_gemm(group, out=total, accumulate=True)
+    for _name, lt, tr, te, full in rest:
+        if full:
+            _cross_dot32(tr, te, lt, mode=mode, out=total, accumulate=True)
+        else:  # a broadcast (batch-1) layer's shared row counts for every sample
+            total += _expand_broadcast(_cross_dot32(tr, te, lt, mode=mode), b_tr, b_te)
+    return total.to(out_dtype)
+
+
+def layerwise_cross_dot_per_token(train, test, *, layers=None, reduce: str = "sum"):
+    """Per-token decomposition (dot.py:607-669) -- not on the MI355X path."""
+    raise NotImplementedError(
+        "token-granularity attribution (cross_gram_per_token) is not implemented on the MI355X path"
+    )
+
+
+# ---------------------------------------------------------------------------
+# Routing (dot.py:686-753)
+# ---------------------------------------------------------------------------
+
+
+def effective_dims(f, layer_type: str) -> tuple[int, int, int, int]:
+    """``(B, S, K, D)`` read from the raw factor shapes (dot.py:686-725)."""
+    bf = f.as_batch_first()
+    a, g = bf.activation, bf.pre_activation_grad
+    if bf.module_kwargs is None:
+        if a.ndim == 4:
+            return a.shape[0], a.shape[1], a.shape[-1], g.shape[-1]
+        return a.shape[0], math.prod(a.shape[1:-1]), a.shape[-1], g.shape[-1]
+    mk = bf.module_kwargs
+    groups = mk.get("groups", 1)
+    if is_conv(layer_type):
+        kprod = math.prod(mk["kernel_size"]) if "kernel_size" in mk else 1
+        return a.shape[0], math.prod(g.shape[2:]), a.shape[1] // groups * kprod, g.shape[1] // groups
+    if is_conv_transpose(layer_type):
+        kprod = math.prod(mk["kernel_size"]) if "kernel_size" in mk else 1
+        return a.shape[0], math.prod(a.shape[2:]), a.shape[1] // groups, g.shape[1] // groups * kprod
+    return a.shape[0], math.prod(a.shape[1:-1]), a.shape[-1], g.shape[-1]
+
+
+def maybe_use_materialized_gram(B1: int, B2: int, S: int, K: int, D: int, kappa: float = 1.0) -> bool:  # noqa: N803
+    """``True`` when materialize-then-GEMM is the cheaper cross-gram.
+
+    Under the default ``"flops"`` policy this is the reference's rule
+    (dot.py:728-745): materialize iff ``kappa * B1*B2*S^2*(D+K) >=
+    (B1+B2)*S*D*K + B1*B2*D*K``.  Under ``set_routing_policy("calibrated")``
+    the two routes are compared by their predicted MI355X time instead
+    (:mod:`dattri_llm_amd.gradient.ops.cost`).
+    """
+    if cost.get_routing_policy() == "calibrated":
+        return cost.calibrated_model().prefers_materialized(B1, B2, S, S, K, D, kappa)
+    cost_f = B1 * B2 * S * S * (D + K)
+    cost_m = (B1 + B2) * S * D * K + B1 * B2 * D * K
+    return kappa * cost_f >= cost_m
+
+
+def maybe_use_materialized_norm(S: int, K: int, D: int) -> bool:  # noqa: N803
+    """Per-sample norms: materialize iff ``S*(D+K) >= D*K`` (dot.py:748-753)."""
+    if cost.get_routing_policy() == "calibrated":
+        return cost.calibrated_model().prefers_materialized(1, 1, S, S, K, D, 1.0)
+    return S * (D + K) >= D * K

@@ -1,0 +1,112 @@
+"""Per-sample weight gradients of factorized captures (materialized form).
+
+Mirrors ``dattri_llm/gradient/ops/materialize.py:56-146`` for linear layers
+(``bmm(g^T, a)`` flattened to ``(B, out*in)``, index ``o*K + i``, with the bias
+column last) and token norms (``sum_t x_hat * g``, and ``[dgamma, dbeta]`` with
+a bias).  The linear case runs the ``da_materialize_linear`` MFMA kernel; the
+norm case runs ``da_norm_weight_grad``, which normalises in registers and never
+forms x_hat.  Results are in the resolved compute dtype with fp32 accumulation.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from dattri_llm_amd import kernels
+from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops.preprocess import (
+    final_linear,
+    fold_norm_rows,
+    norm_spec,
+    to_3d,
+)
+from dattri_llm_amd.gradient.ops.types import (
+    TOKEN_NORM_TYPES,
+    is_embedding,
+    is_linear,
+    is_norm,
+    require_supported,
+)
+
+
+def _operands(*tensors):
+    """Align to the compute dtype; kernels read fp32 for a float64 policy."""
+    aligned = dtypes.align(*tensors)
+    out_dtype = aligned[0].dtype
+    kd = dtypes.kernel_dtype(out_dtype)
+    return tuple(t.to(kd) for t in aligned), out_dtype
+
+
+def norm_grad_from_raw(x, g, layer_type: str, module_kwargs: dict, include_bias: bool = True):
+    """Fused preprocess + token sum of a raw token-norm capture -> (B, d[*2])."""
+    spec = norm_spec(x, layer_type, module_kwargs, include_bias)
+    x3 = fold_norm_rows(x, spec.width)
+    g3 = fold_norm_rows(g, spec.width)
+    (xo, go), out_dtype = _operands(x3, g3)
+    out = kernels.norm_weight_grad(xo, go, kind=spec.kind, eps=spec.eps, bias=spec.has_bias,
+                                   out_dtype=dtypes.kernel_dtype(out_dtype))
+    return out.to(out_dtype)
+
+
+def norm_grad_from_final(a, g):
+    """Token sum ``(a * g).sum(1)`` of already-preprocessed norm factors."""
+    (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
+    out = kernels.norm_weight_grad(ao, go, kind=2, eps=0.0, bias=False,
+                                   out_dtype=dtypes.kernel_dtype(out_dtype))
+    return out.to(out_dtype)
+
+
+def linear_dense(a, g, bias: bool) -> torch.Tensor:
+    """(B, D*(K+bias)) per-sample dW of linear factors, in the compute dtype."""
+    (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
+    out = kernels.materialize_linear(ao, go, bias=bias, out_dtype=dtypes.kernel_dtype(out_dtype))
+    return out.to(out_dtype)
+
+
+def materialize_factors(
+    a: torch.Tensor,
+    g: torch.Tensor,
+    layer_type: str,
+    module_kwargs: dict | None = None,
+    include_bias: bool = True,
+    per_token: bool = False,
+) -> torch.Tensor:
+    """Per-sample weight gradient ``(B, d)`` (materialize.py:56-116)."""
+    if is_embedding(layer_type):
+        if module_kwargs is None:
+            raise ValueError(
+                "Materializing an embedding gradient requires module_kwargs with 'num_embeddings' "
+                "(the weight's vocab size cannot be inferred from the captured factors)."
+            )
+        require_supported(layer_type, "materialize_factors")
+    if layer_type in TOKEN_NORM_TYPES:
+        if per_token:
+            if module_kwargs is not None:
+                spec = norm_spec(a, layer_type, module_kwargs, include_bias)
+                x_hat = kernels.norm_xhat(a, kind=spec.kind, eps=spec.eps)
+                x3, g3 = fold_norm_rows(x_hat, spec.width), fold_norm_rows(g, spec.width)
+                if spec.has_bias:
+                    x3 = torch.cat([x3, torch.ones_like(x3)], dim=-1)
+                    g3 = torch.cat([g3, g3], dim=-1)
+            else:
+                x3, g3 = to_3d(a), to_3d(g)
+            x3, g3 = dtypes.align(x3, g3)
+            return (x3 * g3).flatten(1)
+        if module_kwargs is not None:
+            return norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
+        return norm_grad_from_final(a, g)
+    if is_norm(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, "materialize_factors")
+    if a.ndim == 4:
+        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
+    a, g, bias = final_linear(a, g, layer_type, module_kwargs, include_bias)
+    return linear_dense(a, g, bias)
+
+
+def materialize(f, layer_type: str, include_bias: bool = True, per_token: bool = False) -> torch.Tensor:
+    """Per-sample weight gradient of one layer, whatever its form (materialize.py:119-146)."""
+    if isinstance(f, torch.Tensor):
+        return f.reshape(f.shape[0], -1)
+    bf = f.as_batch_first()
+    return materialize_factors(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
+                               include_bias, per_token)

@@ -1,0 +1,160 @@
+"""Preprocessing of raw hook captures into the (a, g) form the kernels contract.
+
+Mirrors ``dattri_llm/gradient/ops/preprocess.py`` for the layer families of the
+scoring path: linear layers (bias folded as a ones column, :436-437) and token
+norms (RMSNorm / LayerNorm x_hat, :366-384, computed by the ``da_norm_xhat``
+kernel, with the bias augmentation of ``norm.py:95-110``).  Conv, embedding and
+channel-norm layers raise ``NotImplementedError``.
+
+The public ``preprocess_factors`` returns exactly the reference's tensors.  The
+scoring kernels never need them: :func:`final_linear` and :func:`norm_spec`
+describe the same preprocessing so a kernel applies it on the fly (the bias is
+an implicit ones column, x_hat is recomputed in registers).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from dattri_llm_amd import kernels
+from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops.types import (
+    CONV_TRANSPOSE_TYPES,
+    CONV_TYPES,
+    TOKEN_NORM_TYPES,
+    is_linear,
+    is_norm,
+)
+
+NORM_KIND = {"nn.RMSNorm": 0, "nn.LayerNorm": 1}
+
+
+def to_3d(x: torch.Tensor) -> torch.Tensor:
+    """(B, D) -> (B, 1, D); (B, T, D) unchanged (preprocess.py:447-455)."""
+    return x.unsqueeze(1) if x.ndim == 2 else x
+
+
+def extract_module_kwargs(module, layer_type: str) -> dict:
+    """Minimal serialisable hyperparameters of a hooked module
+    (preprocess.py:231-298)."""
+    kwargs: dict = {"has_bias": getattr(module, "bias", None) is not None}
+    if layer_type in ("nn.Embedding", "nn.EmbeddingBag") and getattr(module, "scale_grad_by_freq", False):
+        raise NotImplementedError(
+            f"{layer_type} with scale_grad_by_freq=True is not supported: the inverse-frequency "
+            "gradient scaling is a whole-batch statistic that the factorized capture does not model."
+        )
+    if layer_type == "nn.Embedding":
+        kwargs["num_embeddings"] = module.num_embeddings
+        kwargs["padding_idx"] = module.padding_idx
+    elif layer_type in CONV_TYPES or layer_type in CONV_TRANSPOSE_TYPES:
+        for key in ("kernel_size", "stride", "padding", "dilation", "groups"):
+            kwargs[key] = getattr(module, key)
+    elif layer_type in ("nn.LayerNorm", "nn.RMSNorm"):
+        kwargs["normalized_shape"] = tuple(module.normalized_shape)
+        kwargs["eps"] = module.eps
+    elif layer_type == "nn.GroupNorm":
+        kwargs.update(num_groups=module.num_groups, num_channels=module.num_channels, eps=module.eps)
+    elif layer_type in ("nn.InstanceNorm1d", "nn.InstanceNorm2d", "nn.InstanceNorm3d"):
+        kwargs.update(num_features=module.num_features, eps=module.eps)
+    elif layer_type == "nn.EmbeddingBag":
+        kwargs.update(num_embeddings=module.num_embeddings, mode=module.mode, padding_idx=module.padding_idx)
+    return kwargs
+
+
+@dataclass(frozen=True)
+class NormSpec:
+    """How to normalise a token norm's raw activation inside a kernel."""
+
+    kind: int  # 0 RMSNorm, 1 LayerNorm
+    eps: float
+    has_bias: bool
+    width: int
+
+
+def norm_spec(a: torch.Tensor, layer_type: str, module_kwargs: dict, include_bias: bool) -> NormSpec:
+    """The reference's eps rule: ``eps=None`` is the raw activation dtype's
+    machine epsilon (norm.py:38-39, applied before any dtype alignment)."""
+    shape = tuple(module_kwargs.get("normalized_shape", (a.shape[-1],)))
+    if len(shape) != 1:
+        raise NotImplementedError(
+            f"{layer_type} over {len(shape)} trailing axes: the norm kernels normalise the last axis only"
+        )
+    eps = module_kwargs["eps"]
+    if eps is None:
+        eps = torch.finfo(a.dtype).eps
+    return NormSpec(NORM_KIND[layer_type], float(eps), bool(module_kwargs["has_bias"] and include_bias), shape[0])
+
+
+def fold_norm_rows(x: torch.Tensor, width: int) -> torch.Tensor:
+    """Every axis between batch and the normalised one becomes a position
+    axis (norm.py:65-87): (B, ..., d) -> (B, P, d); 2-D (B, d) -> (B, 1, d)."""
+    if x.ndim == 2:
+        return x.unsqueeze(1)
+    if x.ndim == 3:
+        return x
+    return x.reshape(x.shape[0], -1, width)
+
+
+def final_linear(a, g, layer_type: str, module_kwargs: dict | None, include_bias: bool):
+    """A linear layer's final factors without forming the ones column:
+    ``(a, g, bias)`` where ``bias`` says an implicit ones column follows ``a``."""
+    if module_kwargs is None:
+        return a, g, False
+    return a, g, bool(module_kwargs["has_bias"] and include_bias)
+
+
+def preprocess_factors(
+    a: torch.Tensor,
+    g: torch.Tensor,
+    layer_type: str,
+    module_kwargs: dict | None = None,
+    include_bias: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Transform raw captures into the reference's ``(a, g)`` form
+    (preprocess.py:301-439) for linear and token-norm layers."""
+    if module_kwargs is None:
+        return a, g
+    has_bias = module_kwargs["has_bias"] and include_bias
+    if layer_type in TOKEN_NORM_TYPES:
+        spec = norm_spec(a, layer_type, module_kwargs, include_bias)
+        x_hat = kernels.norm_xhat(a, kind=spec.kind, eps=spec.eps, out_dtype=a.dtype)
+        if x_hat.ndim > 3:
+            x_hat = x_hat.reshape(x_hat.shape[0], -1, spec.width)
+            g = g.reshape(g.shape[0], -1, spec.width)
+        if has_bias:
+            return torch.cat([x_hat, torch.ones_like(x_hat)], dim=-1), torch.cat([g, g], dim=-1)
+        return x_hat, g
+    if is_norm(layer_type) or not is_linear(layer_type):
+        raise NotImplementedError(
+            f"preprocess_factors: {layer_type!r} is outside the MI355X scoring path "
+            "(linear layers and RMSNorm/LayerNorm)."
+        )
+    if has_bias:
+        return torch.cat([a, torch.ones_like(a[..., :1])], dim=-1), g
+    return a, g
+
+
+def preprocess_factorized(f, layer_type: str, include_bias: bool = True):
+    """:func:`preprocess_factors` on a ``Factorized`` (batch-first-safe)."""
+    bf = f.as_batch_first()
+    return preprocess_factors(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs, include_bias)
+
+
+def flat_width(shape) -> int:
+    return math.prod(shape)
+
+
+__all__ = [
+    "NormSpec",
+    "extract_module_kwargs",
+    "final_linear",
+    "fold_norm_rows",
+    "norm_spec",
+    "preprocess_factorized",
+    "preprocess_factors",
+    "to_3d",
+]
+_ = dtypes  # re-exported policy lives next door

@@ -1,0 +1,334 @@
+"""Random projection of per-sample gradients on the MI355X kernels.
+
+Mirrors ``dattri_llm/gradient/ops/projection.py`` for the ``"logra"`` style:
+
+* :class:`DattriProjector` (projection.py:93-328) builds a layer's ``(d, k)``
+  matrix once from a projector factory following dattri's ``random_project``
+  protocol -- ``factory(feature, batch_size, *, proj_dim, proj_seed, device,
+  **kw) -> callable(x)`` -- by projecting identity chunks through it, and
+  caches it.  dattri itself is not available here, so the default factory is
+  :func:`gaussian_projector`, this package's own seeded Gaussian map (its
+  values are not dattri's; any dattri-protocol factory can be passed instead).
+* :class:`ProjectionMatrix` (projection.py:331-370) applies it with the
+  ``da_project_rows`` kernel; the bias row of a linear layer is a broadcast
+  add, so the ones-augmented activation is never formed.
+* the activation side uses ``proj_seed + 1`` and the gradient side
+  ``proj_seed`` (projection.py:437-440, :476-488).
+* when the capture style materializes the projected factors
+  (:func:`should_materialize`, projection.py:846-899), the projection of both
+  factors and the per-sample outer-product sum run as ONE kernel
+  (``da_project_outer``) that reads each factor row once.
+
+``"dense"`` and ``"mask"`` styles are not on the MI355X path.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from dattri_llm_amd import kernels
+from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops.materialize import linear_dense
+from dattri_llm_amd.gradient.ops.preprocess import to_3d
+from dattri_llm_amd.gradient.ops.types import is_embedding, is_linear, is_norm, require_supported
+from dattri_llm_amd.utils.cache import TensorCache
+
+PROJECTION_STYLES = ("logra", "dense", "mask")
+CAPTURE_STYLES = ("factorized", "materialized", "auto")
+MASK_KEYS = frozenset({"style", "proj_dim", "proj_seed", "include_bias", "device"})
+_IDENTITY_CHUNK_ROWS = 8192
+_FUSED_MAX_WIDTH = 64
+
+
+def gaussian_matrix(d: int, proj_dim: int, proj_seed: int) -> torch.Tensor:
+    """The default projector's ``(d, proj_dim)`` float32 matrix: i.i.d.
+    N(0, 1/proj_dim) entries drawn on the CPU from ``proj_seed``, so every
+    device and process gets the same map."""
+    gen = torch.Generator(device="cpu").manual_seed(int(proj_seed))
+    return torch.randn(d, proj_dim, generator=gen, dtype=torch.float32) / math.sqrt(proj_dim)
+
+
+def gaussian_projector(feature, batch_size, *, proj_dim: int, proj_seed: int = 0, device=None, **_kw):
+    """A dattri-protocol projector factory over :func:`gaussian_matrix`."""
+    d = feature.shape[-1]
+    matrix = gaussian_matrix(d, proj_dim, proj_seed)
+    dev = torch.device(device) if device is not None else feature.device
+    matrix = matrix.to(dev)
+
+    def project(x, ensemble_id=0):  # noqa: ARG001 - protocol
+        return x.to(matrix.dtype) @ matrix
+
+    project.matrix = matrix
+    return project
+
+
+def _projector_key(projector) -> str:
+    return f"{getattr(projector, '__module__', '')}.{getattr(projector, '__qualname__', repr(projector))}"
+
+
+class DattriProjector:
+    """A projection factory plus the cache of the matrices it builds."""
+
+    def __init__(self, projector=None, *, cache: TensorCache | None = None) -> None:
+        self._factory = projector
+        self._cache = cache if cache is not None else TensorCache("memory")
+
+    @classmethod
+    def coerce(cls, projector):
+        return projector if isinstance(projector, DattriProjector) else cls(projector)
+
+    @property
+    def factory(self):
+        if self._factory is None:
+            self._factory = gaussian_projector
+        return self._factory
+
+    @property
+    def cache(self) -> TensorCache:
+        return self._cache
+
+    def matrix(self, d_in: int, *, proj_dim: int, proj_seed: int, device, dtype, **proj_kwargs) -> torch.Tensor:
+        """The ``(d_in, proj_dim)`` matrix the factory applies, built once
+        (projection.py:150-200): identity chunks pushed through the factory."""
+        key = (_projector_key(self.factory), d_in, proj_dim, proj_seed, str(device), dtype,
+               tuple(sorted((k, repr(v)) for k, v in proj_kwargs.items())))
+        cached = self._cache.get(key)
+        if cached is not None:
+            return cached
+        if self.factory is gaussian_projector:
+            matrix = gaussian_matrix(d_in, proj_dim, proj_seed).to(device=device, dtype=dtype)
+        else:
+            rows = []
+            for start in range(0, d_in, _IDENTITY_CHUNK_ROWS):
+                stop = min(start + _IDENTITY_CHUNK_ROWS, d_in)
+                block = torch.zeros(stop - start, d_in, device=device, dtype=torch.float32)
+                idx = torch.arange(stop - start, device=device)
+                block[idx, idx + start] = 1.0
+                fn = self.factory(block, block.shape[0], proj_dim=proj_dim, proj_seed=proj_seed,
+                                  device=device, **proj_kwargs)
+                rows.append(fn(block))
+            matrix = torch.cat(rows, dim=0).to(dtype)
+        self._cache.put(key, matrix)
+        return matrix
+
+    def apply(self, x: torch.Tensor, *, proj_dim: int, proj_seed: int = 0, include_bias: bool = False,
+              **proj_kwargs) -> torch.Tensor:
+        """Project the last axis of *x* to ``proj_dim`` (projection.py:235-280)."""
+        (x,) = dtypes.as_float(x)
+        device = torch.device(proj_kwargs.pop("device", x.device))
+        x = x.to(device)
+        pm = self.resolve(x.shape[-1], proj_dim=proj_dim, proj_seed=proj_seed, include_bias=include_bias,
+                          device=device, dtype=x.dtype, **proj_kwargs)
+        return pm(x)
+
+    def resolve(self, d_in: int, *, proj_dim: int, proj_seed: int = 0, include_bias: bool = False,
+                device, dtype, **proj_kwargs) -> ProjectionMatrix:
+        """The projection :meth:`apply` would perform, resolved once (projection.py:282-311)."""
+        device = torch.device(proj_kwargs.pop("device", device))
+        matrix = self.matrix(d_in + (1 if include_bias else 0), proj_dim=proj_dim, proj_seed=proj_seed,
+                             device=device, dtype=dtype, **proj_kwargs)
+        return ProjectionMatrix(matrix, include_bias, d_in, dtype, device)
+
+    def clear(self) -> None:
+        self._cache.clear()
+
+    def close(self) -> None:
+        self._cache.clear()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *_exc) -> bool:
+        self.close()
+        return False
+
+
+class ProjectionMatrix:
+    """One layer's projection with everything but the kernel done
+    (projection.py:331-370).  Holds the transposed matrix the kernel reads and
+    the bias row in fp32."""
+
+    __slots__ = ("_bias32", "_pt", "bias_row", "d_in", "device", "dtype", "matrix", "proj_dim")
+
+    def __init__(self, matrix: torch.Tensor, include_bias: bool, d_in: int, dtype, device) -> None:
+        self.matrix = matrix[:-1] if include_bias else matrix
+        self.bias_row = matrix[-1] if include_bias else None
+        self.d_in, self.dtype, self.device = d_in, dtype, torch.device(device)
+        self.proj_dim = matrix.shape[1]
+        kd = dtypes.kernel_dtype(dtype)
+        self._pt = self.matrix.t().to(kd).contiguous()
+        self._bias32 = self.bias_row.to(torch.float32).contiguous() if self.bias_row is not None else None
+
+    def matches(self, x: torch.Tensor) -> bool:
+        return x.shape[-1] == self.d_in and x.dtype == self.dtype and x.device == self.device
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """Project the last axis of *x* (``(..., d_in)`` to ``(..., proj_dim)``)."""
+        if x.shape[-1] != self.d_in:
+            raise ValueError(f"projection expects width {self.d_in}, got {x.shape[-1]}")
+        kd = dtypes.kernel_dtype(self.dtype)
+        out = kernels.project_rows(x.to(kd), self._pt, bias=self._bias32, out_dtype=kd)
+        return out.to(self.dtype)
+
+    @property
+    def transposed(self) -> torch.Tensor:
+        """The (proj_dim, d_in) operand the kernels read."""
+        return self._pt
+
+    @property
+    def bias32(self):
+        return self._bias32
+
+
+def apply_projection(projector, x: torch.Tensor, *, proj_dim: int, proj_seed: int = 0,
+                     include_bias: bool = False, **proj_kwargs) -> torch.Tensor:
+    """:meth:`DattriProjector.apply` for a factory or a projector (projection.py:373-393)."""
+    return DattriProjector.coerce(projector).apply(x, proj_dim=proj_dim, proj_seed=proj_seed,
+                                                   include_bias=include_bias, **proj_kwargs)
+
+
+def _linear_only(layer_type: str, what: str) -> None:
+    if is_norm(layer_type):
+        raise ValueError(
+            f"factorized projection is undefined for {layer_type!r}: its gradient is not an outer "
+            "product of the factors -- use materialized projection"
+        )
+    if is_embedding(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, what)
+
+
+def _resolve_pair(projector, a, g, bias, proj_dim, proj_seed, proj_kwargs):
+    proj = DattriProjector.coerce(projector)
+    kw = dict(proj_kwargs)
+    device = torch.device(kw.pop("device", g.device))
+    dtype = dtypes.resolve(a, g)
+    p_in = proj.resolve(a.shape[-1], proj_dim=proj_dim, proj_seed=proj_seed + 1, include_bias=bias,
+                        device=device, dtype=dtype, **kw)
+    p_out = proj.resolve(g.shape[-1], proj_dim=proj_dim, proj_seed=proj_seed, device=device,
+                         dtype=dtype, **kw)
+    return p_in, p_out
+
+
+def project_factors(a, g, layer_type: str, projector, module_kwargs: dict | None = None,
+                    include_bias: bool = True, *, proj_dim: int, proj_seed: int = 0, **proj_kwargs):
+    """LoGRA: project both factors, keeping the outer-product structure
+    (projection.py:423-489).  Returns ``(a_p, g_p)``."""
+    _linear_only(layer_type, "project_factors")
+    bias = bool(module_kwargs is not None and module_kwargs["has_bias"] and include_bias)
+    a, g = dtypes.align(to_3d(a), to_3d(g))
+    p_in, p_out = _resolve_pair(projector, a, g, bias, proj_dim, proj_seed, proj_kwargs)
+    return p_in(a.to(p_in.device)), p_out(g.to(p_out.device))
+
+
+def project_activation(a, layer_type: str, projector, module_kwargs: dict | None, include_bias: bool = True,
+                       *, proj_dim: int, proj_seed: int = 0, **proj_kwargs) -> torch.Tensor:
+    """Project only a linear layer's activation (forward hook, projection.py:492-529)."""
+    if not is_linear(layer_type):
+        raise ValueError(f"project_activation is for linear layers only, got {layer_type!r}.")
+    with_bias = module_kwargs is not None and module_kwargs["has_bias"] and include_bias
+    a_f = to_3d(dtypes.align(a)[0])
+    return apply_projection(projector, a_f, proj_dim=proj_dim, proj_seed=proj_seed + 1,
+                            include_bias=with_bias, **proj_kwargs)
+
+
+def project_gradient(g, layer_type: str, projector, module_kwargs: dict | None, *, proj_dim: int,
+                     proj_seed: int = 0, **proj_kwargs) -> torch.Tensor:
+    """Project only a linear layer's gradient (backward hook, projection.py:532-560)."""
+    if not is_linear(layer_type):
+        raise ValueError(f"project_gradient is for linear layers only, got {layer_type!r}.")
+    g_f = to_3d(dtypes.align(g)[0])
+    return apply_projection(projector, g_f, proj_dim=proj_dim, proj_seed=proj_seed, **proj_kwargs)
+
+
+def project_outer_factors(a, g, layer_type: str, projector, module_kwargs: dict | None = None,
+                          include_bias: bool = True, *, proj_dim: int, proj_seed: int = 0,
+                          **proj_kwargs) -> torch.Tensor:
+    """``materialize_factors(*project_factors(...), "nn.Linear")`` in one pass:
+    the fused projection + per-sample outer-product kernel.  Returns
+    ``(B, k_g * k_a)``, index ``o * k_a + i``."""
+    _linear_only(layer_type, "project_outer_factors")
+    bias = bool(module_kwargs is not None and module_kwargs["has_bias"] and include_bias)
+    a, g = dtypes.align(to_3d(a), to_3d(g))
+    p_in, p_out = _resolve_pair(projector, a, g, bias, proj_dim, proj_seed, proj_kwargs)
+    return fused_outer(a, g, p_in, p_out)
+
+
+def fused_outer(a, g, p_in: ProjectionMatrix, p_out: ProjectionMatrix) -> torch.Tensor:
+    """(B, kg*ka) outer-product sum of the two projections of raw factors."""
+    out_dtype = dtypes.resolve(a, g)
+    kd = dtypes.kernel_dtype(out_dtype)
+    if p_in.proj_dim <= _FUSED_MAX_WIDTH and p_out.proj_dim <= _FUSED_MAX_WIDTH:
+        out = kernels.project_outer(a.to(kd), g.to(kd), p_in.transposed, p_out.transposed,
+                                    bias_in=p_in.bias32, out_dtype=kd)
+        return out.to(out_dtype)
+    # wider projections: the two row projections, then the dW kernel
+    return linear_dense(p_in(a), p_out(g), False).to(out_dtype)
+
+
+def capture_projected(a_p: torch.Tensor, g: torch.Tensor, p_out: ProjectionMatrix, materialize: bool):
+    """Backward-hook step of the LoGRA capture (hooks.py:631-648): the activation
+    was projected in the forward hook; project the gradient and either keep
+    the factor pair or contract it into the ``(B, k_g * k_a)`` per-sample block.
+    The contraction reads ``g`` once (identity projection on the small a_p side)."""
+    a_p, g = to_3d(a_p), to_3d(g)
+    if not materialize:
+        return a_p, p_out(g)
+    ka = a_p.shape[-1]
+    ident = ProjectionMatrix(torch.eye(ka, dtype=p_out.dtype, device=p_out.device), False, ka,
+                             p_out.dtype, p_out.device)
+    return fused_outer(a_p.to(p_out.dtype), g.to(p_out.dtype), ident, p_out)
+
+
+def maybe_materialize_projected(seq_len: int, k_a: int, k_g: int, kappa: float = 1.0) -> bool:
+    """Capture-time rule: materialize iff ``S >= kappa*k_a*k_g/(k_a+k_g)``
+    (projection.py:846-874)."""
+    denom = k_a + k_g
+    if denom <= 0:
+        return False
+    return seq_len >= kappa * (k_a * k_g) / denom
+
+
+def should_materialize(capture_style: str, seq_len: int, k_a: int, k_g: int) -> bool:
+    """projection.py:877-899."""
+    if capture_style == "factorized":
+        return False
+    if capture_style == "materialized":
+        return True
+    if capture_style != "auto":
+        raise ValueError(f"capture_style must be one of {CAPTURE_STYLES}, got {capture_style!r}.")
+    return maybe_materialize_projected(seq_len, k_a, k_g)
+
+
+def project_factorized(f, layer_type: str, projector, *, proj_dim: int, include_bias: bool = True,
+                       proj_seed: int = 0, **proj_kwargs):
+    bf = f.as_batch_first()
+    return project_factors(bf.activation, bf.pre_activation_grad, layer_type, projector, bf.module_kwargs,
+                           include_bias, proj_dim=proj_dim, proj_seed=proj_seed, **proj_kwargs)
+
+
+def project_layer(f, layer_type: str, projector, *, style: str = "logra", capture_style: str = "factorized",
+                  **proj_kwargs):
+    """Route one layer through a projection style (projection.py:902-944).
+
+    ``"logra"`` keeps ``(a_p, g_p)`` or -- when :func:`should_materialize`
+    says so -- returns the ``(B, k_g*k_a)`` block from the fused kernel."""
+    if style not in PROJECTION_STYLES:
+        raise ValueError(f"style must be one of {PROJECTION_STYLES}, got {style!r}.")
+    if style != "logra" or isinstance(f, torch.Tensor):
+        raise NotImplementedError(f"projection style {style!r} is not on the MI355X path (use 'logra')")
+    bf = f.as_batch_first()
+    a, g = bf.activation, bf.pre_activation_grad
+    seq_len = a.shape[1] if a.ndim >= 3 else 1
+    proj_dim = proj_kwargs["proj_dim"]
+    include_bias = proj_kwargs.pop("include_bias", True)
+    bias = bool(bf.module_kwargs is not None and bf.module_kwargs["has_bias"] and include_bias)
+    if should_materialize(capture_style, seq_len, proj_dim, proj_dim):
+        kw = dict(proj_kwargs)
+        dim, seed = kw.pop("proj_dim"), kw.pop("proj_seed", 0)
+        mk = {"has_bias": bias}
+        return project_outer_factors(a, g, layer_type, projector, mk, True, proj_dim=dim,
+                                     proj_seed=seed, **kw), False
+    a_p, g_p = project_factorized(f, layer_type, projector, include_bias=include_bias, **proj_kwargs)
+    return (a_p, g_p), True

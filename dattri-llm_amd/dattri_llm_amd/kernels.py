@@ -304,13 +304,176 @@ def norm_xhat(x: torch.Tensor, *, kind: int, eps: float, out_dtype: torch.dtype 
     return out
 
 
-def selftest_mfma(dtype: torch.dtype, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """Raw accumulator dump of one 32x32 MFMA (see da_selftest_mfma)."""
+def selftest_mfma(dtype: torch.dtype, a: torch.Tensor, b: torch.Tensor, shape: int = 32) -> torch.Tensor:
+    """Raw accumulator dump of one MFMA block (see da_selftest_mfma)."""
     dev = nat.require_device(a, b)
-    out = torch.empty(64 * 16, dtype=torch.float32, device=dev)
+    regs = 16 if shape == 32 else 4
+    out = torch.empty(64 * regs, dtype=torch.float32, device=dev)
     nat.check(
-        nat.load().da_selftest_mfma(nat.dtype_code(dtype), a.data_ptr(), b.data_ptr(),
+        nat.load().da_selftest_mfma(nat.dtype_code(dtype), shape, a.data_ptr(), b.data_ptr(),
                                     out.data_ptr(), nat.stream_ptr(dev)),
         "selftest_mfma",
     )
-    return out.view(64, 16)
+    return out.view(64, regs)
+
+
+def project_rows(x: torch.Tensor, pt: torch.Tensor, *, bias: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``x @ pt.T (+ bias)`` over the last axis: x (..., d), pt (k, d) -- the
+    transposed projection matrix -- bias (k,) fp32 or None."""
+    dev = nat.require_device(x, pt, bias)
+    if pt.dim() != 2 or x.shape[-1] > pt.shape[1]:
+        raise ValueError("project_rows: pt must be (k, >= d)")
+    if x.dtype != pt.dtype:
+        raise ValueError("project_rows: x and the matrix must share one dtype")
+    out_dtype = out_dtype or x.dtype
+    d = x.shape[-1]
+    k = pt.shape[0]
+    rows = x.numel() // d if d else 0
+    out = torch.empty(*x.shape[:-1], k, dtype=out_dtype, device=dev)
+    if rows == 0 or k == 0:
+        return out
+    vec = _chunk_elems(x.dtype)
+    dp = -(-d // vec) * vec
+    flat = prepare_rows(x.reshape(rows, d), dp)
+    ptp = prepare_rows(pt[:, :d] if pt.shape[1] != dp else pt, dp)
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+        if bias.numel() != k:
+            raise ValueError("project_rows: bias must have k entries")
+    nat.check(
+        nat.load().da_project_rows(
+            flat.data_ptr(), nat.dtype_code(x.dtype), rows, dp, flat.stride(0), ptp.data_ptr(), k,
+            ptp.stride(0), bias.data_ptr() if bias is not None else None, out.data_ptr(),
+            nat.dtype_code(out_dtype), k, nat.stream_ptr(dev),
+        ),
+        "project_rows",
+    )
+    return out
+
+
+def project_outer(a: torch.Tensor, g: torch.Tensor, pin_t: torch.Tensor, pout_t: torch.Tensor, *,
+                  bias_in: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Fused ``bmm((g @ P_out)^T, a @ P_in (+ bias_in))`` flattened to (B, kg*ka).
+
+    a (B, T, K), g (B, T, D); pin_t (ka, K) and pout_t (kg, D) are the
+    transposed projection matrices; ka, kg <= 64."""
+    dev = nat.require_device(a, g, pin_t, pout_t, bias_in)
+    if a.dim() != 3 or g.dim() != 3 or a.shape[:2] != g.shape[:2]:
+        raise ValueError("project_outer expects a (B, T, K) and g (B, T, D)")
+    if not (a.dtype == g.dtype == pin_t.dtype == pout_t.dtype):
+        raise ValueError("project_outer operands must share one dtype")
+    out_dtype = out_dtype or a.dtype
+    b, t, k = a.shape
+    d = g.shape[-1]
+    ka, kg = pin_t.shape[0], pout_t.shape[0]
+    out = torch.empty(b, kg * ka, dtype=out_dtype, device=dev)
+    if b == 0 or ka == 0 or kg == 0:
+        return out
+    if t == 0:
+        return out.zero_()
+    vec = _chunk_elems(a.dtype)
+    kp, dp = -(-k // vec) * vec, -(-d // vec) * vec
+    a, g = prepare_rows(a, kp), prepare_rows(g, dp)
+    pin_t, pout_t = prepare_rows(pin_t[:, :k], kp), prepare_rows(pout_t[:, :d], dp)
+    if bias_in is not None:
+        bias_in = bias_in.to(torch.float32).contiguous()
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_project_outer_workspace(b, t, ka, kg, ctypes.byref(nbytes)), "project_outer")
+    ws = nat.workspace(nbytes.value, dev)
+    nat.check(
+        lib.da_project_outer(
+            a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, kp, dp,
+            a.stride(0), a.stride(1), g.stride(0), g.stride(1),
+            pin_t.data_ptr(), ka, pin_t.stride(0), bias_in.data_ptr() if bias_in is not None else None,
+            pout_t.data_ptr(), kg, pout_t.stride(0), out.data_ptr(), nat.dtype_code(out_dtype), kg * ka,
+            ws.data_ptr(), ws.numel(), nat.stream_ptr(dev),
+        ),
+        "project_outer",
+    )
+    return out
+
+
+def moe_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Router top-k of softmax(logits) -> (weights (N, k) fp32, indices (N, k) int64)."""
+    dev = nat.require_device(logits)
+    if logits.dim() != 2:
+        raise ValueError("moe_topk expects (tokens, experts) logits")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    n, e = logits.shape
+    weights = torch.empty(n, k, dtype=torch.float32, device=dev)
+    index = torch.empty(n, k, dtype=torch.int64, device=dev)
+    nat.check(
+        nat.load().da_moe_topk(logits.data_ptr(), nat.dtype_code(logits.dtype), n, e, k, logits.stride(0),
+                               weights.data_ptr(), index.data_ptr(), nat.stream_ptr(dev)),
+        "moe_topk",
+    )
+    return weights, index
+
+
+def counting_sort(keys: torch.Tensor, bins: int, *, slot_major: bool = False,
+                  key_div: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stable counting sort -> (offsets (bins+1) int32, perm (n) int32).
+
+    ``keys`` is int32/int64 (flattened), or with ``slot_major`` an int64
+    (rows, k) matrix read column by column."""
+    dev = nat.require_device(keys)
+    if keys.dtype not in (torch.int32, torch.int64):
+        raise ValueError("counting_sort keys must be int32 or int64")
+    keys = keys.contiguous()
+    if slot_major:
+        if keys.dim() != 2 or keys.dtype != torch.int64:
+            raise ValueError("slot-major keys must be an int64 (rows, k) matrix")
+        rows, k = keys.shape
+    else:
+        keys = keys.reshape(-1)
+        rows, k = keys.numel(), 1
+    n = keys.numel()
+    offsets = torch.empty(bins + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    k32 = keys.data_ptr() if keys.dtype == torch.int32 else None
+    k64 = keys.data_ptr() if keys.dtype == torch.int64 else None
+    nat.check(
+        nat.load().da_counting_sort(k32, k64, n, rows, k, int(slot_major), key_div, bins,
+                                    offsets.data_ptr(), perm.data_ptr(), nat.stream_ptr(dev)),
+        "counting_sort",
+    )
+    return offsets, perm[:n]
+
+
+def ghost_gram_segmented(a1, g1, seg1, idx1, tokens1, a2, g2, seg2, idx2, tokens2, *,
+                         bias: bool = False, out: torch.Tensor | None = None,
+                         accumulate: bool = False) -> torch.Tensor:
+    """Ghost cross-gram over row segments: side s sample b owns flat rows
+    [seg_s[b], seg_s[b+1]) of the (rows, width) factors, gathered through idx_s
+    (int32 row ids, or None for identity); ``tokens_s`` >= the longest segment."""
+    dev = nat.require_device(a1, g1, a2, g2, seg1, seg2)
+    if not (a1.dtype == g1.dtype == a2.dtype == g2.dtype):
+        raise ValueError("ghost_gram_segmented factors must share one dtype")
+    for t in (seg1, seg2) + tuple(x for x in (idx1, idx2) if x is not None):
+        if t.dtype != torch.int32:
+            raise ValueError("segment offsets and row indices must be int32")
+    code = nat.dtype_code(a1.dtype)
+    vec = _chunk_elems(a1.dtype)
+    k = -(-a1.shape[-1] // vec) * vec
+    d = -(-g1.shape[-1] // vec) * vec
+    a1, a2 = prepare_rows(a1, k), prepare_rows(a2, k)
+    g1, g2 = prepare_rows(g1, d), prepare_rows(g2, d)
+    b1, b2 = seg1.numel() - 1, seg2.numel() - 1
+    if out is None:
+        out = torch.empty(b1, b2, dtype=torch.float32, device=dev)
+        accumulate = False
+    s1 = _side(a1, g1, bias, seg=seg1.contiguous(), index=idx1, tokens=max(int(tokens1), 1))
+    s2 = _side(a2, g2, bias, seg=seg2.contiguous(), index=idx2, tokens=max(int(tokens2), 1))
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_ghost_gram_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)), "ghost_gram_segmented")
+    ws = nat.workspace(nbytes.value, dev)
+    nat.check(
+        lib.da_ghost_gram(s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate),
+                          ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
+        "ghost_gram_segmented",
+    )
+    return out

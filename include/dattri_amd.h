@@ -144,7 +144,8 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
 
 /*
  * Per-sample weight gradient of a token norm layer (kind 0 = RMSNorm,
- * 1 = LayerNorm), one pass over x and g:
+ * 1 = LayerNorm, 2 = x already normalised, i.e. x_hat = x), one pass over x
+ * and g:
  *
  *   x_hat = x * rsqrt(mean(x^2) + eps)  |  (x - mean) * rsqrt(var + eps)
  *   out[b*out_bstride + f]     = sum_t x_hat[b,t,f] * g[b,t,f]      (f < d)
@@ -173,13 +174,75 @@ int da_norm_xhat(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rs
                  float eps, void* out, int out_dtype, int64_t out_rstride, void* stream);
 
 /*
- * Lane-layout self test of the 32x32 MFMA convention every kernel relies on:
- * a (32 x k) and b (32 x k) row-major (k = 16 for bf16/f16, 8 for f32, i.e.
- * one 16-byte chunk per lane), out receives 64 lanes x 16 accumulator values
- * of C = a . b^T exactly as the registers hold them (out[lane*16 + r]).
+ * Random projection of factor rows (ProjectionMatrix.__call__,
+ * dattri_llm/gradient/ops/projection.py:363-370):
+ *
+ *   out[r*out_rstride + c] = sum_j x[r*x_rstride + j] * P[j, c] (+ bias[c])
+ *
+ * The projection matrix is passed TRANSPOSED: pt is (k, d) with row stride
+ * pt_rstride, so both operands are read along d.  bias is k fp32 values or
+ * NULL (the bias row of a linear layer's (d+1, k) matrix, projection.py:276-277).
+ */
+int da_project_rows(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rstride,
+                    const void* pt, int64_t k, int64_t pt_rstride, const float* bias, void* out,
+                    int out_dtype, int64_t out_rstride, void* stream);
+
+/*
+ * Fused capture-time projection and per-sample outer-product sum of a linear
+ * layer (the LoGRA capture of dattri_llm/gradient/hooks/hooks.py:631-648 with
+ * materialize_factors(a_p, g_p, "nn.Linear"), materialize.py:114-116):
+ *
+ *   a_p = a . P_in (+ bias_in)     (B, T, ka)      P_in^T  = pin_t  (ka, K)
+ *   g_p = g . P_out                (B, T, kg)      P_out^T = pout_t (kg, D)
+ *   out[b*out_bstride + o*ka + i] = sum_t g_p[b,t,o] * a_p[b,t,i]
+ *
+ * ka, kg <= 64 (DA_ERR_UNSUPPORTED above).  One pass over a and g.
+ */
+int da_project_outer_workspace(int64_t batch, int64_t tokens, int64_t ka, int64_t kg, size_t* bytes);
+int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens, int64_t K,
+                     int64_t D, int64_t a_bstride, int64_t a_tstride, int64_t g_bstride,
+                     int64_t g_tstride, const void* pin_t, int64_t ka, int64_t pin_rstride,
+                     const float* bias_in, const void* pout_t, int64_t kg, int64_t pout_rstride,
+                     void* out, int out_dtype, int64_t out_bstride, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/*
+ * MoE router: per token, top-k of softmax(logits) (fp32), weights renormalised
+ * over the k, indices by descending probability, ties to the lower expert
+ * index -- the router contract of transformers' MixtralTopKRouter.forward used
+ * by dattri_llm/gradient/hooks/override_layers/fused_experts.py:210-237.
+ * logits (n_tokens, n_experts) with row stride row_stride; weights (n, k)
+ * fp32; index (n, k) int64.  n_experts <= 256, k <= 16.
+ */
+int da_moe_topk(const void* logits, int dtype, int64_t n_tokens, int n_experts, int k,
+                int64_t row_stride, float* weights, int64_t* index, void* stream);
+
+/*
+ * Stable counting sort of integer keys into `bins` bins (<= 8192).
+ * keys: keys32 or keys64 (n entries), or with slot_major != 0 the int64
+ * (rows, k) matrix keys64 read slot-major (entry p = keys64[(p % rows)*k + p / rows]).
+ * key_div > 1 divides each key first (e.g. flat token -> sample).  Writes
+ * offsets (bins+1: bin b holds sorted positions [offsets[b], offsets[b+1]))
+ * and perm (sorted position -> input entry).  Keys outside [0, bins) are
+ * dropped (offsets[bins] counts the kept ones).  On top-k indices read
+ * slot-major this yields the expert segments in the order of
+ * fused_experts.py:219-228 (torch.where over one_hot(idx).permute(2,1,0)[e]).
+ */
+int da_counting_sort(const int32_t* keys32, const int64_t* keys64, int64_t n, int64_t rows,
+                     int64_t k, int slot_major, int64_t key_div, int bins, int32_t* offsets,
+                     int32_t* perm, void* stream);
+
+/*
+ * Lane-layout self test of the MFMA conventions every kernel relies on.
+ * shape 32: a and b are (32 x k) row-major with k = 16 (bf16/f16) or 8 (f32),
+ *           one 16-byte chunk per lane half; out receives 64 lanes x 16
+ *           accumulator values of C = a . b^T as the registers hold them
+ *           (out[lane*16 + r]).
+ * shape 16: a and b are (16 x k), k = 32 (bf16/f16) or 16 (f32); out receives
+ *           64 lanes x 4 values (out[lane*4 + r]).
  * No counterpart in the reference: used by tests and smoke checks.
  */
-int da_selftest_mfma(int dtype, const void* a, const void* b, float* out, void* stream);
+int da_selftest_mfma(int dtype, int shape, const void* a, const void* b, float* out, void* stream);
 
 #ifdef __cplusplus
 }

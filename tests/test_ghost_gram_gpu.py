@@ -29,23 +29,29 @@ def _inputs(seed, b1, s1, b2, s2, k, d, dtype, scale=True):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_mfma_lane_layout(device, dtype):
-    """The 32x32 operand/accumulator convention every kernel relies on."""
+@pytest.mark.parametrize("shape", [32, 16])
+def test_mfma_lane_layout(device, dtype, shape):
+    """The MFMA operand/accumulator conventions every kernel relies on."""
     from dattri_llm_amd import kernels
 
-    k = 8 if dtype == torch.float32 else 16
+    chunk = 8 if dtype == torch.float32 else 16  # elements per 32 bytes
+    rows, k = (32, chunk) if shape == 32 else (16, 2 * chunk)
     gen = torch.Generator().manual_seed(1)
     # small integers: every product and sum is exact in fp32
-    a = torch.randint(-4, 5, (32, k), generator=gen).to(dtype)
-    b = torch.randint(-4, 5, (32, k), generator=gen).to(dtype)
-    raw = kernels.selftest_mfma(dtype, a.to(device), b.to(device)).cpu()
+    a = torch.randint(-4, 5, (rows, k), generator=gen).to(dtype)
+    b = torch.randint(-4, 5, (rows, k), generator=gen).to(dtype)
+    raw = kernels.selftest_mfma(dtype, a.to(device), b.to(device), shape=shape).cpu()
     c = a.double() @ b.double().T
     lane = torch.arange(64)[:, None]
-    r = torch.arange(16)[None, :]
-    rows = 8 * (r // 4) + 4 * (lane // 32) + (r % 4)
-    cols = (lane % 32).expand(64, 16)
-    expect = c[rows, cols]
-    assert torch.equal(raw.double(), expect)
+    if shape == 32:
+        r = torch.arange(16)[None, :]
+        rows_idx = 8 * (r // 4) + 4 * (lane // 32) + (r % 4)
+        cols_idx = (lane % 32).expand(64, 16)
+    else:
+        r = torch.arange(4)[None, :]
+        rows_idx = 4 * (lane // 16) + r
+        cols_idx = (lane % 16).expand(64, 4)
+    assert torch.equal(raw.double(), c[rows_idx, cols_idx])
 
 
 CASES = [

@@ -42,6 +42,6 @@ def test_abi_version_and_error_plumbing():
     lib = _native.load()
     assert lib.da_abi_version() == _native.ABI_VERSION
     # an invalid call fails without touching a GPU and leaves a message
-    status = lib.da_selftest_mfma(0, None, None, None, None)
+    status = lib.da_selftest_mfma(0, 32, None, None, None, None)
     assert status == _native.DA_ERR_INVALID
     assert b"null" in lib.da_last_error()

@@ -1,0 +1,304 @@
+"""GPU parity of the drop-in ops layer (the reference's gradient.ops API)
+against the oracle, plus C1 end to end against the autograd fixture.
+
+Bar: normwise relative error <= 1e-2 for bf16 inputs, <= 1e-3 for fp32;
+MoE top-k indices and expert segments bit-exact.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import REPO, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 1e-2, torch.float32: 1e-3}
+
+
+def _np(x):
+    return x.double().cpu().numpy()
+
+
+def _rand(gen, *shape, dtype=torch.float32, scale=1.0):
+    return (torch.randn(*shape, generator=gen) * scale).to(dtype)
+
+
+@pytest.fixture
+def ops():
+    from dattri_llm_amd.gradient import ops
+
+    return ops
+
+
+# ---------------------------------------------------------------------------
+# cross_gram / cross_dot
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["factorized", "materialized", "auto"])
+def test_cross_gram_routes_agree_with_oracle(device, ops, dtype, mode):
+    gen = torch.Generator().manual_seed(1)
+    a1, g1 = _rand(gen, 5, 40, 64, dtype=dtype), _rand(gen, 5, 40, 48, dtype=dtype)
+    a2, g2 = _rand(gen, 3, 24, 64, dtype=dtype), _rand(gen, 3, 24, 48, dtype=dtype)
+    got = ops.cross_gram(*(t.to(device) for t in (a1, g1, a2, g2)), "nn.Linear", mode=mode)
+    assert got.dtype == dtype
+    ref = oracle.cross_gram_factorized(_np(a1), _np(g1), _np(a2), _np(g2))
+    assert rel_err(got.float().cpu().numpy(), ref) <= TOL[dtype]
+
+
+def test_cross_gram_norm_branch(device, ops):
+    gen = torch.Generator().manual_seed(2)
+    a1, g1 = _rand(gen, 3, 10, 64), _rand(gen, 3, 10, 64)
+    a2, g2 = _rand(gen, 2, 7, 64), _rand(gen, 2, 7, 64)
+    got = ops.cross_gram(*(t.to(device) for t in (a1, g1, a2, g2)), "nn.RMSNorm")
+    ref = oracle.cross_gram(_np(a1), _np(g1), _np(a2), _np(g2), "nn.RMSNorm")
+    assert rel_err(got.cpu().numpy(), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("layer_type", ["nn.Linear", "nn.RMSNorm", "nn.LayerNorm"])
+@pytest.mark.parametrize("eps", [1e-5, None])
+def test_cross_dot_factors_raw_captures(device, ops, layer_type, eps):
+    """Raw captures with module_kwargs: preprocessing happens inside the kernels."""
+    gen = torch.Generator().manual_seed(3)
+    d_in, d_out = 64, (48 if layer_type == "nn.Linear" else 64)
+    a1, g1 = _rand(gen, 4, 20, d_in, dtype=torch.bfloat16, scale=2.0), _rand(gen, 4, 20, d_out, dtype=torch.bfloat16)
+    a2, g2 = _rand(gen, 3, 12, d_in, dtype=torch.bfloat16, scale=2.0), _rand(gen, 3, 12, d_out, dtype=torch.bfloat16)
+    has_bias = layer_type != "nn.RMSNorm"
+    mk = {"has_bias": has_bias, "eps": eps, "normalized_shape": (d_in,)}
+    got = ops.cross_dot_factors(*(t.to(device) for t in (a1, g1, a2, g2)), layer_type, mk, mk)
+    eps_v = torch.finfo(torch.bfloat16).eps if eps is None else eps
+    mko = {"has_bias": has_bias, "eps": eps_v}
+    p1 = oracle.preprocess(_np(a1), _np(g1), layer_type, mko)
+    p2 = oracle.preprocess(_np(a2), _np(g2), layer_type, mko)
+    ref = oracle.cross_gram(*p1, *p2, layer_type, mode="factorized")
+    assert rel_err(got.float().cpu().numpy(), ref) <= 1e-2
+
+
+def test_preprocess_and_materialize_factors(device, ops):
+    gen = torch.Generator().manual_seed(4)
+    x, g = _rand(gen, 3, 9, 128, scale=3.0), _rand(gen, 3, 9, 128)
+    mk = {"has_bias": True, "eps": 1e-5, "normalized_shape": (128,)}
+    a_p, g_p = ops.preprocess_factors(x.to(device), g.to(device), "nn.LayerNorm", mk)
+    ra, rg = oracle.preprocess(_np(x), _np(g), "nn.LayerNorm", mk)
+    assert rel_err(a_p.cpu().numpy(), ra) <= 1e-5 and rel_err(g_p.cpu().numpy(), rg) == 0.0
+    m = ops.materialize_factors(x.to(device), g.to(device), "nn.LayerNorm", mk)
+    assert rel_err(m.cpu().numpy(), oracle.norm_weight_grad(_np(x), _np(g), "nn.LayerNorm", 1e-5, True)) <= 1e-4
+    # linear with bias: (B, D*(K+1)), index o*(K+1)+i
+    a, gg = _rand(gen, 2, 30, 40), _rand(gen, 2, 30, 24)
+    m = ops.materialize_factors(a.to(device), gg.to(device), "nn.Linear", {"has_bias": True})
+    assert m.shape == (2, 24 * 41)
+    assert rel_err(m.cpu().numpy(), oracle.materialize_linear(_np(a), _np(gg), bias=True)) <= 1e-4
+
+
+def test_grad_norm_and_per_sample_dot(device, ops):
+    gen = torch.Generator().manual_seed(5)
+    a, g = _rand(gen, 4, 16, 32), _rand(gen, 4, 16, 24)
+    b, h = _rand(gen, 4, 8, 32), _rand(gen, 4, 8, 24)
+    want = np.diag(oracle.cross_gram_factorized(_np(a), _np(g), _np(a), _np(g)))
+    for mode in ("factorized", "materialized"):
+        got = ops.grad_norm_sq_factors(a.to(device), g.to(device), "nn.Linear", mode=mode)
+        assert rel_err(got.cpu().numpy(), want) <= 1e-3
+    got = ops.dot_factors(a.to(device), g.to(device), b.to(device), h.to(device), "nn.Linear")
+    want = np.diag(oracle.cross_gram_factorized(_np(a), _np(g), _np(b), _np(h)))
+    assert rel_err(got.cpu().numpy(), want) <= 1e-3
+
+
+def test_layerwise_cross_dot_mixed_representations(device, ops):
+    """Dense x dense (one multi-layer launch), factorized x factorized, dense x
+    factorized, and a broadcast batch-1 layer, summed -- against the oracle."""
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    gen = torch.Generator().manual_seed(6)
+    bt, bq = 6, 4
+    fac = {n: (_rand(gen, bt, 12, 32), _rand(gen, bt, 12, 16), _rand(gen, bq, 10, 32), _rand(gen, bq, 10, 16))
+           for n in ("l0", "l1", "l2")}
+    pos_tr, pos_q = _rand(gen, 1, 20), _rand(gen, bq, 20)
+    ref = 0.0
+    tr_data, te_data = {}, {}
+    for n, (a1, g1, a2, g2) in fac.items():
+        ref = ref + oracle.cross_gram_factorized(_np(a1), _np(g1), _np(a2), _np(g2), bias=True)
+        mk = {"has_bias": True}
+        f1 = Factorized(a1.to(device), g1.to(device), module_kwargs=mk)
+        f2 = Factorized(a2.to(device), g2.to(device), module_kwargs=mk)
+        tr_data[n] = f1 if n != "l0" else ops.materialize(f1, "nn.Linear")
+        te_data[n] = f2 if n == "l1" else ops.materialize(f2, "nn.Linear")
+    ref = ref + np.broadcast_to(_np(pos_tr) @ _np(pos_q).T, (bt, bq))
+    tr_data["pos"], te_data["pos"] = pos_tr.to(device), pos_q.to(device)
+    rep = lambda d: {n: ("materialized" if isinstance(v, torch.Tensor) else "factorized") for n, v in d.items()}  # noqa: E731
+    lts = dict.fromkeys(tr_data, "nn.Linear")
+    train = Gradient(rep(tr_data), tr_data, lts)
+    test = Gradient(rep(te_data), te_data, lts)
+    got = ops.layerwise_cross_dot(train, test)
+    assert got.shape == (bt, bq)
+    assert rel_err(got.cpu().numpy(), ref) <= 1e-3
+    per = ops.layerwise_cross_dot(train, test, reduce="none")
+    assert set(per) == {"l0", "l1", "l2", "pos"} and per["pos"].shape == (1, bq)
+
+
+# ---------------------------------------------------------------------------
+# projection
+# ---------------------------------------------------------------------------
+
+
+def test_projection_matrix_and_seed_convention(device, ops):
+    gen = torch.Generator().manual_seed(7)
+    a, g = _rand(gen, 3, 17, 96), _rand(gen, 3, 17, 80)
+    mk = {"has_bias": True}
+    a_p, g_p = ops.project_factors(a.to(device), g.to(device), "nn.Linear", None, mk, proj_dim=16, proj_seed=5)
+    p_in = ops.projection.gaussian_matrix(97, 16, 6).double().numpy()   # activation: seed + 1, with bias row
+    p_out = ops.projection.gaussian_matrix(80, 16, 5).double().numpy()  # gradient: seed
+    assert rel_err(a_p.cpu().numpy(), oracle.project(_np(a), p_in[:-1], p_in[-1])) <= 1e-4
+    assert rel_err(g_p.cpu().numpy(), oracle.project(_np(g), p_out)) <= 1e-4
+    fused = ops.project_outer_factors(a.to(device), g.to(device), "nn.Linear", None, mk, proj_dim=16, proj_seed=5)
+    assert rel_err(fused.cpu().numpy(), oracle.project_outer(_np(a), _np(g), p_in, p_out, bias=True)) <= 1e-4
+
+
+def test_capture_projected_and_routing(device, ops):
+    gen = torch.Generator().manual_seed(8)
+    a, g = _rand(gen, 2, 70, 64, dtype=torch.bfloat16), _rand(gen, 2, 70, 48, dtype=torch.bfloat16)
+    proj = ops.DattriProjector()
+    pa = proj.resolve(64, proj_dim=32, proj_seed=1, include_bias=False, device=device, dtype=torch.bfloat16)
+    pg = proj.resolve(48, proj_dim=32, proj_seed=0, device=device, dtype=torch.bfloat16)
+    a_p = pa(a.to(device))
+    dense = ops.capture_projected(a_p, g.to(device), pg, materialize=True)
+    kept = ops.capture_projected(a_p, g.to(device), pg, materialize=False)
+    want = oracle.materialize_linear(_np(a_p), _np(kept[1]))
+    assert dense.shape == (2, 32 * 32)
+    assert rel_err(dense.float().cpu().numpy(), want) <= 1e-2
+    from dattri_llm_amd.gradient import Factorized
+
+    f = Factorized(a.to(device), g.to(device), module_kwargs={"has_bias": False})
+    payload, is_fact = ops.project_layer(f, "nn.Linear", proj, capture_style="auto", proj_dim=32, proj_seed=0)
+    assert not is_fact and payload.shape == (2, 32 * 32)  # T=70 >= H=16: materialized
+
+
+def test_project_outer_c3_geometry_subset(device):
+    """C3 shapes (down_proj 11008 -> 4096, T=128, proj 64) on 4 samples."""
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(9)
+    a = _rand(gen, 4, 128, 11008, dtype=torch.bfloat16, scale=11008**-0.5)
+    g = _rand(gen, 4, 128, 4096, dtype=torch.bfloat16, scale=4096**-0.5)
+    p_in = _rand(gen, 11008, 64, dtype=torch.bfloat16, scale=0.125)
+    p_out = _rand(gen, 4096, 64, dtype=torch.bfloat16, scale=0.125)
+    got = kernels.project_outer(a.to(device), g.to(device), p_in.t().contiguous().to(device),
+                                p_out.t().contiguous().to(device), out_dtype=torch.float32)
+    want = oracle.project_outer(_np(a), _np(g), _np(p_in), _np(p_out))
+    assert rel_err(got.cpu().numpy(), want) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
+# MoE
+# ---------------------------------------------------------------------------
+
+
+def test_router_topk_and_segments_bit_exact(device, ops):
+    gen = torch.Generator().manual_seed(10)
+    logits = torch.randn(16 * 256, 8, generator=gen)
+    w, idx = ops.moe.router_topk(logits.to(device), 2)
+    probs = torch.softmax(logits.float(), dim=-1)
+    tv, ti = torch.topk(probs, 2, dim=-1)
+    assert torch.equal(idx.cpu(), ti)
+    torch.testing.assert_close(w.cpu(), tv / tv.sum(-1, keepdim=True), rtol=1e-5, atol=1e-6)
+    mask = torch.nn.functional.one_hot(ti, num_classes=8).permute(2, 1, 0)
+    rows = ops.moe.expert_rows(idx, 8)
+    for e in range(8):
+        pos, tok = torch.where(mask[e])
+        assert torch.equal(rows[e][0].cpu(), pos) and torch.equal(rows[e][1].cpu(), tok)
+
+
+def test_counting_sort_edge_cases(device):
+    from dattri_llm_amd import kernels
+
+    keys = torch.tensor([3, 0, 3, 9, -1, 1, 3, 0], dtype=torch.int32, device=device)
+    off, perm = kernels.counting_sort(keys, 4)
+    assert off.cpu().tolist() == [0, 2, 3, 3, 6]  # 9 and -1 dropped
+    assert perm[:6].cpu().tolist() == [1, 7, 5, 0, 2, 6]
+    off, perm = kernels.counting_sort(torch.zeros(0, dtype=torch.int32, device=device), 3)
+    assert off.cpu().tolist() == [0, 0, 0, 0] and perm.numel() == 0
+    big = torch.randint(0, 50, (5000,), generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    off, perm = kernels.counting_sort(big.to(device), 50)
+    want = torch.sort(big.long(), stable=True).indices
+    assert torch.equal(perm.cpu().long(), want)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_expert_cross_gram_equals_dense_with_zeros(device, ops, bias):
+    """C5-shaped routing (16 x 256 tokens, 8 experts, top-2), reduced widths."""
+    gen = torch.Generator().manual_seed(11)
+    batch, tokens, n_exp, d_in, d_out = 16, 256, 8, 64, 96
+    logits1, logits2 = torch.randn(batch * tokens, n_exp, generator=gen), torch.randn(batch * tokens, n_exp, generator=gen)
+    _, idx1 = ops.moe.router_topk(logits1.to(device), 2)
+    _, idx2 = ops.moe.router_topk(logits2.to(device), 2)
+    rows1, rows2 = ops.moe.expert_rows(idx1, n_exp), ops.moe.expert_rows(idx2, n_exp)
+    experts, ref = [], np.zeros((batch, batch))
+    for e in range(n_exp):
+        tok1, tok2 = rows1[e][1], rows2[e][1]
+        a1, g1 = _rand(gen, tok1.numel(), d_in, dtype=torch.bfloat16), _rand(gen, tok1.numel(), d_out, dtype=torch.bfloat16)
+        a2, g2 = _rand(gen, tok2.numel(), d_in, dtype=torch.bfloat16), _rand(gen, tok2.numel(), d_out, dtype=torch.bfloat16)
+        ref += oracle.moe_segment_ghost(_np(a1), _np(g1), tok1.cpu().numpy(), _np(a2), _np(g2),
+                                        tok2.cpu().numpy(), batch, batch, tokens, tokens, bias=bias)
+        experts.append((a1.to(device), g1.to(device), tok1, a2.to(device), g2.to(device), tok2))
+    got = ops.moe.moe_cross_gram(experts, batch1=batch, tokens1=tokens, batch2=batch, tokens2=tokens, bias=bias)
+    assert rel_err(got.cpu().numpy(), ref) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
+# C1 end to end: TracIn through the drop-in API == autograd fixture
+# ---------------------------------------------------------------------------
+
+
+def _c1_blocks(device):
+    from c1_model import c1_inputs, capture_factors
+
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    model, train, query = c1_inputs(0)
+    blocks = []
+    for ids in (train, query):
+        f = capture_factors(model, ids)
+        data = {n: Factorized(a.to(device), g.to(device), module_kwargs={"has_bias": True}) for n, (a, g) in f.items()}
+        blocks.append(Gradient(dict.fromkeys(data, "factorized"), data, dict.fromkeys(data, "nn.Linear"),
+                               dict.fromkeys(data, "batch_token")))
+    return blocks
+
+
+def _c1_fixture():
+    with open(os.path.join(REPO, "tests", "golden", "c1_scores.json")) as f:
+        return np.array(json.load(f)["scores"])
+
+
+@pytest.mark.parametrize("mode", ["factorized", "auto"])
+def test_c1_layerwise_scores(device, ops, mode):
+    train, query = _c1_blocks(device)
+    got = ops.layerwise_cross_dot(train, query, mode=mode)
+    assert got.shape == (32, 8)
+    assert rel_err(got.cpu().numpy(), _c1_fixture()) <= 1e-3
+
+
+def test_c1_tracin_attributor_and_cosine(device):
+    from dattri_llm_amd.attribution import TracInAttributor
+
+    train, query = _c1_blocks(device)
+    attr = TracInAttributor(train_batch_size=16, device=device)
+    src_tr = [(0, train, [f"t{i}" for i in range(32)])]
+    src_q = [(0, query, [f"q{j}" for j in range(8)])]
+    score = attr.attribute_sources(src_tr, src_q)
+    assert score.algorithm == "TracIn" and score.scores.shape == (32, 8)
+    assert rel_err(score.scores.numpy(), _c1_fixture()) <= 1e-3
+    cos = TracInAttributor(train_batch_size=16, device=device).attribute_sources(src_tr, src_q, normalized_grad=True)
+    fx = _c1_fixture()
+    # cosine against the fixture: divide by the diagonal norms from the self grams
+    tr_self = train.similarity(train, reduce="all").cpu().double().numpy()
+    q_self = query.similarity(query, reduce="all").cpu().double().numpy()
+    want = fx / (np.sqrt(np.diag(tr_self))[:, None] * np.sqrt(np.diag(q_self))[None, :] + 1e-8)
+    assert cos.algorithm == "GradCos"
+    assert rel_err(cos.scores.numpy(), want) <= 1e-3

@@ -1,0 +1,261 @@
+"""Pinning the numpy oracle (CPU).  Each check is independent of the oracle's
+own formula: brute-force loops, torch autograd per-sample gradients, torch
+library routines, algebraic identities, and the reference's known-answer
+tables (tests/golden/routing_known_answers.json)."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import REPO, rel_err
+
+GOLDEN = os.path.join(REPO, "tests", "golden")
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------------------
+# ghost cross-gram
+# ---------------------------------------------------------------------------
+
+
+def _brute_ghost(a1, g1, a2, g2):
+    b1, s1, _ = a1.shape
+    b2, s2, _ = a2.shape
+    out = np.zeros((b1, b2))
+    for i in range(b1):
+        for j in range(b2):
+            acc = 0.0
+            for t in range(s1):
+                for s in range(s2):
+                    acc += float(a1[i, t] @ a2[j, s]) * float(g1[i, t] @ g2[j, s])
+            out[i, j] = acc
+    return out
+
+
+def test_ghost_matches_brute_force_loops():
+    r = _rng(0)
+    a1, g1 = r.standard_normal((3, 4, 5)), r.standard_normal((3, 4, 6))
+    a2, g2 = r.standard_normal((2, 3, 5)), r.standard_normal((2, 3, 6))
+    np.testing.assert_allclose(oracle.cross_gram_factorized(a1, g1, a2, g2), _brute_ghost(a1, g1, a2, g2),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_ghost_bias_is_a_ones_column():
+    r = _rng(1)
+    a1, g1 = r.standard_normal((2, 5, 4)), r.standard_normal((2, 5, 3))
+    a2, g2 = r.standard_normal((3, 2, 4)), r.standard_normal((3, 2, 3))
+    ones = lambda a: np.concatenate([a, np.ones(a.shape[:-1] + (1,))], -1)  # noqa: E731
+    np.testing.assert_allclose(oracle.cross_gram_factorized(a1, g1, a2, g2, bias=True),
+                               _brute_ghost(ones(a1), g1, ones(a2), g2), rtol=1e-12)
+
+
+def test_ghost_equals_materialized_route():
+    r = _rng(2)
+    a1, g1 = r.standard_normal((4, 7, 6)), r.standard_normal((4, 7, 5))
+    a2, g2 = r.standard_normal((3, 9, 6)), r.standard_normal((3, 9, 5))
+    for bias in (False, True):
+        np.testing.assert_allclose(oracle.cross_gram_factorized(a1, g1, a2, g2, bias),
+                                   oracle.cross_gram_materialized(a1, g1, a2, g2, bias), rtol=1e-10)
+
+
+def _linear_per_sample(a, c):
+    """Per-sample [W.grad, b.grad] of a linear layer under loss_i = sum_t c_it . y_it."""
+    a_t = torch.tensor(a)
+    c_t = torch.tensor(c)
+    lin = torch.nn.Linear(a.shape[-1], c.shape[-1]).double()
+    rows = []
+    for i in range(a.shape[0]):
+        lin.zero_grad()
+        (lin(a_t[i]) * c_t[i]).sum().backward()
+        rows.append(torch.cat([lin.weight.grad, lin.bias.grad[:, None]], 1).flatten().numpy().copy())
+    return np.stack(rows)
+
+
+def test_cross_gram_and_materialize_against_autograd():
+    """<dW_i, dW_j> with the bias and the (B, out*(in+1)) layout pinned by autograd."""
+    r = _rng(3)
+    a1, c1 = r.standard_normal((3, 6, 5)), r.standard_normal((3, 6, 4))
+    a2, c2 = r.standard_normal((2, 4, 5)), r.standard_normal((2, 4, 4))
+    w1, w2 = _linear_per_sample(a1, c1), _linear_per_sample(a2, c2)
+    np.testing.assert_allclose(oracle.materialize_linear(a1, c1, bias=True), w1, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(oracle.cross_gram_factorized(a1, c1, a2, c2, bias=True), w1 @ w2.T, rtol=1e-10)
+
+
+# ---------------------------------------------------------------------------
+# norms
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("eps", [1e-6, None])
+def test_rms_x_hat_matches_torch(eps):
+    x = torch.randn(3, 7, 16, dtype=torch.float64) * 2
+    ref = torch.nn.functional.rms_norm(x, (16,), eps=eps)
+    eps_v = torch.finfo(torch.float64).eps if eps is None else eps
+    np.testing.assert_allclose(oracle.rms_x_hat(x.numpy(), eps_v), ref.numpy(), rtol=1e-12)
+
+
+def test_machine_eps_constants():
+    assert oracle.BF16_EPS == torch.finfo(torch.bfloat16).eps
+    assert oracle.F32_EPS == torch.finfo(torch.float32).eps
+    assert oracle.F16_EPS == torch.finfo(torch.float16).eps
+
+
+def test_layer_norm_x_hat_matches_torch():
+    x = torch.randn(2, 5, 12, dtype=torch.float64) + 3
+    ref = torch.nn.functional.layer_norm(x, (12,), eps=1e-5)
+    np.testing.assert_allclose(oracle.layer_norm_x_hat(x.numpy(), 1e-5), ref.numpy(), rtol=1e-10)
+
+
+@pytest.mark.parametrize("layer_type", ["nn.RMSNorm", "nn.LayerNorm"])
+def test_norm_weight_grad_against_autograd(layer_type):
+    torch.manual_seed(4)
+    d = 10
+    x = torch.randn(3, 6, d, dtype=torch.float64)
+    c = torch.randn(3, 6, d, dtype=torch.float64)
+    mod = (torch.nn.RMSNorm(d, eps=1e-5) if layer_type == "nn.RMSNorm" else torch.nn.LayerNorm(d, eps=1e-5)).double()
+    with torch.no_grad():
+        mod.weight.copy_(torch.randn(d))
+    has_bias = getattr(mod, "bias", None) is not None
+    rows = []
+    for i in range(3):
+        mod.zero_grad()
+        (mod(x[i]) * c[i]).sum().backward()
+        parts = [mod.weight.grad.clone()] + ([mod.bias.grad.clone()] if has_bias else [])
+        rows.append(torch.cat(parts).numpy())
+    # the captured output gradient of a norm's *affine* input is c * weight
+    g = (c * mod.weight.detach()).numpy()
+    got = oracle.norm_weight_grad(x.numpy(), g / mod.weight.detach().numpy(), layer_type, 1e-5, has_bias)
+    np.testing.assert_allclose(got, np.stack(rows), rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# projection
+# ---------------------------------------------------------------------------
+
+
+def test_project_bias_row_is_a_ones_column():
+    r = _rng(5)
+    x = r.standard_normal((2, 3, 6))
+    p = r.standard_normal((7, 4))
+    with_ones = np.concatenate([x, np.ones((2, 3, 1))], -1)
+    np.testing.assert_allclose(oracle.project(x, p[:-1], p[-1]), with_ones @ p, rtol=1e-12)
+
+
+def test_project_outer_is_kronecker_of_materialized():
+    """materialize(project) == P_out^T dW P_in (vec-Kronecker identity)."""
+    r = _rng(6)
+    a, g = r.standard_normal((3, 8, 6)), r.standard_normal((3, 8, 5))
+    p_in, p_out = r.standard_normal((7, 4)), r.standard_normal((5, 3))
+    got = oracle.project_outer(a, g, p_in, p_out, bias=True).reshape(3, 3, 4)
+    dw = oracle.materialize_linear(a, g, bias=True).reshape(3, 5, 7)
+    want = np.einsum("go,bgi,ik->bok", p_out, dw, p_in)
+    np.testing.assert_allclose(got, want, rtol=1e-10)
+
+
+# ---------------------------------------------------------------------------
+# score GEMM and cost rules
+# ---------------------------------------------------------------------------
+
+
+def test_score_gemm_matches_loops():
+    r = _rng(7)
+    m1 = [r.standard_normal((3, 5)), r.standard_normal((3, 2))]
+    m2 = [r.standard_normal((4, 5)), r.standard_normal((4, 2))]
+    want = np.array([[sum(float(m1[L][i] @ m2[L][j]) for L in range(2)) for j in range(4)] for i in range(3)])
+    np.testing.assert_allclose(oracle.score_gemm(m1, m2), want, rtol=1e-12)
+
+
+def _known():
+    with open(os.path.join(GOLDEN, "routing_known_answers.json")) as f:
+        return json.load(f)
+
+
+def test_cost_rules_known_answers():
+    k = _known()
+    for c in k["maybe_materialize_projected"]:
+        assert oracle.maybe_materialize_projected(c["seq_len"], c["k_a"], c["k_g"], c["kappa"]) is c["expected"]
+    for c in k["should_materialize"]:
+        assert oracle.should_materialize(c["style"], c["seq_len"], c["k_a"], c["k_g"]) is c["expected"]
+    for c in k["maybe_use_materialized_gram"]:
+        assert oracle.maybe_use_materialized_gram(c["B1"], c["B2"], c["S"], c["K"], c["D"]) is c["expected"]
+    with pytest.raises(ValueError, match="capture_style"):
+        oracle.should_materialize("bogus", 4, 8, 8)
+
+
+def test_cost_rule_is_the_flop_comparison():
+    """A route the rule calls cheaper really has fewer counted flops."""
+    for b1, b2, s, k, d in [(8, 64, 2048, 4096, 14336), (256, 64, 512, 4096, 4096), (8, 1, 4, 8, 8)]:
+        f = b1 * b2 * s * s * (k + d)
+        m = (b1 + b2) * s * d * k + b1 * b2 * d * k
+        assert oracle.maybe_use_materialized_gram(b1, b2, s, k, d) == (f >= m)
+
+
+# ---------------------------------------------------------------------------
+# MoE
+# ---------------------------------------------------------------------------
+
+
+def test_router_matches_torch_topk():
+    logits = torch.randn(300, 8, generator=torch.Generator().manual_seed(8))
+    w, idx = oracle.moe_router_topk(logits.numpy(), 2)
+    probs = torch.softmax(logits.float(), dim=-1)
+    tv, ti = torch.topk(probs, 2, dim=-1)
+    assert np.array_equal(idx, ti.numpy())
+    np.testing.assert_allclose(w, (tv / tv.sum(-1, keepdim=True)).numpy(), rtol=1e-6)
+
+
+def test_segments_match_torch_where_order():
+    idx = torch.randint(0, 8, (50, 2), generator=torch.Generator().manual_seed(9))
+    mask = torch.nn.functional.one_hot(idx, num_classes=8).permute(2, 1, 0)
+    segs = oracle.moe_segments(idx.numpy(), 8)
+    for e in range(8):
+        pos, tok = torch.where(mask[e])
+        assert np.array_equal(segs[e][0], pos.numpy()) and np.array_equal(segs[e][1], tok.numpy())
+
+
+def test_segment_ghost_equals_dense_with_zeros_by_brute_force():
+    r = _rng(10)
+    batch, tokens = 3, 5
+    tok1 = np.array([0, 3, 7, 8, 14])
+    tok2 = np.array([1, 2, 9])
+    a1, g1 = r.standard_normal((5, 4)), r.standard_normal((5, 3))
+    a2, g2 = r.standard_normal((3, 4)), r.standard_normal((3, 3))
+    got = oracle.moe_segment_ghost(a1, g1, tok1, a2, g2, tok2, batch, batch, tokens, tokens)
+    want = np.zeros((batch, batch))
+    for p in range(5):
+        for q in range(3):
+            want[tok1[p] // tokens, tok2[q] // tokens] += float(a1[p] @ a2[q]) * float(g1[p] @ g2[q])
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# C1 end to end: oracle from captured factors == autograd ground truth fixture
+# ---------------------------------------------------------------------------
+
+
+def test_c1_oracle_matches_autograd_fixture():
+    from c1_model import c1_inputs, capture_factors
+
+    with open(os.path.join(GOLDEN, "c1_scores.json")) as f:
+        fixture = json.load(f)
+    model, train, query = c1_inputs(0)
+    assert int(train.sum()) == fixture["train_ids_checksum"]
+    assert int(query.sum()) == fixture["query_ids_checksum"]
+    f_tr = capture_factors(model, train)
+    f_q = capture_factors(model, query)
+    total = None
+    for name in f_tr:
+        a1, g1 = (t.double().numpy() for t in f_tr[name])
+        a2, g2 = (t.double().numpy() for t in f_q[name])
+        part = oracle.cross_gram(a1, g1, a2, g2, "nn.Linear", mode="factorized", bias=True)
+        total = part if total is None else total + part
+    assert rel_err(total, np.array(fixture["scores"])) <= 1e-5
