@@ -12,7 +12,10 @@
 // the row-major captures.  Each stage therefore loads 8x8 (bf16/f16) or 4x4
 // (fp32) blocks with 16-byte row loads, transposes them in registers and
 // stores them into LDS token-contiguous, so the MFMA fragment reads are single
-// 16-byte LDS reads.  A workgroup owns a 128 (o) x 128 (k) output tile of one
+// 16-byte LDS reads.  Consecutive lanes take consecutive token blocks of one
+// column block, so the 8 lanes the LDS serves together write one 128-byte row
+// (all banks distinct); mapping them to consecutive column blocks instead puts
+// their rows 8 apart and folds them onto two bank groups.  A workgroup owns a 128 (o) x 128 (k) output tile of one
 // sample; the fp32 accumulators are converted to the output dtype and staged
 // through LDS so the tile leaves as coalesced 16-byte row stores.
 #include "common.h"
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(kThreads, 2) void materialize_tiles(MatArgs m) {
 #pragma unroll
     for (int q = 0; q < PER_THREAD; ++q) {
       const int bi = tsub + q * (kThreads / 2);
-      const int bt = bi / BLK_C, bc = bi % BLK_C;
+      const int bt = bi % BLK_T, bc = bi / BLK_T;
       const int64_t col = c0 + (int64_t)bc * VEC;
       const bool cin = col < width;
 #pragma unroll
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(kThreads, 2) void materialize_tiles(MatArgs m) {
 #pragma unroll
     for (int q = 0; q < PER_THREAD; ++q) {
       const int bi = tsub + q * (kThreads / 2);
-      const int bt = bi / BLK_C, bc = bi % BLK_C;
+      const int bt = bi % BLK_T, bc = bi / BLK_T;
       u32x4 tr[VEC];
       transpose_block<DT>(blk[q], tr);
 #pragma unroll
@@ -202,6 +205,149 @@ __global__ __launch_bounds__(kThreads, 2) void materialize_tiles(MatArgs m) {
   }
 }
 
+// Large-tile variant for the big layers: a 256 (o) x 256 (k) tile per
+// workgroup, one wave per SIMD, each wave a 128 x 128 block (4 x 4 MFMA blocks,
+// 256 fp32 accumulators).  Twice the MFMA work per LDS byte of the 128-tile
+// kernel and four times the work per stage to hide the next stage's loads.
+namespace big {
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kStageBytes = (kBM + kBN) * kLdsRow;  // 73,728 B; two stages fit LDS
+}  // namespace big
+
+template <int DT, int OT>
+__global__ __launch_bounds__(kThreads, 1) void materialize_tiles_big(MatArgs m) {
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int ES = Elem<DT>::kBytes;
+  constexpr int TS = kRowBytes / ES;           // tokens per stage
+  constexpr int BLK_T = TS / VEC;              // token blocks per stage
+  constexpr int BLK_C = big::kBM / VEC;        // column blocks per operand tile
+  constexpr int BLOCKS = BLK_T * BLK_C;        // blocks per operand per stage
+  constexpr int PER_THREAD = BLOCKS / (kThreads / 2);
+  static_assert(PER_THREAD >= 1 && BLOCKS % (kThreads / 2) == 0, "stage/block mismatch");
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];  // 2 * big::kStageBytes
+
+  const int64_t ntiles = (int64_t)gridDim.x;
+  const int64_t logical = xcd_remap(blockIdx.x, ntiles);
+  const int64_t per_sample = m.tiles_m * m.tiles_n;
+  const int64_t b = logical / per_sample;
+  const int64_t rem = logical - b * per_sample;
+  const int64_t per_group = (int64_t)kGroup * m.tiles_n;
+  const int64_t group = rem / per_group;
+  const int64_t first = group * kGroup;
+  const int64_t gsize = min(m.tiles_m - first, (int64_t)kGroup);
+  const int64_t in_group = rem - group * per_group;
+  const int64_t tm = first + in_group % gsize;
+  const int64_t tn = in_group / gsize;
+  const int64_t o0 = tm * big::kBM, k0 = tn * big::kBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int side = tid / (kThreads / 2);
+  const int tsub = tid % (kThreads / 2);
+  const char* src = side == 0 ? m.g + b * m.g_bstride : m.a + b * m.a_bstride;
+  const int64_t tstride = side == 0 ? m.g_tstride : m.a_tstride;
+  const int64_t width = side == 0 ? m.d : m.k;
+  const int64_t c0 = side == 0 ? o0 : k0;
+
+  u32x4 blk[PER_THREAD][VEC];
+  auto gload = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int bi = tsub + q * (kThreads / 2);
+      const int bt = bi % BLK_T, bc = bi / BLK_T;
+      const int64_t col = c0 + (int64_t)bc * VEC;
+      const bool cin = col < width;
+#pragma unroll
+      for (int r = 0; r < VEC; ++r) {
+        const int64_t t = (int64_t)st * TS + bt * VEC + r;
+        blk[q][r] = (cin && t < m.tokens) ? ld16(src + t * tstride + col * ES) : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
+    char* base = smem + buf * big::kStageBytes + (side == 0 ? 0 : big::kBM * kLdsRow);
+#pragma unroll
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int bi = tsub + q * (kThreads / 2);
+      const int bt = bi % BLK_T, bc = bi / BLK_T;
+      u32x4 tr[VEC];
+      transpose_block<DT>(blk[q], tr);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) st16(base + (bc * VEC + c) * kLdsRow + bt * 16, tr[c]);
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) acc[x][y] = f32x16{};
+
+  const int nst = (int)((m.tokens + TS - 1) / TS);
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int frow = lane & 31, fhalf = lane >> 5;
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) gload(st + 1);
+    const char* base = smem + buf * big::kStageBytes;
+#pragma unroll
+    for (int kg = 0; kg < kRowBytes / 32; ++kg) {
+      u32x4 fa[4], fb[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        fa[x] = ld16(base + (128 * wm + 32 * x + frow) * kLdsRow + 32 * kg + 16 * fhalf);
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+        fb[y] = ld16(base + (big::kBM + 128 * wn + 32 * y + frow) * kLdsRow + 32 * kg + 16 * fhalf);
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) Mfma32<DT>::mma(acc[x][y], fa[x], fb[y]);
+    }
+    if (st + 1 < nst) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: each wave stages its 128 x 128 block in LDS (output dtype), in
+  // passes of kPassRows rows so fp32 fits, and writes whole 16-byte chunks.
+  constexpr int OS = Elem<OT>::kBytes;
+  constexpr int kPassRows = OS == 4 ? 64 : 128;
+  constexpr int ROWB = 128 * OS;
+  char* wbuf = smem + wave * (kPassRows * ROWB);
+  const int64_t orow0 = o0 + 128 * wm, ocol0 = k0 + 128 * wn;
+  char* obase = m.out + (b * m.out_bstride) * OS;
+#pragma unroll
+  for (int pass = 0; pass < 128 / kPassRows; ++pass) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      if ((32 * x) / kPassRows != pass) continue;
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * x + acc_row(r, lane) - pass * kPassRows, col = 32 * y + acc_col(lane);
+          Elem<OT>::store(wbuf, (int64_t)row * 128 + col, acc[x][y][r]);
+        }
+    }
+    __syncthreads();
+    constexpr int CH = ROWB / 16;
+    constexpr int RPP = 64 / CH;  // rows per 64-lane pass
+    for (int rr = 0; rr < kPassRows; rr += RPP) {
+      const int row = rr + lane / CH, ch = lane % CH;
+      const int64_t orow = orow0 + pass * kPassRows + row;
+      const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
+      if (orow < m.d && ocol < m.k)
+        st16(obase + (orow * m.out_rstride + ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
+    }
+    __syncthreads();
+  }
+}
+
 // Bias column dW[b, o, K] = sum_t g[b, t, o]: one thread per (b, o).
 template <int DT, int OT>
 __global__ void bias_column(const char* g, int64_t batch, int64_t tokens, int64_t d,
@@ -224,7 +370,23 @@ int launch(const MatArgs& m, int has_bias, hipStream_t st) {
   const bool aligned = (m.k % (16 / Elem<OT>::kBytes) == 0) &&
                        ((m.out_rstride * Elem<OT>::kBytes) % 16 == 0) &&
                        ((m.out_bstride * Elem<OT>::kBytes) % 16 == 0) && (((uintptr_t)m.out & 15) == 0);
-  if (ntiles > 0) {
+  const bool use_big = aligned && m.d >= big::kBM && m.k >= big::kBN && m.k % 8 == 0;
+  if (use_big) {
+    MatArgs mb = m;
+    mb.tiles_m = (m.d + big::kBM - 1) / big::kBM;
+    mb.tiles_n = (m.k + big::kBN - 1) / big::kBN;
+    const int64_t nb = m.batch * mb.tiles_m * mb.tiles_n;
+    const size_t lds = 2 * (size_t)big::kStageBytes;
+    static bool attr_set = false;  // idempotent; per template instance
+    if (!attr_set) {
+      hipFuncSetAttribute((const void*)materialize_tiles_big<DT, OT>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      attr_set = true;
+    }
+    materialize_tiles_big<DT, OT><<<(unsigned)nb, kThreads, lds, st>>>(mb);
+    int rc = check_launch("da_materialize_linear(big tiles)");
+    if (rc) return rc;
+  } else if (ntiles > 0) {
     if (aligned)
       materialize_tiles<DT, OT, true><<<(unsigned)ntiles, kThreads, 0, st>>>(m);
     else

@@ -36,6 +36,8 @@ MAT_CASES = [
     (1, 1, 8, 8, False),
     (2, 130, 256, 136, True),
     (4, 33, 100, 60, False),      # widths not multiples of 8 -> padded path
+    (2, 100, 264, 520, False),    # 256x256-tile kernel, partial tiles on both axes
+    (1, 2048, 512, 768, False),   # 256x256-tile kernel, long token axis
 ]
 
 
