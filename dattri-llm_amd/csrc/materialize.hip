@@ -39,8 +39,16 @@ struct MatArgs {
   int64_t g_bstride, g_tstride;              // bytes
   char* out;
   int64_t out_bstride, out_rstride;          // elements
+  int64_t out_blk;                           // elements between 64-element output blocks
   int64_t tiles_m, tiles_n;                  // per sample
 };
+
+// Element offset (from the sample's base) of output (o, k): flat c = o*rstride + k
+// stored in 64-element blocks out_blk apart (out_blk == 64: plain row-major).
+__device__ __forceinline__ int64_t out_index(const MatArgs& m, int64_t o, int64_t k) {
+  const int64_t c = o * m.out_rstride + k;
+  return (c >> 6) * m.out_blk + (c & 63);
+}
 
 // Transpose a VEC x VEC block held as VEC rows of one 16-byte chunk each.
 template <int DT>
@@ -189,7 +197,7 @@ __global__ __launch_bounds__(kThreads, 2) void materialize_tiles(MatArgs m) {
       const int64_t orow = orow0 + row;
       const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
       if (orow < m.d && ocol < m.k)
-        st16(obase + (orow * m.out_rstride + ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
+        st16(obase + out_index(m, orow, ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
     }
   } else {
     for (int e = lane; e < 64 * 64; e += 64) {
@@ -197,9 +205,9 @@ __global__ __launch_bounds__(kThreads, 2) void materialize_tiles(MatArgs m) {
       const int64_t orow = orow0 + row, ocol = ocol0 + col;
       if (orow < m.d && ocol < m.k) {
         if constexpr (OS == 4)
-          ((uint32_t*)obase)[orow * m.out_rstride + ocol] = ((const uint32_t*)wbuf)[e];
+          ((uint32_t*)obase)[out_index(m, orow, ocol)] = ((const uint32_t*)wbuf)[e];
         else
-          ((uint16_t*)obase)[orow * m.out_rstride + ocol] = ((const uint16_t*)wbuf)[e];
+          ((uint16_t*)obase)[out_index(m, orow, ocol)] = ((const uint16_t*)wbuf)[e];
       }
     }
   }
@@ -342,7 +350,7 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_big(MatArgs m) 
       const int64_t orow = orow0 + pass * kPassRows + row;
       const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
       if (orow < m.d && ocol < m.k)
-        st16(obase + (orow * m.out_rstride + ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
+        st16(obase + out_index(m, orow, ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
     }
     __syncthreads();
   }
@@ -352,14 +360,15 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_big(MatArgs m) 
 template <int DT, int OT>
 __global__ void bias_column(const char* g, int64_t batch, int64_t tokens, int64_t d,
                             int64_t g_bstride, int64_t g_tstride, char* out, int64_t out_bstride,
-                            int64_t out_rstride, int64_t kcol) {
+                            int64_t out_rstride, int64_t out_blk, int64_t kcol) {
   const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t b = blockIdx.y;
   if (o >= d) return;
   const char* src = g + b * g_bstride;
   float s = 0.f;
   for (int64_t t = 0; t < tokens; ++t) s += Elem<DT>::load(src + t * g_tstride, o);
-  Elem<OT>::store(out, b * out_bstride + o * out_rstride + kcol, s);
+  const int64_t c = o * out_rstride + kcol;
+  Elem<OT>::store(out, b * out_bstride + (c >> 6) * out_blk + (c & 63), s);
 }
 
 template <int DT, int OT>
@@ -369,6 +378,7 @@ int launch(const MatArgs& m, int has_bias, hipStream_t st) {
   // 16-byte output stores need whole output chunks inside every row.
   const bool aligned = (m.k % (16 / Elem<OT>::kBytes) == 0) &&
                        ((m.out_rstride * Elem<OT>::kBytes) % 16 == 0) &&
+                       ((m.out_blk * Elem<OT>::kBytes) % 16 == 0) &&
                        ((m.out_bstride * Elem<OT>::kBytes) % 16 == 0) && (((uintptr_t)m.out & 15) == 0);
   const bool use_big = aligned && m.d >= big::kBM && m.k >= big::kBN && m.k % 8 == 0;
   if (use_big) {
@@ -397,7 +407,7 @@ int launch(const MatArgs& m, int has_bias, hipStream_t st) {
   if (has_bias) {
     dim3 grid((unsigned)((m.d + 255) / 256), (unsigned)m.batch);
     bias_column<DT, OT><<<grid, 256, 0, st>>>(m.g, m.batch, m.tokens, m.d, m.g_bstride, m.g_tstride,
-                                              m.out, m.out_bstride, m.out_rstride, m.k);
+                                              m.out, m.out_bstride, m.out_rstride, m.out_blk, m.k);
     return check_launch("da_materialize_linear(bias)");
   }
   return DA_OK;
@@ -410,7 +420,7 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
                                      int64_t tokens, int64_t K, int64_t D, int64_t a_bstride,
                                      int64_t a_tstride, int64_t g_bstride, int64_t g_tstride,
                                      int has_bias, void* out, int out_dtype, int64_t out_bstride,
-                                     int64_t out_rstride, void* stream) {
+                                     int64_t out_rstride, int64_t out_blk, void* stream) {
   using namespace da;
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype))
     return set_error(DA_ERR_INVALID, "da_materialize_linear: bad dtype");
@@ -428,6 +438,12 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
     return set_error(DA_ERR_INVALID, "da_materialize_linear: strides must be multiples of 16 bytes");
   if (out_rstride < K + (has_bias ? 1 : 0))
     return set_error(DA_ERR_INVALID, "da_materialize_linear: out row stride too small");
+  if (out_blk == 0) out_blk = 64;
+  if (out_blk < 64) return set_error(DA_ERR_INVALID, "da_materialize_linear: out_blk must be 0 or >= 64");
+  if (out_blk != 64 && ((out_rstride % 64) || out_bstride < 64))
+    return set_error(DA_ERR_INVALID,
+                     "da_materialize_linear: a blocked output needs a row stride multiple of 64 and "
+                     "out_bstride >= 64");
   if (tokens == 0) return set_error(DA_ERR_INVALID, "da_materialize_linear: tokens must be >= 1");
   MatArgs m;
   m.a = (const char*)a;
@@ -443,6 +459,7 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
   m.out = (char*)out;
   m.out_bstride = out_bstride;
   m.out_rstride = out_rstride;
+  m.out_blk = out_blk;
   m.tiles_m = (D + kBM - 1) / kBM;
   m.tiles_n = (K + kBN - 1) / kBN;
   hipStream_t st = (hipStream_t)stream;

@@ -32,10 +32,20 @@ constexpr int kUnit = 4 * kStep;  // chunk granularity: one iteration of every w
 struct LayerDev {
   const char* m1;
   const char* m2;
-  int64_t bytes;     // row width in bytes (multiple of 16)
-  int64_t ld1, ld2;  // row strides in bytes
-  int64_t chunk0;    // first global chunk index of this layer
+  int64_t bytes;       // row width in bytes (multiple of 16)
+  int64_t ld1, ld2;    // row strides in bytes
+  int64_t blk1, blk2;  // strides between consecutive 64-element blocks of a row, in bytes
+  int64_t chunk0;      // first global chunk index of this layer
 };
+
+// Byte address of logical byte `off` of a row: rows are sequences of
+// 64-element blocks (kBlk bytes) placed blk bytes apart -- blk == kBlk is the
+// plain row-major layout, blk == rows * kBlk the k-blocked (sample-interleaved)
+// layout in which one block of every row is contiguous.
+template <int kBlk>
+__device__ __forceinline__ const char* at(const char* row, int64_t blk, int64_t off) {
+  return row + (off / kBlk) * blk + (off % kBlk);
+}
 
 struct ScoreArgs {
   LayerDev layers[kMaxLayers];
@@ -49,6 +59,7 @@ struct ScoreArgs {
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void score_gemm_chunks(ScoreArgs s) {
+  constexpr int kBlk = 64 * Elem<DT>::kBytes;  // bytes of one 64-element block
   __shared__ float red[3][kTileM * kTileN];
 
   const int64_t chunk = blockIdx.x;
@@ -82,10 +93,10 @@ __global__ __launch_bounds__(kThreads) void score_gemm_chunks(ScoreArgs s) {
     for (int st = 0; st < 4; ++st) {
       const int64_t off = base + 64 * st + 16 * q;
       const bool in = off < w1;
-      va[st] = (p1 && in) ? ld16(p1 + off) : u32x4{0, 0, 0, 0};
+      va[st] = (p1 && in) ? ld16(at<kBlk>(p1, L.blk1, off)) : u32x4{0, 0, 0, 0};
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
-        vb[blk][st] = (p2[blk] && in) ? ld16(p2[blk] + off) : u32x4{0, 0, 0, 0};
+        vb[blk][st] = (p2[blk] && in) ? ld16(at<kBlk>(p2[blk], L.blk2, off)) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int st = 0; st < 4; ++st)
@@ -161,6 +172,8 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
                        "da_score_gemm: layer %d width/strides must be multiples of 16 bytes", l);
     if (L.width > 0 && (!L.m1 || !L.m2 || (((uintptr_t)L.m1 | (uintptr_t)L.m2) & 15)))
       return set_error(DA_ERR_INVALID, "da_score_gemm: layer %d pointers NULL or misaligned", l);
+    if (L.blk1 < 0 || L.blk2 < 0 || ((L.blk1 * es) % 16) || ((L.blk2 * es) % 16))
+      return set_error(DA_ERR_INVALID, "da_score_gemm: layer %d block strides must be >= 0 and 16-byte multiples", l);
     total += L.width * es;
   }
   // Aim for ~4096 chunks over all layers (16 waves per CU), at least one
@@ -219,6 +232,8 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
     s.layers[l].bytes = layers[l].width * es;
     s.layers[l].ld1 = layers[l].ld1 * es;
     s.layers[l].ld2 = layers[l].ld2 * es;
+    s.layers[l].blk1 = (layers[l].blk1 ? layers[l].blk1 : 64) * es;
+    s.layers[l].blk2 = (layers[l].blk2 ? layers[l].blk2 : 64) * es;
     s.layers[l].chunk0 = c;
     c += (s.layers[l].bytes + p.chunk_bytes - 1) / p.chunk_bytes;
   }

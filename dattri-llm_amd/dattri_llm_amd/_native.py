@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdattri_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DA_F32, DA_F16, DA_BF16 = 0, 1, 2
 DA_OK, DA_ERR_INVALID, DA_ERR_UNSUPPORTED, DA_ERR_HIP, DA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -72,6 +72,8 @@ class DenseLayer(ctypes.Structure):
         ("width", ctypes.c_int64),
         ("ld1", ctypes.c_int64),
         ("ld2", ctypes.c_int64),
+        ("blk1", ctypes.c_int64),
+        ("blk2", ctypes.c_int64),
     ]
 
 
@@ -80,7 +82,7 @@ SIGNATURES.update(
     {
         "da_materialize_linear": (
             _I32,
-            [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _I32, _I64, _I64, _P],
+            [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P],
         ),
         "da_score_gemm_workspace": (_I32, [_I64, _I64, _LAYERS, _I32, _I32, ctypes.POINTER(_SZ)]),
         "da_score_gemm": (

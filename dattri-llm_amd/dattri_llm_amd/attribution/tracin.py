@@ -19,6 +19,7 @@ from dattri_llm_amd.attribution.score import AttributionScore
 from dattri_llm_amd.attribution.utils import finalize_factors, score_sources
 from dattri_llm_amd.gradient import ops
 from dattri_llm_amd.gradient.gradient import Factorized, Gradient
+from dattri_llm_amd.gradient.ops.materialize import materialize_blocked
 from dattri_llm_amd.utils.cache import CacheBudget
 
 
@@ -71,7 +72,8 @@ class TracInAttributor:
                 dense.append(name)
                 held += growth
         if dense:
-            test_rep = test_rep.map_layers(lambda _n, v, t: ops.materialize(v, t), layers=dense, consume=True)
+            # resident dense query layers in the k-blocked layout the score GEMM streams
+            test_rep = test_rep.map_layers(lambda _n, v, t: materialize_blocked(v, t), layers=dense, consume=True)
         return finalize_factors(test_rep, budget=budget, held=held)
 
     def inner_product(self, train_rep: Gradient, test_rep: Gradient, *, dense_cache=None) -> torch.Tensor:

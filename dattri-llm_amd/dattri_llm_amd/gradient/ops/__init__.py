@@ -25,7 +25,7 @@ from dattri_llm_amd.gradient.ops.dot import (
     pairwise_dot_factors,
 )
 from dattri_llm_amd.gradient.ops.dtypes import as_float, compute_dtype, get_compute_dtype, set_compute_dtype
-from dattri_llm_amd.gradient.ops.materialize import materialize, materialize_factors
+from dattri_llm_amd.gradient.ops.materialize import materialize, materialize_blocked, materialize_factors
 from dattri_llm_amd.gradient.ops.preprocess import (
     extract_module_kwargs,
     preprocess_factorized,
@@ -76,7 +76,7 @@ __all__ = [
     "extract_module_kwargs", "gaussian_projector", "get_compute_dtype", "get_routing_policy",
     "grad_norm_sq", "grad_norm_sq_factors", "is_conv", "is_conv_transpose", "is_embedding",
     "is_kfac_eligible", "is_linear", "is_norm", "layerwise_cross_dot", "layerwise_cross_dot_per_token",
-    "materialize", "materialize_factors", "maybe_materialize_projected", "maybe_use_materialized_gram",
+    "materialize", "materialize_blocked", "materialize_factors", "maybe_materialize_projected", "maybe_use_materialized_gram",
     "maybe_use_materialized_norm", "moe", "pairwise_dot", "pairwise_dot_factors", "preprocess_factorized",
     "preprocess_factors", "project_activation", "project_factorized", "project_factors",
     "project_gradient", "project_layer", "project_outer_factors", "set_compute_dtype",

@@ -31,6 +31,7 @@ from dattri_llm_amd.gradient.ops import cost, dtypes
 from dattri_llm_amd.gradient.ops.materialize import (
     linear_dense,
     materialize,
+    materialize_blocked,
     norm_grad_from_final,
     norm_grad_from_raw,
 )
@@ -57,9 +58,15 @@ def _kernel_operands(*tensors):
     return tuple(t.to(kd) for t in aligned), out_dtype
 
 
+def _rows(m: torch.Tensor) -> torch.Tensor:
+    """A dense layer as the score kernel takes it: k-blocked views as they are
+    (reshaping one would copy it), anything else flattened to (B, d)."""
+    return m if kernels.is_blocked(m) else m.reshape(m.shape[0], -1)
+
+
 def _dense_gram(m1: torch.Tensor, m2: torch.Tensor, out=None, accumulate=False) -> torch.Tensor:
     """fp32 ``m1 @ m2.T`` of two dense (B, d) blocks via the score kernel."""
-    (m1, m2), _ = _kernel_operands(m1.reshape(m1.shape[0], -1), m2.reshape(m2.shape[0], -1))
+    (m1, m2), _ = _kernel_operands(_rows(m1), _rows(m2))
     return kernels.score_gemm([(m1, m2)], out=out, accumulate=accumulate)
 
 
@@ -81,8 +88,8 @@ def _linear_gram32(a1, g1, bias1, a2, g2, bias2, mode, out=None, accumulate=Fals
     if mode == "auto":
         mode = _route(b1, b2, s, k + int(bias1), d)
     if mode == "materialized":
-        m1 = kernels.materialize_linear(a1, g1, bias=bias1)
-        m2 = kernels.materialize_linear(a2, g2, bias=bias2)
+        m1 = kernels.materialize_linear(a1, g1, bias=bias1, blocked=True)
+        m2 = kernels.materialize_linear(a2, g2, bias=bias2, blocked=True)
         return kernels.score_gemm([(m1, m2)], out=out, accumulate=accumulate)
     if mode != "factorized":
         raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
@@ -263,8 +270,8 @@ def layerwise_cross_dot(train, test, *, layers: Iterable[str] | None = None, mod
             continue
         tr, te = train.data[name], test.data[name]
         if isinstance(te, torch.Tensor) and not isinstance(tr, torch.Tensor):
-            tr = (dense_cache.get_or_compute(name, lambda tr=tr, lt=layer_type: materialize(tr, lt))
-                  if dense_cache is not None else materialize(tr, layer_type))
+            tr = (dense_cache.get_or_compute(name, lambda tr=tr, lt=layer_type: materialize_blocked(tr, lt))
+                  if dense_cache is not None else materialize_blocked(tr, layer_type))
         pairs.append((name, layer_type, tr, te))
     if reduce == "none":
         return {n: cross_dot(tr, te, lt, mode=mode) for n, lt, tr, te in pairs}
@@ -286,7 +293,7 @@ def layerwise_cross_dot(train, test, *, layers: Iterable[str] | None = None, mod
     for name, lt, tr, te in pairs:
         full = _batch(tr) == b_tr and _batch(te) == b_te
         if full and isinstance(tr, torch.Tensor) and isinstance(te, torch.Tensor):
-            (m1, m2), _ = _kernel_operands(tr.reshape(b_tr, -1), te.reshape(b_te, -1))
+            (m1, m2), _ = _kernel_operands(_rows(tr), _rows(te))
             dense_groups.setdefault(m1.dtype, []).append((m1, m2))
         else:
             rest.append((name, lt, tr, te, full))

@@ -103,6 +103,26 @@ def materialize_factors(
     return linear_dense(a, g, bias)
 
 
+def materialize_blocked(f, layer_type: str, include_bias: bool = True) -> torch.Tensor:
+    """:func:`materialize` for a dense copy that only the score kernel reads.
+
+    Linear layers without a bias column whose input width is a multiple of 64
+    come back in the k-blocked layout -- the ``(B, W/64, 64)`` view of a
+    buffer in which block j of every sample is one contiguous run, which the
+    score GEMM streams at full HBM rate.  Other layers are materialized as
+    usual.  ``x.reshape(B, -1)`` recovers the reference's ``(B, d)`` matrix."""
+    if isinstance(f, torch.Tensor) or not is_linear(layer_type):
+        return materialize(f, layer_type, include_bias)
+    bf = f.as_batch_first()
+    a, g, bias = final_linear(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
+                              include_bias)
+    if bias or a.ndim == 4 or to_3d(a).shape[-1] % 64:
+        return materialize(f, layer_type, include_bias)
+    (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
+    out = kernels.materialize_linear(ao, go, out_dtype=dtypes.kernel_dtype(out_dtype), blocked=True)
+    return out.to(out_dtype)
+
+
 def materialize(f, layer_type: str, include_bias: bool = True, per_token: bool = False) -> torch.Tensor:
     """Per-sample weight gradient of one layer, whatever its form (materialize.py:119-146)."""
     if isinstance(f, torch.Tensor):

@@ -118,14 +118,30 @@ def ghost_gram(
     return out
 
 
+def is_blocked(x: torch.Tensor) -> bool:
+    """A (B, W/64, 64) view of a dense (B, W) block stored in 64-element blocks."""
+    return x.dim() == 3 and x.shape[2] == 64 and x.stride(2) == 1
+
+
+def blocked_storage(b: int, width: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """An uninitialised k-blocked (B, width) block: the (B, width/64, 64) view
+    of a (width/64, B, 64) buffer, so block j of every sample is one run."""
+    return torch.empty(width // 64, b, 64, dtype=dtype, device=device).permute(1, 0, 2)
+
+
 def materialize_linear(
     a: torch.Tensor,
     g: torch.Tensor,
     *,
     bias: bool = False,
     out_dtype: torch.dtype | None = None,
+    blocked: bool = False,
 ) -> torch.Tensor:
-    """Per-sample linear weight gradient ``(B, D*(K+bias))``, index o*(K+bias)+k."""
+    """Per-sample linear weight gradient ``(B, D*(K+bias))``, index o*(K+bias)+k.
+
+    With ``blocked`` (and K a multiple of 64, no bias) the result is written in
+    the k-blocked layout and returned as its ``(B, D*K/64, 64)`` view (see
+    :func:`is_blocked`); otherwise ``blocked`` is ignored."""
     dev = nat.require_device(a, g)
     if a.dim() != 3 or g.dim() != 3 or a.shape[:2] != g.shape[:2]:
         raise ValueError("materialize_linear expects a (B, T, K) and g (B, T, D)")
@@ -135,6 +151,18 @@ def materialize_linear(
     b, t, k = a.shape
     d = g.shape[-1]
     kb = k + int(bias)
+    if blocked and not bias and k % 64 == 0 and d % _chunk_elems(a.dtype) == 0 and b > 0 and t > 0:
+        out = blocked_storage(b, d * k, out_dtype, dev)
+        a, g = prepare_rows(a, k), prepare_rows(g, d)
+        nat.check(
+            nat.load().da_materialize_linear(
+                a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d,
+                a.stride(0), a.stride(1), g.stride(0), g.stride(1), 0,
+                out.data_ptr(), nat.dtype_code(out_dtype), 64, k, b * 64, nat.stream_ptr(dev),
+            ),
+            "materialize_linear",
+        )
+        return out
     out = torch.empty(b, d * kb, dtype=out_dtype, device=dev)
     if b == 0 or d == 0 or kb == 0:
         return out
@@ -156,7 +184,7 @@ def materialize_linear(
         nat.load().da_materialize_linear(
             a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d,
             a.stride(0), a.stride(1), g.stride(0), g.stride(1), int(bias),
-            out.data_ptr(), nat.dtype_code(out_dtype), d * kb, kb, nat.stream_ptr(dev),
+            out.data_ptr(), nat.dtype_code(out_dtype), d * kb, kb, 64, nat.stream_ptr(dev),
         ),
         "materialize_linear",
     )
@@ -188,14 +216,21 @@ def score_gemm(
     """
     if not pairs:
         raise ValueError("score_gemm needs at least one layer pair")
-    flat = [(m1.reshape(m1.shape[0], -1), m2.reshape(m2.shape[0], -1)) for m1, m2 in pairs]
+
+    def rows(m):  # k-blocked views pass as they are; anything else as (B, W)
+        return m if is_blocked(m) else m.reshape(m.shape[0], -1)
+
+    def width(m):
+        return m.shape[1] * 64 if is_blocked(m) else m.shape[1]
+
+    flat = [(rows(m1), rows(m2)) for m1, m2 in pairs]
     dev = nat.require_device(*[t for p in flat for t in p])
     dtype = flat[0][0].dtype
     b1, b2 = flat[0][0].shape[0], flat[0][1].shape[0]
     for m1, m2 in flat:
         if m1.dtype != dtype or m2.dtype != dtype:
             raise ValueError("score_gemm layers must share one dtype")
-        if m1.shape[0] != b1 or m2.shape[0] != b2 or m1.shape[1] != m2.shape[1]:
+        if m1.shape[0] != b1 or m2.shape[0] != b2 or width(m1) != width(m2):
             raise ValueError("score_gemm layer shapes disagree")
     if out is None:
         out = torch.empty(b1, b2, dtype=torch.float32, device=dev)
@@ -206,13 +241,23 @@ def score_gemm(
     swap = b1 > b2
     layers = []
     keep = []
+    def operand(m, w):
+        """(tensor, row stride, block stride) in elements for the kernel."""
+        if is_blocked(m) and m.data_ptr() % 16 == 0 and all(
+                (st * m.element_size()) % 16 == 0 for st in m.stride()[:2]):
+            return m, m.stride(0), m.stride(1)
+        if is_blocked(m):
+            m = m.reshape(m.shape[0], -1)
+        m = prepare_rows(m, w)
+        return m, m.stride(0), 64
+
     for m1, m2 in flat:
-        w = -(-m1.shape[1] // vec) * vec
-        m1, m2 = prepare_rows(m1, w), prepare_rows(m2, w)
+        w = -(-width(m1) // vec) * vec
+        (m1, ld1, bk1), (m2, ld2, bk2) = operand(m1, w), operand(m2, w)
         keep += [m1, m2]
         if swap:
-            m1, m2 = m2, m1
-        layers.append(nat.DenseLayer(m1.data_ptr(), m2.data_ptr(), w, m1.stride(0), m2.stride(0)))
+            m1, ld1, bk1, m2, ld2, bk2 = m2, ld2, bk2, m1, ld1, bk1
+        layers.append(nat.DenseLayer(m1.data_ptr(), m2.data_ptr(), w, ld1, ld2, bk1, bk2))
     n1, n2 = (b2, b1) if swap else (b1, b2)
     ld_row, ld_col = (out.stride(1), out.stride(0)) if swap else (out.stride(0), out.stride(1))
     lib = nat.load()

@@ -104,6 +104,10 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
  *
  * a is (B, T, K), g is (B, T, D) with element strides (bstride, tstride) and
  * unit feature stride; out is written in out_dtype (fp32 accumulation).
+ * Output addressing: flat index c = o*out_rstride + k of sample b is stored at
+ * out + b*out_bstride + (c/64)*out_blk + c%64 (elements).  out_blk = 64 (or 0)
+ * is plain row-major; out_bstride = 64, out_blk = B*64 (needs K % 64 == 0 and
+ * no bias) writes the k-blocked layout da_score_gemm streams contiguously.
  * Replaces materialize_factors for linear layers,
  * dattri_llm/gradient/ops/materialize.py:114-116 (bmm(g^T, a) flattened to
  * (B, out*in)), with the bias column of preprocess.py:436-437.
@@ -111,11 +115,16 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
 int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens,
                           int64_t K, int64_t D, int64_t a_bstride, int64_t a_tstride,
                           int64_t g_bstride, int64_t g_tstride, int has_bias, void* out,
-                          int out_dtype, int64_t out_bstride, int64_t out_rstride, void* stream);
+                          int out_dtype, int64_t out_bstride, int64_t out_rstride,
+                          int64_t out_blk, void* stream);
 
 /*
- * One dense layer of a score GEMM: m1 is (B1, width), m2 is (B2, width), row
- * strides ld1/ld2 in elements, unit column stride.
+ * One dense layer of a score GEMM: m1 is (B1, width), m2 is (B2, width).
+ * Element c of row r of side s lives at  m_s + r*ld_s + (c/64)*blk_s + c%64
+ * (elements): rows are sequences of 64-element blocks.  blk_s = 64 (or 0) is
+ * plain row-major; blk_s = B_s*64 with ld_s = 64 is the k-blocked layout, in
+ * which block b of every row is one contiguous B_s*64 run (what
+ * da_materialize_linear writes with out_blk = B*64).
  */
 typedef struct da_dense_layer {
   const void* m1;
@@ -123,6 +132,8 @@ typedef struct da_dense_layer {
   int64_t width;
   int64_t ld1;
   int64_t ld2;
+  int64_t blk1;
+  int64_t blk2;
 } da_dense_layer;
 
 /*

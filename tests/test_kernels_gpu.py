@@ -136,3 +136,44 @@ def test_norm_xhat(device, dtype, lt):
     fn = oracle.rms_x_hat if lt == "nn.RMSNorm" else oracle.layer_norm_x_hat
     got = kernels.norm_xhat(x.to(device), kind=kernels.NORM_KIND[lt], eps=1e-5, out_dtype=torch.float32)
     assert rel_err(got.cpu().numpy(), fn(_np(x), 1e-5)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("shape", [(3, 70, 128, 200), (8, 256, 512, 520), (2, 33, 64, 8)])
+def test_blocked_materialize_equals_plain(device, shape):
+    """The k-blocked dW layout holds exactly the plain layout's values."""
+    from dattri_llm_amd import kernels
+
+    b, t, k, d = shape
+    gen = torch.Generator().manual_seed(b * t)
+    a = _rand(gen, b, t, k, dtype=torch.bfloat16).to(device)
+    g = _rand(gen, b, t, d, dtype=torch.bfloat16).to(device)
+    plain = kernels.materialize_linear(a, g)
+    blk = kernels.materialize_linear(a, g, blocked=True)
+    assert kernels.is_blocked(blk) and blk.shape == (b, d * k // 64, 64)
+    assert blk.stride() == (64, b * 64, 1)
+    assert torch.equal(blk.reshape(b, -1), plain)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_score_gemm_blocked_operands(device, dtype):
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(21)
+    pairs, m1s, m2s = [], [], []
+    for w, (bl1, bl2) in [(4096, (True, True)), (1024, (False, True)), (192, (True, False)), (136, (False, False))]:
+        m1, m2 = _rand(gen, 8, w, dtype=dtype), _rand(gen, 64, w, dtype=dtype)
+        m1s.append(_np(m1))
+        m2s.append(_np(m2))
+
+        def block(m, on):
+            if not on:
+                return m.to(device)
+            buf = kernels.blocked_storage(m.shape[0], m.shape[1], dtype, device)
+            buf.copy_(m.view(m.shape[0], -1, 64).to(device))
+            return buf
+
+        pairs.append((block(m1, bl1), block(m2, bl2)))
+    got = kernels.score_gemm(pairs)
+    assert rel_err(got.cpu().numpy(), oracle.score_gemm(m1s, m2s)) <= TOL[dtype]
+    got_t = kernels.score_gemm([(q, p) for p, q in pairs])  # transposed launch (B1 > B2)
+    assert rel_err(got_t.cpu().numpy(), oracle.score_gemm(m2s, m1s)) <= TOL[dtype]
