@@ -18,8 +18,11 @@ Inputs are synthetic (seeded on the device) and already resident in HBM; the
 query-side preparation (64 queries materialized once) runs before the timed
 region and is reported as ``query_prep_ms``.
 
-Prints ONE JSON line.  ``--workload ghost`` instead times the fused ghost
-cross-gram at 256 train x 64 query samples, T=512, d_in=d_out=4096.
+Prints ONE JSON line.  Other workloads (not the headline):
+``--workload ghost``   the fused ghost cross-gram, 256 train x 64 query, T=512, d 4096;
+``--workload project`` projected (k=64) capture of the Llama-7B MLP, 512 + 128 samples;
+``--workload moe``     a Mixtral-shaped MoE layer on the segmented ghost route;
+``--workload copy``    a 2 GiB device copy, the reference point for byte counters.
 """
 
 from __future__ import annotations
@@ -116,6 +119,23 @@ def _ev_end(e):
 def _mean_ms(timers, key):
     pairs = timers.get(key, [])
     return sum(s.elapsed_time(e) for s, e in pairs) / max(len(pairs), 1)
+
+
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "llama8b_block_hbm_traffic.md")
+
+
+def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (FETCH_SIZE / WRITE_SIZE runs scaled by the copy calibration), or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_per_launch" and parts[1] == kernel:
+                    return float(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_info():
@@ -223,6 +243,9 @@ def bench_block(args):
         roof = {"bound": "hbm", "kernel": big, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "launches_per_step": 2}
     roof["step_share"] = round(totals[big] / ms, 3)
+    roof["traffic"] = profiled_traffic(big)
+    if roof["traffic"] is not None:
+        roof["traffic_source"] = os.path.relpath(TRAFFIC_PROFILE, REPO)
 
     pairs = n_train * n_query
     result = {
@@ -378,17 +401,241 @@ def bench_ghost(args):
     return result
 
 
+# ---------------------------------------------------------------------------
+# projected capture (LoGRA route): fused project + outer product, then score
+# ---------------------------------------------------------------------------
+
+PROJ_LAYERS = [("gate_proj", 4096, 11008), ("up_proj", 4096, 11008), ("down_proj", 11008, 4096)]
+
+
+def bench_project(args):
+    """Llama-7B MLP projected capture: 512 train + 128 query samples at T=128,
+    k=64 on both sides; one step projects and outer-sums every sample of the 3
+    MLP linears (fused kernel) and scores the 512 x 128 projected gradients."""
+    import torch
+
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.gradient.ops.projection import gaussian_matrix
+
+    n_train, n_query, t, k = 512, 128, 128, 64
+    n = n_train + n_query
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    bf = torch.bfloat16
+    acts = {"mlp_in": _randn((n, t, 4096), gen, bf, 4096**-0.5), "down_in": _randn((n, t, 11008), gen, bf, 11008**-0.5)}
+    grads = {name: _randn((n, t, dout), gen, bf, dout**-0.5) for name, _i, dout in PROJ_LAYERS}
+    mats = {}
+    for li, (name, din, dout) in enumerate(PROJ_LAYERS):
+        pin = gaussian_matrix(din, k, 2 * li + 1).t().contiguous().to("cuda", bf)
+        pout = gaussian_matrix(dout, k, 2 * li).t().contiguous().to("cuda", bf)
+        mats[name] = (pin, pout)
+    act_of = {"gate_proj": "mlp_in", "up_proj": "mlp_in", "down_proj": "down_in"}
+    scores = torch.empty(n_train, n_query, dtype=torch.float32, device="cuda")
+
+    def step(timers=None):
+        feats = {}
+        for name, _i, _o in PROJ_LAYERS:
+            ev = _ev(timers, "project_outer")
+            feats[name] = kernels.project_outer(acts[act_of[name]], grads[name], *mats[name])
+            _ev_end(ev)
+        ev = _ev(timers, "score_gemm")
+        kernels.score_gemm([(f[:n_train], f[n_train:]) for f in feats.values()], out=scores)
+        _ev_end(ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timers)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    layer_bytes = {name: n * t * (din + dout) * 2.0 for name, din, dout in PROJ_LAYERS}
+    t_proj = _mean_ms(timers, "project_outer")
+    t_score = _mean_ms(timers, "score_gemm")
+    gbs = sum(layer_bytes.values()) / 3 / t_proj / 1e6
+    result = {
+        "metric": "train x query pair-scores/sec (Llama-7B MLP, projected k=64 capture, bf16)",
+        "value": round(n_train * n_query / (ms / 1e3), 1),
+        "unit": "pair-scores/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "llama-7b MLP projected capture: 512 train + 128 query, T=128, "
+                               "gate/up 4096->11008, down 11008->4096, k=64"},
+        "roofline": {"bound": "hbm", "kernel": "project_outer_kernel", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "work_per_launch": "640 samples x 128 tokens x (d_in + d_out) x 2 B = 2.47e9 B",
+                     "launches_per_step": 3, "step_share": round(3 * t_proj / ms, 3)},
+        "kernels": {"project_outer": {"ms": round(t_proj, 4), "gbs": round(gbs, 1)},
+                    "score_gemm": {"ms": round(t_score, 4)}},
+    }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import oracle
+
+        rng = np.random.default_rng(0)
+        f32 = np.float32
+        nb = 16
+        feats_cpu, dt = [], 0.0
+        for li, (name, din, dout) in enumerate(PROJ_LAYERS):
+            a = rng.standard_normal((nb, t, din), dtype=f32)
+            g = rng.standard_normal((nb, t, dout), dtype=f32)
+            pin = gaussian_matrix(din, k, 2 * li + 1).numpy()
+            pout = gaussian_matrix(dout, k, 2 * li).numpy()
+            t0 = time.perf_counter()
+            feats_cpu.append(oracle.project_outer(a, g, pin, pout))
+            dt += time.perf_counter() - t0
+        per_sample = dt / nb
+        step_s = per_sample * n
+        cores, model = cpu_info()
+        result["cpu_baseline"] = {
+            "value": round(n_train * n_query / step_s, 3), "unit": "pair-scores/s", "cores": blas_threads(),
+            "kind": "port",
+            "sample": f"numpy fp32 oracle: projected capture of 16 samples on the 3 layers ({dt:.2f} s), "
+                      f"scaled to 640 samples (score GEMM of 512x128x12288 omitted: < 1% of the step); "
+                      f"host {model}, {cores} cores visible"}
+    return result
+
+
+# ---------------------------------------------------------------------------
+# MoE: router top-k, expert segments, segmented ghost products
+# ---------------------------------------------------------------------------
+
+
+def bench_moe(args):
+    """Mixtral-shaped MoE layer: 8 experts, top-2, d 4096, d_ff 14336 (fused
+    gate_up 4096->28672, down 14336->4096); 16 train x 256 tokens vs 16 query
+    x 256 tokens.  One step: router top-k and expert segments of both sides,
+    then the segment-summed ghost products of both expert linears."""
+    import torch
+
+    from dattri_llm_amd.gradient import ops
+
+    n_exp, top_k, b, t = 8, 2, 16, 256
+    layers = [("gate_up", 4096, 28672), ("down", 14336, 4096)]
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    bf = torch.bfloat16
+    logits = [_randn((b * t, n_exp), gen, torch.float32) for _ in range(2)]
+    # Captures in routed order, one set per side, sized from the routing.
+    routing = [ops.moe.expert_rows(ops.moe.router_topk(lg, top_k)[1], n_exp) for lg in logits]
+    caps = []
+    for side in routing:
+        per_exp = []
+        for _slot, tok in side:
+            r = tok.numel()
+            per_exp.append({name: (_randn((r, din), gen, bf, din**-0.5), _randn((r, dout), gen, bf, dout**-0.5))
+                            for name, din, dout in layers})
+        caps.append(per_exp)
+    rows = [[tok.numel() for _s, tok in side] for side in routing]
+    scores = torch.zeros(b, b, dtype=torch.float32, device="cuda")
+
+    def step(timers=None):
+        ev = _ev(timers, "route")
+        tok = [[tk for _s, tk in ops.moe.expert_rows(ops.moe.router_topk(lg, top_k)[1], n_exp)] for lg in logits]
+        _ev_end(ev)
+        ev = _ev(timers, "ghost")
+        scores.zero_()
+        for e in range(n_exp):
+            if rows[0][e] == 0 or rows[1][e] == 0:
+                continue
+            for name, _i, _o in layers:
+                a1, g1 = caps[0][e][name]
+                a2, g2 = caps[1][e][name]
+                ops.moe.expert_cross_gram(a1, g1, tok[0][e], a2, g2, tok[1][e], batch1=b, tokens1=t, batch2=b,
+                                          tokens2=t, out=scores, accumulate=True)
+        _ev_end(ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timers)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    flops = sum(2.0 * rows[0][e] * rows[1][e] * (din + dout) for e in range(n_exp) for _n, din, dout in layers)
+    t_ghost = _mean_ms(timers, "ghost")
+    tf = flops / t_ghost / 1e9
+    return {
+        "metric": "train x query pair-scores/sec (Mixtral-shaped MoE layer, top-2 of 8, bf16)",
+        "value": round(b * b / (ms / 1e3), 1),
+        "unit": "pair-scores/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "mixtral moe layer: 16 train x 256 tok vs 16 query x 256 tok, 8 experts top-2, "
+                               "gate_up 4096->28672, down 14336->4096, segmented ghost route",
+                   "rows_per_expert": rows},
+        "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles", "achieved": round(tf, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "work_per_step": f"{flops:.4g} flop = sum over experts and both linears "
+                                                       "of 2 x rows1 x rows2 x (d_in + d_out)",
+                     "launches_per_step": 2 * n_exp, "step_share": round(t_ghost / ms, 3)},
+        "kernels": {"route_ms": round(_mean_ms(timers, "route"), 4), "ghost_ms": round(t_ghost, 4)},
+    }
+
+
+# ---------------------------------------------------------------------------
+# plain device copy: the reference point for HBM byte counters
+# ---------------------------------------------------------------------------
+
+
+def bench_copy(args):
+    """A 2 GiB device-to-device copy (torch's copy kernel): its achieved
+    bandwidth, and under a counter profiler the FETCH_SIZE / WRITE_SIZE
+    readings that correspond to exactly 2 GiB read and 2 GiB written."""
+    import torch
+
+    nbytes = 2 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ev = _ev(timers, "copy")
+        dst.copy_(src)
+        _ev_end(ev)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    t_k = _mean_ms(timers, "copy")
+    gbs = 2 * nbytes / t_k / 1e6
+    return {"metric": "device copy bandwidth (2 GiB read + 2 GiB written)", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "device copy 2 GiB"},
+            "roofline": {"bound": "hbm", "kernel": "copy", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["block", "ghost"], default="block")
+    ap.add_argument("--workload", choices=["block", "ghost", "project", "moe", "copy"], default="block")
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the scoring path shards train rows; see DESIGN.md). Run with --gpus 1.",
+              "(the scoring path would shard train rows, one slice per GPU). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     import torch
@@ -396,7 +643,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
-    result = bench_block(args) if args.workload == "block" else bench_ghost(args)
+    runs = {"block": bench_block, "ghost": bench_ghost, "project": bench_project, "moe": bench_moe,
+            "copy": bench_copy}
+    result = runs[args.workload](args)
     print(json.dumps(result), flush=True)
 
 
