@@ -224,14 +224,14 @@ def bench_block(args):
     # Dominant kernel: the one taking most of the step (summed over its launches).
     # Its roofline uses the step's algorithmic work over the summed event time,
     # i.e. per-launch work over the average launch duration.
-    totals = {"materialize_tiles_big": t_mat, "score_gemm_chunks": t_score, "norm_grad_chunks": 2 * t_norm}
+    totals = {"materialize_tiles_tr": t_mat, "score_gemm_chunks": t_score, "norm_grad_chunks": 2 * t_norm}
     big = max(totals, key=totals.get)
     if big == "score_gemm_chunks":
         gbs = score_bytes / t_score / 1e6
         roof = {"bound": "hbm", "kernel": big, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": f"{score_bytes:.4g} B (72 rows x {width} weights x 2 B)", "launches_per_step": 1}
-    elif big == "materialize_tiles_big":
+    elif big == "materialize_tiles_tr":
         tf = sum(mat_flops.values()) / (t_mat * 1e9)
         roof = {"bound": "mfma", "kernel": big, "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,

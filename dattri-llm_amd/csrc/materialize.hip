@@ -356,6 +356,222 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_big(MatArgs m) 
   }
 }
 
+// Transposing-read variant for 2-byte inputs (bf16 / f16), used for the large
+// layers.  Operand tiles go from HBM to LDS untouched, by buffer loads with the
+// LDS-direct bit (16 bytes per lane, nothing staged in VGPRs), and the MFMA
+// fragments come out of LDS token-contiguous through ds_read_b64_tr_b16: within
+// each 16-lane group, lane j addresses 4 consecutive columns of token row
+// (r0 + j/4) and lane i receives tokens r0..r0+3 of column i.  Rows past the
+// sample's last token and columns past the width read as zero through the
+// buffer range check.  The ring holds four 32-token stages, three in flight
+// while the fourth is multiplied.
+namespace trk {
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kTS = 32;                     // tokens per stage
+constexpr int kRow = 512;                   // bytes per token row of a 256-column operand tile
+constexpr int kOp = kTS * kRow;             // 16 KB per operand per stage
+constexpr int kStage = 2 * kOp;             // g tile, then a tile
+constexpr int kNBuf = 4;                    // ring of stages: 128 KB
+constexpr int kDma = kTS * (kRow / 16) / (kWave * 4);  // DMA instructions per wave, operand and stage
+constexpr uint32_t kOob = 0x80000000u;      // offset past every range: the load returns zeros
+static_assert(kDma == 4, "the vmcnt waits below assume 8 DMA instructions per wave and stage");
+// 16-byte chunk c of token row r is stored in slot c ^ swz(r).  One transposing
+// read touches 8 token rows (r % 4 = 0..3, twice) x 64 bytes; the swizzle puts
+// the four rows of each half in different 64-byte quarters of a 256-byte bank
+// sweep.
+__device__ __forceinline__ int swz(int r) { return (r & 3) << 2; }
+}  // namespace trk
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+// One 16-byte-per-lane buffer load into LDS at lds_addr + 16 * lane (M0 holds
+// the wave-uniform LDS byte address).  Written as inline assembly because the
+// compiler, seeing an LDS write it cannot tell apart from the other stages,
+// would otherwise put a full vmcnt(0) wait in front of every LDS read and
+// serialize the ring; the kernel waits for these loads with explicit counts.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+__device__ __forceinline__ u32x4 tr_frag(const lds_char* p0, const lds_char* p1) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p0);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p1);
+  const u32x2 l = __builtin_bit_cast(u32x2, lo), h = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l[0], l[1], h[0], h[1]};
+}
+
+template <int DT, int OT>
+__global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
+  static_assert(Elem<DT>::kBytes == 2, "transposing reads are 16-bit");
+  __shared__ __attribute__((aligned(1024))) char smem[trk::kNBuf * trk::kStage];
+  lds_char* const L = (lds_char*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)L;
+
+  const int64_t ntiles = (int64_t)gridDim.x;
+  const int64_t logical = xcd_remap(blockIdx.x, ntiles);
+  const int64_t per_sample = m.tiles_m * m.tiles_n;
+  const int64_t b = logical / per_sample;
+  const int64_t rem = logical - b * per_sample;
+  const int64_t per_group = (int64_t)kGroup * m.tiles_n;
+  const int64_t group = rem / per_group;
+  const int64_t first = group * kGroup;
+  const int64_t gsize = min(m.tiles_m - first, (int64_t)kGroup);
+  const int64_t in_group = rem - group * per_group;
+  const int64_t tm = first + in_group % gsize;
+  const int64_t tn = in_group / gsize;
+  const int64_t o0 = tm * trk::kBM, k0 = tn * trk::kBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform, for M0
+
+  // Buffer resources over the sample's token rows (the host guarantees
+  // (tokens + kTS) * stride < 2^31, so no offset below wraps).
+  const u32x4 rg = make_rsrc(m.g + b * m.g_bstride, (uint32_t)(m.tokens * m.g_tstride));
+  const u32x4 ra = make_rsrc(m.a + b * m.a_bstride, (uint32_t)(m.tokens * m.a_tstride));
+  const uint32_t gts = (uint32_t)m.g_tstride, ats = (uint32_t)m.a_tstride;
+
+  // DMA: wave w fills token rows 8w .. 8w+7 of both operand tiles, two rows per
+  // instruction; lane l takes row 8w + 2j + l/32 and slot l % 32.
+  uint32_t goff[trk::kDma], aoff[trk::kDma];
+#pragma unroll
+  for (int j = 0; j < trk::kDma; ++j) {
+    const int r = 8 * wave + 2 * j + (lane >> 5);
+    const int c = (lane & 31) ^ trk::swz(r);
+    const int64_t gc = o0 + 8 * c, ac = k0 + 8 * c;
+    goff[j] = gc < m.d ? (uint32_t)(r * gts + gc * 2) : trk::kOob;
+    aoff[j] = ac < m.k ? (uint32_t)(r * ats + ac * 2) : trk::kOob;
+  }
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const uint32_t base = lds0 + (uint32_t)((st % trk::kNBuf) * trk::kStage + 8 * uwave * trk::kRow);
+    const uint32_t gs = (uint32_t)st * (trk::kTS * gts), as = (uint32_t)st * (trk::kTS * ats);
+#pragma unroll
+    for (int j = 0; j < trk::kDma; ++j) dma16(rg, base + 2 * j * trk::kRow, goff[j] + gs);
+#pragma unroll
+    for (int j = 0; j < trk::kDma; ++j) dma16(ra, base + trk::kOp + 2 * j * trk::kRow, aoff[j] + as);
+  };
+
+  // Fragment addresses: lane (q = lane/16, i = lane%16) reads token row
+  // 16*kk + 8*(q/2) + 4*h + i/4 and columns W0 + 32f + 16*(q%2) + 4*(i%4) .. +3.
+  const int q = lane >> 4, i16 = lane & 15;
+  const int rsw = (i16 >> 2) << 2;  // swz() of that row: row % 4 == i16 / 4
+  const int rowoff = (8 * (q >> 1) + (i16 >> 2)) * trk::kRow;
+  int gfr[4], afr[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int cg = (128 * wm + 32 * f) / 8 + 2 * (q & 1) + ((i16 & 3) >> 1);
+    const int ca = (128 * wn + 32 * f) / 8 + 2 * (q & 1) + ((i16 & 3) >> 1);
+    gfr[f] = rowoff + ((cg ^ rsw) << 4) + 8 * (i16 & 1);
+    afr[f] = trk::kOp + rowoff + ((ca ^ rsw) << 4) + 8 * (i16 & 1);
+  }
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) acc[x][y] = f32x16{};
+
+  static_assert(trk::kTS == 32, "the loop below multiplies two 16-token slices per stage");
+  u32x4 f0a[4], f0b[4], f1a[4], f1b[4];
+  auto read = [&](const lds_char* sb, u32x4 (&fa)[4], u32x4 (&fb)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) fa[f] = tr_frag(sb + gfr[f], sb + gfr[f] + 4 * trk::kRow);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) fb[f] = tr_frag(sb + afr[f], sb + afr[f] + 4 * trk::kRow);
+  };
+  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) Mfma32<DT>::mma(acc[x][y], fa[x], fb[y]);
+  };
+  // Wait until this wave's loads of a stage are done (at most `ahead` later
+  // stages, 8 instructions each, still outstanding) and its own LDS reads have
+  // returned, then barrier: every wave's part of the stage is visible and the
+  // buffer read before the barrier may be refilled.  The LDS wait is the
+  // compiler's own s_waitcnt (lgkmcnt(0), all other counters at their maximum)
+  // so that it knows the fragments in registers are complete.
+  auto stage_sync = [&](int ahead) __attribute__((always_inline)) {
+    if (ahead >= 2)
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (ahead == 1)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+  };
+
+  // Software pipeline over 16-token slices: the second slice of stage st is
+  // multiplied after the barrier that opens stage st + 1, while the first
+  // slice of st + 1 is being read, so the MFMA pipe does not drain at barriers.
+  const int nst = (int)((m.tokens + trk::kTS - 1) / trk::kTS);
+#pragma unroll
+  for (int s = 0; s < trk::kNBuf - 1; ++s)
+    if (s < nst) issue(s);
+  stage_sync(min(nst - 1, trk::kNBuf - 2));
+  if (trk::kNBuf - 1 < nst) issue(trk::kNBuf - 1);
+  read(L, f0a, f0b);
+  for (int st = 0; st + 1 < nst; ++st) {
+    read(L + (st % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b);
+    mma(f0a, f0b);
+    stage_sync(min(nst - 2 - st, trk::kNBuf - 2));
+    if (st + trk::kNBuf < nst) issue(st + trk::kNBuf);
+    read(L + ((st + 1) % trk::kNBuf) * trk::kStage, f0a, f0b);
+    mma(f1a, f1b);
+  }
+  // Last stage (peeled, so no branch joins the loop's two MFMA groups).
+  read(L + ((nst - 1) % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b);
+  mma(f0a, f0b);
+  mma(f1a, f1b);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Epilogue (as in materialize_tiles_big): stage the output dtype through the
+  // ring, then 16-byte row stores.
+  constexpr int OS = Elem<OT>::kBytes;
+  constexpr int kPassRows = OS == 4 ? 64 : 128;
+  constexpr int ROWB = 128 * OS;
+  char* wbuf = smem + wave * (kPassRows * ROWB);
+  const int64_t orow0 = o0 + 128 * wm, ocol0 = k0 + 128 * wn;
+  char* obase = m.out + (b * m.out_bstride) * OS;
+#pragma unroll
+  for (int pass = 0; pass < 128 / kPassRows; ++pass) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      if ((32 * x) / kPassRows != pass) continue;
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * x + acc_row(r, lane) - pass * kPassRows, col = 32 * y + acc_col(lane);
+          Elem<OT>::store(wbuf, (int64_t)row * 128 + col, acc[x][y][r]);
+        }
+    }
+    __syncthreads();
+    constexpr int CH = ROWB / 16;
+    constexpr int RPP = 64 / CH;
+    for (int rr = 0; rr < kPassRows; rr += RPP) {
+      const int row = rr + lane / CH, ch = lane % CH;
+      const int64_t orow = orow0 + pass * kPassRows + row;
+      const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
+      if (orow < m.d && ocol < m.k)
+        st16(obase + out_index(m, orow, ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
+    }
+    __syncthreads();
+  }
+}
+
 // Bias column dW[b, o, K] = sum_t g[b, t, o]: one thread per (b, o).
 template <int DT, int OT>
 __global__ void bias_column(const char* g, int64_t batch, int64_t tokens, int64_t d,
@@ -381,7 +597,20 @@ int launch(const MatArgs& m, int has_bias, hipStream_t st) {
                        ((m.out_blk * Elem<OT>::kBytes) % 16 == 0) &&
                        ((m.out_bstride * Elem<OT>::kBytes) % 16 == 0) && (((uintptr_t)m.out & 15) == 0);
   const bool use_big = aligned && m.d >= big::kBM && m.k >= big::kBN && m.k % 8 == 0;
-  if (use_big) {
+  // The transposing-read kernel addresses a sample's rows with 32-bit buffer
+  // offsets and needs disjoint rows (a zero token stride would read as empty).
+  const int64_t max_ts = m.g_tstride > m.a_tstride ? m.g_tstride : m.a_tstride;
+  const bool use_tr = Elem<DT>::kBytes == 2 && use_big && (m.tokens + trk::kTS) * max_ts < (1LL << 31) &&
+                      m.g_tstride >= m.d * 2 && m.a_tstride >= m.k * 2;
+  if (use_tr) {
+    MatArgs mt = m;
+    mt.tiles_m = (m.d + trk::kBM - 1) / trk::kBM;
+    mt.tiles_n = (m.k + trk::kBN - 1) / trk::kBN;
+    const int64_t nt = m.batch * mt.tiles_m * mt.tiles_n;
+    if constexpr (Elem<DT>::kBytes == 2) materialize_tiles_tr<DT, OT><<<(unsigned)nt, kThreads, 0, st>>>(mt);
+    int rc = check_launch("da_materialize_linear(transposing reads)");
+    if (rc) return rc;
+  } else if (use_big) {
     MatArgs mb = m;
     mb.tiles_m = (m.d + big::kBM - 1) / big::kBM;
     mb.tiles_n = (m.k + big::kBN - 1) / big::kBN;

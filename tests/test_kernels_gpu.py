@@ -38,10 +38,12 @@ MAT_CASES = [
     (4, 33, 100, 60, False),      # widths not multiples of 8 -> padded path
     (2, 100, 264, 520, False),    # 256x256-tile kernel, partial tiles on both axes
     (1, 2048, 512, 768, False),   # 256x256-tile kernel, long token axis
+    (3, 77, 512, 264, True),      # 256x256 tiles, ragged last stage, bias column
+    (2, 31, 256, 256, False),     # 256x256 tiles, a single partial stage
 ]
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("out_dtype", [None, torch.float32])
 @pytest.mark.parametrize("case", MAT_CASES)
 def test_materialize_linear(device, dtype, out_dtype, case):
@@ -68,6 +70,20 @@ def test_materialize_linear_strided(device):
     got = kernels.materialize_linear(a.to(device).transpose(0, 1), g.to(device).transpose(0, 1))
     ref = oracle.materialize_linear(_np(a.transpose(0, 1)), _np(g.transpose(0, 1)))
     assert rel_err(got.float().cpu().numpy(), ref) <= 1e-2
+
+
+def test_materialize_linear_strided_large(device):
+    """Sequence-first captures on the 256x256-tile path: token stride 3x the row."""
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(6)
+    a = _rand(gen, 300, 3, 512, dtype=torch.bfloat16)  # (T, B, K)
+    g = _rand(gen, 300, 3, 768, dtype=torch.bfloat16)
+    print("materialize strided large (3, 300, 512, 768)", flush=True)
+    got = kernels.materialize_linear(a.to(device).transpose(0, 1), g.to(device).transpose(0, 1),
+                                     out_dtype=torch.float32)
+    ref = oracle.materialize_linear(_np(a.transpose(0, 1)), _np(g.transpose(0, 1)))
+    assert rel_err(got.cpu().numpy(), ref) <= 1e-3
 
 
 SCORE_CASES = [
