@@ -411,6 +411,24 @@ __device__ __forceinline__ u32x4 tr_frag(const lds_char* p0, const lds_char* p1)
   return u32x4{l[0], l[1], h[0], h[1]};
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Store 4 consecutive outputs in the output dtype (round to nearest even).
+template <int OT>
+__device__ __forceinline__ void store_run4(char* p, float a, float b, float c, float d) {
+  if constexpr (OT == DA_F32) {
+    *(f32x4*)p = f32x4{a, b, c, d};
+  } else if constexpr (OT == DA_BF16) {
+    *(u32x2*)p = u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2)),
+                       __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{c, d}, bf16x2))};
+  } else {
+    *(u32x2*)p = u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2)),
+                       __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{c, d}, f16x2))};
+  }
+}
+
 template <int DT, int OT>
 __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   static_assert(Elem<DT>::kBytes == 2, "transposing reads are 16-bit");
@@ -490,11 +508,14 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
 #pragma unroll
     for (int f = 0; f < 4; ++f) fb[f] = tr_frag(sb + afr[f], sb + afr[f] + 4 * trk::kRow);
   };
+  // acc[x][y] holds the transposed 32x32 block: its MFMA rows are the k
+  // columns (a tile) and its MFMA columns the o rows (g tile), so each lane ends
+  // with 4 consecutive k of one o -- one short contiguous store per 4 values.
   auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int y = 0; y < 4; ++y) Mfma32<DT>::mma(acc[x][y], fa[x], fb[y]);
+      for (int y = 0; y < 4; ++y) Mfma32<DT>::mma(acc[x][y], fb[y], fa[x]);
   };
   // Wait until this wave's loads of a stage are done (at most `ahead` later
   // stages, 8 instructions each, still outstanding) and its own LDS reads have
@@ -535,40 +556,44 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   read(L + ((nst - 1) % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b);
   mma(f0a, f0b);
   mma(f1a, f1b);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-
-  // Epilogue (as in materialize_tiles_big): stage the output dtype through the
-  // ring, then 16-byte row stores.
+  // Epilogue: lane l of acc[x][y] holds row o = 32x + l%32 and columns
+  // k = 32y + 8q + 4*(l/32) + (0..3) in acc[x][y][4q .. 4q+3].  Per 32-row
+  // group x, each wave converts in pairs (v_cvt_pk_*), writes its 32 x 128
+  // block into its own padded LDS rows (one 8- or 16-byte write per run of 4),
+  // and stores whole 16-byte chunks of each row.  No other wave touches that
+  // LDS region, so only the loop's final barrier (ring reads done) is needed.
+  // (Storing the runs of 4 straight to HBM puts the 32 rows of one
+  // instruction a row stride apart; at 8 KB strides they serialize on one
+  // memory channel.)
   constexpr int OS = Elem<OT>::kBytes;
-  constexpr int kPassRows = OS == 4 ? 64 : 128;
-  constexpr int ROWB = 128 * OS;
-  char* wbuf = smem + wave * (kPassRows * ROWB);
-  const int64_t orow0 = o0 + 128 * wm, ocol0 = k0 + 128 * wn;
+  constexpr int ROWB = 128 * OS;           // bytes of one staged row
+  constexpr int LROW = ROWB + 16;          // padded LDS row
+  constexpr int CH = ROWB / 16;            // 16-byte chunks per row
+  constexpr int RPI = kWave / CH;          // rows per store instruction
+  static_assert(4 * 32 * LROW <= (int)sizeof(smem), "epilogue staging exceeds the ring");
+  char* wbuf = smem + wave * (32 * LROW);
+  const int h = lane >> 5, ol = lane & 31;
+  const int64_t ocol0 = k0 + 128 * wn;
   char* obase = m.out + (b * m.out_bstride) * OS;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
-  for (int pass = 0; pass < 128 / kPassRows; ++pass) {
+  for (int x = 0; x < 4; ++x) {
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      if ((32 * x) / kPassRows != pass) continue;
+    for (int y = 0; y < 4; ++y)
 #pragma unroll
-      for (int y = 0; y < 4; ++y)
+      for (int q = 0; q < 4; ++q) {
+        const f32x16& v = acc[x][y];
+        store_run4<OT>(wbuf + ol * LROW + (32 * y + 8 * q + 4 * h) * OS, v[4 * q], v[4 * q + 1], v[4 * q + 2],
+                       v[4 * q + 3]);
+      }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 32 * x + acc_row(r, lane) - pass * kPassRows, col = 32 * y + acc_col(lane);
-          Elem<OT>::store(wbuf, (int64_t)row * 128 + col, acc[x][y][r]);
-        }
-    }
-    __syncthreads();
-    constexpr int CH = ROWB / 16;
-    constexpr int RPP = 64 / CH;
-    for (int rr = 0; rr < kPassRows; rr += RPP) {
+    for (int rr = 0; rr < 32; rr += RPI) {
       const int row = rr + lane / CH, ch = lane % CH;
-      const int64_t orow = orow0 + pass * kPassRows + row;
+      const int64_t orow = o0 + 128 * wm + 32 * x + row;
       const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
-      if (orow < m.d && ocol < m.k)
-        st16(obase + out_index(m, orow, ocol) * OS, ld16(wbuf + row * ROWB + ch * 16));
+      const u32x4 val = ld16(wbuf + row * LROW + ch * 16);
+      if (orow < m.d && ocol < m.k) st16(obase + out_index(m, orow, ocol) * OS, val);
     }
-    __syncthreads();
   }
 }
 
