@@ -432,9 +432,12 @@ __device__ __forceinline__ void store_run4(char* p, float a, float b, float c, f
 template <int DT, int OT>
 __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   static_assert(Elem<DT>::kBytes == 2, "transposing reads are 16-bit");
-  __shared__ __attribute__((aligned(1024))) char smem[trk::kNBuf * trk::kStage];
+  __shared__ __attribute__((aligned(1024))) char smem[trk::kNBuf * trk::kStage + 1024];
   lds_char* const L = (lds_char*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)L;
+  // Loads for stages past the last land here: every stage slot issues the same
+  // 8 instructions per wave, so the vmcnt waits below are one constant.
+  const uint32_t lds_dummy = lds0 + (uint32_t)(trk::kNBuf * trk::kStage);
 
   const int64_t ntiles = (int64_t)gridDim.x;
   const int64_t logical = xcd_remap(blockIdx.x, ntiles);
@@ -460,6 +463,7 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   const u32x4 ra = make_rsrc(m.a + b * m.a_bstride, (uint32_t)(m.tokens * m.a_tstride));
   const uint32_t gts = (uint32_t)m.g_tstride, ats = (uint32_t)m.a_tstride;
 
+  const int nst = (int)((m.tokens + trk::kTS - 1) / trk::kTS);
   // DMA: wave w fills token rows 8w .. 8w+7 of both operand tiles, two rows per
   // instruction; lane l takes row 8w + 2j + l/32 and slot l % 32.
   uint32_t goff[trk::kDma], aoff[trk::kDma];
@@ -471,13 +475,22 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
     goff[j] = gc < m.d ? (uint32_t)(r * gts + gc * 2) : trk::kOob;
     aoff[j] = ac < m.k ? (uint32_t)(r * ats + ac * 2) : trk::kOob;
   }
+  // One operand's 4 DMA instructions of stage st (side 0: g tile, 1: a tile);
+  // j selects the instruction.  Stages past the last read nothing (offset past
+  // the range) into the dummy block.
+  auto dma_one = [&](int side, int st, int j) __attribute__((always_inline)) {
+    const bool en = st < nst;
+    const uint32_t lbase = lds0 + (uint32_t)((st % trk::kNBuf) * trk::kStage + side * trk::kOp +
+                                             (8 * uwave + 2 * j) * trk::kRow);
+    const uint32_t step = (uint32_t)st * (trk::kTS * (side == 0 ? gts : ats));
+    const uint32_t off = (side == 0 ? goff[j] : aoff[j]) + step;
+    dma16(side == 0 ? rg : ra, en ? lbase : lds_dummy, en ? off : trk::kOob);
+  };
   auto issue = [&](int st) __attribute__((always_inline)) {
-    const uint32_t base = lds0 + (uint32_t)((st % trk::kNBuf) * trk::kStage + 8 * uwave * trk::kRow);
-    const uint32_t gs = (uint32_t)st * (trk::kTS * gts), as = (uint32_t)st * (trk::kTS * ats);
 #pragma unroll
-    for (int j = 0; j < trk::kDma; ++j) dma16(rg, base + 2 * j * trk::kRow, goff[j] + gs);
+    for (int j = 0; j < trk::kDma; ++j) dma_one(0, st, j);
 #pragma unroll
-    for (int j = 0; j < trk::kDma; ++j) dma16(ra, base + trk::kOp + 2 * j * trk::kRow, aoff[j] + as);
+    for (int j = 0; j < trk::kDma; ++j) dma_one(1, st, j);
   };
 
   // Fragment addresses: lane (q = lane/16, i = lane%16) reads token row
@@ -517,45 +530,62 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
 #pragma unroll
       for (int y = 0; y < 4; ++y) Mfma32<DT>::mma(acc[x][y], fb[y], fa[x]);
   };
-  // Wait until this wave's loads of a stage are done (at most `ahead` later
-  // stages, 8 instructions each, still outstanding) and its own LDS reads have
-  // returned, then barrier: every wave's part of the stage is visible and the
-  // buffer read before the barrier may be refilled.  The LDS wait is the
-  // compiler's own s_waitcnt (lgkmcnt(0), all other counters at their maximum)
-  // so that it knows the fragments in registers are complete.
-  auto stage_sync = [&](int ahead) __attribute__((always_inline)) {
-    if (ahead >= 2)
-      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (ahead == 1)
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // Wait until this wave's loads of stage st are done -- the 16 instructions
+  // issued after them (stages st+1 and st+2, real or dummy) may still be in
+  // flight -- and its own LDS reads have returned, then barrier: every wave's
+  // part of the stage is visible and the buffer read before the barrier may be
+  // refilled.  The LDS wait is the compiler's own s_waitcnt (lgkmcnt(0), all
+  // other counters at their maximum) so it knows the fragments are complete.
+  auto stage_sync = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("s_barrier" ::: "memory");
   };
+  // Half a stage: the 16 MFMAs of one 16-token slice held in (ua, ub), the 16
+  // transposing reads of the next slice into (na, nb), and one operand's 4 DMA
+  // instructions of a later stage, interleaved one read per MFMA and one DMA
+  // per 4 MFMAs.  Issuing a stage's loads in one burst fills the address
+  // FIFO, and the stalled wave then cannot issue MFMAs either.
+  auto half = [&](const u32x4 (&ua)[4], const u32x4 (&ub)[4], const lds_char* sb, u32x4 (&na)[4],
+                  u32x4 (&nb)[4], int side, int dst) __attribute__((always_inline)) {
+    s16x4 t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int fr = i >> 1;
+      const int fo = fr < 4 ? gfr[fr] : afr[fr - 4];
+      t[i] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(sb + fo + (i & 1) * 4 * trk::kRow));
+      Mfma32<DT>::mma(acc[i >> 2][i & 3], ub[i & 3], ua[i >> 2]);
+      if ((i & 3) == 2 && side >= 0) dma_one(side, dst, i >> 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const u32x2 lo = __builtin_bit_cast(u32x2, t[2 * f]), hi = __builtin_bit_cast(u32x2, t[2 * f + 1]);
+      (f < 4 ? na[f] : nb[f - 4]) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
 
   // Software pipeline over 16-token slices: the second slice of stage st is
-  // multiplied after the barrier that opens stage st + 1, while the first
-  // slice of st + 1 is being read, so the MFMA pipe does not drain at barriers.
-  const int nst = (int)((m.tokens + trk::kTS - 1) / trk::kTS);
+  // multiplied after the barrier that opens stage st + 1 while the first slice
+  // of st + 1 is read, so the MFMA pipe does not drain at barriers.  Stage
+  // st + 3's a-tile loads go out in the first half of iteration st, stage
+  // st + 4's g-tile loads in the second half.
 #pragma unroll
-  for (int s = 0; s < trk::kNBuf - 1; ++s)
-    if (s < nst) issue(s);
-  stage_sync(min(nst - 1, trk::kNBuf - 2));
-  if (trk::kNBuf - 1 < nst) issue(trk::kNBuf - 1);
+  for (int s = 0; s < trk::kNBuf - 1; ++s) issue(s);
+  stage_sync();
+#pragma unroll
+  for (int j = 0; j < trk::kDma; ++j) dma_one(0, trk::kNBuf - 1, j);
   read(L, f0a, f0b);
   for (int st = 0; st + 1 < nst; ++st) {
-    read(L + (st % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b);
-    mma(f0a, f0b);
-    stage_sync(min(nst - 2 - st, trk::kNBuf - 2));
-    if (st + trk::kNBuf < nst) issue(st + trk::kNBuf);
-    read(L + ((st + 1) % trk::kNBuf) * trk::kStage, f0a, f0b);
-    mma(f1a, f1b);
+    half(f0a, f0b, L + (st % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b, 1, st + trk::kNBuf - 1);
+    stage_sync();
+    half(f1a, f1b, L + ((st + 1) % trk::kNBuf) * trk::kStage, f0a, f0b, 0, st + trk::kNBuf);
   }
-  // Last stage (peeled, so no branch joins the loop's two MFMA groups).
-  read(L + ((nst - 1) % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b);
-  mma(f0a, f0b);
+  // Last stage (peeled, so no branch joins the loop's MFMA groups).
+  half(f0a, f0b, L + ((nst - 1) % trk::kNBuf) * trk::kStage + 16 * trk::kRow, f1a, f1b, -1, 0);
   mma(f1a, f1b);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // Epilogue: lane l of acc[x][y] holds row o = 32x + l%32 and columns
   // k = 32y + 8q + 4*(l/32) + (0..3) in acc[x][y][4q .. 4q+3].  Per 32-row
   // group x, each wave converts in pairs (v_cvt_pk_*), writes its 32 x 128
