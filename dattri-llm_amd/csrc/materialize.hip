@@ -364,7 +364,8 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_big(MatArgs m) 
 // (r0 + j/4) and lane i receives tokens r0..r0+3 of column i.  Rows past the
 // sample's last token and columns past the width read as zero through the
 // buffer range check.  The ring holds four 32-token stages, three in flight
-// while the fourth is multiplied.
+// while the fourth is multiplied (a fifth stage, all 160 KB of LDS, measured
+// slower).
 namespace trk {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
@@ -375,7 +376,7 @@ constexpr int kStage = 2 * kOp;             // g tile, then a tile
 constexpr int kNBuf = 4;                    // ring of stages: 128 KB
 constexpr int kDma = kTS * (kRow / 16) / (kWave * 4);  // DMA instructions per wave, operand and stage
 constexpr uint32_t kOob = 0x80000000u;      // offset past every range: the load returns zeros
-static_assert(kDma == 4, "the vmcnt waits below assume 8 DMA instructions per wave and stage");
+static_assert(kDma == 4, "the vmcnt wait assumes 8 DMA instructions per wave and stage");
 // 16-byte chunk c of token row r is stored in slot c ^ swz(r).  One transposing
 // read touches 8 token rows (r % 4 = 0..3, twice) x 64 bytes; the swizzle puts
 // the four rows of each half in different 64-byte quarters of a 256-byte bank
@@ -432,12 +433,9 @@ __device__ __forceinline__ void store_run4(char* p, float a, float b, float c, f
 template <int DT, int OT>
 __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   static_assert(Elem<DT>::kBytes == 2, "transposing reads are 16-bit");
-  __shared__ __attribute__((aligned(1024))) char smem[trk::kNBuf * trk::kStage + 1024];
+  __shared__ __attribute__((aligned(1024))) char smem[trk::kNBuf * trk::kStage];
   lds_char* const L = (lds_char*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)L;
-  // Loads for stages past the last land here: every stage slot issues the same
-  // 8 instructions per wave, so the vmcnt waits below are one constant.
-  const uint32_t lds_dummy = lds0 + (uint32_t)(trk::kNBuf * trk::kStage);
 
   const int64_t ntiles = (int64_t)gridDim.x;
   const int64_t logical = xcd_remap(blockIdx.x, ntiles);
@@ -476,15 +474,17 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
     aoff[j] = ac < m.k ? (uint32_t)(r * ats + ac * 2) : trk::kOob;
   }
   // One operand's 4 DMA instructions of stage st (side 0: g tile, 1: a tile);
-  // j selects the instruction.  Stages past the last read nothing (offset past
-  // the range) into the dummy block.
+  // j selects the instruction.  A stage past the last still issues them, with
+  // an offset past the range (no memory is read; its ring slot, which no one
+  // reads, is filled with zeros), so every stage slot issues the same 8
+  // instructions per wave and the vmcnt wait below is one constant.
   auto dma_one = [&](int side, int st, int j) __attribute__((always_inline)) {
     const bool en = st < nst;
     const uint32_t lbase = lds0 + (uint32_t)((st % trk::kNBuf) * trk::kStage + side * trk::kOp +
                                              (8 * uwave + 2 * j) * trk::kRow);
     const uint32_t step = (uint32_t)st * (trk::kTS * (side == 0 ? gts : ats));
     const uint32_t off = (side == 0 ? goff[j] : aoff[j]) + step;
-    dma16(side == 0 ? rg : ra, en ? lbase : lds_dummy, en ? off : trk::kOob);
+    dma16(side == 0 ? rg : ra, lbase, en ? off : trk::kOob);
   };
   auto issue = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
@@ -530,13 +530,14 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
 #pragma unroll
       for (int y = 0; y < 4; ++y) Mfma32<DT>::mma(acc[x][y], fb[y], fa[x]);
   };
-  // Wait until this wave's loads of stage st are done -- the 16 instructions
-  // issued after them (stages st+1 and st+2, real or dummy) may still be in
-  // flight -- and its own LDS reads have returned, then barrier: every wave's
+  // Wait until this wave's loads of a stage are done -- the 8 * (kNBuf - 2)
+  // instructions issued after them may still be in flight -- and its own LDS
+  // reads have returned, then barrier: every wave's
   // part of the stage is visible and the buffer read before the barrier may be
   // refilled.  The LDS wait is the compiler's own s_waitcnt (lgkmcnt(0), all
   // other counters at their maximum) so it knows the fragments are complete.
   auto stage_sync = [&]() __attribute__((always_inline)) {
+    static_assert(trk::kNBuf == 4, "vmcnt below is 8 * (kNBuf - 2)");
     asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("s_barrier" ::: "memory");
@@ -569,8 +570,8 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   // Software pipeline over 16-token slices: the second slice of stage st is
   // multiplied after the barrier that opens stage st + 1 while the first slice
   // of st + 1 is read, so the MFMA pipe does not drain at barriers.  Stage
-  // st + 3's a-tile loads go out in the first half of iteration st, stage
-  // st + 4's g-tile loads in the second half.
+  // st + kNBuf - 1's a-tile loads go out in the first half of iteration st,
+  // stage st + kNBuf's g-tile loads in the second half.
 #pragma unroll
   for (int s = 0; s < trk::kNBuf - 1; ++s) issue(s);
   stage_sync();
