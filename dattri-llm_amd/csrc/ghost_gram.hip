@@ -201,6 +201,192 @@ __global__ void ghost_gram_reduce(const float* __restrict__ partial, int64_t b1,
   *o = accumulate ? *o + s : s;
 }
 
+// ---------------------------------------------------------------------------
+// Grouped (MoE) form: tiles over each expert's packed, sample-sorted rows.
+// ---------------------------------------------------------------------------
+constexpr int kMaxGroups = 16;  // groups per launch (the table travels as kernel arguments)
+constexpr int kPRow = kBN + 1; // padded fp32 row of the parked product tile
+
+struct GroupDev {
+  const char* a1;
+  const char* g1;
+  const char* a2;
+  const char* g2;
+  const int32_t* seg1;
+  const int32_t* seg2;
+  const int32_t* idx1;
+  const int32_t* idx2;
+  int64_t rows1, rows2;               // packed rows per side (seg[B])
+  int64_t a1_ts, g1_ts, a2_ts, g2_ts; // row strides, bytes
+  int64_t tile0;                      // first tile of this group in the launch
+  int64_t tiles_r, tiles_c;
+  int64_t part_off, part_ld;          // partial region (floats) and its row length
+  int64_t meta_off;                   // int32 offset of this group's span tables
+  int64_t kbytes_a, kbytes_g;         // K * esize, D * esize
+  float bias;                         // 1 with an implicit ones column, else 0
+};
+
+struct GroupedArgs {
+  GroupDev grp[kMaxGroups];
+  int n_groups;
+  int64_t b1, b2;
+  float* partial;
+  int32_t* meta;  // per group: first1[B1], pre1[B1+1], first2[B2], pre2[B2+1]
+};
+static_assert(sizeof(GroupedArgs) <= 3584, "grouped kernel arguments must stay well under 4 KB");
+
+// Sample owning packed row p (p < seg[B]): the last b with seg[b] <= p.
+__device__ __forceinline__ int64_t sample_of(const int32_t* seg, int64_t nb, int64_t p) {
+  int64_t lo = 0, hi = nb;  // seg[lo] <= p < seg[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)seg[mid] <= p) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// Span tables of one side of one group: first[b] = first row tile of sample b,
+// pre[b] = sum of spans (row tiles touched) of samples < b.  One workgroup per
+// (group, side); sequential per thread chunk, then a scan of the chunk sums.
+__global__ __launch_bounds__(256) void grouped_spans(GroupedArgs ga) {
+  __shared__ int32_t part[256];
+  const int e = blockIdx.x >> 1, side = blockIdx.x & 1;
+  const GroupDev& G = ga.grp[e];
+  const int64_t nb = side ? ga.b2 : ga.b1;
+  const int32_t* seg = side ? G.seg2 : G.seg1;
+  int32_t* first = ga.meta + G.meta_off + (side ? (2 * ga.b1 + 1) : 0);
+  int32_t* pre = first + nb;
+  const int tid = threadIdx.x;
+  const int64_t per = (nb + 255) / 256;
+  const int64_t b0 = tid * per, b1e = min(b0 + per, nb);
+  int32_t local = 0;
+  for (int64_t b = b0; b < b1e; ++b) {
+    const int32_t s0 = seg[b], s1 = seg[b + 1];
+    first[b] = s0 / kBM;
+    local += s1 > s0 ? (s1 - 1) / kBM - s0 / kBM + 1 : 0;
+  }
+  part[tid] = local;
+  __syncthreads();
+  if (tid == 0) {
+    int32_t run = 0;
+    for (int q = 0; q < 256; ++q) { const int32_t v = part[q]; part[q] = run; run += v; }
+    pre[nb] = run;
+  }
+  __syncthreads();
+  int32_t run = part[tid];
+  for (int64_t b = b0; b < b1e; ++b) {
+    pre[b] = run;
+    const int32_t s0 = seg[b], s1 = seg[b + 1];
+    run += s1 > s0 ? (s1 - 1) / kBM - s0 / kBM + 1 : 0;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads, 2) void ghost_grouped_tiles(GroupedArgs ga) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * kStageBytes];
+  static_assert(kBM * kPRow * 4 <= 2 * kStageBytes, "product tile must fit the stage buffers");
+
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  int e = 0;
+  while (e + 1 < ga.n_groups && ga.grp[e + 1].tile0 <= logical) ++e;
+  const GroupDev& G = ga.grp[e];
+  const int64_t local = logical - G.tile0;
+  const int64_t per_group = (int64_t)kGroup * G.tiles_c;
+  const int64_t grp = local / per_group;
+  const int64_t first_r = grp * kGroup;
+  const int64_t gsize = min(G.tiles_r - first_r, (int64_t)kGroup);
+  const int64_t in_group = local - grp * per_group;
+  const int64_t m = first_r + in_group % gsize;
+  const int64_t n = in_group / gsize;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = tid >> 3;
+  const int64_t t0 = m * kBM, s0 = n * kBN;
+  // Rows at or past seg[B] belong to no sample (and may have no row_index
+  // entry): treat them as absent.
+  const int64_t n1 = min(G.rows1, (int64_t)G.seg1[ga.b1]), n2 = min(G.rows2, (int64_t)G.seg2[ga.b2]);
+  const char* a1[4];
+  const char* g1[4];
+  const char* a2[4];
+  const char* g2[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int64_t t = t0 + lr + 32 * p, s = s0 + lr + 32 * p;
+    const bool v1 = t < n1, v2 = s < n2;
+    const int64_t r1 = v1 ? (G.idx1 ? (int64_t)G.idx1[t] : t) : 0;
+    const int64_t r2 = v2 ? (G.idx2 ? (int64_t)G.idx2[s] : s) : 0;
+    a1[p] = v1 ? G.a1 + r1 * G.a1_ts : nullptr;
+    g1[p] = v1 ? G.g1 + r1 * G.g1_ts : nullptr;
+    a2[p] = v2 ? G.a2 + r2 * G.a2_ts : nullptr;
+    g2[p] = v2 ? G.g2 + r2 * G.g2_ts : nullptr;
+  }
+
+  f32x16 ka[2][2], kg[2][2];
+  gram_tile<DT>(smem, a1, a2, G.kbytes_a, ka, tid, lane, wm, wn);
+  gram_tile<DT>(smem, g1, g2, G.kbytes_g, kg, tid, lane, wm, wn);
+
+  // Park (K_a + bias) * K_g in LDS (rows past an end are zero rows: K_g = 0).
+  float* P = (float*)smem;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 64 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
+        P[row * kPRow + col] = (ka[x][y][r] + G.bias) * kg[x][y][r];
+      }
+  __syncthreads();
+
+  // Bins: (sample i, sample j) pairs meeting this tile; one wave per bin, lanes
+  // over rows, each lane summing its rows' columns in order, then a fixed
+  // butterfly.  Bin (i, j) of tile (m, n) goes to slot
+  // (pre1[i] + m - first1[i], pre2[j] + n - first2[j]) of the group's region.
+  const int64_t last_r = min(t0 + kBM, n1) - 1, last_c = min(s0 + kBN, n2) - 1;
+  if (last_r < t0 || last_c < s0) return;  // no live rows on a side: no bins
+  const int64_t i_lo = sample_of(G.seg1, ga.b1, t0), i_hi = sample_of(G.seg1, ga.b1, last_r);
+  const int64_t j_lo = sample_of(G.seg2, ga.b2, s0), j_hi = sample_of(G.seg2, ga.b2, last_c);
+  const int64_t nj = j_hi - j_lo + 1, nbins = (i_hi - i_lo + 1) * nj;
+  const int32_t* first1 = ga.meta + G.meta_off;
+  const int32_t* pre1 = first1 + ga.b1;
+  const int32_t* first2 = pre1 + ga.b1 + 1;
+  const int32_t* pre2 = first2 + ga.b2;
+  for (int64_t bin = wave; bin < nbins; bin += kThreads / kWave) {
+    const int64_t i = i_lo + bin / nj, j = j_lo + bin % nj;
+    const int64_t r0 = max((int64_t)G.seg1[i], t0) - t0, r1 = min((int64_t)G.seg1[i + 1], t0 + kBM) - t0;
+    const int64_t c0 = max((int64_t)G.seg2[j], s0) - s0, c1 = min((int64_t)G.seg2[j + 1], s0 + kBN) - s0;
+    if (r1 <= r0 || c1 <= c0) continue;  // an empty sample: it owns no slot
+    float v = 0.f;
+    for (int64_t t = r0 + lane; t < r1; t += kWave)
+      for (int64_t c = c0; c < c1; ++c) v += P[t * kPRow + c];
+    v = wave_sum(v);
+    const int64_t row = pre1[i] + m - first1[i], col = pre2[j] + n - first2[j];
+    if (lane == 0 && row >= 0 && row < G.tiles_r + ga.b1 && col >= 0 && col < G.part_ld)
+      ga.partial[G.part_off + row * G.part_ld + col] = v;
+  }
+}
+
+// out[i, j] (+)= sum over groups of the (span1 x span2) slot block, in a fixed order.
+__global__ void grouped_reduce(GroupedArgs ga, float* __restrict__ out, int64_t ld_out, int accumulate) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= ga.b1 * ga.b2) return;
+  const int64_t i = idx / ga.b2, j = idx - i * ga.b2;
+  float v = 0.f;
+  for (int e = 0; e < ga.n_groups; ++e) {
+    const GroupDev& G = ga.grp[e];
+    const int32_t* pre1 = ga.meta + G.meta_off + ga.b1;
+    const int32_t* pre2 = pre1 + ga.b1 + 1 + ga.b2;
+    const float* base = ga.partial + G.part_off;
+    const int64_t r_end = min((int64_t)pre1[i + 1], G.tiles_r + ga.b1);
+    const int64_t c_end = min((int64_t)pre2[j + 1], G.part_ld);
+    for (int64_t r = max((int64_t)pre1[i], (int64_t)0); r < r_end; ++r)
+      for (int64_t c = max((int64_t)pre2[j], (int64_t)0); c < c_end; ++c) v += base[r * G.part_ld + c];
+  }
+  float* o = out + i * ld_out + j;
+  *o = accumulate ? *o + v : v;
+}
+
 struct Plan {
   int64_t tiles_r, tiles_c, n_r, n_c, per_pair;
   size_t ws;
@@ -268,6 +454,60 @@ SideDev to_dev(const da_factor_side* s, int64_t es) {
 }  // namespace
 }  // namespace da
 
+namespace da {
+namespace {
+
+struct GroupedPlan {
+  size_t meta_ints, part_floats, ws;
+};
+
+// Layout of the grouped workspace for the groups [g0, g0 + n): int32 span
+// tables first, then the partial regions, per group.
+int grouped_plan(const da_factor_side* s1, const da_factor_side* s2, int n_groups, const int64_t* K,
+                 const int64_t* D, int dtype, GroupedPlan* p) {
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: bad dtype %d", dtype);
+  if (n_groups < 0 || (n_groups > 0 && (!s1 || !s2 || !K || !D)))
+    return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: bad group list");
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  p->meta_ints = 0;
+  p->part_floats = 0;
+  if (n_groups == 0) { p->ws = 0; return DA_OK; }
+  const int64_t b1 = s1[0].batch, b2 = s2[0].batch;
+  for (int e = 0; e < n_groups; ++e) {
+    if (K[e] < 0 || D[e] < 0) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: group %d negative width", e);
+    if ((K[e] * es) % 16 || (D[e] * es) % 16)
+      return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: group %d widths must be multiples of %lld elements",
+                       e, (long long)(16 / es));
+    if (s1[e].has_bias != s2[e].has_bias)
+      return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: group %d sides disagree on has_bias", e);
+    const da_factor_side* sides[2] = {&s1[e], &s2[e]};
+    for (int q = 0; q < 2; ++q) {
+      const da_factor_side* sd = sides[q];
+      if (sd->batch != (q ? b2 : b1))
+        return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: group %d has a different batch", e);
+      if (sd->tokens < 0) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: negative row count");
+      if (sd->batch > 0 && !sd->seg_offsets)
+        return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: group %d needs seg_offsets", e);
+      if (sd->tokens > 0) {
+        if (!sd->act || !sd->grad)
+          return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: group %d has a NULL factor", e);
+        if (((uintptr_t)sd->act | (uintptr_t)sd->grad) & 15)
+          return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: factors must be 16-byte aligned");
+        if ((sd->act_tstride * es) % 16 || (sd->grad_tstride * es) % 16)
+          return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: row strides must be multiples of 16 bytes");
+      }
+    }
+    const int64_t tr = (s1[e].tokens + kBM - 1) / kBM, tc = (s2[e].tokens + kBN - 1) / kBN;
+    p->meta_ints += (size_t)(2 * b1 + 1 + 2 * b2 + 1);
+    p->part_floats += (size_t)((tr + b1) * (tc + b2));
+  }
+  p->ws = ((p->meta_ints * sizeof(int32_t) + 255) / 256) * 256 + p->part_floats * sizeof(float);
+  return DA_OK;
+}
+
+}  // namespace
+}  // namespace da
+
 extern "C" {
 
 int da_ghost_gram_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
@@ -324,6 +564,100 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
   ghost_gram_reduce<<<(unsigned)((pairs + 255) / 256), 256, 0, st>>>(
       (const float*)workspace, b1, b2, plan.per_pair, out, ld_out, accumulate);
   return check_launch("da_ghost_gram(reduce)");
+}
+
+int da_ghost_gram_grouped_workspace(const da_factor_side* s1, const da_factor_side* s2, int n_groups,
+                                    const int64_t* K, const int64_t* D, int dtype, size_t* bytes) {
+  da::GroupedPlan plan;
+  int rc = da::grouped_plan(s1, s2, n_groups, K, D, dtype, &plan);
+  if (rc) return rc;
+  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_ghost_gram_grouped_workspace: bytes is NULL");
+  *bytes = plan.ws;
+  return DA_OK;
+}
+
+int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, int n_groups,
+                          const int64_t* K, const int64_t* D, int dtype, float* out, int64_t ld_out,
+                          int accumulate, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace da;
+  GroupedPlan plan;
+  int rc = grouped_plan(s1, s2, n_groups, K, D, dtype, &plan);
+  if (rc) return rc;
+  if (n_groups == 0) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: no groups");
+  const int64_t b1 = s1[0].batch, b2 = s2[0].batch;
+  if (b1 == 0 || b2 == 0) return DA_OK;
+  if (!out) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: out is NULL");
+  if (ld_out < b2) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: ld_out < B2");
+  if (!workspace || workspace_bytes < plan.ws)
+    return set_error(DA_ERR_WORKSPACE, "da_ghost_gram_grouped: workspace needs %zu bytes, got %zu", plan.ws,
+                     workspace_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  int32_t* meta = (int32_t*)workspace;
+  float* part = (float*)((char*)workspace + ((plan.meta_ints * sizeof(int32_t) + 255) / 256) * 256);
+  int64_t meta_off = 0, part_off = 0;
+  bool first_launch = true;
+  for (int g0 = 0; g0 < n_groups; g0 += kMaxGroups) {
+    const int n = n_groups - g0 < kMaxGroups ? n_groups - g0 : kMaxGroups;
+    GroupedArgs ga;
+    ga.n_groups = 0;
+    ga.b1 = b1;
+    ga.b2 = b2;
+    ga.partial = part;
+    ga.meta = meta;
+    int64_t tiles = 0;
+    for (int q = 0; q < n; ++q) {
+      const da_factor_side& x = s1[g0 + q];
+      const da_factor_side& y = s2[g0 + q];
+      const int64_t tr = (x.tokens + kBM - 1) / kBM, tc = (y.tokens + kBN - 1) / kBN;
+      GroupDev& G = ga.grp[ga.n_groups++];
+      G.a1 = (const char*)x.act;
+      G.g1 = (const char*)x.grad;
+      G.a2 = (const char*)y.act;
+      G.g2 = (const char*)y.grad;
+      G.seg1 = x.seg_offsets;
+      G.seg2 = y.seg_offsets;
+      G.idx1 = x.row_index;
+      G.idx2 = y.row_index;
+      G.rows1 = x.tokens;
+      G.rows2 = y.tokens;
+      G.a1_ts = x.act_tstride * es;
+      G.g1_ts = x.grad_tstride * es;
+      G.a2_ts = y.act_tstride * es;
+      G.g2_ts = y.grad_tstride * es;
+      G.tile0 = tiles;
+      G.tiles_r = tr;
+      G.tiles_c = tc;
+      G.part_off = part_off;
+      G.part_ld = tc + b2;
+      G.meta_off = meta_off;
+      G.kbytes_a = K[g0 + q] * es;
+      G.kbytes_g = D[g0 + q] * es;
+      G.bias = x.has_bias ? 1.f : 0.f;
+      tiles += tr * tc;
+      part_off += (tr + b1) * (tc + b2);
+      meta_off += 2 * b1 + 1 + 2 * b2 + 1;
+    }
+    if (tiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: too many tiles");
+    grouped_spans<<<2 * ga.n_groups, 256, 0, st>>>(ga);
+    rc = check_launch("da_ghost_gram_grouped(spans)");
+    if (rc) return rc;
+    if (tiles > 0) {
+      switch (dtype) {
+        case DA_BF16: ghost_grouped_tiles<DA_BF16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+        case DA_F16: ghost_grouped_tiles<DA_F16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+        default: ghost_grouped_tiles<DA_F32><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+      }
+      rc = check_launch("da_ghost_gram_grouped(tiles)");
+      if (rc) return rc;
+    }
+    grouped_reduce<<<(unsigned)((b1 * b2 + 255) / 256), 256, 0, st>>>(ga, out, ld_out,
+                                                                    (accumulate || !first_launch) ? 1 : 0);
+    rc = check_launch("da_ghost_gram_grouped(reduce)");
+    if (rc) return rc;
+    first_launch = false;
+  }
+  return DA_OK;
 }
 
 }  // extern "C"

@@ -63,26 +63,57 @@ def expert_cross_gram(a1, g1, tok1, a2, g2, tok2, *, batch1: int, tokens1: int, 
     ``a*``/``g*`` are the expert's (rows, width) captures in routed order and
     ``tok*`` the flat token index of every row; equals the reference's ghost
     product on the zero-filled ``(B, T, d)`` regroup."""
-    seg1, rows1 = segment_by_sample(tok1, batch1, tokens1)
-    seg2, rows2 = segment_by_sample(tok2, batch2, tokens2)
-    (a1, g1, a2, g2) = dtypes.align(a1, g1, a2, g2)
-    kd = dtypes.kernel_dtype(a1.dtype)
-    return kernels.ghost_gram_segmented(
-        a1.to(kd), g1.to(kd), seg1, rows1, tokens1, a2.to(kd), g2.to(kd), seg2, rows2, tokens2,
-        bias=bias, out=out, accumulate=accumulate)
+    return moe_cross_gram([(a1, g1, tok1, a2, g2, tok2)], batch1=batch1, tokens1=tokens1, batch2=batch2,
+                          tokens2=tokens2, bias=bias, out=out, accumulate=accumulate)
 
 
-def moe_cross_gram(experts, *, batch1: int, tokens1: int, batch2: int, tokens2: int, bias: bool = False):
+def segment_experts(expert_tokens, batch: int, tokens: int) -> list[tuple[torch.Tensor, torch.Tensor]]:
+    """Per-sample segments of every expert of one side: ``expert_tokens[e]`` is
+    expert e's flat token index per routed row; returns ``(seg, rows)`` per
+    expert (see :func:`segment_by_sample`).  The routing is shared by every
+    routed layer, so this runs once per routing, not per layer."""
+    return [segment_by_sample(tok, batch, tokens) for tok in expert_tokens]
+
+
+def moe_layers_cross_gram(layers, segs1, segs2, *, out: torch.Tensor | None = None, accumulate: bool = False):
+    """Cross-gram summed over experts AND routed layers in one grouped launch.
+
+    ``layers`` is a list of ``(experts, bias)`` with ``experts[e] = (a1, g1,
+    a2, g2)`` -- expert e's (rows, width) captures of that layer on both
+    sides, in routed order -- and ``segs*[e] = (seg, rows)`` the per-sample
+    segments of expert e's rows (:func:`segment_experts`), shared by all
+    layers.  Groups are ordered widest layer first so the longest tiles are
+    scheduled first."""
+    groups1, groups2, biases, widths = [], [], [], []
+    for experts, bias in layers:
+        if len(experts) != len(segs1) or len(experts) != len(segs2):
+            raise ValueError("one (a1, g1, a2, g2) per expert, matching the segment lists")
+        for e, (a1, g1, a2, g2) in enumerate(experts):
+            a1, g1, a2, g2 = dtypes.align(a1, g1, a2, g2)
+            kd = dtypes.kernel_dtype(a1.dtype)
+            groups1.append((a1.to(kd), g1.to(kd), *segs1[e]))
+            groups2.append((a2.to(kd), g2.to(kd), *segs2[e]))
+            biases.append(bool(bias))
+            widths.append(a1.shape[-1] + g1.shape[-1])
+    if not groups1:
+        raise ValueError("moe_layers_cross_gram needs at least one layer with experts")
+    order = sorted(range(len(groups1)), key=lambda i: -widths[i])
+    return kernels.ghost_gram_grouped([groups1[i] for i in order], [groups2[i] for i in order],
+                                      bias=[biases[i] for i in order], out=out, accumulate=accumulate)
+
+
+def moe_cross_gram(experts, *, batch1: int, tokens1: int, batch2: int, tokens2: int, bias: bool = False,
+                   out: torch.Tensor | None = None, accumulate: bool = False):
     """Segment-sum over experts: ``experts`` yields ``(a1, g1, tok1, a2, g2, tok2)``
-    per expert; returns the fp32 ``(B1, B2)`` total."""
-    out = None
-    for a1, g1, tok1, a2, g2, tok2 in experts:
-        if out is None:
-            out = torch.zeros(batch1, batch2, dtype=torch.float32, device=a1.device)
-        if a1.shape[0] == 0 or a2.shape[0] == 0:
-            continue
-        expert_cross_gram(a1, g1, tok1, a2, g2, tok2, batch1=batch1, tokens1=tokens1, batch2=batch2,
-                          tokens2=tokens2, bias=bias, out=out, accumulate=True)
-    if out is None:
+    per expert; returns the fp32 ``(B1, B2)`` total.
+
+    All experts go to one grouped launch: each expert's rows are grouped by
+    sample (stable counting sort of ``tok // tokens``) and tiled as packed
+    rows, so no tile is spent on the zero rows of the reference's regroup."""
+    experts = list(experts)
+    if not experts:
         raise ValueError("moe_cross_gram needs at least one expert")
-    return out
+    segs1 = segment_experts([x[2] for x in experts], batch1, tokens1)
+    segs2 = segment_experts([x[5] for x in experts], batch2, tokens2)
+    layer = ([(a1, g1, a2, g2) for a1, g1, _t1, a2, g2, _t2 in experts], bias)
+    return moe_layers_cross_gram([layer], segs1, segs2, out=out, accumulate=accumulate)

@@ -118,6 +118,74 @@ def ghost_gram(
     return out
 
 
+def ghost_gram_grouped(groups1, groups2, *, bias=False, out: torch.Tensor | None = None,
+                       accumulate: bool = False) -> torch.Tensor:
+    """Segment-summed ghost product over groups (experts of one or several
+    linear layers), fp32 ``(B1, B2)``.
+
+    ``groups*`` are equally long lists of ``(a, g, seg, idx)``: a group's
+    (rows, K) activation and (rows, D) gradient captures, its int32 per-sample
+    offsets ``seg`` (B+1 entries, non-decreasing, ``seg[B] <= rows``) and an
+    optional int32 row index (packed row r is physical row ``idx[r]``).  Group
+    e's two sides share K and D; groups may differ in widths (the experts of
+    several layers in one launch, widest first) and ``bias`` may be one bool or
+    one per group.  All groups share B1 / B2 and the dtype."""
+    n = len(groups1)
+    if len(groups2) != n or n == 0:
+        raise ValueError("ghost_gram_grouped needs the same, non-zero number of groups on both sides")
+    biases = list(bias) if isinstance(bias, (list, tuple)) else [bias] * n
+    if len(biases) != n:
+        raise ValueError("one bias flag per group")
+    flat = [t for grp in (*groups1, *groups2) for t in grp if t is not None]
+    dev = nat.require_device(*flat)
+    dtype = groups1[0][0].dtype
+    b1, b2 = groups1[0][2].numel() - 1, groups2[0][2].numel() - 1
+    vec = _chunk_elems(dtype)
+    ks, ds = [], []
+    for e in range(n):
+        kw, dw = groups1[e][0].shape[-1], groups1[e][1].shape[-1]
+        if groups2[e][0].shape[-1] != kw or groups2[e][1].shape[-1] != dw:
+            raise ValueError(f"group {e}: the two sides disagree on the layer widths")
+        ks.append(-(-kw // vec) * vec)
+        ds.append(-(-dw // vec) * vec)
+    sides = []
+    keep = []
+    for groups, nb in ((groups1, b1), (groups2, b2)):
+        row = []
+        for e, (a, g, seg, idx) in enumerate(groups):
+            if a.dim() != 2 or g.dim() != 2 or a.shape[0] != g.shape[0]:
+                raise ValueError("grouped factors must be (rows, width) with matching rows")
+            if a.dtype != dtype or g.dtype != dtype:
+                raise ValueError("grouped factors must share one dtype")
+            if seg.dtype != torch.int32 or seg.numel() != nb + 1 or (idx is not None and idx.dtype != torch.int32):
+                raise ValueError("segment offsets (B+1) and row indices must be int32, one batch per side")
+            a, g = prepare_rows(a, ks[e]), prepare_rows(g, ds[e])
+            seg = seg.contiguous()
+            idx = idx.contiguous() if idx is not None else None
+            keep += [a, g, seg, idx]
+            row.append(_side(a, g, biases[e], seg=seg, index=idx, tokens=a.shape[0]))
+        sides.append((nat.FactorSide * n)(*row))
+    if out is None:
+        out = torch.empty(b1, b2, dtype=torch.float32, device=dev)
+        accumulate = False
+    elif out.dtype != torch.float32 or tuple(out.shape) != (b1, b2) or out.stride(1) != 1:
+        raise ValueError("out must be a float32 (B1, B2) tensor with unit column stride")
+    karr, darr = (ctypes.c_int64 * n)(*ks), (ctypes.c_int64 * n)(*ds)
+    code = nat.dtype_code(dtype)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_ghost_gram_grouped_workspace(sides[0], sides[1], n, karr, darr, code, ctypes.byref(nbytes)),
+              "ghost_gram_grouped")
+    ws = nat.workspace(nbytes.value, dev)
+    nat.check(
+        lib.da_ghost_gram_grouped(sides[0], sides[1], n, karr, darr, code, out.data_ptr(), out.stride(0),
+                                  int(accumulate), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
+        "ghost_gram_grouped",
+    )
+    del keep
+    return out
+
+
 def is_blocked(x: torch.Tensor) -> bool:
     """A (B, W/64, 64) view of a dense (B, W) block stored in 64-element blocks."""
     return x.dim() == 3 and x.shape[2] == 64 and x.stride(2) == 1

@@ -97,6 +97,36 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
                   size_t workspace_bytes, void* stream);
 
 /*
+ * Segment-summed ghost product over experts (MoE routed layers):
+ *
+ *   out[i*ld_out + j] (+)= sum_e sum_{t in seg1_e(i), s in seg2_e(j)}
+ *                            (a1_e,t . a2_e,s) * (g1_e,t . g2_e,s)
+ *
+ * s1[e], s2[e] (e < n_groups) describe group e -- one expert of one linear
+ * layer -- in packed segmented form: seg_offsets (B+1 int32, non-decreasing)
+ * split the expert's rows by sample, `tokens` is the expert's total row count
+ * (>= seg_offsets[B]), row_index optionally gathers physical rows,
+ * act/grad_tstride are row strides, has_bias (equal on both sides) adds the
+ * implicit ones column.  K[e], D[e] are the group's activation and gradient
+ * widths, so the experts of several layers can share one launch (put the
+ * widest first: groups are scheduled in order).  All groups share the batch
+ * sizes (B1, B2) and dtype.  Tiles run over each expert's rows as packed (no
+ * per-sample padding); each tile's products are binned by (sample, sample) and
+ * reduced in a fixed order (deterministic).  Empty experts and samples are
+ * allowed.
+ *
+ * Replaces, for routed experts, the per-expert regroup to zero-filled
+ * (B, T, d) captures (dattri_llm/gradient/hooks/routing.py:71-86) followed by
+ * the factorized cross_gram (dattri_llm/gradient/ops/dot.py:115-118), summed
+ * over experts and layers as layerwise_cross_dot sums layers (dot.py:599-604).
+ */
+int da_ghost_gram_grouped_workspace(const da_factor_side* s1, const da_factor_side* s2, int n_groups,
+                                    const int64_t* K, const int64_t* D, int dtype, size_t* bytes);
+int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, int n_groups,
+                          const int64_t* K, const int64_t* D, int dtype, float* out, int64_t ld_out,
+                          int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Per-sample weight gradient of a linear layer (materialized route):
  *
  *   out[b*out_bstride + o*out_rstride + k] = sum_t g[b,t,o] * a[b,t,k]   (k < K)

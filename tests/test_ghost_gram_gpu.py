@@ -112,3 +112,93 @@ def test_ghost_gram_c2_subset_pairs(device):
     got = kernels.ghost_gram(*(x.to(device) for x in (a1, g1, a2, g2)))
     ref = oracle.cross_gram_factorized(*(x.double().numpy() for x in (a1, g1, a2, g2)))
     assert rel_err(got.cpu().numpy(), ref) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
+# Grouped (MoE) form: packed expert rows, per-sample bins
+# ---------------------------------------------------------------------------
+
+
+def _rand(gen, *shape, dtype):
+    return (torch.randn(*shape, generator=gen) / 4).to(dtype)
+
+
+def _np(x):
+    return x.double().cpu().numpy()
+
+
+def _grouped_case(device, dtype, bias, n_exp, seed):
+    """Experts with edge-case routing: one takes every token of side 1 (300-row
+    samples span three tiles), one is empty, one sees a single sample, the rest
+    a random 30%; rows arrive in a shuffled (routed) order."""
+    from dattri_llm_amd.gradient import ops
+
+    gen = torch.Generator().manual_seed(seed)
+    b1, b2, tokens, k, d = 5, 3, 300, 64, 96
+    groups1, groups2, ref = [], [], np.zeros((b1, b2))
+    for e in range(n_exp):
+        def pick(batch, side):
+            flat = torch.arange(batch * tokens)
+            if e == 0 and side == 1:
+                keep = flat
+            elif e == 1:
+                keep = flat[:0]
+            elif e == 2:
+                keep = flat[(flat // tokens) == (batch - 1)]
+            else:
+                keep = flat[torch.rand(batch * tokens, generator=gen) < 0.3]
+            return keep[torch.randperm(keep.numel(), generator=gen)]
+
+        tok1, tok2 = pick(b1, 1), pick(b2, 2)
+        a1, g1 = _rand(gen, tok1.numel(), k, dtype=dtype), _rand(gen, tok1.numel(), d, dtype=dtype)
+        a2, g2 = _rand(gen, tok2.numel(), k, dtype=dtype), _rand(gen, tok2.numel(), d, dtype=dtype)
+        ref += oracle.moe_segment_ghost(_np(a1), _np(g1), tok1.numpy(), _np(a2), _np(g2), tok2.numpy(),
+                                        b1, b2, tokens, tokens, bias=bias)
+        seg1, rows1 = ops.moe.segment_by_sample(tok1.to(device), b1, tokens)
+        seg2, rows2 = ops.moe.segment_by_sample(tok2.to(device), b2, tokens)
+        groups1.append((a1.to(device), g1.to(device), seg1, rows1))
+        groups2.append((a2.to(device), g2.to(device), seg2, rows2))
+    return groups1, groups2, ref
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("n_exp", [4, 11])  # 11 > 8 experts per launch: two launches
+def test_ghost_gram_grouped(device, dtype, bias, n_exp):
+    from dattri_llm_amd import kernels
+
+    print(f"grouped dtype={dtype} bias={bias} n_exp={n_exp}", flush=True)
+    groups1, groups2, ref = _grouped_case(device, dtype, bias, n_exp, seed=31 + n_exp)
+    got = kernels.ghost_gram_grouped(groups1, groups2, bias=bias)
+    assert rel_err(got.cpu().numpy(), ref) <= TOL[dtype]
+    again = kernels.ghost_gram_grouped(groups1, groups2, bias=bias)
+    assert torch.equal(got, again)  # fixed reduction order: bitwise repeatable
+    acc = torch.ones_like(got)
+    kernels.ghost_gram_grouped(groups1, groups2, bias=bias, out=acc, accumulate=True)
+    assert rel_err(acc.cpu().numpy(), ref + 1.0) <= TOL[dtype]
+
+
+def test_moe_layers_cross_gram(device):
+    """Experts of two routed layers (different widths, one with bias) in one launch."""
+    from dattri_llm_amd.gradient import ops
+
+    gen = torch.Generator().manual_seed(41)
+    b, tokens, n_exp = 4, 200, 3
+    shapes = [((64, 160), True), ((128, 64), False)]  # ((d_in, d_out), bias); the wider one first
+    flat = torch.arange(b * tokens)
+    toks = [[flat[torch.rand(b * tokens, generator=gen) < 0.4] for _ in range(n_exp)] for _ in range(2)]
+    segs = [ops.moe.segment_experts([t.to(device) for t in side], b, tokens) for side in toks]
+    ref = np.zeros((b, b))
+    layers = []
+    for (k, d), bias in shapes:
+        experts = []
+        for e in range(n_exp):
+            t1, t2 = toks[0][e], toks[1][e]
+            a1, g1 = _rand(gen, t1.numel(), k, dtype=torch.bfloat16), _rand(gen, t1.numel(), d, dtype=torch.bfloat16)
+            a2, g2 = _rand(gen, t2.numel(), k, dtype=torch.bfloat16), _rand(gen, t2.numel(), d, dtype=torch.bfloat16)
+            ref += oracle.moe_segment_ghost(_np(a1), _np(g1), t1.numpy(), _np(a2), _np(g2), t2.numpy(),
+                                            b, b, tokens, tokens, bias=bias)
+            experts.append(tuple(x.to(device) for x in (a1, g1, a2, g2)))
+        layers.append((experts, bias))
+    got = ops.moe.moe_layers_cross_gram(layers, segs[0], segs[1])
+    assert rel_err(got.cpu().numpy(), ref) <= 1e-2
