@@ -540,9 +540,8 @@ def bench_moe(args):
     def step(timers=None):
         ev = _ev(timers, "route")
         segs = []
-        for lg in logits:  # router top-k, expert rows, per-sample segments of every expert
-            tok = [tk for _s, tk in ops.moe.expert_rows(ops.moe.router_topk(lg, top_k)[1], n_exp)]
-            segs.append(ops.moe.segment_experts(tok, b, t))
+        for lg, r in zip(logits, rows):  # router top-k, then every expert's per-sample segments in one launch
+            segs.append(ops.moe.route_segments(ops.moe.router_topk(lg, top_k)[1], n_exp, b, t, rows_per_expert=r))
         _ev_end(ev)
         ev = _ev(timers, "ghost")  # one grouped launch: every expert of both linears
         per_layer = [([(*caps[0][e][name], *caps[1][e][name]) for e in range(n_exp)], False)

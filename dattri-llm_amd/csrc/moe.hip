@@ -146,6 +146,104 @@ __global__ __launch_bounds__(256) void counting_sort_kernel(SortArgs a) {
   }
 }
 
+// Expert routing of one side in one workgroup.  Entries p = slot*N + token are
+// visited in order (the reference's slot-major enumeration); with e = idx[token][slot]
+// and b = token / T the kernel runs two stable counting sorts in the same pass:
+//   by e      -> entries[off[e] + r] = p for expert e's local row r (routed order);
+//   by e*B+b  -> rows[off2[e*B+b] + q] = r, expert e's local rows grouped by sample,
+// and seg[e*(B+1) + b] = off2[e*B+b] - off2[e*B] (per-expert relative offsets).
+struct RouteArgs {
+  const int64_t* index;  // (N, k)
+  int64_t n, k, experts, batch, tokens;
+  int32_t* offsets;  // experts + 1
+  int32_t* entries;  // n*k
+  int32_t* seg;      // experts * (batch + 1)
+  int32_t* rows;     // n*k
+};
+
+__global__ __launch_bounds__(256) void moe_route_kernel(RouteArgs a) {
+  __shared__ int32_t c1[kMaxExperts + 1];
+  __shared__ int32_t c2[kMaxBins + 1];
+  const int tid = threadIdx.x;
+  const int64_t total = a.n * a.k, nb2 = a.experts * a.batch;
+  for (int64_t b = tid; b <= a.experts; b += 256) c1[b] = 0;
+  for (int64_t b = tid; b <= nb2; b += 256) c2[b] = 0;
+  __syncthreads();
+  auto keys = [&](int64_t p, int64_t& e, int64_t& e2) __attribute__((always_inline)) {
+    const int64_t slot = p / a.n, tok = p - slot * a.n;
+    e = a.index[tok * a.k + slot];
+    e2 = (e >= 0 && e < a.experts) ? e * a.batch + tok / a.tokens : -1;
+    if (e < 0 || e >= a.experts) e = -1;
+  };
+  for (int64_t p = tid; p < total; p += 256) {
+    int64_t e, e2;
+    keys(p, e, e2);
+    if (e >= 0) {
+      atomicAdd(&c1[e], 1);
+      atomicAdd(&c2[e2], 1);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t run = 0;
+    for (int64_t e = 0; e < a.experts; ++e) {
+      const int32_t c = c1[e];
+      a.offsets[e] = run;
+      c1[e] = run;  // next free slot of expert e
+      run += c;
+    }
+    a.offsets[a.experts] = run;
+  } else if (tid == 64) {
+    int32_t run = 0;
+    for (int64_t q = 0; q < nb2; ++q) {
+      const int32_t c = c2[q];
+      c2[q] = run;
+      run += c;
+    }
+    c2[nb2] = run;
+  }
+  __syncthreads();
+  // Relative per-sample offsets of every expert (c2 holds bin starts until the
+  // scatter below advances them, so read them first).
+  for (int64_t q = tid; q < a.experts * (a.batch + 1); q += 256) {
+    const int64_t e = q / (a.batch + 1), b = q - e * (a.batch + 1);
+    a.seg[q] = c2[e * a.batch + b] - c2[e * a.batch];
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+  const int lane = tid;
+  for (int64_t base = 0; base < total; base += 64) {
+    const int64_t p = base + lane;
+    int64_t e = -1, e2 = -1;
+    if (p < total) keys(p, e, e2);
+    int r1 = 0, t1 = 0, r2 = 0, t2 = 0;
+    for (int src = 0; src < 64; ++src) {
+      const int64_t oe = __shfl(e, src, 64), oe2 = __shfl(e2, src, 64);
+      if (e >= 0 && oe == e) {
+        t1 += 1;
+        if (src < lane) r1 += 1;
+      }
+      if (e >= 0 && oe2 == e2) {
+        t2 += 1;
+        if (src < lane) r2 += 1;
+      }
+    }
+    int32_t slot1 = 0, slot2 = 0;
+    if (e >= 0) {
+      slot1 = c1[e] + r1;
+      slot2 = c2[e2] + r2;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) {
+      a.entries[slot1] = (int32_t)p;
+      a.rows[slot2] = slot1 - a.offsets[e];  // expert-local routed row
+      if (r1 == t1 - 1) c1[e] = slot1 + 1;
+      if (r2 == t2 - 1) c2[e2] = slot2 + 1;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 }  // namespace
 }  // namespace da
 
@@ -202,6 +300,37 @@ int da_counting_sort(const int32_t* keys32, const int64_t* keys64, int64_t n, in
   a.perm = perm;
   a.key_div = key_div;
   counting_sort_kernel<<<1, 256, 0, (hipStream_t)stream>>>(a);
+  return check_launch(who);
+}
+
+int da_moe_route(const int64_t* index, int64_t n_tokens, int k, int n_experts, int64_t batch,
+                 int64_t tokens, int32_t* expert_offsets, int32_t* entries, int32_t* seg, int32_t* rows,
+                 void* stream) {
+  using namespace da;
+  const char* who = "da_moe_route";
+  if (n_tokens < 0 || k < 1 || k > kMaxTopK)
+    return set_error(DA_ERR_INVALID, "%s: need n_tokens >= 0 and 1 <= k <= %d", who, kMaxTopK);
+  if (n_experts < 1 || n_experts > kMaxExperts)
+    return set_error(DA_ERR_INVALID, "%s: n_experts must be in [1, %d]", who, kMaxExperts);
+  if (batch < 1 || tokens < 1 || batch * tokens != n_tokens)
+    return set_error(DA_ERR_INVALID, "%s: n_tokens must equal batch * tokens", who);
+  if ((int64_t)n_experts * batch > kMaxBins)
+    return set_error(DA_ERR_INVALID, "%s: n_experts * batch must be <= %d", who, kMaxBins);
+  if (n_tokens * k > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: at most 2^31-1 entries", who);
+  if (!index || !expert_offsets || !entries || !seg || !rows)
+    return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  RouteArgs a;
+  a.index = index;
+  a.n = n_tokens;
+  a.k = k;
+  a.experts = n_experts;
+  a.batch = batch;
+  a.tokens = tokens;
+  a.offsets = expert_offsets;
+  a.entries = entries;
+  a.seg = seg;
+  a.rows = rows;
+  moe_route_kernel<<<1, 256, 0, (hipStream_t)stream>>>(a);
   return check_launch(who);
 }
 

@@ -118,7 +118,8 @@ SIGNATURES.update(
              _I64, _I64, _P, _I32, _I64, _P, _SZ, _P],
         ),
         "da_moe_topk": (_I32, [_P, _I32, _I64, _I32, _I32, _I64, _P, _P, _P]),
-        "da_counting_sort": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _I64, _I32, _P, _P, _P]),
+        "da_moe_route": (_I32, [_P, _I64, _I32, _I32, _I64, _I64, _P, _P, _P, _P, _P]),
+    "da_counting_sort": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _I64, _I32, _P, _P, _P]),
     }
 )
 

@@ -67,6 +67,25 @@ def expert_cross_gram(a1, g1, tok1, a2, g2, tok2, *, batch1: int, tokens1: int, 
                           tokens2=tokens2, bias=bias, out=out, accumulate=accumulate)
 
 
+def route_segments(top_idx: torch.Tensor, n_experts: int, batch: int, tokens: int,
+                   rows_per_expert=None) -> list[tuple[torch.Tensor, torch.Tensor]]:
+    """Per-sample segments of every expert straight from the top-k indices, in
+    one launch: ``(seg, rows)`` per expert, the same as
+    ``segment_experts([tok of expert_rows(top_idx)], batch, tokens)``.
+
+    ``rows_per_expert`` (host ints, e.g. the captures' row counts) avoids
+    reading the expert sizes back from the device."""
+    offsets, _entries, seg, rows = kernels.moe_route(top_idx.reshape(-1, top_idx.shape[-1]).to(torch.int64),
+                                                     n_experts, batch, tokens)
+    if rows_per_expert is None:
+        rows_per_expert = (offsets[1:] - offsets[:-1]).cpu().tolist()
+    out, start = [], 0
+    for e, r in enumerate(rows_per_expert):
+        out.append((seg[e], rows[start:start + int(r)]))
+        start += int(r)
+    return out
+
+
 def segment_experts(expert_tokens, batch: int, tokens: int) -> list[tuple[torch.Tensor, torch.Tensor]]:
     """Per-sample segments of every expert of one side: ``expert_tokens[e]`` is
     expert e's flat token index per routed row; returns ``(seg, rows)`` per

@@ -556,6 +556,27 @@ def counting_sort(keys: torch.Tensor, bins: int, *, slot_major: bool = False,
     return offsets, perm[:n]
 
 
+def moe_route(index: torch.Tensor, n_experts: int, batch: int, tokens: int):
+    """Expert routing of one side: ``(offsets (E+1), entries (N*k), seg (E, B+1),
+    rows (N*k))`` int32, as documented for ``da_moe_route``."""
+    dev = nat.require_device(index)
+    if index.dim() != 2 or index.dtype != torch.int64:
+        raise ValueError("moe_route expects the (N, k) int64 top-k index matrix")
+    index = index.contiguous()
+    n, k = index.shape
+    total = max(n * k, 1)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    entries = torch.empty(total, dtype=torch.int32, device=dev)
+    seg = torch.empty(n_experts, batch + 1, dtype=torch.int32, device=dev)
+    rows = torch.empty(total, dtype=torch.int32, device=dev)
+    nat.check(
+        nat.load().da_moe_route(index.data_ptr(), n, k, n_experts, batch, tokens, offsets.data_ptr(),
+                                entries.data_ptr(), seg.data_ptr(), rows.data_ptr(), nat.stream_ptr(dev)),
+        "moe_route",
+    )
+    return offsets, entries[: n * k], seg, rows[: n * k]
+
+
 def ghost_gram_segmented(a1, g1, seg1, idx1, tokens1, a2, g2, seg2, idx2, tokens2, *,
                          bias: bool = False, out: torch.Tensor | None = None,
                          accumulate: bool = False) -> torch.Tensor:

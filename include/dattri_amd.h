@@ -274,6 +274,29 @@ int da_counting_sort(const int32_t* keys32, const int64_t* keys64, int64_t n, in
                      int32_t* perm, void* stream);
 
 /*
+ * Expert routing of one side in one launch.  index is the (n_tokens, k) int64
+ * top-k matrix (da_moe_topk), n_tokens = batch * tokens (flat token
+ * b*tokens + t).  Entries p = slot*n_tokens + token are taken in the
+ * reference's order (slot-major, token ascending: torch.where over
+ * one_hot(idx).permute(2,1,0)[e], fused_experts.py:219-228) and sorted
+ * stably twice in one pass:
+ *   expert_offsets (n_experts+1): expert e owns routed rows
+ *       [expert_offsets[e], expert_offsets[e+1]);
+ *   entries (n*k): entries[expert_offsets[e] + r] = p of expert e's row r;
+ *   seg (n_experts * (batch+1)): seg[e*(batch+1) + b] = number of expert e's
+ *       rows from samples < b (per-expert relative offsets);
+ *   rows (n*k): rows[expert_offsets[e] + q] = expert e's local row numbers
+ *       grouped by sample (stable): the (seg, row_index) pair of a group of
+ *       da_ghost_gram_grouped.
+ * Replaces the per-expert torch.where loop of fused_experts.py:219-228 plus
+ * the regroup bookkeeping of hooks/routing.py:71-86.  n_experts <= 256,
+ * n_experts * batch <= 8192; indices outside [0, n_experts) are dropped.
+ */
+int da_moe_route(const int64_t* index, int64_t n_tokens, int k, int n_experts, int64_t batch,
+                 int64_t tokens, int32_t* expert_offsets, int32_t* entries, int32_t* seg, int32_t* rows,
+                 void* stream);
+
+/*
  * Lane-layout self test of the MFMA conventions every kernel relies on.
  * shape 32: a and b are (32 x k) row-major with k = 16 (bf16/f16) or 8 (f32),
  *           one 16-byte chunk per lane half; out receives 64 lanes x 16

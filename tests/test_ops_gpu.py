@@ -302,3 +302,27 @@ def test_c1_tracin_attributor_and_cosine(device):
     want = fx / (np.sqrt(np.diag(tr_self))[:, None] * np.sqrt(np.diag(q_self))[None, :] + 1e-8)
     assert cos.algorithm == "GradCos"
     assert rel_err(cos.scores.numpy(), want) <= 1e-3
+
+
+@pytest.mark.parametrize("batch,tokens,n_exp,k", [(16, 256, 8, 2), (3, 37, 5, 3), (1, 64, 4, 1)])
+def test_route_segments_matches_per_expert_sorts(device, ops, batch, tokens, n_exp, k):
+    """One-launch routing == router top-k -> per-expert torch.where order ->
+    per-expert stable sort by sample, bit for bit."""
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(batch * 100 + n_exp)
+    logits = torch.randn(batch * tokens, n_exp, generator=gen).to(device)
+    _, idx = ops.moe.router_topk(logits, k)
+    per_expert = ops.moe.expert_rows(idx, n_exp)
+    want = ops.moe.segment_experts([tok for _slot, tok in per_expert], batch, tokens)
+    got = ops.moe.route_segments(idx, n_exp, batch, tokens)
+    assert len(got) == n_exp
+    for (seg_w, rows_w), (seg_g, rows_g) in zip(want, got):
+        assert torch.equal(seg_w.cpu(), seg_g.cpu())
+        assert torch.equal(rows_w.cpu(), rows_g.cpu())
+    offsets, entries, _seg, _rows = kernels.moe_route(idx, n_exp, batch, tokens)
+    off = offsets.cpu().tolist()
+    n = idx.shape[0]
+    for e, (slot, tok) in enumerate(per_expert):
+        ent = entries[off[e]:off[e + 1]].to(torch.int64)
+        assert torch.equal((ent // n).cpu(), slot.cpu()) and torch.equal((ent % n).cpu(), tok.cpu())
