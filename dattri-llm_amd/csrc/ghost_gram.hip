@@ -387,10 +387,308 @@ __global__ void grouped_reduce(GroupedArgs ga, float* __restrict__ out, int64_t 
   *o = accumulate ? *o + v : v;
 }
 
+// ---------------------------------------------------------------------------
+// 256 x 128 tile engine (the gfx950 path).
+//
+// Both Gram products of a tile -- K_a over the activation width, then K_g over
+// the gradient width -- run as ONE stream of 64-byte K stages through a ring of
+// four LDS stages (24 KB each).  Operand rows go HBM -> LDS untouched by buffer
+// loads with the LDS-direct bit (16 bytes per lane); rows past a sample's end,
+// and chunks past the width, read as zero (offset past the buffer range).  The
+// four waves each own a 128 x 64 block (4 x 2 MFMA blocks of 32 x 32); K_a and
+// K_g together fill the 256 accumulator registers.  As in the dW kernel, the
+// loads are issued as inline assembly with explicit vmcnt waits, interleaved
+// with the MFMAs, and each stage's second slice is multiplied after the
+// barrier that opens the next stage.
+// ---------------------------------------------------------------------------
+namespace v2 {
+constexpr int kBM = 256;                 // side-1 rows per tile
+constexpr int kBN = 128;                 // side-2 rows per tile
+constexpr int kRows = kBM + kBN;         // LDS rows per stage
+constexpr int kSB = 128;                 // bytes of K per row and stage: one cache line, four 32-byte slices
+constexpr int kStage = kRows * kSB;      // 48 KB
+constexpr int kNBuf = 3;                 // ring: two stages in flight
+constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // DMA instructions per wave and stage
+constexpr uint32_t kOob = 0x80000000u;
+constexpr int kPRow = kBN + 1;           // parked fp32 product row (grouped epilogue)
+constexpr int kRing = kNBuf * kStage;
+constexpr int kPark = kBM * kPRow * 4;
+constexpr int kSmem = kPark > kRing ? kPark : kRing;
+static_assert(kDma == 12, "three DMA instructions per quarter stage");
+static_assert(kSmem <= 160 * 1024, "LDS");
+// 16-byte chunk c of LDS row r sits in slot c ^ (r & 7): the 8 lanes one LDS
+// cycle serves (8 consecutive rows, one chunk) read 8 distinct bank groups.
+}  // namespace v2
+
+typedef __attribute__((address_space(3))) char lds_char;
+
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+__device__ __forceinline__ u32x4 uniform4(u32x4 v) {
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane(v[0]), (uint32_t)__builtin_amdgcn_readfirstlane(v[1]),
+               (uint32_t)__builtin_amdgcn_readfirstlane(v[2]), (uint32_t)__builtin_amdgcn_readfirstlane(v[3])};
+}
+
+// Operand sources of one tile: buffer resources of the four factors and, per
+// lane, the byte offset of the row each of its 12 DMA instructions loads
+// (kOob for rows past an end), for the activation and the gradient.
+struct TileSrc {
+  u32x4 ra1, rg1, ra2, rg2;
+  uint32_t roff_a[v2::kDma], roff_g[v2::kDma];
+  int64_t kbytes_a, kbytes_g;
+};
+
+// Tile row loaded by lane `lane` of DMA instruction j of wave w.
+__device__ __forceinline__ int dma_row(int w, int j, int lane) { return 8 * (v2::kDma * w + j) + (lane >> 3); }
+
+// Load-issue state of one wave (plain locals after inlining).
+struct DmaState {
+  u32x4 ra1, rg1, ra2, rg2;            // wave-uniform
+  uint32_t roa[v2::kDma], rog[v2::kDma];
+  uint32_t cbyte, lds0;
+  int uwave, na, nst;
+  int64_t kba, kbg;
+};
+
+// Quarter q of stage st's loads = instructions 3q .. 3q+2 of every wave.
+// DMA instruction j of wave w loads tile rows 8*(12w + j) .. +7 (rows < 256 are
+// side 1); lane l -> row 8*(12w+j) + l/8, slot l%8 holding logical chunk
+// (l%8) ^ (l/8), which is cbyte / 16.
+__device__ __forceinline__ void dma_quarter(const DmaState& D, int q, int st) {
+  const bool act = st < D.na;
+  const uint32_t koff = (uint32_t)(act ? st : st - D.na) * v2::kSB;
+  const int64_t kb = act ? D.kba : D.kbg;
+  const bool kin = st < D.nst && (int64_t)(koff + D.cbyte) < kb;
+  const uint32_t base = D.lds0 + (uint32_t)((st % v2::kNBuf) * v2::kStage + v2::kDma * D.uwave * 8 * v2::kSB);
+#pragma unroll
+  for (int x = 0; x < 3; ++x) {
+    const int j = 3 * q + x;
+    const bool side1 = v2::kDma * D.uwave + j < v2::kBM / 8;  // uniform
+    const uint32_t m = act ? 0xffffffffu : 0u;
+    const uint32_t roff = (D.roa[j] & m) | (D.rog[j] & ~m);
+    // Mask arithmetic, not a select: a select between the four descriptors is
+    // turned into a pointer select over stack copies (a scratch load, and the
+    // compiler then waits for every outstanding load before using it).
+    const uint32_t ms = side1 ? 0xffffffffu : 0u;
+    u32x4 rs;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      rs[c] = (((D.ra1[c] & m) | (D.rg1[c] & ~m)) & ms) | (((D.ra2[c] & m) | (D.rg2[c] & ~m)) & ~ms);
+    dma16(rs, base + (uint32_t)(j * 8 * v2::kSB), (kin && roff != v2::kOob) ? roff + koff + D.cbyte : v2::kOob);
+  }
+}
+
+// One quarter of a stage: the 8 MFMAs of one slice held in (ua, ub) into acc;
+// with rd, the 6 fragment reads of the slice (stage base sb, slice kk) into
+// (na, nb) interleaved one per MFMA; with qd >= 0, quarter qd of stage dst's
+// loads after the second MFMA.
+template <int DT>
+__device__ __forceinline__ void ghost_quarter(f32x16 (&acc)[4][2], const u32x4 (&ua)[4], const u32x4 (&ub)[2],
+                                              bool rd, const lds_char* sb, int coff, int wm, int wn,
+                                              u32x4 (&na)[4], u32x4 (&nb)[2], const DmaState& D, int qd, int dst) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (rd) {
+      if (i < 4) na[i] = *(const u32x4*)(sb + (128 * wm + 32 * i) * v2::kSB + coff);
+      else if (i < 6) nb[i - 4] = *(const u32x4*)(sb + (v2::kBM + 64 * wn + 32 * (i - 4)) * v2::kSB + coff);
+    }
+    Mfma32<DT>::mma(acc[i >> 1][i & 1], ua[i >> 1], ub[i & 1]);
+    if (qd >= 0 && i == 1) dma_quarter(D, qd, dst);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Wait for this wave's loads of the next stage (the 12 instructions of the
+// stage after it may stay in flight) and its own LDS reads, then barrier.  The
+// LDS wait is the compiler's own s_waitcnt (lgkmcnt(0), others at maximum) so
+// it knows the fragments in registers are complete.
+__device__ __forceinline__ void ghost_stage_sync() {
+  static_assert(v2::kNBuf == 3, "vmcnt below is one stage of 12 instructions");
+  asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Runs the tile's two K loops; returns with every wave done reading the ring
+// (so the caller may reuse the LDS) and no load in flight.
+template <int DT>
+__device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, f32x16 (&ka)[4][2],
+                                                  f32x16 (&kg)[4][2]) {
+  lds_char* const L = (lds_char*)smem;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  DmaState D;
+  D.uwave = __builtin_amdgcn_readfirstlane(wave);
+  D.na = (int)((S.kbytes_a + v2::kSB - 1) / v2::kSB);
+  D.nst = D.na + (int)((S.kbytes_g + v2::kSB - 1) / v2::kSB);
+  D.ra1 = uniform4(S.ra1);
+  D.rg1 = uniform4(S.rg1);
+  D.ra2 = uniform4(S.ra2);
+  D.rg2 = uniform4(S.rg2);
+  D.kba = S.kbytes_a;
+  D.kbg = S.kbytes_g;
+  D.lds0 = (uint32_t)(uintptr_t)L;
+  D.cbyte = 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
+#pragma unroll
+  for (int j = 0; j < v2::kDma; ++j) {
+    D.roa[j] = S.roff_a[j];
+    D.rog[j] = S.roff_g[j];
+  }
+  const int na = D.na, nst = D.nst;
+
+  // Fragment offsets inside a stage: A fragment x = rows 128wm + 32x + l%32,
+  // B fragment y = rows 256 + 64wn + 32y + l%32; slice kk reads logical chunk
+  // 2kk + l/32, stored in slot (2kk + l/32) ^ (l%8).
+  const int lrow = lane & 31, hh = lane >> 5;
+  const int c0 = lrow * v2::kSB + (((0 + hh) ^ (lane & 7)) << 4), c1 = lrow * v2::kSB + (((2 + hh) ^ (lane & 7)) << 4);
+  const int c2 = lrow * v2::kSB + (((4 + hh) ^ (lane & 7)) << 4), c3 = lrow * v2::kSB + (((6 + hh) ^ (lane & 7)) << 4);
+  u32x4 f0a[4], f0b[2], f1a[4], f1b[2];
+
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      ka[x][y] = f32x16{};
+      kg[x][y] = f32x16{};
+    }
+
+  // Stage s's loads: quarter 0 in the last quarter of iteration s - 3,
+  // quarters 1..3 in the first three quarters of iteration s - 2.  Iteration
+  // st: quarters 0..2 multiply slices 0..2 of stage st (reading 1..3), the
+  // barrier opens stage st + 1, quarter 3 multiplies slice 3 of st while
+  // reading slice 0 of st + 1.  Before each barrier exactly 12 instructions
+  // follow the awaited stage's last one.
+#pragma unroll
+  for (int s0 = 0; s0 < v2::kNBuf - 1; ++s0)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma_quarter(D, q, s0);
+  ghost_stage_sync();
+  dma_quarter(D, 0, v2::kNBuf - 1);
+#pragma unroll
+  for (int x = 0; x < 4; ++x) f0a[x] = *(const u32x4*)(L + (128 * wm + 32 * x) * v2::kSB + c0);
+#pragma unroll
+  for (int y = 0; y < 2; ++y) f0b[y] = *(const u32x4*)(L + (v2::kBM + 64 * wn + 32 * y) * v2::kSB + c0);
+
+  // The loops carry no branch around their MFMAs (a join there makes the
+  // register allocator shuffle accumulators); the last stage is peeled
+  // (nst > na >= 0 because the gradient width is non-zero).
+#define DA_GHOST_ITER(ACC)                                                                            \
+  {                                                                                                   \
+    const lds_char* cur = L + (st % v2::kNBuf) * v2::kStage;                                                  \
+    ghost_quarter<DT>(ACC, f0a, f0b, true, cur, c1, wm, wn, f1a, f1b, D, 1, st + 2);                   \
+    ghost_quarter<DT>(ACC, f1a, f1b, true, cur, c2, wm, wn, f0a, f0b, D, 2, st + 2);                   \
+    ghost_quarter<DT>(ACC, f0a, f0b, true, cur, c3, wm, wn, f1a, f1b, D, 3, st + 2);                   \
+    ghost_stage_sync();                                                                               \
+    ghost_quarter<DT>(ACC, f1a, f1b, true, L + ((st + 1) % v2::kNBuf) * v2::kStage, c0, wm, wn, f0a, f0b, D, 0, \
+                      st + 3);                                                                        \
+  }
+  for (int st = 0; st < na; ++st) DA_GHOST_ITER(ka)
+  for (int st = na; st + 1 < nst; ++st) DA_GHOST_ITER(kg)
+#undef DA_GHOST_ITER
+  {
+    const lds_char* cur = L + ((nst - 1) % v2::kNBuf) * v2::kStage;
+    ghost_quarter<DT>(kg, f0a, f0b, true, cur, c1, wm, wn, f1a, f1b, D, -1, 0);
+    ghost_quarter<DT>(kg, f1a, f1b, true, cur, c2, wm, wn, f0a, f0b, D, -1, 0);
+    ghost_quarter<DT>(kg, f0a, f0b, true, cur, c3, wm, wn, f1a, f1b, D, -1, 0);
+    ghost_quarter<DT>(kg, f1a, f1b, false, cur, c0, wm, wn, f0a, f0b, D, -1, 0);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Dense / per-sample segmented mode: a 256 x 128 tile inside one sample pair.
+template <int DT>
+__global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
+  __shared__ float red[kThreads / kWave];
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t per_group = (int64_t)kGroup * g.n_c;
+  const int64_t group = logical / per_group;
+  const int64_t first_r = group * kGroup;
+  const int64_t gsize = min(g.n_r - first_r, (int64_t)kGroup);
+  const int64_t in_group = logical - group * per_group;
+  const int64_t R = first_r + in_group % gsize;
+  const int64_t C = in_group / gsize;
+  const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
+  const int64_t j = C / g.tiles_c, ss = C % g.tiles_c;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  const int64_t len1 = seg_len(g.s1, i), len2 = seg_len(g.s2, j);
+  const int64_t t0 = tt * v2::kBM, s0 = ss * v2::kBN;
+  float* dst = g.partial + ((i * g.s2.batch + j) * g.tiles_r + tt) * g.tiles_c + ss;
+  if (t0 >= len1 || s0 >= len2) {
+    if (tid == 0) *dst = 0.f;
+    return;
+  }
+  const int64_t st1 = seg_start(g.s1, i), st2 = seg_start(g.s2, j);
+  // Buffer bases: the sample's first row (dense) or the factor (segmented);
+  // the host checked that every offset stays below 2^31.
+  const char* ba1 = g.s1.seg ? g.s1.act : g.s1.act + i * g.s1.act_bstride;
+  const char* bg1 = g.s1.seg ? g.s1.grad : g.s1.grad + i * g.s1.grad_bstride;
+  const char* ba2 = g.s2.seg ? g.s2.act : g.s2.act + j * g.s2.act_bstride;
+  const char* bg2 = g.s2.seg ? g.s2.grad : g.s2.grad + j * g.s2.grad_bstride;
+  TileSrc S;
+  S.ra1 = make_rsrc(ba1, 0x7fffffffu);
+  S.rg1 = make_rsrc(bg1, 0x7fffffffu);
+  S.ra2 = make_rsrc(ba2, 0x7fffffffu);
+  S.rg2 = make_rsrc(bg2, 0x7fffffffu);
+  S.kbytes_a = g.kbytes_a;
+  S.kbytes_g = g.kbytes_g;
+#pragma unroll
+  for (int q = 0; q < v2::kDma; ++q) {
+    const int row = dma_row(wave, q, lane);
+    const bool side1 = row < v2::kBM;
+    const SideDev& sd = side1 ? g.s1 : g.s2;
+    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
+    const int64_t len = side1 ? len1 : len2;
+    const int64_t start = side1 ? st1 : st2;
+    if (t < len) {
+      const int64_t r = sd.seg ? (sd.idx ? (int64_t)sd.idx[start + t] : start + t) : t;
+      S.roff_a[q] = (uint32_t)(r * sd.act_tstride);
+      S.roff_g[q] = (uint32_t)(r * sd.grad_tstride);
+    } else {
+      S.roff_a[q] = v2::kOob;
+      S.roff_g[q] = v2::kOob;
+    }
+  }
+  f32x16 ka[4][2], kg[4][2];
+  ghost_tile_engine<DT>(S, smem, ka, kg);
+  float s = 0.f;
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += (ka[x][y][r] + g.bias) * kg[x][y][r];
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (tid == 0) *dst = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 struct Plan {
   int64_t tiles_r, tiles_c, n_r, n_c, per_pair;
   size_t ws;
+  bool v2;  // the 256 x 128 tile engine (dense sides whose offsets fit 31 bits)
 };
+
+// The tile engine addresses a sample's rows with 32-bit buffer offsets.
+bool fits_v2(const da_factor_side* s, int64_t K, int64_t D, int64_t es) {
+  if (s->seg_offsets) return false;
+  const int64_t ts = s->act_tstride > s->grad_tstride ? s->act_tstride : s->grad_tstride;
+  const int64_t w = K > D ? K : D;
+  return s->act_tstride >= 0 && s->grad_tstride >= 0 && (s->tokens * ts + w) * es < (1LL << 31) - (1LL << 20);
+}
 
 int validate_side(const da_factor_side* s, int64_t K, int64_t D, int dtype, const char* name) {
   if (!s) return set_error(DA_ERR_INVALID, "da_ghost_gram: %s is NULL", name);
@@ -427,8 +725,10 @@ int make_plan(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int
   if (rc) return rc;
   if (s1->has_bias != s2->has_bias)
     return set_error(DA_ERR_INVALID, "da_ghost_gram: both sides must agree on has_bias");
-  plan->tiles_r = (s1->tokens + kBM - 1) / kBM;
-  plan->tiles_c = (s2->tokens + kBN - 1) / kBN;
+  plan->v2 = fits_v2(s1, K, D, es) && fits_v2(s2, K, D, es);
+  const int64_t bm = plan->v2 ? v2::kBM : kBM, bn = plan->v2 ? v2::kBN : kBN;
+  plan->tiles_r = (s1->tokens + bm - 1) / bm;
+  plan->tiles_c = (s2->tokens + bn - 1) / bn;
   plan->n_r = s1->batch * plan->tiles_r;
   plan->n_c = s2->batch * plan->tiles_c;
   plan->per_pair = plan->tiles_r * plan->tiles_c;
@@ -553,10 +853,18 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
   const int64_t ntiles = plan.n_r * plan.n_c;
   if (ntiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_ghost_gram: too many tiles");
   dim3 grid((unsigned)ntiles);
-  switch (dtype) {
-    case DA_BF16: ghost_gram_tiles<DA_BF16><<<grid, kThreads, 0, st>>>(args); break;
-    case DA_F16: ghost_gram_tiles<DA_F16><<<grid, kThreads, 0, st>>>(args); break;
-    default: ghost_gram_tiles<DA_F32><<<grid, kThreads, 0, st>>>(args); break;
+  if (plan.v2) {
+    switch (dtype) {
+      case DA_BF16: ghost_gram_tiles_v2<DA_BF16><<<grid, kThreads, 0, st>>>(args); break;
+      case DA_F16: ghost_gram_tiles_v2<DA_F16><<<grid, kThreads, 0, st>>>(args); break;
+      default: ghost_gram_tiles_v2<DA_F32><<<grid, kThreads, 0, st>>>(args); break;
+    }
+  } else {
+    switch (dtype) {
+      case DA_BF16: ghost_gram_tiles<DA_BF16><<<grid, kThreads, 0, st>>>(args); break;
+      case DA_F16: ghost_gram_tiles<DA_F16><<<grid, kThreads, 0, st>>>(args); break;
+      default: ghost_gram_tiles<DA_F32><<<grid, kThreads, 0, st>>>(args); break;
+    }
   }
   rc = check_launch("da_ghost_gram(tiles)");
   if (rc) return rc;
