@@ -379,7 +379,7 @@ def bench_ghost(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "ghost cross-gram 256 train x 64 query, T=512, d_in=d_out=4096"},
-        "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles", "achieved": round(tflops, 1),
+        "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles_v2", "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
     }
@@ -577,7 +577,7 @@ def bench_moe(args):
         "config": {"workload": "mixtral moe layer: 16 train x 256 tok vs 16 query x 256 tok, 8 experts top-2, "
                                "gate_up 4096->28672, down 14336->4096, grouped packed ghost route",
                    "rows_per_expert": rows},
-        "roofline": {"bound": "mfma", "kernel": "ghost_grouped_tiles", "achieved": round(tf, 1),
+        "roofline": {"bound": "mfma", "kernel": "ghost_grouped_tiles_v2", "achieved": round(tf, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
                      "traffic": None, "work_per_step": f"{flops:.4g} flop = sum over experts and both linears "
                                                        "of 2 x rows1 x rows2 x (d_in + d_out)",

@@ -229,6 +229,7 @@ struct GroupDev {
 struct GroupedArgs {
   GroupDev grp[kMaxGroups];
   int n_groups;
+  int tile_r, tile_c;  // tile heights on side 1 / side 2 (the spans are counted in tiles)
   int64_t b1, b2;
   float* partial;
   int32_t* meta;  // per group: first1[B1], pre1[B1+1], first2[B2], pre2[B2+1]
@@ -259,11 +260,12 @@ __global__ __launch_bounds__(256) void grouped_spans(GroupedArgs ga) {
   const int tid = threadIdx.x;
   const int64_t per = (nb + 255) / 256;
   const int64_t b0 = tid * per, b1e = min(b0 + per, nb);
+  const int32_t th = side ? ga.tile_c : ga.tile_r;
   int32_t local = 0;
   for (int64_t b = b0; b < b1e; ++b) {
     const int32_t s0 = seg[b], s1 = seg[b + 1];
-    first[b] = s0 / kBM;
-    local += s1 > s0 ? (s1 - 1) / kBM - s0 / kBM + 1 : 0;
+    first[b] = s0 / th;
+    local += s1 > s0 ? (s1 - 1) / th - s0 / th + 1 : 0;
   }
   part[tid] = local;
   __syncthreads();
@@ -277,7 +279,41 @@ __global__ __launch_bounds__(256) void grouped_spans(GroupedArgs ga) {
   for (int64_t b = b0; b < b1e; ++b) {
     pre[b] = run;
     const int32_t s0 = seg[b], s1 = seg[b + 1];
-    run += s1 > s0 ? (s1 - 1) / kBM - s0 / kBM + 1 : 0;
+    run += s1 > s0 ? (s1 - 1) / th - s0 / th + 1 : 0;
+  }
+}
+
+// Bins of one tile's parked products P (rows x cols, row stride prow): the
+// (sample i, sample j) pairs meeting rows [t0, t0 + rows) ∩ [0, n1) and columns
+// [s0, s0 + cols) ∩ [0, n2); one wave per bin, lanes over rows, each lane
+// summing its rows' columns in order, then a fixed butterfly.  Bin (i, j) of
+// tile (m, n) goes to slot (pre1[i] + m - first1[i], pre2[j] + n - first2[j])
+// of the group's region (clamped to it).
+__device__ __forceinline__ void grouped_bins(const float* P, int prow, int rows, int cols, int64_t t0, int64_t s0,
+                                             int64_t n1, int64_t n2, int64_t m, int64_t n, const GroupDev& G,
+                                             const GroupedArgs& ga) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t last_r = min(t0 + rows, n1) - 1, last_c = min(s0 + cols, n2) - 1;
+  if (last_r < t0 || last_c < s0) return;  // no live rows on a side: no bins
+  const int64_t i_lo = sample_of(G.seg1, ga.b1, t0), i_hi = sample_of(G.seg1, ga.b1, last_r);
+  const int64_t j_lo = sample_of(G.seg2, ga.b2, s0), j_hi = sample_of(G.seg2, ga.b2, last_c);
+  const int64_t nj = j_hi - j_lo + 1, nbins = (i_hi - i_lo + 1) * nj;
+  const int32_t* first1 = ga.meta + G.meta_off;
+  const int32_t* pre1 = first1 + ga.b1;
+  const int32_t* first2 = pre1 + ga.b1 + 1;
+  const int32_t* pre2 = first2 + ga.b2;
+  for (int64_t bin = wave; bin < nbins; bin += (int64_t)(blockDim.x / kWave)) {
+    const int64_t i = i_lo + bin / nj, j = j_lo + bin % nj;
+    const int64_t r0 = max((int64_t)G.seg1[i], t0) - t0, r1 = min((int64_t)G.seg1[i + 1], t0 + rows) - t0;
+    const int64_t c0 = max((int64_t)G.seg2[j], s0) - s0, c1 = min((int64_t)G.seg2[j + 1], s0 + cols) - s0;
+    if (r1 <= r0 || c1 <= c0) continue;  // an empty sample: it owns no slot
+    float v = 0.f;
+    for (int64_t t = r0 + lane; t < r1; t += kWave)
+      for (int64_t c = c0; c < c1; ++c) v += P[t * prow + c];
+    v = wave_sum(v);
+    const int64_t row = pre1[i] + m - first1[i], col = pre2[j] + n - first2[j];
+    if (lane == 0 && row >= 0 && row < G.tiles_r + ga.b1 && col >= 0 && col < G.part_ld)
+      ga.partial[G.part_off + row * G.part_ld + col] = v;
   }
 }
 
@@ -339,32 +375,7 @@ __global__ __launch_bounds__(kThreads, 2) void ghost_grouped_tiles(GroupedArgs g
       }
   __syncthreads();
 
-  // Bins: (sample i, sample j) pairs meeting this tile; one wave per bin, lanes
-  // over rows, each lane summing its rows' columns in order, then a fixed
-  // butterfly.  Bin (i, j) of tile (m, n) goes to slot
-  // (pre1[i] + m - first1[i], pre2[j] + n - first2[j]) of the group's region.
-  const int64_t last_r = min(t0 + kBM, n1) - 1, last_c = min(s0 + kBN, n2) - 1;
-  if (last_r < t0 || last_c < s0) return;  // no live rows on a side: no bins
-  const int64_t i_lo = sample_of(G.seg1, ga.b1, t0), i_hi = sample_of(G.seg1, ga.b1, last_r);
-  const int64_t j_lo = sample_of(G.seg2, ga.b2, s0), j_hi = sample_of(G.seg2, ga.b2, last_c);
-  const int64_t nj = j_hi - j_lo + 1, nbins = (i_hi - i_lo + 1) * nj;
-  const int32_t* first1 = ga.meta + G.meta_off;
-  const int32_t* pre1 = first1 + ga.b1;
-  const int32_t* first2 = pre1 + ga.b1 + 1;
-  const int32_t* pre2 = first2 + ga.b2;
-  for (int64_t bin = wave; bin < nbins; bin += kThreads / kWave) {
-    const int64_t i = i_lo + bin / nj, j = j_lo + bin % nj;
-    const int64_t r0 = max((int64_t)G.seg1[i], t0) - t0, r1 = min((int64_t)G.seg1[i + 1], t0 + kBM) - t0;
-    const int64_t c0 = max((int64_t)G.seg2[j], s0) - s0, c1 = min((int64_t)G.seg2[j + 1], s0 + kBN) - s0;
-    if (r1 <= r0 || c1 <= c0) continue;  // an empty sample: it owns no slot
-    float v = 0.f;
-    for (int64_t t = r0 + lane; t < r1; t += kWave)
-      for (int64_t c = c0; c < c1; ++c) v += P[t * kPRow + c];
-    v = wave_sum(v);
-    const int64_t row = pre1[i] + m - first1[i], col = pre2[j] + n - first2[j];
-    if (lane == 0 && row >= 0 && row < G.tiles_r + ga.b1 && col >= 0 && col < G.part_ld)
-      ga.partial[G.part_off + row * G.part_ld + col] = v;
-  }
+  grouped_bins(P, kPRow, kBM, kBN, t0, s0, n1, n2, m, n, G, ga);
 }
 
 // out[i, j] (+)= sum over groups of the (span1 x span2) slot block, in a fixed order.
@@ -607,6 +618,64 @@ __device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, 
     ghost_quarter<DT>(kg, f1a, f1b, false, cur, c0, wm, wn, f0a, f0b, D, -1, 0);
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Grouped (MoE) mode on the 256 x 128 engine: tiles over each group's packed
+// rows, the tile's products parked in LDS and binned by sample pair.
+template <int DT>
+__global__ __launch_bounds__(kThreads, 1) void ghost_grouped_tiles_v2(GroupedArgs ga) {
+  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  int e = 0;
+  while (e + 1 < ga.n_groups && ga.grp[e + 1].tile0 <= logical) ++e;
+  const GroupDev& G = ga.grp[e];
+  const int64_t local = logical - G.tile0;
+  constexpr int64_t kRowGroup = 4;
+  const int64_t per_group = kRowGroup * G.tiles_c;
+  const int64_t grp = local / per_group;
+  const int64_t first_r = grp * kRowGroup;
+  const int64_t gsize = min(G.tiles_r - first_r, kRowGroup);
+  const int64_t in_group = local - grp * per_group;
+  const int64_t m = first_r + in_group % gsize;
+  const int64_t n = in_group / gsize;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t t0 = m * v2::kBM, s0 = n * v2::kBN;
+  // Rows at or past seg[B] belong to no sample (and may have no row_index entry).
+  const int64_t n1 = min(G.rows1, (int64_t)G.seg1[ga.b1]), n2 = min(G.rows2, (int64_t)G.seg2[ga.b2]);
+  TileSrc S;
+  S.ra1 = make_rsrc(G.a1, 0x7fffffffu);
+  S.rg1 = make_rsrc(G.g1, 0x7fffffffu);
+  S.ra2 = make_rsrc(G.a2, 0x7fffffffu);
+  S.rg2 = make_rsrc(G.g2, 0x7fffffffu);
+  S.kbytes_a = G.kbytes_a;
+  S.kbytes_g = G.kbytes_g;
+#pragma unroll
+  for (int q = 0; q < v2::kDma; ++q) {
+    const int row = dma_row(wave, q, lane);
+    const bool side1 = row < v2::kBM;
+    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
+    const bool live = t < (side1 ? n1 : n2);
+    const int32_t* idx = side1 ? G.idx1 : G.idx2;
+    const int64_t r = live ? (idx ? (int64_t)idx[t] : t) : 0;
+    S.roff_a[q] = live ? (uint32_t)(r * (side1 ? G.a1_ts : G.a2_ts)) : v2::kOob;
+    S.roff_g[q] = live ? (uint32_t)(r * (side1 ? G.g1_ts : G.g2_ts)) : v2::kOob;
+  }
+  f32x16 ka[4][2], kg[4][2];
+  ghost_tile_engine<DT>(S, smem, ka, kg);
+  float* P = (float*)smem;
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 128 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
+        P[row * v2::kPRow + col] = (ka[x][y][r] + G.bias) * kg[x][y][r];
+      }
+  __syncthreads();
+  grouped_bins(P, v2::kPRow, v2::kBM, v2::kBN, t0, s0, n1, n2, m, n, G, ga);
 }
 
 // ---------------------------------------------------------------------------
@@ -989,6 +1058,8 @@ namespace {
 
 struct GroupedPlan {
   size_t meta_ints, part_floats, ws;
+  bool v2;         // all groups on the 256 x 128 engine
+  int tile_r, tile_c;
 };
 
 // Layout of the grouped workspace for the groups [g0, g0 + n): int32 span
@@ -1001,6 +1072,19 @@ int grouped_plan(const da_factor_side* s1, const da_factor_side* s2, int n_group
   const int64_t es = (int64_t)elem_bytes(dtype);
   p->meta_ints = 0;
   p->part_floats = 0;
+  p->v2 = true;
+  for (int e = 0; e < n_groups; ++e) {
+    // 32-bit buffer offsets over every group's rows, and a gradient loop
+    const da_factor_side* sd[2] = {&s1[e], &s2[e]};
+    for (int q = 0; q < 2; ++q) {
+      const int64_t ts = sd[q]->act_tstride > sd[q]->grad_tstride ? sd[q]->act_tstride : sd[q]->grad_tstride;
+      const int64_t w = K[e] > D[e] ? K[e] : D[e];
+      if (sd[q]->tokens < 0 || ts < 0 || (sd[q]->tokens * ts + w) * es >= (1LL << 31) - (1LL << 20)) p->v2 = false;
+    }
+    if (D[e] <= 0) p->v2 = false;
+  }
+  p->tile_r = p->v2 ? v2::kBM : kBM;
+  p->tile_c = p->v2 ? v2::kBN : kBN;
   if (n_groups == 0) { p->ws = 0; return DA_OK; }
   const int64_t b1 = s1[0].batch, b2 = s2[0].batch;
   for (int e = 0; e < n_groups; ++e) {
@@ -1027,7 +1111,7 @@ int grouped_plan(const da_factor_side* s1, const da_factor_side* s2, int n_group
           return set_error(DA_ERR_INVALID, "da_ghost_gram_grouped: row strides must be multiples of 16 bytes");
       }
     }
-    const int64_t tr = (s1[e].tokens + kBM - 1) / kBM, tc = (s2[e].tokens + kBN - 1) / kBN;
+    const int64_t tr = (s1[e].tokens + p->tile_r - 1) / p->tile_r, tc = (s2[e].tokens + p->tile_c - 1) / p->tile_c;
     p->meta_ints += (size_t)(2 * b1 + 1 + 2 * b2 + 1);
     p->part_floats += (size_t)((tr + b1) * (tc + b2));
   }
@@ -1139,6 +1223,8 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
     const int n = n_groups - g0 < kMaxGroups ? n_groups - g0 : kMaxGroups;
     GroupedArgs ga;
     ga.n_groups = 0;
+    ga.tile_r = plan.tile_r;
+    ga.tile_c = plan.tile_c;
     ga.b1 = b1;
     ga.b2 = b2;
     ga.partial = part;
@@ -1147,7 +1233,7 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
     for (int q = 0; q < n; ++q) {
       const da_factor_side& x = s1[g0 + q];
       const da_factor_side& y = s2[g0 + q];
-      const int64_t tr = (x.tokens + kBM - 1) / kBM, tc = (y.tokens + kBN - 1) / kBN;
+      const int64_t tr = (x.tokens + plan.tile_r - 1) / plan.tile_r, tc = (y.tokens + plan.tile_c - 1) / plan.tile_c;
       GroupDev& G = ga.grp[ga.n_groups++];
       G.a1 = (const char*)x.act;
       G.g1 = (const char*)x.grad;
@@ -1181,10 +1267,18 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
     rc = check_launch("da_ghost_gram_grouped(spans)");
     if (rc) return rc;
     if (tiles > 0) {
-      switch (dtype) {
-        case DA_BF16: ghost_grouped_tiles<DA_BF16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
-        case DA_F16: ghost_grouped_tiles<DA_F16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
-        default: ghost_grouped_tiles<DA_F32><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+      if (plan.v2) {
+        switch (dtype) {
+          case DA_BF16: ghost_grouped_tiles_v2<DA_BF16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+          case DA_F16: ghost_grouped_tiles_v2<DA_F16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+          default: ghost_grouped_tiles_v2<DA_F32><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+        }
+      } else {
+        switch (dtype) {
+          case DA_BF16: ghost_grouped_tiles<DA_BF16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+          case DA_F16: ghost_grouped_tiles<DA_F16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+          default: ghost_grouped_tiles<DA_F32><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+        }
       }
       rc = check_launch("da_ghost_gram_grouped(tiles)");
       if (rc) return rc;
