@@ -191,6 +191,35 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t w, int64_t n) {
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *(u32x4*)p = v; }
 
+// ---------------------------------------------------------------------------
+// Buffer loads straight into LDS (gfx950: 16 bytes per lane).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) char lds_char;
+
+// One 16-byte-per-lane buffer load into LDS at lds_addr + 16 * lane (M0 holds
+// the wave-uniform LDS byte address).  Inline assembly, so the compiler does
+// not wait for every outstanding load before each LDS read (it cannot tell a
+// ring's stages apart); callers wait with explicit vmcnt counts.  An offset
+// at or past the resource's range reads zeros and touches no memory.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// A wave-uniform 16-byte value, forced into scalar registers.
+__device__ __forceinline__ u32x4 uniform4(u32x4 v) {
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane(v[0]), (uint32_t)__builtin_amdgcn_readfirstlane(v[1]),
+               (uint32_t)__builtin_amdgcn_readfirstlane(v[2]), (uint32_t)__builtin_amdgcn_readfirstlane(v[3])};
+}
+
 }  // namespace da
 
 // ---------------------------------------------------------------------------

@@ -434,26 +434,6 @@ static_assert(kSmem <= 160 * 1024, "LDS");
 // cycle serves (8 consecutive rows, one chunk) read 8 distinct bank groups.
 }  // namespace v2
 
-typedef __attribute__((address_space(3))) char lds_char;
-
-__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-
-// Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
-__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
-}
-
-__device__ __forceinline__ u32x4 uniform4(u32x4 v) {
-  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane(v[0]), (uint32_t)__builtin_amdgcn_readfirstlane(v[1]),
-               (uint32_t)__builtin_amdgcn_readfirstlane(v[2]), (uint32_t)__builtin_amdgcn_readfirstlane(v[3])};
-}
-
 // Operand sources of one tile: buffer resources of the four factors and, per
 // lane, the byte offset of the row each of its 12 DMA instructions loads
 // (kOob for rows past an end), for the activation and the gradient.

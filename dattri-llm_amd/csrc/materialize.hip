@@ -385,25 +385,6 @@ __device__ __forceinline__ int swz(int r) { return (r & 3) << 2; }
 }  // namespace trk
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) char lds_char;
-
-// One 16-byte-per-lane buffer load into LDS at lds_addr + 16 * lane (M0 holds
-// the wave-uniform LDS byte address).  Written as inline assembly because the
-// compiler, seeing an LDS write it cannot tell apart from the other stages,
-// would otherwise put a full vmcnt(0) wait in front of every LDS read and
-// serialize the ring; the kernel waits for these loads with explicit counts.
-__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-
-// Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
-__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
-}
 
 __device__ __forceinline__ u32x4 tr_frag(const lds_char* p0, const lds_char* p1) {
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p0);

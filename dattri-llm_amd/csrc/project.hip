@@ -189,6 +189,172 @@ __global__ __launch_bounds__(kThreads) void project_outer_kernel(OuterArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused projection + outer product, streaming form (the gfx950 path).
+//
+// A workgroup owns a 128-token chunk of one sample.  The factor rows and the
+// projection rows go HBM -> LDS by buffer loads with the LDS-direct bit (each
+// instruction 4 rows x 256 contiguous bytes) through a ring of three 48 KB
+// stages (128 factor rows + 64 projection rows, 256 bytes of width each), two
+// stages in flight; the activation stages (with P_in^T) run first, then the
+// gradient stages (with P_out^T), as one stream.  Each wave multiplies its 32
+// rows against the 64 projection rows with 16x16x32 MFMAs read from LDS.  A
+// 16-byte-chunk XOR swizzle by row (c ^ row % 16) keeps the fragment reads
+// conflict-free.  The two projected chunks (128 x 64 fp32 each) are parked in
+// LDS and contracted over the chunk's tokens.
+// ---------------------------------------------------------------------------
+namespace ps {
+constexpr int kTok = 128;                // tokens per workgroup
+constexpr int kRows = kTok + kCols;      // LDS rows per stage
+constexpr int kSB = 256;                 // bytes of width per row and stage
+constexpr int kStage = kRows * kSB;      // 48 KB
+constexpr int kNBuf = 3;                 // two stages in flight
+constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // 12 instructions per wave and stage
+constexpr uint32_t kOob = 0x80000000u;
+static_assert(kDma == 12, "vmcnt below assumes 12 instructions per wave and stage");
+static_assert(2 * kTok * kCols * 4 <= kNBuf * kStage, "parked chunks must fit the ring");
+}  // namespace ps
+
+struct OuterArgs2 {
+  OuterArgs o;
+  int64_t chunks2;  // 128-token chunks per sample
+};
+
+template <int DT>
+__global__ __launch_bounds__(kThreads, 1) void project_outer_stream(OuterArgs2 args) {
+  const OuterArgs& a = args.o;
+  __shared__ __attribute__((aligned(1024))) char smem[ps::kNBuf * ps::kStage];
+  lds_char* const L = (lds_char*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  const int64_t b = blockIdx.x / args.chunks2, chunk = blockIdx.x % args.chunks2;
+  const int64_t tok0 = chunk * ps::kTok;
+
+  // Stage st < na: activation rows with P_in^T; else gradient rows with P_out^T.
+  const int na = (int)((a.abytes + ps::kSB - 1) / ps::kSB);
+  const int nst = na + (int)((a.gbytes + ps::kSB - 1) / ps::kSB);
+  const u32x4 ra = uniform4(make_rsrc(a.a + b * a.a_bstride, 0x7fffffffu));
+  const u32x4 rg = uniform4(make_rsrc(a.g + b * a.g_bstride, 0x7fffffffu));
+  const u32x4 rpi = uniform4(make_rsrc(a.pin_t, 0x7fffffffu));
+  const u32x4 rpo = uniform4(make_rsrc(a.pout_t, 0x7fffffffu));
+  // DMA instruction j of this wave: rows 4*(12w + j) .. +3 (rows < 128 are
+  // factor rows, then projection rows); lane l -> row 4*(12w+j) + l/16, slot
+  // l%16 holding logical chunk (l%16) ^ (row%16).
+  uint32_t rof_x[ps::kDma], rof_p[ps::kDma], cb[ps::kDma];
+  uint32_t rof_xg[ps::kDma], rof_pg[ps::kDma];
+#pragma unroll
+  for (int j = 0; j < ps::kDma; ++j) {
+    const int row = 4 * (ps::kDma * wave + j) + (lane >> 4);
+    cb[j] = 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    const int64_t t = tok0 + row;
+    const int c = row - ps::kTok;
+    rof_x[j] = (row < ps::kTok && t < a.tokens) ? (uint32_t)(t * a.a_tstride) : ps::kOob;
+    rof_xg[j] = (row < ps::kTok && t < a.tokens) ? (uint32_t)(t * a.g_tstride) : ps::kOob;
+    rof_p[j] = (row >= ps::kTok && c < a.ka) ? (uint32_t)(c * a.pin_rstride) : ps::kOob;
+    rof_pg[j] = (row >= ps::kTok && c < a.kg) ? (uint32_t)(c * a.pout_rstride) : ps::kOob;
+  }
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const bool act = st < na;
+    const uint32_t koff = (uint32_t)(act ? st : st - na) * ps::kSB;
+    const int64_t wb = act ? a.abytes : a.gbytes;
+    const uint32_t m = act ? 0xffffffffu : 0u;
+    const uint32_t base = lds0 + (uint32_t)((st % ps::kNBuf) * ps::kStage + ps::kDma * uwave * 4 * ps::kSB);
+#pragma unroll
+    for (int j = 0; j < ps::kDma; ++j) {
+      const bool xrow = ps::kDma * uwave + j < ps::kTok / 4;  // uniform
+      const uint32_t mx = xrow ? 0xffffffffu : 0u;
+      u32x4 rs;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        rs[c] = (((ra[c] & m) | (rg[c] & ~m)) & mx) | (((rpi[c] & m) | (rpo[c] & ~m)) & ~mx);
+      const uint32_t rx = (rof_x[j] & m) | (rof_xg[j] & ~m), rp = (rof_p[j] & m) | (rof_pg[j] & ~m);
+      const uint32_t roff = (rx & mx) | (rp & ~mx);
+      const bool en = st < nst && roff != ps::kOob && (int64_t)(koff + cb[j]) < wb;
+      dma16(rs, base + (uint32_t)(j * 4 * ps::kSB), en ? roff + koff + cb[j] : ps::kOob);
+    }
+  };
+  auto sync = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  // Fragments: factor rows 32w + 16rb + l%16, projection rows 128 + 16cb + l%16;
+  // k-step ks reads logical chunk 4ks + l/16 in slot (4ks + l/16) ^ (l%16).
+  const int r16 = lane & 15, q = lane >> 4;
+  f32x4 pa[2][4], pg[2][4];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      pa[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      pg[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  auto compute = [&](const lds_char* sb, f32x4 (&acc)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int off = r16 * ps::kSB + (((4 * ks + q) ^ r16) << 4);
+      u32x4 xf[2], pf[4];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) xf[rb] = *(const u32x4*)(sb + (32 * wave + 16 * rb) * ps::kSB + off);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) pf[c] = *(const u32x4*)(sb + (ps::kTok + 16 * c) * ps::kSB + off);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) Mfma16<DT>::mma(acc[rb][c], xf[rb], pf[c]);
+    }
+  };
+
+  issue(0);
+  issue(1);
+  for (int st = 0; st < na; ++st) {
+    sync();
+    issue(st + 2);
+    compute(L + (st % ps::kNBuf) * ps::kStage, pa);
+  }
+  for (int st = na; st < nst; ++st) {
+    sync();
+    issue(st + 2);
+    compute(L + (st % ps::kNBuf) * ps::kStage, pg);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Park both projected chunks (tokens x 64 fp32) in the ring, then
+  // M[o][i] = sum_tok gp[tok][o] * ap[tok][i]: thread -> one o, 16 consecutive i.
+  float* ap = (float*)smem;
+  float* gp = ap + ps::kTok * kCols;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tok = 32 * wave + 16 * rb + acc16_row(e, lane);
+        const int col = 16 * c + acc16_col(lane);
+        const bool tv = tok0 + tok < a.tokens;
+        const float bias = (a.bias_in && col < a.ka && tv) ? a.bias_in[col] : 0.f;
+        ap[tok * kCols + col] = pa[rb][c][e] + bias;
+        gp[tok * kCols + col] = pg[rb][c][e];
+      }
+  __syncthreads();
+  const int o = tid >> 2, i0 = (tid & 3) * 16;
+  float mo[16];
+#pragma unroll
+  for (int x = 0; x < 16; ++x) mo[x] = 0.f;
+  for (int tok = 0; tok < ps::kTok; ++tok) {
+    const float gv = gp[tok * kCols + o];
+    const float* arow = ap + tok * kCols + i0;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) mo[x] += gv * arow[x];
+  }
+  if (o < a.kg) {
+    float* dst = a.partial + ((b * args.chunks2 + chunk) * a.kg + o) * a.ka;
+#pragma unroll
+    for (int x = 0; x < 16; ++x)
+      if (i0 + x < a.ka) dst[i0 + x] = mo[x];
+  }
+}
+
 template <int OT>
 __global__ void project_outer_reduce(const float* __restrict__ partial, int64_t batch, int64_t chunks,
                                      int64_t width, char* out, int64_t out_bstride) {
@@ -317,13 +483,33 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
   o.bias_in = bias_in;
   o.chunks = (tokens + kRows - 1) / kRows;
   o.partial = (float*)workspace;
-  const int64_t blocks = batch * o.chunks;
-  if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
   hipStream_t st = (hipStream_t)stream;
-  switch (dtype) {
-    case DA_BF16: project_outer_kernel<DA_BF16><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
-    case DA_F16: project_outer_kernel<DA_F16><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
-    default: project_outer_kernel<DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+  // The streaming kernel addresses a sample's rows and the projection rows
+  // with 32-bit buffer offsets.
+  const int64_t span_a = tokens * o.a_tstride + o.abytes, span_g = tokens * o.g_tstride + o.gbytes;
+  const int64_t span_p = kCols * (o.pin_rstride > o.pout_rstride ? o.pin_rstride : o.pout_rstride);
+  const bool stream_ok = o.a_tstride >= 0 && o.g_tstride >= 0 && span_a < (1LL << 31) - (1LL << 20) &&
+                         span_g < (1LL << 31) - (1LL << 20) && span_p < (1LL << 31) - (1LL << 20);
+  if (stream_ok) {
+    OuterArgs2 o2;
+    o2.o = o;
+    o2.chunks2 = (tokens + ps::kTok - 1) / ps::kTok;
+    o.chunks = o2.chunks2;  // the reduce below sums these chunks
+    const int64_t blocks = batch * o2.chunks2;
+    if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+    switch (dtype) {
+      case DA_BF16: project_outer_stream<DA_BF16><<<(unsigned)blocks, kThreads, 0, st>>>(o2); break;
+      case DA_F16: project_outer_stream<DA_F16><<<(unsigned)blocks, kThreads, 0, st>>>(o2); break;
+      default: project_outer_stream<DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(o2); break;
+    }
+  } else {
+    const int64_t blocks = batch * o.chunks;
+    if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+    switch (dtype) {
+      case DA_BF16: project_outer_kernel<DA_BF16><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+      case DA_F16: project_outer_kernel<DA_F16><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+      default: project_outer_kernel<DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(o); break;
+    }
   }
   rc = check_launch("da_project_outer(chunks)");
   if (rc) return rc;

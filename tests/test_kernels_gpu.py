@@ -193,3 +193,38 @@ def test_score_gemm_blocked_operands(device, dtype):
     assert rel_err(got.cpu().numpy(), oracle.score_gemm(m1s, m2s)) <= TOL[dtype]
     got_t = kernels.score_gemm([(q, p) for p, q in pairs])  # transposed launch (B1 > B2)
     assert rel_err(got_t.cpu().numpy(), oracle.score_gemm(m2s, m1s)) <= TOL[dtype]
+
+
+PROJ_CASES = [
+    # (b, t, k, d, ka, kg, bias, dtype, seq_first)
+    (3, 300, 200, 136, 24, 40, True, torch.bfloat16, False),   # 3 chunks, ragged; widths not whole stages
+    (2, 128, 4096, 1024, 64, 64, False, torch.bfloat16, False),
+    (2, 77, 100, 36, 64, 16, True, torch.float32, False),      # fp32 rows
+    (3, 50, 512, 264, 32, 64, False, torch.bfloat16, True),    # sequence-first captures (token stride B*width)
+]
+
+
+@pytest.mark.parametrize("case", PROJ_CASES)
+def test_project_outer_kernel(device, case):
+    from dattri_llm_amd import kernels
+
+    b, t, k, d, ka, kg, bias, dtype, seq_first = case
+    print(f"project_outer case={case}", flush=True)
+    gen = torch.Generator().manual_seed(b * t + k)
+    if seq_first:
+        a = _rand(gen, t, b, k, dtype=dtype).transpose(0, 1)
+        g = _rand(gen, t, b, d, dtype=dtype).transpose(0, 1)
+    else:
+        a, g = _rand(gen, b, t, k, dtype=dtype), _rand(gen, b, t, d, dtype=dtype)
+    p_in = _rand(gen, k, ka, dtype=dtype, scale=k**-0.5)
+    p_out = _rand(gen, d, kg, dtype=dtype, scale=d**-0.5)
+    bias_in = torch.randn(ka, generator=gen) if bias else None
+    got = kernels.project_outer(a.to(device), g.to(device), p_in.t().contiguous().to(device),
+                                p_out.t().contiguous().to(device),
+                                bias_in=bias_in.to(device) if bias else None, out_dtype=torch.float32)
+    p_in_np = _np(p_in)
+    if bias:
+        p_in_np = np.concatenate([p_in_np, bias_in.double().numpy()[None, :]], axis=0)
+    want = oracle.project_outer(_np(a), _np(g), p_in_np, _np(p_out), bias=bias)
+    assert got.shape == (b, kg * ka)
+    assert rel_err(got.cpu().numpy(), want) <= TOL[dtype]
