@@ -190,109 +190,122 @@ __global__ __launch_bounds__(kThreads) void project_outer_kernel(OuterArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Fused projection + outer product, streaming form (the gfx950 path).
+// Streaming projection (the gfx950 path).
 //
-// A workgroup owns a 128-token chunk of one sample.  The factor rows and the
-// projection rows go HBM -> LDS by buffer loads with the LDS-direct bit (each
-// instruction 4 rows x 256 contiguous bytes) through a ring of three 48 KB
-// stages (128 factor rows + 64 projection rows, 256 bytes of width each), two
-// stages in flight; the activation stages (with P_in^T) run first, then the
-// gradient stages (with P_out^T), as one stream.  Each wave multiplies its 32
-// rows against the 64 projection rows with 16x16x32 MFMAs read from LDS.  A
-// 16-byte-chunk XOR swizzle by row (c ^ row % 16) keeps the fragment reads
-// conflict-free.  The two projected chunks (128 x 64 fp32 each) are parked in
-// LDS and contracted over the chunk's tokens.
+// project_rows_stream: out[b, t, c] = sum_j x[b, t, j] * P[j, c] (+ bias[c])
+// for up to kMaxPGroups (x, P) pairs in one launch -- the activation and the
+// gradient side of a fused capture share a launch, so the two row streams
+// (of different widths) pack the GPU together, widest first.
+//
+// A workgroup owns a 128-token chunk of one sample of one group.  Factor rows
+// and projection rows go HBM -> LDS by buffer loads with the LDS-direct bit
+// (each instruction 4 rows x 256 contiguous bytes) through a ring of three
+// 48 KB stages (128 factor rows + 64 projection rows, 256 bytes of width
+// each), two stages in flight.  Each wave multiplies its 32 rows against the
+// 64 projection rows with 16x16x32 MFMAs read from LDS; a 16-byte-chunk XOR
+// swizzle by row (c ^ row % 16) keeps those reads conflict-free.  The chunk's
+// results are staged through LDS and leave as 16-byte row stores.
 // ---------------------------------------------------------------------------
 namespace ps {
 constexpr int kTok = 128;                // tokens per workgroup
 constexpr int kRows = kTok + kCols;      // LDS rows per stage
-constexpr int kSB = 256;                 // bytes of width per row and stage
-constexpr int kStage = kRows * kSB;      // 48 KB
-constexpr int kNBuf = 3;                 // two stages in flight
-constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // 12 instructions per wave and stage
+constexpr int kSB = 128;                 // bytes of width per row and stage (two 64-byte k-steps)
+constexpr int kStage = kRows * kSB;      // 24 KB
+constexpr int kNBuf = 6;                 // five stages in flight
+constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // 6 instructions per wave and stage
+constexpr int kKs = kSB / 64;            // 16x16x32 k-steps per stage
 constexpr uint32_t kOob = 0x80000000u;
-static_assert(kDma == 12, "vmcnt below assumes 12 instructions per wave and stage");
-static_assert(2 * kTok * kCols * 4 <= kNBuf * kStage, "parked chunks must fit the ring");
+constexpr int kMaxPGroups = 4;
+static_assert(kDma == 6 && kNBuf == 6, "the vmcnt wait below is 6 * (kNBuf - 2) = 24");
+static_assert(2 * kTok * 64 * 4 <= kNBuf * kStage, "output staging must fit the ring");
 }  // namespace ps
 
-struct OuterArgs2 {
-  OuterArgs o;
-  int64_t chunks2;  // 128-token chunks per sample
+struct PGroup {
+  const char* x;                // factor rows: sample b, token t at x + b*bstride + t*tstride
+  int64_t batch, tokens, bstride, tstride, wbytes;  // bytes
+  const char* pt;               // (ncols, width) transposed projection, rows pt_rstride bytes apart
+  int64_t pt_rstride;
+  int ncols;                    // <= 64
+  const float* bias;            // ncols floats or nullptr
+  char* out;                    // out + (b*out_bstride + t*out_tstride + c) elements
+  int64_t out_bstride, out_tstride;
+  int64_t chunks;               // 128-token chunks per sample
+  int64_t wg0;                  // first workgroup of this group
 };
 
-template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void project_outer_stream(OuterArgs2 args) {
-  const OuterArgs& a = args.o;
+struct PGroupArgs {
+  PGroup g[ps::kMaxPGroups];
+  int n;
+};
+
+template <int DT, int OT>
+__global__ __launch_bounds__(kThreads, 1) void project_rows_stream(PGroupArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[ps::kNBuf * ps::kStage];
   lds_char* const L = (lds_char*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
-  const int64_t b = blockIdx.x / args.chunks2, chunk = blockIdx.x % args.chunks2;
+  // Dispatch order, not an XCD-contiguous remap: the widest group comes
+  // first and every XCD should take its share of it.
+  const int64_t wg = blockIdx.x;
+  int gi = 0;
+  while (gi + 1 < args.n && args.g[gi + 1].wg0 <= wg) ++gi;
+  const PGroup& G = args.g[gi];
+  const int64_t local = wg - G.wg0;
+  const int64_t b = local / G.chunks, chunk = local % G.chunks;
   const int64_t tok0 = chunk * ps::kTok;
-
-  // Stage st < na: activation rows with P_in^T; else gradient rows with P_out^T.
-  const int na = (int)((a.abytes + ps::kSB - 1) / ps::kSB);
-  const int nst = na + (int)((a.gbytes + ps::kSB - 1) / ps::kSB);
-  const u32x4 ra = uniform4(make_rsrc(a.a + b * a.a_bstride, 0x7fffffffu));
-  const u32x4 rg = uniform4(make_rsrc(a.g + b * a.g_bstride, 0x7fffffffu));
-  const u32x4 rpi = uniform4(make_rsrc(a.pin_t, 0x7fffffffu));
-  const u32x4 rpo = uniform4(make_rsrc(a.pout_t, 0x7fffffffu));
-  // DMA instruction j of this wave: rows 4*(12w + j) .. +3 (rows < 128 are
-  // factor rows, then projection rows); lane l -> row 4*(12w+j) + l/16, slot
-  // l%16 holding logical chunk (l%16) ^ (row%16).
-  uint32_t rof_x[ps::kDma], rof_p[ps::kDma], cb[ps::kDma];
-  uint32_t rof_xg[ps::kDma], rof_pg[ps::kDma];
+  const int nst = (int)((G.wbytes + ps::kSB - 1) / ps::kSB);
+  const u32x4 rx = uniform4(make_rsrc(G.x + b * G.bstride, 0x7fffffffu));
+  const u32x4 rp = uniform4(make_rsrc(G.pt, 0x7fffffffu));
+  // DMA instruction j of this wave: rows 8*(6w + j) .. +7 (rows < 128 are
+  // factor rows, then projection rows); lane l -> row 8*(6w+j) + l/8, slot l%8
+  // holding logical chunk (l%8) ^ (row%8).
+  uint32_t rof[ps::kDma], cb[ps::kDma];
 #pragma unroll
   for (int j = 0; j < ps::kDma; ++j) {
-    const int row = 4 * (ps::kDma * wave + j) + (lane >> 4);
-    cb[j] = 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    const int row = 8 * (ps::kDma * wave + j) + (lane >> 3);
+    cb[j] = 16u * (uint32_t)((lane & 7) ^ (row & 7));
     const int64_t t = tok0 + row;
     const int c = row - ps::kTok;
-    rof_x[j] = (row < ps::kTok && t < a.tokens) ? (uint32_t)(t * a.a_tstride) : ps::kOob;
-    rof_xg[j] = (row < ps::kTok && t < a.tokens) ? (uint32_t)(t * a.g_tstride) : ps::kOob;
-    rof_p[j] = (row >= ps::kTok && c < a.ka) ? (uint32_t)(c * a.pin_rstride) : ps::kOob;
-    rof_pg[j] = (row >= ps::kTok && c < a.kg) ? (uint32_t)(c * a.pout_rstride) : ps::kOob;
+    rof[j] = row < ps::kTok ? (t < G.tokens ? (uint32_t)(t * G.tstride) : ps::kOob)
+                            : (c < G.ncols ? (uint32_t)(c * G.pt_rstride) : ps::kOob);
   }
   auto issue = [&](int st) __attribute__((always_inline)) {
-    const bool act = st < na;
-    const uint32_t koff = (uint32_t)(act ? st : st - na) * ps::kSB;
-    const int64_t wb = act ? a.abytes : a.gbytes;
-    const uint32_t m = act ? 0xffffffffu : 0u;
-    const uint32_t base = lds0 + (uint32_t)((st % ps::kNBuf) * ps::kStage + ps::kDma * uwave * 4 * ps::kSB);
+    const uint32_t koff = (uint32_t)st * ps::kSB;
+    const uint32_t base = lds0 + (uint32_t)((st % ps::kNBuf) * ps::kStage + ps::kDma * uwave * 8 * ps::kSB);
 #pragma unroll
     for (int j = 0; j < ps::kDma; ++j) {
-      const bool xrow = ps::kDma * uwave + j < ps::kTok / 4;  // uniform
+      const bool xrow = ps::kDma * uwave + j < ps::kTok / 8;  // uniform
       const uint32_t mx = xrow ? 0xffffffffu : 0u;
       u32x4 rs;
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        rs[c] = (((ra[c] & m) | (rg[c] & ~m)) & mx) | (((rpi[c] & m) | (rpo[c] & ~m)) & ~mx);
-      const uint32_t rx = (rof_x[j] & m) | (rof_xg[j] & ~m), rp = (rof_p[j] & m) | (rof_pg[j] & ~m);
-      const uint32_t roff = (rx & mx) | (rp & ~mx);
-      const bool en = st < nst && roff != ps::kOob && (int64_t)(koff + cb[j]) < wb;
-      dma16(rs, base + (uint32_t)(j * 4 * ps::kSB), en ? roff + koff + cb[j] : ps::kOob);
+      for (int c = 0; c < 4; ++c) rs[c] = (rx[c] & mx) | (rp[c] & ~mx);
+      const bool en = st < nst && rof[j] != ps::kOob && (int64_t)(koff + cb[j]) < G.wbytes;
+      dma16(rs, base + (uint32_t)(j * 8 * ps::kSB), en ? rof[j] + koff + cb[j] : ps::kOob);
     }
   };
-  auto sync = [&]() __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  };
 
-  // Fragments: factor rows 32w + 16rb + l%16, projection rows 128 + 16cb + l%16;
-  // k-step ks reads logical chunk 4ks + l/16 in slot (4ks + l/16) ^ (l%16).
+  // Fragments: factor rows 32w + 16rb + l%16, projection rows 128 + 16c + l%16;
+  // k-step ks reads logical chunk 4ks + l/16 in slot (4ks + l/16) ^ (row%8),
+  // row%8 = l%8: the 8 lanes one LDS cycle serves hit 8 distinct slots.
   const int r16 = lane & 15, q = lane >> 4;
-  f32x4 pa[2][4], pg[2][4];
+  f32x4 acc[2][4];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      pa[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-      pg[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  auto compute = [&](const lds_char* sb, f32x4 (&acc)[2][4]) __attribute__((always_inline)) {
+    for (int c = 0; c < 4; ++c) acc[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int off = r16 * ps::kSB + (((4 * ks + q) ^ r16) << 4);
+  for (int s0 = 0; s0 < ps::kNBuf - 1; ++s0) issue(s0);
+  for (int st = 0; st < nst; ++st) {
+    // this wave's loads of stage st done (the later kNBuf - 2 stages, 24
+    // instructions, may be in flight), its LDS reads done; then every wave's
+    // part is visible and the buffer read one stage ago may be refilled
+    asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(st + ps::kNBuf - 1);
+    const lds_char* sb = L + (st % ps::kNBuf) * ps::kStage;
+#pragma unroll
+    for (int ks = 0; ks < ps::kKs; ++ks) {
+      const int off = r16 * ps::kSB + (((4 * ks + q) ^ (r16 & 7)) << 4);
       u32x4 xf[2], pf[4];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) xf[rb] = *(const u32x4*)(sb + (32 * wave + 16 * rb) * ps::kSB + off);
@@ -303,26 +316,13 @@ __global__ __launch_bounds__(kThreads, 1) void project_outer_stream(OuterArgs2 a
 #pragma unroll
         for (int c = 0; c < 4; ++c) Mfma16<DT>::mma(acc[rb][c], xf[rb], pf[c]);
     }
-  };
-
-  issue(0);
-  issue(1);
-  for (int st = 0; st < na; ++st) {
-    sync();
-    issue(st + 2);
-    compute(L + (st % ps::kNBuf) * ps::kStage, pa);
-  }
-  for (int st = na; st < nst; ++st) {
-    sync();
-    issue(st + 2);
-    compute(L + (st % ps::kNBuf) * ps::kStage, pg);
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  // Park both projected chunks (tokens x 64 fp32) in the ring, then
-  // M[o][i] = sum_tok gp[tok][o] * ap[tok][i]: thread -> one o, 16 consecutive i.
-  float* ap = (float*)smem;
-  float* gp = ap + ps::kTok * kCols;
+  // Stage the chunk (128 x 64, output dtype) in the ring, then 16-byte stores.
+  constexpr int OS = Elem<OT>::kBytes;
+  constexpr int ROWB = kCols * OS;
+  char* obuf = smem;
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -331,28 +331,71 @@ __global__ __launch_bounds__(kThreads, 1) void project_outer_stream(OuterArgs2 a
       for (int e = 0; e < 4; ++e) {
         const int tok = 32 * wave + 16 * rb + acc16_row(e, lane);
         const int col = 16 * c + acc16_col(lane);
-        const bool tv = tok0 + tok < a.tokens;
-        const float bias = (a.bias_in && col < a.ka && tv) ? a.bias_in[col] : 0.f;
-        ap[tok * kCols + col] = pa[rb][c][e] + bias;
-        gp[tok * kCols + col] = pg[rb][c][e];
+        const float bias = (G.bias && col < G.ncols) ? G.bias[col] : 0.f;
+        Elem<OT>::store(obuf, (int64_t)tok * kCols + col, acc[rb][c][e] + bias);
       }
   __syncthreads();
+  constexpr int CH = ROWB / 16;
+  const int64_t wcols = G.ncols;
+  for (int idx = tid; idx < ps::kTok * CH; idx += kThreads) {
+    const int tok = idx / CH, ch = idx % CH;
+    const int64_t t = tok0 + tok;
+    const int64_t c0 = (int64_t)ch * (16 / OS);
+    if (t >= G.tokens || c0 >= wcols) continue;
+    char* dst = G.out + (b * G.out_bstride + t * G.out_tstride + c0) * OS;
+    const char* src = obuf + tok * ROWB + ch * 16;
+    if (c0 + 16 / OS <= wcols && ((uintptr_t)dst & 15) == 0) {
+      st16(dst, ld16(src));
+    } else {
+      for (int64_t c = c0; c < wcols && c < c0 + 16 / OS; ++c)
+        for (int by = 0; by < OS; ++by) dst[(c - c0) * OS + by] = src[(c - c0) * OS + by];
+    }
+  }
+}
+
+// M[b, o*ka + i] = sum_t gp[b, t, o] * ap[b, t, i] from the fp32 projected rows
+// (64 columns per row): one workgroup per sample, 128 tokens at a time through
+// LDS; thread -> one o, 16 consecutive i; tokens summed in order.
+template <int OT>
+__global__ __launch_bounds__(kThreads) void outer_from_projected(const float* __restrict__ ap,
+                                                                 const float* __restrict__ gp, int64_t tokens,
+                                                                 int ka, int kg, char* out, int64_t out_bstride) {
+  __shared__ float sa[ps::kTok * kCols], sg[ps::kTok * kCols];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const float* a0 = ap + b * tokens * kCols;
+  const float* g0 = gp + b * tokens * kCols;
   const int o = tid >> 2, i0 = (tid & 3) * 16;
   float mo[16];
 #pragma unroll
   for (int x = 0; x < 16; ++x) mo[x] = 0.f;
-  for (int tok = 0; tok < ps::kTok; ++tok) {
-    const float gv = gp[tok * kCols + o];
-    const float* arow = ap + tok * kCols + i0;
+  for (int64_t t0 = 0; t0 < tokens; t0 += ps::kTok) {
+    const int n = (int)min((int64_t)ps::kTok, tokens - t0);
+    __syncthreads();
+    for (int idx = tid; idx < n * kCols / 4; idx += kThreads) {
+      ((f32x4*)sa)[idx] = ((const f32x4*)(a0 + t0 * kCols))[idx];
+      ((f32x4*)sg)[idx] = ((const f32x4*)(g0 + t0 * kCols))[idx];
+    }
+    __syncthreads();
+    for (int t = 0; t < n; ++t) {
+      const float gv = sg[t * kCols + o];
+      const float* arow = sa + t * kCols + i0;
 #pragma unroll
-    for (int x = 0; x < 16; ++x) mo[x] += gv * arow[x];
+      for (int x = 0; x < 16; ++x) mo[x] += gv * arow[x];
+    }
   }
-  if (o < a.kg) {
-    float* dst = a.partial + ((b * args.chunks2 + chunk) * a.kg + o) * a.ka;
+  if (o < kg) {
 #pragma unroll
     for (int x = 0; x < 16; ++x)
-      if (i0 + x < a.ka) dst[i0 + x] = mo[x];
+      if (i0 + x < ka) Elem<OT>::store(out, b * out_bstride + (int64_t)o * ka + i0 + x, mo[x]);
   }
+}
+
+// The streaming kernel addresses a sample's rows and the projection rows with
+// 32-bit buffer offsets.
+bool stream_fits(int64_t tokens, int64_t tstride_b, int64_t wbytes, int64_t pt_rstride_b) {
+  const int64_t lim = (1LL << 31) - (1LL << 20);
+  return tstride_b >= 0 && tokens * tstride_b + wbytes < lim && kCols * pt_rstride_b + wbytes < lim;
 }
 
 template <int OT>
@@ -404,10 +447,45 @@ int da_project_rows(const void* x, int dtype, int64_t rows, int64_t d, int64_t x
   a.bias = bias;
   a.out = (char*)out;
   a.out_rstride = out_rstride;
+  hipStream_t st = (hipStream_t)stream;
+  if (k <= kCols && stream_fits(rows, a.x_rstride, a.wbytes, a.pt_rstride)) {
+    PGroupArgs pa;
+    pa.n = 1;
+    PGroup& G = pa.g[0];
+    G.x = a.x;
+    G.batch = 1;
+    G.tokens = rows;
+    G.bstride = 0;
+    G.tstride = a.x_rstride;
+    G.wbytes = a.wbytes;
+    G.pt = a.pt;
+    G.pt_rstride = a.pt_rstride;
+    G.ncols = (int)k;
+    G.bias = bias;
+    G.out = (char*)out;
+    G.out_bstride = 0;
+    G.out_tstride = out_rstride;
+    G.chunks = (rows + ps::kTok - 1) / ps::kTok;
+    G.wg0 = 0;
+    if (G.chunks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+    const unsigned blocks = (unsigned)G.chunks;
+#define DA_PRS(DT)                                                                            \
+    switch (out_dtype) {                                                                      \
+      case DA_F32: project_rows_stream<DT, DA_F32><<<blocks, kThreads, 0, st>>>(pa); break;   \
+      case DA_BF16: project_rows_stream<DT, DA_BF16><<<blocks, kThreads, 0, st>>>(pa); break; \
+      default: project_rows_stream<DT, DA_F16><<<blocks, kThreads, 0, st>>>(pa); break;       \
+    }
+    switch (dtype) {
+      case DA_BF16: DA_PRS(DA_BF16) break;
+      case DA_F16: DA_PRS(DA_F16) break;
+      default: DA_PRS(DA_F32) break;
+    }
+#undef DA_PRS
+    return check_launch(who);
+  }
   const int64_t gx = (rows + kRows - 1) / kRows, gy = (k + kCols - 1) / kCols;
   if (gx > 0x7fffffffLL || gy > 65535) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
   dim3 grid((unsigned)gx, (unsigned)gy);
-  hipStream_t st = (hipStream_t)stream;
 #define DA_PR(DT)                                                                           \
   switch (out_dtype) {                                                                      \
     case DA_F32: project_rows_kernel<DT, DA_F32><<<grid, kThreads, 0, st>>>(a); break;      \
@@ -427,7 +505,10 @@ int da_project_outer_workspace(int64_t batch, int64_t tokens, int64_t ka, int64_
   if (batch < 0 || tokens < 0 || ka < 0 || kg < 0 || !bytes)
     return da::set_error(DA_ERR_INVALID, "da_project_outer_workspace: bad arguments");
   const int64_t chunks = (tokens + da::kRows - 1) / da::kRows;
-  *bytes = (size_t)(batch * chunks * ka * kg) * sizeof(float);
+  const size_t partials = (size_t)(batch * chunks * ka * kg) * sizeof(float);
+  // the streaming path parks both projected sides, (B, T, 64) fp32 each
+  const size_t projected = (size_t)(2 * batch * tokens * da::kCols) * sizeof(float);
+  *bytes = partials > projected ? partials : projected;
   return DA_OK;
 }
 
@@ -484,24 +565,51 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
   o.chunks = (tokens + kRows - 1) / kRows;
   o.partial = (float*)workspace;
   hipStream_t st = (hipStream_t)stream;
-  // The streaming kernel addresses a sample's rows and the projection rows
-  // with 32-bit buffer offsets.
-  const int64_t span_a = tokens * o.a_tstride + o.abytes, span_g = tokens * o.g_tstride + o.gbytes;
-  const int64_t span_p = kCols * (o.pin_rstride > o.pout_rstride ? o.pin_rstride : o.pout_rstride);
-  const bool stream_ok = o.a_tstride >= 0 && o.g_tstride >= 0 && span_a < (1LL << 31) - (1LL << 20) &&
-                         span_g < (1LL << 31) - (1LL << 20) && span_p < (1LL << 31) - (1LL << 20);
+  const bool stream_ok = stream_fits(tokens, o.a_tstride, o.abytes, o.pin_rstride) &&
+                         stream_fits(tokens, o.g_tstride, o.gbytes, o.pout_rstride);
   if (stream_ok) {
-    OuterArgs2 o2;
-    o2.o = o;
-    o2.chunks2 = (tokens + ps::kTok - 1) / ps::kTok;
-    o.chunks = o2.chunks2;  // the reduce below sums these chunks
-    const int64_t blocks = batch * o2.chunks2;
+    // Both sides projected in one launch (wider rows first), parked as fp32
+    // (B, T, 64) in the workspace, then contracted per sample.
+    float* ap = (float*)workspace;
+    float* gp = ap + batch * tokens * kCols;
+    PGroupArgs pa;
+    pa.n = 2;
+    const bool g_first = o.gbytes > o.abytes;
+    for (int side = 0; side < 2; ++side) {
+      PGroup& G = pa.g[g_first ? 1 - side : side];
+      const bool act = side == 0;
+      G.x = act ? o.a : o.g;
+      G.batch = batch;
+      G.tokens = tokens;
+      G.bstride = act ? o.a_bstride : o.g_bstride;
+      G.tstride = act ? o.a_tstride : o.g_tstride;
+      G.wbytes = act ? o.abytes : o.gbytes;
+      G.pt = act ? o.pin_t : o.pout_t;
+      G.pt_rstride = act ? o.pin_rstride : o.pout_rstride;
+      G.ncols = act ? o.ka : o.kg;
+      G.bias = act ? bias_in : nullptr;
+      G.out = (char*)(act ? ap : gp);
+      G.out_bstride = tokens * kCols;
+      G.out_tstride = kCols;
+      G.chunks = (tokens + ps::kTok - 1) / ps::kTok;
+    }
+    pa.g[0].wg0 = 0;
+    pa.g[1].wg0 = batch * pa.g[0].chunks;
+    const int64_t blocks = 2 * batch * pa.g[0].chunks;
     if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
     switch (dtype) {
-      case DA_BF16: project_outer_stream<DA_BF16><<<(unsigned)blocks, kThreads, 0, st>>>(o2); break;
-      case DA_F16: project_outer_stream<DA_F16><<<(unsigned)blocks, kThreads, 0, st>>>(o2); break;
-      default: project_outer_stream<DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(o2); break;
+      case DA_BF16: project_rows_stream<DA_BF16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(pa); break;
+      case DA_F16: project_rows_stream<DA_F16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(pa); break;
+      default: project_rows_stream<DA_F32, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(pa); break;
     }
+    rc = check_launch("da_project_outer(projection)");
+    if (rc) return rc;
+    switch (out_dtype) {
+      case DA_F32: outer_from_projected<DA_F32><<<(unsigned)batch, kThreads, 0, st>>>(ap, gp, tokens, o.ka, o.kg, (char*)out, out_bstride); break;
+      case DA_BF16: outer_from_projected<DA_BF16><<<(unsigned)batch, kThreads, 0, st>>>(ap, gp, tokens, o.ka, o.kg, (char*)out, out_bstride); break;
+      default: outer_from_projected<DA_F16><<<(unsigned)batch, kThreads, 0, st>>>(ap, gp, tokens, o.ka, o.kg, (char*)out, out_bstride); break;
+    }
+    return check_launch("da_project_outer(outer)");
   } else {
     const int64_t blocks = batch * o.chunks;
     if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
