@@ -208,6 +208,15 @@ __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t vo
                : "memory", "m0");
 }
 
+// The same with the non-temporal hint: for data read once (streamed factor
+// rows), so that it does not push data that is read again out of L2.
+__device__ __forceinline__ void dma16_nt(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
 __device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
   const uint64_t p = (uint64_t)base;
@@ -215,6 +224,11 @@ __device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
 }
 
 // A wave-uniform 16-byte value, forced into scalar registers.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ u32x4 uniform4(u32x4 v) {
   return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane(v[0]), (uint32_t)__builtin_amdgcn_readfirstlane(v[1]),
                (uint32_t)__builtin_amdgcn_readfirstlane(v[2]), (uint32_t)__builtin_amdgcn_readfirstlane(v[3])};

@@ -211,12 +211,12 @@ constexpr int kTok = 128;                // tokens per workgroup
 constexpr int kRows = kTok + kCols;      // LDS rows per stage
 constexpr int kSB = 128;                 // bytes of width per row and stage (two 64-byte k-steps)
 constexpr int kStage = kRows * kSB;      // 24 KB
-constexpr int kNBuf = 6;                 // five stages in flight
+constexpr int kNBuf = 3;                 // two stages in flight, two workgroups per CU
 constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // 6 instructions per wave and stage
 constexpr int kKs = kSB / 64;            // 16x16x32 k-steps per stage
 constexpr uint32_t kOob = 0x80000000u;
 constexpr int kMaxPGroups = 4;
-static_assert(kDma == 6 && kNBuf == 6, "the vmcnt wait below is 6 * (kNBuf - 2) = 24");
+static_assert(kDma == 6 && kNBuf == 3, "the vmcnt wait below is 6 * (kNBuf - 2) = 6");
 static_assert(2 * kTok * 64 * 4 <= kNBuf * kStage, "output staging must fit the ring");
 }  // namespace ps
 
@@ -239,7 +239,7 @@ struct PGroupArgs {
 };
 
 template <int DT, int OT>
-__global__ __launch_bounds__(kThreads, 1) void project_rows_stream(PGroupArgs args) {
+__global__ __launch_bounds__(kThreads, 2) void project_rows_stream(PGroupArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[ps::kNBuf * ps::kStage];
   lds_char* const L = (lds_char*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)L;
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kThreads, 1) void project_rows_stream(PGroupArgs ar
     // this wave's loads of stage st done (the later kNBuf - 2 stages, 24
     // instructions, may be in flight), its LDS reads done; then every wave's
     // part is visible and the buffer read one stage ago may be refilled
-    asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(st + ps::kNBuf - 1);
     const lds_char* sb = L + (st % ps::kNBuf) * ps::kStage;
 #pragma unroll
@@ -353,42 +353,271 @@ __global__ __launch_bounds__(kThreads, 1) void project_rows_stream(PGroupArgs ar
   }
 }
 
-// M[b, o*ka + i] = sum_t gp[b, t, o] * ap[b, t, i] from the fp32 projected rows
-// (64 columns per row): one workgroup per sample, 128 tokens at a time through
-// LDS; thread -> one o, 16 consecutive i; tokens summed in order.
+// Stream-K capture projection.  The work of da_project_outer is the stage
+// sequence (side, item, stage): side 0 = activations with P_in, side 1 =
+// gradients with P_out; an item is one 128-token chunk of one sample; a stage
+// is 128 bytes of feature width of the item's rows (plus the same bytes of the
+// 64 P^T rows).  Workgroup w of nwg owns stages [w*total/nwg, (w+1)*total/nwg)
+// and streams them through one DMA ring without draining it at item
+// boundaries; at the end of each item (or of its range) it writes its fp32
+// partial projection, a "piece", to slot item + w.  Along the stage sequence
+// every new piece advances the item, the workgroup or both, so item + w is
+// strictly increasing: slots are unique and < items + nwg.  The pieces of an
+// item are those of workgroups sk_owner(first stage) .. sk_owner(last stage);
+// outer_from_pieces sums them in that order, so the result does not depend on
+// timing.
+struct SkSide {
+  const char* x;                // sample b, token t at x + b*bstride + t*tstride (bytes)
+  int64_t bstride, tstride, wbytes;
+  const char* pt;               // (ncols, width) transposed projection
+  int64_t pt_rstride;
+  int ncols, nst;               // projected width (<= 64), stages per item
+  int64_t items, s0, i0;        // items of this side, its first stage, its first item
+  const float* bias;            // ncols floats added to this side's projected rows, or nullptr
+};
+
+struct SkArgs {
+  SkSide s[2];
+  int64_t tokens, chunks, total;  // tokens per sample, 128-token chunks, stages of both sides
+  int64_t nwg;
+  float* pieces;                // (items of both sides + nwg) pieces of kPieceFloats
+};
+
+constexpr int kPieceFloats = ps::kTok * kCols;  // one piece: 128 tokens x 64 columns, MFMA layout
+
+__device__ __forceinline__ int64_t sk_first(int64_t w, const SkArgs& a) { return w * a.total / a.nwg; }
+// the workgroup whose range holds stage x
+__device__ __forceinline__ int64_t sk_owner(int64_t x, const SkArgs& a) { return ((x + 1) * a.nwg - 1) / a.total; }
+
+template <int DT>
+__global__ __launch_bounds__(kThreads, 2) void project_pieces(SkArgs args) {
+  __shared__ __attribute__((aligned(1024))) char smem[ps::kNBuf * ps::kStage];
+  lds_char* const L = (lds_char*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  const int64_t w = blockIdx.x;
+  const int64_t sb = uniform64(sk_first(w, args));
+  const int nloc = __builtin_amdgcn_readfirstlane((int)(sk_first(w + 1, args) - sb));  // stages of this workgroup
+
+  // Issue cursor (side is, item ii, stage ik) and the DMA state of its item.
+  // DMA instruction j of this wave: j < 4 -> factor rows 32w + 8j .. +7
+  // (streamed once: non-temporal), j >= 4 -> projection rows 16w + 8(j-4) ..
+  // +7 (LDS rows 128 + ...); lane l -> row + l/8, slot l%8 holding logical
+  // chunk (l%8) ^ (row%8).
+  int is = sb >= args.s[1].s0 ? 1 : 0;
+  int64_t ii = uniform64((sb - args.s[is].s0) / args.s[is].nst);
+  int ik = __builtin_amdgcn_readfirstlane((int)(sb - args.s[is].s0 - ii * args.s[is].nst));
+  const int xs0 = is, xk0 = ik;
+  const int64_t xi0 = ii;
+  u32x4 rx, rp;
+  uint32_t wb, rof[ps::kDma], cb[ps::kDma];
+  int nst = 0;        // stages per item of the cursor's side
+  int64_t items = 0;  // items of the cursor's side
+  auto dma_row = [&](int j) __attribute__((always_inline)) {  // LDS row of instruction j, lane 0
+    return j < 4 ? 32 * uwave + 8 * j : ps::kTok + 16 * uwave + 8 * (j - 4);
+  };
+#pragma unroll
+  for (int j = 0; j < ps::kDma; ++j) {
+    const int row = dma_row(j) + (lane >> 3);
+    cb[j] = 16u * (uint32_t)((lane & 7) ^ (row & 7));
+  }
+  auto set_item = [&]() __attribute__((always_inline)) {
+    const SkSide& S = args.s[is];
+    const int64_t b = uniform64(ii / args.chunks), t0 = (ii - b * args.chunks) * ps::kTok;
+    rx = uniform4(make_rsrc(S.x + b * S.bstride + t0 * S.tstride, 0x7fffffffu));
+    rp = uniform4(make_rsrc(S.pt, 0x7fffffffu));
+    wb = (uint32_t)S.wbytes;
+    nst = S.nst;
+    items = S.items;
+    const int64_t nv = args.tokens - t0;  // valid rows of this chunk (may exceed 128)
+#pragma unroll
+    for (int j = 0; j < ps::kDma; ++j) {
+      const int row = dma_row(j) + (lane >> 3);
+      const int c = row - ps::kTok;
+      rof[j] = j < 4 ? (row < nv ? (uint32_t)(row * S.tstride) : ps::kOob)
+                     : (c < S.ncols ? (uint32_t)(c * S.pt_rstride) : ps::kOob);
+    }
+  };
+  // DMA of the cursor's stage into ring slot `slot` (zero fill when !live),
+  // then the cursor moves on.
+  auto issue = [&](int slot, bool live, bool more) __attribute__((always_inline)) {
+    const uint32_t koff = (uint32_t)ik * ps::kSB;
+    const uint32_t base = lds0 + (uint32_t)(slot * ps::kStage);
+#pragma unroll
+    for (int j = 0; j < ps::kDma; ++j) {
+      const bool en = live & (rof[j] != ps::kOob) & (koff + cb[j] < wb);
+      const uint32_t off = en ? rof[j] + koff + cb[j] : ps::kOob;
+      const uint32_t dst = base + (uint32_t)(dma_row(j) * ps::kSB);
+      if (j < 4)
+        dma16_nt(rx, dst, off);
+      else
+        dma16(rp, dst, off);
+    }
+    if (live && ++ik == nst) {
+      ik = 0;
+      if (++ii == items) {
+        ii = 0;
+        ++is;
+      }
+      if (more) set_item();
+    }
+  };
+
+  set_item();
+  int ix = 0;  // next stage to issue, relative to sb
+#pragma unroll
+  for (int p = 0; p < ps::kNBuf - 1; ++p, ++ix) issue(p, ix < nloc, ix + 1 < nloc);
+
+  // Fragments: factor rows 32w + 16rb + l%16, projection rows 128 + 16c + l%16;
+  // k-step ks reads logical chunk 4ks + l/16 in slot (4ks + l/16) ^ (row%8),
+  // row%8 = l%8: the 8 lanes one LDS cycle serves hit 8 distinct slots.
+  const int r16 = lane & 15, q = lane >> 4;
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int slot = 0, xs = xs0, xk = xk0, x = 0;
+  int64_t xi = xi0;
+  while (x < nloc) {
+    const int seg_end = min(nloc, x + (args.s[xs].nst - xk));
+    for (; x < seg_end; ++x, ++ix) {
+      // this wave's loads of stage x done (those of the next stage may be in
+      // flight; piece stores may be pending too, but loads complete in
+      // order), its LDS reads done; then every wave's part is visible and the
+      // slot read one stage ago may be refilled
+      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(slot == 0 ? ps::kNBuf - 1 : slot - 1, ix < nloc, ix + 1 < nloc);
+      const lds_char* sbuf = L + slot * ps::kStage;
+#pragma unroll
+      for (int ks = 0; ks < ps::kKs; ++ks) {
+        const int off = r16 * ps::kSB + (((4 * ks + q) ^ (r16 & 7)) << 4);
+        u32x4 xf[2], pf[4];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) xf[rb] = *(const u32x4*)(sbuf + (32 * wave + 16 * rb) * ps::kSB + off);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) pf[c] = *(const u32x4*)(sbuf + (ps::kTok + 16 * c) * ps::kSB + off);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) Mfma16<DT>::mma(acc[rb][c], xf[rb], pf[c]);
+      }
+      slot = slot + 1 == ps::kNBuf ? 0 : slot + 1;
+    }
+    // piece of item (xs, xi): lane-major MFMA layout, (wave, rb, c) blocks of 64 x 16 B
+    f32x4* dst = (f32x4*)(args.pieces + (args.s[xs].i0 + xi + w) * kPieceFloats) + wave * 8 * 64 + lane;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        dst[(rb * 4 + c) * 64] = acc[rb][c];
+        acc[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    xk = 0;
+    if (++xi == args.s[xs].items) {
+      xi = 0;
+      ++xs;
+    }
+  }
+  // the zero-filling DMAs past the range still write this workgroup's LDS
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// M[b, o*ka + i] = sum over chunks and tokens of gp[t, o] * ap[t, i], where
+// ap / gp are the summed pieces (plus the bias row on the activation side,
+// on valid tokens only).  One workgroup per sample; wave w contracts its 32
+// tokens of each chunk with fp32 16x16x4 MFMAs straight from the piece layout:
+// lane l holds tokens 4*(l/16) + r (r = 0..3) of column l%16 of each 16x16
+// block, so step r pairs MFMA k-slot l/16 with token 4*(l/16) + r on both
+// operands.  The four waves' sums are added in wave order.
 template <int OT>
-__global__ __launch_bounds__(kThreads) void outer_from_projected(const float* __restrict__ ap,
-                                                                 const float* __restrict__ gp, int64_t tokens,
-                                                                 int ka, int kg, char* out, int64_t out_bstride) {
-  __shared__ float sa[ps::kTok * kCols], sg[ps::kTok * kCols];
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int ka, int kg, char* out,
+                                                              int64_t out_bstride) {
+  __shared__ f32x4 red[4][16][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.x;
-  const float* a0 = ap + b * tokens * kCols;
-  const float* g0 = gp + b * tokens * kCols;
-  const int o = tid >> 2, i0 = (tid & 3) * 16;
-  float mo[16];
+  f32x4 m[4][4];
 #pragma unroll
-  for (int x = 0; x < 16; ++x) mo[x] = 0.f;
-  for (int64_t t0 = 0; t0 < tokens; t0 += ps::kTok) {
-    const int n = (int)min((int64_t)ps::kTok, tokens - t0);
-    __syncthreads();
-    for (int idx = tid; idx < n * kCols / 4; idx += kThreads) {
-      ((f32x4*)sa)[idx] = ((const f32x4*)(a0 + t0 * kCols))[idx];
-      ((f32x4*)sg)[idx] = ((const f32x4*)(g0 + t0 * kCols))[idx];
+  for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) m[ob][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t ch = 0; ch < args.chunks; ++ch) {
+    f32x4 v[2][2][4];  // side, rb, column block
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      const SkSide& S = args.s[side];
+      const int64_t il = b * args.chunks + ch;
+      const int64_t fs = S.s0 + il * S.nst;
+      const int64_t w0 = sk_owner(fs, args), w1 = sk_owner(fs + S.nst - 1, args);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[side][rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int64_t wq = w0; wq <= w1; ++wq) {
+        const f32x4* src = (const f32x4*)(args.pieces + (S.i0 + il + wq) * kPieceFloats) + wave * 8 * 64 + lane;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[side][rb][c] += src[(rb * 4 + c) * 64];
+      }
+      if (S.bias) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int col = 16 * c + (lane & 15);
+          const float bv = col < S.ncols ? S.bias[col] : 0.f;
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int64_t t = ch * ps::kTok + 32 * wave + 16 * rb + 4 * (lane >> 4) + r;
+              if (t < args.tokens) v[side][rb][c][r] += bv;
+            }
+        }
+      }
     }
-    __syncthreads();
-    for (int t = 0; t < n; ++t) {
-      const float gv = sg[t * kCols + o];
-      const float* arow = sa + t * kCols + i0;
 #pragma unroll
-      for (int x = 0; x < 16; ++x) mo[x] += gv * arow[x];
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+          for (int ib = 0; ib < 4; ++ib)
+            m[ob][ib] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[1][rb][ob][r], v[0][rb][ib][r], m[ob][ib], 0, 0, 0);
+  }
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) red[wave][ob * 4 + ib][lane] = m[ob][ib];
+  __syncthreads();
+  for (int idx = tid; idx < 16 * 64; idx += kThreads) {
+    const int blk = idx >> 6, ln = idx & 63;
+    const f32x4 sum = red[0][blk][ln] + red[1][blk][ln] + red[2][blk][ln] + red[3][blk][ln];
+    const int i = 16 * (blk & 3) + (ln & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = 16 * (blk >> 2) + 4 * (ln >> 4) + r;
+      if (o < kg && i < ka) Elem<OT>::store(out, b * out_bstride + (int64_t)o * ka + i, sum[r]);
     }
   }
-  if (o < kg) {
-#pragma unroll
-    for (int x = 0; x < 16; ++x)
-      if (i0 + x < ka) Elem<OT>::store(out, b * out_bstride + (int64_t)o * ka + i0 + x, mo[x]);
+}
+
+// Workgroup slots of the stream-K launch on the current device: two per CU.
+int sk_slots(int64_t* n) {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "hipGetDevice failed");
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+    *n = cache[dev];
+    return DA_OK;
   }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
+  if (dev >= 0 && dev < 64) cache[dev] = 2 * cus;
+  *n = 2 * cus;
+  return DA_OK;
 }
 
 // The streaming kernel addresses a sample's rows and the projection rows with
@@ -396,6 +625,13 @@ __global__ __launch_bounds__(kThreads) void outer_from_projected(const float* __
 bool stream_fits(int64_t tokens, int64_t tstride_b, int64_t wbytes, int64_t pt_rstride_b) {
   const int64_t lim = (1LL << 31) - (1LL << 20);
   return tstride_b >= 0 && tokens * tstride_b + wbytes < lim && kCols * pt_rstride_b + wbytes < lim;
+}
+
+// The stream-K kernel addresses one 128-token chunk and the projection rows
+// with 32-bit buffer offsets.
+bool sk_fits(int64_t tstride_b, int64_t wbytes, int64_t pt_rstride_b) {
+  const int64_t lim = (1LL << 31) - (1LL << 20);
+  return tstride_b >= 0 && ps::kTok * tstride_b + wbytes < lim && kCols * pt_rstride_b + wbytes < lim;
 }
 
 template <int OT>
@@ -506,9 +742,13 @@ int da_project_outer_workspace(int64_t batch, int64_t tokens, int64_t ka, int64_
     return da::set_error(DA_ERR_INVALID, "da_project_outer_workspace: bad arguments");
   const int64_t chunks = (tokens + da::kRows - 1) / da::kRows;
   const size_t partials = (size_t)(batch * chunks * ka * kg) * sizeof(float);
-  // the streaming path parks both projected sides, (B, T, 64) fp32 each
-  const size_t projected = (size_t)(2 * batch * tokens * da::kCols) * sizeof(float);
-  *bytes = partials > projected ? partials : projected;
+  // the stream-K path keeps one fp32 piece per (item, workgroup) boundary
+  int64_t slots = 0;
+  const int rc = da::sk_slots(&slots);
+  if (rc) return rc;
+  const int64_t items = 2 * batch * ((tokens + da::ps::kTok - 1) / da::ps::kTok);
+  const size_t pieces = (size_t)(items + slots) * da::kPieceFloats * sizeof(float);
+  *bytes = partials > pieces ? partials : pieces;
   return DA_OK;
 }
 
@@ -565,49 +805,52 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
   o.chunks = (tokens + kRows - 1) / kRows;
   o.partial = (float*)workspace;
   hipStream_t st = (hipStream_t)stream;
-  const bool stream_ok = stream_fits(tokens, o.a_tstride, o.abytes, o.pin_rstride) &&
-                         stream_fits(tokens, o.g_tstride, o.gbytes, o.pout_rstride);
+  const bool stream_ok = sk_fits(o.a_tstride, o.abytes, o.pin_rstride) && sk_fits(o.g_tstride, o.gbytes, o.pout_rstride);
   if (stream_ok) {
-    // Both sides projected in one launch (wider rows first), parked as fp32
-    // (B, T, 64) in the workspace, then contracted per sample.
-    float* ap = (float*)workspace;
-    float* gp = ap + batch * tokens * kCols;
-    PGroupArgs pa;
-    pa.n = 2;
-    const bool g_first = o.gbytes > o.abytes;
+    // Stream-K projection of both sides into fp32 pieces, then the per-sample
+    // contraction.
+    SkArgs sk;
+    sk.tokens = tokens;
+    sk.chunks = (tokens + ps::kTok - 1) / ps::kTok;
+    sk.pieces = (float*)workspace;
+    int64_t s0 = 0;
     for (int side = 0; side < 2; ++side) {
-      PGroup& G = pa.g[g_first ? 1 - side : side];
+      SkSide& S = sk.s[side];
       const bool act = side == 0;
-      G.x = act ? o.a : o.g;
-      G.batch = batch;
-      G.tokens = tokens;
-      G.bstride = act ? o.a_bstride : o.g_bstride;
-      G.tstride = act ? o.a_tstride : o.g_tstride;
-      G.wbytes = act ? o.abytes : o.gbytes;
-      G.pt = act ? o.pin_t : o.pout_t;
-      G.pt_rstride = act ? o.pin_rstride : o.pout_rstride;
-      G.ncols = act ? o.ka : o.kg;
-      G.bias = act ? bias_in : nullptr;
-      G.out = (char*)(act ? ap : gp);
-      G.out_bstride = tokens * kCols;
-      G.out_tstride = kCols;
-      G.chunks = (tokens + ps::kTok - 1) / ps::kTok;
+      S.x = act ? o.a : o.g;
+      S.bstride = act ? o.a_bstride : o.g_bstride;
+      S.tstride = act ? o.a_tstride : o.g_tstride;
+      S.wbytes = act ? o.abytes : o.gbytes;
+      S.pt = act ? o.pin_t : o.pout_t;
+      S.pt_rstride = act ? o.pin_rstride : o.pout_rstride;
+      S.ncols = act ? o.ka : o.kg;
+      S.nst = (int)((S.wbytes + ps::kSB - 1) / ps::kSB);
+      S.items = batch * sk.chunks;
+      S.s0 = s0;
+      S.i0 = side * S.items;
+      S.bias = act ? bias_in : nullptr;
+      if (S.nst == 0) return set_error(DA_ERR_INVALID, "%s: K and D must be >= 1", who);
+      s0 += S.items * S.nst;
     }
-    pa.g[0].wg0 = 0;
-    pa.g[1].wg0 = batch * pa.g[0].chunks;
-    const int64_t blocks = 2 * batch * pa.g[0].chunks;
-    if (blocks > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+    sk.total = s0;
+    int64_t slots = 0;
+    rc = sk_slots(&slots);
+    if (rc) return rc;
+    sk.nwg = slots < sk.total ? slots : sk.total;
+    if (sk.total / sk.nwg > (1LL << 30) || batch > 0x7fffffffLL)
+      return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+    const unsigned blocks = (unsigned)sk.nwg;
     switch (dtype) {
-      case DA_BF16: project_rows_stream<DA_BF16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(pa); break;
-      case DA_F16: project_rows_stream<DA_F16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(pa); break;
-      default: project_rows_stream<DA_F32, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(pa); break;
+      case DA_BF16: project_pieces<DA_BF16><<<blocks, kThreads, 0, st>>>(sk); break;
+      case DA_F16: project_pieces<DA_F16><<<blocks, kThreads, 0, st>>>(sk); break;
+      default: project_pieces<DA_F32><<<blocks, kThreads, 0, st>>>(sk); break;
     }
     rc = check_launch("da_project_outer(projection)");
     if (rc) return rc;
     switch (out_dtype) {
-      case DA_F32: outer_from_projected<DA_F32><<<(unsigned)batch, kThreads, 0, st>>>(ap, gp, tokens, o.ka, o.kg, (char*)out, out_bstride); break;
-      case DA_BF16: outer_from_projected<DA_BF16><<<(unsigned)batch, kThreads, 0, st>>>(ap, gp, tokens, o.ka, o.kg, (char*)out, out_bstride); break;
-      default: outer_from_projected<DA_F16><<<(unsigned)batch, kThreads, 0, st>>>(ap, gp, tokens, o.ka, o.kg, (char*)out, out_bstride); break;
+      case DA_F32: outer_from_pieces<DA_F32><<<(unsigned)batch, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
+      case DA_BF16: outer_from_pieces<DA_BF16><<<(unsigned)batch, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
+      default: outer_from_pieces<DA_F16><<<(unsigned)batch, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
     }
     return check_launch("da_project_outer(outer)");
   } else {

@@ -201,6 +201,8 @@ PROJ_CASES = [
     (2, 128, 4096, 1024, 64, 64, False, torch.bfloat16, False),
     (2, 77, 100, 36, 64, 16, True, torch.float32, False),      # fp32 rows
     (3, 50, 512, 264, 32, 64, False, torch.bfloat16, True),    # sequence-first captures (token stride B*width)
+    (9, 260, 2048, 4096, 64, 64, True, torch.float16, False),  # 3 chunks per sample, fp16
+    (40, 128, 1024, 2752, 64, 48, False, torch.bfloat16, False),  # more stages than workgroups
 ]
 
 
