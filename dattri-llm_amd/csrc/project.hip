@@ -378,7 +378,7 @@ struct SkSide {
 
 struct SkArgs {
   SkSide s[2];
-  int64_t tokens, chunks, total;  // tokens per sample, 128-token chunks, stages of both sides
+  int64_t batch, tokens, chunks, total;  // samples, tokens per sample, 128-token chunks, stages of both sides
   int64_t nwg;
   float* pieces;                // (items of both sides + nwg) pieces of kPieceFloats
 };
@@ -389,132 +389,208 @@ __device__ __forceinline__ int64_t sk_first(int64_t w, const SkArgs& a) { return
 // the workgroup whose range holds stage x
 __device__ __forceinline__ int64_t sk_owner(int64_t x, const SkArgs& a) { return ((x + 1) * a.nwg - 1) / a.total; }
 
+namespace sk {
+constexpr int kKB = 512;                          // bytes of width per k-block
+constexpr int kRG = 32;                           // factor rows per stage (a row group)
+constexpr int kNRG = ps::kTok / kRG;              // 4 stages per k-block
+constexpr int kFStage = kRG * kKB;                // 16 KB
+constexpr int kNF = 6;                            // factor ring depth
+constexpr int kPBlock = kCols * kKB;              // 32 KB of projection rows per k-block
+constexpr int kLds = kNF * kFStage + 2 * kPBlock; // 160 KB: one workgroup per CU
+constexpr int kFDma = kFStage / 1024 / 4;         // 4 instructions per wave and stage
+constexpr int kPDma = kPBlock / 1024 / 4;         // 8 instructions per wave and k-block
+constexpr int kKs = kKB / 64;                     // 8 MFMA k-steps per stage
+static_assert(kFDma == 4 && kPDma == 8 && kNF == 6 && kNRG == 4,
+              "the vmcnt waits below (12 and 24) assume these counts");
+}  // namespace sk
+
+// The stream-K unit is a k-block of an item: 512 bytes of width of its 128
+// rows, read as four stages of one row group (32 rows) each, every DMA
+// instruction two 512-byte runs.  Per side nst = ceil(width / 512) units per
+// item.  The factor stages stream through a 6-deep ring; the unit's projection
+// rows (64 x 512 B) are double-buffered and serve its four stages.  Wave w owns
+// output columns 16w .. 16w+15 for all 128 tokens: per stage it runs 2 x 8
+// MFMAs into the accumulators of that row group (static indices: the unit loop
+// is unrolled over its four stages).
 template <int DT>
-__global__ __launch_bounds__(kThreads, 2) void project_pieces(SkArgs args) {
-  __shared__ __attribute__((aligned(1024))) char smem[ps::kNBuf * ps::kStage];
+__global__ __launch_bounds__(kThreads, 1) void project_pieces(SkArgs args) {
+  __shared__ __attribute__((aligned(1024))) char smem[sk::kLds];
   lds_char* const L = (lds_char*)smem;
   const uint32_t lds0 = (uint32_t)(uintptr_t)L;
+  const uint32_t ldsp = lds0 + sk::kNF * sk::kFStage;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int uwave = __builtin_amdgcn_readfirstlane(wave);
   const int64_t w = blockIdx.x;
-  const int64_t sb = uniform64(sk_first(w, args));
-  const int nloc = __builtin_amdgcn_readfirstlane((int)(sk_first(w + 1, args) - sb));  // stages of this workgroup
+  const int64_t ub = uniform64(sk_first(w, args));
+  const int nu = __builtin_amdgcn_readfirstlane((int)(sk_first(w + 1, args) - ub));  // units of this workgroup
+  const int nstage = sk::kNRG * nu;
 
-  // Issue cursor (side is, item ii, stage ik) and the DMA state of its item.
-  // DMA instruction j of this wave: j < 4 -> factor rows 32w + 8j .. +7
-  // (streamed once: non-temporal), j >= 4 -> projection rows 16w + 8(j-4) ..
-  // +7 (LDS rows 128 + ...); lane l -> row + l/8, slot l%8 holding logical
-  // chunk (l%8) ^ (row%8).
-  int is = sb >= args.s[1].s0 ? 1 : 0;
-  int64_t ii = uniform64((sb - args.s[is].s0) / args.s[is].nst);
-  int ik = __builtin_amdgcn_readfirstlane((int)(sb - args.s[is].s0 - ii * args.s[is].nst));
-  const int xs0 = is, xk0 = ik;
-  const int64_t xi0 = ii;
-  u32x4 rx, rp;
-  uint32_t wb, rof[ps::kDma], cb[ps::kDma];
-  int nst = 0;        // stages per item of the cursor's side
-  int64_t items = 0;  // items of the cursor's side
-  auto dma_row = [&](int j) __attribute__((always_inline)) {  // LDS row of instruction j, lane 0
-    return j < 4 ? 32 * uwave + 8 * j : ps::kTok + 16 * uwave + 8 * (j - 4);
-  };
+  // Lane roles.  Factor instruction j of wave w: stage rows 8w + 2j + l/32;
+  // projection instruction j: projection rows 16w + 2j + l/32.  Lane l writes
+  // slot l%32 of its 512-byte LDS row, holding logical chunk (l%32) ^ (row%16):
+  // a 16-byte read serves 16 lanes (256 bytes of banks) per cycle, and the 16
+  // rows of a fragment, 512 bytes apart, then hit 16 distinct bank groups.
+  uint32_t fcb[sk::kFDma], pcb[sk::kPDma];
+  int frow[sk::kFDma], prow[sk::kPDma];
 #pragma unroll
-  for (int j = 0; j < ps::kDma; ++j) {
-    const int row = dma_row(j) + (lane >> 3);
-    cb[j] = 16u * (uint32_t)((lane & 7) ^ (row & 7));
+  for (int j = 0; j < sk::kFDma; ++j) {
+    frow[j] = 8 * wave + 2 * j + (lane >> 5);
+    fcb[j] = 16u * (uint32_t)((lane & 31) ^ (frow[j] & 15));
   }
+#pragma unroll
+  for (int j = 0; j < sk::kPDma; ++j) {
+    prow[j] = 16 * wave + 2 * j + (lane >> 5);
+    pcb[j] = 16u * (uint32_t)((lane & 31) ^ (prow[j] & 15));
+  }
+
+  // Factor cursor: side is, item ii, unit iu, row group ir, and its item's state.
+  int is = ub >= args.s[1].s0 ? 1 : 0;
+  int64_t ii = uniform64((ub - args.s[is].s0) / args.s[is].nst);
+  int iu = __builtin_amdgcn_readfirstlane((int)(ub - args.s[is].s0 - ii * args.s[is].nst)), ir = 0;
+  const int xs0 = is, xu0 = iu;
+  const int64_t xi0 = ii;
+  u32x4 rx;
+  uint32_t fwb = 0, ftst = 0;
+  int64_t fnv = 0, fitems = 0;
+  int fnu = 0;
   auto set_item = [&]() __attribute__((always_inline)) {
     const SkSide& S = args.s[is];
     const int64_t b = uniform64(ii / args.chunks), t0 = (ii - b * args.chunks) * ps::kTok;
     rx = uniform4(make_rsrc(S.x + b * S.bstride + t0 * S.tstride, 0x7fffffffu));
-    rp = uniform4(make_rsrc(S.pt, 0x7fffffffu));
-    wb = (uint32_t)S.wbytes;
-    nst = S.nst;
-    items = S.items;
-    const int64_t nv = args.tokens - t0;  // valid rows of this chunk (may exceed 128)
+    fwb = (uint32_t)S.wbytes;
+    ftst = (uint32_t)S.tstride;
+    fnv = args.tokens - t0;  // valid rows of this chunk (may exceed 128)
+    fnu = S.nst;
+    fitems = S.items;
+  };
+  auto issue_f = [&](uint32_t dst0, bool live, bool more) __attribute__((always_inline)) {
+    const uint32_t koff = (uint32_t)iu * sk::kKB;
 #pragma unroll
-    for (int j = 0; j < ps::kDma; ++j) {
-      const int row = dma_row(j) + (lane >> 3);
-      const int c = row - ps::kTok;
-      rof[j] = j < 4 ? (row < nv ? (uint32_t)(row * S.tstride) : ps::kOob)
-                     : (c < S.ncols ? (uint32_t)(c * S.pt_rstride) : ps::kOob);
+    for (int j = 0; j < sk::kFDma; ++j) {
+      const int row = 32 * ir + frow[j];
+      const bool en = live & (row < fnv) & (koff + fcb[j] < fwb);
+      dma16_nt(rx, dst0 + (uint32_t)((8 * uwave + 2 * j) * sk::kKB),
+               en ? (uint32_t)row * ftst + koff + fcb[j] : ps::kOob);
+    }
+    if (live && ++ir == sk::kNRG) {
+      ir = 0;
+      if (++iu == fnu) {
+        iu = 0;
+        if (++ii == fitems) {
+          ii = 0;
+          ++is;
+        }
+        if (more) set_item();
+      }
     }
   };
-  // DMA of the cursor's stage into ring slot `slot` (zero fill when !live),
-  // then the cursor moves on.
-  auto issue = [&](int slot, bool live, bool more) __attribute__((always_inline)) {
-    const uint32_t koff = (uint32_t)ik * ps::kSB;
-    const uint32_t base = lds0 + (uint32_t)(slot * ps::kStage);
+
+  // Projection cursor: side pside, item pitem, unit pu (one issue per unit).
+  int pside = xs0, pu = xu0, pnu = 0, pcols = 0;
+  int64_t pitem = xi0, pitems = 0;
+  u32x4 rp;
+  uint32_t pwb = 0, prs = 0;
+  auto set_side = [&]() __attribute__((always_inline)) {
+    const SkSide& S = args.s[pside];
+    rp = uniform4(make_rsrc(S.pt, 0x7fffffffu));
+    pwb = (uint32_t)S.wbytes;
+    prs = (uint32_t)S.pt_rstride;
+    pnu = S.nst;
+    pitems = S.items;
+    pcols = S.ncols;
+  };
+  auto issue_p = [&](uint32_t dst0) __attribute__((always_inline)) {
+    const bool live = pside < 2;  // uniform; past the last side: zero fill
+    const uint32_t koff = (uint32_t)pu * sk::kKB;
 #pragma unroll
-    for (int j = 0; j < ps::kDma; ++j) {
-      const bool en = live & (rof[j] != ps::kOob) & (koff + cb[j] < wb);
-      const uint32_t off = en ? rof[j] + koff + cb[j] : ps::kOob;
-      const uint32_t dst = base + (uint32_t)(dma_row(j) * ps::kSB);
-      if (j < 4)
-        dma16_nt(rx, dst, off);
-      else
-        dma16(rp, dst, off);
+    for (int j = 0; j < sk::kPDma; ++j) {
+      const bool en = live & (prow[j] < pcols) & (koff + pcb[j] < pwb);
+      dma16(rp, dst0 + (uint32_t)((16 * uwave + 2 * j) * sk::kKB),
+            en ? (uint32_t)prow[j] * prs + koff + pcb[j] : ps::kOob);
     }
-    if (live && ++ik == nst) {
-      ik = 0;
-      if (++ii == items) {
-        ii = 0;
-        ++is;
+    if (live && ++pu == pnu) {
+      pu = 0;
+      if (++pitem == pitems) {
+        pitem = 0;
+        if (++pside < 2) set_side();
       }
-      if (more) set_item();
     }
   };
 
   set_item();
-  int ix = 0;  // next stage to issue, relative to sb
+  set_side();
+  issue_p(ldsp);
+  issue_p(ldsp + sk::kPBlock);
+  int ix = 0;  // next factor stage to issue, relative to the first
 #pragma unroll
-  for (int p = 0; p < ps::kNBuf - 1; ++p, ++ix) issue(p, ix < nloc, ix + 1 < nloc);
+  for (int p = 0; p < sk::kNF - 1; ++p, ++ix) issue_f(lds0 + p * sk::kFStage, ix < nstage, ix + 1 < nstage);
 
-  // Fragments: factor rows 32w + 16rb + l%16, projection rows 128 + 16c + l%16;
-  // k-step ks reads logical chunk 4ks + l/16 in slot (4ks + l/16) ^ (row%8),
-  // row%8 = l%8: the 8 lanes one LDS cycle serves hit 8 distinct slots.
   const int r16 = lane & 15, q = lane >> 4;
-  f32x4 acc[2][4];
+  f32x4 acc[8];  // row block tb = 2 * row group + rb: tokens 16tb .., columns 16w ..
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int fslot = 0, islot = sk::kNF - 1, pslot = 0;
+  // One unit.  Waits: this wave's loads of the stage (and, at row group 0, of
+  // the unit's projection rows) must be done; later loads and piece stores may
+  // be pending (loads complete in order).  At row group 0 the projection load
+  // was issued one unit earlier, after the stage's own loads: 12 may stay
+  // pending.  At row groups 1-3 of every unit but the first, the projection
+  // load of this unit's row group 0 lies between the stage's loads and now:
+  // 24 may stay pending.  Then every wave's part is visible and the slots read
+  // before may be refilled.
+  u32x4 pf[sk::kKs];
+  auto unit = [&](auto firstc) __attribute__((always_inline)) {
+    constexpr bool kFirst = decltype(firstc)::value;
+    const lds_char* pb = L + sk::kNF * sk::kFStage + (16 * wave + r16) * sk::kKB;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int slot = 0, xs = xs0, xk = xk0, x = 0;
-  int64_t xi = xi0;
-  while (x < nloc) {
-    const int seg_end = min(nloc, x + (args.s[xs].nst - xk));
-    for (; x < seg_end; ++x, ++ix) {
-      // this wave's loads of stage x done (those of the next stage may be in
-      // flight; piece stores may be pending too, but loads complete in
-      // order), its LDS reads done; then every wave's part is visible and the
-      // slot read one stage ago may be refilled
-      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      issue(slot == 0 ? ps::kNBuf - 1 : slot - 1, ix < nloc, ix + 1 < nloc);
-      const lds_char* sbuf = L + slot * ps::kStage;
-#pragma unroll
-      for (int ks = 0; ks < ps::kKs; ++ks) {
-        const int off = r16 * ps::kSB + (((4 * ks + q) ^ (r16 & 7)) << 4);
-        u32x4 xf[2], pf[4];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) xf[rb] = *(const u32x4*)(sbuf + (32 * wave + 16 * rb) * ps::kSB + off);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) pf[c] = *(const u32x4*)(sbuf + (ps::kTok + 16 * c) * ps::kSB + off);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) Mfma16<DT>::mma(acc[rb][c], xf[rb], pf[c]);
+    for (int r = 0; r < sk::kNRG; ++r) {
+      if (r == 0 || kFirst)
+        asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue_f(lds0 + islot * sk::kFStage, ix < nstage, ix + 1 < nstage);
+      ++ix;
+      islot = islot + 1 == sk::kNF ? 0 : islot + 1;
+      if (r == 0 && !kFirst) {
+        pslot ^= 1;                                // this unit's projection rows
+        issue_p(ldsp + (pslot ^ 1) * sk::kPBlock);  // the next unit's, into the freed buffer
       }
-      slot = slot + 1 == ps::kNBuf ? 0 : slot + 1;
+      if (r == 0) {  // this wave's projection fragments of the unit, kept for its four stages
+        const lds_char* pbs = pb + pslot * sk::kPBlock;
+#pragma unroll
+        for (int ks = 0; ks < sk::kKs; ++ks) pf[ks] = *(const u32x4*)(pbs + (((4 * ks + q) ^ r16) << 4));
+      }
+      const lds_char* fb = L + fslot * sk::kFStage;
+#pragma unroll
+      for (int ks = 0; ks < sk::kKs; ++ks) {
+        const int sw = ((4 * ks + q) ^ r16) << 4;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const u32x4 xf = *(const u32x4*)(fb + (16 * rb + r16) * sk::kKB + sw);
+          Mfma16<DT>::mma(acc[2 * r + rb], xf, pf[ks]);
+        }
+      }
+      fslot = fslot + 1 == sk::kNF ? 0 : fslot + 1;
     }
-    // piece of item (xs, xi): lane-major MFMA layout, (wave, rb, c) blocks of 64 x 16 B
+  };
+
+  int xs = xs0, xu = xu0, u = 0;
+  int64_t xi = xi0;
+  while (u < nu) {
+    const int seg_end = min(nu, u + (args.s[xs].nst - xu));
+    if (u == 0) {
+      unit(std::true_type{});
+      ++u;
+    }
+    for (; u < seg_end; ++u) unit(std::false_type{});
+    // piece of item (xs, xi): lane-major MFMA layout, blocks (column block w, row block tb) of 64 x 16 B
     f32x4* dst = (f32x4*)(args.pieces + (args.s[xs].i0 + xi + w) * kPieceFloats) + wave * 8 * 64 + lane;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        dst[(rb * 4 + c) * 64] = acc[rb][c];
-        acc[rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    xk = 0;
+    for (int t = 0; t < 8; ++t) {
+      dst[t * 64] = acc[t];
+      acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    xu = 0;
     if (++xi == args.s[xs].items) {
       xi = 0;
       ++xs;
@@ -526,54 +602,71 @@ __global__ __launch_bounds__(kThreads, 2) void project_pieces(SkArgs args) {
 
 // M[b, o*ka + i] = sum over chunks and tokens of gp[t, o] * ap[t, i], where
 // ap / gp are the summed pieces (plus the bias row on the activation side,
-// on valid tokens only).  One workgroup per sample; wave w contracts its 32
-// tokens of each chunk with fp32 16x16x4 MFMAs straight from the piece layout:
-// lane l holds tokens 4*(l/16) + r (r = 0..3) of column l%16 of each 16x16
-// block, so step r pairs MFMA k-slot l/16 with token 4*(l/16) + r on both
-// operands.  The four waves' sums are added in wave order.
+// on valid tokens only).  Four workgroups per sample, one per 16-row block ob
+// of M; workgroup id 32q + 8ob + x takes sample 8q + x, so the four share an
+// XCD (ids are dealt to the 8 XCDs round robin) and its L2 copy of the
+// activation pieces.  Wave w contracts its 32 tokens of each chunk with fp32
+// 16x16x4 MFMAs straight from the piece layout: lane l holds tokens
+// 4*(l/16) + r (r = 0..3) of column l%16 of each 16x16 block, so step r pairs
+// MFMA k-slot l/16 with token 4*(l/16) + r on both operands.  The four waves'
+// sums are added in wave order.
 template <int OT>
 __global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int ka, int kg, char* out,
                                                               int64_t out_bstride) {
-  __shared__ f32x4 red[4][16][64];
+  __shared__ f32x4 red[4][4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t b = blockIdx.x;
-  f32x4 m[4][4];
+  const int64_t id = blockIdx.x;
+  const int64_t b = 8 * (id >> 5) + (id & 7);
+  const int ob = (int)((id >> 3) & 3);
+  if (b >= args.batch || 16 * ob >= kg) return;  // uniform
+  const SkSide& SA = args.s[0];
+  const SkSide& SG = args.s[1];
+  f32x4 m[4];
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob)
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) m[ob][ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int ib = 0; ib < 4; ++ib) m[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int64_t ch = 0; ch < args.chunks; ++ch) {
-    f32x4 v[2][2][4];  // side, rb, column block
+    const int64_t il = b * args.chunks + ch;
+    const int64_t fa = SA.s0 + il * SA.nst, fg = SG.s0 + il * SG.nst;
+    const int64_t a0 = sk_owner(fa, args), a1 = sk_owner(fa + SA.nst - 1, args);
+    const int64_t g0 = sk_owner(fg, args), g1 = sk_owner(fg + SG.nst - 1, args);
+    auto piece = [&](const SkSide& S, int64_t wq) __attribute__((always_inline)) {
+      return (const f32x4*)(args.pieces + (S.i0 + il + wq) * kPieceFloats) + 2 * wave * 64 + lane;
+    };
+    f32x4 va[2][4], vg[2];  // activation: rb x column block; gradient: rb (column block ob)
+    {
+      const f32x4* pa = piece(SA, a0);
+      const f32x4* pg = piece(SG, g0);
 #pragma unroll
-    for (int side = 0; side < 2; ++side) {
-      const SkSide& S = args.s[side];
-      const int64_t il = b * args.chunks + ch;
-      const int64_t fs = S.s0 + il * S.nst;
-      const int64_t w0 = sk_owner(fs, args), w1 = sk_owner(fs + S.nst - 1, args);
+      for (int rb = 0; rb < 2; ++rb) {
+        vg[rb] = pg[(ob * 8 + rb) * 64];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) va[rb][c] = pa[(c * 8 + rb) * 64];
+      }
+    }
+    for (int64_t wq = a0 + 1; wq <= a1; ++wq) {
+      const f32x4* pa = piece(SA, wq);
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[side][rb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int64_t wq = w0; wq <= w1; ++wq) {
-        const f32x4* src = (const f32x4*)(args.pieces + (S.i0 + il + wq) * kPieceFloats) + wave * 8 * 64 + lane;
+        for (int c = 0; c < 4; ++c) va[rb][c] += pa[(c * 8 + rb) * 64];
+    }
+    for (int64_t wq = g0 + 1; wq <= g1; ++wq) {
+      const f32x4* pg = piece(SG, wq);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) vg[rb] += pg[(ob * 8 + rb) * 64];
+    }
+    if (SA.bias) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = 16 * c + (lane & 15);
+        const float bv = col < SA.ncols ? SA.bias[col] : 0.f;
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) v[side][rb][c] += src[(rb * 4 + c) * 64];
-      }
-      if (S.bias) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int col = 16 * c + (lane & 15);
-          const float bv = col < S.ncols ? S.bias[col] : 0.f;
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int64_t t = ch * ps::kTok + 32 * wave + 16 * rb + 4 * (lane >> 4) + r;
-              if (t < args.tokens) v[side][rb][c][r] += bv;
-            }
-        }
+          for (int r = 0; r < 4; ++r) {
+            const int64_t t = ch * ps::kTok + 32 * wave + 16 * rb + 4 * (lane >> 4) + r;
+            if (t < args.tokens) va[rb][c][r] += bv;
+          }
       }
     }
 #pragma unroll
@@ -581,29 +674,23 @@ __global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int k
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int ob = 0; ob < 4; ++ob)
-#pragma unroll
-          for (int ib = 0; ib < 4; ++ib)
-            m[ob][ib] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[1][rb][ob][r], v[0][rb][ib][r], m[ob][ib], 0, 0, 0);
+        for (int ib = 0; ib < 4; ++ib)
+          m[ib] = __builtin_amdgcn_mfma_f32_16x16x4f32(vg[rb][r], va[rb][ib][r], m[ib], 0, 0, 0);
   }
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob)
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) red[wave][ob * 4 + ib][lane] = m[ob][ib];
+  for (int ib = 0; ib < 4; ++ib) red[wave][ib][lane] = m[ib];
   __syncthreads();
-  for (int idx = tid; idx < 16 * 64; idx += kThreads) {
-    const int blk = idx >> 6, ln = idx & 63;
-    const f32x4 sum = red[0][blk][ln] + red[1][blk][ln] + red[2][blk][ln] + red[3][blk][ln];
-    const int i = 16 * (blk & 3) + (ln & 15);
+  const int ib = tid >> 6, ln = tid & 63;
+  const f32x4 sum = red[0][ib][ln] + red[1][ib][ln] + red[2][ib][ln] + red[3][ib][ln];
+  const int i = 16 * ib + (ln & 15);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int o = 16 * (blk >> 2) + 4 * (ln >> 4) + r;
-      if (o < kg && i < ka) Elem<OT>::store(out, b * out_bstride + (int64_t)o * ka + i, sum[r]);
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int o = 16 * ob + 4 * (ln >> 4) + r;
+    if (o < kg && i < ka) Elem<OT>::store(out, b * out_bstride + (int64_t)o * ka + i, sum[r]);
   }
 }
 
-// Workgroup slots of the stream-K launch on the current device: two per CU.
+// Workgroup slots of the stream-K launch on the current device: one per CU.
 int sk_slots(int64_t* n) {
   static int cache[64];
   int dev = 0;
@@ -615,8 +702,8 @@ int sk_slots(int64_t* n) {
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
-  if (dev >= 0 && dev < 64) cache[dev] = 2 * cus;
-  *n = 2 * cus;
+  if (dev >= 0 && dev < 64) cache[dev] = cus;
+  *n = cus;
   return DA_OK;
 }
 
@@ -810,6 +897,7 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
     // Stream-K projection of both sides into fp32 pieces, then the per-sample
     // contraction.
     SkArgs sk;
+    sk.batch = batch;
     sk.tokens = tokens;
     sk.chunks = (tokens + ps::kTok - 1) / ps::kTok;
     sk.pieces = (float*)workspace;
@@ -824,7 +912,7 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
       S.pt = act ? o.pin_t : o.pout_t;
       S.pt_rstride = act ? o.pin_rstride : o.pout_rstride;
       S.ncols = act ? o.ka : o.kg;
-      S.nst = (int)((S.wbytes + ps::kSB - 1) / ps::kSB);
+      S.nst = (int)((S.wbytes + sk::kKB - 1) / sk::kKB);  // stream-K units (k-blocks) per item
       S.items = batch * sk.chunks;
       S.s0 = s0;
       S.i0 = side * S.items;
@@ -837,7 +925,7 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
     rc = sk_slots(&slots);
     if (rc) return rc;
     sk.nwg = slots < sk.total ? slots : sk.total;
-    if (sk.total / sk.nwg > (1LL << 30) || batch > 0x7fffffffLL)
+    if (sk.total / sk.nwg > (1LL << 30) || batch > (1LL << 28))
       return set_error(DA_ERR_INVALID, "%s: problem too large", who);
     const unsigned blocks = (unsigned)sk.nwg;
     switch (dtype) {
@@ -847,10 +935,11 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
     }
     rc = check_launch("da_project_outer(projection)");
     if (rc) return rc;
+    const unsigned ob_blocks = (unsigned)(32 * ((batch + 7) / 8));  // 4 row blocks x 8 samples per 32 ids
     switch (out_dtype) {
-      case DA_F32: outer_from_pieces<DA_F32><<<(unsigned)batch, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
-      case DA_BF16: outer_from_pieces<DA_BF16><<<(unsigned)batch, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
-      default: outer_from_pieces<DA_F16><<<(unsigned)batch, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
+      case DA_F32: outer_from_pieces<DA_F32><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
+      case DA_BF16: outer_from_pieces<DA_BF16><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
+      default: outer_from_pieces<DA_F16><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
     }
     return check_launch("da_project_outer(outer)");
   } else {
