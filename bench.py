@@ -122,6 +122,9 @@ def _mean_ms(timers, key):
 
 
 TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "llama8b_block_hbm_traffic.md")
+GHOST_TRAFFIC = os.path.join(REPO, "profiles", "ghost_c2_hbm_traffic.md")
+PROJECT_TRAFFIC = os.path.join(REPO, "profiles", "project_llama7b_mlp_hbm_traffic.md")
+MOE_TRAFFIC = os.path.join(REPO, "profiles", "moe_mixtral_layer_hbm_traffic.md")
 
 
 def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
@@ -381,7 +384,10 @@ def bench_ghost(args):
         "config": {"workload": "ghost cross-gram 256 train x 64 query, T=512, d_in=d_out=4096"},
         "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles_v2", "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": profiled_traffic("ghost_gram_tiles_v2", GHOST_TRAFFIC),
+                     "traffic_source": os.path.relpath(GHOST_TRAFFIC, REPO),
+                     "work_per_launch": f"{flops:.4g} flop = 2 x 256 x 64 pairs x 512^2 x (4096 + 4096)"},
     }
     if args.cpu_baseline:
         import numpy as np
@@ -469,8 +475,11 @@ def bench_project(args):
         "data": "synthetic",
         "config": {"workload": "llama-7b MLP projected capture: 512 train + 128 query, T=128, "
                                "gate/up 4096->11008, down 11008->4096, k=64"},
-        "roofline": {"bound": "hbm", "kernel": "project_outer_kernel", "achieved": round(gbs, 1),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+        "roofline": {"bound": "hbm", "kernel": "da_project_outer (project_pieces + outer_from_pieces)",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("da_project_outer", PROJECT_TRAFFIC),
+                     "traffic_source": os.path.relpath(PROJECT_TRAFFIC, REPO),
                      "work_per_launch": "640 samples x 128 tokens x (d_in + d_out) x 2 B = 2.47e9 B",
                      "launches_per_step": 3, "step_share": round(3 * t_proj / ms, 3)},
         "kernels": {"project_outer": {"ms": round(t_proj, 4), "gbs": round(gbs, 1)},
@@ -579,7 +588,9 @@ def bench_moe(args):
                    "rows_per_expert": rows},
         "roofline": {"bound": "mfma", "kernel": "ghost_grouped_tiles_v2", "achieved": round(tf, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "work_per_step": f"{flops:.4g} flop = sum over experts and both linears "
+                     "traffic": profiled_traffic("ghost_grouped_tiles_v2", MOE_TRAFFIC),
+                     "traffic_source": os.path.relpath(MOE_TRAFFIC, REPO),
+                     "work_per_step": f"{flops:.4g} flop = sum over experts and both linears "
                                                        "of 2 x rows1 x rows2 x (d_in + d_out)",
                      "launches_per_step": 1, "step_share": round(t_ghost / ms, 3)},
         "kernels": {"route_ms": round(_mean_ms(timers, "route"), 4), "ghost_ms": round(t_ghost, 4)},

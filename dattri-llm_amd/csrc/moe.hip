@@ -152,6 +152,9 @@ __global__ __launch_bounds__(256) void counting_sort_kernel(SortArgs a) {
 //   by e      -> entries[off[e] + r] = p for expert e's local row r (routed order);
 //   by e*B+b  -> rows[off2[e*B+b] + q] = r, expert e's local rows grouped by sample,
 // and seg[e*(B+1) + b] = off2[e*B+b] - off2[e*B] (per-expert relative offsets).
+// Histograms and scans use the whole workgroup; the order-dependent scatter is
+// one wave walking LDS-resident keys 64 at a time, each lane's rank among the
+// lanes of equal key coming from one ballot per distinct key in the wave.
 struct RouteArgs {
   const int64_t* index;  // (N, k)
   int64_t n, k, experts, batch, tokens;
@@ -161,86 +164,210 @@ struct RouteArgs {
   int32_t* rows;     // n*k
 };
 
-__global__ __launch_bounds__(256) void moe_route_kernel(RouteArgs a) {
-  __shared__ int32_t c1[kMaxExperts + 1];
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kRouteTile = 8192;      // keys staged in LDS per pass of the scatter
+constexpr int kRouteWaveBins = 1024;  // per-wave histograms of both keys when E*B fits
+
+// In-place exclusive scan of the LDS array a[0, len) by the whole workgroup;
+// returns the total.  wsum: kRouteWaves ints of LDS.
+__device__ int32_t route_scan(int32_t* a, int len, int32_t* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (len + kRouteThreads - 1) / kRouteThreads;
+  const int beg = tid * per;
+  int32_t s = 0;
+  for (int i = 0; i < per; ++i)
+    if (beg + i < len) s += a[beg + i];
+  int32_t x = s;  // inclusive scan over the wave
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int32_t v = lane < kRouteWaves ? wsum[lane] : 0;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t y = __shfl_up(v, off, 64);
+      if (lane >= off) v += y;
+    }
+    if (lane < kRouteWaves) wsum[lane] = v;
+  }
+  __syncthreads();
+  int32_t run = (wave > 0 ? wsum[wave - 1] : 0) + x - s;
+  for (int i = 0; i < per; ++i)
+    if (beg + i < len) {
+      const int32_t c = a[beg + i];
+      a[beg + i] = run;
+      run += c;
+    }
+  const int32_t total = wsum[kRouteWaves - 1];
+  __syncthreads();
+  return total;
+}
+
+// Ranks of this wave's 64 keys among equal keys of the wave (stable), one
+// ballot per distinct key; r = lanes below with the same key, t = all of them.
+__device__ __forceinline__ void route_ranks(bool ok, int key, uint64_t lt, int& r, int& t) {
+  r = 0;
+  t = 0;
+  for (uint64_t act = __ballot(ok); act;) {
+    const int ke = __builtin_amdgcn_readlane(key, __builtin_ctzll(act));
+    const bool mine = ok && key == ke;
+    const uint64_t m = __ballot(mine);
+    if (mine) {
+      r = __popcll(m & lt);
+      t = __popcll(m);
+    }
+    act &= ~m;
+  }
+}
+
+// The ordered scatter of one wave over keys[beg, end) of the tile starting at
+// entry t0, advancing the running counters n1 (by expert) and n2 (by expert
+// and sample).
+__device__ __forceinline__ void route_scatter(const RouteArgs& a, const int32_t* keys, uint32_t t0, uint32_t beg,
+                                              uint32_t end, int32_t* n1, int32_t* n2, const int32_t* o1) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));  // lanes below this one
+  for (uint32_t base = beg; base < end; base += 64) {
+    const uint32_t i = base + lane;
+    const int32_t kk = i < end ? keys[i] : -1;
+    const bool ok = kk >= 0;
+    const int e = kk & 511, e2 = kk >> 9;
+    int r1, t1, r2, t2;
+    route_ranks(ok, e, lt, r1, t1);
+    route_ranks(ok, e2, lt, r2, t2);
+    int32_t s1 = 0, s2 = 0;
+    if (ok) {
+      s1 = n1[e] + r1;
+      s2 = n2[e2] + r2;
+    }
+    // every lane has read the counters before the last lane of each key bumps them
+    __builtin_amdgcn_wave_barrier();
+    if (ok) {
+      a.entries[s1] = (int32_t)(t0 + i);
+      a.rows[s2] = s1 - o1[e];  // expert-local routed row
+      if (r1 == t1 - 1) n1[e] = s1 + 1;
+      if (r2 == t2 - 1) n2[e2] = s2 + 1;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
+  __shared__ int32_t c1[kMaxExperts + 1], o1[kMaxExperts + 1];
   __shared__ int32_t c2[kMaxBins + 1];
-  const int tid = threadIdx.x;
-  const int64_t total = a.n * a.k, nb2 = a.experts * a.batch;
-  for (int64_t b = tid; b <= a.experts; b += 256) c1[b] = 0;
-  for (int64_t b = tid; b <= nb2; b += 256) c2[b] = 0;
+  __shared__ int32_t keys[kRouteTile];
+  __shared__ int32_t h1[kRouteWaves][kMaxExperts];    // per-wave counters by expert
+  __shared__ int32_t h2[kRouteWaves][kRouteWaveBins];  // per-wave counters by expert and sample
+  __shared__ int32_t wsum[kRouteWaves];
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const uint32_t n = (uint32_t)a.n, total = (uint32_t)(a.n * a.k), T = (uint32_t)a.tokens;
+  const uint32_t B = (uint32_t)a.batch;
+  const int E = (int)a.experts, nb2 = E * (int)B;
+  const bool per_wave = nb2 <= kRouteWaveBins;  // uniform
+  for (int i = tid; i <= E; i += kRouteThreads) c1[i] = 0;
+  for (int i = tid; i <= nb2; i += kRouteThreads) c2[i] = 0;
   __syncthreads();
-  auto keys = [&](int64_t p, int64_t& e, int64_t& e2) __attribute__((always_inline)) {
-    const int64_t slot = p / a.n, tok = p - slot * a.n;
-    e = a.index[tok * a.k + slot];
-    e2 = (e >= 0 && e < a.experts) ? e * a.batch + tok / a.tokens : -1;
-    if (e < 0 || e >= a.experts) e = -1;
+  // entry p -> (e*B + b) << 9 | e, or -1 when its expert index is out of range
+  auto key = [&](uint32_t p, int64_t e) __attribute__((always_inline)) {
+    const uint32_t slot = p / n, tok = p - slot * n;
+    return (e < 0 || e >= E) ? -1 : (int32_t)((((uint32_t)e * B + tok / T) << 9) | (uint32_t)e);
   };
-  for (int64_t p = tid; p < total; p += 256) {
-    int64_t e, e2;
-    keys(p, e, e2);
-    if (e >= 0) {
-      atomicAdd(&c1[e], 1);
-      atomicAdd(&c2[e2], 1);
+  auto index_of = [&](uint32_t p) __attribute__((always_inline)) {
+    const uint32_t slot = p / n, tok = p - slot * n;
+    return a.index[(int64_t)tok * a.k + slot];
+  };
+  // keys of entries p0 + kRouteThreads*j, j < 8, loads first
+  auto keys8 = [&](uint32_t p0, uint32_t lim, int32_t (&kk)[8]) __attribute__((always_inline)) {
+    int64_t ev[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t p = p0 + (uint32_t)(kRouteThreads * j);
+      ev[j] = p < lim ? index_of(p) : -1;
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kk[j] = key(p0 + (uint32_t)(kRouteThreads * j), ev[j]);
+  };
+  for (uint32_t p0 = tid; p0 < total; p0 += 8 * kRouteThreads) {
+    int32_t kk[8];
+    keys8(p0, total, kk);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (kk[j] >= 0) {
+        atomicAdd(&c1[kk[j] & 511], 1);
+        atomicAdd(&c2[kk[j] >> 9], 1);
+      }
   }
   __syncthreads();
+  const int32_t nvalid = route_scan(c1, E, wsum);
+  route_scan(c2, nb2, wsum);
+  for (int i = tid; i < E; i += kRouteThreads) {
+    o1[i] = c1[i];
+    a.offsets[i] = c1[i];
+  }
   if (tid == 0) {
-    int32_t run = 0;
-    for (int64_t e = 0; e < a.experts; ++e) {
-      const int32_t c = c1[e];
-      a.offsets[e] = run;
-      c1[e] = run;  // next free slot of expert e
-      run += c;
-    }
-    a.offsets[a.experts] = run;
-  } else if (tid == 64) {
-    int32_t run = 0;
-    for (int64_t q = 0; q < nb2; ++q) {
-      const int32_t c = c2[q];
-      c2[q] = run;
-      run += c;
-    }
-    c2[nb2] = run;
+    a.offsets[E] = nvalid;
+    c2[nb2] = nvalid;
   }
   __syncthreads();
-  // Relative per-sample offsets of every expert (c2 holds bin starts until the
-  // scatter below advances them, so read them first).
-  for (int64_t q = tid; q < a.experts * (a.batch + 1); q += 256) {
-    const int64_t e = q / (a.batch + 1), b = q - e * (a.batch + 1);
-    a.seg[q] = c2[e * a.batch + b] - c2[e * a.batch];
+  // per-expert relative offsets (c2 holds bin starts until the scatter advances them)
+  for (int q = tid; q < E * ((int)B + 1); q += kRouteThreads) {
+    const int e = q / ((int)B + 1), b = q - e * ((int)B + 1);
+    a.seg[q] = c2[e * (int)B + b] - c2[e * (int)B];
   }
   __syncthreads();
-  if (tid >= 64) return;
-  const int lane = tid;
-  for (int64_t base = 0; base < total; base += 64) {
-    const int64_t p = base + lane;
-    int64_t e = -1, e2 = -1;
-    if (p < total) keys(p, e, e2);
-    int r1 = 0, t1 = 0, r2 = 0, t2 = 0;
-    for (int src = 0; src < 64; ++src) {
-      const int64_t oe = __shfl(e, src, 64), oe2 = __shfl(e2, src, 64);
-      if (e >= 0 && oe == e) {
-        t1 += 1;
-        if (src < lane) r1 += 1;
+  for (uint32_t t0 = 0; t0 < total; t0 += kRouteTile) {
+    const uint32_t nt = min((uint32_t)kRouteTile, total - t0);
+    for (uint32_t i0 = tid; i0 < nt; i0 += 8 * kRouteThreads) {
+      int32_t kk[8];
+      keys8(t0 + i0, t0 + nt, kk);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (i0 + (uint32_t)(kRouteThreads * j) < nt) keys[i0 + kRouteThreads * j] = kk[j];
+    }
+    if (per_wave) {
+      // wave w takes keys [w*seg, (w+1)*seg) of the tile, in order
+      const uint32_t segl = (nt + kRouteWaves - 1) / kRouteWaves;
+      for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) (&h1[0][0])[(i / E) * kMaxExperts + i % E] = 0;
+      for (int i = tid; i < kRouteWaves * nb2; i += kRouteThreads) (&h2[0][0])[(i / nb2) * kRouteWaveBins + i % nb2] = 0;
+      __syncthreads();
+      const uint32_t beg = min(nt, wave * segl), end = min(nt, beg + segl);
+      for (uint32_t i = beg + (tid & 63); i < end; i += 64) {
+        const int32_t kk = keys[i];
+        if (kk >= 0) {
+          atomicAdd(&h1[wave][kk & 511], 1);
+          atomicAdd(&h2[wave][kk >> 9], 1);
+        }
       }
-      if (e >= 0 && oe2 == e2) {
-        t2 += 1;
-        if (src < lane) r2 += 1;
+      __syncthreads();
+      // per key: wave w starts at the running counter plus the counts of waves < w
+      for (int e = tid; e < E; e += kRouteThreads) {
+        int32_t run = c1[e];
+        for (int w = 0; w < kRouteWaves; ++w) {
+          const int32_t c = h1[w][e];
+          h1[w][e] = run;
+          run += c;
+        }
+        c1[e] = run;
       }
+      for (int q = tid; q < nb2; q += kRouteThreads) {
+        int32_t run = c2[q];
+        for (int w = 0; w < kRouteWaves; ++w) {
+          const int32_t c = h2[w][q];
+          h2[w][q] = run;
+          run += c;
+        }
+        c2[q] = run;
+      }
+      __syncthreads();
+      route_scatter(a, keys, t0, beg, end, h1[wave], h2[wave], o1);
+    } else {
+      __syncthreads();
+      if (tid < 64) route_scatter(a, keys, t0, 0, nt, c1, c2, o1);
     }
-    int32_t slot1 = 0, slot2 = 0;
-    if (e >= 0) {
-      slot1 = c1[e] + r1;
-      slot2 = c2[e2] + r2;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (e >= 0) {
-      a.entries[slot1] = (int32_t)p;
-      a.rows[slot2] = slot1 - a.offsets[e];  // expert-local routed row
-      if (r1 == t1 - 1) c1[e] = slot1 + 1;
-      if (r2 == t2 - 1) c2[e2] = slot2 + 1;
-    }
-    __builtin_amdgcn_wave_barrier();
+    __syncthreads();
   }
 }
 
@@ -330,7 +457,7 @@ int da_moe_route(const int64_t* index, int64_t n_tokens, int k, int n_experts, i
   a.entries = entries;
   a.seg = seg;
   a.rows = rows;
-  moe_route_kernel<<<1, 256, 0, (hipStream_t)stream>>>(a);
+  moe_route_kernel<<<1, kRouteThreads, 0, (hipStream_t)stream>>>(a);
   return check_launch(who);
 }
 

@@ -304,7 +304,8 @@ def test_c1_tracin_attributor_and_cosine(device):
     assert rel_err(cos.scores.numpy(), want) <= 1e-3
 
 
-@pytest.mark.parametrize("batch,tokens,n_exp,k", [(16, 256, 8, 2), (3, 37, 5, 3), (1, 64, 4, 1)])
+@pytest.mark.parametrize("batch,tokens,n_exp,k", [(16, 256, 8, 2), (3, 37, 5, 3), (1, 64, 4, 1),
+                                                    (64, 300, 64, 4), (8, 1024, 256, 2), (32, 512, 8, 2)])
 def test_route_segments_matches_per_expert_sorts(device, ops, batch, tokens, n_exp, k):
     """One-launch routing == router top-k -> per-expert torch.where order ->
     per-expert stable sort by sample, bit for bit."""
@@ -326,3 +327,28 @@ def test_route_segments_matches_per_expert_sorts(device, ops, batch, tokens, n_e
     for e, (slot, tok) in enumerate(per_expert):
         ent = entries[off[e]:off[e + 1]].to(torch.int64)
         assert torch.equal((ent // n).cpu(), slot.cpu()) and torch.equal((ent % n).cpu(), tok.cpu())
+
+
+def test_route_drops_out_of_range_experts(device):
+    """Entries whose expert index is outside [0, n_experts) are dropped; the
+    rest keep the slot-major, token-ascending order, grouped by sample."""
+    from dattri_llm_amd import kernels
+
+    batch, tokens, n_exp, k = 5, 41, 6, 2
+    n = batch * tokens
+    gen = torch.Generator().manual_seed(7)
+    idx = torch.randint(-2, n_exp + 2, (n, k), generator=gen, dtype=torch.int64)
+    print(f"route drop case batch={batch} tokens={tokens} n_exp={n_exp} k={k}", flush=True)
+    offsets, entries, seg, rows = (x.cpu() for x in kernels.moe_route(idx.to(device), n_exp, batch, tokens))
+    idx_np = idx.numpy()
+    off = [0]
+    for e in range(n_exp):
+        ps = [s_ * n + t for s_ in range(k) for t in range(n) if idx_np[t, s_] == e]
+        assert entries[off[-1]:off[-1] + len(ps)].tolist() == ps
+        samples = [(p % n) // tokens for p in ps]
+        want_rows = [r for b in range(batch) for r, sb in enumerate(samples) if sb == b]
+        assert rows[off[-1]:off[-1] + len(ps)].tolist() == want_rows
+        assert seg.flatten()[e * (batch + 1):(e + 1) * (batch + 1)].tolist() == [
+            sum(sb < b for sb in samples) for b in range(batch + 1)]
+        off.append(off[-1] + len(ps))
+    assert offsets.tolist() == off
