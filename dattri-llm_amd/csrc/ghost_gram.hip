@@ -7,16 +7,20 @@
 // HBM and then reduces their Hadamard product over each (S1 x S2) block.
 //
 // Here the same two products are computed as ONE tiled GEMM pair over the row
-// spaces (B1*S1) x (B2*S2): a workgroup owns a 128 x 128 tile that lies inside a
-// single (i, j) sample pair, runs the activation K-loop into one set of fp32
-// MFMA accumulators and the gradient K-loop into a second set, and reduces
+// spaces (B1*S1) x (B2*S2): a workgroup owns a tile that lies inside a single
+// (i, j) sample pair, runs the activation K-loop into one set of fp32 MFMA
+// accumulators and the gradient K-loop into a second set, and reduces
 // (K_a + bias) * K_g in registers.  Only one fp32 per tile reaches HBM; a
 // second tiny kernel sums the per-tile partials of each pair in a fixed order,
 // so results are deterministic.
 //
-// Tile order: workgroups are remapped so each XCD owns a contiguous run of
-// tiles, grouped 8 row-tiles wide, so the concurrently running tiles on one
-// XCD share their operand row blocks through that XCD's L2.
+// Two tile engines: the 256 x 128 engine (ghost_gram_tiles_v2 and the grouped
+// MoE form ghost_grouped_tiles_v2, below) takes dense and grouped launches
+// whose rows it can address with 32-bit offsets; the 128 x 128 kernels first
+// in this file take per-sample segmented sides and the rest.  Tile order:
+// workgroups are remapped so each XCD owns a contiguous run of tiles, grouped
+// a few row tiles wide, so the concurrently running tiles on one XCD share
+// their operand row blocks through that XCD's L2.
 #include "common.h"
 
 namespace da {
@@ -402,15 +406,16 @@ __global__ void grouped_reduce(GroupedArgs ga, float* __restrict__ out, int64_t 
 // 256 x 128 tile engine (the gfx950 path).
 //
 // Both Gram products of a tile -- K_a over the activation width, then K_g over
-// the gradient width -- run as ONE stream of 64-byte K stages through a ring of
-// four LDS stages (24 KB each).  Operand rows go HBM -> LDS untouched by buffer
-// loads with the LDS-direct bit (16 bytes per lane); rows past a sample's end,
-// and chunks past the width, read as zero (offset past the buffer range).  The
-// four waves each own a 128 x 64 block (4 x 2 MFMA blocks of 32 x 32); K_a and
-// K_g together fill the 256 accumulator registers.  As in the dW kernel, the
-// loads are issued as inline assembly with explicit vmcnt waits, interleaved
-// with the MFMAs, and each stage's second slice is multiplied after the
-// barrier that opens the next stage.
+// the gradient width -- run as ONE stream of 128-byte K stages (one cache line
+// of every operand row) through a ring of three LDS stages (48 KB each, two in
+// flight).  Operand rows go HBM -> LDS untouched by buffer loads with the
+// LDS-direct bit (16 bytes per lane); rows past a sample's end, and chunks past
+// the width, read as zero (offset past the buffer range).  The four waves each
+// own a 128 x 64 block (4 x 2 MFMA blocks of 32 x 32); K_a and K_g together
+// fill the 256 accumulator registers.  As in the dW kernel, the loads are
+// issued as inline assembly with explicit vmcnt waits, interleaved with the
+// MFMAs (a quarter stage of loads per quarter stage of MFMAs), and the last
+// quarter of each stage is multiplied after the barrier that opens the next.
 // ---------------------------------------------------------------------------
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -656,228 +661,6 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_grouped_tiles_v2(GroupedArg
       }
   __syncthreads();
   grouped_bins(P, v2::kPRow, v2::kBM, v2::kBN, t0, s0, n1, n2, m, n, G, ga);
-}
-
-// ---------------------------------------------------------------------------
-// 256 x 256 tile engine.  Each wave owns a 128 x 128 block (4 x 4 MFMA blocks,
-// 256 fp32 accumulators in AGPRs).  K_a is accumulated first; after the last
-// activation stage it is rounded to bf16 and packed into 128 VGPRs (the
-// reference forms K_a with torch's bf16 GEMM, i.e. also rounded to bf16; here
-// the rounding happens once, after fp32 accumulation), freeing the
-// accumulators for K_g, which stays fp32, as do the products and their sum.
-// Twice the tile area of the 256 x 128 engine for 4/3 of its operand rows:
-// 128 instead of 85 flop per byte streamed through L2.  Stages are 64 bytes
-// of K (two 32-byte slices) in a ring of four, as in the dW kernel.
-// ---------------------------------------------------------------------------
-namespace v3 {
-constexpr int kB = 256;                  // rows per side
-constexpr int kRows = 2 * kB;            // LDS rows per stage
-constexpr int kSB = 64;                  // bytes of K per row and stage
-constexpr int kStage = kRows * kSB;      // 32 KB
-constexpr int kNBuf = 4;                 // ring: three stages in flight
-constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // 8 per wave and stage
-constexpr uint32_t kOob = 0x80000000u;
-static_assert(kDma == 8, "two halves of 4 DMA instructions per stage");
-}  // namespace v3
-
-struct TileSrc3 {
-  u32x4 ra, rg;                          // this wave's side (waves 0, 1: side 1; 2, 3: side 2)
-  uint32_t roff_a[v3::kDma], roff_g[v3::kDma];
-  int64_t kbytes_a, kbytes_g;
-};
-
-// Row of the tile loaded by lane `lane` of DMA instruction j of wave w:
-// 16 rows x 64 bytes per instruction, lane l -> row 16*(8w + j) + l/4, slot
-// l%4 holding logical chunk (l%4) ^ ((row/4)%4) = (l%4) ^ ((l/16)%4).
-__device__ __forceinline__ int dma_row3(int w, int j, int lane) { return 16 * (v3::kDma * w + j) + (lane >> 2); }
-
-struct DmaState3 {
-  u32x4 ra, rg;
-  uint32_t roa[v3::kDma], rog[v3::kDma];
-  uint32_t cbyte, lds0;
-  int uwave, na, nst;
-  int64_t kba, kbg;
-};
-
-// DMA instruction j of stage st for this wave (a stage past the last, or
-// a chunk past the width, loads zeros from no memory into its own slot).
-__device__ __forceinline__ void dma_one3(const DmaState3& D, int j, int st) {
-  const bool act = st < D.na;
-  const uint32_t koff = (uint32_t)(act ? st : st - D.na) * v3::kSB;
-  const int64_t kb = act ? D.kba : D.kbg;
-  const bool kin = st < D.nst && (int64_t)(koff + D.cbyte) < kb;
-  const uint32_t base = D.lds0 + (uint32_t)((st % v3::kNBuf) * v3::kStage + (v3::kDma * D.uwave + j) * 16 * v3::kSB);
-  // Mask arithmetic, not selects: see dma_quarter.
-  const uint32_t m = act ? 0xffffffffu : 0u;
-  u32x4 rs;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) rs[c] = (D.ra[c] & m) | (D.rg[c] & ~m);
-  const uint32_t roff = (D.roa[j] & m) | (D.rog[j] & ~m);
-  dma16(rs, base, (kin && roff != v3::kOob) ? roff + koff + D.cbyte : v3::kOob);
-}
-
-// Half a stage: the 16 MFMAs of one slice held in (ua, ub) into acc; with rd,
-// the 8 fragment reads of the next slice (stage base sb, slice offset coff)
-// interleaved one per MFMA; with h >= 0, half h (instructions 4h .. 4h+3) of
-// stage dst's loads, one per four MFMAs.
-template <int DT>
-__device__ __forceinline__ void ghost_half3(f32x16 (&acc)[4][4], const u32x4 (&ua)[4], const u32x4 (&ub)[4], bool rd,
-                                            const lds_char* sb, int coff, int wm, int wn, u32x4 (&na)[4],
-                                            u32x4 (&nb)[4], const DmaState3& D, int h, int dst) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (rd && i < 8) {
-      if (i < 4) na[i] = *(const u32x4*)(sb + (128 * wm + 32 * i) * v3::kSB + coff);
-      else nb[i - 4] = *(const u32x4*)(sb + (v3::kB + 128 * wn + 32 * (i - 4)) * v3::kSB + coff);
-    }
-    Mfma32<DT>::mma(acc[i >> 2][i & 3], ua[i >> 2], ub[i & 3]);
-    if (h >= 0 && (i & 3) == 1) dma_one3(D, 4 * h + (i >> 2), dst);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-__device__ __forceinline__ void ghost_stage_sync3() {
-  static_assert(v3::kNBuf == 4, "vmcnt below is two stages of 8 instructions");
-  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  asm volatile("s_barrier" ::: "memory");
-}
-
-// Runs both K loops of a 256 x 256 tile: on return kab holds K_a (bf16 pairs:
-// kab[x][y][q] = acc elements 2q, 2q+1) and acc holds K_g; every wave is done
-// with the ring and no load is in flight.
-template <int DT>
-__device__ __forceinline__ void ghost_tile_engine3(const TileSrc3& S, char* smem, f32x16 (&acc)[4][4],
-                                                   uint32_t (&kab)[4][4][8]) {
-  lds_char* const L = (lds_char*)smem;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  DmaState3 D;
-  D.uwave = __builtin_amdgcn_readfirstlane(wave);
-  D.na = (int)((S.kbytes_a + v3::kSB - 1) / v3::kSB);
-  D.nst = D.na + (int)((S.kbytes_g + v3::kSB - 1) / v3::kSB);
-  D.ra = uniform4(S.ra);
-  D.rg = uniform4(S.rg);
-  D.kba = S.kbytes_a;
-  D.kbg = S.kbytes_g;
-  D.lds0 = (uint32_t)(uintptr_t)L;
-  D.cbyte = 16u * (uint32_t)((lane & 3) ^ ((lane >> 4) & 3));
-#pragma unroll
-  for (int j = 0; j < v3::kDma; ++j) {
-    D.roa[j] = S.roff_a[j];
-    D.rog[j] = S.roff_g[j];
-  }
-  const int na = D.na, nst = D.nst;
-  // Fragment rows: A x = 128wm + 32x + l%32, B y = 256 + 128wn + 32y + l%32;
-  // slice kk reads logical chunk 2kk + l/32, in slot (2kk + l/32) ^ ((l%32)/4 % 4).
-  const int lrow = lane & 31, sw = (lrow >> 2) & 3, hh = lane >> 5;
-  const int c0 = lrow * v3::kSB + (((0 + hh) ^ sw) << 4), c1 = lrow * v3::kSB + (((2 + hh) ^ sw) << 4);
-  u32x4 f0a[4], f0b[4], f1a[4], f1b[4];
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y) acc[x][y] = f32x16{};
-
-  // Stage s's loads: half 1 in the second half of iteration s - 4, half 0 in
-  // the first half of iteration s - 3 (as in the dW kernel): 16 instructions
-  // follow the awaited stage's last one at every barrier.
-#pragma unroll
-  for (int s0 = 0; s0 < v3::kNBuf - 1; ++s0)
-#pragma unroll
-    for (int j = 0; j < v3::kDma; ++j) dma_one3(D, (j + 4) & 7, s0);
-  ghost_stage_sync3();
-#pragma unroll
-  for (int j = 4; j < 8; ++j) dma_one3(D, j, v3::kNBuf - 1);
-#pragma unroll
-  for (int x = 0; x < 4; ++x) f0a[x] = *(const u32x4*)(L + (128 * wm + 32 * x) * v3::kSB + c0);
-#pragma unroll
-  for (int y = 0; y < 4; ++y) f0b[y] = *(const u32x4*)(L + (v3::kB + 128 * wn + 32 * y) * v3::kSB + c0);
-
-#define DA_GHOST_ITER3                                                                                  \
-  {                                                                                                     \
-    ghost_half3<DT>(acc, f0a, f0b, true, L + (st % v3::kNBuf) * v3::kStage, c1, wm, wn, f1a, f1b, D, 0,  \
-                    st + v3::kNBuf - 1);                                                                \
-    ghost_stage_sync3();                                                                                \
-    ghost_half3<DT>(acc, f1a, f1b, true, L + ((st + 1) % v3::kNBuf) * v3::kStage, c0, wm, wn, f0a, f0b,  \
-                    D, 1, st + v3::kNBuf);                                                              \
-  }
-  for (int st = 0; st < na; ++st) DA_GHOST_ITER3
-  // K_a complete: round to bf16 pairs, free the accumulators for K_g.
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        kab[x][y][q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
-                                                        f32x2{acc[x][y][2 * q], acc[x][y][2 * q + 1]}, bf16x2));
-      acc[x][y] = f32x16{};
-    }
-  for (int st = na; st + 1 < nst; ++st) DA_GHOST_ITER3
-#undef DA_GHOST_ITER3
-  ghost_half3<DT>(acc, f0a, f0b, true, L + ((nst - 1) % v3::kNBuf) * v3::kStage, c1, wm, wn, f1a, f1b, D, -1, 0);
-  ghost_half3<DT>(acc, f1a, f1b, false, L, 0, wm, wn, f0a, f0b, D, -1, 0);
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Dense mode on the 256 x 256 engine: one tile inside one sample pair.
-template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v3(GhostArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[v3::kNBuf * v3::kStage];
-  __shared__ float red[kThreads / kWave];
-  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t per_group = (int64_t)kGroup * g.n_c;
-  const int64_t group = logical / per_group;
-  const int64_t first_r = group * kGroup;
-  const int64_t gsize = min(g.n_r - first_r, (int64_t)kGroup);
-  const int64_t in_group = logical - group * per_group;
-  const int64_t R = first_r + in_group % gsize;
-  const int64_t C = in_group / gsize;
-  const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
-  const int64_t j = C / g.tiles_c, ss = C % g.tiles_c;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-  const int64_t len1 = seg_len(g.s1, i), len2 = seg_len(g.s2, j);
-  const int64_t t0 = tt * v3::kB, s0 = ss * v3::kB;
-  float* dst = g.partial + ((i * g.s2.batch + j) * g.tiles_r + tt) * g.tiles_c + ss;
-  if (t0 >= len1 || s0 >= len2) {
-    if (tid == 0) *dst = 0.f;
-    return;
-  }
-  // Waves 0, 1 load side-1 rows, waves 2, 3 side-2 rows (dense layout only).
-  const bool side1 = wave < 2;
-  const SideDev& sd = side1 ? g.s1 : g.s2;
-  const int64_t smp = side1 ? i : j, len = side1 ? len1 : len2, r0 = side1 ? t0 : s0;
-  TileSrc3 S;
-  S.ra = make_rsrc(sd.act + smp * sd.act_bstride, 0x7fffffffu);
-  S.rg = make_rsrc(sd.grad + smp * sd.grad_bstride, 0x7fffffffu);
-  S.kbytes_a = g.kbytes_a;
-  S.kbytes_g = g.kbytes_g;
-#pragma unroll
-  for (int q = 0; q < v3::kDma; ++q) {
-    const int row = dma_row3(wave, q, lane) - (side1 ? 0 : v3::kB);
-    const int64_t t = r0 + row;
-    S.roff_a[q] = t < len ? (uint32_t)(t * sd.act_tstride) : v3::kOob;
-    S.roff_g[q] = t < len ? (uint32_t)(t * sd.grad_tstride) : v3::kOob;
-  }
-  f32x16 acc[4][4];
-  uint32_t kab[4][4][8];
-  ghost_tile_engine3<DT>(S, smem, acc, kab);
-  float s = 0.f;
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t w = kab[x][y][q];
-        s += (__uint_as_float(w << 16) + g.bias) * acc[x][y][2 * q];
-        s += (__uint_as_float(w & 0xffff0000u) + g.bias) * acc[x][y][2 * q + 1];
-      }
-  s = wave_sum(s);
-  if (lane == 0) red[wave] = s;
-  __syncthreads();
-  if (tid == 0) *dst = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // Dense / per-sample segmented mode: a 256 x 128 tile inside one sample pair.

@@ -12,15 +12,18 @@
 //     bmm(g_p^T, a_p) flattened to (B, k_g*k_a) (materialize.py:114-116).
 //
 // Both are bound by streaming the factor rows from HBM (the projected widths
-// are <= 64, so every input byte meets at most 2*64 flops).  A workgroup owns
-// 64 rows (4 waves x 16) and up to 64 projected columns; each wave feeds its
-// rows straight from HBM into 16x16x32 MFMAs (four lanes per row, 64
-// contiguous bytes per load instruction, prefetched one stage ahead), while
-// the transposed projection matrix P^T -- tiny, L2-resident and shared by
-// the four waves -- is staged through double-buffered LDS.  The fused kernel
-// runs the activation and gradient projections back to back for one 64-token
-// chunk of one sample, parks both (64 x 64 fp32) in LDS and contracts them over
-// the chunk's tokens; chunk partials are summed in a fixed order.
+// are <= 64, so every input byte meets at most 2*64 flops); each factor row is
+// read once.
+//
+//   project_rows_stream  128-token chunks, factor and projection rows staged
+//                        HBM -> LDS by buffer loads (da_project_rows).
+//   project_pieces       stream-K over both sides of da_project_outer: equal
+//                        ranges of 512-byte k-blocks per workgroup, fp32 partial
+//                        projections ("pieces") at item boundaries;
+//   outer_from_pieces    then sums each sample's pieces in a fixed order and
+//                        contracts them on fp32 MFMAs.
+//   project_tile / project_outer_kernel / project_rows_kernel: register-fed
+//                        kernels for rows the buffer-offset paths cannot address.
 #include "common.h"
 
 namespace da {

@@ -237,7 +237,10 @@ int da_project_rows(const void* x, int dtype, int64_t rows, int64_t d, int64_t x
  *   g_p = g . P_out                (B, T, kg)      P_out^T = pout_t (kg, D)
  *   out[b*out_bstride + o*ka + i] = sum_t g_p[b,t,o] * a_p[b,t,i]
  *
- * ka, kg <= 64 (DA_ERR_UNSUPPORTED above).  One pass over a and g.
+ * ka, kg <= 64 (DA_ERR_UNSUPPORTED above).  One pass over a and g.  The
+ * workspace size depends on the current device's CU count (one partial
+ * projection per CU at most): query it with the device current on which the
+ * call will run.
  */
 int da_project_outer_workspace(int64_t batch, int64_t tokens, int64_t ka, int64_t kg, size_t* bytes);
 int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens, int64_t K,
