@@ -127,6 +127,162 @@ __global__ __launch_bounds__(kThreads) void score_gemm_chunks(ScoreArgs s) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming form: stream-K over 512-byte units of width through an LDS ring.
+//
+// The width of every layer is cut into units of 512 bytes (4 blocks of 128 B);
+// the units of all layers form one sequence per output tile, and workgroup w
+// of the tile's nwg owns units [w*U/nwg, (w+1)*U/nwg), accumulating across
+// layer boundaries into one 16 x 64 partial (the score sums over layers).  A
+// stage is one unit of the tile's 16 side-1 rows and 64 side-2 rows: 80 rows x
+// 4 blocks, each DMA instruction 8 rows x one 128-byte block (with the
+// k-blocked layout of the scoring loop, 1 KB contiguous), into a 4-deep ring.
+// Rows past a side's end and bytes past a layer's width read as zero.  Wave w
+// loads block w of every stage and multiplies it: 2 x 4 16x16x32 MFMAs.  LDS
+// row r of a block holds logical 16-byte chunk c in slot c ^ ((r/2) % 8): the
+// 16 rows of a fragment, 128 bytes apart, then hit 16 distinct bank groups.
+// ---------------------------------------------------------------------------
+namespace sr {
+constexpr int kRows = kTileM + kTileN;   // 80 LDS rows per block
+constexpr int kBlkB = 128;               // bytes per block
+constexpr int kUnitB = 4 * kBlkB;        // 512 bytes of width per unit
+constexpr int kStage = 4 * kRows * kBlkB;  // 40 KB
+constexpr int kNBuf = 4;                 // three stages in flight
+constexpr int kDma = kRows / 8;          // 10 instructions per wave and stage
+constexpr uint32_t kOob = 0x80000000u;
+static_assert(kNBuf * kStage <= 160 * 1024, "LDS");
+static_assert(kDma == 10 && kNBuf == 4, "the vmcnt wait below is 10 * (kNBuf - 2) = 20");
+}  // namespace sr
+
+struct RingLayer {
+  const char* m1;
+  const char* m2;
+  int64_t bytes;                 // row width in bytes
+  int64_t ld1, ld2, blk1, blk2;  // row and 128-byte-block strides, bytes
+  int64_t units, u0;             // units of this layer and its first unit in the sequence
+};
+
+struct RingArgs {
+  RingLayer layers[kMaxLayers];
+  int n_layers;
+  int64_t units;          // units of all layers
+  int64_t nwg;            // workgroups per output tile
+  int64_t b1, b2, tiles_n;
+  float* partial;         // [b1][b2][nwg]
+};
+
+__device__ __forceinline__ int64_t ring_first(int64_t w, const RingArgs& a) { return w * a.units / a.nwg; }
+
+template <int DT>
+__global__ __launch_bounds__(kThreads, 1) void score_ring(RingArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[sr::kNBuf * sr::kStage];
+  lds_char* const Ls = (lds_char*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)Ls;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  const int64_t tile = blockIdx.x / a.nwg, w = blockIdx.x % a.nwg;
+  const int64_t tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  const int64_t ub = uniform64(ring_first(w, a));
+  const int nloc = __builtin_amdgcn_readfirstlane((int)(ring_first(w + 1, a) - ub));
+
+  // DMA instruction i of wave w: LDS rows 8i .. 8i+7 of block w (rows < 16:
+  // side 1, row tm*16 + r; else side 2, row tn*64 + r - 16); lane l -> row
+  // 8i + l/8, slot l%8 holding chunk (l%8) ^ ((row/2) % 8).
+  int rowv[sr::kDma];
+  uint32_t cbo[sr::kDma];
+#pragma unroll
+  for (int i = 0; i < sr::kDma; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    cbo[i] = 16u * (uint32_t)((lane & 7) ^ ((r >> 1) & 7));
+    const int64_t row = i < 2 ? tm * kTileM + r : tn * kTileN + r - kTileM;  // row of its side
+    rowv[i] = row < (i < 2 ? a.b1 : a.b2) ? (i < 2 ? r : r - kTileM) : -1;      // row of the tile, or dead
+  }
+  // issue cursor: layer il, unit iu of the layer, and the layer's per-lane offsets
+  int il = 0;
+  while (il + 1 < a.n_layers && a.layers[il + 1].u0 <= ub) ++il;
+  int64_t iu = uniform64(ub - a.layers[il].u0);
+  uint32_t roff[sr::kDma];
+  uint32_t lbytes = 0;
+  int64_t lunits = 0, blk1 = 0, blk2 = 0;
+  const char* m1 = nullptr;  // the tile's first row of each side
+  const char* m2 = nullptr;
+  auto set_layer = [&]() __attribute__((always_inline)) {
+    const RingLayer& Ly = a.layers[il];
+    m1 = Ly.m1 + tm * kTileM * Ly.ld1;
+    m2 = Ly.m2 + tn * kTileN * Ly.ld2;
+    blk1 = Ly.blk1;
+    blk2 = Ly.blk2;
+    lbytes = (uint32_t)min(Ly.bytes, (int64_t)0x7fffffff);
+    lunits = Ly.units;
+#pragma unroll
+    for (int i = 0; i < sr::kDma; ++i)
+      roff[i] = rowv[i] < 0 ? sr::kOob
+                            : (uint32_t)(rowv[i] * (i < 2 ? Ly.ld1 : Ly.ld2) + uwave * (i < 2 ? Ly.blk1 : Ly.blk2)) + cbo[i];
+  };
+  auto issue = [&](int slot, bool live, bool more) __attribute__((always_inline)) {
+    // the unit's first block of every row is the resource base; block w, chunk, row are per-lane offsets
+    const u32x4 r1 = uniform4(make_rsrc(m1 + iu * 4 * blk1, 0x7fffffffu));
+    const u32x4 r2 = uniform4(make_rsrc(m2 + iu * 4 * blk2, 0x7fffffffu));
+    const uint32_t kin = (uint32_t)iu * sr::kUnitB + (uint32_t)uwave * sr::kBlkB;  // byte of the layer row
+    const uint32_t dst0 = lds0 + (uint32_t)(slot * sr::kStage + uwave * sr::kRows * sr::kBlkB);
+#pragma unroll
+    for (int i = 0; i < sr::kDma; ++i) {
+      const bool en = live & (roff[i] != sr::kOob) & (kin + cbo[i] < lbytes);
+      dma16(i < 2 ? r1 : r2, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
+    }
+    if (live && ++iu == lunits) {
+      iu = 0;
+      do {
+        ++il;
+      } while (il < a.n_layers && a.layers[il].units == 0);
+      if (more) set_layer();
+    }
+  };
+
+  set_layer();
+  int ix = 0;
+#pragma unroll
+  for (int p = 0; p < sr::kNBuf - 1; ++p, ++ix) issue(p, ix < nloc, ix + 1 < nloc);
+
+  const int r16 = lane & 15, q = lane >> 4;
+  const int sw = (r16 >> 1) & 7;
+  f32x4 acc[4] = {};
+  int slot = 0;
+  for (int x = 0; x < nloc; ++x, ++ix) {
+    // this wave's loads of stage x done (the next stage's 10 may be in
+    // flight), its LDS reads done; then every wave's block is visible and the
+    // slot read one stage ago may be refilled
+    asm volatile("s_waitcnt vmcnt(20) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(slot == 0 ? sr::kNBuf - 1 : slot - 1, ix < nloc, ix + 1 < nloc);
+    const lds_char* bb = Ls + slot * sr::kStage + wave * sr::kRows * sr::kBlkB;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int so = (((4 * ks + q) ^ sw) << 4);
+      const u32x4 va = *(const u32x4*)(bb + r16 * sr::kBlkB + so);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const u32x4 vb = *(const u32x4*)(bb + (kTileM + 16 * cb + r16) * sr::kBlkB + so);
+        Mfma16<DT>::mma(acc[cb], va, vb);
+      }
+    }
+    slot = slot + 1 == sr::kNBuf ? 0 : slot + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // the four waves' tiles through LDS, summed in wave order
+  float* red = (float*)smem;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[(wave * kTileM + acc16_row(e, lane)) * kTileN + 16 * cb + acc16_col(lane)] = acc[cb][e];
+  __syncthreads();
+  for (int x = tid; x < kTileM * kTileN; x += kThreads) {
+    const int row = x / kTileN, col = x % kTileN;
+    const float v = ((red[x] + red[kTileM * kTileN + x]) + red[2 * kTileM * kTileN + x]) + red[3 * kTileM * kTileN + x];
+    const int64_t oi = tm * kTileM + row, oj = tn * kTileN + col;
+    if (oi < a.b1 && oj < a.b2) a.partial[(oi * a.b2 + oj) * a.nwg + w] = v;
+  }
+}
+
 // One workgroup per output: its n_chunks partials are contiguous; each thread
 // sums a fixed strided subset, then a fixed tree combines the threads.
 __global__ __launch_bounds__(256) void score_gemm_reduce(const float* __restrict__ partial,
@@ -152,7 +308,26 @@ __global__ __launch_bounds__(256) void score_gemm_reduce(const float* __restrict
 struct Plan {
   int64_t chunk_bytes, n_chunks;
   size_t ws;
+  bool ring;              // streaming form (2-byte dtypes, offsets within a tile fit 32 bits)
+  int64_t units, nwg;     // its units and workgroups per tile
 };
+
+// Workgroup slots on the current device: one per CU.
+int ring_slots(int64_t* n) {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "hipGetDevice failed");
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+    *n = cache[dev];
+    return DA_OK;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
+  if (dev >= 0 && dev < 64) cache[dev] = cus;
+  *n = cus;
+  return DA_OK;
+}
 
 int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
               Plan* p) {
@@ -186,6 +361,33 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
   for (int l = 0; l < n_layers; ++l) n += (layers[l].width * es + cb - 1) / cb;
   p->n_chunks = n;
   p->ws = (size_t)(n * b1 * b2) * sizeof(float);
+  // Streaming form: 2-byte dtypes (a 64-element block is one 128-byte run);
+  // per-lane offsets within one tile and the row widths fit 32 bits.
+  const int64_t lim = (1LL << 31) - (1LL << 20);
+  p->ring = es == 2 && b1 > 0 && b2 > 0;
+  int64_t units = 0;
+  for (int l = 0; l < n_layers && p->ring; ++l) {
+    const da_dense_layer& L = layers[l];
+    const int64_t bytes = L.width * es, ld1 = L.ld1 * es, ld2 = L.ld2 * es;
+    const int64_t bk1 = (L.blk1 ? L.blk1 : 64) * es, bk2 = (L.blk2 ? L.blk2 : 64) * es;
+    if (bytes >= lim || (kTileN - 1) * ld1 + 4 * bk1 >= lim || (kTileN - 1) * ld2 + 4 * bk2 >= lim) p->ring = false;
+    units += (bytes + sr::kUnitB - 1) / sr::kUnitB;
+  }
+  if (p->ring && units > 0) {
+    int64_t slots = 0;
+    const int rc = ring_slots(&slots);
+    if (rc) return rc;
+    const int64_t tiles = ((b1 + kTileM - 1) / kTileM) * ((b2 + kTileN - 1) / kTileN);
+    int64_t nwg = slots / tiles;
+    if (nwg < 1) nwg = 1;
+    if (nwg > units) nwg = units;
+    p->units = units;
+    p->nwg = nwg;
+    if (tiles * nwg > 0x7fffffffLL || units / nwg > (1LL << 30)) p->ring = false;
+    else p->ws = (size_t)(nwg * b1 * b2) * sizeof(float);
+  } else {
+    p->ring = false;
+  }
   return DA_OK;
 }
 
@@ -223,6 +425,43 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
     return set_error(DA_ERR_WORKSPACE, "da_score_gemm: workspace needs %zu bytes, got %zu", p.ws,
                      workspace_bytes);
   const int64_t es = (int64_t)elem_bytes(dtype);
+  if (p.ring) {
+    RingArgs r;
+    r.n_layers = n_layers;
+    int64_t u = 0;
+    for (int l = 0; l < n_layers; ++l) {
+      RingLayer& Ly = r.layers[l];
+      Ly.m1 = (const char*)layers[l].m1;
+      Ly.m2 = (const char*)layers[l].m2;
+      Ly.bytes = layers[l].width * es;
+      Ly.ld1 = layers[l].ld1 * es;
+      Ly.ld2 = layers[l].ld2 * es;
+      Ly.blk1 = (layers[l].blk1 ? layers[l].blk1 : 64) * es;
+      Ly.blk2 = (layers[l].blk2 ? layers[l].blk2 : 64) * es;
+      Ly.units = (Ly.bytes + sr::kUnitB - 1) / sr::kUnitB;
+      Ly.u0 = u;
+      u += Ly.units;
+    }
+    r.units = p.units;
+    r.nwg = p.nwg;
+    r.b1 = b1;
+    r.b2 = b2;
+    r.tiles_n = (b2 + kTileN - 1) / kTileN;
+    r.partial = (float*)workspace;
+    const int64_t tiles = ((b1 + kTileM - 1) / kTileM) * r.tiles_n;
+    const unsigned grid = (unsigned)(tiles * p.nwg);
+    switch (dtype) {
+      case DA_BF16: score_ring<DA_BF16><<<grid, kThreads, 0, st>>>(r); break;
+      default: score_ring<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+    }
+    rc = check_launch("da_score_gemm(ring)");
+    if (rc) return rc;
+    const int64_t n = b1 * b2;
+    if (n > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_score_gemm: too many outputs");
+    score_gemm_reduce<<<(unsigned)n, 256, 0, st>>>((const float*)workspace, p.nwg, b1, b2, out, ld_row, ld_col,
+                                                   accumulate);
+    return check_launch("da_score_gemm(reduce)");
+  }
   ScoreArgs s;
   s.n_layers = n_layers;
   int64_t c = 0;

@@ -320,6 +320,8 @@ def score_gemm(
         return m, m.stride(0), 64
 
     for m1, m2 in flat:
+        if width(m1) == 0:  # contributes nothing (and an empty tensor's strides are arbitrary)
+            continue
         w = -(-width(m1) // vec) * vec
         (m1, ld1, bk1), (m2, ld2, bk2) = operand(m1, w), operand(m2, w)
         keep += [m1, m2]
@@ -330,6 +332,10 @@ def score_gemm(
     ld_row, ld_col = (out.stride(1), out.stride(0)) if swap else (out.stride(0), out.stride(1))
     lib = nat.load()
     code = nat.dtype_code(dtype)
+    if not layers:  # every layer empty: the library writes the zero product (or leaves out to accumulate)
+        nat.check(lib.da_score_gemm(n1, n2, None, 0, code, out.data_ptr(), ld_row, ld_col, int(accumulate),
+                                    None, 0, nat.stream_ptr(dev)), "score_gemm")
+        return out
     for start in range(0, len(layers), 32):
         group = layers[start : start + 32]
         arr = (nat.DenseLayer * len(group))(*group)

@@ -172,7 +172,9 @@ typedef struct da_dense_layer {
  *   out[i*ld_row + j*ld_col] (+)= sum_L sum_c m1_L[i,c] * m2_L[j,c]
  *
  * All layers share one dtype; at most 32 layers per call.  Deterministic
- * (fixed-order split-K reduction through the workspace).
+ * (fixed-order split-K reduction through the workspace).  For 2-byte dtypes
+ * the workspace size depends on the current device's CU count (one partial
+ * tile per CU): query it with the device current on which the call will run.
  * Replaces the dense products of cross_gram / cross_dot,
  * dattri_llm/gradient/ops/dot.py:114 and :501-505, and the layer sum of
  * layerwise_cross_dot, dot.py:599-604.

@@ -93,6 +93,7 @@ SCORE_CASES = [
     (70, 20, [520, 8, 2000]),        # b1 > b2 -> transposed launch; b1 > 32
     (1, 1, [8]),
     (33, 130, [4104]),
+    (4, 64, [16384] * 6 + [0, 136] + [16384] * 6),  # workgroup ranges across layers, an empty layer
 ]
 
 
