@@ -738,6 +738,120 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
   if (tid == 0) *dst = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// ---------------------------------------------------------------------------
+// Per-token cross-gram on the 256 x 128 engine: K[i, t, j] keeps side 1's
+// token t and sums side 2 out (the token decomposition of the score).
+//
+//   factorized side 2:  K[i,t,j] = sum_s (a1_it . a2_js + bias)(g1_it . g2_js)
+//   dense side 2:       K[i,t,j] = sum_o (a1_it . M2_j[o,:] + mb_j[o]) g1_it[o]
+//
+// The factorized form is the ghost tile with a row epilogue; the dense form
+// runs the engine's second product alone over a1 rows against M2_j's rows (the
+// output channels o play side 2's tokens) and multiplies by g1 in the
+// epilogue.  Each tile parks its (256 x 128) products in LDS and sums every
+// row over its 128 columns; a second kernel adds the column tiles in order.
+// ---------------------------------------------------------------------------
+struct PerTokArgs {
+  SideDev s1, s2;                  // dense form: s2.grad = M2 rows (tokens = D)
+  int64_t kbytes_a, kbytes_g;
+  int64_t tiles_r, tiles_c, n_r, n_c;
+  float bias;                      // factorized: the implicit ones column
+  const float* m2bias;             // dense: (B2, D) fp32 bias-column gradients, or nullptr
+  int64_t m2bias_ld;               // floats between samples
+  int64_t tpad;                    // tiles_r * 256
+  float* partial;                  // [B1][B2][tpad][tiles_c]
+};
+
+template <int DT, bool kDense>
+__global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
+  constexpr int64_t kRowGroup = 4;
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t per_group = kRowGroup * g.n_c;
+  const int64_t group = logical / per_group;
+  const int64_t first_r = group * kRowGroup;
+  const int64_t gsize = min(g.n_r - first_r, kRowGroup);
+  const int64_t in_group = logical - group * per_group;
+  const int64_t R = first_r + in_group % gsize;
+  const int64_t C = in_group / gsize;
+  const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
+  const int64_t j = C / g.tiles_c, ss = C % g.tiles_c;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t len1 = g.s1.tokens, len2 = g.s2.tokens;
+  const int64_t t0 = tt * v2::kBM, s0 = ss * v2::kBN;
+  if (t0 >= len1) return;  // uniform: no row of this tile is read back
+  TileSrc S;
+  S.ra1 = make_rsrc(g.s1.act + i * g.s1.act_bstride, 0x7fffffffu);
+  S.rg1 = make_rsrc((kDense ? g.s1.act : g.s1.grad) + i * (kDense ? g.s1.act_bstride : g.s1.grad_bstride),
+                    0x7fffffffu);
+  S.ra2 = make_rsrc(g.s2.grad + j * g.s2.grad_bstride, 0x7fffffffu);
+  S.rg2 = make_rsrc(g.s2.grad + j * g.s2.grad_bstride, 0x7fffffffu);
+  if (!kDense) S.ra2 = make_rsrc(g.s2.act + j * g.s2.act_bstride, 0x7fffffffu);
+  S.kbytes_a = g.kbytes_a;
+  S.kbytes_g = g.kbytes_g;
+#pragma unroll
+  for (int q = 0; q < v2::kDma; ++q) {
+    const int row = dma_row(wave, q, lane);
+    const bool side1 = row < v2::kBM;
+    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
+    if (t < (side1 ? len1 : len2)) {
+      // dense form: side 1 streams a1 rows and side 2 M2_j rows, both in the gradient loop
+      const int64_t ts1 = kDense ? g.s1.act_tstride : g.s1.grad_tstride;
+      S.roff_a[q] = (uint32_t)(t * (side1 ? g.s1.act_tstride : g.s2.act_tstride));
+      S.roff_g[q] = (uint32_t)(t * (side1 ? ts1 : g.s2.grad_tstride));
+    } else {
+      S.roff_a[q] = v2::kOob;
+      S.roff_g[q] = v2::kOob;
+    }
+  }
+  f32x16 ka[4][2], kg[4][2];
+  ghost_tile_engine<DT>(S, smem, ka, kg);
+  float* P = (float*)smem;
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 128 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
+        float v;
+        if constexpr (kDense) {
+          const int64_t t = t0 + row, o = s0 + col;
+          const bool ok = t < len1 && o < len2;
+          const float gv = ok ? Elem<DT>::load(g.s1.grad + i * g.s1.grad_bstride + t * g.s1.grad_tstride, o) : 0.f;
+          const float mb = (ok && g.m2bias) ? g.m2bias[j * g.m2bias_ld + o] : 0.f;
+          v = (kg[x][y][r] + mb) * gv;
+        } else {
+          v = (ka[x][y][r] + g.bias) * kg[x][y][r];
+        }
+        P[row * v2::kPRow + col] = v;
+      }
+  __syncthreads();
+  // one thread per row: the row's 128 columns in order (zero past side 2's end)
+  const int64_t t = t0 + tid;
+  if (t < len1) {
+    const float* pr = P + tid * v2::kPRow;
+    float sum = 0.f;
+    for (int c = 0; c < v2::kBN; ++c) sum += pr[c];
+    g.partial[((i * g.s2.batch + j) * g.tpad + t) * g.tiles_c + ss] = sum;
+  }
+}
+
+// out[i*ld_b1 + t*ld_t + j*ld_b2] (+)= sum over column tiles, in order.
+__global__ void per_token_reduce(const float* __restrict__ partial, int64_t b1, int64_t len1, int64_t b2,
+                                 int64_t tpad, int64_t tiles_c, float* __restrict__ out, int64_t ld_b1,
+                                 int64_t ld_t, int64_t ld_b2, int accumulate) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= b1 * len1 * b2) return;
+  const int64_t j = idx % b2, t = (idx / b2) % len1, i = idx / (b2 * len1);
+  const float* p = partial + ((i * b2 + j) * tpad + t) * tiles_c;
+  float s = 0.f;
+  for (int64_t q = 0; q < tiles_c; ++q) s += p[q];
+  float* o = out + i * ld_b1 + t * ld_t + j * ld_b2;
+  *o = accumulate ? *o + s : s;
+}
+
 struct Plan {
   int64_t tiles_r, tiles_c, n_r, n_c, per_pair;
   size_t ws;
@@ -813,6 +927,48 @@ SideDev to_dev(const da_factor_side* s, int64_t es) {
   return d;
 }
 
+
+// Per-token plans.  Both forms need dense sides (one row range per sample)
+// whose rows the 256 x 128 engine addresses with 32-bit offsets.
+struct PerTokPlan {
+  int64_t tiles_r, tiles_c, tpad;
+  size_t ws;
+};
+
+int per_token_plan(const da_factor_side* s1, int64_t b2, int64_t len2, int64_t K, int64_t D, int dtype,
+                   const char* who, PerTokPlan* p) {
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype %d", who, dtype);
+  if (K < 0 || D < 0 || b2 < 0 || len2 < 0) return set_error(DA_ERR_INVALID, "%s: negative size", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if ((K * es) % 16 || (D * es) % 16)
+    return set_error(DA_ERR_INVALID, "%s: K=%lld and D=%lld must be multiples of %lld elements", who,
+                     (long long)K, (long long)D, (long long)(16 / es));
+  if (!s1) return set_error(DA_ERR_INVALID, "%s: s1 is NULL", who);
+  p->tiles_r = (s1->tokens + v2::kBM - 1) / v2::kBM;
+  p->tiles_c = (len2 + v2::kBN - 1) / v2::kBN;
+  p->tpad = p->tiles_r * v2::kBM;
+  p->ws = (size_t)(s1->batch * b2 * p->tpad * p->tiles_c) * sizeof(float);
+  return DA_OK;
+}
+
+int per_token_launch(const PerTokArgs& g, bool dense, int dtype, int64_t len1, float* out, int64_t ld_b1,
+                     int64_t ld_t, int64_t ld_b2, int accumulate, hipStream_t st, const char* who) {
+  const int64_t tiles = g.n_r * g.n_c;
+  if (tiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+#define DA_PT(DT)                                                                                            if (dense) ghost_per_token_v2<DT, true><<<(unsigned)tiles, kThreads, 0, st>>>(g);                           else ghost_per_token_v2<DT, false><<<(unsigned)tiles, kThreads, 0, st>>>(g);
+  switch (dtype) {
+    case DA_BF16: DA_PT(DA_BF16) break;
+    case DA_F16: DA_PT(DA_F16) break;
+    default: DA_PT(DA_F32) break;
+  }
+#undef DA_PT
+  int rc = check_launch(who);
+  if (rc) return rc;
+  const int64_t n = g.s1.batch * len1 * g.s2.batch;
+  per_token_reduce<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(g.partial, g.s1.batch, len1, g.s2.batch, g.tpad,
+                                                                g.tiles_c, out, ld_b1, ld_t, ld_b2, accumulate);
+  return check_launch(who);
+}
 }  // namespace
 }  // namespace da
 
@@ -1053,6 +1209,123 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
     first_launch = false;
   }
   return DA_OK;
+}
+
+
+int da_ghost_gram_per_token_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D,
+                                      int dtype, size_t* bytes) {
+  using namespace da;
+  if (!bytes || !s2) return set_error(DA_ERR_INVALID, "da_ghost_gram_per_token_workspace: NULL argument");
+  PerTokPlan p;
+  const int rc = per_token_plan(s1, s2->batch, s2->tokens, K, D, dtype, "da_ghost_gram_per_token", &p);
+  if (rc) return rc;
+  *bytes = p.ws;
+  return DA_OK;
+}
+
+int da_ghost_gram_per_token(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D, int dtype,
+                            float* out, int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace da;
+  const char* who = "da_ghost_gram_per_token";
+  if (!s1 || !s2) return set_error(DA_ERR_INVALID, "%s: NULL side", who);
+  PerTokPlan p;
+  int rc = per_token_plan(s1, s2->batch, s2->tokens, K, D, dtype, who, &p);
+  if (rc) return rc;
+  rc = validate_side(s1, K, D, dtype, "s1");
+  if (rc) return rc;
+  rc = validate_side(s2, K, D, dtype, "s2");
+  if (rc) return rc;
+  if (s1->has_bias != s2->has_bias) return set_error(DA_ERR_INVALID, "%s: both sides must agree on has_bias", who);
+  if (s1->batch == 0 || s1->tokens == 0 || s2->batch == 0) return DA_OK;
+  if (!out) return set_error(DA_ERR_INVALID, "%s: out is NULL", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if (s1->seg_offsets || s2->seg_offsets || !fits_v2(s1, K, D, es) || !fits_v2(s2, K, D, es) || D == 0)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: needs dense sides with rows addressable by 32-bit offsets and D > 0",
+                     who);
+  if (!workspace || workspace_bytes < p.ws)
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace needs %zu bytes", who, p.ws);
+  PerTokArgs g;
+  g.s1 = to_dev(s1, es);
+  g.s2 = to_dev(s2, es);
+  g.kbytes_a = K * es;
+  g.kbytes_g = D * es;
+  g.tiles_r = p.tiles_r;
+  g.tiles_c = p.tiles_c;
+  g.n_r = s1->batch * p.tiles_r;
+  g.n_c = s2->batch * p.tiles_c;
+  g.bias = s1->has_bias ? 1.f : 0.f;
+  g.m2bias = nullptr;
+  g.m2bias_ld = 0;
+  g.tpad = p.tpad;
+  g.partial = (float*)workspace;
+  if (s2->tokens == 0) {  // nothing on side 2: the sums are zero
+    g.tiles_c = 0;
+    const int64_t n = s1->batch * s1->tokens * s2->batch;
+    per_token_reduce<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        g.partial, s1->batch, s1->tokens, s2->batch, g.tpad, 0, out, ld_b1, ld_t, ld_b2, accumulate);
+    return check_launch(who);
+  }
+  return per_token_launch(g, false, dtype, s1->tokens, out, ld_b1, ld_t, ld_b2, accumulate, (hipStream_t)stream, who);
+}
+
+int da_dense_per_token_workspace(const da_factor_side* s1, int64_t b2, int64_t K, int64_t D, int dtype,
+                                 size_t* bytes) {
+  using namespace da;
+  if (!bytes) return set_error(DA_ERR_INVALID, "da_dense_per_token_workspace: bytes is NULL");
+  PerTokPlan p;
+  const int rc = per_token_plan(s1, b2, D, K, D, dtype, "da_dense_per_token", &p);
+  if (rc) return rc;
+  *bytes = p.ws;
+  return DA_OK;
+}
+
+int da_dense_per_token(const da_factor_side* s1, const void* m2, int64_t b2, int64_t m2_bstride, int64_t m2_rstride,
+                       const float* m2_bias, int64_t m2_bias_ld, int64_t K, int64_t D, int dtype, float* out,
+                       int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  using namespace da;
+  const char* who = "da_dense_per_token";
+  PerTokPlan p;
+  int rc = per_token_plan(s1, b2, D, K, D, dtype, who, &p);
+  if (rc) return rc;
+  rc = validate_side(s1, K, D, dtype, "s1");
+  if (rc) return rc;
+  if (s1->batch == 0 || s1->tokens == 0 || b2 == 0) return DA_OK;
+  if (!out) return set_error(DA_ERR_INVALID, "%s: out is NULL", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if (K == 0 || D == 0) return set_error(DA_ERR_UNSUPPORTED, "%s: needs K > 0 and D > 0", who);
+  if (!m2 || ((uintptr_t)m2 & 15) || (m2_bstride * es) % 16 || (m2_rstride * es) % 16 || m2_rstride < K ||
+      m2_bstride < 0)
+    return set_error(DA_ERR_INVALID, "%s: m2 rows must be 16-byte aligned, row stride >= K", who);
+  if (s1->has_bias && !m2_bias) return set_error(DA_ERR_INVALID, "%s: a bias column needs m2_bias", who);
+  const int64_t lim = (1LL << 31) - (1LL << 20);
+  if (s1->seg_offsets || !fits_v2(s1, K, D, es) || D * m2_rstride * es + K * es >= lim)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: needs a dense side 1 and rows addressable by 32-bit offsets", who);
+  if (!workspace || workspace_bytes < p.ws)
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace needs %zu bytes", who, p.ws);
+  PerTokArgs g;
+  g.s1 = to_dev(s1, es);
+  g.s2.act = (const char*)m2;
+  g.s2.grad = (const char*)m2;
+  g.s2.batch = b2;
+  g.s2.tokens = D;  // M2_j's rows (output channels) take side 2's tokens
+  g.s2.act_bstride = g.s2.grad_bstride = m2_bstride * es;
+  g.s2.act_tstride = g.s2.grad_tstride = m2_rstride * es;
+  g.s2.seg = nullptr;
+  g.s2.idx = nullptr;
+  g.kbytes_a = 0;  // one product: a1 rows against M2_j rows over K
+  g.kbytes_g = K * es;
+  g.tiles_r = p.tiles_r;
+  g.tiles_c = p.tiles_c;
+  g.n_r = s1->batch * p.tiles_r;
+  g.n_c = b2 * p.tiles_c;
+  g.bias = 0.f;
+  g.m2bias = s1->has_bias ? m2_bias : nullptr;
+  g.m2bias_ld = m2_bias_ld;
+  g.tpad = p.tpad;
+  g.partial = (float*)workspace;
+  return per_token_launch(g, true, dtype, s1->tokens, out, ld_b1, ld_t, ld_b2, accumulate, (hipStream_t)stream, who);
 }
 
 }  // extern "C"

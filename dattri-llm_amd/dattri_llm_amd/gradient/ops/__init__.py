@@ -11,7 +11,10 @@ from dattri_llm_amd.gradient.ops.cost import CostModel, calibrate, get_routing_p
 from dattri_llm_amd.gradient.ops.dot import (
     cross_dot,
     cross_dot_factors,
+    cross_dot_per_token,
     cross_gram,
+    cross_gram_per_token,
+    cross_gram_per_token_dense,
     dot,
     dot_factors,
     effective_dims,
@@ -72,7 +75,8 @@ __all__ = [
     "LINEAR_TYPES", "MASK_KEYS", "NORM_TYPES", "PARAM_GRAD_TYPES", "PROJECTION_STYLES", "CostModel",
     "DattriProjector", "ProjectionMatrix", "apply_projection", "as_float", "calibrate",
     "canonical_class_name", "capture_projected", "compute_dtype", "cost", "cross_dot",
-    "cross_dot_factors", "cross_gram", "dot", "dot_factors", "dtypes", "effective_dims",
+    "cross_dot_factors", "cross_dot_per_token", "cross_gram", "cross_gram_per_token",
+    "cross_gram_per_token_dense", "dot", "dot_factors", "dtypes", "effective_dims",
     "extract_module_kwargs", "gaussian_projector", "get_compute_dtype", "get_routing_policy",
     "grad_norm_sq", "grad_norm_sq_factors", "is_conv", "is_conv_transpose", "is_embedding",
     "is_kfac_eligible", "is_linear", "is_norm", "layerwise_cross_dot", "layerwise_cross_dot_per_token",

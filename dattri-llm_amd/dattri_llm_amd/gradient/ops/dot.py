@@ -32,6 +32,7 @@ from dattri_llm_amd.gradient.ops.materialize import (
     linear_dense,
     materialize,
     materialize_blocked,
+    norm_token_rows,
     norm_grad_from_final,
     norm_grad_from_raw,
 )
@@ -307,11 +308,124 @@ def layerwise_cross_dot(train, test, *, layers: Iterable[str] | None = None, mod
     return total.to(out_dtype)
 
 
-def layerwise_cross_dot_per_token(train, test, *, layers=None, reduce: str = "sum"):
-    """Per-token decomposition (dot.py:607-669) -- not on the MI355X path."""
-    raise NotImplementedError(
-        "token-granularity attribution (cross_gram_per_token) is not implemented on the MI355X path"
-    )
+# ---------------------------------------------------------------------------
+# Per-token decomposition (dot.py:166-299, :607-669)
+# ---------------------------------------------------------------------------
+
+
+def _norm_per_token32(rows1: torch.Tensor, m2: torch.Tensor) -> torch.Tensor:
+    """fp32 (B1, T1, B2): every token row of side 1 against side 2's (B2, d')
+    norm gradients, through the score kernel."""
+    b1, t1, d = rows1.shape
+    return _dense_gram(rows1.reshape(b1 * t1, d), m2.reshape(m2.shape[0], -1)).reshape(b1, t1, m2.shape[0])
+
+
+def _linear_operands(*tensors):
+    (ts), _ = _kernel_operands(*(to_3d(t) for t in tensors))
+    if any(t.ndim == 4 for t in ts):
+        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
+    return ts
+
+
+def cross_gram_per_token(a1, g1, a2, g2, layer_type: str) -> torch.Tensor:
+    """Per-token cross-gram ``K[i, t, j]`` on preprocessed factors
+    (dot.py:171-222): side 1's token t against side 2's whole per-sample
+    gradient; summing over t gives :func:`cross_gram`.  ``(B1, T1, B2)``."""
+    if is_embedding(layer_type):
+        require_supported(layer_type, "cross_gram_per_token")
+    out_dtype = dtypes.resolve(a1, g1, a2, g2)
+    if is_norm(layer_type):
+        if layer_type not in TOKEN_NORM_TYPES:
+            require_supported(layer_type, "cross_gram_per_token")
+        x1, y1, x2, y2 = dtypes.align(to_3d(a1), to_3d(g1), to_3d(a2), to_3d(g2))
+        return _norm_per_token32(x1 * y1, norm_grad_from_final(x2, y2)).to(out_dtype)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, "cross_gram_per_token")
+    a1, g1, a2, g2 = _linear_operands(a1, g1, a2, g2)
+    return kernels.ghost_gram_per_token(a1, g1, a2, g2).to(out_dtype)
+
+
+def cross_gram_per_token_dense(a1, g1, m2, layer_type: str) -> torch.Tensor:
+    """:func:`cross_gram_per_token` with side 2 dense (dot.py:225-263): ``m2`` is
+    the (B2, D) per-sample gradient block in materialize's layout."""
+    if is_embedding(layer_type):
+        require_supported(layer_type, "cross_gram_per_token_dense")
+    out_dtype = dtypes.resolve(a1, g1, m2)
+    m2 = m2.reshape(m2.shape[0], -1)
+    if is_norm(layer_type):
+        if layer_type not in TOKEN_NORM_TYPES:
+            require_supported(layer_type, "cross_gram_per_token_dense")
+        x1, y1 = dtypes.align(to_3d(a1), to_3d(g1))
+        return _norm_per_token32(x1 * y1, m2).to(out_dtype)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, "cross_gram_per_token_dense")
+    a1, g1, m2 = _linear_operands(a1, g1, m2)
+    return kernels.dense_per_token(a1, g1, m2.reshape(m2.shape[0], -1)).to(out_dtype)
+
+
+def cross_dot_per_token(f1, f2, layer_type: str, include_bias: bool = True) -> torch.Tensor:
+    """Per-token cross-gram of a factorized side 1 against side 2 in whatever
+    form it holds (dot.py:266-299); ``(B1, T1, B2)``.  Raw captures are
+    preprocessed inside the kernels (implicit bias column)."""
+    b1 = f1.as_batch_first()
+    a1, g1, mk1 = b1.activation, b1.pre_activation_grad, b1.module_kwargs
+    dense2 = isinstance(f2, torch.Tensor)
+    out_dtype = dtypes.resolve(a1, g1, f2) if dense2 else dtypes.resolve(a1, g1, f2.activation, f2.pre_activation_grad)
+    if layer_type in TOKEN_NORM_TYPES:
+        rows1 = norm_token_rows(a1, g1, layer_type, mk1, include_bias)
+        m2 = f2.reshape(f2.shape[0], -1) if dense2 else materialize(f2, layer_type, include_bias)
+        return _norm_per_token32(rows1, m2).to(out_dtype)
+    if is_embedding(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, "cross_dot_per_token")
+    x1, y1, bias1 = final_linear(a1, g1, layer_type, mk1, include_bias)
+    if dense2:
+        x1, y1, m2 = _linear_operands(x1, y1, f2.reshape(f2.shape[0], -1))
+        return kernels.dense_per_token(x1, y1, m2.reshape(m2.shape[0], -1), bias=bias1).to(out_dtype)
+    b2 = f2.as_batch_first()
+    x2, y2, bias2 = final_linear(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs, include_bias)
+    if bias1 != bias2:
+        raise ValueError("the two sides disagree on the bias column")
+    x1, y1, x2, y2 = _linear_operands(x1, y1, x2, y2)
+    return kernels.ghost_gram_per_token(x1, y1, x2, y2, bias=bias1).to(out_dtype)
+
+
+def layerwise_cross_dot_per_token(train, test, *, layers: Iterable[str] | None = None, reduce: str = "sum"):
+    """Layer-by-layer per-token cross-gram (dot.py:607-669): the
+    ``(B_train, T_train, B_test)`` contribution of every train token position to
+    :func:`layerwise_cross_dot`, which it sums back to exactly over ``T``.  The
+    train side must hold every scored layer factorized with a token axis; the
+    test side may be factorized or dense per layer."""
+    if reduce not in {"sum", "none"}:
+        raise ValueError("reduce must be 'sum' or 'none'")
+    names = list(train.data) if layers is None else list(layers)
+    per_layer: dict[str, torch.Tensor] = {}
+    for name in names:
+        if name not in train.data or name not in test.data:
+            continue
+        if train.layer_types[name] == PARAM_GRAD_TYPES:
+            continue  # a batch-level gradient: no per-sample rows to score
+        tr = train.data[name]
+        if isinstance(tr, torch.Tensor) or train.indexing[name] != "batch_token":
+            raise ValueError(
+                f"layer {name!r} has no token axis on the train side "
+                f"(stored {train.representation[name]}, indexing {train.indexing[name]!r}); token-level "
+                "attribution needs the train gradients captured factorized."
+            )
+        per_layer[name] = cross_dot_per_token(tr, test.data[name], train.layer_types[name])
+    if reduce == "none":
+        return per_layer
+    if not per_layer:
+        raise ValueError("No shared layers between the two gradient blocks.")
+    shapes = {tuple(v.shape) for v in per_layer.values()}
+    if len(shapes) > 1:
+        raise ValueError(
+            "Layers disagree on the token axis, so their per-token contributions cannot be summed: "
+            f"{sorted(shapes)}.  Use reduce='none'."
+        )
+    total = None
+    for v in per_layer.values():
+        total = v.float() if total is None else total + v.float()
+    return total.to(next(iter(per_layer.values())).dtype)
 
 
 # ---------------------------------------------------------------------------

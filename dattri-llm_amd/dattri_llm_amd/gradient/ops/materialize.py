@@ -63,6 +63,23 @@ def linear_dense(a, g, bias: bool) -> torch.Tensor:
     return out.to(out_dtype)
 
 
+def norm_token_rows(a, g, layer_type: str, module_kwargs: dict | None = None,
+                    include_bias: bool = True) -> torch.Tensor:
+    """(B, T, d') per-token norm gradients x_hat * g (with a bias, [x_hat * g, g]):
+    the terms whose token sum is the norm weight gradient (materialize.py:96-98)."""
+    if module_kwargs is not None:
+        spec = norm_spec(a, layer_type, module_kwargs, include_bias)
+        x_hat = kernels.norm_xhat(a, kind=spec.kind, eps=spec.eps)
+        x3, g3 = fold_norm_rows(x_hat, spec.width), fold_norm_rows(g, spec.width)
+        if spec.has_bias:
+            x3 = torch.cat([x3, torch.ones_like(x3)], dim=-1)
+            g3 = torch.cat([g3, g3], dim=-1)
+    else:
+        x3, g3 = to_3d(a), to_3d(g)
+    x3, g3 = dtypes.align(x3, g3)
+    return x3 * g3
+
+
 def materialize_factors(
     a: torch.Tensor,
     g: torch.Tensor,
@@ -81,17 +98,7 @@ def materialize_factors(
         require_supported(layer_type, "materialize_factors")
     if layer_type in TOKEN_NORM_TYPES:
         if per_token:
-            if module_kwargs is not None:
-                spec = norm_spec(a, layer_type, module_kwargs, include_bias)
-                x_hat = kernels.norm_xhat(a, kind=spec.kind, eps=spec.eps)
-                x3, g3 = fold_norm_rows(x_hat, spec.width), fold_norm_rows(g, spec.width)
-                if spec.has_bias:
-                    x3 = torch.cat([x3, torch.ones_like(x3)], dim=-1)
-                    g3 = torch.cat([g3, g3], dim=-1)
-            else:
-                x3, g3 = to_3d(a), to_3d(g)
-            x3, g3 = dtypes.align(x3, g3)
-            return (x3 * g3).flatten(1)
+            return norm_token_rows(a, g, layer_type, module_kwargs, include_bias).flatten(1)
         if module_kwargs is not None:
             return norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
         return norm_grad_from_final(a, g)

@@ -118,6 +118,116 @@ def ghost_gram(
     return out
 
 
+def _per_token_out(out, b1, t1, b2, dev, accumulate):
+    if out is None:
+        return torch.empty(b1, t1, b2, dtype=torch.float32, device=dev), False
+    if out.dtype != torch.float32 or tuple(out.shape) != (b1, t1, b2):
+        raise ValueError("out must be a float32 (B1, T1, B2) tensor")
+    return out, accumulate
+
+
+def ghost_gram_per_token(
+    a1: torch.Tensor,
+    g1: torch.Tensor,
+    a2: torch.Tensor,
+    g2: torch.Tensor,
+    *,
+    bias: bool = False,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Per-token cross-gram of one linear layer, fp32 ``(B1, T1, B2)``:
+    ``K[i, t, j] = sum_s (a1_it . a2_js + bias)(g1_it . g2_js)``, i.e. side 1's
+    token t against side 2's whole per-sample gradient (``da_ghost_gram_per_token``).
+    Factors as for :func:`ghost_gram`."""
+    dev = nat.require_device(a1, g1, a2, g2)
+    if a1.dim() != 3 or g1.dim() != 3 or a2.dim() != 3 or g2.dim() != 3:
+        raise ValueError("ghost_gram_per_token expects 3-D (B, S, width) factors")
+    if not (a1.dtype == g1.dtype == a2.dtype == g2.dtype):
+        raise ValueError("ghost_gram_per_token factors must share one dtype")
+    if a1.shape[:2] != g1.shape[:2] or a2.shape[:2] != g2.shape[:2]:
+        raise ValueError("activation and gradient factors disagree on (B, S)")
+    if a1.shape[-1] != a2.shape[-1] or g1.shape[-1] != g2.shape[-1]:
+        raise ValueError("the two sides disagree on the layer widths")
+    code = nat.dtype_code(a1.dtype)
+    vec = _chunk_elems(a1.dtype)
+    k = -(-a1.shape[-1] // vec) * vec
+    d = -(-g1.shape[-1] // vec) * vec
+    a1, a2 = prepare_rows(a1, k), prepare_rows(a2, k)
+    g1, g2 = prepare_rows(g1, d), prepare_rows(g2, d)
+    b1, t1, b2 = a1.shape[0], a1.shape[1], a2.shape[0]
+    out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
+    s1, s2 = _side(a1, g1, bias), _side(a2, g2, bias)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_ghost_gram_per_token_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)),
+              "ghost_gram_per_token")
+    ws = nat.workspace(nbytes.value, dev)
+    nat.check(
+        lib.da_ghost_gram_per_token(s1, s2, k, d, code, out.data_ptr(), out.stride(0), out.stride(1),
+                                    out.stride(2), int(accumulate), ws.data_ptr(), ws.numel(),
+                                    nat.stream_ptr(dev)),
+        "ghost_gram_per_token",
+    )
+    return out
+
+
+def dense_per_token(
+    a1: torch.Tensor,
+    g1: torch.Tensor,
+    m2: torch.Tensor,
+    *,
+    bias: bool = False,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Per-token cross-gram against dense per-sample gradients, fp32
+    ``(B1, T1, B2)``: ``K[i, t, j] = g1_it^T M2_j a1_it`` (``da_dense_per_token``).
+
+    ``m2`` is (B2, D, K) -- or (B2, D, K+1) with ``bias``, the last column the
+    bias gradient -- in materialize's ``o*(K+bias) + i`` order; a flat
+    (B2, D*(K+bias)) block is reshaped."""
+    dev = nat.require_device(a1, g1, m2)
+    if a1.dim() != 3 or g1.dim() != 3 or a1.shape[:2] != g1.shape[:2]:
+        raise ValueError("dense_per_token expects (B, T, K) and (B, T, D) factors")
+    if a1.dtype != g1.dtype or m2.dtype != a1.dtype:
+        raise ValueError("dense_per_token operands must share one dtype")
+    kk, dd = a1.shape[-1], g1.shape[-1]
+    kb = kk + int(bias)
+    if m2.numel() != m2.shape[0] * dd * kb:
+        raise ValueError(f"m2 must hold (B2, {dd}, {kb}) values")
+    m2 = m2.reshape(m2.shape[0], dd, kb)
+    bias_grad = m2[:, :, kk].float().contiguous() if bias else None
+    code = nat.dtype_code(a1.dtype)
+    vec = _chunk_elems(a1.dtype)
+    k = -(-kk // vec) * vec
+    d = -(-dd // vec) * vec
+    a1, g1 = prepare_rows(a1, k), prepare_rows(g1, d)
+    w = m2[:, :, :kk]
+    if k != kk or d != dd or not _aligned(w) or w.stride(2) != 1:
+        padded = torch.zeros(w.shape[0], d, k, dtype=w.dtype, device=dev)
+        padded[:, :dd, :kk] = w
+        w = padded
+    if bias_grad is not None and d != dd:
+        bias_grad = torch.nn.functional.pad(bias_grad, (0, d - dd))
+    b1, t1, b2 = a1.shape[0], a1.shape[1], w.shape[0]
+    out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
+    s1 = _side(a1, g1, bias)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_dense_per_token_workspace(s1, b2, k, d, code, ctypes.byref(nbytes)), "dense_per_token")
+    ws = nat.workspace(nbytes.value, dev)
+    nat.check(
+        lib.da_dense_per_token(s1, w.data_ptr(), b2, w.stride(0), w.stride(1),
+                               bias_grad.data_ptr() if bias_grad is not None else None,
+                               bias_grad.stride(0) if bias_grad is not None else 0, k, d, code,
+                               out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
+                               ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
+        "dense_per_token",
+    )
+    return out
+
+
 def ghost_gram_grouped(groups1, groups2, *, bias=False, out: torch.Tensor | None = None,
                        accumulate: bool = False) -> torch.Tensor:
     """Segment-summed ghost product over groups (experts of one or several

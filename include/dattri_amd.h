@@ -97,6 +97,46 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
                   size_t workspace_bytes, void* stream);
 
 /*
+ * Per-token cross-gram of two factorized sides: side 1's token axis kept,
+ * side 2's summed out,
+ *
+ *   out[i*ld_b1 + t*ld_t + j*ld_b2] (+)= sum_s (a1[i,t,:].a2[j,s,:] + bias) * (g1[i,t,:].g2[j,s,:])
+ *                                     = a1_it^T (sum_s a2_js g2_js^T) g1_it,
+ *
+ * fp32, (B1, T1, B2).  Summing over t gives da_ghost_gram's (B1, B2).
+ * Replaces cross_gram_per_token for linear layers,
+ * dattri_llm/gradient/ops/dot.py:171-222 (einsum over the materialized side-2
+ * gradient, :220-222), which cross_dot_per_token (:266-299) and
+ * layerwise_cross_dot_per_token (:607-669) call.  Dense sides only (no
+ * seg_offsets), D > 0; DA_ERR_UNSUPPORTED for rows beyond 32-bit offsets.
+ */
+int da_ghost_gram_per_token_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D,
+                                      int dtype, size_t* bytes);
+int da_ghost_gram_per_token(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D, int dtype,
+                            float* out, int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Per-token cross-gram against a dense side 2 (materialized or
+ * preconditioned per-sample gradients):
+ *
+ *   out[i*ld_b1 + t*ld_t + j*ld_b2] (+)= sum_o (a1[i,t,:] . M2_j[o,:] + mb_j[o]) * g1[i,t,o]
+ *
+ * with M2_j[o, k] at m2 + j*m2_bstride + o*m2_rstride + k (elements, K
+ * columns, 16-byte aligned rows) and, when s1->has_bias, the bias column's
+ * gradients mb_j[o] = m2_bias[j*m2_bias_ld + o] (fp32).  Only s1's factors
+ * are read (act (B1, T1, K), grad (B1, T1, D)).  Replaces
+ * cross_gram_per_token_dense for linear layers,
+ * dattri_llm/gradient/ops/dot.py:225-263 (einsum "btk,btd,cdk->btc").
+ */
+int da_dense_per_token_workspace(const da_factor_side* s1, int64_t b2, int64_t K, int64_t D, int dtype,
+                                 size_t* bytes);
+int da_dense_per_token(const da_factor_side* s1, const void* m2, int64_t b2, int64_t m2_bstride, int64_t m2_rstride,
+                       const float* m2_bias, int64_t m2_bias_ld, int64_t K, int64_t D, int dtype, float* out,
+                       int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
  * Segment-summed ghost product over experts (MoE routed layers):
  *
  *   out[i*ld_out + j] (+)= sum_e sum_{t in seg1_e(i), s in seg2_e(j)}

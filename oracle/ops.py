@@ -13,6 +13,10 @@ cross_gram_factorized          gradient/ops/dot.py:115-118                    br
                                                                               grads (linear layer, with bias)
 cross_gram_materialized        gradient/ops/dot.py:110-114                    equals the factorized form; autograd
 cross_gram                     gradient/ops/dot.py:36-118 (linear, norm)      the two above + norm branch vs autograd
+cross_gram_per_token           gradient/ops/dot.py:171-222 (linear, norm)     brute-force loops over (i, t, j, s); the
+                                                                              sum over t equals cross_gram (dot.py:181-183)
+cross_gram_per_token_dense     gradient/ops/dot.py:225-263 (linear, norm)     equals cross_gram_per_token with m2 =
+                                                                              materialize_linear of side 2
 materialize_linear             gradient/ops/materialize.py:114-116,           torch autograd weight.grad (+ bias.grad)
                                preprocess.py:436-437                          flattened o*K+i layout
 rms_x_hat / layer_norm_x_hat   gradient/ops/norm.py:25-41, :10-22             torch.nn.functional.rms_norm / layer_norm
@@ -42,6 +46,8 @@ __all__ = [
     "cross_gram",
     "cross_gram_factorized",
     "cross_gram_materialized",
+    "cross_gram_per_token",
+    "cross_gram_per_token_dense",
     "layer_norm_x_hat",
     "materialize_linear",
     "maybe_materialize_projected",
@@ -137,6 +143,37 @@ def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto", bias: bool =
     if mode == "materialized":
         return cross_gram_materialized(a1, g1, a2, g2, bias)
     return cross_gram_factorized(a1, g1, a2, g2, bias)
+
+
+def cross_gram_per_token(a1, g1, a2, g2, layer_type: str = "nn.Linear", bias: bool = False) -> np.ndarray:
+    """cross_gram_per_token (dot.py:171-222) on preprocessed factors, (B1, T1, B2):
+    side 2's per-sample gradient M2_j = sum_s a2_js (x) g2_js, then
+    K[i, t, j] = a1_it^T M2_j g1_it (einsum "btk,btd,ckd->btc", :220-222).  Norm
+    layers: (a1 * g1) against sum_s a2 * g2 (:209-214).  ``bias`` folds the
+    ones column into both activations (the preprocessed linear factors)."""
+    a1, g1, a2, g2 = (_to_3d(x) for x in (a1, g1, a2, g2))
+    if layer_type in NORM_TYPES:
+        grad2 = (a2 * g2).sum(axis=1)
+        return np.einsum("btd,cd->btc", a1 * g1, grad2)
+    if bias:
+        a1, a2 = _with_ones(a1), _with_ones(a2)
+    m2 = np.einsum("csk,csd->ckd", a2, g2)
+    return np.einsum("btk,btd,ckd->btc", a1, g1, m2, optimize=True)
+
+
+def cross_gram_per_token_dense(a1, g1, m2, layer_type: str = "nn.Linear", bias: bool = False) -> np.ndarray:
+    """cross_gram_per_token_dense (dot.py:225-263): side 2 dense, ``m2`` (B2, D*K')
+    in materialize's o*K' + i layout (K' = K + bias), reshaped to (B2, D, K');
+    K[i, t, j] = einsum("btk,btd,cdk->btc") (:260-263).  Norm layers:
+    einsum("btd,cd->btc", a1 * g1, m2) (:246-247)."""
+    a1, g1 = _to_3d(a1), _to_3d(g1)
+    b2 = m2.shape[0]
+    if layer_type in NORM_TYPES:
+        return np.einsum("btd,cd->btc", a1 * g1, m2.reshape(b2, -1))
+    if bias:
+        a1 = _with_ones(a1)
+    m2 = m2.reshape(b2, g1.shape[-1], a1.shape[-1])
+    return np.einsum("btk,btd,cdk->btc", a1, g1, m2, optimize=True)
 
 
 # ---------------------------------------------------------------------------

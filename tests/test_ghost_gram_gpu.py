@@ -202,3 +202,59 @@ def test_moe_layers_cross_gram(device):
         layers.append((experts, bias))
     got = ops.moe.moe_layers_cross_gram(layers, segs[0], segs[1])
     assert rel_err(got.cpu().numpy(), ref) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
+# per-token cross-gram (token decomposition of the score)
+# ---------------------------------------------------------------------------
+
+PT_CASES = [
+    # (b1, t1, b2, t2, k, d, bias, dtype)
+    (2, 300, 3, 200, 64, 48, True, torch.bfloat16),   # 2 row tiles x 2 column tiles, ragged
+    (3, 64, 2, 129, 40, 24, False, torch.float32),
+    (1, 513, 4, 64, 256, 512, True, torch.float16),    # 3 row tiles
+    (4, 128, 5, 128, 136, 72, False, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", PT_CASES)
+def test_ghost_gram_per_token(device, case):
+    from dattri_llm_amd import kernels
+
+    b1, t1, b2, t2, k, d, bias, dtype = case
+    print(f"ghost_gram_per_token case={case}", flush=True)
+    a1, g1, a2, g2 = _inputs(31 + t1, b1, t1, b2, t2, k, d, dtype)
+    dev = [x.to(device) for x in (a1, g1, a2, g2)]
+    got = kernels.ghost_gram_per_token(*dev, bias=bias)
+    assert got.shape == (b1, t1, b2)
+    want = oracle.cross_gram_per_token(*(_np(x) for x in (a1, g1, a2, g2)), bias=bias)
+    assert rel_err(got.cpu().numpy(), want) <= TOL[dtype]
+    # the token sum is the ordinary cross-gram
+    gram = kernels.ghost_gram(*dev, bias=bias)
+    assert rel_err(got.sum(1).cpu().numpy(), gram.cpu().numpy()) <= TOL[dtype]
+    kernels.ghost_gram_per_token(*dev, bias=bias, out=got, accumulate=True)
+    assert rel_err(got.cpu().numpy(), 2 * want) <= TOL[dtype]
+
+
+DENSE_PT_CASES = [
+    # (b1, t1, b2, k, d, bias, dtype)
+    (2, 300, 3, 64, 136, True, torch.bfloat16),   # 2 output-channel tiles, ragged
+    (3, 70, 2, 200, 48, False, torch.float32),
+    (1, 257, 4, 520, 264, True, torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", DENSE_PT_CASES)
+def test_dense_per_token(device, case):
+    from dattri_llm_amd import kernels
+
+    b1, t1, b2, k, d, bias, dtype = case
+    print(f"dense_per_token case={case}", flush=True)
+    gen = torch.Generator().manual_seed(7 + k)
+    a1 = (torch.randn(b1, t1, k, generator=gen) / k**0.5).to(dtype)
+    g1 = (torch.randn(b1, t1, d, generator=gen) / d**0.5).to(dtype)
+    m2 = (torch.randn(b2, d * (k + int(bias)), generator=gen) / (k * d) ** 0.25).to(dtype)
+    got = kernels.dense_per_token(a1.to(device), g1.to(device), m2.to(device), bias=bias)
+    want = oracle.cross_gram_per_token_dense(_np(a1), _np(g1), _np(m2), bias=bias)
+    assert got.shape == (b1, t1, b2)
+    assert rel_err(got.cpu().numpy(), want) <= TOL[dtype]

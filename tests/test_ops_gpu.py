@@ -143,6 +143,48 @@ def test_layerwise_cross_dot_mixed_representations(device, ops):
     assert set(per) == {"l0", "l1", "l2", "pos"} and per["pos"].shape == (1, bq)
 
 
+def test_layerwise_cross_dot_per_token(device, ops):
+    """Token decomposition over a block of linear (with and without bias) and
+    norm layers, test side factorized or dense per layer: against the oracle,
+    and its token sum against layerwise_cross_dot."""
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    gen = torch.Generator().manual_seed(9)
+    bt, tt, bq, tq = 3, 40, 2, 24
+    lin = (_rand(gen, bt, tt, 48), _rand(gen, bt, tt, 32), _rand(gen, bq, tq, 48), _rand(gen, bq, tq, 32))
+    lin2 = (_rand(gen, bt, tt, 64), _rand(gen, bt, tt, 16), _rand(gen, bq, tq, 64), _rand(gen, bq, tq, 16))
+    nrm = (_rand(gen, bt, tt, 32), _rand(gen, bt, tt, 32), _rand(gen, bq, tq, 32), _rand(gen, bq, tq, 32))
+    want = {
+        "lin": oracle.cross_gram_per_token(*(_np(x) for x in lin), bias=True),
+        "lin2": oracle.cross_gram_per_token_dense(_np(lin2[0]), _np(lin2[1]),
+                                                  oracle.materialize_linear(_np(lin2[2]), _np(lin2[3]))),
+        "norm": oracle.cross_gram_per_token(*(_np(x) for x in nrm), "nn.RMSNorm"),
+    }
+    dv = lambda x: x.to(device)  # noqa: E731
+    tr = {"lin": Factorized(dv(lin[0]), dv(lin[1]), module_kwargs={"has_bias": True}),
+          "lin2": Factorized(dv(lin2[0]), dv(lin2[1])),
+          "norm": Factorized(dv(nrm[0]), dv(nrm[1]))}
+    te = {"lin": Factorized(dv(lin[2]), dv(lin[3]), module_kwargs={"has_bias": True}),
+          "lin2": ops.materialize(Factorized(dv(lin2[2]), dv(lin2[3])), "nn.Linear"),
+          "norm": Factorized(dv(nrm[2]), dv(nrm[3]))}
+    lts = {"lin": "nn.Linear", "lin2": "nn.Linear", "norm": "nn.RMSNorm"}
+    rep = lambda d: {n: ("materialized" if isinstance(v, torch.Tensor) else "factorized") for n, v in d.items()}  # noqa: E731
+    idx = lambda d: {n: ("batch" if isinstance(v, torch.Tensor) else "batch_token") for n, v in d.items()}  # noqa: E731
+    train = Gradient(rep(tr), tr, lts, idx(tr))
+    test = Gradient(rep(te), te, lts, idx(te))
+    per = ops.layerwise_cross_dot_per_token(train, test, reduce="none")
+    for n, w in want.items():
+        assert per[n].shape == (bt, tt, bq)
+        assert rel_err(per[n].cpu().numpy(), w) <= 1e-3, n
+    total = ops.layerwise_cross_dot_per_token(train, test)
+    assert rel_err(total.cpu().numpy(), sum(want.values())) <= 1e-3
+    assert rel_err(total.sum(1).cpu().numpy(), ops.layerwise_cross_dot(train, test).cpu().numpy()) <= 1e-3
+    # a train layer without a token axis cannot be decomposed
+    dense_tr = dict(tr, lin2=ops.materialize(tr["lin2"], "nn.Linear"))
+    with pytest.raises(ValueError, match="no token axis"):
+        ops.layerwise_cross_dot_per_token(Gradient(rep(dense_tr), dense_tr, lts, idx(dense_tr)), test)
+
+
 # ---------------------------------------------------------------------------
 # projection
 # ---------------------------------------------------------------------------

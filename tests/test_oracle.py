@@ -58,6 +58,59 @@ def test_ghost_bias_is_a_ones_column():
                                _brute_ghost(ones(a1), g1, ones(a2), g2), rtol=1e-12)
 
 
+def _brute_per_token(a1, g1, a2, g2, bias=0.0):
+    b1, s1, _ = a1.shape
+    b2, s2, _ = a2.shape
+    out = np.zeros((b1, s1, b2))
+    for i in range(b1):
+        for t in range(s1):
+            for j in range(b2):
+                out[i, t, j] = sum((float(a1[i, t] @ a2[j, s]) + bias) * float(g1[i, t] @ g2[j, s])
+                                   for s in range(s2))
+    return out
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_per_token_matches_brute_force_loops(bias):
+    r = _rng(11)
+    a1, g1 = r.standard_normal((2, 5, 4)), r.standard_normal((2, 5, 3))
+    a2, g2 = r.standard_normal((3, 2, 4)), r.standard_normal((3, 2, 3))
+    got = oracle.cross_gram_per_token(a1, g1, a2, g2, bias=bias)
+    np.testing.assert_allclose(got, _brute_per_token(a1, g1, a2, g2, 1.0 if bias else 0.0), rtol=1e-12, atol=1e-12)
+
+
+def test_per_token_sums_to_the_cross_gram():
+    """dot.py:181-183: summing over side 1's tokens recovers the (B1, B2) score."""
+    r = _rng(12)
+    a1, g1 = r.standard_normal((3, 7, 6)), r.standard_normal((3, 7, 5))
+    a2, g2 = r.standard_normal((2, 4, 6)), r.standard_normal((2, 4, 5))
+    for bias in (False, True):
+        np.testing.assert_allclose(oracle.cross_gram_per_token(a1, g1, a2, g2, bias=bias).sum(axis=1),
+                                   _brute_ghost(*(np.concatenate([x, np.ones(x.shape[:-1] + (1,))], -1)
+                                                  if bias and n in (0, 2) else x
+                                                  for n, x in enumerate((a1, g1, a2, g2)))),
+                                   rtol=1e-10)
+    x1, y1, x2, y2 = r.standard_normal((2, 5, 8)), r.standard_normal((2, 5, 8)), \
+        r.standard_normal((3, 4, 8)), r.standard_normal((3, 4, 8))
+    np.testing.assert_allclose(oracle.cross_gram_per_token(x1, y1, x2, y2, "nn.RMSNorm").sum(axis=1),
+                               (x1 * y1).sum(1) @ (x2 * y2).sum(1).T, rtol=1e-10)
+
+
+def test_per_token_dense_equals_factorized_form():
+    r = _rng(13)
+    a1, g1 = r.standard_normal((2, 6, 5)), r.standard_normal((2, 6, 4))
+    a2, g2 = r.standard_normal((3, 3, 5)), r.standard_normal((3, 3, 4))
+    for bias in (False, True):
+        m2 = oracle.materialize_linear(a2, g2, bias=bias)  # (B2, D*(K+bias)), index o*K' + i
+        np.testing.assert_allclose(oracle.cross_gram_per_token_dense(a1, g1, m2, bias=bias),
+                                   _brute_per_token(a1, g1, a2, g2, 1.0 if bias else 0.0), rtol=1e-10)
+    x1, y1 = r.standard_normal((2, 5, 8)), r.standard_normal((2, 5, 8))
+    grad2 = r.standard_normal((3, 8))
+    want = np.array([[[sum(x1[i, t, d] * y1[i, t, d] * grad2[j, d] for d in range(8)) for j in range(3)]
+                      for t in range(5)] for i in range(2)])
+    np.testing.assert_allclose(oracle.cross_gram_per_token_dense(x1, y1, grad2, "nn.RMSNorm"), want, rtol=1e-10)
+
+
 def test_ghost_equals_materialized_route():
     r = _rng(2)
     a1, g1 = r.standard_normal((4, 7, 6)), r.standard_normal((4, 7, 5))
