@@ -95,6 +95,24 @@ class AttributionScore:
         steps = sorted(by_step)
         return steps, torch.stack([self.scores[by_step[s]].sum(dim=0) for s in steps])
 
+    def token_scores(self, train_hash: str, step: int | None = None) -> tuple[list[int], torch.Tensor]:
+        """(positions, (len(positions), num_test)) per-token-position scores of one
+        training sample (score.py:185-226); ``step=None`` sums the positions over
+        every step the sample appears at."""
+        if self.row_token_ids is None:
+            raise ValueError("token_scores() needs a token-level score; attribute with "
+                             "attribution_granularity='token'.")
+        entries = self._require_train(train_hash)
+        rows = [r for s, r in entries if step is None or s == step]
+        if not rows:
+            known = sorted({s for s, _ in entries})
+            raise KeyError(f"train sample {train_hash[:16]}... has no row at step {step}; known steps: {known}")
+        by_pos: dict[int, list[int]] = {}
+        for r in rows:
+            by_pos.setdefault(self.row_token_ids[r], []).append(r)
+        positions = sorted(by_pos)
+        return positions, torch.stack([self.scores[by_pos[p]].sum(dim=0) for p in positions])
+
     def trajectory_agnostic(self, train_hash: str) -> torch.Tensor:
         return self.trajectory_aware(train_hash)[1].sum(dim=0)
 

@@ -87,6 +87,23 @@ class TracInAttributor:
         n_te = self._norm(test_rep, shared, None)
         return dot / (n_tr[:, None] * n_te[None, :] + 1e-8)
 
+    def inner_product_per_token(self, train_rep: Gradient, test_rep: Gradient) -> torch.Tensor:
+        """(B_train, T_train, B_test) decomposition of :meth:`inner_product` over the
+        train side's token positions (tracin.py:110-126, base.py:677-698); for
+        GradCos each position's share of the cosine (the per-token dots over the
+        two whole-sample norms)."""
+        if not any(name in test_rep.data for name in train_rep.data):
+            tokens = [t for t in train_rep.token_dim.values() if t is not None]
+            return torch.zeros(train_rep.batch_size, max(tokens) if tokens else 1, test_rep.batch_size,
+                               device=self.device)
+        dot = ops.layerwise_cross_dot_per_token(train_rep, test_rep)
+        if self._metric == "dot":
+            return dot
+        shared = [n for n in train_rep.data if n in test_rep.data]
+        n_tr = self._norm(train_rep, shared, None)
+        n_te = self._norm(test_rep, shared, None)
+        return dot / (n_tr[:, None, None] * n_te[None, None, :] + 1e-8)
+
     @staticmethod
     def _norm(rep: Gradient, layers, dense_cache) -> torch.Tensor:
         total = torch.zeros(rep.batch_size, device=rep.device)
@@ -99,13 +116,18 @@ class TracInAttributor:
         return total.clamp_min(0).sqrt()
 
     def attribute_sources(self, train_source, test_source, *, normalized_grad: bool = False,
-                          batch_size: int | None = None) -> AttributionScore:
-        """Score two ``(step, Gradient, hashes)`` sources (base.py:704-770)."""
+                          batch_size: int | None = None,
+                          attribution_granularity: str = "instance") -> AttributionScore:
+        """Score two ``(step, Gradient, hashes)`` sources (base.py:704-770);
+        ``attribution_granularity="token"`` gives one row per training token
+        position (:meth:`inner_product_per_token`)."""
         self._set_metric(normalized_grad)
-        scores, row_ids, row_steps, test_ids, _ = score_sources(
+        scores, row_ids, row_steps, test_ids, row_tokens = score_sources(
             train_source, test_source, self.device, inner_product=self.inner_product,
             transform_test=self.route_test_rep, batch_size=batch_size or self.train_batch_size,
+            granularity=attribution_granularity, inner_product_per_token=self.inner_product_per_token,
         )
         return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
                                 algorithm=self.algorithm,
-                                algorithm_meta={"normalized_grad": normalized_grad}, layer_name=None)
+                                algorithm_meta={"normalized_grad": normalized_grad}, layer_name=None,
+                                row_token_ids=row_tokens)

@@ -109,11 +109,24 @@ def score_sources(
     transform_test: Callable | None = None,
     batch_size: int = 1,
     cache_budget: CacheBudget | None = None,
+    granularity: str = "instance",
+    inner_product_per_token: Callable | None = None,
 ):
     """Score every train block against every cached test block
-    (utils.py:239-440, instance granularity, cached test side).
+    (utils.py:239-440, cached test side).
 
-    Returns ``(scores (rows, num_test) fp32 CPU, row_train_ids, row_steps, test_ids, None)``."""
+    ``granularity="instance"`` gives one row per training sample;
+    ``"token"`` one row per training token position, scored by
+    ``inner_product_per_token(train_rep, test_rep) -> (B_train, T, B_test)``
+    (a sample of T positions contributes T consecutive rows).
+
+    Returns ``(scores (rows, num_test) fp32 CPU, row_train_ids, row_steps,
+    test_ids, row_token_ids or None)``."""
+    if granularity not in {"instance", "token"}:
+        raise ValueError(f"granularity must be 'instance' or 'token', got {granularity!r}.")
+    per_token = granularity == "token"
+    if per_token and inner_product_per_token is None:
+        raise ValueError("granularity='token' needs inner_product_per_token.")
     transform_train = transform_train or (lambda g: g)
     transform_test = transform_test or (lambda g: g)
     budget = cache_budget if cache_budget is not None else CacheBudget(device)
@@ -130,14 +143,27 @@ def score_sources(
         cached.append((transform_test(test_g.to(device)), cols))
     cached = _merge_dense_test(cached)
     num_test = len(test_ids)
-    reuse = len(cached) > 1
-    chunks, row_ids, row_steps = [], [], []
+    # a dense copy of the train block pays off only against several test blocks,
+    # and only the instance-level kernel materializes the train side
+    reuse = len(cached) > 1 and not per_token
+
+    def n_rows(train_rep) -> int:
+        if not per_token:
+            return train_rep.batch_size
+        tokens = [t for t in train_rep.token_dim.values() if t is not None]
+        return train_rep.batch_size * (max(tokens) if tokens else 1)
+
+    chunks, row_ids, row_steps, row_tokens = [], [], [], []
     for steps, train_g, ids in rebatch_blocks(train_source, batch_size):
         train_rep = transform_train(train_g.to(device))
-        row = torch.zeros(train_rep.batch_size, num_test, dtype=torch.float32, device=device)
+        row = torch.zeros(n_rows(train_rep), num_test, dtype=torch.float32, device=device)
         cache = TensorCache("memory", budget=budget) if reuse else None
         for test_rep, cols in cached:
-            block = inner_product(train_rep, test_rep, dense_cache=cache).to(torch.float32)
+            if per_token:
+                block = inner_product_per_token(train_rep, test_rep).to(torch.float32)
+                block = block.reshape(-1, block.shape[-1])
+            else:
+                block = inner_product(train_rep, test_rep, dense_cache=cache).to(torch.float32)
             if cols and cols == list(range(cols[0], cols[0] + len(cols))):
                 row[:, cols[0]:cols[0] + len(cols)] = block
             else:
@@ -145,7 +171,14 @@ def score_sources(
         if cache is not None:
             cache.clear()
         chunks.append(row.cpu())
-        row_ids.extend(ids)
-        row_steps.extend(steps)
+        if per_token:
+            t = row.shape[0] // max(len(ids), 1)
+            for h, st in zip(ids, steps, strict=True):
+                row_ids.extend([h] * t)
+                row_steps.extend([st] * t)
+                row_tokens.extend(range(t))
+        else:
+            row_ids.extend(ids)
+            row_steps.extend(steps)
     scores = torch.cat(chunks, dim=0) if chunks else torch.zeros(0, num_test)
-    return scores, row_ids, row_steps, test_ids, None
+    return scores, row_ids, row_steps, test_ids, (row_tokens if per_token else None)

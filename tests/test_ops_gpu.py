@@ -346,6 +346,36 @@ def test_c1_tracin_attributor_and_cosine(device):
     assert rel_err(cos.scores.numpy(), want) <= 1e-3
 
 
+@pytest.mark.parametrize("normalized", [False, True])
+def test_c1_token_granularity(device, normalized):
+    """attribution_granularity='token': one row per train token position; the
+    positions sum to the instance-level scores, and TracIn's rows match the
+    oracle's per-token cross-gram summed over the captured layers."""
+    from c1_model import c1_inputs, capture_factors
+
+    from dattri_llm_amd.attribution import TracInAttributor
+
+    train, query = _c1_blocks(device)
+    src_tr = [(0, train, [f"t{i}" for i in range(32)])]
+    src_q = [(0, query, [f"q{j}" for j in range(8)])]
+    tok = TracInAttributor(train_batch_size=16, device=device).attribute_sources(
+        src_tr, src_q, normalized_grad=normalized, attribution_granularity="token")
+    inst = TracInAttributor(train_batch_size=16, device=device).attribute_sources(
+        src_tr, src_q, normalized_grad=normalized)
+    t = 64
+    assert tok.granularity == "token" and tok.scores.shape == (32 * t, 8)
+    _ids, agn = tok.agnostic_matrix()
+    assert rel_err(agn.numpy(), inst.scores.numpy()) <= 1e-3
+    positions, m = tok.token_scores("t3")
+    assert positions == list(range(t)) and m.shape == (t, 8)
+    if not normalized:
+        model, tr_ids, q_ids = c1_inputs(0)
+        ftr, fq = capture_factors(model, tr_ids), capture_factors(model, q_ids)
+        want = sum(oracle.cross_gram_per_token(_np(ftr[n][0]), _np(ftr[n][1]), _np(fq[n][0]), _np(fq[n][1]),
+                                               bias=True) for n in ftr)
+        assert rel_err(tok.scores.numpy().reshape(32, t, 8), want) <= 1e-3
+
+
 @pytest.mark.parametrize("batch,tokens,n_exp,k", [(16, 256, 8, 2), (3, 37, 5, 3), (1, 64, 4, 1),
                                                     (64, 300, 64, 4), (8, 1024, 256, 2), (32, 512, 8, 2)])
 def test_route_segments_matches_per_expert_sorts(device, ops, batch, tokens, n_exp, k):
