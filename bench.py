@@ -407,6 +407,71 @@ def bench_ghost(args):
     return result
 
 
+def bench_per_token(args):
+    """Per-token cross-gram on the C2 shapes: every train token position of 256
+    samples x 512 tokens against 64 whole query samples (T=512, d=4096): the
+    ghost flops with a per-row epilogue, (256, 512, 64) fp32 out."""
+    import torch
+
+    from dattri_llm_amd import kernels
+
+    n1, n2, t, d = 256, 64, 512, 4096
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    bf = torch.bfloat16
+    a1, g1 = _randn((n1, t, d), gen, bf, d**-0.5), _randn((n1, t, d), gen, bf, d**-0.5)
+    a2, g2 = _randn((n2, t, d), gen, bf, d**-0.5), _randn((n2, t, d), gen, bf, d**-0.5)
+    out = torch.empty(n1, t, n2, dtype=torch.float32, device="cuda")
+    for _ in range(args.warmup):
+        kernels.ghost_gram_per_token(a1, g1, a2, g2, out=out)
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ev = _ev(timers, "per_token")
+        kernels.ghost_gram_per_token(a1, g1, a2, g2, out=out)
+        _ev_end(ev)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    flops = 2.0 * n1 * n2 * t * t * (d + d)
+    t_k = _mean_ms(timers, "per_token")
+    tflops = flops / t_k / 1e9
+    result = {
+        "metric": "per-token train x query scores/sec (256 x 512 train tokens x 64 queries, T=512, d=4096, bf16)",
+        "value": round(n1 * t * n2 / (ms / 1e3), 1),
+        "unit": "token-scores/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "per-token cross-gram 256 train x 512 tok vs 64 query x 512 tok, d_in=d_out=4096"},
+        "roofline": {"bound": "mfma", "kernel": "ghost_per_token_v2", "achieved": round(tflops, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "work_per_launch": f"{flops:.4g} flop = 2 x 256 x 64 pairs x 512^2 x (4096 + 4096)"},
+    }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import oracle
+
+        rng = np.random.default_rng(0)
+        s = [rng.standard_normal((n, t, d), dtype=np.float32) for n in (4, 4, 2, 2)]
+        t0 = time.perf_counter()
+        oracle.cross_gram_per_token(s[0], s[1], s[2], s[3])
+        dt = time.perf_counter() - t0
+        cores, model = cpu_info()
+        result["cpu_baseline"] = {"value": round(4 * t * 2 / dt, 1), "unit": "token-scores/s",
+                                  "cores": blas_threads(), "kind": "port",
+                                  "sample": f"numpy fp32 oracle, 4 train x 512 tokens x 2 query at d=4096 "
+                                            f"({dt:.2f} s); host {model}, {cores} cores visible"}
+    return result
+
+
 # ---------------------------------------------------------------------------
 # projected capture (LoGRA route): fused project + outer product, then score
 # ---------------------------------------------------------------------------
@@ -637,7 +702,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["block", "ghost", "project", "moe", "copy"], default="block")
+    ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "copy"], default="block")
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -650,8 +715,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
-    runs = {"block": bench_block, "ghost": bench_ghost, "project": bench_project, "moe": bench_moe,
-            "copy": bench_copy}
+    runs = {"block": bench_block, "ghost": bench_ghost, "per_token": bench_per_token, "project": bench_project,
+            "moe": bench_moe, "copy": bench_copy}
     result = runs[args.workload](args)
     print(json.dumps(result), flush=True)
 
