@@ -464,14 +464,14 @@ struct DmaState {
 // DMA instruction j of wave w loads tile rows 8*(12w + j) .. +7 (rows < 256 are
 // side 1); lane l -> row 8*(12w+j) + l/8, slot l%8 holding logical chunk
 // (l%8) ^ (l/8), which is cbyte / 16.
-__device__ __forceinline__ void dma_quarter(const DmaState& D, int q, int st) {
+__device__ __forceinline__ void dma_quarter(const DmaState& D, int q, int st, int x0 = 0, int x1 = 3) {
   const bool act = st < D.na;
   const uint32_t koff = (uint32_t)(act ? st : st - D.na) * v2::kSB;
   const int64_t kb = act ? D.kba : D.kbg;
   const bool kin = st < D.nst && (int64_t)(koff + D.cbyte) < kb;
   const uint32_t base = D.lds0 + (uint32_t)((st % v2::kNBuf) * v2::kStage + v2::kDma * D.uwave * 8 * v2::kSB);
 #pragma unroll
-  for (int x = 0; x < 3; ++x) {
+  for (int x = x0; x < x1; ++x) {
     const int j = 3 * q + x;
     const bool side1 = v2::kDma * D.uwave + j < v2::kBM / 8;  // uniform
     const uint32_t m = act ? 0xffffffffu : 0u;
@@ -491,7 +491,8 @@ __device__ __forceinline__ void dma_quarter(const DmaState& D, int q, int st) {
 // One quarter of a stage: the 8 MFMAs of one slice held in (ua, ub) into acc;
 // with rd, the 6 fragment reads of the slice (stage base sb, slice kk) into
 // (na, nb) interleaved one per MFMA; with qd >= 0, quarter qd of stage dst's
-// loads after the second MFMA.
+// loads, one instruction after each of MFMAs 1, 3 and 5 (spread out, so the
+// address unit never queues a wave's loads behind each other).
 template <int DT>
 __device__ __forceinline__ void ghost_quarter(f32x16 (&acc)[4][2], const u32x4 (&ua)[4], const u32x4 (&ub)[2],
                                               bool rd, const lds_char* sb, int coff, int wm, int wn,
@@ -503,7 +504,7 @@ __device__ __forceinline__ void ghost_quarter(f32x16 (&acc)[4][2], const u32x4 (
       else if (i < 6) nb[i - 4] = *(const u32x4*)(sb + (v2::kBM + 64 * wn + 32 * (i - 4)) * v2::kSB + coff);
     }
     Mfma32<DT>::mma(acc[i >> 1][i & 1], ua[i >> 1], ub[i & 1]);
-    if (qd >= 0 && i == 1) dma_quarter(D, qd, dst);
+    if (qd >= 0 && (i == 1 || i == 3 || i == 5)) dma_quarter(D, qd, dst, i / 2, i / 2 + 1);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -519,9 +520,11 @@ __device__ __forceinline__ void ghost_stage_sync() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-// Runs the tile's two K loops; returns with every wave done reading the ring
+// Runs the tile's K stages; returns with every wave done reading the ring
 // (so the caller may reuse the LDS) and no load in flight.
-template <int DT>
+// kHasA: the tile has activation stages (K > 0), multiplied into ka before
+// the gradient stages into kg; otherwise every stage goes to kg and ka stays 0.
+template <int DT, bool kHasA>
 __device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, f32x16 (&ka)[4][2],
                                                   f32x16 (&kg)[4][2]) {
   lds_char* const L = (lds_char*)smem;
@@ -552,7 +555,8 @@ __device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, 
   const int lrow = lane & 31, hh = lane >> 5;
   const int c0 = lrow * v2::kSB + (((0 + hh) ^ (lane & 7)) << 4), c1 = lrow * v2::kSB + (((2 + hh) ^ (lane & 7)) << 4);
   const int c2 = lrow * v2::kSB + (((4 + hh) ^ (lane & 7)) << 4), c3 = lrow * v2::kSB + (((6 + hh) ^ (lane & 7)) << 4);
-  u32x4 f0a[4], f0b[2], f1a[4], f1b[2];
+  // Slice kk of every stage lives in fragment buffer kk.
+  u32x4 fa[4][4], fb[4][2];
 
 #pragma unroll
   for (int x = 0; x < 4; ++x)
@@ -562,46 +566,61 @@ __device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, 
       kg[x][y] = f32x16{};
     }
 
-  // Stage s's loads: quarter 0 in the last quarter of iteration s - 3,
-  // quarters 1..3 in the first three quarters of iteration s - 2.  Iteration
-  // st: quarters 0..2 multiply slices 0..2 of stage st (reading 1..3), the
-  // barrier opens stage st + 1, quarter 3 multiplies slice 3 of st while
-  // reading slice 0 of st + 1.  Before each barrier exactly 12 instructions
-  // follow the awaited stage's last one.
+  // Fragments are read two slices ahead of their MFMAs, so a read has a whole
+  // quarter (8 MFMAs) to come back while the DMA writes share the LDS.  A loop
+  // body starts right after a barrier (no read in flight, so the loop header
+  // needs no wait): it multiplies slices 2 and 3 of stage st and slices 0 and
+  // 1 of st + 1 while reading slices 0..3 of st + 1, loads stage st + 3 into
+  // the buffer stage st left (its reads all ended before that barrier), then
+  // waits for stage st + 2.  Exactly the 12 instructions of the body's own
+  // loads follow the awaited stage's last one at every barrier.
 #pragma unroll
   for (int s0 = 0; s0 < v2::kNBuf - 1; ++s0)
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_quarter(D, q, s0);
   ghost_stage_sync();
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int co = kk == 0 ? c0 : c1;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) fa[kk][x] = *(const u32x4*)(L + (128 * wm + 32 * x) * v2::kSB + co);
+#pragma unroll
+    for (int y = 0; y < 2; ++y) fb[kk][y] = *(const u32x4*)(L + (v2::kBM + 64 * wn + 32 * y) * v2::kSB + co);
+  }
   dma_quarter(D, 0, v2::kNBuf - 1);
-#pragma unroll
-  for (int x = 0; x < 4; ++x) f0a[x] = *(const u32x4*)(L + (128 * wm + 32 * x) * v2::kSB + c0);
-#pragma unroll
-  for (int y = 0; y < 2; ++y) f0b[y] = *(const u32x4*)(L + (v2::kBM + 64 * wn + 32 * y) * v2::kSB + c0);
+  dma_quarter(D, 1, v2::kNBuf - 1);
+  {
+    f32x16(&acc0)[4][2] = kHasA ? ka : kg;
+    ghost_quarter<DT>(acc0, fa[0], fb[0], true, L, c2, wm, wn, fa[2], fb[2], D, 2, v2::kNBuf - 1);
+    ghost_quarter<DT>(acc0, fa[1], fb[1], true, L, c3, wm, wn, fa[3], fb[3], D, 3, v2::kNBuf - 1);
+  }
+  ghost_stage_sync();
 
   // The loops carry no branch around their MFMAs (a join there makes the
-  // register allocator shuffle accumulators); the last stage is peeled
-  // (nst > na >= 0 because the gradient width is non-zero).
-#define DA_GHOST_ITER(ACC)                                                                            \
+  // register allocator shuffle accumulators): the activation loop, the body
+  // that crosses into the gradient stages and the gradient loop are separate,
+  // and the last stage's second half is peeled (nst > na, and na >= 1 when
+  // kHasA, because both widths are non-zero).
+#define DA_GHOST_BODY(A1, A2)                                                                         \
   {                                                                                                   \
-    const lds_char* cur = L + (st % v2::kNBuf) * v2::kStage;                                                  \
-    ghost_quarter<DT>(ACC, f0a, f0b, true, cur, c1, wm, wn, f1a, f1b, D, 1, st + 2);                   \
-    ghost_quarter<DT>(ACC, f1a, f1b, true, cur, c2, wm, wn, f0a, f0b, D, 2, st + 2);                   \
-    ghost_quarter<DT>(ACC, f0a, f0b, true, cur, c3, wm, wn, f1a, f1b, D, 3, st + 2);                   \
+    const lds_char* nxt = L + ((st + 1) % v2::kNBuf) * v2::kStage;                                    \
+    ghost_quarter<DT>(A1, fa[2], fb[2], true, nxt, c0, wm, wn, fa[0], fb[0], D, 0, st + 3);           \
+    ghost_quarter<DT>(A1, fa[3], fb[3], true, nxt, c1, wm, wn, fa[1], fb[1], D, 1, st + 3);           \
+    ghost_quarter<DT>(A2, fa[0], fb[0], true, nxt, c2, wm, wn, fa[2], fb[2], D, 2, st + 3);           \
+    ghost_quarter<DT>(A2, fa[1], fb[1], true, nxt, c3, wm, wn, fa[3], fb[3], D, 3, st + 3);           \
     ghost_stage_sync();                                                                               \
-    ghost_quarter<DT>(ACC, f1a, f1b, true, L + ((st + 1) % v2::kNBuf) * v2::kStage, c0, wm, wn, f0a, f0b, D, 0, \
-                      st + 3);                                                                        \
   }
-  for (int st = 0; st < na; ++st) DA_GHOST_ITER(ka)
-  for (int st = na; st + 1 < nst; ++st) DA_GHOST_ITER(kg)
-#undef DA_GHOST_ITER
-  {
-    const lds_char* cur = L + ((nst - 1) % v2::kNBuf) * v2::kStage;
-    ghost_quarter<DT>(kg, f0a, f0b, true, cur, c1, wm, wn, f1a, f1b, D, -1, 0);
-    ghost_quarter<DT>(kg, f1a, f1b, true, cur, c2, wm, wn, f0a, f0b, D, -1, 0);
-    ghost_quarter<DT>(kg, f0a, f0b, true, cur, c3, wm, wn, f1a, f1b, D, -1, 0);
-    ghost_quarter<DT>(kg, f1a, f1b, false, cur, c0, wm, wn, f0a, f0b, D, -1, 0);
+  if constexpr (kHasA) {
+    for (int st = 0; st + 1 < na; ++st) DA_GHOST_BODY(ka, ka)
+    {
+      const int st = na - 1;
+      DA_GHOST_BODY(ka, kg)
+    }
   }
+  for (int st = kHasA ? na : 0; st + 1 < nst; ++st) DA_GHOST_BODY(kg, kg)
+#undef DA_GHOST_BODY
+  ghost_quarter<DT>(kg, fa[2], fb[2], false, L, c0, wm, wn, fa[0], fb[0], D, -1, 0);
+  ghost_quarter<DT>(kg, fa[3], fb[3], false, L, c1, wm, wn, fa[1], fb[1], D, -1, 0);
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -648,7 +667,7 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_grouped_tiles_v2(GroupedArg
     S.roff_g[q] = live ? (uint32_t)(r * (side1 ? G.g1_ts : G.g2_ts)) : v2::kOob;
   }
   f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT>(S, smem, ka, kg);
+  ghost_tile_engine<DT, true>(S, smem, ka, kg);
   float* P = (float*)smem;
 #pragma unroll
   for (int x = 0; x < 4; ++x)
@@ -724,7 +743,7 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
     }
   }
   f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT>(S, smem, ka, kg);
+  ghost_tile_engine<DT, true>(S, smem, ka, kg);
   float s = 0.f;
 #pragma unroll
   for (int x = 0; x < 4; ++x)
@@ -806,7 +825,7 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) 
     }
   }
   f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT>(S, smem, ka, kg);
+  ghost_tile_engine<DT, !kDense>(S, smem, ka, kg);
   float* P = (float*)smem;
 #pragma unroll
   for (int x = 0; x < 4; ++x)
@@ -901,7 +920,7 @@ int make_plan(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int
   if (rc) return rc;
   if (s1->has_bias != s2->has_bias)
     return set_error(DA_ERR_INVALID, "da_ghost_gram: both sides must agree on has_bias");
-  plan->v2 = fits_v2(s1, K, D, es) && fits_v2(s2, K, D, es) && D > 0;
+  plan->v2 = fits_v2(s1, K, D, es) && fits_v2(s2, K, D, es) && D > 0 && K > 0;
   const int64_t bm = plan->v2 ? v2::kBM : kBM, bn = plan->v2 ? v2::kBN : kBN;
   plan->tiles_r = (s1->tokens + bm - 1) / bm;
   plan->tiles_c = (s2->tokens + bn - 1) / bn;
@@ -993,14 +1012,14 @@ int grouped_plan(const da_factor_side* s1, const da_factor_side* s2, int n_group
   p->part_floats = 0;
   p->v2 = true;
   for (int e = 0; e < n_groups; ++e) {
-    // 32-bit buffer offsets over every group's rows, and a gradient loop
+    // 32-bit buffer offsets over every group's rows, and both loops non-empty
     const da_factor_side* sd[2] = {&s1[e], &s2[e]};
     for (int q = 0; q < 2; ++q) {
       const int64_t ts = sd[q]->act_tstride > sd[q]->grad_tstride ? sd[q]->act_tstride : sd[q]->grad_tstride;
       const int64_t w = K[e] > D[e] ? K[e] : D[e];
       if (sd[q]->tokens < 0 || ts < 0 || (sd[q]->tokens * ts + w) * es >= (1LL << 31) - (1LL << 20)) p->v2 = false;
     }
-    if (D[e] <= 0) p->v2 = false;
+    if (D[e] <= 0 || K[e] <= 0) p->v2 = false;
   }
   p->tile_r = p->v2 ? v2::kBM : kBM;
   p->tile_c = p->v2 ? v2::kBN : kBN;
@@ -1240,9 +1259,9 @@ int da_ghost_gram_per_token(const da_factor_side* s1, const da_factor_side* s2, 
   if (s1->batch == 0 || s1->tokens == 0 || s2->batch == 0) return DA_OK;
   if (!out) return set_error(DA_ERR_INVALID, "%s: out is NULL", who);
   const int64_t es = (int64_t)elem_bytes(dtype);
-  if (s1->seg_offsets || s2->seg_offsets || !fits_v2(s1, K, D, es) || !fits_v2(s2, K, D, es) || D == 0)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: needs dense sides with rows addressable by 32-bit offsets and D > 0",
-                     who);
+  if (s1->seg_offsets || s2->seg_offsets || !fits_v2(s1, K, D, es) || !fits_v2(s2, K, D, es) || D == 0 || K == 0)
+    return set_error(DA_ERR_UNSUPPORTED,
+                     "%s: needs dense sides with rows addressable by 32-bit offsets, K > 0 and D > 0", who);
   if (!workspace || workspace_bytes < p.ws)
     return set_error(DA_ERR_WORKSPACE, "%s: workspace needs %zu bytes", who, p.ws);
   PerTokArgs g;
