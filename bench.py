@@ -20,6 +20,7 @@ region and is reported as ``query_prep_ms``.
 
 Prints ONE JSON line.  Other workloads (not the headline):
 ``--workload ghost``   the fused ghost cross-gram, 256 train x 64 query, T=512, d 4096;
+``--workload per_token`` the per-token cross-gram on the same shapes, (256, 512, 64) out;
 ``--workload project`` projected (k=64) capture of the Llama-7B MLP, 512 + 128 samples;
 ``--workload moe``     a Mixtral-shaped MoE layer on the segmented ghost route;
 ``--workload copy``    a 2 GiB device copy, the reference point for byte counters.
@@ -139,6 +140,39 @@ def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
     except OSError:
         pass
     return None
+
+
+def vendor_gemm_ref(seconds: float = 1.0):
+    """Sustained throughput of the vendor library's square bf16 GEMM
+    (torch.matmul -> hipBLASLt, 8192^3) on this GPU, run after the timed region.
+    Under dense bf16 MFMA load on random data the chip lowers its clock to stay
+    within its power limit, so this is the attainable MFMA reference that an
+    MFMA-bound kernel's fraction of the spec-sheet peak should be read against."""
+    import torch
+
+    n = 8192
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    a = _randn((n, n), gen, torch.bfloat16)
+    b = _randn((n, n), gen, torch.bfloat16)
+    c = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
+    for _ in range(10):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    reps = max(10, int(seconds / max((time.perf_counter() - t0) / 10, 1e-6)))
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        torch.matmul(a, b, out=c)
+    e.record()
+    torch.cuda.synchronize()
+    tf = 2.0 * n**3 * reps / (s.elapsed_time(e) * 1e9)
+    del a, b, c
+    return {"ref": f"torch.matmul bf16 {n}x{n}x{n} (hipBLASLt), sustained {reps} launches",
+            "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
 def cpu_info():
@@ -704,6 +738,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "copy"], default="block")
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--no-gemm-ref", dest="gemm_ref", action="store_false",
+                    help="skip the vendor-GEMM reference added to MFMA-bound lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -718,6 +754,10 @@ def main():
     runs = {"block": bench_block, "ghost": bench_ghost, "per_token": bench_per_token, "project": bench_project,
             "moe": bench_moe, "copy": bench_copy}
     result = runs[args.workload](args)
+    roof = result.get("roofline") or {}
+    if args.gemm_ref and roof.get("bound") == "mfma":
+        roof["attainable"] = vendor_gemm_ref()
+        roof["frac_of_attainable"] = round(roof["achieved"] / roof["attainable"]["tflops"], 4)
     print(json.dumps(result), flush=True)
 
 
