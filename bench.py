@@ -23,6 +23,7 @@ Prints ONE JSON line.  Other workloads (not the headline):
 ``--workload per_token`` the per-token cross-gram on the same shapes, (256, 512, 64) out;
 ``--workload project`` projected (k=64) capture of the Llama-7B MLP, 512 + 128 samples;
 ``--workload moe``     a Mixtral-shaped MoE layer on the segmented ghost route;
+``--workload kfac``    the K-FAC covariance fit of the Llama-8B block's 7 linears over one train block;
 ``--workload copy``    a 2 GiB device copy, the reference point for byte counters.
 """
 
@@ -697,6 +698,89 @@ def bench_moe(args):
 
 
 # ---------------------------------------------------------------------------
+# K-FAC covariance fit (gradient/ops/kronecker.py, streaming accumulators)
+# ---------------------------------------------------------------------------
+
+
+def bench_kfac(args):
+    """K-FAC fit pass over one Llama-8B-block train block (8 x 2048 tokens):
+    the A = a^T a and G = g^T g covariance sums of the 7 linears
+    (``LayerKroneckerAccumulator.update``), each a token-axis contraction on
+    the per-sample dW kernel with the block's 16384 rows as one sample."""
+    import torch
+
+    from dattri_llm_amd.gradient import ops
+
+    n_train, t_train = 8, 2048
+    acts, grads, _norms = make_block(n_train, t_train, seed=0)
+    torch.cuda.synchronize()
+
+    def step(timers=None):
+        accs = {}
+        for name, act, _din, _dout in LINEARS:
+            ev = _ev(timers, "kfac")
+            acc = ops.LayerKroneckerAccumulator()
+            acc.update(acts[act], grads[name], "nn.Linear")
+            accs[name] = acc
+            _ev_end(ev)
+        return accs
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timers: dict = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timers)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    rows = n_train * t_train
+    flops = sum(2.0 * rows * (din * din + dout * dout) for _n, _a, din, dout in LINEARS)
+    t_k = _mean_ms(timers, "kfac") * len(LINEARS)
+    tf = flops / t_k / 1e9
+    result = {
+        "metric": "K-FAC covariance fit token rows/sec (Llama-8B-shaped block, 7 linears, bf16)",
+        "value": round(rows / (ms / 1e3), 1),
+        "unit": "token-rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "k-fac covariances (a^T a, g^T g, fp32 out) of the llama3-8b block's 7 linears "
+                               "over one 8 x 2048-token train block"},
+        "roofline": {"bound": "mfma", "kernel": "materialize_tiles_tr (row Gram, one sample of 16384 rows)",
+                     "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "work_per_step": f"{flops:.4g} flop = sum over the 7 linears of 2 x 16384 x (d_in^2 + d_out^2)",
+                     "step_share": round(t_k / ms, 3)},
+    }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import oracle
+
+        rng = np.random.default_rng(0)
+        n = 2048  # one sequence of q_proj's factors
+        a = rng.standard_normal((1, n, D_MODEL), dtype=np.float32)
+        g = rng.standard_normal((1, n, D_MODEL), dtype=np.float32)
+        t0 = time.perf_counter()
+        oracle.kfac_factors(a, g)
+        dt = time.perf_counter() - t0
+        cores, model = cpu_info()
+        result["cpu_baseline"] = {"value": round(n / dt, 1), "unit": "token-rows/s (q_proj only)",
+                                  "cores": blas_threads(), "kind": "port",
+                                  "sample": f"numpy float64 oracle kfac_factors on 2048 rows of q_proj "
+                                            f"(4096 x 4096 both sides, {dt:.2f} s); host {model}, "
+                                            f"{cores} cores visible"}
+    return result
+
+
+# ---------------------------------------------------------------------------
 # plain device copy: the reference point for HBM byte counters
 # ---------------------------------------------------------------------------
 
@@ -736,7 +820,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "copy"], default="block")
+    ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "kfac", "copy"],
+                    default="block")
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--no-gemm-ref", dest="gemm_ref", action="store_false",
                     help="skip the vendor-GEMM reference added to MFMA-bound lines")
@@ -752,7 +837,7 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
     runs = {"block": bench_block, "ghost": bench_ghost, "per_token": bench_per_token, "project": bench_project,
-            "moe": bench_moe, "copy": bench_copy}
+            "moe": bench_moe, "kfac": bench_kfac, "copy": bench_copy}
     result = runs[args.workload](args)
     roof = result.get("roofline") or {}
     if args.gemm_ref and roof.get("bound") == "mfma":

@@ -6,7 +6,7 @@ functions take raw batch-first ``(activation, pre_activation_grad)``
 tensors, the unsuffixed ones take :class:`Factorized` (or dense tensors).
 """
 
-from dattri_llm_amd.gradient.ops import cost, dtypes, moe
+from dattri_llm_amd.gradient.ops import cost, dtypes, kronecker, moe
 from dattri_llm_amd.gradient.ops.cost import CostModel, calibrate, get_routing_policy, set_routing_policy
 from dattri_llm_amd.gradient.ops.dot import (
     cross_dot,
@@ -28,6 +28,26 @@ from dattri_llm_amd.gradient.ops.dot import (
     pairwise_dot_factors,
 )
 from dattri_llm_amd.gradient.ops.dtypes import as_float, compute_dtype, get_compute_dtype, set_compute_dtype
+from dattri_llm_amd.gradient.ops.kronecker import (
+    FisherAccumulator,
+    KroneckerAccumulator,
+    LayerFisherAccumulator,
+    LayerKroneckerAccumulator,
+    dense_inverse,
+    ekfac_materialize,
+    ekfac_materialize_factors,
+    ekfac_precondition,
+    fim,
+    fim_factors,
+    kfac,
+    kfac_cross,
+    kfac_cross_factors,
+    kfac_eigh,
+    kfac_factors,
+    kfac_precondition,
+    kfac_precondition_materialized,
+    sym_inverse,
+)
 from dattri_llm_amd.gradient.ops.materialize import materialize, materialize_blocked, materialize_factors
 from dattri_llm_amd.gradient.ops.preprocess import (
     extract_module_kwargs,
@@ -71,6 +91,10 @@ from dattri_llm_amd.gradient.ops.types import (
 )
 
 __all__ = [
+    "FisherAccumulator", "KroneckerAccumulator", "LayerFisherAccumulator", "LayerKroneckerAccumulator",
+    "dense_inverse", "ekfac_materialize", "ekfac_materialize_factors", "ekfac_precondition", "fim",
+    "fim_factors", "kfac", "kfac_cross", "kfac_cross_factors", "kfac_eigh", "kfac_factors",
+    "kfac_precondition", "kfac_precondition_materialized", "kronecker", "sym_inverse",
     "ALL_LAYER_TYPES", "CAPTURE_STYLES", "CONV_TRANSPOSE_TYPES", "CONV_TYPES", "EMBEDDING_TYPES",
     "LINEAR_TYPES", "MASK_KEYS", "NORM_TYPES", "PARAM_GRAD_TYPES", "PROJECTION_STYLES", "CostModel",
     "DattriProjector", "ProjectionMatrix", "apply_projection", "as_float", "calibrate",

@@ -35,6 +35,19 @@ moe_segments                   hooks/override_layers/fused_experts.py:219-228 to
 moe_regroup_dense              hooks/routing.py:71-86                         explicit scatter check
 moe_segment_ghost              dense-with-zeros cross_gram (routing.py:17-23) equals cross_gram on the regrouped
                                                                               zero-filled (B, T, d) factors
+kfac_factors                   gradient/ops/kronecker.py:65-118               brute-force sums of row outer products over
+                                                                              the rows with a non-zero gradient
+fim_factors                    gradient/ops/kronecker.py:121-141              brute-force sum of per-sample outer products
+sym_inverse                    gradient/ops/kronecker.py:144-152              (M + damping I) @ result == I
+kfac_cross_factors             gradient/ops/kronecker.py:178-202              vec(dW1)^T kron(G^-1, A^-1) vec(dW2) with the
+                                                                              Kronecker matrix formed explicitly; identity
+                                                                              inverses reduce to cross_gram
+ekfac_materialize_factors      gradient/ops/kronecker.py:215-233              U_G^T (g^T a) U_A from materialize_linear
+ekfac_rotate_materialized      gradient/ops/kronecker.py:323-354              equals ekfac_materialize_factors
+ekfac_precondition             gradient/ops/kronecker.py:413-458              lam = 1 undoes the rotation (U orthogonal);
+                                                                              score == vec(dW1)^T (U (x) U) diag(1/lam)
+                                                                              (U (x) U)^T vec(dW2), matrices formed
+kfac_precondition_materialized gradient/ops/kronecker.py:386-410              kron(G^-1, A^-1) @ vec(dW)
 =============================  =============================================  ===========================================
 """
 
@@ -48,6 +61,14 @@ __all__ = [
     "cross_gram_materialized",
     "cross_gram_per_token",
     "cross_gram_per_token_dense",
+    "ekfac_materialize_factors",
+    "ekfac_precondition",
+    "ekfac_rotate_materialized",
+    "fim_factors",
+    "kfac_cross_factors",
+    "kfac_factors",
+    "kfac_precondition_materialized",
+    "sym_inverse",
     "layer_norm_x_hat",
     "materialize_linear",
     "maybe_materialize_projected",
@@ -391,3 +412,72 @@ def moe_segment_ghost(a1, g1, tok1, a2, g2, tok2, batch1, batch2, tokens1, token
     A2 = moe_regroup_dense(a2, tok2, batch2, tokens2)
     G2 = moe_regroup_dense(g2, tok2, batch2, tokens2)
     return cross_gram_factorized(A1, G1, A2, G2, bias)
+
+
+# ---------------------------------------------------------------------------
+# K-FAC / EK-FAC (gradient/ops/kronecker.py), on preprocessed linear factors
+# ---------------------------------------------------------------------------
+
+
+def kfac_factors(a, g):
+    """kronecker.py:84-118 for a linear layer: over the flattened token rows
+    whose output gradient is not exactly zero (:65-81), A = a^T a / N and
+    G = g^T g / N.  Raises ValueError when every row is gradient-free."""
+    a_f = np.asarray(a, np.float64).reshape(-1, np.shape(a)[-1])
+    g_f = np.asarray(g, np.float64).reshape(-1, np.shape(g)[-1])
+    keep = ~(g_f == 0).all(axis=1)
+    a_f, g_f = a_f[keep], g_f[keep]
+    n = a_f.shape[0]
+    if n == 0:
+        raise ValueError("K-FAC factors are undefined: every token row carries a zero gradient")
+    return a_f.T @ a_f / n, g_f.T @ g_f / n
+
+
+def fim_factors(grad):
+    """kronecker.py:121-141: the empirical Fisher grad^T grad / B of per-sample
+    gradients (B, d)."""
+    grad = np.asarray(grad, np.float64)
+    return grad.T @ grad / grad.shape[0]
+
+
+def sym_inverse(m, damping: float = 0.0):
+    """kronecker.py:144-152: (m + damping I)^-1 through the eigendecomposition."""
+    w, v = np.linalg.eigh(np.asarray(m, np.float64))
+    return (v / (w + damping)[None, :]) @ v.T
+
+
+def kfac_cross_factors(a1, g1, a2, g2, a_inv, g_inv):
+    """kronecker.py:178-202: side 1's preprocessed factors right-multiplied by
+    A^-1 and G^-1, then the factorized cross-gram against side 2."""
+    a1w = _to_3d(np.asarray(a1, np.float64)) @ np.asarray(a_inv, np.float64)
+    g1w = _to_3d(np.asarray(g1, np.float64)) @ np.asarray(g_inv, np.float64)
+    return cross_gram_factorized(a1w, g1w, a2, g2)
+
+
+def ekfac_materialize_factors(a, g, u_a, u_g):
+    """kronecker.py:215-233: per-sample dW rotated into the K-FAC eigenbasis,
+    (B, D*K) of U_G^T dW U_A, from the rotated factors."""
+    a = _to_3d(np.asarray(a, np.float64)) @ np.asarray(u_a, np.float64)
+    g = _to_3d(np.asarray(g, np.float64)) @ np.asarray(u_g, np.float64)
+    return materialize_linear(a, g)
+
+
+def ekfac_rotate_materialized(block, u_a, u_g):
+    """kronecker.py:323-354 (linear): U_G^T dW U_A per row of a (B, d_out*d_in) block."""
+    u_a, u_g = np.asarray(u_a, np.float64), np.asarray(u_g, np.float64)
+    d_w = np.asarray(block, np.float64).reshape(len(block), u_g.shape[0], u_a.shape[0])
+    return np.einsum("oe,boi,if->bef", u_g, d_w, u_a).reshape(len(block), -1)
+
+
+def ekfac_precondition(m, u_a, u_g, lam):
+    """kronecker.py:413-458 (linear): U_G (M / lam) U_A^T, back in the original basis."""
+    u_a, u_g = np.asarray(u_a, np.float64), np.asarray(u_g, np.float64)
+    md = (np.asarray(m, np.float64) / np.asarray(lam, np.float64)).reshape(len(m), u_g.shape[1], u_a.shape[1])
+    return np.einsum("oe,bef,if->boi", u_g, md, u_a).reshape(len(m), -1)
+
+
+def kfac_precondition_materialized(block, a_inv, g_inv):
+    """kronecker.py:386-410: G^-1 dW A^-1 per row of a (B, k_g*k_a) block."""
+    a_inv, g_inv = np.asarray(a_inv, np.float64), np.asarray(g_inv, np.float64)
+    d_w = np.asarray(block, np.float64).reshape(len(block), g_inv.shape[0], a_inv.shape[0])
+    return (g_inv @ d_w @ a_inv).reshape(len(block), -1)

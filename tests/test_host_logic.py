@@ -78,10 +78,19 @@ def test_kernels_refuse_cpu_tensors(ops):
         ops.cross_gram(a, a, a, a, "nn.Linear", mode="factorized")
     with pytest.raises(NativeLibraryError):
         ops.materialize_factors(a, a, "nn.Linear")
+    with pytest.raises(NativeLibraryError):
+        ops.kfac_factors(a, a, "nn.Linear")
+    eye = torch.eye(8)
+    with pytest.raises(NativeLibraryError):
+        ops.kfac_cross_factors(a, a, a, a, "nn.Linear", eye, eye)
 
 
 def test_unsupported_layers_raise(ops):
     a = torch.randn(2, 3, 8)
+    with pytest.raises(NotImplementedError, match="normalization"):
+        ops.kfac_factors(a, a, "nn.LayerNorm")
+    with pytest.raises(NotImplementedError):
+        ops.kfac_cross_factors(a, a, a, a, "nn.Embedding", torch.eye(8), torch.eye(8))
     with pytest.raises(NotImplementedError):
         ops.preprocess_factors(a, a, "nn.Conv2d", {"has_bias": False})
     with pytest.raises(ValueError, match="factorized projection is undefined"):

@@ -312,3 +312,98 @@ def test_c1_oracle_matches_autograd_fixture():
         part = oracle.cross_gram(a1, g1, a2, g2, "nn.Linear", mode="factorized", bias=True)
         total = part if total is None else total + part
     assert rel_err(total, np.array(fixture["scores"])) <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# K-FAC / EK-FAC
+# ---------------------------------------------------------------------------
+
+
+def _spd(rng, n):
+    m = rng.standard_normal((n, n))
+    return m @ m.T / n + 0.5 * np.eye(n)
+
+
+def _dw(a, g):
+    """Per-sample dW = sum_t g_t a_t^T by explicit loops: (B, D, K)."""
+    b, t, k = a.shape
+    d = g.shape[-1]
+    out = np.zeros((b, d, k))
+    for i in range(b):
+        for s in range(t):
+            out[i] += np.outer(g[i, s], a[i, s])
+    return out
+
+
+def test_kfac_factors_brute_force_with_gradient_free_rows():
+    rng = _rng(41)
+    a = rng.standard_normal((3, 5, 4))
+    g = rng.standard_normal((3, 5, 3))
+    g[0, 1] = 0.0
+    g[2, 4] = 0.0
+    big_a, big_g = oracle.kfac_factors(a, g)
+    rows = [(i, s) for i in range(3) for s in range(5) if (i, s) not in ((0, 1), (2, 4))]
+    ref_a = sum(np.outer(a[i, s], a[i, s]) for i, s in rows) / len(rows)
+    ref_g = sum(np.outer(g[i, s], g[i, s]) for i, s in rows) / len(rows)
+    assert rel_err(big_a, ref_a) < 1e-12 and rel_err(big_g, ref_g) < 1e-12
+    with pytest.raises(ValueError):
+        oracle.kfac_factors(a, np.zeros_like(g))
+
+
+def test_fim_and_sym_inverse_identities():
+    rng = _rng(42)
+    grad = rng.standard_normal((6, 5))
+    ref = sum(np.outer(r, r) for r in grad) / 6
+    assert rel_err(oracle.fim_factors(grad), ref) < 1e-12
+    m = _spd(rng, 7)
+    inv = oracle.sym_inverse(m, 0.3)
+    assert np.abs((m + 0.3 * np.eye(7)) @ inv - np.eye(7)).max() < 1e-10
+
+
+def test_kfac_cross_equals_explicit_kronecker_form():
+    rng = _rng(43)
+    b1, b2, t, k, d = 3, 2, 4, 5, 3
+    a1, g1 = rng.standard_normal((b1, t, k)), rng.standard_normal((b1, t, d))
+    a2, g2 = rng.standard_normal((b2, t, k)), rng.standard_normal((b2, t, d))
+    a_inv, g_inv = np.linalg.inv(_spd(rng, k)), np.linalg.inv(_spd(rng, d))
+    got = oracle.kfac_cross_factors(a1, g1, a2, g2, a_inv, g_inv)
+    # vec(dW) row-major (index o*K + k): the preconditioner is kron(G^-1, A^-1)
+    f_inv = np.kron(g_inv, a_inv)
+    v1, v2 = _dw(a1, g1).reshape(b1, -1), _dw(a2, g2).reshape(b2, -1)
+    ref = v1 @ f_inv @ v2.T
+    assert rel_err(got, ref) < 1e-12
+    # identity inverses reduce to the plain cross-gram; whitening side 2 instead gives the same
+    assert rel_err(oracle.kfac_cross_factors(a1, g1, a2, g2, np.eye(k), np.eye(d)),
+                   oracle.cross_gram_factorized(a1, g1, a2, g2)) < 1e-12
+    assert rel_err(oracle.kfac_cross_factors(a2, g2, a1, g1, a_inv, g_inv).T, ref) < 1e-12
+
+
+def test_kfac_precondition_materialized_is_the_kronecker_product():
+    rng = _rng(44)
+    k, d = 4, 3
+    a_inv, g_inv = np.linalg.inv(_spd(rng, k)), np.linalg.inv(_spd(rng, d))
+    block = rng.standard_normal((5, d * k))
+    got = oracle.kfac_precondition_materialized(block, a_inv, g_inv)
+    assert rel_err(got, block @ np.kron(g_inv, a_inv).T) < 1e-12
+
+
+def test_ekfac_rotation_and_precondition():
+    rng = _rng(45)
+    b, t, k, d = 3, 4, 5, 3
+    a, g = rng.standard_normal((b, t, k)), rng.standard_normal((b, t, d))
+    _, u_a = np.linalg.eigh(_spd(rng, k))
+    _, u_g = np.linalg.eigh(_spd(rng, d))
+    rot = oracle.ekfac_materialize_factors(a, g, u_a, u_g)
+    dw = _dw(a, g)
+    ref = np.stack([u_g.T @ m @ u_a for m in dw]).reshape(b, -1)
+    assert rel_err(rot, ref) < 1e-12
+    assert rel_err(oracle.ekfac_rotate_materialized(dw.reshape(b, -1), u_a, u_g), ref) < 1e-12
+    # lam = 1 undoes the rotation (orthogonal bases)
+    assert rel_err(oracle.ekfac_precondition(rot, u_a, u_g, np.ones(d * k)), dw.reshape(b, -1)) < 1e-12
+    # the EK-FAC score against a raw side: vec(dW1)^T (U (x) U) diag(1/lam) (U (x) U)^T vec(dW2)
+    lam = rng.uniform(0.5, 2.0, d * k)
+    u = np.kron(u_g, u_a)
+    dw2 = _dw(rng.standard_normal((2, t, k)), rng.standard_normal((2, t, d))).reshape(2, -1)
+    score = dw.reshape(b, -1) @ oracle.ekfac_precondition(
+        oracle.ekfac_rotate_materialized(dw2, u_a, u_g), u_a, u_g, lam).T
+    assert rel_err(score, dw.reshape(b, -1) @ u @ np.diag(1 / lam) @ u.T @ dw2.T) < 1e-12
