@@ -24,6 +24,7 @@ Prints ONE JSON line.  Other workloads (not the headline):
 ``--workload project`` projected (k=64) capture of the Llama-7B MLP, 512 + 128 samples;
 ``--workload moe``     a Mixtral-shaped MoE layer on the segmented ghost route;
 ``--workload kfac``    the K-FAC covariance fit of the Llama-8B block's 7 linears over one train block;
+``--workload capture`` the LoGRA capture fused into autograd on a Llama-7B MLP (128 x 128 tokens);
 ``--workload copy``    a 2 GiB device copy, the reference point for byte counters.
 """
 
@@ -698,6 +699,159 @@ def bench_moe(args):
 
 
 # ---------------------------------------------------------------------------
+# projected capture fused into autograd (gradient/capture.py)
+# ---------------------------------------------------------------------------
+
+
+def bench_capture(args):
+    """LoGRA capture (k = 64, materialized) of a Llama-7B SwiGLU MLP (gate/up
+    4096 -> 11008, down 11008 -> 4096, bf16) inside autograd, one micro-batch of
+    128 samples x 128 tokens per step: forward + backward with FusedCapture
+    (the capture is the layers' backward: input gradient + one fused
+    project-and-outer-sum launch, no weight-gradient GEMM).  Beside it, on the
+    same inputs: the plain forward + backward (weight gradients, no capture) and
+    the hook-based capture of the reference's design (forward hook keeps the
+    activation, backward hook projects both factors and contracts them, weight
+    gradients still formed)."""
+    import torch
+    from torch import nn
+
+    from dattri_llm_amd.gradient import FusedCapture, ops
+
+    b, t, d, f, k = 128, 128, 4096, 11008, 64
+    torch.manual_seed(0)
+
+    class Mlp(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate = nn.Linear(d, f, bias=False)
+            self.up = nn.Linear(d, f, bias=False)
+            self.down = nn.Linear(f, d, bias=False)
+
+        def forward(self, x):
+            return self.down(nn.functional.silu(self.gate(x)) * self.up(x))
+
+    model = Mlp().to(device="cuda", dtype=torch.bfloat16)
+    for p_ in model.parameters():
+        p_.data.mul_(0.05)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    x = _randn((b, t, d), gen, torch.bfloat16)
+    w = _randn((b, t, d), gen, torch.bfloat16, d**-0.5)
+
+    def loss():
+        return (model(x).float() * w.float()).sum()
+
+    cap = FusedCapture(model, proj_dim=k, capture_style="materialized")
+    proj = ops.DattriProjector()
+    seen: dict = {}  # the last step's (input, grad_output) per layer, to time the capture launches alone
+    for name, slot in cap.slots.items():
+        inner = slot.capture
+
+        def keep(xa, ga, _inner=inner, _n=name):
+            seen[_n] = (xa, ga, _inner)
+            _inner(xa, ga)
+
+        slot.capture = keep
+
+    def fused():
+        cap.clear()
+        with cap:
+            loss().backward()
+        return cap.gradient()
+
+    def plain():
+        model.zero_grad(set_to_none=True)
+        loss().backward()
+
+    stash, out = {}, {}
+
+    def hooked():
+        model.zero_grad(set_to_none=True)
+        hs = []
+        for name, m in (("gate", model.gate), ("up", model.up), ("down", model.down)):
+            hs.append(m.register_forward_hook(lambda _m, inp, _o, n=name: stash.__setitem__(n, inp[0].detach())))
+
+            def bw(_m, _gi, go, n=name):
+                a_p, g_p = ops.project_factors(stash.pop(n), go[0].detach(), "nn.Linear", proj,
+                                               {"has_bias": False}, proj_dim=k)
+                out[n] = ops.materialize_factors(a_p, g_p, "nn.Linear")
+
+            hs.append(m.register_full_backward_hook(bw))
+        loss().backward()
+        for h in hs:
+            h.remove()
+
+    def run(fn, steps, warm):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    ms_plain = run(plain, args.steps, args.warmup)
+    ms_hook = run(hooked, args.steps, args.warmup)
+    ms = run(fused, args.steps, args.warmup)
+    cap.clear()
+    # The capture kernel (da_project_outer) back to back on the last step's
+    # tensors with the session's resolved matrices: GPU time per launch (inside
+    # backward, events around a launch would also hold the host work between).
+    from dattri_llm_amd import kernels
+
+    launches = []
+    for xa, ga, _inner in seen.values():
+        p_in = cap.projector.resolve(xa.shape[-1], proj_dim=k, proj_seed=cap.proj_seed + 1,
+                                     device=xa.device, dtype=xa.dtype)
+        p_out = cap.projector.resolve(ga.shape[-1], proj_dim=k, proj_seed=cap.proj_seed,
+                                      device=ga.device, dtype=ga.dtype)
+        launches.append((xa, ga, p_in.transposed, p_out.transposed))
+
+    def capture_kernels():
+        for xa, ga, pi, po in launches:
+            kernels.project_outer(xa, ga, pi, po)
+
+    reps = 10
+    for _ in range(2):
+        capture_kernels()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(reps):
+        capture_kernels()
+    e_ev.record()
+    torch.cuda.synchronize()
+    t_cap = s_ev.elapsed_time(e_ev) / (reps * len(launches))  # per layer launch
+    layer_bytes = {"gate": b * t * (d + f) * 2.0, "up": b * t * (d + f) * 2.0, "down": b * t * (f + d) * 2.0}
+    cap_bytes = sum(layer_bytes.values()) / 3  # average per capture launch
+    gbs = cap_bytes / t_cap / 1e6
+    return {
+        "metric": "captured samples/sec, LoGRA k=64 capture inside autograd (Llama-7B SwiGLU MLP, bf16)",
+        "value": round(b / (ms / 1e3), 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "llama-7b mlp (gate/up 4096->11008, down 11008->4096, SwiGLU) forward + backward, "
+                               "128 samples x 128 tokens, FusedCapture proj_dim 64 materialized"},
+        "roofline": {"bound": "hbm", "kernel": "da_project_outer (the capture launch of each layer's backward)",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "work_per_launch": f"{cap_bytes:.4g} B average = B x T x (d_in + d_out) x 2 B per layer",
+                     "launches_per_step": 3},
+        "kernels": {"fused_step_ms": round(ms, 4), "plain_backward_step_ms": round(ms_plain, 4),
+                    "hook_capture_step_ms": round(ms_hook, 4), "capture_ms_per_layer": round(t_cap, 4)},
+    }
+
+
+# ---------------------------------------------------------------------------
 # K-FAC covariance fit (gradient/ops/kronecker.py, streaming accumulators)
 # ---------------------------------------------------------------------------
 
@@ -820,7 +974,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "kfac", "copy"],
+    ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "kfac", "capture",
+                                           "copy"],
                     default="block")
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--no-gemm-ref", dest="gemm_ref", action="store_false",
@@ -837,7 +992,7 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
     runs = {"block": bench_block, "ghost": bench_ghost, "per_token": bench_per_token, "project": bench_project,
-            "moe": bench_moe, "kfac": bench_kfac, "copy": bench_copy}
+            "moe": bench_moe, "kfac": bench_kfac, "capture": bench_capture, "copy": bench_copy}
     result = runs[args.workload](args)
     roof = result.get("roofline") or {}
     if args.gemm_ref and roof.get("bound") == "mfma":

@@ -2,5 +2,6 @@
 
 from dattri_llm_amd.gradient import ops
 from dattri_llm_amd.gradient.gradient import Factorized, Gradient, GradientRecord
+from dattri_llm_amd.gradient.capture import FusedCapture
 
-__all__ = ["Factorized", "Gradient", "GradientRecord", "ops"]
+__all__ = ["Factorized", "FusedCapture", "Gradient", "GradientRecord", "ops"]
