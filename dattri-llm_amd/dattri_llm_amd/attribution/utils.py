@@ -170,7 +170,14 @@ def score_sources(
                 row[:, torch.tensor(cols, device=device)] = block
         if cache is not None:
             cache.clear()
-        chunks.append(row.cpu())
+        if row.is_cuda:
+            # an asynchronous copy into pinned host memory, so that the next
+            # block's transfer and kernels are not held behind this one's copy
+            host = torch.empty(row.shape, dtype=row.dtype, pin_memory=True)
+            host.copy_(row, non_blocking=True)
+            chunks.append(host)
+        else:
+            chunks.append(row)
         if per_token:
             t = row.shape[0] // max(len(ids), 1)
             for h, st in zip(ids, steps, strict=True):
@@ -180,5 +187,7 @@ def score_sources(
         else:
             row_ids.extend(ids)
             row_steps.extend(steps)
+    if chunks and torch.device(device).type == "cuda":
+        torch.cuda.synchronize(device)
     scores = torch.cat(chunks, dim=0) if chunks else torch.zeros(0, num_test)
     return scores, row_ids, row_steps, test_ids, (row_tokens if per_token else None)

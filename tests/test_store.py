@@ -1,0 +1,161 @@
+"""The on-disk gradient store (CPU): the reader against a store built by hand
+from the reference's memmap format (gradient/storage_manager.py:46-56,
+:620-694 -- raw 8-byte-aligned parts in .mmap.bin, a primitives-only
+.mmap.meta, an append-only index.jsonl), the writer's exact layout, block
+assembly, and the background writer."""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from dattri_llm_amd.gradient.gradient import Factorized, Gradient, GradientRecord
+from dattri_llm_amd.gradient.store import AsyncGradientWriter, GradientStore, records_to_block
+
+
+def _hand_store(root, rank_dir=None):
+    """Two records in one group, written byte by byte from the format description."""
+    d = root if rank_dir is None else root / rank_dir
+    d.mkdir(parents=True, exist_ok=True)
+    rng = np.random.default_rng(0)
+    dense = rng.standard_normal((2, 5)).astype(np.float32)          # 40 bytes
+    act = rng.standard_normal((2, 3, 3)).astype(np.float16)         # 36 bytes -> pad to 40
+    grad = rng.standard_normal((2, 3, 2)).astype(np.float32)        # 48 bytes
+    blob = bytearray()
+    specs = []
+    for arr, name in ((dense, "float32"), (act, "float16"), (grad, "float32")):
+        off = len(blob)
+        blob += arr.tobytes()
+        blob += b"\x00" * ((-len(blob)) % 8)
+        specs.append({"byte_off": off, "nbytes": arr.nbytes, "shape": list(arr.shape), "dtype": name})
+    (d / "batch_000000.mmap.bin").write_bytes(bytes(blob))
+    rec = lambda step, h, layers: {  # noqa: E731
+        "step": step, "input_hash": h, "sample_id_key": None,
+        "representation": {"fc": "materialized", "lin": "factorized"},
+        "layer_types": {"fc": "nn.Linear", "lin": "nn.Linear"}, "indexing": {"fc": "batch", "lin": "batch"},
+        "layers": layers}
+    layers = {"fc": {"kind": "dense", "parts": {"data": specs[0]}},
+              "lin": {"kind": "factorized", "parts": {"activation": specs[1], "pre_activation_grad": specs[2]},
+                      "module_kwargs": {"has_bias": True}, "batch_first": True}}
+    torch.save({"format": 2, "records": [rec(7, ["h0", "h1"], layers)]}, d / "batch_000000.mmap.meta")
+    prefix = "" if rank_dir is None else f"{rank_dir}/"
+    (d / "index.jsonl").write_text(json.dumps(
+        {"file": f"{prefix}batch_000000.mmap", "records": [{"idx": 0, "step": 7, "hashes": ["h0", "h1"]}]}) + "\n")
+    (d / "index_meta.json").write_text(json.dumps({"format": 2, "sample_id_key": None,
+                                                   "gradient_accumulation_steps": 1}))
+    return dense, act, grad
+
+
+def test_reader_follows_the_format(tmp_path):
+    dense, act, grad = _hand_store(tmp_path)
+    store = GradientStore(tmp_path)
+    assert store.available_steps() == [7]
+    assert store.iter_steps([7]) == [("batch_000000.mmap", {7: [0]})]
+    assert store.index["h1"] == [{"file": "batch_000000.mmap", "idx": 0, "step": 7, "sample_idx": 1}]
+    (rec,) = store.load_records("batch_000000.mmap")
+    assert rec.step == 7 and rec.input_hash == ["h0", "h1"]
+    assert np.array_equal(rec.gradient.data["fc"].numpy(), dense)
+    f = rec.gradient.data["lin"]
+    assert f.activation.dtype == torch.float16 and np.array_equal(f.activation.numpy(), act)
+    assert np.array_equal(f.pre_activation_grad.numpy(), grad) and f.module_kwargs == {"has_bias": True}
+    block, hashes = records_to_block([rec], [0])
+    assert hashes == ["h0", "h1"] and block.batch_size == 2
+
+
+def test_rank_directories_merge(tmp_path):
+    _hand_store(tmp_path, "rank_1")
+    store = GradientStore(tmp_path)
+    assert store.iter_steps(7) == [("rank_1/batch_000000.mmap", {7: [0]})]
+    (rec,) = store.load_records("rank_1/batch_000000.mmap")
+    assert rec.gradient.batch_size == 2
+
+
+def test_reader_refuses_pickles_and_other_formats(tmp_path):
+    _hand_store(tmp_path)
+    store = GradientStore(tmp_path)
+    with pytest.raises(NotImplementedError, match="pickled"):
+        store.load_records("batch_000001.pt")
+    meta = torch.load(tmp_path / "batch_000000.mmap.meta", weights_only=True)
+    meta["format"] = 1
+    torch.save(meta, tmp_path / "batch_000000.mmap.meta")
+    with pytest.raises(ValueError, match="format 1"):
+        store.load_records("batch_000000.mmap")
+    meta["format"] = 2
+    meta["records"][0]["layers"]["fc"]["parts"]["data"]["byte_off"] = 4
+    torch.save(meta, tmp_path / "batch_000000.mmap.meta")
+    with pytest.raises(ValueError, match="misaligned"):
+        store.load_records("batch_000000.mmap")
+
+
+def _records(step, n, seed):
+    gen = torch.Generator().manual_seed(seed)
+    recs = []
+    for i in range(n):
+        g = Gradient({"fc": "materialized", "lin": "factorized"},
+                     {"fc": torch.randn(2, 6, generator=gen),
+                      "lin": Factorized(torch.randn(2, 4, 3, generator=gen).bfloat16(),
+                                        torch.randn(2, 4, 5, generator=gen), module_kwargs={"has_bias": False})},
+                     {"fc": "nn.Linear", "lin": "nn.Linear"})
+        recs.append(GradientRecord(step, [f"s{seed}_{i}_a", f"s{seed}_{i}_b"], g))
+    return recs
+
+
+def test_writer_layout_and_round_trip(tmp_path):
+    store = GradientStore(tmp_path / "st")
+    recs = _records(3, 2, 1)
+    assert store.save_bulk(recs) == "batch_000000.mmap"
+    assert store.save_bulk(_records(4, 1, 2)) == "batch_000001.mmap"
+    meta = torch.load(tmp_path / "st" / "batch_000000.mmap.meta", weights_only=True)
+    assert meta["format"] == 2 and len(meta["records"]) == 2
+    raw = (tmp_path / "st" / "batch_000000.mmap.bin").read_bytes()
+    for r, m in zip(recs, meta["records"]):
+        for name, layer in m["layers"].items():
+            for key, spec in layer["parts"].items():
+                assert spec["byte_off"] % 8 == 0
+                t = r.gradient.data[name] if key == "data" else getattr(r.gradient.data[name], key)
+                assert raw[spec["byte_off"]:spec["byte_off"] + spec["nbytes"]] == t.contiguous().view(
+                    torch.uint8).flatten().numpy().tobytes()
+    lines = [json.loads(x) for x in (tmp_path / "st" / "index.jsonl").read_text().splitlines()]
+    assert lines[0] == {"file": "batch_000000.mmap", "records": [
+        {"idx": 0, "step": 3, "hashes": ["s1_0_a", "s1_0_b"]}, {"idx": 1, "step": 3, "hashes": ["s1_1_a", "s1_1_b"]}]}
+    again = GradientStore(tmp_path / "st")  # a fresh reader of the same directory
+    assert again.available_steps() == [3, 4]
+    block, hashes = records_to_block(again.load_records("batch_000000.mmap"), [0, 1])
+    assert hashes == ["s1_0_a", "s1_0_b", "s1_1_a", "s1_1_b"]
+    assert torch.equal(block.data["fc"], torch.cat([r.gradient.data["fc"] for r in recs]))
+    assert torch.equal(block.data["lin"].activation,
+                       torch.cat([r.gradient.data["lin"].activation for r in recs]))
+    with pytest.raises(KeyError):
+        records_to_block(again.load_records("batch_000000.mmap"), [0], ["nope"])
+
+
+def test_async_writer_keeps_order(tmp_path):
+    store = GradientStore(tmp_path)
+    with AsyncGradientWriter(store, max_pending=1) as w:
+        for step in range(4):
+            w.submit(_records(step, 1, 10 + step))
+        w.flush()
+        assert w.locations == [f"batch_{i:06d}.mmap" for i in range(4)]
+    assert GradientStore(tmp_path).available_steps() == [0, 1, 2, 3]
+    with pytest.raises(RuntimeError, match="closed"):
+        w.submit(_records(9, 1, 0))
+
+
+def test_parallel_read_and_buffer_views(tmp_path):
+    store = GradientStore(tmp_path)
+    store.save_bulk(_records(1, 3, 5))
+    total = store.bin_nbytes("batch_000000.mmap")
+    buf = torch.empty(total, dtype=torch.uint8)
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(4) as pool:
+        store.read_bin_into("batch_000000.mmap", buf, pool)
+    assert buf.numpy().tobytes() == (tmp_path / "batch_000000.mmap.bin").read_bytes()
+    a = store.load_records("batch_000000.mmap")
+    b = store.records_from(store.read_meta("batch_000000.mmap"), buf, "batch_000000.mmap")
+    for ra, rb in zip(a, b):
+        assert torch.equal(ra.gradient.data["fc"], rb.gradient.data["fc"])
+        assert torch.equal(ra.gradient.data["lin"].pre_activation_grad, rb.gradient.data["lin"].pre_activation_grad)
