@@ -305,6 +305,35 @@ __global__ __launch_bounds__(256) void score_gemm_reduce(const float* __restrict
   }
 }
 
+// Few partials per output (many output tiles, each with one or a few
+// workgroups): one thread per output sums its partials in order.
+constexpr int64_t kRowReduceMax = 32;
+__global__ __launch_bounds__(256) void score_gemm_reduce_rows(const float* __restrict__ partial, int64_t n,
+                                                              int64_t b1, int64_t b2, float* __restrict__ out,
+                                                              int64_t ld_row, int64_t ld_col, int accumulate) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= b1 * b2) return;
+  const float* p = partial + idx * n;
+  float sum = 0.f;
+  for (int64_t c = 0; c < n; ++c) sum += p[c];
+  const int64_t i = idx / b2, j = idx - i * b2;
+  float* o = out + i * ld_row + j * ld_col;
+  *o = accumulate ? *o + sum : sum;
+}
+
+// Sum the n partials of every output into out.
+int reduce_partials(const float* partial, int64_t n, int64_t b1, int64_t b2, float* out, int64_t ld_row,
+                    int64_t ld_col, int accumulate, hipStream_t st) {
+  const int64_t outs = b1 * b2;
+  if (outs > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_score_gemm: too many outputs");
+  if (n <= kRowReduceMax)
+    score_gemm_reduce_rows<<<(unsigned)((outs + 255) / 256), 256, 0, st>>>(partial, n, b1, b2, out, ld_row,
+                                                                            ld_col, accumulate);
+  else
+    score_gemm_reduce<<<(unsigned)outs, 256, 0, st>>>(partial, n, b1, b2, out, ld_row, ld_col, accumulate);
+  return check_launch("da_score_gemm(reduce)");
+}
+
 struct Plan {
   int64_t chunk_bytes, n_chunks;
   size_t ws;
@@ -456,11 +485,7 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
     }
     rc = check_launch("da_score_gemm(ring)");
     if (rc) return rc;
-    const int64_t n = b1 * b2;
-    if (n > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_score_gemm: too many outputs");
-    score_gemm_reduce<<<(unsigned)n, 256, 0, st>>>((const float*)workspace, p.nwg, b1, b2, out, ld_row, ld_col,
-                                                   accumulate);
-    return check_launch("da_score_gemm(reduce)");
+    return reduce_partials((const float*)workspace, p.nwg, b1, b2, out, ld_row, ld_col, accumulate, st);
   }
   ScoreArgs s;
   s.n_layers = n_layers;
@@ -494,11 +519,7 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
   }
   rc = check_launch("da_score_gemm(chunks)");
   if (rc) return rc;
-  const int64_t n = b1 * b2;
-  if (n > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_score_gemm: too many outputs");
-  score_gemm_reduce<<<(unsigned)n, 256, 0, st>>>(
-      (const float*)workspace, p.n_chunks, b1, b2, out, ld_row, ld_col, accumulate);
-  return check_launch("da_score_gemm(reduce)");
+  return reduce_partials((const float*)workspace, p.n_chunks, b1, b2, out, ld_row, ld_col, accumulate, st);
 }
 
 }  // extern "C"
