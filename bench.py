@@ -980,8 +980,10 @@ def bench_store(args):
 def bench_kfac(args):
     """K-FAC fit pass over one Llama-8B-block train block (8 x 2048 tokens):
     the A = a^T a and G = g^T g covariance sums of the 7 linears
-    (``LayerKroneckerAccumulator.update``), each a token-axis contraction on
-    the per-sample dW kernel with the block's 16384 rows as one sample."""
+    (``LayerKroneckerAccumulator.update``), each a symmetric token-axis
+    contraction (``da_row_gram``: the 256 x 256 tiles on or above the
+    diagonal, then the mirror) over the block's 16384 rows.  The work counted
+    is the distinct entries, 2 x rows x p(p+1)/2 flop per factor of width p."""
     import torch
 
     from dattri_llm_amd.gradient import ops
@@ -1010,7 +1012,7 @@ def bench_kfac(args):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     rows = n_train * t_train
-    flops = sum(2.0 * rows * (din * din + dout * dout) for _n, _a, din, dout in LINEARS)
+    flops = sum(1.0 * rows * (din * (din + 1) + dout * (dout + 1)) for _n, _a, din, dout in LINEARS)
     t_k = _mean_ms(timers, "kfac") * len(LINEARS)
     tf = flops / t_k / 1e9
     result = {
@@ -1028,10 +1030,12 @@ def bench_kfac(args):
         "data": "synthetic",
         "config": {"workload": "k-fac covariances (a^T a, g^T g, fp32 out) of the llama3-8b block's 7 linears "
                                "over one 8 x 2048-token train block"},
-        "roofline": {"bound": "mfma", "kernel": "materialize_tiles_tr (row Gram, one sample of 16384 rows)",
+        "roofline": {"bound": "mfma",
+                     "kernel": "materialize_tiles_tr (symmetric row Gram of 16384 rows) + mirror_lower",
                      "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "work_per_step": f"{flops:.4g} flop = sum over the 7 linears of 2 x 16384 x (d_in^2 + d_out^2)",
+                     "work_per_step": f"{flops:.4g} flop = sum over the 7 linears of 16384 x (d_in (d_in + 1) "
+                                      "+ d_out (d_out + 1)), the distinct entries of A and G",
                      "step_share": round(t_k / ms, 3)},
     }
     if args.cpu_baseline:

@@ -41,6 +41,8 @@ struct MatArgs {
   int64_t out_bstride, out_rstride;          // elements
   int64_t out_blk;                           // elements between 64-element output blocks
   int64_t tiles_m, tiles_n;                  // per sample
+  int sym;                                   // a == g (a row Gram): only tiles on or above the diagonal
+  int acc;                                   // add to the fp32 output instead of overwriting it
 };
 
 // Element offset (from the sample's base) of output (o, k): flat c = o*rstride + k
@@ -420,16 +422,29 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
 
   const int64_t ntiles = (int64_t)gridDim.x;
   const int64_t logical = xcd_remap(blockIdx.x, ntiles);
-  const int64_t per_sample = m.tiles_m * m.tiles_n;
-  const int64_t b = logical / per_sample;
-  const int64_t rem = logical - b * per_sample;
-  const int64_t per_group = (int64_t)kGroup * m.tiles_n;
-  const int64_t group = rem / per_group;
-  const int64_t first = group * kGroup;
-  const int64_t gsize = min(m.tiles_m - first, (int64_t)kGroup);
-  const int64_t in_group = rem - group * per_group;
-  const int64_t tm = first + in_group % gsize;
-  const int64_t tn = in_group / gsize;
+  int64_t b, tm, tn;
+  if (m.sym) {
+    // One sample; the tiles with tm <= tn, row by row (tiles_m == tiles_n).
+    b = 0;
+    int64_t r = logical;
+    tm = 0;
+    while (r >= m.tiles_n - tm) {
+      r -= m.tiles_n - tm;
+      ++tm;
+    }
+    tn = tm + r;
+  } else {
+    const int64_t per_sample = m.tiles_m * m.tiles_n;
+    b = logical / per_sample;
+    const int64_t rem = logical - b * per_sample;
+    const int64_t per_group = (int64_t)kGroup * m.tiles_n;
+    const int64_t group = rem / per_group;
+    const int64_t first = group * kGroup;
+    const int64_t gsize = min(m.tiles_m - first, (int64_t)kGroup);
+    const int64_t in_group = rem - group * per_group;
+    tm = first + in_group % gsize;
+    tn = in_group / gsize;
+  }
   const int64_t o0 = tm * trk::kBM, k0 = tn * trk::kBN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -603,9 +618,39 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
       const int row = rr + lane / CH, ch = lane % CH;
       const int64_t orow = o0 + 128 * wm + 32 * x + row;
       const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
-      const u32x4 val = ld16(wbuf + row * LROW + ch * 16);
-      if (orow < m.d && ocol < m.k) st16(obase + out_index(m, orow, ocol) * OS, val);
+      u32x4 val = ld16(wbuf + row * LROW + ch * 16);
+      if (orow < m.d && ocol < m.k) {
+        char* dst = obase + out_index(m, orow, ocol) * OS;
+        if constexpr (OT == DA_F32) {
+          if (m.acc) {
+            const f32x4 old = __builtin_bit_cast(f32x4, ld16(dst));
+            val = __builtin_bit_cast(u32x4, __builtin_bit_cast(f32x4, val) + old);
+          }
+        }
+        st16(dst, val);
+      }
     }
+  }
+}
+
+// Row Gram: copy the tiles above the diagonal (computed) to the ones below it.
+// Block (I, J) of 32 x 32 outputs with tile(I) > tile(J) (256-output tiles)
+// reads the transposed block (J, I) through LDS; both accesses are row-major.
+__global__ __launch_bounds__(256) void mirror_lower(float* __restrict__ out, int64_t n, int64_t ld) {
+  __shared__ float t[32][33];
+  const int64_t bi = blockIdx.y, bj = blockIdx.x;  // output block row, block column
+  if ((bi * 32) / trk::kBM <= (bj * 32) / trk::kBN) return;  // uniform: on or above the diagonal tiles
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = bj * 32 + ty + 8 * k, c = bi * 32 + tx;  // source (upper) element
+    t[ty + 8 * k][tx] = (r < n && c < n) ? out[r * ld + c] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = bi * 32 + ty + 8 * k, c = bj * 32 + tx;  // destination (lower) element
+    if (r < n && c < n) out[r * ld + c] = t[tx][ty + 8 * k];
   }
 }
 
@@ -728,6 +773,8 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
   m.out_blk = out_blk;
   m.tiles_m = (D + kBM - 1) / kBM;
   m.tiles_n = (K + kBN - 1) / kBN;
+  m.sym = 0;
+  m.acc = 0;
   hipStream_t st = (hipStream_t)stream;
 #define DA_MAT_CASE(DT)                                                         \
   switch (out_dtype) {                                                          \
@@ -741,4 +788,64 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
     default: DA_MAT_CASE(DA_F32)
   }
 #undef DA_MAT_CASE
+}
+
+// Row Gram out (+)= x^T x of x (rows, width), fp32 out: the transposing-read
+// dW kernel with every row as one token of one sample and both operands x,
+// over the tiles on or above the diagonal, then the mirror.  Rows are taken in
+// chunks whose buffer offsets fit 32 bits, each adding to the output.
+extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width, int64_t x_stride, float* out,
+                           int64_t ld_out, int accumulate, void* stream) {
+  using namespace da;
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_row_gram: bf16 or fp16 rows only");
+  if (rows < 0 || width < 0) return set_error(DA_ERR_INVALID, "da_row_gram: negative size");
+  if (width == 0) return DA_OK;
+  if (!out || (!x && rows > 0)) return set_error(DA_ERR_INVALID, "da_row_gram: NULL pointer");
+  const int64_t es = 2;
+  if ((width * es) % 16 || (x_stride * es) % 16 || x_stride < width || ((uintptr_t)x & 15))
+    return set_error(DA_ERR_INVALID,
+                     "da_row_gram: width and row stride must be multiples of 8 elements (stride >= width), "
+                     "rows 16-byte aligned");
+  if (ld_out < width || (ld_out * 4) % 16 || ((uintptr_t)out & 15))
+    return set_error(DA_ERR_INVALID, "da_row_gram: out row stride must be >= width and a multiple of 4");
+  hipStream_t st = (hipStream_t)stream;
+  if (rows == 0) return accumulate ? DA_OK : zero_f32_2d(out, width, width, ld_out, st);
+  const int64_t sb = x_stride * es;
+  const int64_t chunk = ((1LL << 31) - (1LL << 20)) / sb - trk::kTS;
+  if (chunk < trk::kTS) return set_error(DA_ERR_INVALID, "da_row_gram: rows too wide for 32-bit offsets");
+  MatArgs m;
+  m.batch = 1;
+  m.k = width;
+  m.d = width;
+  m.a_bstride = 0;
+  m.g_bstride = 0;
+  m.a_tstride = sb;
+  m.g_tstride = sb;
+  m.out = (char*)out;
+  m.out_bstride = 0;
+  m.out_rstride = ld_out;
+  m.out_blk = 64;
+  m.tiles_m = (width + trk::kBM - 1) / trk::kBM;
+  m.tiles_n = (width + trk::kBN - 1) / trk::kBN;
+  m.sym = 1;
+  const int64_t nt = m.tiles_m * (m.tiles_m + 1) / 2;
+  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+    m.a = (const char*)x + r0 * sb;
+    m.g = m.a;
+    m.tokens = rows - r0 < chunk ? rows - r0 : chunk;
+    m.acc = accumulate || r0 > 0;
+    if (dtype == DA_BF16)
+      materialize_tiles_tr<DA_BF16, DA_F32><<<(unsigned)nt, kThreads, 0, st>>>(m);
+    else
+      materialize_tiles_tr<DA_F16, DA_F32><<<(unsigned)nt, kThreads, 0, st>>>(m);
+    const int rc = check_launch("da_row_gram");
+    if (rc) return rc;
+  }
+  const int64_t nb = (width + 31) / 32;
+  if (m.tiles_m > 1) {
+    mirror_lower<<<dim3((unsigned)nb, (unsigned)nb), 256, 0, st>>>(out, width, ld_out);
+    return check_launch("da_row_gram(mirror)");
+  }
+  return DA_OK;
 }

@@ -80,15 +80,20 @@ def _drop_gradient_free_rows(a_f: torch.Tensor, g_f: torch.Tensor):
 def row_gram(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 ``x^T y`` over the rows of ``x (N, p)`` and ``y (N, q)`` -> ``(p, q)``.
 
-    The per-sample dW kernel with all N rows as one sample (it computes
+    ``y`` omitted (``x^T x``, 16-bit rows): ``da_row_gram``, which computes the
+    tiles on or above the diagonal once and mirrors them.  Otherwise the
+    per-sample dW kernel with all N rows as one sample (it computes
     ``sum_t y[t, o] x[t, k]`` into index ``o*p + k``), in row chunks below
     1 GiB that are added in fp32."""
     y = x if y is None else y
     if x.ndim != 2 or y.ndim != 2 or x.shape[0] != y.shape[0]:
         raise ValueError("row_gram expects (N, p) and (N, q) with the same N")
+    same = y is x
     x, y = dtypes.align(x, y)
     kd = dtypes.kernel_dtype(x.dtype)
     x, y = x.to(kd), y.to(kd)
+    if same and kd in (torch.bfloat16, torch.float16):
+        return kernels.row_gram(x)  # the symmetric kernel: tiles on or above the diagonal, mirrored
     n, p, q = x.shape[0], x.shape[1], y.shape[1]
     out = torch.zeros(q, p, dtype=torch.float32, device=x.device)
     if n == 0 or p == 0 or q == 0:
@@ -310,6 +315,19 @@ def _all_reduce_sum(t: torch.Tensor) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 
 
+def _accumulate_gram(acc: torch.Tensor | None, x: torch.Tensor) -> torch.Tensor:
+    """``acc + x^T x`` in fp32: the product itself when ``acc`` is None (no
+    zero fill), else added into ``acc`` -- in the kernel's epilogue for 16-bit
+    rows."""
+    if acc is None:
+        return row_gram(x)
+    if x.dtype in (torch.bfloat16, torch.float16) and acc.dtype == torch.float32 and acc.is_contiguous():
+        kernels.row_gram(x, out=acc, accumulate=True)
+    else:
+        acc += row_gram(x)
+    return acc
+
+
 @dataclass
 class LayerKroneckerAccumulator:
     """Streaming K-FAC covariance sums of one layer (kronecker.py:460-550)."""
@@ -322,11 +340,8 @@ class LayerKroneckerAccumulator:
         a, g = preprocess_factors(a, g, layer_type, module_kwargs, include_bias)
         a_f, g_f = _flatten_for_kfac(a, g, layer_type)
         a_f, g_f = _drop_gradient_free_rows(a_f, g_f)
-        if self._A is None:
-            self._A = torch.zeros(a_f.shape[-1], a_f.shape[-1], dtype=torch.float32, device=a_f.device)
-            self._G = torch.zeros(g_f.shape[-1], g_f.shape[-1], dtype=torch.float32, device=g_f.device)
-        self._A += row_gram(a_f)
-        self._G += row_gram(g_f)
+        self._A = _accumulate_gram(self._A, a_f)
+        self._G = _accumulate_gram(self._G, g_f)
         self._n += a_f.shape[-2]
 
     def all_reduce(self) -> None:

@@ -369,6 +369,41 @@ def materialize_linear(
     return out
 
 
+def row_gram(x: torch.Tensor, *, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """fp32 ``x^T x`` of bf16/fp16 rows ``x (N, p)`` -> ``(p, p)``; with
+    ``accumulate`` it is added to ``out``.  The product is computed once per
+    tile pair on or above the diagonal and mirrored."""
+    dev = nat.require_device(x, out)
+    if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("row_gram expects bf16/fp16 rows (N, p)")
+    n, p = x.shape
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs out")
+        out = torch.empty(p, p, dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or out.shape != (p, p) or out.stride(1) != 1:
+        raise ValueError("row_gram out must be (p, p) fp32 with unit column stride")
+    if p == 0:
+        return out
+    vec = _chunk_elems(x.dtype)
+    xp = prepare_rows(x, -(-p // vec) * vec)
+    if xp.shape[-1] != p:  # padded columns: the product of the padded rows, then the (p, p) corner
+        full = row_gram(xp)
+        if accumulate:
+            out += full[:p, :p]
+        else:
+            out.copy_(full[:p, :p])
+        return out
+    if xp.stride(1) != 1:
+        xp = xp.contiguous()
+    nat.check(
+        nat.load().da_row_gram(xp.data_ptr(), nat.dtype_code(xp.dtype), n, p, xp.stride(0), out.data_ptr(),
+                               out.stride(0), int(accumulate), nat.stream_ptr(dev)),
+        "row_gram",
+    )
+    return out
+
+
 def _column_sums(g: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     """sum_t g[b, t, :] through the materialize kernel with a ones activation."""
     b, t, _ = g.shape

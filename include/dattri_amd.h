@@ -189,6 +189,20 @@ int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch
                           int64_t out_blk, void* stream);
 
 /*
+ * Row Gram: out (+)= x^T x, fp32 (width, width) with row stride ld_out, of the
+ * bf16/fp16 rows x (rows, width) with row stride x_stride (elements; width and
+ * x_stride multiples of 8, rows 16-byte aligned).  accumulate = 0 overwrites,
+ * 1 adds; rows = 0 (x may then be NULL) zeroes or leaves out.  The symmetric product is computed once per pair of tiles (the ones
+ * on or above the diagonal) and mirrored.  Returns DA_ERR_UNSUPPORTED for
+ * other dtypes.  Replaces the covariance products of the K-FAC factors and the
+ * empirical Fisher, dattri_llm/gradient/ops/kronecker.py:111-112
+ * ((a_f^T a_f), (g_f^T g_f)), :136 (grad^T grad) and the accumulators'
+ * :512-513 and :594.
+ */
+int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width, int64_t x_stride, float* out,
+                int64_t ld_out, int accumulate, void* stream);
+
+/*
  * One dense layer of a score GEMM: m1 is (B1, width), m2 is (B2, width).
  * Element c of row r of side s lives at  m_s + r*ld_s + (c/64)*blk_s + c%64
  * (elements): rows are sequences of 64-element blocks.  blk_s = 64 (or 0) is

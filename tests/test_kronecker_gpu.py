@@ -174,3 +174,72 @@ def test_accumulators_match_one_shot(device):
     capped.update(Gradient({"fc": "factorized"}, {"fc": Factorized(*[x.to(device) for x in blocks[0]])},
                            {"fc": LIN}), ["fc"])
     assert capped.skipped == {"fc": 40 * 24} and capped.result() == {}
+
+
+# ---- the symmetric row Gram (da_row_gram) on its own -------------------------
+
+def _rows(seed, n, p, dtype):
+    gen = torch.Generator().manual_seed(seed)
+    return (torch.randn(n, p, generator=gen) / p**0.25).to(dtype)
+
+
+def _off_diagonal_tiles_mirrored(out, tile=256):
+    """Tiles below the diagonal are copies of the ones above it, bit for bit."""
+    p = out.shape[0]
+    for i in range(tile, p, tile):
+        for j in range(0, i, tile):
+            if not torch.equal(out[i:i + tile, j:j + tile], out[j:j + tile, i:i + tile].T):
+                return False
+    return True
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,p", [(1000, 40), (5000, 264), (777, 520), (3000, 1032), (64, 300), (1, 8)])
+def test_row_gram_kernel(device, dtype, n, p):
+    from dattri_llm_amd import kernels
+
+    x = _rows(n + p, n, p, dtype)
+    want = x.double().T @ x.double()
+    got = kernels.row_gram(x.to(device))
+    torch.cuda.synchronize()
+    assert got.shape == (p, p) and got.dtype == torch.float32
+    # exactly representable inputs, fp32 accumulation: far inside the fp32 bar
+    assert rel_err(got.double().cpu(), want) <= 1e-4
+    assert _off_diagonal_tiles_mirrored(got.cpu())
+
+
+def test_row_gram_accumulate_and_out_stride(device):
+    from dattri_llm_amd import kernels
+
+    p = 520
+    x1, x2 = _rows(1, 900, p, torch.bfloat16), _rows(2, 1300, p, torch.bfloat16)
+    base = torch.full((p, p + 8), float("nan"), device=device)
+    out = base[:, :p]  # row stride p + 8: the 8 columns past p must stay untouched
+    kernels.row_gram(x1.to(device), out=out)
+    kernels.row_gram(x2.to(device), out=out, accumulate=True)
+    want = x1.double().T @ x1.double() + x2.double().T @ x2.double()
+    assert rel_err(out.double().cpu(), want) <= 1e-4
+    assert torch.isnan(base[:, p:]).all()
+    kernels.row_gram(x1[:0].to(device), out=out, accumulate=True)  # no rows: unchanged
+    assert rel_err(out.double().cpu(), want) <= 1e-4
+    assert torch.equal(kernels.row_gram(x1[:0].to(device)).cpu(), torch.zeros(p, p))
+    with pytest.raises(ValueError):
+        kernels.row_gram(x1.float().to(device))
+    with pytest.raises(ValueError):
+        kernels.row_gram(x1.to(device), accumulate=True)
+
+
+def test_row_gram_row_chunks(device):
+    """Rows 4 MiB apart: the entry point splits them into chunks whose buffer
+    offsets stay below 2^31 bytes (479 + 479 + 42 rows), each adding to the
+    output."""
+    from dattri_llm_amd import kernels
+
+    n, p, stride = 1000, 264, 1 << 21
+    x = _rows(7, n, p, torch.bfloat16)
+    big = torch.zeros(n, stride, dtype=torch.bfloat16, device=device)
+    big[:, :p] = x.to(device)
+    got = kernels.row_gram(big[:, :p])
+    want = x.double().T @ x.double()
+    assert rel_err(got.double().cpu(), want) <= 1e-4
+    del big
