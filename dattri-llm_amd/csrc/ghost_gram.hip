@@ -21,6 +21,9 @@
 // workgroups are remapped so each XCD owns a contiguous run of tiles, grouped
 // a few row tiles wide, so the concurrently running tiles on one XCD share
 // their operand row blocks through that XCD's L2.
+#include <algorithm>
+#include <vector>
+
 #include "common.h"
 
 namespace da {
@@ -629,7 +632,11 @@ __device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, 
 template <int DT>
 __global__ __launch_bounds__(kThreads, 1) void ghost_grouped_tiles_v2(GroupedArgs ga) {
   __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
-  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  // Tiles go to the XCDs round-robin in launch order (no XCD remap): the host
+  // orders the groups longest reduction first, so every XCD gets the same mix
+  // of tile lengths, longest first.  A contiguous range per XCD would hand the
+  // long groups' tiles to some XCDs and the short ones to the rest.
+  const int64_t logical = blockIdx.x;
   int e = 0;
   while (e + 1 < ga.n_groups && ga.grp[e + 1].tile0 <= logical) ++e;
   const GroupDev& G = ga.grp[e];
@@ -1157,6 +1164,13 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
   float* part = (float*)((char*)workspace + ((plan.meta_ints * sizeof(int32_t) + 255) / 256) * 256);
   int64_t meta_off = 0, part_off = 0;
   bool first_launch = true;
+  // Groups in order of decreasing reduction length K + D (stable): the tile
+  // kernel deals tiles to the XCDs round-robin, so this is a longest-first
+  // schedule on every XCD.  The partial sums land in the same per-pair bins
+  // whatever the order.
+  std::vector<int> order(n_groups);
+  for (int e = 0; e < n_groups; ++e) order[e] = e;
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return K[x] + D[x] > K[y] + D[y]; });
   for (int g0 = 0; g0 < n_groups; g0 += kMaxGroups) {
     const int n = n_groups - g0 < kMaxGroups ? n_groups - g0 : kMaxGroups;
     GroupedArgs ga;
@@ -1169,8 +1183,9 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
     ga.meta = meta;
     int64_t tiles = 0;
     for (int q = 0; q < n; ++q) {
-      const da_factor_side& x = s1[g0 + q];
-      const da_factor_side& y = s2[g0 + q];
+      const int e = order[g0 + q];
+      const da_factor_side& x = s1[e];
+      const da_factor_side& y = s2[e];
       const int64_t tr = (x.tokens + plan.tile_r - 1) / plan.tile_r, tc = (y.tokens + plan.tile_c - 1) / plan.tile_c;
       GroupDev& G = ga.grp[ga.n_groups++];
       G.a1 = (const char*)x.act;
@@ -1193,8 +1208,8 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
       G.part_off = part_off;
       G.part_ld = tc + b2;
       G.meta_off = meta_off;
-      G.kbytes_a = K[g0 + q] * es;
-      G.kbytes_g = D[g0 + q] * es;
+      G.kbytes_a = K[e] * es;
+      G.kbytes_g = D[e] * es;
       G.bias = x.has_bias ? 1.f : 0.f;
       tiles += tr * tc;
       part_off += (tr + b1) * (tc + b2);

@@ -178,13 +178,18 @@ def test_ghost_gram_grouped(device, dtype, bias, n_exp):
     assert rel_err(acc.cpu().numpy(), ref + 1.0) <= TOL[dtype]
 
 
-def test_moe_layers_cross_gram(device):
-    """Experts of two routed layers (different widths, one with bias) in one launch."""
+@pytest.mark.parametrize("wide_first", [True, False])
+def test_moe_layers_cross_gram(device, wide_first):
+    """Experts of two routed layers (different widths, one with bias) in one
+    launch.  The launch deals tiles longest reduction first, so the narrower
+    layer first exercises the reordering of the groups."""
     from dattri_llm_amd.gradient import ops
 
     gen = torch.Generator().manual_seed(41)
     b, tokens, n_exp = 4, 200, 3
-    shapes = [((64, 160), True), ((128, 64), False)]  # ((d_in, d_out), bias); the wider one first
+    shapes = [((64, 160), True), ((128, 64), False)]  # ((d_in, d_out), bias)
+    if not wide_first:
+        shapes = shapes[::-1]
     flat = torch.arange(b * tokens)
     toks = [[flat[torch.rand(b * tokens, generator=gen) < 0.4] for _ in range(n_exp)] for _ in range(2)]
     segs = [ops.moe.segment_experts([t.to(device) for t in side], b, tokens) for side in toks]
