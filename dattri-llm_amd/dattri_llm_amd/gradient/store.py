@@ -361,26 +361,34 @@ class PinnedBlockSource:
     def __len__(self) -> int:
         return sum(len(by_step) for _f, by_step in self.store.iter_steps(self.steps))
 
+    @staticmethod
+    def _put(out: queue.Queue, item, stop: threading.Event) -> bool:
+        """Hand ``item`` to the consumer; False once the consumer has stopped
+        (so a reader never blocks on a full queue nobody drains)."""
+        while not stop.is_set():
+            try:
+                out.put(item, timeout=0.1)
+                return True
+            except queue.Full:
+                continue
+        return False
+
     def _host_files(self, out: queue.Queue, stop: threading.Event) -> None:
-        """Reader thread: each file's meta and its bytes in a pinned buffer."""
+        """Reader thread: each file's meta and its bytes in a pinned buffer,
+        then ``None``; an exception is handed over in place of the rest."""
         try:
             with ThreadPoolExecutor(max_workers=8) as pool:
                 for file_rel, by_step in self.store.iter_steps(self.steps):
+                    if stop.is_set():
+                        return
                     payload = self.store.read_meta(file_rel)
                     host = torch.empty(self.store.bin_nbytes(file_rel), dtype=torch.uint8, pin_memory=True)
                     self.store.read_bin_into(file_rel, host, pool)
-                    item = (file_rel, by_step, payload, host)
-                    while not stop.is_set():
-                        try:
-                            out.put(item, timeout=0.1)
-                            break
-                        except queue.Full:
-                            continue
-                    if stop.is_set():
+                    if not self._put(out, (file_rel, by_step, payload, host), stop):
                         return
-            out.put(None)
+            self._put(out, None, stop)
         except BaseException as exc:  # noqa: BLE001 - handed to the consumer
-            out.put(exc)
+            self._put(out, exc, stop)
 
     def __iter__(self):
         if self.device.type != "cuda":

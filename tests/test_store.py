@@ -159,3 +159,32 @@ def test_parallel_read_and_buffer_views(tmp_path):
     for ra, rb in zip(a, b):
         assert torch.equal(ra.gradient.data["fc"], rb.gradient.data["fc"])
         assert torch.equal(ra.gradient.data["lin"].pre_activation_grad, rb.gradient.data["lin"].pre_activation_grad)
+
+
+def test_reader_thread_never_blocks_after_stop(tmp_path):
+    """The source's reader thread hands over blocks, its end marker and any
+    error through a bounded queue; once the consumer stops, none of those puts
+    may block (a full queue that nobody drains)."""
+    import queue
+    import threading
+    import time
+
+    from dattri_llm_amd.gradient.store import PinnedBlockSource
+
+    store = GradientStore(tmp_path)
+    store.save_bulk(_records(1, 2, 7))
+    src = PinnedBlockSource(store, device="cuda")
+    full = queue.Queue(maxsize=1)
+    full.put("occupied")
+    stop = threading.Event()
+    stop.set()
+    t0 = time.perf_counter()
+    assert PinnedBlockSource._put(full, "x", stop) is False
+    src._host_files(full, stop)  # stopped before the first file: returns at once
+    assert time.perf_counter() - t0 < 2.0 and full.get_nowait() == "occupied"
+    # A failing read (here: no pinned memory without a GPU, or any I/O error)
+    # reaches a live consumer as the exception object itself.
+    if not torch.cuda.is_available():
+        out = queue.Queue(maxsize=1)
+        src._host_files(out, threading.Event())
+        assert isinstance(out.get_nowait(), BaseException)
