@@ -45,3 +45,49 @@ def test_abi_version_and_error_plumbing():
     status = lib.da_selftest_mfma(0, 32, None, None, None, None)
     assert status == _native.DA_ERR_INVALID
     assert b"null" in lib.da_last_error()
+
+
+def test_argument_checks_fail_before_any_gpu_work():
+    """Each entry point validates its arguments on the host first: a bad call
+    returns its status and message without touching a device.  Pointers here
+    are aligned placeholders that no rejected call dereferences."""
+    from dattri_llm_amd import _native
+
+    lib = _native.load()
+    X, OUT = 0x10000, 0x20000  # 16-byte aligned, never dereferenced
+    bf, f32 = _native.DA_BF16, _native.DA_F32
+
+    def check(status, code, words):
+        assert status == code, (status, lib.da_last_error())
+        msg = lib.da_last_error().decode()
+        assert all(w in msg for w in words), msg
+
+    # da_row_gram(x, dtype, rows, width, x_stride, out, ld_out, accumulate, stream)
+    check(lib.da_row_gram(X, f32, 10, 8, 8, OUT, 8, 0, None), _native.DA_ERR_UNSUPPORTED, ["bf16 or fp16"])
+    check(lib.da_row_gram(X, bf, -1, 8, 8, OUT, 8, 0, None), _native.DA_ERR_INVALID, ["negative"])
+    check(lib.da_row_gram(None, bf, 10, 8, 8, OUT, 8, 0, None), _native.DA_ERR_INVALID, ["NULL"])
+    check(lib.da_row_gram(X, bf, 10, 8, 8, None, 8, 0, None), _native.DA_ERR_INVALID, ["NULL"])
+    check(lib.da_row_gram(X, bf, 10, 12, 12, OUT, 12, 0, None), _native.DA_ERR_INVALID, ["multiples of 8"])
+    check(lib.da_row_gram(X + 8, bf, 10, 8, 8, OUT, 8, 0, None), _native.DA_ERR_INVALID, ["aligned"])
+    check(lib.da_row_gram(X, bf, 10, 8, 8, OUT, 6, 0, None), _native.DA_ERR_INVALID, ["out row stride"])
+    # nothing to do: no launch, success (no rows with accumulate, or no width)
+    assert lib.da_row_gram(None, bf, 0, 8, 8, OUT, 8, 1, None) == _native.DA_OK
+    assert lib.da_row_gram(X, bf, 10, 0, 8, OUT, 8, 0, None) == _native.DA_OK
+
+    # da_materialize_linear(a, g, dtype, batch, tokens, K, D, a_bs, a_ts, g_bs, g_ts, bias,
+    #                       out, out_dtype, out_bs, out_rs, out_blk, stream)
+    def mat(dtype=bf, k=64, d=64, a=X, blk=64, out_rs=64, tokens=4):
+        return lib.da_materialize_linear(a, X, dtype, 2, tokens, k, d, 4 * k, k, 4 * d, d, 0, OUT, f32,
+                                         d * out_rs, out_rs, blk, None)
+
+    check(mat(dtype=9), _native.DA_ERR_INVALID, ["bad dtype"])
+    check(mat(k=12), _native.DA_ERR_INVALID, ["multiples of 8"])
+    check(mat(a=None), _native.DA_ERR_INVALID, ["NULL"])
+    check(mat(blk=32), _native.DA_ERR_INVALID, ["out_blk"])
+    check(mat(out_rs=32), _native.DA_ERR_INVALID, ["row stride"])
+    check(mat(tokens=0), _native.DA_ERR_INVALID, ["tokens"])
+
+    # da_project_outer: projected widths above 64 are refused before anything else
+    st = lib.da_project_outer(X, X, bf, 2, 16, 64, 64, 1024, 64, 1024, 64, X, 65, 64, None, X, 64, 64,
+                              OUT, f32, 65 * 64, None, 0, None)
+    check(st, _native.DA_ERR_UNSUPPORTED, ["projected widths"])
