@@ -672,7 +672,7 @@ def bench_moe(args):
     flops = sum(2.0 * rows[0][e] * rows[1][e] * (din + dout) for e in range(n_exp) for _n, din, dout in layers)
     t_ghost = _mean_ms(timers, "ghost")
     tf = flops / t_ghost / 1e9
-    return {
+    result = {
         "metric": "train x query pair-scores/sec (Mixtral-shaped MoE layer, top-2 of 8, bf16)",
         "value": round(b * b / (ms / 1e3), 1),
         "unit": "pair-scores/s",
@@ -697,6 +697,35 @@ def bench_moe(args):
                      "launches_per_step": 1, "step_share": round(t_ghost / ms, 3)},
         "kernels": {"route_ms": round(_mean_ms(timers, "route"), 4), "ghost_ms": round(t_ghost, 4)},
     }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import oracle
+
+        # The reference's CPU path on the whole step (all 16 train x 16 query samples): per expert
+        # and linear, the routed rows regrouped to zero-filled (B, T, d) factors, then the dense
+        # ghost product.
+        ns = b
+        sample = []
+        for e in range(n_exp):
+            toks = [routing[side][e][1] for side in range(2)]
+            keep = [(tk < ns * t).cpu() for tk in toks]
+            for li, (name, _i, _o) in enumerate(layers):
+                fac = [tuple(x[k.to(x.device)].float().cpu().numpy() for x in caps[side][e][name])
+                       for side, k in zip(range(2), keep)]
+                sample.append((fac, [tk.cpu()[k].numpy() for tk, k in zip(toks, keep)]))
+        t0 = time.perf_counter()
+        total = np.zeros((ns, ns))
+        for ((a1, g1), (a2, g2)), (tk1, tk2) in sample:
+            total += oracle.moe_segment_ghost(a1, g1, tk1, a2, g2, tk2, ns, ns, t, t)
+        dt = time.perf_counter() - t0
+        cores, model = cpu_info()
+        result["cpu_baseline"] = {"value": round(ns * ns / dt, 3), "unit": "pair-scores/s", "cores": blas_threads(),
+                                  "kind": "port",
+                                  "sample": f"numpy float64 oracle (the reference's zero-filled regroup + dense ghost "
+                                            f"product) over all 8 experts and both linears for {ns} train x {ns} "
+                                            f"query samples ({dt:.2f} s); host {model}, {cores} cores visible"}
+    return result
 
 
 # ---------------------------------------------------------------------------
