@@ -856,7 +856,7 @@ def bench_capture(args):
     layer_bytes = {"gate": b * t * (d + f) * 2.0, "up": b * t * (d + f) * 2.0, "down": b * t * (f + d) * 2.0}
     cap_bytes = sum(layer_bytes.values()) / 3  # average per capture launch
     gbs = cap_bytes / t_cap / 1e6
-    return {
+    result = {
         "metric": "captured samples/sec, LoGRA k=64 capture inside autograd (Llama-7B SwiGLU MLP, bf16)",
         "value": round(b / (ms / 1e3), 1),
         "unit": "samples/s",
@@ -879,6 +879,41 @@ def bench_capture(args):
         "kernels": {"fused_step_ms": round(ms, 4), "plain_backward_step_ms": round(ms_plain, 4),
                     "hook_capture_step_ms": round(ms_hook, 4), "capture_ms_per_layer": round(t_cap, 4)},
     }
+    if args.cpu_baseline:
+        import copy
+
+        import oracle
+        from dattri_llm_amd.gradient.ops.projection import gaussian_matrix
+
+        # The reference's capture on the CPU for the whole step (all 128 samples): fp32 forward +
+        # backward with hooks keeping each layer's (input, output gradient), then the oracle's
+        # projected outer product per layer.
+        nb = b
+        cpu_model = copy.deepcopy(model).float().cpu()
+        xs, ws = x[:nb].float().cpu(), w[:nb].float().cpu()
+        kept: dict = {}
+        hooks = []
+        shapes = {"gate": (d, f), "up": (d, f), "down": (f, d)}
+        for name in shapes:
+            mod = getattr(cpu_model, name)
+            hooks.append(mod.register_forward_hook(lambda _m, i, _o, n=name: kept.__setitem__(n, [i[0].detach()])))
+            hooks.append(mod.register_full_backward_hook(lambda _m, _gi, go, n=name: kept[n].append(go[0].detach())))
+        mats = {n: (gaussian_matrix(din, k, 2 * li + 1).numpy(), gaussian_matrix(dout, k, 2 * li).numpy())
+                for li, (n, (din, dout)) in enumerate(shapes.items())}
+        t0 = time.perf_counter()
+        (cpu_model(xs) * ws).sum().backward()
+        feats = [oracle.project_outer(av.numpy(), gv.numpy(), *mats[n]) for n, (av, gv) in kept.items()]
+        dt = time.perf_counter() - t0
+        for h in hooks:
+            h.remove()
+        assert all(fe.shape == (nb, k * k) for fe in feats)
+        cores, model_name = cpu_info()
+        result["cpu_baseline"] = {"value": round(nb / dt, 3), "unit": "samples/s", "cores": blas_threads(),
+                                  "kind": "port",
+                                  "sample": f"torch fp32 forward + backward on the CPU with hook capture and the "
+                                            f"numpy oracle's projected outer product, all {nb} samples of the step "
+                                            f"({dt:.2f} s); host {model_name}, {cores} cores visible"}
+    return result
 
 
 # ---------------------------------------------------------------------------
