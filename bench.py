@@ -1006,6 +1006,32 @@ def bench_store(args):
         e_ev.record()
         torch.cuda.synchronize()
         t_score = s_ev.elapsed_time(e_ev) / reps
+        cpu = None
+        if args.cpu_baseline:
+            import numpy as np
+
+            import oracle
+
+            # The reference's CPU path over the whole store: each memmap group read back
+            # (load_records), its blocks assembled, then the numpy oracle's layer-summed scores
+            # against the 128 queries.
+            q_recs = test.load_records(test.iter_steps(test.available_steps())[0][0])
+            q_block, _ = records_to_block(q_recs, list(range(len(q_recs))))
+            q_np = [q_block.data[l].float().numpy() for l in layers]
+            t0 = time.perf_counter()
+            rows = 0
+            for f, by_step in train.iter_steps(train.available_steps()):
+                recs = train.load_records(f)
+                for _step, idxs in by_step.items():
+                    blk, _h = records_to_block(recs, idxs)
+                    oracle.score_gemm([blk.data[l].float().numpy() for l in layers], q_np)
+                    rows += blk.batch_size
+            dt = time.perf_counter() - t0
+            cores, model_name = cpu_info()
+            cpu = {"value": round(rows / dt, 1), "unit": "train-samples/s", "cores": blas_threads(), "kind": "port",
+                   "sample": f"the whole store ({rows} train rows, {dt:.2f} s): memmap groups read back, blocks "
+                             f"assembled, numpy oracle scores against the 128 queries; host {model_name}, "
+                             f"{cores} cores visible"}
     finally:
         shutil.rmtree(root, ignore_errors=True)
     n_train = files * per_file
@@ -1033,6 +1059,7 @@ def bench_store(args):
                      "launch_ms": round(t_score, 4), "launches_per_step": files // 8},
         "pipeline": {"h2d_bytes_per_step": h2d, "h2d_gbs": round(h2d / ms / 1e6, 1),
                      "resident_ms_per_step": round(ms_mem, 4)},
+        **({"cpu_baseline": cpu} if cpu else {}),
     }
 
 
