@@ -43,6 +43,8 @@ struct MatArgs {
   int64_t tiles_m, tiles_n;                  // per sample
   int sym;                                   // a == g (a row Gram): only tiles on or above the diagonal
   int acc;                                   // add to the fp32 output instead of overwriting it
+  int64_t rows_total;                        // sym with token splits: rows of all splits (sample b holds
+                                             // rows b*tokens .. ; the last one may be short), else 0
 };
 
 // Element offset (from the sample's base) of output (o, k): flat c = o*rstride + k
@@ -424,9 +426,11 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   const int64_t logical = xcd_remap(blockIdx.x, ntiles);
   int64_t b, tm, tn;
   if (m.sym) {
-    // One sample; the tiles with tm <= tn, row by row (tiles_m == tiles_n).
-    b = 0;
-    int64_t r = logical;
+    // Sample b (a token split of the rows), then its tiles with tm <= tn, row
+    // by row (tiles_m == tiles_n).
+    const int64_t ntri = m.tiles_n * (m.tiles_n + 1) / 2;
+    b = logical / ntri;
+    int64_t r = logical - b * ntri;
     tm = 0;
     while (r >= m.tiles_n - tm) {
       r -= m.tiles_n - tm;
@@ -453,11 +457,14 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
 
   // Buffer resources over the sample's token rows (the host guarantees
   // (tokens + kTS) * stride < 2^31, so no offset below wraps).
-  const u32x4 rg = make_rsrc(m.g + b * m.g_bstride, (uint32_t)(m.tokens * m.g_tstride));
-  const u32x4 ra = make_rsrc(m.a + b * m.a_bstride, (uint32_t)(m.tokens * m.a_tstride));
+  // A token split's resources end at the last real row: the rows past it
+  // (the short last split) read as zeros and touch no memory.
+  const int64_t tok_b = m.rows_total > 0 ? min(m.tokens, m.rows_total - b * m.tokens) : m.tokens;
+  const u32x4 rg = make_rsrc(m.g + b * m.g_bstride, (uint32_t)(tok_b * m.g_tstride));
+  const u32x4 ra = make_rsrc(m.a + b * m.a_bstride, (uint32_t)(tok_b * m.a_tstride));
   const uint32_t gts = (uint32_t)m.g_tstride, ats = (uint32_t)m.a_tstride;
 
-  const int nst = (int)((m.tokens + trk::kTS - 1) / trk::kTS);
+  const int nst = (int)((tok_b + trk::kTS - 1) / trk::kTS);
   // DMA: wave w fills token rows 8w .. 8w+7 of both operand tiles, two rows per
   // instruction; lane l takes row 8w + 2j + l/32 and slot l % 32.
   uint32_t goff[trk::kDma], aoff[trk::kDma];
@@ -633,24 +640,47 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   }
 }
 
+// Row Gram with token splits: out[i][j] (+)= sum over splits s (in order) of
+// ws[s][i][j], for the elements of the tiles on or above the diagonal (the
+// four columns of a thread share one 256-wide tile).
+__global__ __launch_bounds__(256) void sum_splits_upper(const float* __restrict__ ws, int splits, int64_t n,
+                                                        float* __restrict__ out, int64_t ld, int acc) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index over the n x n/4 square
+  const int64_t row = q / (n / 4), c4 = q - row * (n / 4);
+  if (row >= n) return;
+  const int64_t col = 4 * c4;
+  if (row / trk::kBM > col / trk::kBN) return;  // below the diagonal tiles: the mirror fills it
+  f32x4 v = *(const f32x4*)(ws + row * n + col);
+  for (int s = 1; s < splits; ++s) v += *(const f32x4*)(ws + (int64_t)s * n * n + row * n + col);
+  float* dst = out + row * ld + col;
+  if (acc) v += *(const f32x4*)dst;
+  *(f32x4*)dst = v;
+}
+
 // Row Gram: copy the tiles above the diagonal (computed) to the ones below it.
-// Block (I, J) of 32 x 32 outputs with tile(I) > tile(J) (256-output tiles)
-// reads the transposed block (J, I) through LDS; both accesses are row-major.
+// Block (I, J) of 64 x 64 outputs with tile(I) > tile(J) (256-output tiles,
+// so a block lies in one tile pair) reads the transposed block (J, I) through
+// LDS with 16-byte row accesses on both sides (n and ld are multiples of 4).
 __global__ __launch_bounds__(256) void mirror_lower(float* __restrict__ out, int64_t n, int64_t ld) {
-  __shared__ float t[32][33];
+  __shared__ float t[64][65];
   const int64_t bi = blockIdx.y, bj = blockIdx.x;  // output block row, block column
-  if ((bi * 32) / trk::kBM <= (bj * 32) / trk::kBN) return;  // uniform: on or above the diagonal tiles
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  if ((bi * 64) / trk::kBM <= (bj * 64) / trk::kBN) return;  // uniform: on or above the diagonal tiles
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int64_t r = bj * 32 + ty + 8 * k, c = bi * 32 + tx;  // source (upper) element
-    t[ty + 8 * k][tx] = (r < n && c < n) ? out[r * ld + c] : 0.f;
+    const int idx = tid + 256 * k, r = idx >> 4, c4 = idx & 15;
+    const int64_t sr = bj * 64 + r, sc = bi * 64 + 4 * c4;  // source (upper) row and first column
+    const f32x4 v = (sr < n && sc < n) ? *(const f32x4*)(out + sr * ld + sc) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[r][4 * c4 + e] = v[e];
   }
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int64_t r = bi * 32 + ty + 8 * k, c = bj * 32 + tx;  // destination (lower) element
-    if (r < n && c < n) out[r * ld + c] = t[tx][ty + 8 * k];
+    const int idx = tid + 256 * k, r = idx >> 4, c4 = idx & 15;
+    const int64_t dr = bi * 64 + r, dc = bj * 64 + 4 * c4;  // destination (lower) row and first column
+    if (dr < n && dc < n)
+      *(f32x4*)(out + dr * ld + dc) = f32x4{t[4 * c4][r], t[4 * c4 + 1][r], t[4 * c4 + 2][r], t[4 * c4 + 3][r]};
   }
 }
 
@@ -775,6 +805,7 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
   m.tiles_n = (K + kBN - 1) / kBN;
   m.sym = 0;
   m.acc = 0;
+  m.rows_total = 0;
   hipStream_t st = (hipStream_t)stream;
 #define DA_MAT_CASE(DT)                                                         \
   switch (out_dtype) {                                                          \
@@ -790,12 +821,88 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
 #undef DA_MAT_CASE
 }
 
+namespace da {
+namespace {
+
+// CUs of the current device (cached per device).
+int device_cus(int64_t* n) {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "hipGetDevice failed");
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+    *n = cache[dev];
+    return DA_OK;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
+  if (dev >= 0 && dev < 64) cache[dev] = cus;
+  *n = cus;
+  return DA_OK;
+}
+
+struct GramPlan {
+  int splits;      // token splits (1: straight into out)
+  int64_t chunk;   // rows per split
+  size_t ws;       // workspace bytes for the splits' partial squares
+};
+
+// Token splits of a row Gram: a triangle with few tiles (width 4096: 136,
+// width 1024: 10) leaves most CUs idle while each tile runs over every row, so
+// the rows are cut into splits that run side by side and a second pass sums
+// their partial squares.  Time model in rows of one tile's work: a round of
+// tiles over `chunk` rows costs `chunk`; the partials' HBM traffic, (S + 1)
+// upper halves of fp32 at ~5 TB/s against a tile's ~29 ns per row on one CU,
+// costs (S + 1) * width^2 * 1.4e-5.
+GramPlan gram_plan(int64_t rows, int64_t width, int64_t sb, int64_t slots, size_t ws_limit) {
+  GramPlan g{1, rows, 0};
+  const int64_t t = (width + trk::kBM - 1) / trk::kBM, nt = t * (t + 1) / 2;
+  const int64_t lim32 = ((1LL << 31) - (1LL << 20)) / sb - trk::kTS;  // rows one buffer resource can span
+  const double per_split = 1.4e-5 * (double)width * (double)width;
+  double best = (double)((nt + slots - 1) / slots) * (double)rows;
+  const size_t sq = (size_t)width * (size_t)width * sizeof(float);
+  for (int s = 2; s <= 64; ++s) {
+    int64_t chunk = (rows + s - 1) / s;
+    chunk = (chunk + trk::kTS - 1) / trk::kTS * trk::kTS;
+    if (chunk < 8 * trk::kTS || chunk > lim32) continue;
+    const int64_t sp = (rows + chunk - 1) / chunk;
+    if ((size_t)sp * sq > ws_limit || nt * sp > 0x7fffffffLL) continue;
+    const double cost = (double)((nt * sp + slots - 1) / slots) * (double)chunk + (double)(sp + 1) * per_split;
+    if (cost < 0.95 * best) {
+      best = cost;
+      g = GramPlan{(int)sp, chunk, (size_t)sp * sq};
+    }
+  }
+  return g;
+}
+
+}  // namespace
+}  // namespace da
+
 // Row Gram out (+)= x^T x of x (rows, width), fp32 out: the transposing-read
-// dW kernel with every row as one token of one sample and both operands x,
-// over the tiles on or above the diagonal, then the mirror.  Rows are taken in
+// dW kernel with every row as one token and both operands x, over the tiles on
+// or above the diagonal, then the mirror.  With token splits (a workspace
+// holding them), each split's partial square goes to the workspace and
+// sum_splits_upper adds them in split order; otherwise rows are taken in
 // chunks whose buffer offsets fit 32 bits, each adding to the output.
+extern "C" int da_row_gram_workspace(int64_t rows, int64_t width, int dtype, size_t* bytes) {
+  using namespace da;
+  if (!bytes) return set_error(DA_ERR_INVALID, "da_row_gram_workspace: bytes is NULL");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_row_gram_workspace: bf16 or fp16 rows only");
+  if (rows < 0 || width < 0) return set_error(DA_ERR_INVALID, "da_row_gram_workspace: negative size");
+  *bytes = 0;
+  if (rows == 0 || width == 0) return DA_OK;
+  int64_t slots = 0;
+  const int rc = device_cus(&slots);
+  if (rc) return rc;
+  *bytes = gram_plan(rows, width, width * 2, slots, (size_t)1 << 33).ws;
+  return DA_OK;
+}
+
 extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width, int64_t x_stride, float* out,
-                           int64_t ld_out, int accumulate, void* stream) {
+                           int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes,
+                           void* stream) {
   using namespace da;
   if (dtype != DA_BF16 && dtype != DA_F16)
     return set_error(DA_ERR_UNSUPPORTED, "da_row_gram: bf16 or fp16 rows only");
@@ -809,11 +916,17 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
                      "rows 16-byte aligned");
   if (ld_out < width || (ld_out * 4) % 16 || ((uintptr_t)out & 15))
     return set_error(DA_ERR_INVALID, "da_row_gram: out row stride must be >= width and a multiple of 4");
+  if (workspace && ((uintptr_t)workspace & 15))
+    return set_error(DA_ERR_INVALID, "da_row_gram: workspace must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (rows == 0) return accumulate ? DA_OK : zero_f32_2d(out, width, width, ld_out, st);
   const int64_t sb = x_stride * es;
-  const int64_t chunk = ((1LL << 31) - (1LL << 20)) / sb - trk::kTS;
-  if (chunk < trk::kTS) return set_error(DA_ERR_INVALID, "da_row_gram: rows too wide for 32-bit offsets");
+  const int64_t chunk32 = ((1LL << 31) - (1LL << 20)) / sb - trk::kTS;
+  if (chunk32 < trk::kTS) return set_error(DA_ERR_INVALID, "da_row_gram: rows too wide for 32-bit offsets");
+  int64_t slots = 0;
+  int rc = device_cus(&slots);
+  if (rc) return rc;
+  const GramPlan g = gram_plan(rows, width, sb, slots, workspace ? workspace_bytes : 0);
   MatArgs m;
   m.batch = 1;
   m.k = width;
@@ -829,20 +942,46 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
   m.tiles_m = (width + trk::kBM - 1) / trk::kBM;
   m.tiles_n = (width + trk::kBN - 1) / trk::kBN;
   m.sym = 1;
+  m.rows_total = 0;
   const int64_t nt = m.tiles_m * (m.tiles_m + 1) / 2;
-  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
-    m.a = (const char*)x + r0 * sb;
-    m.g = m.a;
-    m.tokens = rows - r0 < chunk ? rows - r0 : chunk;
-    m.acc = accumulate || r0 > 0;
+  auto launch_tiles = [&](int64_t blocks) {
     if (dtype == DA_BF16)
-      materialize_tiles_tr<DA_BF16, DA_F32><<<(unsigned)nt, kThreads, 0, st>>>(m);
+      materialize_tiles_tr<DA_BF16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(m);
     else
-      materialize_tiles_tr<DA_F16, DA_F32><<<(unsigned)nt, kThreads, 0, st>>>(m);
-    const int rc = check_launch("da_row_gram");
+      materialize_tiles_tr<DA_F16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(m);
+    return check_launch("da_row_gram");
+  };
+  if (g.splits > 1) {
+    // split b = rows b*chunk .. of x into its own square of the workspace
+    m.a = (const char*)x;
+    m.g = m.a;
+    m.batch = g.splits;
+    m.tokens = g.chunk;
+    m.rows_total = rows;
+    m.a_bstride = g.chunk * sb;
+    m.g_bstride = m.a_bstride;
+    m.out = (char*)workspace;
+    m.out_bstride = width * width;
+    m.out_rstride = width;
+    m.acc = 0;
+    rc = launch_tiles(nt * g.splits);
     if (rc) return rc;
+    const int64_t quads = width * (width / 4);
+    sum_splits_upper<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>((const float*)workspace, g.splits, width,
+                                                                     out, ld_out, accumulate ? 1 : 0);
+    rc = check_launch("da_row_gram(sum)");
+    if (rc) return rc;
+  } else {
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk32) {
+      m.a = (const char*)x + r0 * sb;
+      m.g = m.a;
+      m.tokens = rows - r0 < chunk32 ? rows - r0 : chunk32;
+      m.acc = accumulate || r0 > 0;
+      rc = launch_tiles(nt);
+      if (rc) return rc;
+    }
   }
-  const int64_t nb = (width + 31) / 32;
+  const int64_t nb = (width + 63) / 64;
   if (m.tiles_m > 1) {
     mirror_lower<<<dim3((unsigned)nb, (unsigned)nb), 256, 0, st>>>(out, width, ld_out);
     return check_launch("da_row_gram(mirror)");

@@ -371,8 +371,10 @@ def materialize_linear(
 
 def row_gram(x: torch.Tensor, *, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
     """fp32 ``x^T x`` of bf16/fp16 rows ``x (N, p)`` -> ``(p, p)``; with
-    ``accumulate`` it is added to ``out``.  The product is computed once per
-    tile pair on or above the diagonal and mirrored."""
+    ``accumulate`` it is added to ``out``, which must be symmetric (its lower
+    tiles are rewritten as the mirror of the upper ones).  The product is
+    computed once per tile pair on or above the diagonal and mirrored; a small
+    triangle of tiles runs as token splits summed by a second pass."""
     dev = nat.require_device(x, out)
     if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("row_gram expects bf16/fp16 rows (N, p)")
@@ -396,9 +398,14 @@ def row_gram(x: torch.Tensor, *, out: torch.Tensor | None = None, accumulate: bo
         return out
     if xp.stride(1) != 1:
         xp = xp.contiguous()
+    lib = nat.load()
+    need = ctypes.c_size_t(0)
+    nat.check(lib.da_row_gram_workspace(n, p, nat.dtype_code(xp.dtype), ctypes.byref(need)), "row_gram")
+    ws = torch.empty(need.value, dtype=torch.uint8, device=dev) if need.value else None
     nat.check(
-        nat.load().da_row_gram(xp.data_ptr(), nat.dtype_code(xp.dtype), n, p, xp.stride(0), out.data_ptr(),
-                               out.stride(0), int(accumulate), nat.stream_ptr(dev)),
+        lib.da_row_gram(xp.data_ptr(), nat.dtype_code(xp.dtype), n, p, xp.stride(0), out.data_ptr(),
+                        out.stride(0), int(accumulate), ws.data_ptr() if ws is not None else None,
+                        need.value, nat.stream_ptr(dev)),
         "row_gram",
     )
     return out

@@ -148,8 +148,8 @@ int da_dense_per_token(const da_factor_side* s1, const void* m2, int64_t b2, int
  * (>= seg_offsets[B]), row_index optionally gathers physical rows,
  * act/grad_tstride are row strides, has_bias (equal on both sides) adds the
  * implicit ones column.  K[e], D[e] are the group's activation and gradient
- * widths, so the experts of several layers can share one launch (put the
- * widest first: groups are scheduled in order).  All groups share the batch
+ * widths, so the experts of several layers can share one launch (the launch
+ * orders the groups by decreasing K + D itself).  All groups share the batch
  * sizes (B1, B2) and dtype.  Tiles run over each expert's rows as packed (no
  * per-sample padding); each tile's products are binned by (sample, sample) and
  * reduced in a fixed order (deterministic).  Empty experts and samples are
@@ -192,7 +192,8 @@ int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch
  * Row Gram: out (+)= x^T x, fp32 (width, width) with row stride ld_out, of the
  * bf16/fp16 rows x (rows, width) with row stride x_stride (elements; width and
  * x_stride multiples of 8, rows 16-byte aligned).  accumulate = 0 overwrites,
- * 1 adds; rows = 0 (x may then be NULL) zeroes or leaves out.  The symmetric product is computed once per pair of tiles (the ones
+ * 1 adds to a symmetric out (the tiles below the diagonal are rewritten as the
+ * mirror of those above it); rows = 0 (x may then be NULL) zeroes or leaves out.  The symmetric product is computed once per pair of tiles (the ones
  * on or above the diagonal) and mirrored.  Returns DA_ERR_UNSUPPORTED for
  * other dtypes.  Replaces the covariance products of the K-FAC factors and the
  * empirical Fisher, dattri_llm/gradient/ops/kronecker.py:111-112
@@ -200,7 +201,17 @@ int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch
  * :512-513 and :594.
  */
 int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width, int64_t x_stride, float* out,
-                int64_t ld_out, int accumulate, void* stream);
+                int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes da_row_gram can use on the current device for (rows, width)
+ * packed rows (x_stride == width): token splits that let a small triangle of
+ * tiles fill the GPU (a fp32 width x width partial per split).  0 when one
+ * pass is best.  A smaller or NULL workspace is accepted: the call then uses
+ * the splits that fit (down to none).  Calls sharing a workspace must be
+ * ordered on one stream.  No reference counterpart (workspace sizing).
+ */
+int da_row_gram_workspace(int64_t rows, int64_t width, int dtype, size_t* bytes);
 
 /*
  * One dense layer of a score GEMM: m1 is (B1, width), m2 is (B2, width).

@@ -229,17 +229,92 @@ def test_row_gram_accumulate_and_out_stride(device):
         kernels.row_gram(x1.to(device), accumulate=True)
 
 
-def test_row_gram_row_chunks(device):
-    """Rows 4 MiB apart: the entry point splits them into chunks whose buffer
-    offsets stay below 2^31 bytes (479 + 479 + 42 rows), each adding to the
-    output."""
-    from dattri_llm_amd import kernels
+def _row_gram_raw(x, ws, out=None, accumulate=False):
+    """da_row_gram through the C ABI with an explicit workspace (None: none)."""
+    from dattri_llm_amd import _native as nat
 
+    p = x.shape[1]
+    out = torch.empty(p, p, dtype=torch.float32, device=x.device) if out is None else out
+    nat.check(nat.load().da_row_gram(x.data_ptr(), nat.DA_BF16, x.shape[0], p, x.stride(0), out.data_ptr(),
+                                     out.stride(0), int(accumulate), None if ws is None else ws.data_ptr(),
+                                     0 if ws is None else ws.numel(), torch.cuda.current_stream().cuda_stream),
+              "row_gram")
+    return out
+
+
+def _row_gram_ws(n, p):
+    import ctypes
+
+    from dattri_llm_amd import _native as nat
+
+    need = ctypes.c_size_t(0)
+    nat.check(nat.load().da_row_gram_workspace(n, p, nat.DA_BF16, ctypes.byref(need)), "row_gram_workspace")
+    return need.value
+
+
+def test_row_gram_row_chunks(device):
+    """Rows 4 MiB apart.  Without a workspace the entry point takes the rows in
+    chunks whose buffer offsets stay below 2^31 bytes (479 + 479 + 42 rows),
+    each adding to the output; with one, in token splits of at most 479 rows
+    summed by the second pass.  Both equal the float64 product."""
     n, p, stride = 1000, 264, 1 << 21
     x = _rows(7, n, p, torch.bfloat16)
     big = torch.zeros(n, stride, dtype=torch.bfloat16, device=device)
     big[:, :p] = x.to(device)
-    got = kernels.row_gram(big[:, :p])
     want = x.double().T @ x.double()
-    assert rel_err(got.double().cpu(), want) <= 1e-4
+    chunked = _row_gram_raw(big[:, :p], None)
+    need = _row_gram_ws(n, p)
+    assert need > 0  # a 2 x 2 triangle of tiles: splits pay
+    split = _row_gram_raw(big[:, :p], torch.empty(need, dtype=torch.uint8, device=device))
+    torch.cuda.synchronize()
+    assert rel_err(chunked.double().cpu(), want) <= 1e-4
+    assert rel_err(split.double().cpu(), want) <= 1e-4
     del big
+
+
+@pytest.mark.parametrize("n,p", [(16384, 1024), (16384, 4096), (3000, 520), (700, 8)])
+def test_row_gram_token_splits(device, n, p):
+    """Token splits (workspace) against one pass (no workspace): the same
+    product to fp32 rounding, with and without accumulation, twice in a row on
+    one workspace (each call rewrites every partial it reads), and a workspace
+    too small for the planned splits falls back to fewer."""
+    x = _rows(11 + p, n, p, torch.bfloat16).to(device)
+    need = _row_gram_ws(n, p)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+    one = _row_gram_raw(x, None)
+    split = _row_gram_raw(x, ws)
+    again = _row_gram_raw(x, ws)
+    base = torch.randn(p, p, device=device)
+    base = base + base.T  # an accumulator of Grams is symmetric (the lower tiles are rewritten by the mirror)
+    acc = _row_gram_raw(x, ws, out=base.clone(), accumulate=True)
+    small = _row_gram_raw(x, ws[: need // 2] if need > 1 else None)
+    torch.cuda.synchronize()
+    assert torch.equal(split, again)
+    for got in (split, small):
+        assert rel_err(got.double().cpu(), one.double().cpu()) <= 1e-5
+    assert rel_err(acc.double().cpu(), (one + base).double().cpu()) <= 1e-5
+    assert _off_diagonal_tiles_mirrored(split.cpu())
+
+
+def test_gradient_free_rows_match_the_reference_rule(device):
+    """Token rows are dropped exactly when every gradient entry compares equal
+    to zero (kronecker.py:65-81: (g != 0).any(1)); -0.0 rows go, rows holding
+    only a NaN, an inf or a subnormal stay."""
+    from dattri_llm_amd.gradient.ops import kronecker
+
+    g = torch.randn(9, 40).bfloat16()
+    g[1] = 0
+    g[2] = -0.0
+    g[3] = 0
+    g[3, 5] = float("nan")
+    g[4] = 0
+    g[4, 0] = -1e-38  # subnormal in bf16
+    g[5] = 0
+    g[5, 7] = float("inf")
+    g[6] = 0
+    a = torch.randn(9, 24).bfloat16()
+    want = (g != 0).any(dim=1)
+    a_f, g_f = kronecker._drop_gradient_free_rows(a.to(device), g.to(device))
+    assert torch.equal(a_f.cpu(), a[want])  # the activation rows kept are exactly the reference's
+    got, ref = g_f.cpu(), g[want]  # (NaN != NaN, so compare with the NaNs replaced)
+    assert torch.equal(torch.isnan(got), torch.isnan(ref)) and torch.equal(got.nan_to_num(7.0), ref.nan_to_num(7.0))

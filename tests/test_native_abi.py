@@ -62,17 +62,17 @@ def test_argument_checks_fail_before_any_gpu_work():
         msg = lib.da_last_error().decode()
         assert all(w in msg for w in words), msg
 
-    # da_row_gram(x, dtype, rows, width, x_stride, out, ld_out, accumulate, stream)
-    check(lib.da_row_gram(X, f32, 10, 8, 8, OUT, 8, 0, None), _native.DA_ERR_UNSUPPORTED, ["bf16 or fp16"])
-    check(lib.da_row_gram(X, bf, -1, 8, 8, OUT, 8, 0, None), _native.DA_ERR_INVALID, ["negative"])
-    check(lib.da_row_gram(None, bf, 10, 8, 8, OUT, 8, 0, None), _native.DA_ERR_INVALID, ["NULL"])
-    check(lib.da_row_gram(X, bf, 10, 8, 8, None, 8, 0, None), _native.DA_ERR_INVALID, ["NULL"])
-    check(lib.da_row_gram(X, bf, 10, 12, 12, OUT, 12, 0, None), _native.DA_ERR_INVALID, ["multiples of 8"])
-    check(lib.da_row_gram(X + 8, bf, 10, 8, 8, OUT, 8, 0, None), _native.DA_ERR_INVALID, ["aligned"])
-    check(lib.da_row_gram(X, bf, 10, 8, 8, OUT, 6, 0, None), _native.DA_ERR_INVALID, ["out row stride"])
+    # da_row_gram(x, dtype, rows, width, x_stride, out, ld_out, accumulate, workspace, workspace_bytes, stream)
+    check(lib.da_row_gram(X, f32, 10, 8, 8, OUT, 8, 0, None, 0, None), _native.DA_ERR_UNSUPPORTED, ["bf16 or fp16"])
+    check(lib.da_row_gram(X, bf, -1, 8, 8, OUT, 8, 0, None, 0, None), _native.DA_ERR_INVALID, ["negative"])
+    check(lib.da_row_gram(None, bf, 10, 8, 8, OUT, 8, 0, None, 0, None), _native.DA_ERR_INVALID, ["NULL"])
+    check(lib.da_row_gram(X, bf, 10, 8, 8, None, 8, 0, None, 0, None), _native.DA_ERR_INVALID, ["NULL"])
+    check(lib.da_row_gram(X, bf, 10, 12, 12, OUT, 12, 0, None, 0, None), _native.DA_ERR_INVALID, ["multiples of 8"])
+    check(lib.da_row_gram(X + 8, bf, 10, 8, 8, OUT, 8, 0, None, 0, None), _native.DA_ERR_INVALID, ["aligned"])
+    check(lib.da_row_gram(X, bf, 10, 8, 8, OUT, 6, 0, None, 0, None), _native.DA_ERR_INVALID, ["out row stride"])
     # nothing to do: no launch, success (no rows with accumulate, or no width)
-    assert lib.da_row_gram(None, bf, 0, 8, 8, OUT, 8, 1, None) == _native.DA_OK
-    assert lib.da_row_gram(X, bf, 10, 0, 8, OUT, 8, 0, None) == _native.DA_OK
+    assert lib.da_row_gram(None, bf, 0, 8, 8, OUT, 8, 1, None, 0, None) == _native.DA_OK
+    assert lib.da_row_gram(X, bf, 10, 0, 8, OUT, 8, 0, None, 0, None) == _native.DA_OK
 
     # da_materialize_linear(a, g, dtype, batch, tokens, K, D, a_bs, a_ts, g_bs, g_ts, bias,
     #                       out, out_dtype, out_bs, out_rs, out_blk, stream)
