@@ -129,6 +129,9 @@ TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "llama8b_block_hbm_traffic.md")
 GHOST_TRAFFIC = os.path.join(REPO, "profiles", "ghost_c2_hbm_traffic.md")
 PROJECT_TRAFFIC = os.path.join(REPO, "profiles", "project_llama7b_mlp_hbm_traffic.md")
 MOE_TRAFFIC = os.path.join(REPO, "profiles", "moe_mixtral_layer_hbm_traffic.md")
+KFAC_TRAFFIC = os.path.join(REPO, "profiles", "kfac_llama8b_block_hbm_traffic.md")
+CAPTURE_TRAFFIC = os.path.join(REPO, "profiles", "capture_llama7b_mlp_hbm_traffic.md")
+STORE_TRAFFIC = os.path.join(REPO, "profiles", "store_attribute_hbm_traffic.md")
 
 
 def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
@@ -873,7 +876,9 @@ def bench_capture(args):
                                "128 samples x 128 tokens, FusedCapture proj_dim 64 materialized"},
         "roofline": {"bound": "hbm", "kernel": "da_project_outer (the capture launch of each layer's backward)",
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("da_project_outer", CAPTURE_TRAFFIC),
+                     "traffic_source": os.path.relpath(CAPTURE_TRAFFIC, REPO),
                      "work_per_launch": f"{cap_bytes:.4g} B average = B x T x (d_in + d_out) x 2 B per layer",
                      "launches_per_step": 3},
         "kernels": {"fused_step_ms": round(ms, 4), "plain_backward_step_ms": round(ms_plain, 4),
@@ -1054,7 +1059,9 @@ def bench_store(args):
                                "(64x64 LoGRA blocks) bf16, 64 files of 512; store in the page cache"},
         "roofline": {"bound": "hbm", "kernel": "da_score_gemm (score_ring + reduce), one 4096-row train batch",
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": profiled_traffic("score_ring", STORE_TRAFFIC),
+                     "traffic_source": os.path.relpath(STORE_TRAFFIC, REPO),
                      "work_per_launch": f"{launch_bytes:.4g} B = (4096 + 128) x 3 x 4096 x 2 B",
                      "launch_ms": round(t_score, 4), "launches_per_step": files // 8},
         "pipeline": {"h2d_bytes_per_step": h2d, "h2d_gbs": round(h2d / ms / 1e6, 1),
@@ -1124,7 +1131,9 @@ def bench_kfac(args):
         "roofline": {"bound": "mfma",
                      "kernel": "materialize_tiles_tr (symmetric row Gram of 16384 rows) + mirror_lower",
                      "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "traffic": profiled_traffic("materialize_tiles_tr", KFAC_TRAFFIC),
+                     "traffic_source": os.path.relpath(KFAC_TRAFFIC, REPO),
                      "work_per_step": f"{flops:.4g} flop = sum over the 7 linears of 16384 x (d_in (d_in + 1) "
                                       "+ d_out (d_out + 1)), the distinct entries of A and G",
                      "step_share": round(t_k / ms, 3)},

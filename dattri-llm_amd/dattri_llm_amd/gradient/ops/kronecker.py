@@ -71,9 +71,7 @@ def _right_multiply(x: torch.Tensor, matrix: torch.Tensor) -> torch.Tensor:
 
 def _drop_gradient_free_rows(a_f: torch.Tensor, g_f: torch.Tensor):
     """kronecker.py:65-81: drop token rows whose output gradient is exactly zero."""
-    # a row's largest magnitude is 0 exactly when every entry compares equal to
-    # 0 (-0.0 included; a NaN row stays), in one reduction pass over g
-    keep = torch.linalg.vector_norm(g_f, ord=float("inf"), dim=1) != 0
+    keep = (g_f != 0).any(dim=1)
     if bool(keep.all()):
         return a_f, g_f
     return a_f[keep], g_f[keep]
