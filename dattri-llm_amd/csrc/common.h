@@ -245,6 +245,9 @@ int check_launch(const char* what);
 // Zero a (rows x cols) fp32 matrix with leading dimension ld using a kernel
 // (never a memset node, so callers may capture it in a HIP graph).
 int zero_f32_2d(float* out, int64_t rows, int64_t cols, int64_t ld, hipStream_t stream);
+// CUs of the current device (the workgroup slots of the stream-K and split
+// launches), cached per device.
+int device_cu_count(int64_t* n);
 inline size_t elem_bytes(int dt) { return dt == DA_F32 ? 4 : 2; }
 inline bool valid_dtype(int dt) { return dt == DA_F32 || dt == DA_BF16 || dt == DA_F16; }
 }  // namespace da

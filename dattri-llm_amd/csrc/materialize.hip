@@ -824,23 +824,6 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
 namespace da {
 namespace {
 
-// CUs of the current device (cached per device).
-int device_cus(int64_t* n) {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "hipGetDevice failed");
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
-    *n = cache[dev];
-    return DA_OK;
-  }
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
-  if (dev >= 0 && dev < 64) cache[dev] = cus;
-  *n = cus;
-  return DA_OK;
-}
-
 struct GramPlan {
   int splits;      // token splits (1: straight into out)
   int64_t chunk;   // rows per split
@@ -894,7 +877,7 @@ extern "C" int da_row_gram_workspace(int64_t rows, int64_t width, int dtype, siz
   *bytes = 0;
   if (rows == 0 || width == 0) return DA_OK;
   int64_t slots = 0;
-  const int rc = device_cus(&slots);
+  const int rc = device_cu_count(&slots);
   if (rc) return rc;
   *bytes = gram_plan(rows, width, width * 2, slots, (size_t)1 << 33).ws;
   return DA_OK;
@@ -924,7 +907,7 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
   const int64_t chunk32 = ((1LL << 31) - (1LL << 20)) / sb - trk::kTS;
   if (chunk32 < trk::kTS) return set_error(DA_ERR_INVALID, "da_row_gram: rows too wide for 32-bit offsets");
   int64_t slots = 0;
-  int rc = device_cus(&slots);
+  int rc = device_cu_count(&slots);
   if (rc) return rc;
   const GramPlan g = gram_plan(rows, width, sb, slots, workspace ? workspace_bytes : 0);
   MatArgs m;

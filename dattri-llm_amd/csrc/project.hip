@@ -693,23 +693,6 @@ __global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int k
   }
 }
 
-// Workgroup slots of the stream-K launch on the current device: one per CU.
-int sk_slots(int64_t* n) {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "hipGetDevice failed");
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
-    *n = cache[dev];
-    return DA_OK;
-  }
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
-  if (dev >= 0 && dev < 64) cache[dev] = cus;
-  *n = cus;
-  return DA_OK;
-}
-
 // The streaming kernel addresses a sample's rows and the projection rows with
 // 32-bit buffer offsets.
 bool stream_fits(int64_t tokens, int64_t tstride_b, int64_t wbytes, int64_t pt_rstride_b) {
@@ -834,7 +817,7 @@ int da_project_outer_workspace(int64_t batch, int64_t tokens, int64_t ka, int64_
   const size_t partials = (size_t)(batch * chunks * ka * kg) * sizeof(float);
   // the stream-K path keeps one fp32 piece per (item, workgroup) boundary
   int64_t slots = 0;
-  const int rc = da::sk_slots(&slots);
+  const int rc = da::device_cu_count(&slots);
   if (rc) return rc;
   const int64_t items = 2 * batch * ((tokens + da::ps::kTok - 1) / da::ps::kTok);
   const size_t pieces = (size_t)(items + slots) * da::kPieceFloats * sizeof(float);
@@ -925,7 +908,7 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
     }
     sk.total = s0;
     int64_t slots = 0;
-    rc = sk_slots(&slots);
+    rc = device_cu_count(&slots);
     if (rc) return rc;
     sk.nwg = slots < sk.total ? slots : sk.total;
     if (sk.total / sk.nwg > (1LL << 30) || batch > (1LL << 28))

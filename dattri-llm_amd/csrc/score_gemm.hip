@@ -343,23 +343,6 @@ struct Plan {
   int64_t units, nwg;     // its units and workgroups per tile
 };
 
-// Workgroup slots on the current device: one per CU.
-int ring_slots(int64_t* n) {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "hipGetDevice failed");
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
-    *n = cache[dev];
-    return DA_OK;
-  }
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return set_error(DA_ERR_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
-  if (dev >= 0 && dev < 64) cache[dev] = cus;
-  *n = cus;
-  return DA_OK;
-}
-
 int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
               Plan* p) {
   if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "da_score_gemm: bad dtype %d", dtype);
@@ -406,7 +389,7 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
   }
   if (p->ring && units > 0) {
     int64_t slots = 0;
-    const int rc = ring_slots(&slots);
+    const int rc = device_cu_count(&slots);
     if (rc) return rc;
     const int64_t tiles = ((b1 + kTileM - 1) / kTileM) * ((b2 + kTileN - 1) / kTileN);
     int64_t nwg = slots / tiles;
