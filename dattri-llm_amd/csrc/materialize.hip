@@ -45,6 +45,8 @@ struct MatArgs {
   int acc;                                   // add to the fp32 output instead of overwriting it
   int64_t rows_total;                        // sym with token splits: rows of all splits (sample b holds
                                              // rows b*tokens .. ; the last one may be short), else 0
+  int64_t tile0, sym_count;                  // sym: triangle tiles tile0 .. tile0 + sym_count - 1 (row by row)
+  int compact;                               // sym: tile t of split b lands at out + (b*sym_count + t) * 256^2
 };
 
 // Element offset (from the sample's base) of output (o, k): flat c = o*rstride + k
@@ -425,12 +427,13 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   const int64_t ntiles = (int64_t)gridDim.x;
   const int64_t logical = xcd_remap(blockIdx.x, ntiles);
   int64_t b, tm, tn;
+  int64_t sym_local = 0;
   if (m.sym) {
-    // Sample b (a token split of the rows), then its tiles with tm <= tn, row
-    // by row (tiles_m == tiles_n).
-    const int64_t ntri = m.tiles_n * (m.tiles_n + 1) / 2;
-    b = logical / ntri;
-    int64_t r = logical - b * ntri;
+    // Sample b (a token split of the rows), then its tiles tile0 + .. of the
+    // triangle tm <= tn, numbered row by row (tiles_m == tiles_n).
+    b = logical / m.sym_count;
+    sym_local = logical - b * m.sym_count;
+    int64_t r = m.tile0 + sym_local;
     tm = 0;
     while (r >= m.tiles_n - tm) {
       r -= m.tiles_n - tm;
@@ -627,7 +630,9 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
       const int64_t ocol = ocol0 + (int64_t)ch * (16 / OS);
       u32x4 val = ld16(wbuf + row * LROW + ch * 16);
       if (orow < m.d && ocol < m.k) {
-        char* dst = obase + out_index(m, orow, ocol) * OS;
+        char* dst = m.compact ? m.out + ((b * m.sym_count + sym_local) * (int64_t)(trk::kBM * trk::kBN) +
+                                         (orow - o0) * trk::kBN + (ocol - k0)) * OS
+                              : obase + out_index(m, orow, ocol) * OS;
         if constexpr (OT == DA_F32) {
           if (m.acc) {
             const f32x4 old = __builtin_bit_cast(f32x4, ld16(dst));
@@ -640,19 +645,28 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
   }
 }
 
-// Row Gram with token splits: out[i][j] (+)= sum over splits s (in order) of
-// ws[s][i][j], for the elements of the tiles on or above the diagonal (the
-// four columns of a thread share one 256-wide tile).
-__global__ __launch_bounds__(256) void sum_splits_upper(const float* __restrict__ ws, int splits, int64_t n,
-                                                        float* __restrict__ out, int64_t ld, int acc) {
-  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index over the n x n/4 square
-  const int64_t row = q / (n / 4), c4 = q - row * (n / 4);
-  if (row >= n) return;
-  const int64_t col = 4 * c4;
-  if (row / trk::kBM > col / trk::kBN) return;  // below the diagonal tiles: the mirror fills it
-  f32x4 v = *(const f32x4*)(ws + row * n + col);
-  for (int s = 1; s < splits; ++s) v += *(const f32x4*)(ws + (int64_t)s * n * n + row * n + col);
-  float* dst = out + row * ld + col;
+// Row Gram with token splits: for the triangle tiles tile0 .. tile0 + count - 1
+// (row by row over T tiles per side), out (+)= the sum over splits s, in order,
+// of the compact partial tiles ws[s][t] (256 x 256 fp32 each).  Block (t, y):
+// rows 4y .. 4y + 3 of tile t, one float4 per thread.
+__global__ __launch_bounds__(256) void sum_split_tiles(const float* __restrict__ ws, int splits, int64_t count,
+                                                       int64_t tile0, int64_t T, int64_t n, float* __restrict__ out,
+                                                       int64_t ld, int acc) {
+  const int64_t t = blockIdx.x;
+  int64_t r = tile0 + t, tm = 0;
+  while (r >= T - tm) {
+    r -= T - tm;
+    ++tm;
+  }
+  const int64_t tn = tm + r;
+  const int row = (int)blockIdx.y * 4 + (int)(threadIdx.x >> 6), c4 = (int)(threadIdx.x & 63);
+  const int64_t i = tm * trk::kBM + row, jc = tn * trk::kBN + 4 * c4;
+  if (i >= n || jc >= n) return;  // n is a multiple of 8: the float4 lies inside
+  const int64_t tile = (int64_t)trk::kBM * trk::kBN;
+  const float* src = ws + t * tile + (int64_t)row * trk::kBN + 4 * c4;
+  f32x4 v = *(const f32x4*)src;
+  for (int s = 1; s < splits; ++s) v += *(const f32x4*)(src + (int64_t)s * count * tile);
+  float* dst = out + i * ld + jc;
   if (acc) v += *(const f32x4*)dst;
   *(f32x4*)dst = v;
 }
@@ -806,6 +820,9 @@ extern "C" int da_materialize_linear(const void* a, const void* g, int dtype, in
   m.sym = 0;
   m.acc = 0;
   m.rows_total = 0;
+  m.tile0 = 0;
+  m.sym_count = 0;
+  m.compact = 0;
   hipStream_t st = (hipStream_t)stream;
 #define DA_MAT_CASE(DT)                                                         \
   switch (out_dtype) {                                                          \
@@ -825,35 +842,42 @@ namespace da {
 namespace {
 
 struct GramPlan {
-  int splits;      // token splits (1: straight into out)
+  int64_t head;    // triangle tiles 0 .. head - 1 run over all rows, straight into out
+  int splits;      // token splits of the remaining tiles (1: no split launch)
   int64_t chunk;   // rows per split
-  size_t ws;       // workspace bytes for the splits' partial squares
+  size_t ws;       // workspace bytes: splits x (tiles - head) compact 256 x 256 fp32 partials
 };
 
-// Token splits of a row Gram: a triangle with few tiles (width 4096: 136,
-// width 1024: 10) leaves most CUs idle while each tile runs over every row, so
-// the rows are cut into splits that run side by side and a second pass sums
-// their partial squares.  Time model in rows of one tile's work: a round of
-// tiles over `chunk` rows costs `chunk`; the partials' HBM traffic, (S + 1)
-// upper halves of fp32 at ~5 TB/s against a tile's ~29 ns per row on one CU,
-// costs (S + 1) * width^2 * 1.4e-5.
+// Token splits of a row Gram.  Every tile runs over all the rows, so a triangle
+// whose tile count is not a multiple of the CU count ends in a partly filled
+// round (width 4096: 136 tiles in one round; width 14336: 1596 tiles, the
+// seventh round a quarter full).  The tiles of the whole rounds (head) run as
+// they are; the rest are cut into token splits that run side by side, and a
+// second pass sums their partial tiles.  Time model in rows of one tile's
+// work: a round over `chunk` rows costs `chunk`; the partials' HBM traffic,
+// (S + 1) tiles of 256^2 fp32 per split tile at ~5 TB/s against a tile's ~29 ns
+// per row on one CU, costs (S + 1) * tiles * 1.8.
 GramPlan gram_plan(int64_t rows, int64_t width, int64_t sb, int64_t slots, size_t ws_limit) {
-  GramPlan g{1, rows, 0};
   const int64_t t = (width + trk::kBM - 1) / trk::kBM, nt = t * (t + 1) / 2;
+  GramPlan g{nt, 1, rows, 0};
+  const int64_t head = nt > slots ? nt / slots * slots : 0, tail = nt - head;
+  if (tail == 0) return g;
   const int64_t lim32 = ((1LL << 31) - (1LL << 20)) / sb - trk::kTS;  // rows one buffer resource can span
-  const double per_split = 1.4e-5 * (double)width * (double)width;
-  double best = (double)((nt + slots - 1) / slots) * (double)rows;
-  const size_t sq = (size_t)width * (size_t)width * sizeof(float);
+  const size_t tile_bytes = (size_t)trk::kBM * trk::kBN * sizeof(float);
+  // the cheapest split, kept when it beats one pass by 5%
+  const double one_pass = (double)((nt + slots - 1) / slots) * (double)rows;
+  double best = 0.95 * one_pass;
   for (int s = 2; s <= 64; ++s) {
     int64_t chunk = (rows + s - 1) / s;
     chunk = (chunk + trk::kTS - 1) / trk::kTS * trk::kTS;
     if (chunk < 8 * trk::kTS || chunk > lim32) continue;
     const int64_t sp = (rows + chunk - 1) / chunk;
-    if ((size_t)sp * sq > ws_limit || nt * sp > 0x7fffffffLL) continue;
-    const double cost = (double)((nt * sp + slots - 1) / slots) * (double)chunk + (double)(sp + 1) * per_split;
-    if (cost < 0.95 * best) {
+    if ((size_t)(sp * tail) * tile_bytes > ws_limit || tail * sp > 0x7fffffffLL) continue;
+    const double cost = (double)(head / slots) * (double)rows + (double)((tail * sp + slots - 1) / slots) * (double)chunk +
+                        1.8 * (double)(sp + 1) * (double)tail;
+    if (cost < best) {
       best = cost;
-      g = GramPlan{(int)sp, chunk, (size_t)sp * sq};
+      g = GramPlan{head, (int)sp, chunk, (size_t)(sp * tail) * tile_bytes};
     }
   }
   return g;
@@ -864,10 +888,11 @@ GramPlan gram_plan(int64_t rows, int64_t width, int64_t sb, int64_t slots, size_
 
 // Row Gram out (+)= x^T x of x (rows, width), fp32 out: the transposing-read
 // dW kernel with every row as one token and both operands x, over the tiles on
-// or above the diagonal, then the mirror.  With token splits (a workspace
-// holding them), each split's partial square goes to the workspace and
-// sum_splits_upper adds them in split order; otherwise rows are taken in
-// chunks whose buffer offsets fit 32 bits, each adding to the output.
+// or above the diagonal, then the mirror.  Tiles run over all rows straight into
+// out, in chunks of rows whose buffer offsets fit 32 bits, each adding to the
+// output; with token splits (a workspace holding them), the tiles past the
+// whole rounds run per split into compact partial tiles, which
+// sum_split_tiles adds in split order.
 extern "C" int da_row_gram_workspace(int64_t rows, int64_t width, int dtype, size_t* bytes) {
   using namespace da;
   if (!bytes) return set_error(DA_ERR_INVALID, "da_row_gram_workspace: bytes is NULL");
@@ -927,6 +952,9 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
   m.sym = 1;
   m.rows_total = 0;
   const int64_t nt = m.tiles_m * (m.tiles_m + 1) / 2;
+  m.tile0 = 0;
+  m.sym_count = nt;
+  m.compact = 0;
   auto launch_tiles = [&](int64_t blocks) {
     if (dtype == DA_BF16)
       materialize_tiles_tr<DA_BF16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(m);
@@ -934,8 +962,23 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
       materialize_tiles_tr<DA_F16, DA_F32><<<(unsigned)blocks, kThreads, 0, st>>>(m);
     return check_launch("da_row_gram");
   };
+  // head: tiles 0 .. head - 1 over all rows, into out (the whole triangle when
+  // there are no splits)
+  const int64_t head = g.splits > 1 ? g.head : nt;
+  if (head > 0) {
+    m.sym_count = head;
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk32) {
+      m.a = (const char*)x + r0 * sb;
+      m.g = m.a;
+      m.tokens = rows - r0 < chunk32 ? rows - r0 : chunk32;
+      m.acc = accumulate || r0 > 0;
+      rc = launch_tiles(head);
+      if (rc) return rc;
+    }
+  }
   if (g.splits > 1) {
-    // split b = rows b*chunk .. of x into its own square of the workspace
+    // tiles head .. nt - 1: split b = rows b*chunk .. of x, compact partial tiles
+    const int64_t tail = nt - head;
     m.a = (const char*)x;
     m.g = m.a;
     m.batch = g.splits;
@@ -944,25 +987,16 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
     m.a_bstride = g.chunk * sb;
     m.g_bstride = m.a_bstride;
     m.out = (char*)workspace;
-    m.out_bstride = width * width;
-    m.out_rstride = width;
+    m.tile0 = head;
+    m.sym_count = tail;
+    m.compact = 1;
     m.acc = 0;
-    rc = launch_tiles(nt * g.splits);
+    rc = launch_tiles(tail * g.splits);
     if (rc) return rc;
-    const int64_t quads = width * (width / 4);
-    sum_splits_upper<<<(unsigned)((quads + 255) / 256), 256, 0, st>>>((const float*)workspace, g.splits, width,
-                                                                     out, ld_out, accumulate ? 1 : 0);
+    sum_split_tiles<<<dim3((unsigned)tail, trk::kBM / 4), 256, 0, st>>>(
+        (const float*)workspace, g.splits, tail, head, m.tiles_m, width, out, ld_out, accumulate ? 1 : 0);
     rc = check_launch("da_row_gram(sum)");
     if (rc) return rc;
-  } else {
-    for (int64_t r0 = 0; r0 < rows; r0 += chunk32) {
-      m.a = (const char*)x + r0 * sb;
-      m.g = m.a;
-      m.tokens = rows - r0 < chunk32 ? rows - r0 : chunk32;
-      m.acc = accumulate || r0 > 0;
-      rc = launch_tiles(nt);
-      if (rc) return rc;
-    }
   }
   const int64_t nb = (width + 63) / 64;
   if (m.tiles_m > 1) {

@@ -205,8 +205,9 @@ int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width, int64_t x
 
 /*
  * Workspace bytes da_row_gram can use on the current device for (rows, width)
- * packed rows (x_stride == width): token splits that let a small triangle of
- * tiles fill the GPU (a fp32 width x width partial per split).  0 when one
+ * packed rows (x_stride == width): the tiles past the triangle's last whole
+ * round of CUs run as token splits into compact fp32 256 x 256 partial tiles,
+ * so a partly filled round (or a small triangle) fills the GPU.  0 when one
  * pass is best.  A smaller or NULL workspace is accepted: the call then uses
  * the splits that fit (down to none).  Calls sharing a workspace must be
  * ordered on one stream.  No reference counterpart (workspace sizing).
