@@ -671,6 +671,24 @@ __global__ __launch_bounds__(256) void sum_split_tiles(const float* __restrict__
   *(f32x4*)dst = v;
 }
 
+// Gradient-free rows: out[r] = 1 when some entry of row r compares unequal to
+// zero, by its magnitude bits (-0.0 is zero; NaN, inf and subnormals are not),
+// one workgroup per row reading it once in 16-byte chunks.
+template <int ES>
+__global__ __launch_bounds__(256) void nonzero_rows_kernel(const char* __restrict__ x, int64_t chunks,
+                                                           int64_t stride_b, uint8_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const u32x4* p = (const u32x4*)(x + r * stride_b);
+  constexpr uint32_t kMag = ES == 4 ? 0x7fffffffu : 0x7fff7fffu;  // both halves of a 16-bit pair
+  uint32_t any = 0;
+  for (int64_t c = threadIdx.x; c < chunks; c += 256) {
+    const u32x4 v = __builtin_nontemporal_load(p + c);
+    any |= (v[0] & kMag) | (v[1] & kMag) | (v[2] & kMag) | (v[3] & kMag);
+  }
+  const int nz = __syncthreads_or(any != 0u);
+  if (threadIdx.x == 0) out[r] = nz ? 1 : 0;
+}
+
 // Row Gram: copy the tiles above the diagonal (computed) to the ones below it.
 // Block (I, J) of 64 x 64 outputs with tile(I) > tile(J) (256-output tiles,
 // so a block lies in one tile pair) reads the transposed block (J, I) through
@@ -1004,4 +1022,27 @@ extern "C" int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width
     return check_launch("da_row_gram(mirror)");
   }
   return DA_OK;
+}
+
+// out[r] = (x[r, :] != 0).any() for the rows of x (rows, width) with row stride
+// x_stride (elements): the gradient-free-row test of the K-FAC factors.
+extern "C" int da_nonzero_rows(const void* x, int dtype, int64_t rows, int64_t width, int64_t x_stride,
+                               uint8_t* out, void* stream) {
+  using namespace da;
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "da_nonzero_rows: bad dtype %d", dtype);
+  if (rows < 0 || width < 0) return set_error(DA_ERR_INVALID, "da_nonzero_rows: negative size");
+  if (rows == 0) return DA_OK;
+  if (!x || !out) return set_error(DA_ERR_INVALID, "da_nonzero_rows: NULL pointer");
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  if ((width * es) % 16 || (x_stride * es) % 16 || x_stride < width || ((uintptr_t)x & 15))
+    return set_error(DA_ERR_INVALID,
+                     "da_nonzero_rows: rows must be 16-byte aligned, width and stride multiples of 16 bytes");
+  if (rows > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_nonzero_rows: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t chunks = width * es / 16;
+  if (es == 4)
+    nonzero_rows_kernel<4><<<(unsigned)rows, 256, 0, st>>>((const char*)x, chunks, x_stride * es, out);
+  else
+    nonzero_rows_kernel<2><<<(unsigned)rows, 256, 0, st>>>((const char*)x, chunks, x_stride * es, out);
+  return check_launch("da_nonzero_rows");
 }

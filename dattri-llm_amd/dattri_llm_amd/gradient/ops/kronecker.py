@@ -71,7 +71,8 @@ def _right_multiply(x: torch.Tensor, matrix: torch.Tensor) -> torch.Tensor:
 
 def _drop_gradient_free_rows(a_f: torch.Tensor, g_f: torch.Tensor):
     """kronecker.py:65-81: drop token rows whose output gradient is exactly zero."""
-    keep = (g_f != 0).any(dim=1)
+    keep = kernels.nonzero_rows(g_f) if g_f.dtype in (torch.bfloat16, torch.float16, torch.float32) \
+        else (g_f != 0).any(dim=1)
     if bool(keep.all()):
         return a_f, g_f
     return a_f[keep], g_f[keep]

@@ -411,6 +411,24 @@ def row_gram(x: torch.Tensor, *, out: torch.Tensor | None = None, accumulate: bo
     return out
 
 
+def nonzero_rows(x: torch.Tensor) -> torch.Tensor:
+    """``(x != 0).any(dim=1)`` of a 2-D tensor as a bool vector (one read of
+    ``x``; -0.0 counts as zero, NaN as nonzero)."""
+    dev = nat.require_device(x)
+    if x.dim() != 2:
+        raise ValueError("nonzero_rows expects a 2-D tensor")
+    n = x.shape[0]
+    out = torch.empty(n, dtype=torch.uint8, device=dev)
+    if n == 0:
+        return out.bool()
+    xp = prepare_rows(x)  # zero padding changes no row's answer
+    if xp.stride(1) != 1:
+        xp = xp.contiguous()
+    nat.check(nat.load().da_nonzero_rows(xp.data_ptr(), nat.dtype_code(xp.dtype), n, xp.shape[1], xp.stride(0),
+                                         out.data_ptr(), nat.stream_ptr(dev)), "nonzero_rows")
+    return out.view(torch.bool)
+
+
 def _column_sums(g: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     """sum_t g[b, t, :] through the materialize kernel with a ones activation."""
     b, t, _ = g.shape

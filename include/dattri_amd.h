@@ -215,6 +215,16 @@ int da_row_gram(const void* x, int dtype, int64_t rows, int64_t width, int64_t x
 int da_row_gram_workspace(int64_t rows, int64_t width, int dtype, size_t* bytes);
 
 /*
+ * Gradient-free rows: out[r] = 1 if some entry of row r of x (rows, width),
+ * row stride x_stride (elements), compares unequal to zero, else 0 (-0.0 is
+ * zero; NaN, inf and subnormals are not).  Rows 16-byte aligned, width and
+ * x_stride multiples of 16 bytes.  Replaces the mask of
+ * dattri_llm/gradient/ops/kronecker.py:65-81 ((g_f != 0).any(dim=1)).
+ */
+int da_nonzero_rows(const void* x, int dtype, int64_t rows, int64_t width, int64_t x_stride, uint8_t* out,
+                    void* stream);
+
+/*
  * One dense layer of a score GEMM: m1 is (B1, width), m2 is (B2, width).
  * Element c of row r of side s lives at  m_s + r*ld_s + (c/64)*blk_s + c%64
  * (elements): rows are sequences of 64-element blocks.  blk_s = 64 (or 0) is

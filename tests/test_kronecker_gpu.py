@@ -324,3 +324,29 @@ def test_gradient_free_rows_match_the_reference_rule(device):
     assert torch.equal(a_f.cpu(), a[want])  # the activation rows kept are exactly the reference's
     got, ref = g_f.cpu(), g[want]  # (NaN != NaN, so compare with the NaNs replaced)
     assert torch.equal(torch.isnan(got), torch.isnan(ref)) and torch.equal(got.nan_to_num(7.0), ref.nan_to_num(7.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("width", [8, 40, 300, 14336])
+def test_nonzero_rows_kernel(device, dtype, width):
+    """da_nonzero_rows against (x != 0).any(1) on the CPU: random rows, all-zero
+    and -0.0 rows, rows whose only nonzero is a NaN, an inf, a subnormal or
+    the last column (past padding when the width is not a chunk multiple)."""
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(width)
+    x = torch.randn(64, width, generator=gen).to(dtype)
+    x[1:9] = 0
+    x[2] = -0.0
+    x[3, width // 2] = float("nan")
+    x[4, 0] = float("-inf")
+    x[5, 1] = torch.finfo(dtype).tiny / 4  # subnormal (a nonzero bit pattern in every dtype)
+    x[6, width - 1] = 1.0
+    want = (x != 0).any(dim=1)
+    got = kernels.nonzero_rows(x.to(device))
+    assert got.dtype == torch.bool and torch.equal(got.cpu(), want)
+    assert kernels.nonzero_rows(x[:0].to(device)).numel() == 0
+    view = torch.zeros(16, width + 8, dtype=dtype)
+    view[3, 2] = 5
+    got_view = kernels.nonzero_rows(view.to(device)[:, :width])  # strided rows
+    assert torch.equal(got_view.cpu(), (view[:, :width] != 0).any(dim=1))

@@ -74,6 +74,12 @@ def test_argument_checks_fail_before_any_gpu_work():
     assert lib.da_row_gram(None, bf, 0, 8, 8, OUT, 8, 1, None, 0, None) == _native.DA_OK
     assert lib.da_row_gram(X, bf, 10, 0, 8, OUT, 8, 0, None, 0, None) == _native.DA_OK
 
+    # da_nonzero_rows(x, dtype, rows, width, x_stride, out, stream)
+    check(lib.da_nonzero_rows(X, 9, 4, 8, 8, OUT, None), _native.DA_ERR_INVALID, ["bad dtype"])
+    check(lib.da_nonzero_rows(None, bf, 4, 8, 8, OUT, None), _native.DA_ERR_INVALID, ["NULL"])
+    check(lib.da_nonzero_rows(X, bf, 4, 12, 12, OUT, None), _native.DA_ERR_INVALID, ["16 bytes"])
+    assert lib.da_nonzero_rows(None, bf, 0, 8, 8, None, None) == _native.DA_OK
+
     # da_materialize_linear(a, g, dtype, batch, tokens, K, D, a_bs, a_ts, g_bs, g_ts, bias,
     #                       out, out_dtype, out_bs, out_rs, out_blk, stream)
     def mat(dtype=bf, k=64, d=64, a=X, blk=64, out_rs=64, tokens=4):
