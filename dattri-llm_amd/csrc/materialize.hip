@@ -375,6 +375,7 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_big(MatArgs m) 
 namespace trk {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
+constexpr int kGroup = 4;                   // row tiles per column sweep (4 beat 8 and 16 on the C4 dW shapes)
 constexpr int kTS = 32;                     // tokens per stage
 constexpr int kRow = 512;                   // bytes per token row of a 256-column operand tile
 constexpr int kOp = kTS * kRow;             // 16 KB per operand per stage
@@ -444,10 +445,10 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
     const int64_t per_sample = m.tiles_m * m.tiles_n;
     b = logical / per_sample;
     const int64_t rem = logical - b * per_sample;
-    const int64_t per_group = (int64_t)kGroup * m.tiles_n;
+    const int64_t per_group = (int64_t)trk::kGroup * m.tiles_n;
     const int64_t group = rem / per_group;
-    const int64_t first = group * kGroup;
-    const int64_t gsize = min(m.tiles_m - first, (int64_t)kGroup);
+    const int64_t first = group * trk::kGroup;
+    const int64_t gsize = min(m.tiles_m - first, (int64_t)trk::kGroup);
     const int64_t in_group = rem - group * per_group;
     tm = first + in_group % gsize;
     tn = in_group / gsize;
