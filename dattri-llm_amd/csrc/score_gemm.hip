@@ -137,8 +137,11 @@ __global__ __launch_bounds__(kThreads) void score_gemm_chunks(ScoreArgs s) {
 // stage is one unit of the tile's 16 side-1 rows and 64 side-2 rows: 80 rows x
 // 4 blocks, each DMA instruction 8 rows x one 128-byte block (with the
 // k-blocked layout of the scoring loop, 1 KB contiguous), into a 4-deep ring.
-// Every row is read once per launch, so the loads carry the non-temporal hint
-// (6.18 -> 6.66 TB/s on the Llama-8B block's 64-query score).
+// A side whose rows are read once per launch (the other side fits one tile)
+// is loaded with the non-temporal hint: 6.18 -> 6.66 TB/s on the Llama-8B
+// block's 8 x 64 score, where both sides are read once.  Rows read again by
+// other tiles (a 4096 x 128 output re-reads each query row per 16-row tile)
+// keep the default policy, which leaves them in L2.
 // Rows past a side's end and bytes past a layer's width read as zero.  Wave w
 // loads block w of every stage and multiplies it: 2 x 4 16x16x32 MFMAs.  LDS
 // row r of a block holds logical 16-byte chunk c in slot c ^ ((r/2) % 8): the
@@ -171,6 +174,8 @@ struct RingArgs {
   int64_t nwg;            // workgroups per output tile
   int64_t b1, b2, tiles_n;
   float* partial;         // [b1][b2][nwg]
+  int nt1, nt2;           // side 1 / side 2 rows are read once (one tile across the other side):
+                          // non-temporal loads
 };
 
 __device__ __forceinline__ int64_t ring_first(int64_t w, const RingArgs& a) { return w * a.units / a.nwg; }
@@ -230,7 +235,10 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring(RingArgs a) {
 #pragma unroll
     for (int i = 0; i < sr::kDma; ++i) {
       const bool en = live & (roff[i] != sr::kOob) & (kin + cbo[i] < lbytes);
-      dma16_nt(i < 2 ? r1 : r2, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
+      if (i < 2 ? a.nt1 : a.nt2)
+        dma16_nt(i < 2 ? r1 : r2, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
+      else
+        dma16(i < 2 ? r1 : r2, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
     }
     if (live && ++iu == lunits) {
       iu = 0;
@@ -462,6 +470,8 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
     r.b2 = b2;
     r.tiles_n = (b2 + kTileN - 1) / kTileN;
     r.partial = (float*)workspace;
+    r.nt1 = r.tiles_n == 1;                     // side-1 rows meet one side-2 tile
+    r.nt2 = (b1 + kTileM - 1) / kTileM == 1;    // side-2 rows meet one side-1 tile
     const int64_t tiles = ((b1 + kTileM - 1) / kTileM) * r.tiles_n;
     const unsigned grid = (unsigned)(tiles * p.nwg);
     switch (dtype) {
