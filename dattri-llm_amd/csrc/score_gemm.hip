@@ -17,6 +17,8 @@
 // element-to-k assignment is used on both sides, so the sum is exact in any
 // order.  The four waves split the chunk, combine through LDS and write one
 // fp32 partial tile; a second kernel sums the partials in a fixed order.
+#include <atomic>
+
 #include "common.h"
 
 namespace da {
@@ -413,31 +415,12 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
   return DA_OK;
 }
 
-}  // namespace
-}  // namespace da
-
-extern "C" {
-
-int da_score_gemm_workspace(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers,
-                            int dtype, size_t* bytes) {
-  da::Plan p;
-  int rc = da::make_plan(b1, b2, layers, n_layers, dtype, &p);
-  if (rc) return rc;
-  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_score_gemm_workspace: bytes is NULL");
-  *bytes = p.ws;
-  return DA_OK;
-}
-
-int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
-                  float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* workspace,
-                  size_t workspace_bytes, void* stream) {
-  using namespace da;
-  Plan p;
-  int rc = make_plan(b1, b2, layers, n_layers, dtype, &p);
-  if (rc) return rc;
+int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
+             float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* workspace,
+             size_t workspace_bytes, hipStream_t st) {
+  int rc = DA_OK;
   if (b1 == 0 || b2 == 0) return DA_OK;
   if (!out) return set_error(DA_ERR_INVALID, "da_score_gemm: out is NULL");
-  hipStream_t st = (hipStream_t)stream;
   if (p.n_chunks == 0) {
     if (accumulate) return DA_OK;
     if (ld_col != 1) return set_error(DA_ERR_INVALID, "da_score_gemm: empty product needs ld_col == 1");
@@ -515,6 +498,79 @@ int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_la
   rc = check_launch("da_score_gemm(chunks)");
   if (rc) return rc;
   return reduce_partials((const float*)workspace, p.n_chunks, b1, b2, out, ld_row, ld_col, accumulate, st);
+}
+
+// The allocation-free entry point keeps its partials in this file-scope
+// device array (one copy per GPU, alive until the process ends).  Host code
+// must never pass `scratch` itself to a kernel: its name is a host-side
+// stand-in, so kernels take the device address scratch_address() resolves.
+constexpr size_t kScratchBytes = DA_SCORE_GEMM_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+// Device address of this GPU's scratch, resolved with the device current on
+// its first use and cached per device (racing threads store the same value).
+int scratch_address(float** ptr) {
+  static std::atomic<float*> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(DA_ERR_HIP, "da_score_gemm_noalloc: hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(DA_ERR_UNSUPPORTED, "da_score_gemm_noalloc: device %d beyond the %d the library tracks", dev,
+                     kMaxDevices);
+  float* p = cache[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !addr)
+      return set_error(DA_ERR_HIP, "da_score_gemm_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(e));
+    p = (float*)addr;
+    cache[dev].store(p, std::memory_order_release);
+  }
+  *ptr = p;
+  return DA_OK;
+}
+
+}  // namespace
+}  // namespace da
+
+extern "C" {
+
+int da_score_gemm_workspace(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers,
+                            int dtype, size_t* bytes) {
+  da::Plan p;
+  int rc = da::make_plan(b1, b2, layers, n_layers, dtype, &p);
+  if (rc) return rc;
+  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_score_gemm_workspace: bytes is NULL");
+  *bytes = p.ws;
+  return DA_OK;
+}
+
+int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
+                  float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  da::Plan p;
+  const int rc = da::make_plan(b1, b2, layers, n_layers, dtype, &p);
+  if (rc) return rc;
+  return da::run_plan(p, b1, b2, layers, n_layers, dtype, out, ld_row, ld_col, accumulate, workspace,
+                      workspace_bytes, (hipStream_t)stream);
+}
+
+int da_score_gemm_noalloc(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
+                          float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* stream) {
+  da::Plan p;
+  int rc = da::make_plan(b1, b2, layers, n_layers, dtype, &p);
+  if (rc) return rc;
+  if (p.ws > da::kScratchBytes)
+    return da::set_error(DA_ERR_WORKSPACE,
+                         "da_score_gemm_noalloc: %lld x %lld outputs need %zu bytes of partials, more than the "
+                         "%zu-byte scratch; call da_score_gemm with a workspace instead",
+                         (long long)b1, (long long)b2, p.ws, da::kScratchBytes);
+  float* ptr = nullptr;
+  rc = da::scratch_address(&ptr);
+  if (rc) return rc;
+  return da::run_plan(p, b1, b2, layers, n_layers, dtype, out, ld_row, ld_col, accumulate, ptr, da::kScratchBytes,
+                      (hipStream_t)stream);
 }
 
 }  // extern "C"

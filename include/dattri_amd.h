@@ -6,9 +6,10 @@
  * void*), launches stream-ordered work and returns a status code.  Nothing is
  * synchronised and nothing is allocated by the library: temporary storage is a
  * caller-provided workspace whose size the matching *_workspace query returns.
- * All entry points are re-entrant (no global mutable state besides a
+ * All entry points but one are re-entrant (no global mutable state besides a
  * thread-local error message), so they may be called from concurrent autograd
- * hook threads on different streams.
+ * hook threads on different streams.  The exception is da_score_gemm_noalloc,
+ * whose partials live in one library-owned device array per GPU.
  *
  * Results are fp32 unless an output dtype is given.  Inputs are never written.
  *
@@ -260,6 +261,27 @@ int da_score_gemm_workspace(int64_t b1, int64_t b2, const da_dense_layer* layers
 int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
                   float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* workspace,
                   size_t workspace_bytes, void* stream);
+
+/*
+ * da_score_gemm without a workspace, for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  No counterpart in the reference.
+ *
+ * Same arguments and results as da_score_gemm (bit-identical: same kernels,
+ * same fixed-order reduction) minus the workspace.  The split-K partials live
+ * in a library-owned device array of DA_SCORE_GEMM_SCRATCH_BYTES on each GPU
+ * the library runs on, held until the process ends; its address is resolved
+ * once per device on the first call there.  A problem whose
+ * da_score_gemm_workspace exceeds that size returns DA_ERR_WORKSPACE (for
+ * 2-byte dtypes one partial tile per CU: e.g. 8 x 64 outputs need 0.5 MiB on
+ * 256 CUs).  Nothing is allocated or freed and no memset is issued; every
+ * partial is written before it is read, so nothing carries over between
+ * calls.  All calls on one GPU share the array: calls that overlap on it
+ * (different streams or threads) race, so order them on one stream.
+ */
+#define DA_SCORE_GEMM_SCRATCH_BYTES ((size_t)8 << 20)
+int da_score_gemm_noalloc(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
+                          float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* stream);
 
 /*
  * Per-sample weight gradient of a token norm layer (kind 0 = RMSNorm,
