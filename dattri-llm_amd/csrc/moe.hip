@@ -1,8 +1,8 @@
 // K3c: MoE routing and expert segmentation (integer work, bit-exact).
 //
 //   da_moe_topk:       top-k of softmax(logits) per token, weights renormalised
-//                      over the k, indices by descending probability with ties
-//                      going to the lower expert index -- the router of
+//                      over the k, indices in torch.topk's CPU order (ties
+//                      included, topk_select.h) -- the router of
 //                      transformers' MixtralTopKRouter.forward
 //                      (softmax(logits.float()) -> topk -> / sum), as consumed by
 //                      dattri_llm/gradient/hooks/override_layers/fused_experts.py:210-237.
@@ -19,6 +19,7 @@
 // Both are tiny next to the expert GEMMs; they exist so the routing never
 // leaves the device and never depends on a library sort's tie order.
 #include "common.h"
+#include "topk_select.h"
 
 namespace da {
 namespace {
@@ -27,47 +28,53 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 16;
 constexpr int kMaxBins = 8192;
 
+// One router queue per lane in LDS: entry i of lane l at [i * lanes + l], so
+// the lanes of a wave touching the same entry hit consecutive words.
+struct LdsQueue {
+  float* p;
+  uint16_t* e;
+  int lanes;
+  __device__ topk::Entry get(int i) const { return {p[i * lanes], (int)e[i * lanes]}; }
+  __device__ void set(int i, topk::Entry x) {
+    p[i * lanes] = x.p;
+    e[i * lanes] = (uint16_t)x.e;
+  }
+  __device__ void swap(int i, int j) {
+    const topk::Entry a = get(i), b = get(j);
+    set(i, b);
+    set(j, a);
+  }
+};
+
+// One lane per token (workgroups of 64 lanes, 32 above 128 experts, so the
+// dynamic LDS of 6 bytes per expert and lane stays within 48 KiB).  softmax(logits.float()) as torch computes it -- a maximum that
+// propagates NaN, then exp(x - max) / sum -- so a row holding a NaN or +inf
+// logit, or only -inf logits, gives NaN probabilities as torch's does; then
+// the selection of topk_select.h and weights = top / sum(top).
 template <int DT>
-__global__ void moe_topk_kernel(const char* logits, int64_t n, int e, int k, int64_t rstride,
-                                float* weights, int64_t* index) {
-  const int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(kWave) void moe_topk_kernel(const char* logits, int64_t n, int e, int k,
+                                                         int64_t rstride, float* weights, int64_t* index) {
+  extern __shared__ __attribute__((aligned(16))) char topk_lds[];
+  const int lane = threadIdx.x, lanes = blockDim.x;
+  const int64_t tok = (int64_t)blockIdx.x * lanes + lane;
   if (tok >= n) return;
+  LdsQueue q{(float*)topk_lds + lane, (uint16_t*)(topk_lds + (size_t)e * lanes * 4) + lane, lanes};
   const char* row = logits + tok * rstride * Elem<DT>::kBytes;
   float mx = -INFINITY;
-  for (int x = 0; x < e; ++x) mx = fmaxf(mx, Elem<DT>::load(row, x));
+  for (int x = 0; x < e; ++x) {
+    const float v = Elem<DT>::load(row, x);
+    if (mx == mx && (v != v || v > mx)) mx = v;
+  }
   float sum = 0.f;
   for (int x = 0; x < e; ++x) sum += expf(Elem<DT>::load(row, x) - mx);
-  // Selection by repeated arg-max over the probabilities; strict '>' keeps the
-  // lower index on ties.  `taken` marks chosen experts (e <= 256).
-  uint32_t taken[kMaxExperts / 32];
-#pragma unroll
-  for (int w = 0; w < kMaxExperts / 32; ++w) taken[w] = 0u;
-  float top[kMaxTopK];
-  int64_t idx[kMaxTopK];
+  for (int x = 0; x < e; ++x) q.set(x, {expf(Elem<DT>::load(row, x) - mx) / sum, x});
+  topk::select_topk(q, e, k);
   float tsum = 0.f;
+  for (int s = 0; s < k; ++s) tsum += q.get(s).p;
   for (int s = 0; s < k; ++s) {
-    float best = -1.f;
-    int bi = -1;
-    for (int x = 0; x < e; ++x) {
-      if (taken[x >> 5] & (1u << (x & 31))) continue;
-      const float p = expf(Elem<DT>::load(row, x) - mx) / sum;
-      if (p > best) {
-        best = p;
-        bi = x;
-      }
-    }
-    if (bi < 0) {  // remaining probabilities are NaN: take the lowest free index
-      for (int x = e - 1; x >= 0; --x)
-        if (!(taken[x >> 5] & (1u << (x & 31)))) bi = x;
-    }
-    taken[bi >> 5] |= 1u << (bi & 31);
-    top[s] = best;
-    idx[s] = bi;
-    tsum += best;
-  }
-  for (int s = 0; s < k; ++s) {
-    weights[tok * k + s] = top[s] / tsum;
-    index[tok * k + s] = idx[s];
+    const topk::Entry t = q.get(s);
+    weights[tok * k + s] = t.p / tsum;
+    index[tok * k + s] = t.e;
   }
 }
 
@@ -389,12 +396,15 @@ int da_moe_topk(const void* logits, int dtype, int64_t n_tokens, int n_experts, 
   if (row_stride < n_experts) return set_error(DA_ERR_INVALID, "%s: row stride < n_experts", who);
   if (n_tokens == 0) return DA_OK;
   if (!logits || !weights || !index) return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
-  const unsigned blocks = (unsigned)((n_tokens + 255) / 256);
+  const int lanes = n_experts <= 128 ? kWave : kWave / 2;
+  if ((n_tokens + lanes - 1) / lanes > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: too many tokens", who);
+  const unsigned blocks = (unsigned)((n_tokens + lanes - 1) / lanes);
+  const size_t lds = (size_t)n_experts * lanes * (sizeof(float) + sizeof(uint16_t));  // <= 48 KiB
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case DA_BF16: moe_topk_kernel<DA_BF16><<<blocks, 256, 0, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
-    case DA_F16: moe_topk_kernel<DA_F16><<<blocks, 256, 0, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
-    default: moe_topk_kernel<DA_F32><<<blocks, 256, 0, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
+    case DA_BF16: moe_topk_kernel<DA_BF16><<<blocks, lanes, lds, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
+    case DA_F16: moe_topk_kernel<DA_F16><<<blocks, lanes, lds, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
+    default: moe_topk_kernel<DA_F32><<<blocks, lanes, lds, st>>>((const char*)logits, n_tokens, n_experts, k, row_stride, weights, index); break;
   }
   return check_launch(who);
 }

@@ -351,10 +351,12 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
                      size_t workspace_bytes, void* stream);
 
 /*
- * MoE router: per token, top-k of softmax(logits) (fp32), weights renormalised
- * over the k, indices by descending probability, ties to the lower expert
- * index -- the router contract of transformers' MixtralTopKRouter.forward used
- * by dattri_llm/gradient/hooks/override_layers/fused_experts.py:210-237.
+ * MoE router: per token, top-k of softmax(logits) (fp32, a NaN or +inf logit
+ * or an all -inf row gives NaN probabilities as torch's softmax does), weights
+ * renormalised over the k, indices in the order torch.topk returns on the CPU,
+ * ties and NaN rows included (ATen's nth_element / partial_sort selection) --
+ * the router contract of transformers' MixtralTopKRouter.forward used by
+ * dattri_llm/gradient/hooks/override_layers/fused_experts.py:210-237.
  * logits (n_tokens, n_experts) with row stride row_stride; weights (n, k)
  * fp32; index (n, k) int64.  n_experts <= 256, k <= 16.
  */
