@@ -29,12 +29,15 @@ project_outer                  hooks/hooks.py:631-648, projection.py:423-489  Kr
                                                                               vec(P_out^T dW P_in) vs materialize_linear
 score_gemm                     gradient/ops/dot.py:114, :505, :599-604        brute-force loops
 cost rules                     dot.py:728-753, projection.py:846-899          the reference's own known-answer tables
-moe_router_topk                transformers MixtralTopKRouter.forward         torch.topk(torch.softmax(x.float()))
-                               (installed transformers, a library routine)
+moe_router_topk                transformers MixtralTopKRouter.forward         torch.topk(torch.softmax(x.float())) on
+                               (installed transformers, a library routine);   thousands of rows with tied, NaN, +-inf
+                               tie order: ATen TopKImpl.h + libstdc++         logits (both selection branches)
 moe_segments                   hooks/override_layers/fused_experts.py:219-228 torch.where(one_hot(idx).permute(2,1,0)[e])
 moe_regroup_dense              hooks/routing.py:71-86                         explicit scatter check
 moe_segment_ghost              dense-with-zeros cross_gram (routing.py:17-23) equals cross_gram on the regrouped
                                                                               zero-filled (B, T, d) factors
+moe_segment_ghost_compact      the same without the zero rows                 equals moe_segment_ghost (empty experts,
+                                                                              bias, one sample); brute force
 kfac_factors                   gradient/ops/kronecker.py:65-118               brute-force sums of row outer products over
                                                                               the rows with a non-zero gradient
 fim_factors                    gradient/ops/kronecker.py:121-141              brute-force sum of per-sample outer products
@@ -77,6 +80,7 @@ __all__ = [
     "moe_regroup_dense",
     "moe_router_topk",
     "moe_segment_ghost",
+    "moe_segment_ghost_compact",
     "moe_segments",
     "norm_weight_grad",
     "preprocess",
@@ -88,20 +92,12 @@ __all__ = [
     "BF16_EPS",
     "F32_EPS",
     "F16_EPS",
-    "bf16_round",
 ]
 
 # torch.finfo(dtype).eps, the RMSNorm eps=None special case (norm.py:38-39).
 F32_EPS = float(np.finfo(np.float32).eps)  # 2**-23
 F16_EPS = float(np.finfo(np.float16).eps)  # 2**-10
 BF16_EPS = 2.0**-7
-
-
-def bf16_round(x: np.ndarray) -> np.ndarray:
-    """Round float32 values to bfloat16 (round-to-nearest-even), returned as float32."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
-    return u.astype(np.uint32).view(np.float32)
 
 
 def _with_ones(a: np.ndarray) -> np.ndarray:
@@ -360,24 +356,146 @@ def should_materialize(capture_style, seq_len, k_a, k_g) -> bool:
 
 
 def _softmax_f32(logits: np.ndarray) -> np.ndarray:
+    """softmax over the last axis in float32; a NaN anywhere in a row makes its
+    maximum NaN (numpy's max propagates NaN, as torch's does)."""
     x = logits.astype(np.float32)
-    m = x.max(axis=-1, keepdims=True)
-    e = np.exp(x - m, dtype=np.float32)
-    return e / e.sum(axis=-1, keepdims=True, dtype=np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        m = x.max(axis=-1, keepdims=True)
+        e = np.exp(x - m, dtype=np.float32)
+        return e / e.sum(axis=-1, keepdims=True, dtype=np.float32)
+
+
+def _before(x, y) -> bool:
+    """ATen's top-k order (largest first): NaN before any number, then larger
+    first (torch/include/ATen/native/TopKImpl.h, topk_impl_loop)."""
+    xn, yn = x[0] != x[0], y[0] != y[0]
+    return (xn and not yn) or x[0] > y[0]
+
+
+def _insertion_sort(q, lo, hi):
+    """libstdc++ __insertion_sort / __unguarded_linear_insert on q[lo:hi]."""
+    for i in range(lo + 1, hi):
+        v = q[i]
+        if _before(v, q[lo]):
+            q[lo + 1 : i + 1] = q[lo:i]
+            q[lo] = v
+            continue
+        j = i
+        while _before(v, q[j - 1]):
+            q[j] = q[j - 1]
+            j -= 1
+        q[j] = v
+
+
+def _adjust_heap(q, first, hole, length, v):
+    """libstdc++ __adjust_heap + __push_heap (root = the entry returned last)."""
+    top = child = hole
+    while child < (length - 1) // 2:
+        child = 2 * (child + 1)
+        if _before(q[first + child], q[first + child - 1]):
+            child -= 1
+        q[first + hole] = q[first + child]
+        hole = child
+    if length % 2 == 0 and child == (length - 2) // 2:
+        child = 2 * (child + 1)
+        q[first + hole] = q[first + child - 1]
+        hole = child - 1
+    while hole > top and _before(q[first + (hole - 1) // 2], v):
+        q[first + hole] = q[first + (hole - 1) // 2]
+        hole = (hole - 1) // 2
+    q[first + hole] = v
+
+
+def _heap_select(q, first, middle, last):
+    """libstdc++ __heap_select: __make_heap on [first, middle), then every later
+    entry that comes before the root replaces it (__pop_heap)."""
+    size = middle - first
+    if size >= 2:
+        for parent in range((size - 2) // 2, -1, -1):
+            _adjust_heap(q, first, parent, size, q[first + parent])
+    for i in range(middle, last):
+        if _before(q[i], q[first]):
+            v = q[i]
+            q[i] = q[first]
+            _adjust_heap(q, first, 0, size, v)
+
+
+def _sort_heap(q, first, last):
+    """libstdc++ __sort_heap."""
+    while last - first > 1:
+        last -= 1
+        v = q[last]
+        q[last] = q[first]
+        _adjust_heap(q, first, 0, last - first, v)
+
+
+def _nth_element(q, nth):
+    """libstdc++ std::nth_element (__introselect: median-of-three pivot moved to
+    the front, unguarded Hoare partition, depth limit 2*floor(log2 n), then an
+    insertion sort of the last range of at most 3)."""
+    first, last = 0, len(q)
+    if last == 0 or nth == last:
+        return
+    depth = 2 * (last.bit_length() - 1)
+    while last - first > 3:
+        if depth == 0:
+            _heap_select(q, first, nth + 1, last)
+            q[first], q[nth] = q[nth], q[first]
+            return
+        depth -= 1
+        a, b, c = first + 1, first + (last - first) // 2, last - 1
+        if _before(q[a], q[b]):
+            m = b if _before(q[b], q[c]) else (c if _before(q[a], q[c]) else a)
+        else:
+            m = a if _before(q[a], q[c]) else (c if _before(q[b], q[c]) else b)
+        q[first], q[m] = q[m], q[first]
+        pivot, lo, hi = q[first], first + 1, last
+        while True:
+            while _before(q[lo], pivot):
+                lo += 1
+            hi -= 1
+            while _before(pivot, q[hi]):
+                hi -= 1
+            if not lo < hi:
+                break
+            q[lo], q[hi] = q[hi], q[lo]
+            lo += 1
+        if lo <= nth:
+            first = lo
+        else:
+            last = lo
+    _insertion_sort(q, first, last)
+
+
+def _topk_order(probs_row, k: int) -> list[int]:
+    """The indices torch.topk(row, k) returns on the CPU: ATen's topk_impl_loop
+    runs std::partial_sort when k * 64 <= n, else std::nth_element at k - 1 and
+    std::sort of the first k - 1 (an insertion sort for k <= 16).  Equal values
+    keep the order those algorithms leave them in."""
+    q = [(float(v), j) for j, v in enumerate(probs_row)]
+    if k * 64 <= len(q):
+        _heap_select(q, 0, k, len(q))
+        _sort_heap(q, 0, k)
+    else:
+        _nth_element(q, k - 1)
+        _insertion_sort(q, 0, k - 1)
+    return [j for _v, j in q[:k]]
 
 
 def moe_router_topk(logits, k: int):
-    """Mixtral top-k router (transformers MixtralTopKRouter.forward): top-k of
-    softmax(logits.float()), weights renormalised over the k.  Indices are
-    ordered by descending probability, ties broken toward the lower expert
-    index.  Returns (weights (N,k) float32, indices (N,k) int64)."""
+    """Mixtral top-k router (installed transformers 5.15.0,
+    MixtralTopKRouter.forward): torch.topk(softmax(logits.float()), k) with the
+    weights renormalised over the k.  Indices follow torch.topk's CPU order,
+    ties and NaN rows included (:func:`_topk_order`).  A row holding a NaN or
+    +inf logit, or only -inf logits, has NaN probabilities, as torch's softmax
+    gives.  Returns (weights (N,k) float32, indices (N,k) int64)."""
     probs = _softmax_f32(np.asarray(logits))
-    n, e = probs.shape
-    # stable sort on (-prob) keeps the lower index first among equal values
-    order = np.argsort(-probs, axis=-1, kind="stable")[:, :k]
+    n = probs.shape[0]
+    order = np.array([_topk_order(probs[r], k) for r in range(n)], dtype=np.int64).reshape(n, k)
     top = np.take_along_axis(probs, order, axis=-1)
-    weights = top / top.sum(axis=-1, keepdims=True, dtype=np.float32)
-    return weights.astype(np.float32), order.astype(np.int64)
+    with np.errstate(invalid="ignore"):
+        weights = top / top.sum(axis=-1, keepdims=True, dtype=np.float32)
+    return weights.astype(np.float32), order
 
 
 def moe_segments(top_idx, n_experts: int):
@@ -412,6 +530,22 @@ def moe_segment_ghost(a1, g1, tok1, a2, g2, tok2, batch1, batch2, tokens1, token
     A2 = moe_regroup_dense(a2, tok2, batch2, tokens2)
     G2 = moe_regroup_dense(g2, tok2, batch2, tokens2)
     return cross_gram_factorized(A1, G1, A2, G2, bias)
+
+
+def moe_segment_ghost_compact(a1, g1, tok1, a2, g2, tok2, batch1, batch2, tokens1, tokens2, bias=False):
+    """moe_segment_ghost without forming the zero rows (they are inert,
+    routing.py:17-23): K_a = A1 A2^T and K_g = G1 G2^T over the routed rows
+    only, their Hadamard product summed into (sample of row p, sample of row q)
+    bins.  Same value, ~(B*T / rows)^2 fewer flops."""
+    a1, g1, a2, g2 = (np.asarray(x, np.float64) for x in (a1, g1, a2, g2))
+    if bias:
+        a1, a2 = _with_ones(a1), _with_ones(a2)
+    prod = (a1 @ a2.T) * (g1 @ g2.T)
+    bins1 = np.zeros((batch1, len(a1)))
+    bins1[np.asarray(tok1) // tokens1, np.arange(len(a1))] = 1.0
+    bins2 = np.zeros((batch2, len(a2)))
+    bins2[np.asarray(tok2) // tokens2, np.arange(len(a2))] = 1.0
+    return bins1 @ prod @ bins2.T
 
 
 # ---------------------------------------------------------------------------

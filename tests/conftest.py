@@ -36,3 +36,58 @@ def rel_err(got, ref) -> float:
     ref = np.asarray(ref, dtype=np.float64)
     denom = float(np.abs(ref).max()) if ref.size else 1.0
     return float(np.abs(got - ref).max() / (denom if denom > 0 else 1.0)) if ref.size else 0.0
+
+
+# The north-star bar: normwise relative error for bf16/fp16 inputs with fp32
+# accumulation, and for fp32 inputs.
+SPEC_BAR = {"bfloat16": 1e-2, "float16": 1e-2, "float32": 1e-3, "float64": 1e-3}
+# What fp32 accumulation against the float64 oracle on identical (already
+# rounded) inputs actually leaves, with margin; a result rounded to a 2-byte
+# dtype adds half an ulp of its own entries (the unit roundoff: 2^-8 for bf16's
+# 8-bit significand, 2^-11 for fp16's 11).
+TIGHT_FP32 = 1e-5
+HALF_ULP = {"bfloat16": 2.0**-8, "float16": 2.0**-11}
+
+
+def roundings(n: int, dtype: str = "bfloat16") -> float:
+    """Tight bound for a result that passes through ``n`` roundings to a 2-byte
+    dtype on the way (an intermediate dense gradient stored in bf16, a bf16
+    output): each perturbs an entry by at most half an ulp."""
+    return TIGHT_FP32 + n * HALF_ULP[dtype]
+
+
+def _dtype_name(dtype) -> str:
+    return str(dtype).replace("torch.", "")
+
+
+def assert_parity(got, ref, in_dtype, *, out_dtype=None, tight=None, label=""):
+    """Assert both bars on a GPU result against its oracle.
+
+    ``got`` is a tensor (its dtype is the output dtype unless ``out_dtype`` is
+    given) or an array of fp32 results; ``in_dtype`` is the dtype of the
+    inputs the kernels read (picks the north-star bar).  The tight bound is
+    ``tight`` or TIGHT_FP32 plus the output rounding.  With DA_PARITY_LOG set,
+    the tight bound is logged to that file instead of asserted (the spec bar
+    still holds), to measure the errors the kernels leave."""
+    import numpy as np
+
+    if hasattr(got, "detach"):
+        out_dtype = out_dtype or got.dtype
+        got = got.detach().double().cpu().numpy()
+    if hasattr(ref, "detach"):
+        ref = ref.detach().double().cpu().numpy()
+    out_name = _dtype_name(out_dtype) if out_dtype is not None else "float32"
+    err = rel_err(np.asarray(got), np.asarray(ref))
+    spec = SPEC_BAR[_dtype_name(in_dtype)]
+    bound = tight if tight is not None else TIGHT_FP32 + HALF_ULP.get(out_name, 0.0)
+    assert err <= spec, f"{label} normwise error {err:.3e} above the {spec:g} bar"
+    log = os.environ.get("DA_PARITY_LOG")
+    if log:
+        import json
+
+        with open(log, "a") as f:
+            f.write(json.dumps({"test": os.environ.get("PYTEST_CURRENT_TEST", ""), "label": label,
+                                "err": err, "bound": bound, "out": out_name}) + "\n")
+        return err
+    assert err <= bound, f"{label} normwise error {err:.3e} above the tight bound {bound:.1e}"
+    return err

@@ -4,7 +4,11 @@ backward gives dW_i = [weight.grad | bias.grad]; the captured block must equal
 P_out^T dW_i P_in (projected, with the session's own matrices: seed for the
 gradient side, seed + 1 for the activation side), or dW_i itself (unprojected).
 
-Bar: normwise relative error <= 1e-2 for bf16 models, <= 1e-3 for fp32."""
+Bars (conftest.assert_parity): normwise relative error <= 1e-2 for bf16
+models, <= 1e-3 for fp32.  The tight bound applies to fp32 models only: a bf16
+model's own forward and backward round every capture, so its per-sample
+gradients differ from the float64 autograd reference by the bf16 rounding of
+the whole network, which the spec bar covers."""
 
 from __future__ import annotations
 
@@ -13,11 +17,14 @@ import pytest
 import torch
 from torch import nn
 
-from conftest import rel_err
+from conftest import assert_parity
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.bfloat16: 1e-2, torch.float32: 1e-3}
+
+def _tight(dtype):
+    return None if dtype == torch.float32 else 1e-2
+
 B, T, D_IN, D_HID, D_OUT = 6, 40, 64, 96, 48
 
 
@@ -84,7 +91,7 @@ def test_projected_capture_matches_autograd(device, dtype, style):
             assert grad.representation[name] == "materialized"
             got = got.double().cpu().numpy()
         assert got.shape == want.shape
-        assert rel_err(got, want) <= TOL[dtype], name
+        assert_parity(got, want, dtype, tight=_tight(dtype), label=name)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -103,10 +110,10 @@ def test_unprojected_capture_and_input_gradient(device, dtype):
     with FusedCapture(model, capture_style="materialized") as cap:
         _loss(model, xc, w).backward()
     # backprop through the captured layers is unchanged (same input-gradient product)
-    assert rel_err(xc.grad.double().cpu().numpy(), plain_dx.double().cpu().numpy()) <= TOL[dtype] / 10
+    assert_parity(xc.grad, plain_dx, dtype, tight=_tight(dtype) and 1e-3, label="input gradient")
     grad = cap.gradient()
-    assert rel_err(grad.data["0"].double().cpu().numpy(), ref["0"].reshape(B, -1)) <= TOL[dtype]
-    assert rel_err(grad.data["2"].double().cpu().numpy(), ref["2"].reshape(B, -1)) <= TOL[dtype]
+    assert_parity(grad.data["0"], ref["0"].reshape(B, -1), dtype, tight=_tight(dtype))
+    assert_parity(grad.data["2"], ref["2"].reshape(B, -1), dtype, tight=_tight(dtype))
 
     with FusedCapture(model, ["0"], capture_style="factorized") as cap2:
         _loss(model, x, w).backward()
@@ -115,7 +122,7 @@ def test_unprojected_capture_and_input_gradient(device, dtype):
     from dattri_llm_amd.gradient import ops
 
     dense = ops.materialize(f, "nn.Linear")
-    assert rel_err(dense.double().cpu().numpy(), ref["0"].reshape(B, -1)) <= TOL[dtype]
+    assert_parity(dense, ref["0"].reshape(B, -1), dtype, tight=_tight(dtype))
     assert model[2].weight.grad is not None  # an uncaptured layer keeps its ordinary gradient
 
 
@@ -134,7 +141,7 @@ def test_micro_batches_concatenate_and_clear(device):
     assert grad.representation["0"] == "materialized" and grad.data["0"].shape == (B, 64)
     p_in, p_out = _mats(cap, "0", D_IN + 1, D_HID, 8, torch.float32, device)
     want = np.einsum("od,bok,ki->bdi", p_out, ref["0"], p_in).reshape(B, -1)
-    assert rel_err(grad.data["0"].double().cpu().numpy(), want) <= 1e-3
+    assert_parity(grad.data["0"], want, torch.float32)
     cap.clear()
     with pytest.raises(RuntimeError, match="no layer has been captured"):
         cap.gradient()

@@ -1,0 +1,193 @@
+"""Parity at the Llama-3-8B block's own shapes (the headline workload).
+
+Every layer at full width -- q/k/v/o 4096 -> 4096/1024/1024/4096, gate/up
+4096 -> 14336, down 14336 -> 4096, two RMSNorm(4096) -- captured as the
+reference's hooks hold them (raw factors, module kwargs), scored through the
+drop-in path: TracInAttributor's query routing (the reference's
+_route_test_rep) and ops.layerwise_cross_dot.
+
+* 2 train sequences x 2048 tokens against 4 queries x 512 tokens on both
+  routes: the materialized route (k-blocked dW of all 7 linears, the norm
+  kernel, one 9-layer score-ring launch over 218 M weights per sample) and
+  the factorized one (the ghost kernel at S1 = 2048, S2 = 512).
+* The headline's own query block, 64 queries x 512 tokens, which the cost
+  rule densifies layer by layer (gate/up/down are 7.5 GB each in bf16): sampled
+  dense rows against the oracle's materialization, and sampled score columns
+  of a train block against it.
+
+The oracle runs in float64, one layer at a time, from the same bf16 inputs
+copied off the device."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_parity, roundings
+
+pytestmark = pytest.mark.gpu
+
+D, D_KV, D_FFN = 4096, 1024, 14336
+# (layer, activation factor, d_in, d_out)
+LINEARS = [
+    ("q_proj", "attn_in", D, D),
+    ("k_proj", "attn_in", D, D_KV),
+    ("v_proj", "attn_in", D, D_KV),
+    ("o_proj", "o_in", D, D),
+    ("gate_proj", "mlp_in", D, D_FFN),
+    ("up_proj", "mlp_in", D, D_FFN),
+    ("down_proj", "down_in", D_FFN, D),
+]
+NORMS = ["input_layernorm", "post_attention_layernorm"]
+ACT = {"attn_in": D, "o_in": D, "mlp_in": D, "down_in": D_FFN}
+EPS = 1e-5
+NAMES = [n for n, *_ in LINEARS] + NORMS
+
+
+def _block(batch, tokens, seed, device):
+    """Synthetic bf16 captures of the block, drawn on the device: shared input
+    activations, one output gradient per linear, norm inputs and gradients."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def rnd(*shape, scale=1.0):
+        x = torch.empty(*shape, device=device)
+        x.normal_(0.0, scale, generator=gen)
+        return x.to(torch.bfloat16)
+
+    acts = {k: rnd(batch, tokens, w) for k, w in ACT.items()}
+    grads = {n: rnd(batch, tokens, dout, scale=dout**-0.5) for n, _a, _i, dout in LINEARS}
+    norms = {n: (rnd(batch, tokens, D), rnd(batch, tokens, D, scale=D**-0.5)) for n in NORMS}
+    return acts, grads, norms
+
+
+def _gradient(acts, grads, norms):
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    data, types = {}, {}
+    for n, act, _i, _o in LINEARS:
+        data[n] = Factorized(acts[act], grads[n], module_kwargs={"has_bias": False})
+        types[n] = "nn.Linear"
+    for n in NORMS:
+        x, g = norms[n]
+        data[n] = Factorized(x, g, module_kwargs={"has_bias": False, "eps": EPS, "normalized_shape": (D,)})
+        types[n] = "nn.RMSNorm"
+    return Gradient(dict.fromkeys(data, "factorized"), data, types, dict.fromkeys(data, "batch_token"))
+
+
+def _f64(x, rows=None):
+    x = x if rows is None else x[rows]
+    return x.double().cpu().numpy()
+
+
+def _oracle_dense(acts, grads, norms, name, rows=None):
+    """float64 per-sample dense gradient of one layer, (B, width)."""
+    if name in NORMS:
+        x, g = norms[name]
+        return oracle.norm_weight_grad(_f64(x, rows), _f64(g, rows), "nn.RMSNorm", EPS)
+    act = next(a for n, a, _i, _o in LINEARS if n == name)
+    return oracle.materialize_linear(_f64(acts[act], rows), _f64(grads[name], rows))
+
+
+def _oracle_scores(train, test, train_rows=None, test_rows=None):
+    total = 0.0
+    for name in NAMES:
+        m1 = _oracle_dense(*train, name, train_rows)
+        m2 = _oracle_dense(*test, name, test_rows)
+        total = total + m1 @ m2.T
+        del m1, m2
+    return total
+
+
+@pytest.fixture
+def pinned_route(monkeypatch):
+    """The reference's pin_route: the cost rule patched in the ops namespace
+    and in the dot module, which cross_gram looks it up through."""
+    import importlib
+
+    from dattri_llm_amd.gradient import ops
+
+    dot = importlib.import_module("dattri_llm_amd.gradient.ops.dot")  # the module, not ops.dot the function
+
+    def pin(route):
+        fn = lambda *a, **k: route == "materialized"  # noqa: E731
+        monkeypatch.setattr(ops, "maybe_use_materialized_gram", fn)
+        monkeypatch.setattr(dot, "maybe_use_materialized_gram", fn)
+
+    return pin
+
+
+@pytest.mark.parametrize("route", ["materialized", "factorized"])
+def test_block_scores_on_both_routes(device, pinned_route, route):
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.attribution import TracInAttributor
+
+    print(f"llama8b block 2x2048 vs 4x512, route={route}", flush=True)
+    train = _block(2, 2048, seed=10, device=device)
+    test = _block(4, 512, seed=11, device=device)
+    want = _oracle_scores(train, test)
+    pinned_route(route)
+    attr = TracInAttributor(train_batch_size=2, device=device)
+    routed = attr.route_test_rep(_gradient(*test))
+    dense = [n for n, v in routed.data.items() if isinstance(v, torch.Tensor)]
+    if route == "materialized":
+        assert sorted(dense) == sorted([n for n, *_ in LINEARS] + NORMS)
+        assert all(kernels.is_blocked(routed.data[n]) for n, *_ in LINEARS)
+    else:
+        assert sorted(dense) == sorted(NORMS)  # norm layers are always scored dense
+    got = attr.inner_product(_gradient(*train), routed)
+    torch.cuda.synchronize()
+    assert got.shape == (2, 4) and got.dtype == torch.bfloat16
+    # bf16 inputs give a bf16 score (the reference's "auto" dtype policy): one
+    # rounding of the output; the materialized route also stores both sides'
+    # dense gradients in bf16 (one rounding each, as the reference does)
+    tight = roundings(3) if route == "materialized" else roundings(1)
+    assert_parity(got, want, torch.bfloat16, tight=tight, label=route)
+
+
+def test_headline_query_block_rows_and_scores(device):
+    """The 64 x 512-token query block routed as the headline routes it (the
+    unpinned cost rule with 8-sample train blocks densifies all 9 layers),
+    scored against a 2 x 2048 train block.  Checked in three parts: sampled
+    dense query rows against the oracle's materialization; the 9-layer score
+    ring (fp32) against float64 products of the very bf16 dense rows it read;
+    and the drop-in score, which must be that ring result rounded to bf16."""
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.attribution import TracInAttributor
+    from dattri_llm_amd.gradient.ops.materialize import materialize_blocked
+
+    print("llama8b headline query block 64x512 (dense gate/up/down 7.5 GB each)", flush=True)
+    test = _block(64, 512, seed=21, device=device)
+    attr = TracInAttributor(train_batch_size=8, device=device)
+    routed = attr.route_test_rep(_gradient(*test))
+    assert all(isinstance(routed.data[n], torch.Tensor) for n in routed.data)
+    gate = routed.data["gate_proj"]
+    assert kernels.is_blocked(gate) and gate.numel() * gate.element_size() > 4 * 2**30
+    rows = [0, 37, 63]
+
+    def sample_rows(m, which):
+        return torch.stack([m[r].reshape(-1) for r in which])
+
+    for name in ["gate_proj", "down_proj", "k_proj", "input_layernorm"]:
+        got = sample_rows(routed.data[name], rows)
+        assert_parity(got, _oracle_dense(*test, name, rows), torch.bfloat16, label=name)
+
+    train = _block(2, 2048, seed=22, device=device)
+    train_rep = _gradient(*train)
+    tr_dense = {n: materialize_blocked(train_rep.data[n], train_rep.layer_types[n]) for n in NAMES}
+    ring = kernels.score_gemm([(tr_dense[n], routed.data[n]) for n in NAMES])
+    torch.cuda.synchronize()
+    assert ring.shape == (2, 64) and ring.dtype == torch.float32
+    want_ring = 0.0
+    for n in NAMES:
+        m1 = sample_rows(tr_dense[n], [0, 1]).double().cpu().numpy()
+        m2 = sample_rows(routed.data[n], rows).double().cpu().numpy()
+        want_ring = want_ring + m1 @ m2.T
+    assert_parity(ring[:, rows], want_ring, torch.bfloat16, label="score ring, 9 layers x 218M")
+
+    scores = attr.inner_product(train_rep, routed)
+    torch.cuda.synchronize()
+    assert scores.dtype == torch.bfloat16 and torch.equal(scores, ring.to(torch.bfloat16))
+    want = _oracle_scores(train, test, test_rows=rows)
+    assert_parity(scores[:, rows], want, torch.bfloat16, tight=roundings(3), label="end to end")

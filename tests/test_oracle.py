@@ -190,6 +190,46 @@ def test_norm_weight_grad_against_autograd(layer_type):
     np.testing.assert_allclose(got, np.stack(rows), rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("layer_type,has_bias", [("nn.LayerNorm", True), ("nn.LayerNorm", False),
+                                                   ("nn.RMSNorm", False), ("nn.Linear", True), ("nn.Linear", False)])
+def test_preprocess_against_autograd(layer_type, has_bias):
+    """preprocess_factors' final factors give the per-sample parameter gradient
+    autograd computes: norms by the token sum of a * g ([dgamma, dbeta] with a
+    bias), linear layers by sum_t g_t a_t^T (the ones column is the bias)."""
+    torch.manual_seed(11)
+    b, t, d_in, d_out = 3, 5, 8, 6
+    d = d_in
+    x = torch.randn(b, t, d, dtype=torch.float64) + 0.5
+    if layer_type == "nn.Linear":
+        mod = torch.nn.Linear(d_in, d_out, bias=has_bias).double()
+        c = torch.randn(b, t, d_out, dtype=torch.float64)
+    elif layer_type == "nn.LayerNorm":
+        mod = torch.nn.LayerNorm(d, eps=1e-5, elementwise_affine=True, bias=has_bias).double()
+        c = torch.randn(b, t, d, dtype=torch.float64)
+    else:
+        mod = torch.nn.RMSNorm(d, eps=1e-5).double()
+        c = torch.randn(b, t, d, dtype=torch.float64)
+    want = []
+    for i in range(b):
+        mod.zero_grad()
+        (mod(x[i]) * c[i]).sum().backward()
+        if layer_type == "nn.Linear":
+            parts = [mod.weight.grad.clone()] + ([mod.bias.grad[:, None].clone()] if has_bias else [])
+            want.append(torch.cat(parts, 1).flatten().numpy())
+        else:
+            parts = [mod.weight.grad.clone()] + ([mod.bias.grad.clone()] if has_bias else [])
+            want.append(torch.cat(parts).numpy())
+    a, g = oracle.preprocess(x.numpy(), c.numpy(), layer_type, {"eps": 1e-5, "has_bias": has_bias})
+    if layer_type == "nn.Linear":
+        got = np.einsum("bto,bti->boi", g, a).reshape(b, -1)
+    else:
+        got = (a * g).sum(1)
+    np.testing.assert_allclose(got, np.stack(want), rtol=1e-10, atol=1e-12)
+    # without module kwargs the factors are already final and pass through
+    a0, g0 = oracle.preprocess(x.numpy(), c.numpy(), layer_type, None)
+    assert a0 is not None and np.array_equal(a0, x.numpy()) and np.array_equal(g0, c.numpy())
+
+
 # ---------------------------------------------------------------------------
 # projection
 # ---------------------------------------------------------------------------
@@ -244,6 +284,43 @@ def test_cost_rules_known_answers():
         oracle.should_materialize("bogus", 4, 8, 8)
 
 
+def test_norm_rule_crossover_known_answers():
+    """Per-sample norms: materialize iff S >= H = D*K / (D + K), the crossover
+    where the ghost's S^2 (D + K) flops meet the dW's S*D*K.  Known answers
+    on both sides of H, at H exactly (materialize), and at the Llama-8B block's
+    train (S = 2048) and query (S = 512) widths."""
+    cases = [
+        ((32, 64, 64), True),       # H = 32
+        ((31, 64, 64), False),
+        ((2048, 4096, 4096), True),  # H = 2048: attention q/o at the train length
+        ((2047, 4096, 4096), False),
+        ((2048, 4096, 1024), True),  # k/v: H = 819.2
+        ((819, 4096, 1024), False),
+        ((820, 4096, 1024), True),
+        ((2048, 4096, 14336), False),  # gate/up: H = 3185.8
+        ((2048, 14336, 4096), False),  # down
+        ((3186, 4096, 14336), True),
+        ((3185, 4096, 14336), False),
+        ((512, 4096, 4096), False),  # every query-length layer stays factorized
+        ((1, 1, 1), True),  # H = 1/2
+        ((0, 8, 8), False),
+    ]
+    for (s, k, d), want in cases:
+        assert oracle.maybe_use_materialized_norm(s, k, d) is want, (s, k, d)
+        assert oracle.maybe_use_materialized_norm(s, d, k) is want  # symmetric in K and D
+
+
+def test_every_oracle_function_is_pinned():
+    """Each public oracle name is exercised by a pinning test in this file or
+    in tests/test_topk_select.py (constants by test_machine_eps_constants)."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    text = "".join(open(os.path.join(here, f)).read() for f in ("test_oracle.py", "test_topk_select.py"))
+    import oracle.ops
+
+    missing = [n for n in oracle.ops.__all__ if f"oracle.{n}" not in text]
+    assert not missing, missing
+
+
 def test_cost_rule_is_the_flop_comparison():
     """A route the rule calls cheaper really has fewer counted flops."""
     for b1, b2, s, k, d in [(8, 64, 2048, 4096, 14336), (256, 64, 512, 4096, 4096), (8, 1, 4, 8, 8)]:
@@ -275,6 +352,20 @@ def test_segments_match_torch_where_order():
         assert np.array_equal(segs[e][0], pos.numpy()) and np.array_equal(segs[e][1], tok.numpy())
 
 
+def test_regroup_scatters_rows_to_their_positions():
+    """RowLayout.regroup: routed row p lands at (token // T, token % T), every
+    other position stays zero."""
+    r = _rng(12)
+    rows = r.standard_normal((4, 3))
+    tok = np.array([5, 0, 11, 7])
+    got = oracle.moe_regroup_dense(rows, tok, 3, 4)
+    want = np.zeros((3, 4, 3))
+    for p in range(4):
+        want[tok[p] // 4, tok[p] % 4] = rows[p]
+    assert np.array_equal(got, want)
+    assert np.count_nonzero(got.any(-1)) == 4
+
+
 def test_segment_ghost_equals_dense_with_zeros_by_brute_force():
     r = _rng(10)
     batch, tokens = 3, 5
@@ -288,6 +379,27 @@ def test_segment_ghost_equals_dense_with_zeros_by_brute_force():
         for q in range(3):
             want[tok1[p] // tokens, tok2[q] // tokens] += float(a1[p] @ a2[q]) * float(g1[p] @ g2[q])
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_compact_segment_ghost_equals_dense_with_zeros(bias):
+    r = _rng(13)
+    b1, b2, t1, t2 = 4, 3, 9, 7
+    cases = [(np.array([0, 5, 8, 13, 30, 35]), np.array([2, 3, 9, 20])),  # ragged samples
+             (np.array([], dtype=np.int64), np.array([1, 4])),             # empty side
+             (np.array([10, 11, 12]), np.array([0, 6]))]                   # one sample per side
+    for tok1, tok2 in cases:
+        a1, g1 = r.standard_normal((len(tok1), 5)), r.standard_normal((len(tok1), 6))
+        a2, g2 = r.standard_normal((len(tok2), 5)), r.standard_normal((len(tok2), 6))
+        want = oracle.moe_segment_ghost(a1, g1, tok1, a2, g2, tok2, b1, b2, t1, t2, bias=bias)
+        got = oracle.moe_segment_ghost_compact(a1, g1, tok1, a2, g2, tok2, b1, b2, t1, t2, bias=bias)
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+        brute = np.zeros((b1, b2))
+        for p in range(len(tok1)):
+            for q in range(len(tok2)):
+                ka = float(a1[p] @ a2[q]) + (1.0 if bias else 0.0)
+                brute[tok1[p] // t1, tok2[q] // t2] += ka * float(g1[p] @ g2[q])
+        np.testing.assert_allclose(got, brute, rtol=1e-12, atol=1e-12)
 
 
 # ---------------------------------------------------------------------------
