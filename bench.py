@@ -5,18 +5,21 @@ Default workload (the headline metric): a Llama-3-8B-shaped decoder block
 (d 4096, 32 q / 8 kv heads -> q/k/v/o 4096->4096/1024/1024/4096, SwiGLU FFN
 14336, two RMSNorm(4096)), bf16, with the factors its 7 linears and 2 norms
 capture for 8 train sequences x 2048 tokens and 64 query sequences x 512
-tokens.  The reference's cost rule routes every layer of this block to the
-materialized form, so -- as in dattri-llm's scoring loop (the query block is
-routed to dense once, then every train block is materialized and scored
-against it) -- one step is one train block:
+tokens.  A step is one train block through the drop-in scoring path, as
+dattri-llm's attribute loop runs it: TracInAttributor.attribute_sources ->
+score_sources -> inner_product -> ops.layerwise_cross_dot.  The reference's
+cost rule routes every layer of this block to the materialized form, so the
+kernels a step launches are
 
     RMSNorm per-sample weight grads  (norm kernel, x2)
     per-sample dW of the 7 linears   (materialize kernel, x7)
     one multi-layer score GEMM       (score kernel: 9 layers, 8 x 64)
 
-Inputs are synthetic (seeded on the device) and already resident in HBM; the
-query-side preparation (64 queries materialized once) runs before the timed
-region and is reported as ``query_prep_ms``.
+and the block's (8, 64) scores are copied to pinned host memory.  Inputs are
+synthetic (seeded on the device) and already resident in HBM; the query block
+is routed to dense once (route_test_rep), before the timed region, and
+reported as ``query_prep_ms``.  The same step issued as raw kernel calls is
+timed beside it (``kernels_only_ms``, ``boundary_overhead``).
 
 Prints ONE JSON line.  Other workloads (not the headline):
 ``--workload ghost``   the fused ghost cross-gram, 256 train x 64 query, T=512, d 4096;
@@ -212,79 +215,126 @@ def blas_threads() -> int:
 # ---------------------------------------------------------------------------
 
 
+def block_gradient(acts, grads, norms):
+    """The block's captures as the reference's hooks hold them: a Gradient of
+    raw factorized layers (module kwargs kept, preprocessing left to the ops)."""
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    data, types = {}, {}
+    for name, act, _din, _dout in LINEARS:
+        data[name] = Factorized(acts[act], grads[name], module_kwargs={"has_bias": False})
+        types[name] = "nn.Linear"
+    for name, d in NORMS:
+        x, g = norms[name]
+        data[name] = Factorized(x, g, module_kwargs={"has_bias": False, "eps": RMS_EPS, "normalized_shape": (d,)})
+        types[name] = "nn.RMSNorm"
+    return Gradient(dict.fromkeys(data, "factorized"), data, types, dict.fromkeys(data, "batch_token"))
+
+
 def bench_block(args):
+    """One step = one train block through the drop-in scoring path, as the
+    reference's attribute loop runs it: TracInAttributor.attribute_sources over
+    a source of train blocks (score_sources -> inner_product ->
+    ops.layerwise_cross_dot, the cost rule routing every layer, the block's
+    scores copied to pinned host memory).  The query block is routed once
+    (route_test_rep), before the timed region.  The same step issued as raw
+    kernel calls is timed beside it (kernels_only_ms)."""
     import torch
 
     from dattri_llm_amd import kernels
+    from dattri_llm_amd.attribution import TracInAttributor
 
     n_train, t_train, n_query, t_query = 8, 2048, 64, 512
-    acts, grads, norms = make_block(n_train, t_train, seed=0)
-    q_acts, q_grads, q_norms = make_block(n_query, t_query, seed=1)
+    train_fac = make_block(n_train, t_train, seed=0)
+    query_fac = make_block(n_query, t_query, seed=1)
+    train = block_gradient(*train_fac)
+    attr = TracInAttributor(train_batch_size=n_train, device="cuda")
     torch.cuda.synchronize()
 
     t0 = time.perf_counter()
-    q_dense = dense_block(q_acts, q_grads, q_norms)
+    routed = attr.route_test_rep(block_gradient(*query_fac))
     torch.cuda.synchronize()
     query_prep_ms = (time.perf_counter() - t0) * 1e3
-    del q_acts, q_grads, q_norms
-    names = [n for n, _ in NORMS] + [n for n, *_ in LINEARS]
-    scores = torch.empty(n_train, n_query, dtype=torch.float32, device="cuda")
+    routes = {n: ("dense" if isinstance(v, torch.Tensor) else "factorized") for n, v in routed.data.items()}
+    train_ids = [f"train{i}" for i in range(n_train)]
+    test_source = [(0, routed, [f"query{j}" for j in range(n_query)])]
 
-    def step(timers=None):
-        tr = dense_block(acts, grads, norms, timers)
-        ev = _ev(timers, "score_gemm")
-        kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=scores)
-        _ev_end(ev)
-        return scores
+    def attribute(k):
+        return attr.attribute_sources(((step, train, train_ids) for step in range(k)), test_source)
+
+    attribute(args.warmup)
+    torch.cuda.synchronize()
+    with kernels.launch_events() as log:
+        t0 = time.perf_counter()
+        score = attribute(args.steps)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    assert score.scores.shape == (n_train * args.steps, n_query)
+
+    def event_ms(name):
+        return sum(s.elapsed_time(e) for s, e in log.get(name, [])) / args.steps, len(log.get(name, [])) // args.steps
+
+    # The same step as raw kernel calls (no boundary): dW of the 7 linears, 2 norm grads, one score GEMM.
+    q_dense = {n: routed.data[n] for n in routed.data}
+    names = list(train.data)  # the order layerwise_cross_dot sums the layers in
+    raw_scores = torch.empty(n_train, n_query, dtype=torch.float32, device="cuda")
+
+    def raw_step():
+        tr = dense_block(*train_fac)
+        kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=raw_scores)
 
     for _ in range(args.warmup):
-        step()
+        raw_step()
     torch.cuda.synchronize()
-    timers: dict = {}
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(timers)
+        raw_step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    raw_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # the drop-in scores are the raw ones rounded to the compute dtype (bf16)
+    same = bool(torch.equal(score.scores[-n_train:], raw_scores.to(torch.bfloat16).float().cpu()))
 
     # Algorithmic work.
     dk = {n: din * dout for n, _a, din, dout in LINEARS}
     width = sum(dk.values()) + sum(d for _, d in NORMS)
-    mat_flops = {n: 2.0 * n_train * t_train * v for n, v in dk.items()}
+    mat_flops = sum(2.0 * n_train * t_train * v for v in dk.values())
     score_bytes = (n_train + n_query) * width * 2.0
-    kern = {}
-    for n, *_ in LINEARS:
-        t = _mean_ms(timers, f"materialize:{n}")
-        kern[f"materialize:{n}"] = {"ms": round(t, 4), "tflops": round(mat_flops[n] / t / 1e9, 1)}
-    t_score = _mean_ms(timers, "score_gemm")
-    kern["score_gemm"] = {"ms": round(t_score, 4), "gbs": round(score_bytes / t_score / 1e6, 1)}
-    t_norm = _mean_ms(timers, "norm_weight_grad")
     norm_bytes = 2.0 * n_train * t_train * D_MODEL * 2
-    kern["norm_weight_grad"] = {"ms": round(t_norm, 4), "gbs": round(norm_bytes / t_norm / 1e6, 1)}
-    t_mat = sum(_mean_ms(timers, f"materialize:{n}") for n, *_ in LINEARS)
-    mfma_util = sum(mat_flops.values()) / (t_mat * 1e9) / PEAK_BF16_TFLOPS
+    t_mat, n_mat = event_ms("materialize_linear")
+    t_score, n_score = event_ms("score_gemm")
+    t_norm, n_norm = event_ms("norm_weight_grad")
+    kern = {
+        "materialize_linear": {"ms_per_step": round(t_mat, 4), "launches_per_step": n_mat,
+                               "tflops": round(mat_flops / t_mat / 1e9, 1)},
+        "score_gemm": {"ms_per_step": round(t_score, 4), "launches_per_step": n_score,
+                       "gbs": round(score_bytes / t_score / 1e6, 1)},
+        "norm_weight_grad": {"ms_per_step": round(t_norm, 4), "launches_per_step": n_norm,
+                             "gbs": round(2 * norm_bytes / t_norm / 1e6, 1)},
+    }
+    mfma_util = mat_flops / (t_mat * 1e9) / PEAK_BF16_TFLOPS
 
     # Dominant kernel: the one taking most of the step (summed over its launches).
-    # Its roofline uses the step's algorithmic work over the summed event time,
+    # Its roofline is the step's algorithmic work over the summed event time,
     # i.e. per-launch work over the average launch duration.
-    totals = {"materialize_tiles_tr": t_mat, "score_ring": t_score, "norm_grad_chunks": 2 * t_norm}
+    totals = {"materialize_tiles_tr": t_mat, "score_ring": t_score, "norm_grad_chunks": t_norm}
     big = max(totals, key=totals.get)
     if big == "score_ring":
         gbs = score_bytes / t_score / 1e6
         roof = {"bound": "hbm", "kernel": big, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                "work_per_launch": f"{score_bytes:.4g} B (72 rows x {width} weights x 2 B)", "launches_per_step": 1}
+                "work_per_launch": f"{score_bytes:.4g} B (72 rows x {width} weights x 2 B)",
+                "launches_per_step": n_score}
     elif big == "materialize_tiles_tr":
-        tf = sum(mat_flops.values()) / (t_mat * 1e9)
+        tf = mat_flops / (t_mat * 1e9)
         roof = {"bound": "mfma", "kernel": big, "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                "work_per_launch": f"{sum(mat_flops.values()) / 7:.4g} flop average over the 7 linears "
+                "work_per_launch": f"{mat_flops / max(n_mat, 1):.4g} flop average over the 7 linears "
                                    "(2 x 8 samples x 2048 tokens x d_in x d_out each)",
-                "launches_per_step": 7}
+                "launches_per_step": n_mat}
     else:
-        gbs = norm_bytes / t_norm / 1e6
+        gbs = 2 * norm_bytes / t_norm / 1e6
         roof = {"bound": "hbm", "kernel": big, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "launches_per_step": 2}
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "launches_per_step": n_norm}
     roof["step_share"] = round(totals[big] / ms, 3)
     roof["traffic"] = profiled_traffic(big)
     if roof["traffic"] is not None:
@@ -305,41 +355,45 @@ def bench_block(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "llama3-8b-block: 8 train x 2048 tok vs 64 query x 512 tok, "
-                        "7 linears + 2 RMSNorm, materialized route",
+            "workload": "llama3-8b-block: 8 train x 2048 tok vs 64 query x 512 tok, 7 linears + 2 RMSNorm, "
+                        "TracInAttributor.attribute_sources (cost-rule routing per layer)",
             "train_block": [n_train, t_train],
             "query_block": [n_query, t_query],
             "score_width_per_sample": width,
+            "routes": routes,
         },
         "mfma_util": round(mfma_util, 4),
         "query_prep_ms": round(query_prep_ms, 2),
+        "kernels_only_ms": round(raw_ms, 4),
+        "boundary_overhead": round(ms / raw_ms - 1.0, 4),
+        "dropin_equals_kernels": same,
         "roofline": roof,
         "kernels": kern,
     }
     if args.cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_block(n_query_total=n_query, n_train_total=n_train)
+        result["cpu_baseline"], result["parity"] = cpu_baseline_block(train_fac, query_fac, score.scores[-n_train:])
     return result
 
 
-def cpu_baseline_block(n_query_total: int, n_train_total: int):
-    """The oracle (numpy fp32) on a bounded sample of the same step: the full
-    8-sample train block (T=2048, all 9 layers) materialized and scored, as one
-    GEMM per layer like the reference's loop, against 16 of the 64 cached dense
-    queries; the score part is scaled to 64 queries (it streams the query
-    matrix, so its time is linear in the query count)."""
+def cpu_baseline_block(train_fac, query_fac, gpu_scores):
+    """The oracle (numpy fp32) on a bounded sample of the same step, from the
+    same bf16 inputs: the whole 8-sample train block (T=2048, all 9 layers)
+    materialized and scored, one GEMM per layer like the reference's loop,
+    against the first 16 of the 64 queries; the score part is scaled to 64
+    queries (it streams the query matrix, so its time is linear in the query
+    count).  The same sample gives the parity of the bench's own scores."""
     import numpy as np
 
     import oracle
 
-    rng = np.random.default_rng(0)
-    f32 = np.float32
+    nq = 16
 
-    def block(b, t):
-        acts = {k: rng.standard_normal((b, t, w), dtype=f32) for k, w in ACT_WIDTH.items()}
-        grads = {n: rng.standard_normal((b, t, dout), dtype=f32) * f32(dout**-0.5) for n, _a, _i, dout in LINEARS}
-        norms = {n: (rng.standard_normal((b, t, d), dtype=f32), rng.standard_normal((b, t, d), dtype=f32))
-                 for n, d in NORMS}
-        return acts, grads, norms
+    def host(fac, rows=None):
+        acts, grads, norms = fac
+        sel = (lambda x: x) if rows is None else (lambda x: x[:rows])
+        return ({k: sel(v).float().cpu().numpy() for k, v in acts.items()},
+                {k: sel(v).float().cpu().numpy() for k, v in grads.items()},
+                {k: (sel(x).float().cpu().numpy(), sel(g).float().cpu().numpy()) for k, (x, g) in norms.items()})
 
     def dense(acts, grads, norms):
         out = {}
@@ -349,31 +403,38 @@ def cpu_baseline_block(n_query_total: int, n_train_total: int):
             out[n] = oracle.materialize_linear(acts[a], grads[n])
         return out
 
-    nq = 16
-    q_dense = dense(*block(nq, 512))
-    tr = block(n_train_total, 2048)
+    q_dense = dense(*host(query_fac, nq))
+    tr = host(train_fac)
     names = list(q_dense)
+    n_train_total = tr[0]["attn_in"].shape[0]
+    n_query_total = query_fac[0]["attn_in"].shape[0]
     best_mat = best_score = float("inf")
+    want = None
     for _ in range(2):
         t0 = time.perf_counter()
         tr_dense = dense(*tr)
         best_mat = min(best_mat, time.perf_counter() - t0)
         t0 = time.perf_counter()
-        oracle.score_gemm([tr_dense[n] for n in names], [q_dense[n] for n in names])
+        want = oracle.score_gemm([tr_dense[n] for n in names], [q_dense[n] for n in names])
         best_score = min(best_score, time.perf_counter() - t0)
         del tr_dense
     step_s = best_mat + (n_query_total / nq) * best_score
     cores, model = cpu_info()
-    return {
+    got = gpu_scores[:, :nq].double().numpy()
+    err = float(np.abs(got - want).max() / np.abs(want).max())
+    baseline = {
         "value": round(n_train_total * n_query_total / step_s, 3),
         "unit": "pair-scores/s",
         "cores": blas_threads(),
         "kind": "port",
-        "sample": f"numpy fp32 oracle: the 8-sample train block (T=2048, 7 linears + 2 RMSNorm) "
-                  f"materialized ({best_mat:.2f} s) and scored vs 16 dense queries ({best_score:.2f} s), "
-                  f"best of 2; score time scaled x{n_query_total // nq} to 64 queries -> step "
-                  f"{step_s:.2f} s; host {model}, {cores} cores visible",
+        "sample": f"numpy fp32 oracle on the bench's own bf16 inputs: the 8-sample train block (T=2048, "
+                  f"7 linears + 2 RMSNorm) materialized ({best_mat:.2f} s) and scored vs 16 dense queries "
+                  f"({best_score:.2f} s), best of 2; score time scaled x{n_query_total // nq} to 64 queries -> "
+                  f"step {step_s:.2f} s; host {model}, {cores} cores visible",
     }
+    parity = {"normwise_rel_err": err, "bar": 1e-2, "ok": err <= 1e-2,
+              "sample": f"the last timed step's 8 x {nq} scores (bf16 results) against the fp32 oracle"}
+    return baseline, parity
 
 
 # ---------------------------------------------------------------------------

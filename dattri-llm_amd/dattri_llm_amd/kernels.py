@@ -9,11 +9,44 @@ current stream of the tensors' device.  No arithmetic happens here.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
 
 from dattri_llm_amd import _native as nat
+
+
+_launch_log: dict | None = None
+
+
+@contextlib.contextmanager
+def launch_events():
+    """While active, every kernel launch made through this module is bracketed
+    by HIP events on the stream it is launched on; yields ``{entry point:
+    [(start, end), ...]}``.  Used to time kernels inside a measured region
+    without changing what runs."""
+    global _launch_log  # noqa: PLW0603
+    prev, _launch_log = _launch_log, {}
+    try:
+        yield _launch_log
+    finally:
+        _launch_log = prev
+
+
+def _run(dev: torch.device, what: str, fn, *args) -> None:
+    """Call the C entry point ``fn(*args)`` (it enqueues work on ``dev``'s
+    current stream) and map its status to an exception."""
+    log = _launch_log
+    if log is None:
+        nat.check(fn(*args), what)
+        return
+    stream = torch.cuda.current_stream(dev)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    nat.check(fn(*args), what)
+    end.record(stream)
+    log.setdefault(what, []).append((start, end))
 
 
 def _chunk_elems(dtype: torch.dtype) -> int:
@@ -108,13 +141,9 @@ def ghost_gram(
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_ghost_gram_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)), "ghost_gram")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_ghost_gram(
-            s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate),
-            ws.data_ptr(), ws.numel(), nat.stream_ptr(dev),
-        ),
-        "ghost_gram",
-    )
+    _run(dev, "ghost_gram", lib.da_ghost_gram,
+         s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate), ws.data_ptr(), ws.numel(),
+         nat.stream_ptr(dev))
     return out
 
 
@@ -163,12 +192,9 @@ def ghost_gram_per_token(
     nat.check(lib.da_ghost_gram_per_token_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)),
               "ghost_gram_per_token")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_ghost_gram_per_token(s1, s2, k, d, code, out.data_ptr(), out.stride(0), out.stride(1),
-                                    out.stride(2), int(accumulate), ws.data_ptr(), ws.numel(),
-                                    nat.stream_ptr(dev)),
-        "ghost_gram_per_token",
-    )
+    _run(dev, "ghost_gram_per_token", lib.da_ghost_gram_per_token,
+         s1, s2, k, d, code, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
+         ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out
 
 
@@ -217,14 +243,11 @@ def dense_per_token(
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_dense_per_token_workspace(s1, b2, k, d, code, ctypes.byref(nbytes)), "dense_per_token")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_dense_per_token(s1, w.data_ptr(), b2, w.stride(0), w.stride(1),
-                               bias_grad.data_ptr() if bias_grad is not None else None,
-                               bias_grad.stride(0) if bias_grad is not None else 0, k, d, code,
-                               out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
-                               ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
-        "dense_per_token",
-    )
+    _run(dev, "dense_per_token", lib.da_dense_per_token,
+         s1, w.data_ptr(), b2, w.stride(0), w.stride(1),
+         bias_grad.data_ptr() if bias_grad is not None else None,
+         bias_grad.stride(0) if bias_grad is not None else 0, k, d, code, out.data_ptr(), out.stride(0),
+         out.stride(1), out.stride(2), int(accumulate), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out
 
 
@@ -287,11 +310,9 @@ def ghost_gram_grouped(groups1, groups2, *, bias=False, out: torch.Tensor | None
     nat.check(lib.da_ghost_gram_grouped_workspace(sides[0], sides[1], n, karr, darr, code, ctypes.byref(nbytes)),
               "ghost_gram_grouped")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_ghost_gram_grouped(sides[0], sides[1], n, karr, darr, code, out.data_ptr(), out.stride(0),
-                                  int(accumulate), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
-        "ghost_gram_grouped",
-    )
+    _run(dev, "ghost_gram_grouped", lib.da_ghost_gram_grouped,
+         sides[0], sides[1], n, karr, darr, code, out.data_ptr(), out.stride(0), int(accumulate),
+         ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     del keep
     return out
 
@@ -332,14 +353,10 @@ def materialize_linear(
     if blocked and not bias and k % 64 == 0 and d % _chunk_elems(a.dtype) == 0 and b > 0 and t > 0:
         out = blocked_storage(b, d * k, out_dtype, dev)
         a, g = prepare_rows(a, k), prepare_rows(g, d)
-        nat.check(
-            nat.load().da_materialize_linear(
-                a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d,
-                a.stride(0), a.stride(1), g.stride(0), g.stride(1), 0,
-                out.data_ptr(), nat.dtype_code(out_dtype), 64, k, b * 64, nat.stream_ptr(dev),
-            ),
-            "materialize_linear",
-        )
+        _run(dev, "materialize_linear", nat.load().da_materialize_linear,
+             a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d, a.stride(0), a.stride(1),
+             g.stride(0), g.stride(1), 0, out.data_ptr(), nat.dtype_code(out_dtype), 64, k, b * 64,
+             nat.stream_ptr(dev))
         return out
     out = torch.empty(b, d * kb, dtype=out_dtype, device=dev)
     if b == 0 or d == 0 or kb == 0:
@@ -358,14 +375,10 @@ def materialize_linear(
             out.view(b, d, kb)[:, :, k] = _column_sums(g, out_dtype)
         return out
     a, g = prepare_rows(a, k), prepare_rows(g, d)
-    nat.check(
-        nat.load().da_materialize_linear(
-            a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d,
-            a.stride(0), a.stride(1), g.stride(0), g.stride(1), int(bias),
-            out.data_ptr(), nat.dtype_code(out_dtype), d * kb, kb, 64, nat.stream_ptr(dev),
-        ),
-        "materialize_linear",
-    )
+    _run(dev, "materialize_linear", nat.load().da_materialize_linear,
+         a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d, a.stride(0), a.stride(1),
+         g.stride(0), g.stride(1), int(bias), out.data_ptr(), nat.dtype_code(out_dtype), d * kb, kb, 64,
+         nat.stream_ptr(dev))
     return out
 
 
@@ -402,12 +415,9 @@ def row_gram(x: torch.Tensor, *, out: torch.Tensor | None = None, accumulate: bo
     need = ctypes.c_size_t(0)
     nat.check(lib.da_row_gram_workspace(n, p, nat.dtype_code(xp.dtype), ctypes.byref(need)), "row_gram")
     ws = torch.empty(need.value, dtype=torch.uint8, device=dev) if need.value else None
-    nat.check(
-        lib.da_row_gram(xp.data_ptr(), nat.dtype_code(xp.dtype), n, p, xp.stride(0), out.data_ptr(),
-                        out.stride(0), int(accumulate), ws.data_ptr() if ws is not None else None,
-                        need.value, nat.stream_ptr(dev)),
-        "row_gram",
-    )
+    _run(dev, "row_gram", lib.da_row_gram,
+         xp.data_ptr(), nat.dtype_code(xp.dtype), n, p, xp.stride(0), out.data_ptr(), out.stride(0),
+         int(accumulate), ws.data_ptr() if ws is not None else None, need.value, nat.stream_ptr(dev))
     return out
 
 
@@ -424,8 +434,9 @@ def nonzero_rows(x: torch.Tensor) -> torch.Tensor:
     xp = prepare_rows(x)  # zero padding changes no row's answer
     if xp.stride(1) != 1:
         xp = xp.contiguous()
-    nat.check(nat.load().da_nonzero_rows(xp.data_ptr(), nat.dtype_code(xp.dtype), n, xp.shape[1], xp.stride(0),
-                                         out.data_ptr(), nat.stream_ptr(dev)), "nonzero_rows")
+    _run(dev, "nonzero_rows", nat.load().da_nonzero_rows,
+         xp.data_ptr(), nat.dtype_code(xp.dtype), n, xp.shape[1], xp.stride(0), out.data_ptr(),
+         nat.stream_ptr(dev))
     return out.view(torch.bool)
 
 
@@ -503,8 +514,9 @@ def score_gemm(
     lib = nat.load()
     code = nat.dtype_code(dtype)
     if not layers:  # every layer empty: the library writes the zero product (or leaves out to accumulate)
-        nat.check(lib.da_score_gemm(n1, n2, None, 0, code, out.data_ptr(), ld_row, ld_col, int(accumulate),
-                                    None, 0, nat.stream_ptr(dev)), "score_gemm")
+        _run(dev, "score_gemm", lib.da_score_gemm,
+             n1, n2, None, 0, code, out.data_ptr(), ld_row, ld_col, int(accumulate), None, 0,
+             nat.stream_ptr(dev))
         return out
     for start in range(0, len(layers), 32):
         group = layers[start : start + 32]
@@ -512,11 +524,9 @@ def score_gemm(
         nbytes = ctypes.c_size_t(0)
         nat.check(lib.da_score_gemm_workspace(n1, n2, arr, len(group), code, ctypes.byref(nbytes)), "score_gemm")
         ws = nat.workspace(nbytes.value, dev)
-        nat.check(
-            lib.da_score_gemm(n1, n2, arr, len(group), code, out.data_ptr(), ld_row, ld_col,
-                              int(accumulate or start > 0), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
-            "score_gemm",
-        )
+        _run(dev, "score_gemm", lib.da_score_gemm,
+             n1, n2, arr, len(group), code, out.data_ptr(), ld_row, ld_col, int(accumulate or start > 0),
+             ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     del keep
     return out
 
@@ -557,15 +567,10 @@ def norm_weight_grad(
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_norm_weight_grad_workspace(b, t, d, int(bias), ctypes.byref(nbytes)), "norm_weight_grad")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_norm_weight_grad(
-            x.data_ptr(), g.data_ptr(), nat.dtype_code(x.dtype), b, t, d,
-            x.stride(0), x.stride(1), g.stride(0), g.stride(1), int(kind), float(eps), int(bias),
-            out.data_ptr(), nat.dtype_code(out_dtype), width, ws.data_ptr(), ws.numel(),
-            nat.stream_ptr(dev),
-        ),
-        "norm_weight_grad",
-    )
+    _run(dev, "norm_weight_grad", lib.da_norm_weight_grad,
+         x.data_ptr(), g.data_ptr(), nat.dtype_code(x.dtype), b, t, d, x.stride(0), x.stride(1), g.stride(0),
+         g.stride(1), int(kind), float(eps), int(bias), out.data_ptr(), nat.dtype_code(out_dtype), width,
+         ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out
 
 
@@ -583,13 +588,9 @@ def norm_xhat(x: torch.Tensor, *, kind: int, eps: float, out_dtype: torch.dtype 
         flat = flat.contiguous()
         if d % _chunk_elems(x.dtype) or not _aligned(flat):
             raise NotImplementedError(f"norm_xhat: width {d} is not a multiple of {_chunk_elems(x.dtype)}")
-    nat.check(
-        nat.load().da_norm_xhat(
-            flat.data_ptr(), nat.dtype_code(x.dtype), rows, d, flat.stride(0), int(kind), float(eps),
-            out.data_ptr(), nat.dtype_code(out_dtype), d, nat.stream_ptr(dev),
-        ),
-        "norm_xhat",
-    )
+    _run(dev, "norm_xhat", nat.load().da_norm_xhat,
+         flat.data_ptr(), nat.dtype_code(x.dtype), rows, d, flat.stride(0), int(kind), float(eps),
+         out.data_ptr(), nat.dtype_code(out_dtype), d, nat.stream_ptr(dev))
     return out
 
 
@@ -630,14 +631,10 @@ def project_rows(x: torch.Tensor, pt: torch.Tensor, *, bias: torch.Tensor | None
         bias = bias.to(torch.float32).contiguous()
         if bias.numel() != k:
             raise ValueError("project_rows: bias must have k entries")
-    nat.check(
-        nat.load().da_project_rows(
-            flat.data_ptr(), nat.dtype_code(x.dtype), rows, dp, flat.stride(0), ptp.data_ptr(), k,
-            ptp.stride(0), bias.data_ptr() if bias is not None else None, out.data_ptr(),
-            nat.dtype_code(out_dtype), k, nat.stream_ptr(dev),
-        ),
-        "project_rows",
-    )
+    _run(dev, "project_rows", nat.load().da_project_rows,
+         flat.data_ptr(), nat.dtype_code(x.dtype), rows, dp, flat.stride(0), ptp.data_ptr(), k, ptp.stride(0),
+         bias.data_ptr() if bias is not None else None, out.data_ptr(), nat.dtype_code(out_dtype), k,
+         nat.stream_ptr(dev))
     return out
 
 
@@ -671,16 +668,11 @@ def project_outer(a: torch.Tensor, g: torch.Tensor, pin_t: torch.Tensor, pout_t:
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_project_outer_workspace(b, t, ka, kg, ctypes.byref(nbytes)), "project_outer")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_project_outer(
-            a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, kp, dp,
-            a.stride(0), a.stride(1), g.stride(0), g.stride(1),
-            pin_t.data_ptr(), ka, pin_t.stride(0), bias_in.data_ptr() if bias_in is not None else None,
-            pout_t.data_ptr(), kg, pout_t.stride(0), out.data_ptr(), nat.dtype_code(out_dtype), kg * ka,
-            ws.data_ptr(), ws.numel(), nat.stream_ptr(dev),
-        ),
-        "project_outer",
-    )
+    _run(dev, "project_outer", lib.da_project_outer,
+         a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, kp, dp, a.stride(0), a.stride(1),
+         g.stride(0), g.stride(1), pin_t.data_ptr(), ka, pin_t.stride(0),
+         bias_in.data_ptr() if bias_in is not None else None, pout_t.data_ptr(), kg, pout_t.stride(0),
+         out.data_ptr(), nat.dtype_code(out_dtype), kg * ka, ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out
 
 
@@ -694,11 +686,9 @@ def moe_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     n, e = logits.shape
     weights = torch.empty(n, k, dtype=torch.float32, device=dev)
     index = torch.empty(n, k, dtype=torch.int64, device=dev)
-    nat.check(
-        nat.load().da_moe_topk(logits.data_ptr(), nat.dtype_code(logits.dtype), n, e, k, logits.stride(0),
-                               weights.data_ptr(), index.data_ptr(), nat.stream_ptr(dev)),
-        "moe_topk",
-    )
+    _run(dev, "moe_topk", nat.load().da_moe_topk,
+         logits.data_ptr(), nat.dtype_code(logits.dtype), n, e, k, logits.stride(0), weights.data_ptr(),
+         index.data_ptr(), nat.stream_ptr(dev))
     return weights, index
 
 
@@ -724,11 +714,9 @@ def counting_sort(keys: torch.Tensor, bins: int, *, slot_major: bool = False,
     perm = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
     k32 = keys.data_ptr() if keys.dtype == torch.int32 else None
     k64 = keys.data_ptr() if keys.dtype == torch.int64 else None
-    nat.check(
-        nat.load().da_counting_sort(k32, k64, n, rows, k, int(slot_major), key_div, bins,
-                                    offsets.data_ptr(), perm.data_ptr(), nat.stream_ptr(dev)),
-        "counting_sort",
-    )
+    _run(dev, "counting_sort", nat.load().da_counting_sort,
+         k32, k64, n, rows, k, int(slot_major), key_div, bins, offsets.data_ptr(), perm.data_ptr(),
+         nat.stream_ptr(dev))
     return offsets, perm[:n]
 
 
@@ -745,11 +733,9 @@ def moe_route(index: torch.Tensor, n_experts: int, batch: int, tokens: int):
     entries = torch.empty(total, dtype=torch.int32, device=dev)
     seg = torch.empty(n_experts, batch + 1, dtype=torch.int32, device=dev)
     rows = torch.empty(total, dtype=torch.int32, device=dev)
-    nat.check(
-        nat.load().da_moe_route(index.data_ptr(), n, k, n_experts, batch, tokens, offsets.data_ptr(),
-                                entries.data_ptr(), seg.data_ptr(), rows.data_ptr(), nat.stream_ptr(dev)),
-        "moe_route",
-    )
+    _run(dev, "moe_route", nat.load().da_moe_route,
+         index.data_ptr(), n, k, n_experts, batch, tokens, offsets.data_ptr(), entries.data_ptr(),
+         seg.data_ptr(), rows.data_ptr(), nat.stream_ptr(dev))
     return offsets, entries[: n * k], seg, rows[: n * k]
 
 
@@ -781,9 +767,7 @@ def ghost_gram_segmented(a1, g1, seg1, idx1, tokens1, a2, g2, seg2, idx2, tokens
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_ghost_gram_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)), "ghost_gram_segmented")
     ws = nat.workspace(nbytes.value, dev)
-    nat.check(
-        lib.da_ghost_gram(s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate),
-                          ws.data_ptr(), ws.numel(), nat.stream_ptr(dev)),
-        "ghost_gram_segmented",
-    )
+    _run(dev, "ghost_gram_segmented", lib.da_ghost_gram,
+         s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate), ws.data_ptr(), ws.numel(),
+         nat.stream_ptr(dev))
     return out
