@@ -51,10 +51,20 @@ struct GhostArgs {
   SideDev s1, s2;
   int64_t kbytes_a, kbytes_g;  // K * esize, D * esize
   int64_t tiles_r, tiles_c;    // tiles per sample on each side
-  int64_t n_r, n_c;            // total row / column tiles
+  int64_t n_r, n_c;            // total row / column tiles (diag: n_c = tiles_c)
   float bias;
-  float* partial;              // [B1][B2][tiles_r][tiles_c]
+  int diag;                    // only the pairs (i, i): sample i of side 1 with sample i of side 2
+  float* partial;              // [B1][B2][tiles_r][tiles_c], diag: [B][tiles_r][tiles_c]
 };
+
+// Sample of side 2 for column tile C of row sample i, and the pair's slot in
+// the partials.
+__device__ __forceinline__ int64_t pair_col_sample(const GhostArgs& g, int64_t i, int64_t C) {
+  return g.diag ? i : C / g.tiles_c;
+}
+__device__ __forceinline__ int64_t pair_slot(const GhostArgs& g, int64_t i, int64_t j) {
+  return g.diag ? i : i * g.s2.batch + j;
+}
 
 __device__ __forceinline__ int64_t seg_start(const SideDev& s, int64_t b) {
   return s.seg ? (int64_t)s.seg[b] : 0;
@@ -146,14 +156,14 @@ __global__ __launch_bounds__(kThreads, 2) void ghost_gram_tiles(GhostArgs g) {
   const int64_t R = first_r + in_group % gsize;
   const int64_t C = in_group / gsize;
   const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
-  const int64_t j = C / g.tiles_c, ss = C % g.tiles_c;
+  const int64_t j = pair_col_sample(g, i, C), ss = C % g.tiles_c;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
   const int64_t len1 = seg_len(g.s1, i), len2 = seg_len(g.s2, j);
   const int64_t t0 = tt * kBM, s0 = ss * kBN;
-  float* dst = g.partial + ((i * g.s2.batch + j) * g.tiles_r + tt) * g.tiles_c + ss;
+  float* dst = g.partial + (pair_slot(g, i, j) * g.tiles_r + tt) * g.tiles_c + ss;
   if (t0 >= len1 || s0 >= len2) {  // tile entirely past a segment end: contributes 0
     if (tid == 0) *dst = 0.f;
     return;
@@ -708,12 +718,12 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
   const int64_t R = first_r + in_group % gsize;
   const int64_t C = in_group / gsize;
   const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
-  const int64_t j = C / g.tiles_c, ss = C % g.tiles_c;
+  const int64_t j = pair_col_sample(g, i, C), ss = C % g.tiles_c;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   const int64_t len1 = seg_len(g.s1, i), len2 = seg_len(g.s2, j);
   const int64_t t0 = tt * v2::kBM, s0 = ss * v2::kBN;
-  float* dst = g.partial + ((i * g.s2.batch + j) * g.tiles_r + tt) * g.tiles_c + ss;
+  float* dst = g.partial + (pair_slot(g, i, j) * g.tiles_r + tt) * g.tiles_c + ss;
   if (t0 >= len1 || s0 >= len2) {
     if (tid == 0) *dst = 0.f;
     return;
@@ -913,7 +923,7 @@ int validate_side(const da_factor_side* s, int64_t K, int64_t D, int dtype, cons
 }
 
 int make_plan(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D, int dtype,
-              Plan* plan) {
+              Plan* plan, bool diag = false) {
   if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "da_ghost_gram: bad dtype %d", dtype);
   if (K < 0 || D < 0) return set_error(DA_ERR_INVALID, "da_ghost_gram: negative width");
   const int64_t es = (int64_t)elem_bytes(dtype);
@@ -931,10 +941,13 @@ int make_plan(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int
   const int64_t bm = plan->v2 ? v2::kBM : kBM, bn = plan->v2 ? v2::kBN : kBN;
   plan->tiles_r = (s1->tokens + bm - 1) / bm;
   plan->tiles_c = (s2->tokens + bn - 1) / bn;
+  if (diag && s1->batch != s2->batch)
+    return set_error(DA_ERR_INVALID, "da_ghost_gram_diag: the two sides need one batch size (%lld vs %lld)",
+                     (long long)s1->batch, (long long)s2->batch);
   plan->n_r = s1->batch * plan->tiles_r;
-  plan->n_c = s2->batch * plan->tiles_c;
+  plan->n_c = (diag ? 1 : s2->batch) * plan->tiles_c;
   plan->per_pair = plan->tiles_r * plan->tiles_c;
-  plan->ws = (size_t)(s1->batch * s2->batch * plan->per_pair) * sizeof(float);
+  plan->ws = (size_t)(s1->batch * (diag ? 1 : s2->batch) * plan->per_pair) * sizeof(float);
   return DA_OK;
 }
 
@@ -1064,33 +1077,19 @@ int grouped_plan(const da_factor_side* s1, const da_factor_side* s2, int n_group
   return DA_OK;
 }
 
-}  // namespace
-}  // namespace da
-
-extern "C" {
-
-int da_ghost_gram_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
-                            int64_t D, int dtype, size_t* bytes) {
-  da::Plan plan;
-  int rc = da::make_plan(s1, s2, K, D, dtype, &plan);
-  if (rc) return rc;
-  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_ghost_gram_workspace: bytes is NULL");
-  *bytes = plan.ws;
-  return DA_OK;
-}
-
-int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D,
-                  int dtype, float* out, int64_t ld_out, int accumulate, void* workspace,
-                  size_t workspace_bytes, void* stream) {
-  using namespace da;
+// Both entry points: all (i, j) pairs into out[i * ld_out + j], or (diag) the
+// pairs (i, i) into out[i * ld_out].
+int run_ghost(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D, int dtype, bool diag,
+              float* out, int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes,
+              hipStream_t st) {
   Plan plan;
-  int rc = make_plan(s1, s2, K, D, dtype, &plan);
+  int rc = make_plan(s1, s2, K, D, dtype, &plan, diag);
   if (rc) return rc;
-  const int64_t b1 = s1->batch, b2 = s2->batch;
-  if (b1 == 0 || b2 == 0) return DA_OK;
+  const int64_t b1 = s1->batch, b2 = diag ? 1 : s2->batch;
+  if (b1 == 0 || s2->batch == 0) return DA_OK;
   if (!out) return set_error(DA_ERR_INVALID, "da_ghost_gram: out is NULL");
-  if (ld_out < b2) return set_error(DA_ERR_INVALID, "da_ghost_gram: ld_out < B2");
-  hipStream_t st = (hipStream_t)stream;
+  if (ld_out < b2)
+    return set_error(DA_ERR_INVALID, diag ? "da_ghost_gram_diag: out_stride < 1" : "da_ghost_gram: ld_out < B2");
   if (s1->tokens == 0 || s2->tokens == 0) {
     return accumulate ? DA_OK : zero_f32_2d(out, b1, b2, ld_out, st);
   }
@@ -1108,6 +1107,7 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
   args.n_r = plan.n_r;
   args.n_c = plan.n_c;
   args.bias = s1->has_bias ? 1.f : 0.f;
+  args.diag = diag ? 1 : 0;
   args.partial = (float*)workspace;
   const int64_t ntiles = plan.n_r * plan.n_c;
   if (ntiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_ghost_gram: too many tiles");
@@ -1131,6 +1131,45 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
   ghost_gram_reduce<<<(unsigned)((pairs + 255) / 256), 256, 0, st>>>(
       (const float*)workspace, b1, b2, plan.per_pair, out, ld_out, accumulate);
   return check_launch("da_ghost_gram(reduce)");
+}
+
+}  // namespace
+}  // namespace da
+
+extern "C" {
+
+int da_ghost_gram_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
+                            int64_t D, int dtype, size_t* bytes) {
+  da::Plan plan;
+  int rc = da::make_plan(s1, s2, K, D, dtype, &plan);
+  if (rc) return rc;
+  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_ghost_gram_workspace: bytes is NULL");
+  *bytes = plan.ws;
+  return DA_OK;
+}
+
+int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D,
+                  int dtype, float* out, int64_t ld_out, int accumulate, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  return da::run_ghost(s1, s2, K, D, dtype, false, out, ld_out, accumulate, workspace, workspace_bytes,
+                       (hipStream_t)stream);
+}
+
+int da_ghost_gram_diag_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D,
+                                 int dtype, size_t* bytes) {
+  da::Plan plan;
+  int rc = da::make_plan(s1, s2, K, D, dtype, &plan, true);
+  if (rc) return rc;
+  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_ghost_gram_diag_workspace: bytes is NULL");
+  *bytes = plan.ws;
+  return DA_OK;
+}
+
+int da_ghost_gram_diag(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D, int dtype,
+                       float* out, int64_t out_stride, int accumulate, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  return da::run_ghost(s1, s2, K, D, dtype, true, out, out_stride, accumulate, workspace, workspace_bytes,
+                       (hipStream_t)stream);
 }
 
 int da_ghost_gram_grouped_workspace(const da_factor_side* s1, const da_factor_side* s2, int n_groups,

@@ -500,6 +500,166 @@ int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers
   return reduce_partials((const float*)workspace, p.n_chunks, b1, b2, out, ld_row, ld_col, accumulate, st);
 }
 
+// ---------------------------------------------------------------------------
+// Per-row dot products of dense layers, summed over layers:
+//
+//   out[r] (+)= sum_L sum_c m1_L[r, c] * m2_L[r, c]     (m2_L = m1_L when NULL)
+//
+// -- the per-sample squared gradient norms of GradCos and the per-sample dots
+// of two blocks, on the dense route.  HBM-bound: every weight is read once.
+// The rows are walked block-major in stages of S consecutive 64-element blocks
+// of R rows (R * S * C = 1024 16-byte chunks, 4 per thread), so in the
+// k-blocked layout a stage reads S contiguous runs and in the row-major one R
+// runs of S blocks.  A workgroup owns one row tile and one range of stages and
+// writes one fp32 partial per row; a second kernel adds a row's partials in
+// range order (deterministic).
+// ---------------------------------------------------------------------------
+namespace rd {
+constexpr int kThreads = 256;
+constexpr int kPer = 4;                        // 16-byte chunks per thread and stage
+constexpr int kStage = kThreads * kPer;        // chunks per stage
+struct Layer {
+  const char* m1;
+  const char* m2;                              // == m1 for a squared norm
+  int64_t ld1, blk1, ld2, blk2;                // bytes
+  int64_t bytes;                               // row width in bytes
+  int64_t blocks;                              // 64-element blocks per row
+};
+struct Args {
+  Layer layers[kMaxLayers];
+  int n_layers;
+  int64_t rows;
+  int64_t tile_rows, stage_blocks;             // R, S
+  int64_t stages, ranges;                      // stages in all, stage ranges per row tile
+  float* partial;                              // [rows][ranges]
+};
+}  // namespace rd
+
+template <int DT>
+__global__ __launch_bounds__(rd::kThreads) void row_dots_kernel(rd::Args a) {
+  __shared__ float red[rd::kPer][rd::kThreads];
+  constexpr int C = 4 * Elem<DT>::kBytes;      // 16-byte chunks per 64-element block
+  constexpr int V = Elem<DT>::kVec;
+  const int tid = threadIdx.x;
+  const int R = (int)a.tile_rows, S = (int)a.stage_blocks;
+  const int64_t rt = blockIdx.x / a.ranges, w = blockIdx.x % a.ranges;
+  const int64_t st0 = w * a.stages / a.ranges, st1 = (w + 1) * a.stages / a.ranges;
+  int row[rd::kPer], cb[rd::kPer], il[rd::kPer];
+  int64_t jb[rd::kPer];
+  float acc[rd::kPer];
+#pragma unroll
+  for (int k = 0; k < rd::kPer; ++k) {
+    const int q = tid + k * rd::kThreads;      // chunk q of a stage: block q / (R*C), row, chunk
+    row[k] = (q % (R * C)) / C;
+    cb[k] = q % C;
+    acc[k] = 0.f;
+    il[k] = 0;
+    jb[k] = st0 * S + q / (R * C);             // global block index, then the layer cursor
+    while (il[k] < a.n_layers && jb[k] >= a.layers[il[k]].blocks) jb[k] -= a.layers[il[k]++].blocks;
+  }
+  for (int64_t st = st0; st < st1; ++st) {
+#pragma unroll
+    for (int k = 0; k < rd::kPer; ++k) {
+      const int64_t r = rt * R + row[k];
+      if (il[k] < a.n_layers && r < a.rows) {
+        const rd::Layer& L = a.layers[il[k]];
+        const int64_t byte = jb[k] * 64 * Elem<DT>::kBytes + cb[k] * 16;
+        if (byte < L.bytes) {
+          float x[V], y[V];
+          unpack16<DT>(ld16(L.m1 + r * L.ld1 + jb[k] * L.blk1 + cb[k] * 16), x);
+          if (L.m2 == L.m1) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[k] += x[e] * x[e];
+          } else {
+            unpack16<DT>(ld16(L.m2 + r * L.ld2 + jb[k] * L.blk2 + cb[k] * 16), y);
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[k] += x[e] * y[e];
+          }
+        }
+      }
+      jb[k] += S;
+      while (il[k] < a.n_layers && jb[k] >= a.layers[il[k]].blocks) jb[k] -= a.layers[il[k]++].blocks;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < rd::kPer; ++k) red[k][tid] = acc[k];
+  __syncthreads();
+  if (tid < R) {
+    float sum = 0.f;
+    for (int sb = 0; sb < S; ++sb)
+      for (int c = 0; c < C; ++c) {
+        const int q = (sb * R + tid) * C + c;
+        sum += red[q / rd::kThreads][q % rd::kThreads];
+      }
+    const int64_t r = rt * R + tid;
+    if (r < a.rows) a.partial[r * a.ranges + w] = sum;
+  }
+}
+
+struct DotPlan {
+  rd::Args args;
+  int64_t row_tiles;
+  size_t ws;
+};
+
+int row_dots_plan(int64_t rows, const da_dense_layer* layers, int n_layers, int dtype, DotPlan* p) {
+  const char* who = "da_row_dots";
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype %d", who, dtype);
+  if (rows < 0) return set_error(DA_ERR_INVALID, "%s: negative row count", who);
+  if (n_layers < 0 || (n_layers > 0 && !layers)) return set_error(DA_ERR_INVALID, "%s: bad layer list", who);
+  if (n_layers > kMaxLayers) return set_error(DA_ERR_INVALID, "%s: at most %d layers per call", who, kMaxLayers);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  rd::Args& a = p->args;
+  a.n_layers = 0;
+  int64_t blocks = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    const da_dense_layer& L = layers[l];
+    const bool sq = L.m2 == nullptr;
+    if (L.width < 0) return set_error(DA_ERR_INVALID, "%s: layer %d negative width", who, l);
+    if (L.width == 0) continue;
+    const int64_t blk1 = L.blk1 ? L.blk1 : 64, blk2 = sq ? blk1 : (L.blk2 ? L.blk2 : 64);
+    const int64_t ld2 = sq ? L.ld1 : L.ld2;
+    if ((L.width * es) % 16 || (L.ld1 * es) % 16 || (ld2 * es) % 16 || blk1 < 64 || blk2 < 64 ||
+        (blk1 * es) % 16 || (blk2 * es) % 16)
+      return set_error(DA_ERR_INVALID, "%s: layer %d width, strides and block strides must be 16-byte multiples "
+                       "(block strides >= 64 elements)", who, l);
+    if (!L.m1 || ((uintptr_t)L.m1 & 15) || (!sq && ((uintptr_t)L.m2 & 15)))
+      return set_error(DA_ERR_INVALID, "%s: layer %d pointers NULL or misaligned", who, l);
+    rd::Layer& D = a.layers[a.n_layers++];
+    D.m1 = (const char*)L.m1;
+    D.m2 = sq ? D.m1 : (const char*)L.m2;
+    D.ld1 = L.ld1 * es;
+    D.ld2 = ld2 * es;
+    D.blk1 = blk1 * es;
+    D.blk2 = blk2 * es;
+    D.bytes = L.width * es;
+    D.blocks = (L.width + 63) / 64;
+    blocks += D.blocks;
+  }
+  const int64_t C = 4 * es;                       // chunks per block
+  int64_t R = 1;
+  while (R < rows && R * C < rd::kStage) R *= 2;  // rows per tile, a power of two with R * C <= 1024
+  a.rows = rows;
+  a.tile_rows = R;
+  a.stage_blocks = rd::kStage / (R * C);
+  a.stages = (blocks + a.stage_blocks - 1) / a.stage_blocks;
+  p->row_tiles = rows > 0 ? (rows + R - 1) / R : 0;
+  a.ranges = 1;
+  p->ws = 0;
+  if (rows == 0 || a.stages == 0) return DA_OK;
+  int64_t cus = 0;
+  const int rc = device_cu_count(&cus);
+  if (rc) return rc;
+  int64_t ranges = 4 * cus / p->row_tiles;         // ~4 workgroups per CU in all
+  const int64_t most = a.stages / 16 > 0 ? a.stages / 16 : 1;  // at least 16 stages per workgroup
+  if (ranges > most) ranges = most;
+  if (ranges < 1) ranges = 1;
+  a.ranges = ranges;
+  if (p->row_tiles * ranges > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+  p->ws = (size_t)(rows * ranges) * sizeof(float);
+  return DA_OK;
+}
+
 // The allocation-free entry point keeps its partials in this file-scope
 // device array (one copy per GPU, alive until the process ends).  Host code
 // must never pass `scratch` itself to a kernel: its name is a host-side
@@ -571,6 +731,39 @@ int da_score_gemm_noalloc(int64_t b1, int64_t b2, const da_dense_layer* layers, 
   if (rc) return rc;
   return da::run_plan(p, b1, b2, layers, n_layers, dtype, out, ld_row, ld_col, accumulate, ptr, da::kScratchBytes,
                       (hipStream_t)stream);
+}
+
+int da_row_dots_workspace(int64_t rows, const da_dense_layer* layers, int n_layers, int dtype, size_t* bytes) {
+  da::DotPlan p;
+  const int rc = da::row_dots_plan(rows, layers, n_layers, dtype, &p);
+  if (rc) return rc;
+  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_row_dots_workspace: bytes is NULL");
+  *bytes = p.ws;
+  return DA_OK;
+}
+
+int da_row_dots(int64_t rows, const da_dense_layer* layers, int n_layers, int dtype, float* out,
+                int64_t out_stride, int accumulate, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace da;
+  DotPlan p;
+  int rc = row_dots_plan(rows, layers, n_layers, dtype, &p);
+  if (rc) return rc;
+  if (rows == 0) return DA_OK;
+  if (!out || out_stride < 1) return set_error(DA_ERR_INVALID, "da_row_dots: out is NULL or out_stride < 1");
+  hipStream_t st = (hipStream_t)stream;
+  if (p.args.stages == 0) return accumulate ? DA_OK : zero_f32_2d(out, rows, 1, out_stride, st);
+  if (!workspace || workspace_bytes < p.ws)
+    return set_error(DA_ERR_WORKSPACE, "da_row_dots: workspace needs %zu bytes, got %zu", p.ws, workspace_bytes);
+  p.args.partial = (float*)workspace;
+  const unsigned grid = (unsigned)(p.row_tiles * p.args.ranges);
+  switch (dtype) {
+    case DA_BF16: row_dots_kernel<DA_BF16><<<grid, rd::kThreads, 0, st>>>(p.args); break;
+    case DA_F16: row_dots_kernel<DA_F16><<<grid, rd::kThreads, 0, st>>>(p.args); break;
+    default: row_dots_kernel<DA_F32><<<grid, rd::kThreads, 0, st>>>(p.args); break;
+  }
+  rc = check_launch("da_row_dots");
+  if (rc) return rc;
+  return reduce_partials((const float*)workspace, p.args.ranges, rows, 1, out, out_stride, 1, accumulate, st);
 }
 
 }  // extern "C"

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdattri_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DA_F32, DA_F16, DA_BF16 = 0, 1, 2
 DA_OK, DA_ERR_INVALID, DA_ERR_UNSUPPORTED, DA_ERR_HIP, DA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -61,6 +61,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "da_selftest_mfma": (_I32, [_I32, _I32, _P, _P, _P, _P]),
     "da_ghost_gram_workspace": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
     "da_ghost_gram": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, _P, _I64, _I32, _P, _SZ, _P]),
+    "da_ghost_gram_diag_workspace": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
+    "da_ghost_gram_diag": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, _P, _I64, _I32, _P, _SZ, _P]),
     "da_ghost_gram_grouped_workspace": (_I32, [_SIDE, _SIDE, _I32, _P, _P, _I32, ctypes.POINTER(_SZ)]),
     "da_ghost_gram_grouped": (_I32, [_SIDE, _SIDE, _I32, _P, _P, _I32, _P, _I64, _I32, _P, _SZ, _P]),
     "da_ghost_gram_per_token_workspace": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
@@ -96,6 +98,8 @@ SIGNATURES.update(
         "da_row_gram_workspace": (_I32, [_I64, _I64, _I32, ctypes.POINTER(_SZ)]),
         "da_nonzero_rows": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P]),
         "da_score_gemm_workspace": (_I32, [_I64, _I64, _LAYERS, _I32, _I32, ctypes.POINTER(_SZ)]),
+        "da_row_dots_workspace": (_I32, [_I64, _LAYERS, _I32, _I32, ctypes.POINTER(_SZ)]),
+        "da_row_dots": (_I32, [_I64, _LAYERS, _I32, _I32, _P, _I64, _I32, _P, _SZ, _P]),
         "da_score_gemm_noalloc": (_I32, [_I64, _I64, _LAYERS, _I32, _I32, _P, _I64, _I64, _I32, _P]),
         "da_score_gemm": (
             _I32,

@@ -1,28 +1,35 @@
 """TracIn / GradCos on the MI355X scoring path.
 
-The scoring half of ``dattri_llm/attribution/algorithm/tracin.py`` and
-``attribution/base.py``: the inner product is the layerwise cross-gram
-(base.py:657-675, tracin.py:92-108), GradCos divides by whole-model gradient
-norms (tracin.py:125-148), and the query block is routed once before scoring
-(``_route_test_rep``, base.py:586-655): layers the cost rule prefers dense are
-materialized (largest flop saving first, under a byte budget), norm layers are
-materialized, and the remaining factorized layers are finalized.
+Follows the scoring half of ``dattri_llm/attribution/algorithm/tracin.py`` and
+``attribution/base.py``: the score of a train block against a query block is
+the layerwise cross-gram (base.py:657-698, tracin.py:92-126); GradCos divides
+it by both sides' whole-model gradient norms (tracin.py:125-148); the query
+block is routed once before scoring (``route_test_rep``, the contract of
+base.py:586-655, planned in :mod:`dattri_llm_amd.attribution.routing`).
+
+GradCos norms: a train block's are computed once per block (reusing the dense
+copies the score already made), a query block's once per routed block -- not
+once per train block -- and each costs one launch per representation (all
+dense layers in one row-dot launch; factorized linears on the ghost kernel's
+diagonal pairs).
 """
 
 from __future__ import annotations
 
 import gc
-
+import weakref
 from typing import ClassVar
 
 import torch
 
+from dattri_llm_amd.attribution.routing import apply_plan, plan_query
 from dattri_llm_amd.attribution.score import AttributionScore
-from dattri_llm_amd.attribution.utils import finalize_factors, score_sources
+from dattri_llm_amd.attribution.utils import score_sources
 from dattri_llm_amd.gradient import ops
-from dattri_llm_amd.gradient.gradient import Factorized, Gradient
-from dattri_llm_amd.gradient.ops.materialize import materialize_blocked
+from dattri_llm_amd.gradient.gradient import Gradient
 from dattri_llm_amd.utils.cache import CacheBudget
+
+_EPS = 1e-8  # added to the product of the norms (tracin.py:108)
 
 
 class TracInAttributor:
@@ -42,80 +49,65 @@ class TracInAttributor:
         self.device = torch.device(device)
         self._budget = cache_budget or (lambda dev: CacheBudget(dev))
         self._metric = "dot"
+        # query block -> {shared layers: (B,) whole-model norms}; entries die with the block
+        self._query_norms: weakref.WeakKeyDictionary = weakref.WeakKeyDictionary()
 
     def _set_metric(self, normalized_grad: bool) -> None:
         self._metric = "cosine" if normalized_grad else "dot"
         self.algorithm = "GradCos" if normalized_grad else "TracIn"
 
+    # -- query routing ------------------------------------------------------
+
     def route_test_rep(self, test_rep: Gradient) -> Gradient:
-        """The query routing of base.py:586-655."""
-        b_train = self.train_batch_size or 1
-        candidates = []
-        for name in test_rep.layer_names:
-            value = test_rep.data[name]
-            if not isinstance(value, Factorized):
-                continue
-            lt = test_rep.layer_types[name]
-            if not (ops.is_linear(lt) or ops.is_conv(lt) or ops.is_conv_transpose(lt)):
-                candidates.append((float("inf"), name))
-                continue
-            b_test, s, k, d = ops.effective_dims(value, lt)
-            if ops.maybe_use_materialized_gram(b_train, b_test, s, k, d):
-                cost_f = b_train * b_test * s * s * (d + k)
-                cost_m = (b_train + b_test) * s * d * k + b_train * b_test * d * k
-                candidates.append((cost_f - cost_m, name))
+        """The query block in the representation it is scored in (base.py:586-655)."""
         budget = self._budget(test_rep.device)
-        held = 0
-        dense = []
-        for _saving, name in sorted(candidates, reverse=True):
-            layer = test_rep.select_layers([name])
-            growth = max(layer.materialized_nbytes - layer.nbytes, 0)
-            if budget.fits(growth, held):
-                dense.append(name)
-                held += growth
-        if dense:
-            # resident dense query layers in the k-blocked layout the score GEMM streams
-            test_rep = test_rep.map_layers(lambda _n, v, t: materialize_blocked(v, t), layers=dense, consume=True)
-        return finalize_factors(test_rep, budget=budget, held=held)
+        return apply_plan(test_rep, plan_query(test_rep, self.train_batch_size or 1, budget), budget)
+
+    # -- scores -------------------------------------------------------------
+
+    @staticmethod
+    def _shared(train_rep: Gradient, test_rep: Gradient) -> list[str]:
+        return [name for name in train_rep.data if name in test_rep.data]
+
+    def _norms(self, rep: Gradient, layers: list[str], dense_cache=None) -> torch.Tensor:
+        return ops.block_grad_norm_sq(rep, layers, dense_cache).clamp_min(0).sqrt()
+
+    def _query_norms_of(self, test_rep: Gradient, layers: list[str]) -> torch.Tensor:
+        per_block = self._query_norms.setdefault(test_rep, {})
+        key = tuple(layers)
+        if key not in per_block:
+            per_block[key] = self._norms(test_rep, layers)
+        return per_block[key]
+
+    def _cosine(self, dot: torch.Tensor, train_rep: Gradient, test_rep: Gradient, layers: list[str],
+                dense_cache=None) -> torch.Tensor:
+        """``dot`` (train axis first, query axis last) over the product of the
+        two sides' whole-model gradient norms, plus 1e-8."""
+        n_tr = self._norms(train_rep, layers, dense_cache)
+        n_te = self._query_norms_of(test_rep, layers)
+        shape = (n_tr.shape[0],) + (1,) * (dot.dim() - 1)
+        return dot / (n_tr.view(shape) * n_te + _EPS)
 
     def inner_product(self, train_rep: Gradient, test_rep: Gradient, *, dense_cache=None) -> torch.Tensor:
-        if not any(name in test_rep.data for name in train_rep.data):
+        """``(B_train, B_test)`` scores of one train block against one query block."""
+        layers = self._shared(train_rep, test_rep)
+        if not layers:
             return torch.zeros(train_rep.batch_size, test_rep.batch_size, device=self.device)
         dot = ops.layerwise_cross_dot(train_rep, test_rep, dense_cache=dense_cache)
-        if self._metric == "dot":
-            return dot
-        shared = [n for n in train_rep.data if n in test_rep.data]
-        n_tr = self._norm(train_rep, shared, dense_cache)
-        n_te = self._norm(test_rep, shared, None)
-        return dot / (n_tr[:, None] * n_te[None, :] + 1e-8)
+        return dot if self._metric == "dot" else self._cosine(dot, train_rep, test_rep, layers, dense_cache)
 
     def inner_product_per_token(self, train_rep: Gradient, test_rep: Gradient) -> torch.Tensor:
         """(B_train, T_train, B_test) decomposition of :meth:`inner_product` over the
         train side's token positions (tracin.py:110-126, base.py:677-698); for
         GradCos each position's share of the cosine (the per-token dots over the
         two whole-sample norms)."""
-        if not any(name in test_rep.data for name in train_rep.data):
+        layers = self._shared(train_rep, test_rep)
+        if not layers:
             tokens = [t for t in train_rep.token_dim.values() if t is not None]
             return torch.zeros(train_rep.batch_size, max(tokens) if tokens else 1, test_rep.batch_size,
                                device=self.device)
         dot = ops.layerwise_cross_dot_per_token(train_rep, test_rep)
-        if self._metric == "dot":
-            return dot
-        shared = [n for n in train_rep.data if n in test_rep.data]
-        n_tr = self._norm(train_rep, shared, None)
-        n_te = self._norm(test_rep, shared, None)
-        return dot / (n_tr[:, None, None] * n_te[None, None, :] + 1e-8)
-
-    @staticmethod
-    def _norm(rep: Gradient, layers, dense_cache) -> torch.Tensor:
-        total = torch.zeros(rep.batch_size, device=rep.device)
-        for name in layers:
-            value = rep.data[name]
-            if dense_cache is not None and name in dense_cache:
-                value = dense_cache.get(name)
-            sq = ops.grad_norm_sq(value, rep.layer_types[name]).to(total.dtype)
-            total += sq.expand(rep.batch_size) if sq.shape[0] == 1 else sq
-        return total.clamp_min(0).sqrt()
+        return dot if self._metric == "dot" else self._cosine(dot, train_rep, test_rep, layers)
 
     def attribute_sources(self, train_source, test_source, *, normalized_grad: bool = False,
                           batch_size: int | None = None,

@@ -9,6 +9,7 @@ tensors, the unsuffixed ones take :class:`Factorized` (or dense tensors).
 from dattri_llm_amd.gradient.ops import cost, dtypes, kronecker, moe
 from dattri_llm_amd.gradient.ops.cost import CostModel, calibrate, get_routing_policy, set_routing_policy
 from dattri_llm_amd.gradient.ops.dot import (
+    block_grad_norm_sq,
     cross_dot,
     cross_dot_factors,
     cross_dot_per_token,
@@ -26,6 +27,7 @@ from dattri_llm_amd.gradient.ops.dot import (
     maybe_use_materialized_norm,
     pairwise_dot,
     pairwise_dot_factors,
+    route_flops,
 )
 from dattri_llm_amd.gradient.ops.dtypes import as_float, compute_dtype, get_compute_dtype, set_compute_dtype
 from dattri_llm_amd.gradient.ops.kronecker import (
@@ -97,7 +99,7 @@ __all__ = [
     "kfac_precondition", "kfac_precondition_materialized", "kronecker", "sym_inverse",
     "ALL_LAYER_TYPES", "CAPTURE_STYLES", "CONV_TRANSPOSE_TYPES", "CONV_TYPES", "EMBEDDING_TYPES",
     "LINEAR_TYPES", "MASK_KEYS", "NORM_TYPES", "PARAM_GRAD_TYPES", "PROJECTION_STYLES", "CostModel",
-    "DattriProjector", "ProjectionMatrix", "apply_projection", "as_float", "calibrate",
+    "DattriProjector", "ProjectionMatrix", "apply_projection", "as_float", "block_grad_norm_sq", "calibrate",
     "canonical_class_name", "capture_projected", "compute_dtype", "cost", "cross_dot",
     "cross_dot_factors", "cross_dot_per_token", "cross_gram", "cross_gram_per_token",
     "cross_gram_per_token_dense", "dot", "dot_factors", "dtypes", "effective_dims",
@@ -107,6 +109,6 @@ __all__ = [
     "materialize", "materialize_blocked", "materialize_factors", "maybe_materialize_projected", "maybe_use_materialized_gram",
     "maybe_use_materialized_norm", "moe", "pairwise_dot", "pairwise_dot_factors", "preprocess_factorized",
     "preprocess_factors", "project_activation", "project_factorized", "project_factors",
-    "project_gradient", "project_layer", "project_outer_factors", "set_compute_dtype",
+    "project_gradient", "project_layer", "project_outer_factors", "route_flops", "set_compute_dtype",
     "set_routing_policy", "should_materialize", "to_3d",
 ]

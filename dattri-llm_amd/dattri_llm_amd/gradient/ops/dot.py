@@ -150,62 +150,87 @@ def pairwise_dot_factors(a, g, layer_type: str, module_kwargs: dict | None = Non
 
 def dot_factors(a1, g1, a2, g2, layer_type: str, module_kwargs1: dict | None = None,
                 module_kwargs2: dict | None = None, include_bias: bool = True) -> torch.Tensor:
-    """(B,) per-sample dots ``<dW1_i, dW2_i>`` (dot.py:307-357)."""
+    """(B,) per-sample dots ``<dW1_i, dW2_i>`` (dot.py:307-357): one launch of
+    the ghost kernel on the diagonal pairs (linear layers) or of the row-dot
+    kernel (norm layers)."""
     out_dtype = dtypes.resolve(a1, g1, a2, g2)
-    b = a1.shape[0]
-    if g2.shape[0] != b:
+    if a1.shape[0] != g2.shape[0]:
         raise ValueError("dot_factors needs two blocks of one batch size")
     kind, s1 = _side(a1, g1, layer_type, module_kwargs1, include_bias)
     _, s2 = _side(a2, g2, layer_type, module_kwargs2, include_bias)
-    out = torch.empty(b, dtype=torch.float32, device=a1.device)
-    for i in range(b):
-        if kind == "norm":
-            out[i] = _dense_gram(s1[i : i + 1], s2[i : i + 1])[0, 0]
-        else:
-            x1, y1, bias1 = s1
-            x2, y2, bias2 = s2
-            out[i] = _linear_gram32(to_3d(x1)[i : i + 1], to_3d(y1)[i : i + 1], bias1,
-                                    to_3d(x2)[i : i + 1], to_3d(y2)[i : i + 1], bias2, "factorized")[0, 0]
-    return out.to(out_dtype)
+    if kind == "norm":
+        (m1, m2), _ = _kernel_operands(_rows(s1), _rows(s2))
+        return kernels.row_dots([(m1, m2)]).to(out_dtype)
+    (x1, y1, bias1), (x2, y2, bias2) = s1, s2
+    if bias1 != bias2:
+        raise ValueError("the two sides disagree on the bias column")
+    (x1, y1, x2, y2), _ = _kernel_operands(to_3d(x1), to_3d(y1), to_3d(x2), to_3d(y2))
+    return kernels.ghost_gram_diag(x1, y1, x2, y2, bias=bias1).to(out_dtype)
 
 
-def _diag_gram(m: torch.Tensor) -> torch.Tensor:
-    """fp32 squared row norms of a dense (B, d) block."""
-    out = torch.empty(m.shape[0], dtype=torch.float32, device=m.device)
-    for i in range(m.shape[0]):
-        _dense_gram(m[i : i + 1], m[i : i + 1], out=out[i : i + 1].view(1, 1))
-    return out
+def _sq_row_norms(m: torch.Tensor) -> torch.Tensor:
+    """fp32 squared row norms of a dense (B, d) block (k-blocked views are
+    read in place), one launch."""
+    (m,), _ = _kernel_operands(_rows(m))
+    return kernels.row_dots([(m, None)])
 
 
 def grad_norm_sq_factors(a, g, layer_type: str, module_kwargs: dict | None = None,
                          include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
-    """(B,) squared per-sample gradient norms (dot.py:365-411)."""
+    """(B,) squared per-sample gradient norms (dot.py:365-411), one launch:
+    the ghost kernel on the diagonal pairs of the block with itself
+    (factorized), or the row-dot kernel on the per-sample gradients
+    (materialized, and norm layers)."""
     out_dtype = dtypes.resolve(a, g)
     kind, side = _side(a, g, layer_type, module_kwargs, include_bias)
     if kind == "norm":
-        return _diag_gram(side).to(out_dtype)
+        return _sq_row_norms(side).to(out_dtype)
     x, y, bias = side
-    x3, y3 = to_3d(x), to_3d(y)
+    (x3, y3), _ = _kernel_operands(to_3d(x), to_3d(y))
     s, k, d = x3.shape[1], x3.shape[-1] + int(bias), y3.shape[-1]
     if mode == "auto":
         mode = "materialized" if maybe_use_materialized_norm(s, k, d) else "factorized"
     if mode == "materialized":
-        return _diag_gram(linear_dense(x3, y3, bias)).to(out_dtype)
-    out = torch.empty(x3.shape[0], dtype=torch.float32, device=x3.device)
-    for i in range(x3.shape[0]):
-        _linear_gram32(x3[i : i + 1], y3[i : i + 1], bias, x3[i : i + 1], y3[i : i + 1], bias,
-                       "factorized", out=out[i : i + 1].view(1, 1))
-    return out.to(out_dtype)
+        return _sq_row_norms(linear_dense(x3, y3, bias)).to(out_dtype)
+    if mode != "factorized":
+        raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
+    return kernels.ghost_gram_diag(x3, y3, x3, y3, bias=bias).to(out_dtype)
 
 
 def grad_norm_sq(f, layer_type: str, include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
     """(B,) squared norms of one layer, whatever its form (dot.py:414-437)."""
     if isinstance(f, torch.Tensor):
-        flat = f.reshape(f.shape[0], -1)
-        return _diag_gram(flat).to(dtypes.resolve(flat))
+        return _sq_row_norms(f).to(dtypes.resolve(f))
     bf = f.as_batch_first()
     return grad_norm_sq_factors(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
                                 include_bias, mode)
+
+
+def block_grad_norm_sq(rep, layers, dense_cache=None) -> torch.Tensor:
+    """fp32 (B,) per-sample squared gradient norms summed over ``layers`` of a
+    block -- the whole-model norm of GradCos (tracin.py:129-148).  Every dense
+    layer of full batch (held dense, or already in ``dense_cache``) is summed
+    in ONE row-dot launch; factorized layers take :func:`grad_norm_sq`; a
+    broadcast batch-1 layer counts for every sample."""
+    b = rep.batch_size
+    total = torch.zeros(b, dtype=torch.float32, device=rep.device)
+    dense = []
+    for name in layers:
+        value = rep.data[name]
+        if dense_cache is not None and name in dense_cache:
+            value = dense_cache.get(name)
+        if isinstance(value, torch.Tensor) and value.shape[0] == b and b > 1:
+            dense.append(_rows(value))
+            continue
+        sq = grad_norm_sq(value, rep.layer_types[name]).float()
+        total += sq.expand(b) if sq.shape[0] == 1 else sq
+    by_dtype: dict[torch.dtype, list] = {}
+    for m in dense:
+        (m,), _ = _kernel_operands(m)
+        by_dtype.setdefault(m.dtype, []).append((m, None))
+    for group in by_dtype.values():
+        kernels.row_dots(group, out=total, accumulate=True)
+    return total
 
 
 def pairwise_dot(f, layer_type: str, include_bias: bool = True, mode: str = "auto") -> torch.Tensor:
@@ -452,6 +477,13 @@ def effective_dims(f, layer_type: str) -> tuple[int, int, int, int]:
     return a.shape[0], math.prod(a.shape[1:-1]), a.shape[-1], g.shape[-1]
 
 
+def route_flops(b1: int, b2: int, s: int, k: int, d: int) -> tuple[int, int]:
+    """The flop counts the reference's rule compares (dot.py:728-745):
+    ``(B1*B2*S^2*(D+K), (B1+B2)*S*D*K + B1*B2*D*K)`` for (factorized,
+    materialized)."""
+    return b1 * b2 * s * s * (d + k), (b1 + b2) * s * d * k + b1 * b2 * d * k
+
+
 def maybe_use_materialized_gram(B1: int, B2: int, S: int, K: int, D: int, kappa: float = 1.0) -> bool:  # noqa: N803
     """``True`` when materialize-then-GEMM is the cheaper cross-gram.
 
@@ -463,8 +495,7 @@ def maybe_use_materialized_gram(B1: int, B2: int, S: int, K: int, D: int, kappa:
     """
     if cost.get_routing_policy() == "calibrated":
         return cost.calibrated_model().prefers_materialized(B1, B2, S, S, K, D, kappa)
-    cost_f = B1 * B2 * S * S * (D + K)
-    cost_m = (B1 + B2) * S * D * K + B1 * B2 * D * K
+    cost_f, cost_m = route_flops(B1, B2, S, K, D)
     return kappa * cost_f >= cost_m
 
 

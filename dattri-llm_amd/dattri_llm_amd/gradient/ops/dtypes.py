@@ -1,55 +1,70 @@
-"""Compute-dtype policy (same contract as ``dattri_llm/gradient/ops/dtypes.py``).
+"""Which dtype the ops compute in.
 
-``"auto"`` resolves to the promoted dtype of the floating operands (bf16 in
-stays bf16), an explicit dtype forces it.  On this path every kernel
-accumulates in fp32 whatever the policy; the policy decides the operand dtype
-the kernels read and the dtype results are returned in.
+The contract is dattri-llm's compute-dtype policy
+(``dattri_llm/gradient/ops/dtypes.py:84-143``): under ``"auto"`` an op works in
+the promotion of its floating operands' dtypes (bf16 captures stay bf16, a
+bf16/fp32 mix becomes fp32, integer operands such as token ids do not count);
+a forced dtype overrides that everywhere; ``minimum`` raises the floor for
+reductions that need it.  Results come back in that dtype.
+
+On this path the policy has one more consumer: the kernels.  They read bf16,
+fp16 or fp32 operands and always accumulate in fp32, so :func:`kernel_dtype`
+maps a resolved dtype to the operand dtype a kernel is launched on (float64
+requests run on fp32 operands; nothing here computes in float64).
 """
 
 from __future__ import annotations
 
-from contextlib import contextmanager
+import contextlib
+import functools
 
 import torch
 
-_POLICY: str | torch.dtype = "auto"
-_NAMED = {
-    "auto": "auto",
-    "float32": torch.float32,
-    "fp32": torch.float32,
-    "float64": torch.float64,
-    "bfloat16": torch.bfloat16,
-    "bf16": torch.bfloat16,
-    "float16": torch.float16,
-    "fp16": torch.float16,
-}
+# Names accepted for a forced policy; short forms map to torch's own names.
+_SHORT = {"fp32": "float32", "bf16": "bfloat16", "fp16": "float16"}
+_FORCEABLE = ("float32", "float64", "bfloat16", "float16")
 
 
-def _as_policy(policy):
-    if isinstance(policy, torch.dtype):
-        return policy
-    if isinstance(policy, str) and policy in _NAMED:
-        return _NAMED[policy]
-    raise ValueError(
-        "compute dtype policy must be 'auto', a torch.dtype, or one of "
-        f"{sorted(k for k in _NAMED if k != 'auto')}; got {policy!r}"
-    )
+class _Policy:
+    """The process-wide policy: ``forced`` is None under "auto"."""
+
+    forced: torch.dtype | None = None
+
+    @staticmethod
+    def parse(spec) -> torch.dtype | None:
+        if isinstance(spec, torch.dtype):
+            return spec
+        if spec == "auto":
+            return None
+        name = _SHORT.get(spec, spec) if isinstance(spec, str) else None
+        if name in _FORCEABLE:
+            return getattr(torch, name)
+        accepted = sorted(set(_FORCEABLE) | set(_SHORT))
+        raise ValueError(f"compute dtype policy must be 'auto', a torch.dtype, or one of {accepted}; got {spec!r}")
+
+    def public(self):
+        return "auto" if self.forced is None else self.forced
+
+
+_policy = _Policy()
 
 
 def set_compute_dtype(policy):
-    """Set the process-wide compute dtype; returns the policy it replaces."""
-    global _POLICY  # noqa: PLW0603
-    previous, _POLICY = _POLICY, _as_policy(policy)
+    """Set the process-wide compute dtype ("auto", a torch.dtype or a dtype
+    name); returns the policy it replaces, in the same form."""
+    previous = _policy.public()
+    _policy.forced = _Policy.parse(policy)
     return previous
 
 
 def get_compute_dtype():
-    return _POLICY
+    """"auto" or the forced torch.dtype."""
+    return _policy.public()
 
 
-@contextmanager
+@contextlib.contextmanager
 def compute_dtype(policy):
-    """Scope a compute-dtype policy to a block."""
+    """The policy for the duration of a ``with`` block."""
     previous = set_compute_dtype(policy)
     try:
         yield
@@ -57,39 +72,37 @@ def compute_dtype(policy):
         set_compute_dtype(previous)
 
 
+def _floating(tensors):
+    return [t.dtype for t in tensors if t is not None and t.is_floating_point()]
+
+
 def resolve(*tensors, minimum: torch.dtype | None = None) -> torch.dtype:
-    """dtypes.py:84-107: the policy dtype, or the promotion of the floating operands."""
-    if _POLICY != "auto":
-        dtype = _POLICY
+    """The compute dtype for these operands: the forced one, else the promotion
+    of the floating operands (fp32 when there are none), raised to ``minimum``."""
+    if _policy.forced is not None:
+        dtype = _policy.forced
     else:
-        dtype = None
-        for t in tensors:
-            if t is None or not t.is_floating_point():
-                continue
-            dtype = t.dtype if dtype is None else torch.promote_types(dtype, t.dtype)
-        if dtype is None:
-            dtype = torch.float32
-    if minimum is not None:
-        dtype = torch.promote_types(dtype, minimum)
-    return dtype
+        floating = _floating(tensors)
+        dtype = functools.reduce(torch.promote_types, floating) if floating else torch.float32
+    return dtype if minimum is None else torch.promote_types(dtype, minimum)
 
 
 def align(*tensors, minimum: torch.dtype | None = None):
-    """Cast every floating operand to :func:`resolve`'s dtype (dtypes.py:110-126)."""
-    dtype = resolve(*tensors, minimum=minimum)
-    return tuple(
-        t if (t is None or not t.is_floating_point() or t.dtype == dtype) else t.to(dtype)
-        for t in tensors
-    )
+    """The operands with every floating one cast to :func:`resolve`'s dtype;
+    integer tensors and None pass through, as do tensors already in it."""
+    target = resolve(*tensors, minimum=minimum)
+    return tuple(t.to(target) if t is not None and t.is_floating_point() and t.dtype != target else t
+                 for t in tensors)
 
 
 def as_float(*tensors, minimum: torch.dtype | None = None):
-    """Like :func:`align` but integer operands are converted too (dtypes.py:129-143)."""
-    dtype = resolve(*tensors, minimum=minimum)
-    return tuple(t if (t is None or t.dtype == dtype) else t.to(dtype) for t in tensors)
+    """:func:`align` that converts integer operands too (for ops that need a
+    floating input, such as a projection of token ids)."""
+    target = resolve(*tensors, minimum=minimum)
+    return tuple(t.to(target) if t is not None and t.dtype != target else t for t in tensors)
 
 
 def kernel_dtype(dtype: torch.dtype) -> torch.dtype:
-    """The operand dtype a kernel reads for a resolved compute dtype: the MFMA
-    kernels take fp32/fp16/bf16; float64 requests run as fp32 operands."""
+    """The operand dtype a kernel reads for a resolved compute dtype: bf16,
+    fp16 and fp32 as they are, float64 as fp32 (fp32 accumulation either way)."""
     return torch.float32 if dtype == torch.float64 else dtype

@@ -66,6 +66,74 @@ def _dtype_from_name(name: str) -> torch.dtype:
         raise ValueError(f"Unknown tensor dtype {name!r} in memmap metadata.") from None
 
 
+# ---------------------------------------------------------------------------
+# group codec: one layer value <-> the format's (kind, tensor parts, extras),
+# shared by the writer and the reader
+# ---------------------------------------------------------------------------
+
+_PART_ALIGN = 8  # every part starts 8-byte aligned, so any dtype can be viewed at its offset
+
+
+def _split_layer(value) -> tuple[str, dict[str, torch.Tensor], dict]:
+    """A layer as the format stores it: its kind, its tensor parts by name and
+    the non-tensor fields kept beside them in the meta."""
+    if isinstance(value, Factorized):
+        parts = {"activation": value.activation, "pre_activation_grad": value.pre_activation_grad}
+        return "factorized", parts, {"module_kwargs": value.module_kwargs, "batch_first": value.batch_first}
+    return "dense", {"data": value}, {}
+
+
+def _join_layer(kind: str, parts: dict[str, torch.Tensor], fields: dict):
+    """The layer value :func:`_split_layer` took apart."""
+    if kind == "factorized":
+        return Factorized(parts["activation"], parts["pre_activation_grad"],
+                          module_kwargs=fields["module_kwargs"], batch_first=fields["batch_first"])
+    return parts["data"]
+
+
+class _BinLayout:
+    """The ``.bin`` of one group, planned before it is written: parts are
+    placed in record, layer, part order, each at the next aligned offset, and
+    the file ends on an aligned boundary."""
+
+    def __init__(self) -> None:
+        self.parts: list[tuple[int, torch.Tensor]] = []
+        self.size = 0
+
+    def place(self, tensor: torch.Tensor) -> dict:
+        host = tensor.detach().to("cpu").contiguous()
+        nbytes = host.numel() * host.element_size()
+        offset = self.size
+        self.parts.append((offset, host))
+        end = offset + nbytes
+        self.size = end + (-end) % _PART_ALIGN
+        return {"byte_off": offset, "nbytes": nbytes, "shape": list(host.shape), "dtype": _dtype_name(host.dtype)}
+
+    def write(self, path: Path) -> None:
+        with open(path, "wb") as f:
+            pos = 0
+            for offset, host in self.parts:
+                if offset > pos:
+                    f.write(bytes(offset - pos))
+                if host.numel():
+                    f.write(memoryview(host.view(torch.uint8).reshape(-1).numpy()))
+                pos = offset + host.numel() * host.element_size()
+            if self.size > pos:
+                f.write(bytes(self.size - pos))
+
+
+def _record_meta(record: GradientRecord, layout: _BinLayout) -> dict:
+    """A record's meta entry, its tensors placed in ``layout``."""
+    g = record.gradient
+    layers = {}
+    for name, value in g.data.items():
+        kind, parts, fields = _split_layer(value)
+        layers[name] = {"kind": kind, "parts": {p: layout.place(t) for p, t in parts.items()}, **fields}
+    return {"step": record.step, "input_hash": record.input_hash, "sample_id_key": record.sample_id_key,
+            "representation": dict(g.representation), "layer_types": dict(g.layer_types),
+            "indexing": dict(g.indexing), "layers": layers}
+
+
 class GradientStore:
     """Index, reader and writer of a memmap gradient store (one process, one rank)."""
 
@@ -184,32 +252,24 @@ class GradientStore:
     def records_from(self, payload: dict, buffer: torch.Tensor, file_rel: str = "") -> list[GradientRecord]:
         """The records of a group as views into ``buffer``, the group's ``.bin``
         bytes (a memory map, a pinned host buffer or a device buffer)."""
-        total = buffer.numel()
 
-        def part(spec: dict) -> torch.Tensor:
-            dtype = _dtype_from_name(spec["dtype"])
-            shape = tuple(spec["shape"])
-            if spec["nbytes"] == 0:
-                return torch.empty(shape, dtype=dtype, device=buffer.device)
+        def view(spec: dict) -> torch.Tensor:
+            dtype, shape = _dtype_from_name(spec["dtype"]), tuple(spec["shape"])
             off, n = spec["byte_off"], spec["nbytes"]
-            if off % 8 or off + n > total:
+            if n == 0:
+                return torch.empty(shape, dtype=dtype, device=buffer.device)
+            if off % _PART_ALIGN or off + n > buffer.numel():
                 raise ValueError(f"{file_rel}: part at byte {off} (+{n}) is misaligned or past the file")
             return buffer[off:off + n].view(dtype).reshape(shape)
 
-        records = []
-        for meta in payload["records"]:
-            data = {}
-            for name, layer in meta["layers"].items():
-                parts = layer["parts"]
-                if layer["kind"] == "factorized":
-                    data[name] = Factorized(part(parts["activation"]), part(parts["pre_activation_grad"]),
-                                            module_kwargs=layer["module_kwargs"], batch_first=layer["batch_first"])
-                else:
-                    data[name] = part(parts["data"])
-            grad = Gradient(meta["representation"], data, meta["layer_types"], meta["indexing"],
+        def gradient(meta: dict) -> Gradient:
+            data = {name: _join_layer(layer["kind"], {p: view(spec) for p, spec in layer["parts"].items()}, layer)
+                    for name, layer in meta["layers"].items()}
+            return Gradient(meta["representation"], data, meta["layer_types"], meta["indexing"],
                             validate_on_init=False)
-            records.append(GradientRecord(meta["step"], meta["input_hash"], grad, meta["sample_id_key"]))
-        return records
+
+        return [GradientRecord(m["step"], m["input_hash"], gradient(m), m["sample_id_key"])
+                for m in payload["records"]]
 
     def load_records(self, file_rel: str) -> list[GradientRecord]:
         """The records of one group as CPU tensors viewing a private map of the file."""
@@ -231,39 +291,9 @@ class GradientStore:
             self._next_batch_id = max(ids) + 1 if ids else 0
         base = f"batch_{self._next_batch_id:06d}.mmap"
         self._next_batch_id += 1
-        meta_records = []
-        off = 0
-        with open(self.root / f"{base}.bin", "wb") as binf:
-
-            def write_part(t: torch.Tensor) -> dict:
-                nonlocal off
-                dense = t.detach().to("cpu").contiguous()
-                raw = memoryview(dense.view(torch.uint8).flatten().numpy()) if dense.numel() else b""
-                n = len(raw) if isinstance(raw, bytes) else raw.nbytes
-                binf.write(raw)
-                spec = {"byte_off": off, "nbytes": n, "shape": list(dense.shape), "dtype": _dtype_name(dense.dtype)}
-                off += n
-                pad = (-off) % 8
-                if pad:
-                    binf.write(b"\x00" * pad)
-                    off += pad
-                return spec
-
-            for rec in records:
-                layers = {}
-                for name, value in rec.gradient.data.items():
-                    if isinstance(value, Factorized):
-                        layers[name] = {"kind": "factorized",
-                                        "parts": {"activation": write_part(value.activation),
-                                                  "pre_activation_grad": write_part(value.pre_activation_grad)},
-                                        "module_kwargs": value.module_kwargs, "batch_first": value.batch_first}
-                    else:
-                        layers[name] = {"kind": "dense", "parts": {"data": write_part(value)}}
-                g = rec.gradient
-                meta_records.append({"step": rec.step, "input_hash": rec.input_hash,
-                                     "sample_id_key": rec.sample_id_key,
-                                     "representation": dict(g.representation), "layer_types": dict(g.layer_types),
-                                     "indexing": dict(g.indexing), "layers": layers})
+        layout = _BinLayout()
+        meta_records = [_record_meta(rec, layout) for rec in records]
+        layout.write(self.root / f"{base}.bin")
         torch.save({"format": MEMMAP_FORMAT, "records": meta_records}, self.root / f"{base}.meta")
         meta_file = self.root / INDEX_META_FILE
         if not meta_file.exists():

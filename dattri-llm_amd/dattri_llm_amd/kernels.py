@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import math
 
 import torch
 
@@ -142,6 +143,54 @@ def ghost_gram(
     nat.check(lib.da_ghost_gram_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)), "ghost_gram")
     ws = nat.workspace(nbytes.value, dev)
     _run(dev, "ghost_gram", lib.da_ghost_gram,
+         s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate), ws.data_ptr(), ws.numel(),
+         nat.stream_ptr(dev))
+    return out
+
+
+def ghost_gram_diag(
+    a1: torch.Tensor,
+    g1: torch.Tensor,
+    a2: torch.Tensor,
+    g2: torch.Tensor,
+    *,
+    bias: bool = False,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """The ghost product on the diagonal pairs only, fp32 ``(B,)``: sample i of
+    side 1 against sample i of side 2 (per-sample dots; per-sample squared
+    norms when both sides are one block), all samples in one launch."""
+    dev = nat.require_device(a1, g1, a2, g2)
+    if a1.dim() != 3 or g1.dim() != 3 or a2.dim() != 3 or g2.dim() != 3:
+        raise ValueError("ghost_gram_diag expects 3-D (B, S, width) factors")
+    if not (a1.dtype == g1.dtype == a2.dtype == g2.dtype):
+        raise ValueError("ghost_gram_diag factors must share one dtype")
+    if a1.shape[:2] != g1.shape[:2] or a2.shape[:2] != g2.shape[:2]:
+        raise ValueError("activation and gradient factors disagree on (B, S)")
+    if a1.shape[0] != a2.shape[0]:
+        raise ValueError("ghost_gram_diag needs two blocks of one batch size")
+    if a1.shape[-1] != a2.shape[-1] or g1.shape[-1] != g2.shape[-1]:
+        raise ValueError("the two sides disagree on the layer widths")
+    code = nat.dtype_code(a1.dtype)
+    vec = _chunk_elems(a1.dtype)
+    k = -(-a1.shape[-1] // vec) * vec
+    d = -(-g1.shape[-1] // vec) * vec
+    same = a1 is a2 and g1 is g2
+    a1, g1 = prepare_rows(a1, k), prepare_rows(g1, d)
+    a2, g2 = (a1, g1) if same else (prepare_rows(a2, k), prepare_rows(g2, d))
+    b = a1.shape[0]
+    if out is None:
+        out = torch.empty(b, dtype=torch.float32, device=dev)
+        accumulate = False
+    elif out.dtype != torch.float32 or tuple(out.shape) != (b,):
+        raise ValueError("out must be a float32 (B,) tensor")
+    s1, s2 = _side(a1, g1, bias), _side(a2, g2, bias)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_ghost_gram_diag_workspace(s1, s2, k, d, code, ctypes.byref(nbytes)), "ghost_gram_diag")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "ghost_gram_diag", lib.da_ghost_gram_diag,
          s1, s2, k, d, code, out.data_ptr(), out.stride(0), int(accumulate), ws.data_ptr(), ws.numel(),
          nat.stream_ptr(dev))
     return out
@@ -527,6 +576,73 @@ def score_gemm(
         _run(dev, "score_gemm", lib.da_score_gemm,
              n1, n2, arr, len(group), code, out.data_ptr(), ld_row, ld_col, int(accumulate or start > 0),
              ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    del keep
+    return out
+
+
+def _dense_operand(m: torch.Tensor, width: int):
+    """(tensor, row stride, block stride) in elements of a dense (B, W) block
+    as the dense-layer kernels address it: k-blocked views as they are,
+    anything else as 16-byte aligned (B, width) rows."""
+    if is_blocked(m) and m.data_ptr() % 16 == 0 and all((st * m.element_size()) % 16 == 0 for st in m.stride()[:2]):
+        return m, m.stride(0), m.stride(1)
+    if is_blocked(m):
+        m = m.reshape(m.shape[0], -1)
+    m = prepare_rows(m, width)
+    return m, m.stride(0), 64
+
+
+def row_dots(layers: list, *, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """``sum_L (m1_L * m2_L).sum(-1)`` over dense layer pairs ``(m1, m2)``,
+    fp32 ``(B,)``; a pair whose ``m2`` is None contributes ``m1``'s squared
+    row norms.  Each ``m`` is (B, width...) -- k-blocked views are read in
+    place, never reshaped -- and all layers share one dtype."""
+    if not layers:
+        raise ValueError("row_dots needs at least one layer")
+
+    def width(m):
+        return m.shape[1] * 64 if is_blocked(m) else math.prod(m.shape[1:])
+
+    tensors = [t for pair in layers for t in pair if t is not None]
+    dev = nat.require_device(*tensors)
+    dtype = tensors[0].dtype
+    b = layers[0][0].shape[0]
+    for m1, m2 in layers:
+        if m1.dtype != dtype or (m2 is not None and m2.dtype != dtype):
+            raise ValueError("row_dots layers must share one dtype")
+        if m1.shape[0] != b or (m2 is not None and (m2.shape[0] != b or width(m2) != width(m1))):
+            raise ValueError("row_dots layer shapes disagree")
+    if out is None:
+        out = torch.empty(b, dtype=torch.float32, device=dev)
+        accumulate = False
+    elif out.dtype != torch.float32 or tuple(out.shape) != (b,):
+        raise ValueError("out must be a float32 (B,) tensor")
+    vec = _chunk_elems(dtype)
+    descs, keep = [], []
+    for m1, m2 in layers:
+        w = width(m1)
+        if w == 0:
+            continue
+        wp = -(-w // vec) * vec
+        t1, ld1, bk1 = _dense_operand(m1, wp)
+        t2, ld2, bk2 = _dense_operand(m2, wp) if m2 is not None else (None, 0, 0)
+        keep += [t1, t2]
+        descs.append(nat.DenseLayer(t1.data_ptr(), t2.data_ptr() if t2 is not None else None, wp, ld1, ld2, bk1, bk2))
+    lib = nat.load()
+    code = nat.dtype_code(dtype)
+    if not descs:
+        if not accumulate:
+            out.zero_()
+        return out
+    for start in range(0, len(descs), 32):
+        group = descs[start : start + 32]
+        arr = (nat.DenseLayer * len(group))(*group)
+        nbytes = ctypes.c_size_t(0)
+        nat.check(lib.da_row_dots_workspace(b, arr, len(group), code, ctypes.byref(nbytes)), "row_dots")
+        ws = nat.workspace(nbytes.value, dev)
+        _run(dev, "row_dots", lib.da_row_dots,
+             b, arr, len(group), code, out.data_ptr(), out.stride(0), int(accumulate or start > 0), ws.data_ptr(),
+             ws.numel(), nat.stream_ptr(dev))
     del keep
     return out
 

@@ -98,6 +98,25 @@ int da_ghost_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t K,
                   size_t workspace_bytes, void* stream);
 
 /*
+ * The ghost inner product on the diagonal pairs only: per-sample dots of two
+ * blocks of one batch size B, or per-sample squared norms when both sides
+ * are the same block,
+ *
+ *   out[i*out_stride] (+)= sum_{t,s} (a1_it . a2_is + bias) * (g1_it . g2_is),  i < B,
+ *
+ * in one launch over the B pairs' tiles (fp32, deterministic).  Replaces the
+ * factorized per-sample norm of grad_norm_sq_factors,
+ * dattri_llm/gradient/ops/dot.py:409-411 (the einsums "btk,bsk->bts" and
+ * "btd,bsd->bts" summed per sample), and the per-sample dots of dot_factors,
+ * dot.py:307-357.  DA_ERR_INVALID when the batch sizes differ.
+ */
+int da_ghost_gram_diag_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D,
+                                 int dtype, size_t* bytes);
+int da_ghost_gram_diag(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int64_t D, int dtype,
+                       float* out, int64_t out_stride, int accumulate, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
  * Per-token cross-gram of two factorized sides: side 1's token axis kept,
  * side 2's summed out,
  *
@@ -261,6 +280,25 @@ int da_score_gemm_workspace(int64_t b1, int64_t b2, const da_dense_layer* layers
 int da_score_gemm(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers, int dtype,
                   float* out, int64_t ld_row, int64_t ld_col, int accumulate, void* workspace,
                   size_t workspace_bytes, void* stream);
+
+/*
+ * Per-row dot products of dense layers, summed over layers, fp32:
+ *
+ *   out[r*out_stride] (+)= sum_L sum_c m1_L[r, c] * m2_L[r, c]
+ *
+ * with the layers' addressing of da_dense_layer (row-major or k-blocked); a
+ * layer whose m2 is NULL contributes its squared row norms.  One pass over
+ * every weight, deterministic (fixed-order reduction through the workspace,
+ * whose size depends on the current device's CU count).  At most 32 layers
+ * per call.  Replaces the dense per-sample squared norms of grad_norm_sq,
+ * dattri_llm/gradient/ops/dot.py:426-428 ((flat * flat).sum(-1)), summed
+ * over layers as TracInAttributor._norm sums them
+ * (dattri_llm/attribution/algorithm/tracin.py:129-148), and the dense
+ * per-sample dots of dot_factors, dot.py:307-357.
+ */
+int da_row_dots_workspace(int64_t rows, const da_dense_layer* layers, int n_layers, int dtype, size_t* bytes);
+int da_row_dots(int64_t rows, const da_dense_layer* layers, int n_layers, int dtype, float* out,
+                int64_t out_stride, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * da_score_gemm without a workspace, for callers that cannot allocate device

@@ -187,3 +187,49 @@ def test_rebatch_blocks_concatenates_dense():
     steps, big, ids = out[0]
     assert steps == [0, 0, 1, 1] and ids == ["a", "b", "c", "d"]
     assert big.data["l"].shape == (4, 3)
+
+
+def _query_block(n_test, seed=0, *, s=4, k=8, d=8):
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    gen = torch.Generator().manual_seed(seed)
+    data = {f"l{i}": Factorized(torch.randn(n_test, s, k, generator=gen), torch.randn(n_test, s, d, generator=gen))
+            for i in range(2)}
+    return Gradient(dict.fromkeys(data, "factorized"), data, dict.fromkeys(data, "nn.Linear"),
+                    dict.fromkeys(data, "batch_token"))
+
+
+def test_query_routing_plan_known_answers():
+    """The reference's routing cases (tests/attribution/test_tracin.py:203-235),
+    decided from shapes alone: one query stays factorized, sixteen go dense,
+    a zero budget keeps them factorized, and a budget that fits one layer
+    admits the one with the larger flop saving."""
+    from dattri_llm_amd.attribution.routing import plan_query
+    from dattri_llm_amd.gradient import Factorized
+    from dattri_llm_amd.utils.cache import CacheBudget
+
+    roomy = CacheBudget(limit_bytes=1 << 40)
+    assert plan_query(_query_block(1), 8, roomy).dense == []
+    assert sorted(plan_query(_query_block(16), 8, roomy).dense) == ["l0", "l1"]
+    assert plan_query(_query_block(16, k=16, d=16), 8, CacheBudget(limit_bytes=0)).dense == []
+    block = _query_block(16, k=16, d=16)
+    block.data["l1"] = Factorized(torch.randn(16, 4, 12), torch.randn(16, 4, 12))
+    layer = block.select_layers(["l1"])
+    growth = layer.materialized_nbytes - layer.nbytes
+    plan = plan_query(block, 8, CacheBudget(limit_bytes=growth))
+    assert plan.dense == ["l1"] and plan.held == growth
+    assert [r.name for r in plan.routes] == ["l1", "l0"]  # admission order: larger saving first
+    assert plan.routes[0].saving > plan.routes[1].saving
+
+
+def test_query_routing_plan_follows_the_patched_rule(monkeypatch):
+    """plan_query looks the cost rule up in the ops namespace, where the
+    reference's pin_route patches it."""
+    from dattri_llm_amd.attribution.routing import plan_query
+    from dattri_llm_amd.gradient import ops
+    from dattri_llm_amd.utils.cache import CacheBudget
+
+    monkeypatch.setattr(ops, "maybe_use_materialized_gram", lambda *a, **k: True)
+    assert sorted(plan_query(_query_block(1), 8, CacheBudget(limit_bytes=1 << 40)).dense) == ["l0", "l1"]
+    monkeypatch.setattr(ops, "maybe_use_materialized_gram", lambda *a, **k: False)
+    assert plan_query(_query_block(16), 8, CacheBudget(limit_bytes=1 << 40)).dense == []

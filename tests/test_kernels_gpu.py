@@ -232,3 +232,77 @@ def test_project_outer_kernel(device, case):
     want = oracle.project_outer(_np(a), _np(g), p_in_np, _np(p_out), bias=bias)
     assert got.shape == (b, kg * ka)
     assert_parity(got, want, dtype)
+
+
+DIAG_CASES = [
+    # (b, s1, s2, k, d, bias, same_block)
+    (5, 128, 128, 64, 64, False, True),
+    (3, 300, 300, 72, 40, True, True),     # ragged S, two row tiles
+    (4, 96, 200, 128, 256, True, False),   # two blocks of one batch, S1 != S2
+    (1, 1, 1, 8, 8, False, True),
+    (6, 520, 77, 264, 136, False, False),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("case", DIAG_CASES)
+def test_ghost_gram_diag(device, dtype, case):
+    """The ghost product on the diagonal pairs (per-sample dots / norms) equals
+    the diagonal of the oracle's full cross-gram."""
+    from dattri_llm_amd import kernels
+
+    b, s1, s2, k, d, bias, same = case
+    gen = torch.Generator().manual_seed(b * s1 + k)
+    a1, g1 = _rand(gen, b, s1, k, dtype=dtype, scale=k**-0.5), _rand(gen, b, s1, d, dtype=dtype, scale=d**-0.5)
+    a2, g2 = (a1, g1) if same else (_rand(gen, b, s2, k, dtype=dtype, scale=k**-0.5),
+                                    _rand(gen, b, s2, d, dtype=dtype, scale=d**-0.5))
+    print(f"ghost_gram_diag case={case} dtype={dtype}", flush=True)
+    x1, y1 = a1.to(device), g1.to(device)
+    x2, y2 = (x1, y1) if same else (a2.to(device), g2.to(device))
+    got = kernels.ghost_gram_diag(x1, y1, x2, y2, bias=bias)
+    want = np.diag(oracle.cross_gram_factorized(_np(a1), _np(g1), _np(a2), _np(g2), bias=bias))
+    assert got.shape == (b,)
+    assert_parity(got, want, dtype)
+    kernels.ghost_gram_diag(x1, y1, x2, y2, bias=bias, out=got, accumulate=True)
+    assert_parity(got, 2 * want, dtype)
+
+
+ROW_DOT_CASES = [
+    # (rows, [(width, blocked1, blocked2 or None for a squared norm)])
+    (8, [(4096, True, True), (1024, False, False), (136, False, None)]),
+    (64, [(16384, True, None), (4096, True, False)]),
+    (3, [(64, False, None)]),
+    (130, [(2048, True, True), (200, False, False)]),   # two row tiles (bf16), ragged widths
+    (1, [(8192, True, None)]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", ROW_DOT_CASES)
+def test_row_dots(device, dtype, case):
+    """Per-row dot products (or squared norms) summed over dense layers, row-major
+    and k-blocked operands read in place, against float64 sums."""
+    from dattri_llm_amd import kernels
+
+    rows, spec = case
+    gen = torch.Generator().manual_seed(rows + len(spec))
+    layers, want = [], np.zeros(rows)
+    for w, bl1, bl2 in spec:
+        m1 = _rand(gen, rows, w, dtype=dtype)
+        m2 = None if bl2 is None else _rand(gen, rows, w, dtype=dtype)
+        want += (_np(m1) * (_np(m1) if m2 is None else _np(m2))).sum(1)
+
+        def place(m, blocked):
+            if not blocked or w % 64:
+                return m.to(device)
+            buf = kernels.blocked_storage(rows, w, dtype, device)
+            buf.copy_(m.view(rows, -1, 64).to(device))
+            return buf
+
+        layers.append((place(m1, bl1), None if m2 is None else place(m2, bl2)))
+    print(f"row_dots rows={rows} layers={spec} dtype={dtype}", flush=True)
+    got = kernels.row_dots(layers)
+    assert got.shape == (rows,)
+    assert_parity(got, want, dtype)
+    kernels.row_dots(layers, out=got, accumulate=True)
+    assert_parity(got, 2 * want, dtype)

@@ -117,6 +117,88 @@ def test_grad_norm_and_per_sample_dot(device, ops):
     assert_parity(got, want, torch.float32)
 
 
+@pytest.mark.parametrize("layer_type", ["nn.Linear", "nn.RMSNorm", "nn.LayerNorm"])
+def test_per_sample_norms_and_dots_one_launch(device, ops, layer_type):
+    """grad_norm_sq_factors (both routes), dot_factors and grad_norm_sq of a
+    k-blocked dense layer, each one launch, against the oracle's diagonals."""
+    from dattri_llm_amd import kernels
+
+    gen = torch.Generator().manual_seed(12)
+    d_in, d_out = 128, (192 if layer_type == "nn.Linear" else 128)
+    a, g = _rand(gen, 6, 40, d_in, dtype=torch.bfloat16), _rand(gen, 6, 40, d_out, dtype=torch.bfloat16)
+    b, h = _rand(gen, 6, 24, d_in, dtype=torch.bfloat16), _rand(gen, 6, 24, d_out, dtype=torch.bfloat16)
+    has_bias = layer_type != "nn.RMSNorm"
+    mk = {"has_bias": has_bias, "eps": 1e-5, "normalized_shape": (d_in,)}
+    mko = {"has_bias": has_bias, "eps": 1e-5}
+    pa, pb = oracle.preprocess(_np(a), _np(g), layer_type, mko), oracle.preprocess(_np(b), _np(h), layer_type, mko)
+    full = oracle.cross_gram(*pa, *pa, layer_type, mode="factorized")
+    cross = oracle.cross_gram(*pa, *pb, layer_type, mode="factorized")
+    dev = [x.to(device) for x in (a, g, b, h)]
+    modes = ("factorized", "materialized") if layer_type == "nn.Linear" else ("auto",)
+    with kernels.launch_events() as log:
+        for mode in modes:
+            got = ops.grad_norm_sq_factors(dev[0], dev[1], layer_type, mk, mode=mode)
+            # bf16 result; the materialized route also stores the dense gradient in bf16
+            assert_parity(got, np.diag(full), torch.bfloat16, tight=roundings(1 + (mode != "factorized")), label=mode)
+        got = ops.dot_factors(*dev, layer_type, mk, mk)
+        assert_parity(got, np.diag(cross), torch.bfloat16, tight=roundings(1 + (layer_type != "nn.Linear") * 2))
+    torch.cuda.synchronize()
+    launches = sum(len(v) for k, v in log.items() if k in ("ghost_gram_diag", "row_dots"))
+    assert launches == len(modes) + 1  # one norm or dot launch per call, whatever the batch
+    if layer_type == "nn.Linear":
+        m = kernels.materialize_linear(dev[0], dev[1], blocked=True)  # k-blocked, read in place
+        assert kernels.is_blocked(m)
+        assert_parity(ops.grad_norm_sq(m, layer_type), np.diag(oracle.cross_gram_factorized(_np(a), _np(g), _np(a), _np(g))),
+                      torch.bfloat16, tight=roundings(2))
+
+
+def test_route_test_rep_applies_the_plan_under_a_budget(device):
+    """TracInAttributor.route_test_rep with an explicit budget: sixteen queries
+    go dense (k-blocked), a zero budget keeps them factorized, scores agree."""
+    from dattri_llm_amd.attribution import TracInAttributor
+    from dattri_llm_amd.gradient import Factorized, Gradient
+    from dattri_llm_amd.utils.cache import CacheBudget
+
+    def block(n, s, seed):  # routing consumes the block it converts, so each routing gets a fresh one
+        gen = torch.Generator().manual_seed(seed)
+        data = {f"l{i}": Factorized(_rand(gen, n, s, 64, dtype=torch.bfloat16).to(device),
+                                    _rand(gen, n, s, 64, dtype=torch.bfloat16).to(device)) for i in range(2)}
+        return Gradient(dict.fromkeys(data, "factorized"), data, dict.fromkeys(data, "nn.Linear"),
+                        dict.fromkeys(data, "batch_token"))
+
+    query, train = block(16, 16, 13), block(8, 16, 14)  # dense copies (16 x 64 x 64) outgrow the factors
+    want = sum(oracle.cross_gram_factorized(_np(train.data[n].activation), _np(train.data[n].pre_activation_grad),
+                                            _np(query.data[n].activation), _np(query.data[n].pre_activation_grad))
+               for n in ("l0", "l1"))
+    roomy = TracInAttributor(8, device, cache_budget=lambda dev: CacheBudget(limit_bytes=1 << 40))
+    dense = roomy.route_test_rep(query)
+    assert all(isinstance(v, torch.Tensor) for v in dense.data.values())
+    tight = TracInAttributor(8, device, cache_budget=lambda dev: CacheBudget(limit_bytes=0))
+    kept = tight.route_test_rep(block(16, 16, 13))
+    assert all(isinstance(v, Factorized) for v in kept.data.values())
+    for attr, rep in ((roomy, dense), (tight, kept)):
+        assert_parity(attr.inner_product(train, rep), want, torch.bfloat16, tight=roundings(3))
+
+
+def test_gradcos_query_norms_once_per_block(device):
+    """GradCos computes a query block's norms once, not once per train block."""
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.attribution import TracInAttributor
+
+    train, query = _c1_blocks(device)
+    attr = TracInAttributor(train_batch_size=8, device=device)
+    attr._set_metric(True)
+    routed = attr.route_test_rep(query)
+    with kernels.launch_events() as first:
+        a = attr.inner_product(train, routed)
+    with kernels.launch_events() as again:
+        b = attr.inner_product(train, routed)
+    assert torch.equal(a, b)
+    n_first = sum(len(v) for k, v in first.items() if k in ("ghost_gram_diag", "row_dots"))
+    n_again = sum(len(v) for k, v in again.items() if k in ("ghost_gram_diag", "row_dots"))
+    assert n_again < n_first  # the train block's norms only
+
+
 def test_layerwise_cross_dot_mixed_representations(device, ops):
     """Dense x dense (one multi-layer launch), factorized x factorized, dense x
     factorized, and a broadcast batch-1 layer, summed -- against the oracle."""
