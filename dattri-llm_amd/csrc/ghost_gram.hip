@@ -357,8 +357,9 @@ __global__ __launch_bounds__(kThreads, 2) void ghost_grouped_tiles(GroupedArgs g
   const int lr = tid >> 3;
   const int64_t t0 = m * kBM, s0 = n * kBN;
   // Rows at or past seg[B] belong to no sample (and may have no row_index
-  // entry): treat them as absent.
+  // entry): treat them as absent; a tile wholly past them has nothing to do.
   const int64_t n1 = min(G.rows1, (int64_t)G.seg1[ga.b1]), n2 = min(G.rows2, (int64_t)G.seg2[ga.b2]);
+  if (t0 >= n1 || s0 >= n2) return;
   const char* a1[4];
   const char* g1[4];
   const char* a2[4];
@@ -665,6 +666,9 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_grouped_tiles_v2(GroupedArg
   const int64_t t0 = m * v2::kBM, s0 = n * v2::kBN;
   // Rows at or past seg[B] belong to no sample (and may have no row_index entry).
   const int64_t n1 = min(G.rows1, (int64_t)G.seg1[ga.b1]), n2 = min(G.rows2, (int64_t)G.seg2[ga.b2]);
+  // A tile wholly past the packed rows of a side owns no bin (the row count a
+  // caller passes may only bound seg[B]): nothing to compute.
+  if (t0 >= n1 || s0 >= n2) return;
   TileSrc S;
   S.ra1 = make_rsrc(G.a1, 0x7fffffffu);
   S.rg1 = make_rsrc(G.g1, 0x7fffffffu);

@@ -78,6 +78,42 @@ __global__ __launch_bounds__(kWave) void moe_topk_kernel(const char* logits, int
   }
 }
 
+// Routed-row compaction: the rows p < batch * tokens whose mask byte is
+// non-zero, in increasing order, with per-sample offsets (row p = b * tokens
+// + t belongs to sample b).  One workgroup: a ballot rank inside each wave,
+// the waves' counts in LDS, and a running carry across 1024-row steps.
+__global__ __launch_bounds__(1024) void compact_rows_kernel(const uint8_t* __restrict__ mask, int64_t batch,
+                                                            int64_t tokens, int32_t* __restrict__ seg,
+                                                            int32_t* __restrict__ rows) {
+  __shared__ int32_t wave_count[16];
+  __shared__ int32_t carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t n = batch * tokens;
+  for (int64_t b = tid; b <= batch; b += 1024) seg[b] = 0;  // samples with no tokens
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base = 0; base < n; base += 1024) {
+    const int64_t p = base + tid;
+    const bool keep = p < n && mask[p] != 0;
+    const uint64_t ballot = __ballot(keep);
+    if (lane == 0) wave_count[wave] = __popcll(ballot);
+    __syncthreads();
+    int32_t rank = carry + __popcll(ballot & below);  // kept rows before p
+    for (int w = 0; w < wave; ++w) rank += wave_count[w];
+    if (p < n && p % tokens == 0) seg[p / tokens] = rank;
+    if (keep) rows[rank] = (int32_t)p;
+    __syncthreads();
+    if (tid == 0) {
+      int32_t total = carry;
+      for (int w = 0; w < 16; ++w) total += wave_count[w];
+      carry = total;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) seg[batch] = carry;
+}
+
 // keys are read either directly (slot_major == 0: key[p] = keys[p]) or as the
 // slot-major view of an (n/k, k) int64 index matrix (slot_major == 1).
 struct SortArgs {
@@ -468,6 +504,18 @@ int da_moe_route(const int64_t* index, int64_t n_tokens, int k, int n_experts, i
   a.seg = seg;
   a.rows = rows;
   moe_route_kernel<<<1, kRouteThreads, 0, (hipStream_t)stream>>>(a);
+  return check_launch(who);
+}
+
+int da_compact_rows(const uint8_t* mask, int64_t batch, int64_t tokens, int32_t* seg_offsets, int32_t* rows,
+                    void* stream) {
+  using namespace da;
+  const char* who = "da_compact_rows";
+  if (batch < 0 || tokens < 0) return set_error(DA_ERR_INVALID, "%s: negative size", who);
+  if (batch * tokens > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: at most 2^31-1 rows", who);
+  if (!seg_offsets || (batch * tokens > 0 && (!mask || !rows)))
+    return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  compact_rows_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(mask, batch, tokens, seg_offsets, rows);
   return check_launch(who);
 }
 

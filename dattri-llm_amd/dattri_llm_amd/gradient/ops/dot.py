@@ -94,7 +94,65 @@ def _linear_gram32(a1, g1, bias1, a2, g2, bias2, mode, out=None, accumulate=Fals
         return kernels.score_gemm([(m1, m2)], out=out, accumulate=accumulate)
     if mode != "factorized":
         raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
-    return kernels.ghost_gram(a1, g1, a2, g2, bias=bias1, out=out, accumulate=accumulate)
+    if out is None:
+        out = torch.zeros(b1, b2, dtype=torch.float32, device=a1.device)
+    elif not accumulate:
+        out.zero_()
+    _ghost_pairs([(a1, g1, a2, g2, bias1)], out)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# The factorized route over packed rows when most rows carry no gradient
+# ---------------------------------------------------------------------------
+
+# Take the packed route when the live rows' pairs are under this share of the
+# dense ghost's (B1*T1) x (B2*T2) rows: the packed kernel bins its products by
+# sample pair and runs at ~3/4 of the dense engine's rate, so it pays from
+# about half the work down.
+_PACKED_SHARE = 0.5
+
+
+def _live_rows(x3: torch.Tensor, y3: torch.Tensor):
+    """Per-sample ``(seg, rows)`` of the rows whose gradient row is non-zero: the
+    rows a routed expert's zero-filled (B, T, d) capture actually holds
+    (routing.py:17-23, :71-86)."""
+    b, t = y3.shape[:2]
+    return kernels.compact_rows(kernels.nonzero_rows(y3.reshape(b * t, y3.shape[-1])), b, t)
+
+
+def _ghost_pairs(pairs, out: torch.Tensor) -> None:
+    """Add the factorized cross-gram of every ``(a1, g1, a2, g2, bias)`` kernel
+    operand pair (3-D, one dtype per pair) into ``out`` (fp32, (B1, B2)).
+
+    Each side's gradient-carrying rows are found on the device (one read of
+    its gradient factor) and packed per sample; one host read of the counts
+    for all pairs decides, per pair, between the dense ghost kernel and the
+    packed grouped kernel, which runs every packed pair of a dtype in ONE
+    launch.  Both give the same sums -- zero rows contribute nothing -- so the
+    choice changes speed only.  The packed kernel's grid is sized for all
+    B*T rows; tiles past the live rows return at once."""
+    probed, plain = [], []
+    for pair in pairs:
+        a1, _g1, a2, _g2, _bias = pair
+        (plain if a1.shape[1] <= 1 and a2.shape[1] <= 1 else probed).append(pair)
+    live = [(_live_rows(a1, g1), _live_rows(a2, g2)) for a1, g1, a2, g2, _b in probed]
+    counts = torch.stack([torch.stack([s1[0][-1], s2[0][-1]]) for s1, s2 in live]).tolist() if live else []
+    packed: dict[torch.dtype, tuple[list, list, list]] = {}
+    for pair, ((seg1, rows1), (seg2, rows2)), (n1, n2) in zip(probed, live, counts):
+        a1, g1, a2, g2, bias = pair
+        rows_1, rows_2 = a1.shape[0] * a1.shape[1], a2.shape[0] * a2.shape[1]
+        if n1 * n2 >= _PACKED_SHARE * rows_1 * rows_2:
+            plain.append(pair)
+            continue
+        g_1, g_2, flags = packed.setdefault(a1.dtype, ([], [], []))
+        g_1.append((a1.reshape(rows_1, -1), g1.reshape(rows_1, -1), seg1, rows1))
+        g_2.append((a2.reshape(rows_2, -1), g2.reshape(rows_2, -1), seg2, rows2))
+        flags.append(bias)
+    for a1, g1, a2, g2, bias in plain:
+        kernels.ghost_gram(a1, g1, a2, g2, bias=bias, out=out, accumulate=True)
+    for g_1, g_2, flags in packed.values():
+        kernels.ghost_gram_grouped(g_1, g_2, bias=flags, out=out, accumulate=True)
 
 
 def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Tensor:
@@ -325,12 +383,42 @@ def layerwise_cross_dot(train, test, *, layers: Iterable[str] | None = None, mod
             rest.append((name, lt, tr, te, full))
     for group in dense_groups.values():
         kernels.score_gemm(group, out=total, accumulate=True)
+    ghost = []  # factorized-route linear pairs: probed together, packed ones in one launch
     for _name, lt, tr, te, full in rest:
-        if full:
-            _cross_dot32(tr, te, lt, mode=mode, out=total, accumulate=True)
-        else:  # a broadcast (batch-1) layer's shared row counts for every sample
+        if not full:  # a broadcast (batch-1) layer's shared row counts for every sample
             total += _expand_broadcast(_cross_dot32(tr, te, lt, mode=mode), b_tr, b_te)
+            continue
+        pair = _factorized_linear_pair(tr, te, lt, mode)
+        if pair is not None:
+            ghost.append(pair)
+        else:
+            _cross_dot32(tr, te, lt, mode=mode, out=total, accumulate=True)
+    if ghost:
+        _ghost_pairs(ghost, total)
     return total.to(out_dtype)
+
+
+def _factorized_linear_pair(f1, f2, layer_type: str, mode: str, include_bias: bool = True):
+    """Kernel operands ``(a1, g1, a2, g2, bias)`` of a factorized linear layer
+    pair the route sends to the ghost product, else None (dense sides, other
+    layer families, the materialized route, grouped factors)."""
+    if isinstance(f1, torch.Tensor) or isinstance(f2, torch.Tensor) or not is_linear(layer_type):
+        return None
+    b1, b2 = f1.as_batch_first(), f2.as_batch_first()
+    x1, y1, bias1 = final_linear(b1.activation, b1.pre_activation_grad, layer_type, b1.module_kwargs, include_bias)
+    x2, y2, bias2 = final_linear(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs, include_bias)
+    if any(to_3d(t).ndim == 4 for t in (x1, y1, x2, y2)):
+        return None
+    if bias1 != bias2:
+        raise ValueError("the two sides disagree on the bias column")
+    (x1, y1, x2, y2), _ = _kernel_operands(to_3d(x1), to_3d(y1), to_3d(x2), to_3d(y2))
+    if x1.shape[-1] != x2.shape[-1] or y1.shape[-1] != y2.shape[-1]:
+        raise ValueError("the two sides disagree on the layer widths")
+    route = mode if mode != "auto" else _route(x1.shape[0], x2.shape[0], x1.shape[1], x1.shape[-1] + int(bias1),
+                                               y1.shape[-1])
+    if route not in ("factorized", "materialized"):
+        raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
+    return (x1, y1, x2, y2, bias1) if route == "factorized" else None
 
 
 # ---------------------------------------------------------------------------

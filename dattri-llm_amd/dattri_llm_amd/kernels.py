@@ -836,6 +836,22 @@ def counting_sort(keys: torch.Tensor, bins: int, *, slot_major: bool = False,
     return offsets, perm[:n]
 
 
+def compact_rows(mask: torch.Tensor, batch: int, tokens: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(seg (B+1) int32, rows (B*T) int32)``: the rows whose mask entry is set,
+    in order, grouped by sample (row ``b*T + t``); the first ``seg[B]`` entries
+    of ``rows`` are written."""
+    dev = nat.require_device(mask)
+    n = batch * tokens
+    if mask.numel() != n:
+        raise ValueError(f"compact_rows: mask has {mask.numel()} entries, expected {n}")
+    flags = mask.contiguous().view(torch.uint8) if mask.dtype == torch.bool else mask.to(torch.uint8).contiguous()
+    seg = torch.empty(batch + 1, dtype=torch.int32, device=dev)
+    rows = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    _run(dev, "compact_rows", nat.load().da_compact_rows,
+         flags.data_ptr() if n else None, batch, tokens, seg.data_ptr(), rows.data_ptr(), nat.stream_ptr(dev))
+    return seg, rows
+
+
 def moe_route(index: torch.Tensor, n_experts: int, batch: int, tokens: int):
     """Expert routing of one side: ``(offsets (E+1), entries (N*k), seg (E, B+1),
     rows (N*k))`` int32, as documented for ``da_moe_route``."""

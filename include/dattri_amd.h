@@ -440,6 +440,21 @@ int da_moe_route(const int64_t* index, int64_t n_tokens, int k, int n_experts, i
                  void* stream);
 
 /*
+ * Routed-row compaction: of the batch * tokens rows (row p = b * tokens + t of
+ * sample b), the ones whose mask byte is non-zero, in increasing order:
+ * rows[seg_offsets[b] .. seg_offsets[b+1]) are sample b's (seg_offsets has
+ * batch + 1 entries; rows holds up to batch * tokens entries, seg_offsets[batch]
+ * of them written).  With the mask of da_nonzero_rows this finds the
+ * gradient-carrying rows of the zero-filled (B, T, d) captures the
+ * reference's routed-token layout produces for MoE experts
+ * (dattri_llm/gradient/hooks/routing.py:71-86: "zero where a sample's token
+ * was not routed to the layer"), as the (seg_offsets, row_index) pair of
+ * da_ghost_gram_grouped -- without a host round trip.
+ */
+int da_compact_rows(const uint8_t* mask, int64_t batch, int64_t tokens, int32_t* seg_offsets, int32_t* rows,
+                    void* stream);
+
+/*
  * Lane-layout self test of the MFMA conventions every kernel relies on.
  * shape 32: a and b are (32 x k) row-major with k = 16 (bf16/f16) or 8 (f32),
  *           one 16-byte chunk per lane half; out receives 64 lanes x 16
