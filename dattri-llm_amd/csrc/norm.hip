@@ -156,16 +156,31 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
   }
 }
 
+// out[b, f] = sum over the sample's chunk partials, in chunk order within
+// eight interleaved accumulators that are added in a fixed tree: the same
+// order on every call.  A thread owns four consecutive features (16-byte
+// loads); eight chunks' loads are in flight per thread.
 template <int OT>
-__global__ void norm_grad_reduce(const float* __restrict__ partial, int64_t batch, int64_t chunks,
-                                 int64_t width, char* out, int64_t out_bstride) {
-  const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void norm_grad_reduce(const float* __restrict__ partial, int64_t batch,
+                                                        int64_t chunks, int64_t width, char* out,
+                                                        int64_t out_bstride) {
+  const int64_t f = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   const int64_t b = blockIdx.y;
   if (f >= width) return;
   const float* p = partial + b * chunks * width + f;
-  float s = 0.f;
-  for (int64_t c = 0; c < chunks; ++c) s += p[c * width];
-  Elem<OT>::store(out, b * out_bstride + f, s);
+  f32x4 acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int64_t c = 0;
+  for (; c + 8 <= chunks; c += 8)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += *(const f32x4*)(p + (c + u) * width);
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (c + u < chunks) acc[u] += *(const f32x4*)(p + (c + u) * width);
+  const f32x4 s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Elem<OT>::store(out, b * out_bstride + f + e, s[e]);
 }
 
 // x_hat rows for the preprocess API: one wave per row, same math as above.
@@ -246,7 +261,7 @@ int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t 
 #undef DA_NORM_Q
   int rc = check_launch("da_norm_weight_grad(chunks)");
   if (rc) return rc;
-  dim3 g2((unsigned)((width + 255) / 256), (unsigned)a.batch);
+  dim3 g2((unsigned)((width / 4 + 255) / 256), (unsigned)a.batch);
   norm_grad_reduce<OT><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, (char*)out,
                                            out_bstride);
   return check_launch("da_norm_weight_grad(reduce)");

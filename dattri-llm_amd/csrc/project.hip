@@ -725,6 +725,38 @@ int check_rows(const void* p, int64_t rstride_bytes, const char* who, const char
 }
 
 }  // namespace
+// ---------------------------------------------------------------------------
+// Coordinate subset ("mask" projection) of per-sample linear weight gradients,
+// gathered from the factors without forming the gradient:
+//   out[b, k] = sum_t g[b, t, rows[k]] * A[b, t, cols[k]]
+// with A's column K the implicit ones column of a bias.  One thread per
+// coordinate and sample; a token row of g and of a is a few tens of KB, so the
+// scattered reads of one workgroup's 256 coordinates hit the caches.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void gather_entries_kernel(const char* a, const char* g, int64_t tokens,
+                                                             int64_t K, int64_t D, int64_t a_bs, int64_t a_ts,
+                                                             int64_t g_bs, int64_t g_ts, int has_bias,
+                                                             const int64_t* rows, const int64_t* cols, int64_t n,
+                                                             float* out, int64_t out_ld) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (k >= n) return;
+  const int64_t r = rows[k], c = cols[k];
+  float acc = 0.f;
+  // indices outside the layer contribute nothing (the host draws them in range)
+  if (r >= 0 && r < D && c >= 0 && c < K + has_bias) {
+    const char* gp = g + b * g_bs + r * Elem<DT>::kBytes;
+    const char* ap = a + b * a_bs + c * Elem<DT>::kBytes;
+    const bool ones = c == K;
+    for (int64_t t = 0; t < tokens; ++t) {
+      const float gv = Elem<DT>::load(gp + t * g_ts, 0);
+      acc += ones ? gv : gv * Elem<DT>::load(ap + t * a_ts, 0);
+    }
+  }
+  out[b * out_ld + k] = acc;
+}
+
 }  // namespace da
 
 extern "C" {
@@ -947,6 +979,35 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
     default: project_outer_reduce<DA_F16><<<g2, 256, 0, st>>>(o.partial, batch, o.chunks, width, (char*)out, out_bstride); break;
   }
   return check_launch("da_project_outer(reduce)");
+}
+
+int da_gather_entries(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens, int64_t K, int64_t D,
+                      int64_t a_bstride, int64_t a_tstride, int64_t g_bstride, int64_t g_tstride, int has_bias,
+                      const int64_t* rows, const int64_t* cols, int64_t n, float* out, int64_t out_ld,
+                      void* stream) {
+  using namespace da;
+  const char* who = "da_gather_entries";
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype %d", who, dtype);
+  if (batch < 0 || tokens < 0 || K < 0 || D < 0 || n < 0) return set_error(DA_ERR_INVALID, "%s: negative size", who);
+  if (batch == 0 || n == 0) return DA_OK;
+  if (!a || !g || !rows || !cols || !out) return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  if (out_ld < n) return set_error(DA_ERR_INVALID, "%s: out_ld < n", who);
+  if (batch > 65535) return set_error(DA_ERR_INVALID, "%s: at most 65535 samples per call", who);
+  if ((n + 255) / 256 > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: too many coordinates", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  dim3 grid((unsigned)((n + 255) / 256), (unsigned)batch);
+  hipStream_t st = (hipStream_t)stream;
+#define DA_GATHER(DT)                                                                                        \
+  gather_entries_kernel<DT><<<grid, 256, 0, st>>>((const char*)a, (const char*)g, tokens, K, D, a_bstride * es,  \
+                                                  a_tstride * es, g_bstride * es, g_tstride * es, has_bias ? 1 : 0, \
+                                                  rows, cols, n, out, out_ld)
+  switch (dtype) {
+    case DA_BF16: DA_GATHER(DA_BF16); break;
+    case DA_F16: DA_GATHER(DA_F16); break;
+    default: DA_GATHER(DA_F32); break;
+  }
+#undef DA_GATHER
+  return check_launch(who);
 }
 
 }  // extern "C"

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdattri_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 DA_F32, DA_F16, DA_BF16 = 0, 1, 2
 DA_OK, DA_ERR_INVALID, DA_ERR_UNSUPPORTED, DA_ERR_HIP, DA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -132,6 +132,10 @@ SIGNATURES.update(
              _I64, _I64, _P, _I32, _I64, _P, _SZ, _P],
         ),
         "da_moe_topk": (_I32, [_P, _I32, _I64, _I32, _I32, _I64, _P, _P, _P]),
+        "da_gather_entries": (
+            _I32,
+            [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _I64, _P, _I64, _P],
+        ),
         "da_moe_route": (_I32, [_P, _I64, _I32, _I32, _I64, _I64, _P, _P, _P, _P, _P]),
     "da_counting_sort": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _I64, _I32, _P, _P, _P]),
         "da_compact_rows": (_I32, [_P, _I64, _I64, _P, _P, _P]),

@@ -153,7 +153,8 @@ def score_sources(
         tokens = [t for t in train_rep.token_dim.values() if t is not None]
         return train_rep.batch_size * (max(tokens) if tokens else 1)
 
-    chunks, row_ids, row_steps, row_tokens = [], [], [], []
+    rows_out = _HostRows()
+    row_ids, row_steps, row_tokens = [], [], []
     for steps, train_g, ids in rebatch_blocks(train_source, batch_size):
         train_rep = transform_train(train_g.to(device))
         row = torch.zeros(n_rows(train_rep), num_test, dtype=torch.float32, device=device)
@@ -170,14 +171,7 @@ def score_sources(
                 row[:, torch.tensor(cols, device=device)] = block
         if cache is not None:
             cache.clear()
-        if row.is_cuda:
-            # an asynchronous copy into pinned host memory, so that the next
-            # block's transfer and kernels are not held behind this one's copy
-            host = torch.empty(row.shape, dtype=row.dtype, pin_memory=True)
-            host.copy_(row, non_blocking=True)
-            chunks.append(host)
-        else:
-            chunks.append(row)
+        rows_out.add(row)
         if per_token:
             t = row.shape[0] // max(len(ids), 1)
             for h, st in zip(ids, steps, strict=True):
@@ -187,7 +181,45 @@ def score_sources(
         else:
             row_ids.extend(ids)
             row_steps.extend(steps)
-    if chunks and torch.device(device).type == "cuda":
-        torch.cuda.synchronize(device)
-    scores = torch.cat(chunks, dim=0) if chunks else torch.zeros(0, num_test)
+    scores = rows_out.result(num_test)
     return scores, row_ids, row_steps, test_ids, (row_tokens if per_token else None)
+
+
+class _HostRows:
+    """Score rows produced on the device, delivered to the host in a few large
+    asynchronous copies: rows wait on the device until ``flush_bytes`` of them
+    have gathered, then go to one pinned buffer on the device's current stream.
+    The loop never waits on a copy and pays one pinned allocation per flush
+    rather than one per block (whose first allocations can stall the stream)."""
+
+    def __init__(self, flush_bytes: int = 256 << 20) -> None:
+        self.flush_bytes = flush_bytes
+        self.pending: list[torch.Tensor] = []
+        self.pending_bytes = 0
+        self.host: list[torch.Tensor] = []
+        self.device = None
+
+    def add(self, row: torch.Tensor) -> None:
+        if not row.is_cuda:
+            self.host.append(row)
+            return
+        self.device = row.device
+        self.pending.append(row)
+        self.pending_bytes += row.numel() * row.element_size()
+        if self.pending_bytes >= self.flush_bytes:
+            self._flush()
+
+    def _flush(self) -> None:
+        if not self.pending:
+            return
+        block = self.pending[0] if len(self.pending) == 1 else torch.cat(self.pending, dim=0)
+        host = torch.empty(block.shape, dtype=block.dtype, pin_memory=True)
+        host.copy_(block, non_blocking=True)
+        self.host.append(host)
+        self.pending, self.pending_bytes = [], 0
+
+    def result(self, num_test: int) -> torch.Tensor:
+        self._flush()
+        if self.device is not None:
+            torch.cuda.synchronize(self.device)
+        return torch.cat(self.host, dim=0) if self.host else torch.zeros(0, num_test)

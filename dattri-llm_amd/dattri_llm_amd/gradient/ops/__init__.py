@@ -66,12 +66,18 @@ from dattri_llm_amd.gradient.ops.projection import (
     apply_projection,
     capture_projected,
     gaussian_projector,
+    mask_coordinates,
+    mask_factorized,
+    mask_factors,
+    mask_materialized,
     maybe_materialize_projected,
     project_activation,
     project_factorized,
     project_factors,
     project_gradient,
     project_layer,
+    project_materialized,
+    project_materialized_factors,
     project_outer_factors,
     should_materialize,
 )
@@ -106,9 +112,11 @@ __all__ = [
     "extract_module_kwargs", "gaussian_projector", "get_compute_dtype", "get_routing_policy",
     "grad_norm_sq", "grad_norm_sq_factors", "is_conv", "is_conv_transpose", "is_embedding",
     "is_kfac_eligible", "is_linear", "is_norm", "layerwise_cross_dot", "layerwise_cross_dot_per_token",
+    "mask_coordinates", "mask_factorized", "mask_factors", "mask_materialized",
     "materialize", "materialize_blocked", "materialize_factors", "maybe_materialize_projected", "maybe_use_materialized_gram",
     "maybe_use_materialized_norm", "moe", "pairwise_dot", "pairwise_dot_factors", "preprocess_factorized",
     "preprocess_factors", "project_activation", "project_factorized", "project_factors",
-    "project_gradient", "project_layer", "project_outer_factors", "route_flops", "set_compute_dtype",
+    "project_gradient", "project_layer", "project_materialized", "project_materialized_factors",
+    "project_outer_factors", "route_flops", "set_compute_dtype",
     "set_routing_policy", "should_materialize", "to_3d",
 ]

@@ -19,7 +19,15 @@ Mirrors ``dattri_llm/gradient/ops/projection.py`` for the ``"logra"`` style:
   factors and the per-sample outer-product sum run as ONE kernel
   (``da_project_outer``) that reads each factor row once.
 
-``"dense"`` and ``"mask"`` styles are not on the MI355X path.
+The other two styles of ``project_layer`` (projection.py:902-944):
+
+* ``"dense"`` (TRAK): the per-sample gradient from the dW kernel, then one
+  row projection (:func:`project_materialized_factors`, projection.py:396-420);
+* ``"mask"``: ``proj_dim`` fixed random coordinates of the per-sample gradient
+  (:func:`mask_factors`, projection.py:687-811), gathered from the factors by
+  the ``da_gather_entries`` kernel without forming the gradient; the subset is
+  drawn as the reference draws it (a CPU generator seeded from ``(proj_seed,
+  width, proj_dim)``), so masked captures interchange.
 """
 
 from __future__ import annotations
@@ -30,8 +38,8 @@ import torch
 
 from dattri_llm_amd import kernels
 from dattri_llm_amd.gradient.ops import dtypes
-from dattri_llm_amd.gradient.ops.materialize import linear_dense
-from dattri_llm_amd.gradient.ops.preprocess import to_3d
+from dattri_llm_amd.gradient.ops.materialize import linear_dense, materialize_factors
+from dattri_llm_amd.gradient.ops.preprocess import final_linear, to_3d
 from dattri_llm_amd.gradient.ops.types import is_embedding, is_linear, is_norm, require_supported
 from dattri_llm_amd.utils.cache import TensorCache
 
@@ -40,6 +48,13 @@ CAPTURE_STYLES = ("factorized", "materialized", "auto")
 MASK_KEYS = frozenset({"style", "proj_dim", "proj_seed", "include_bias", "device"})
 _IDENTITY_CHUNK_ROWS = 8192
 _FUSED_MAX_WIDTH = 64
+
+
+def mask_seed(proj_seed: int, d: int, proj_dim: int) -> int:
+    """Generator seed of a ``"mask"`` coordinate subset, one per ``(seed, width,
+    size)`` -- the reference's formula (projection.py:78-80), so masked
+    gradients from both implementations keep the same coordinates."""
+    return ((proj_seed * 1_000_003 + d) * 1_000_003 + proj_dim) & ((1 << 63) - 1)
 
 
 def gaussian_matrix(d: int, proj_dim: int, proj_seed: int) -> torch.Tensor:
@@ -130,6 +145,21 @@ class DattriProjector:
         matrix = self.matrix(d_in + (1 if include_bias else 0), proj_dim=proj_dim, proj_seed=proj_seed,
                              device=device, dtype=dtype, **proj_kwargs)
         return ProjectionMatrix(matrix, include_bias, d_in, dtype, device)
+
+    def mask_indices(self, d: int, *, proj_dim: int, proj_seed: int, device) -> torch.Tensor:
+        """The sorted ``(proj_dim,)`` coordinates of a width-``d`` flat gradient
+        that a ``"mask"`` capture keeps (projection.py:202-233): drawn without
+        replacement on the CPU from :func:`mask_seed`, so every device and
+        process keeps the same subset.  Cached with the matrices."""
+        if not 0 < proj_dim <= d:
+            raise ValueError(f"a mask needs 0 < proj_dim <= d, got proj_dim={proj_dim} for a width-{d} layer.")
+        key = ("subset", d, proj_dim, proj_seed, str(device))
+        cached = self._cache.get(key)
+        if cached is None:
+            gen = torch.Generator(device="cpu").manual_seed(mask_seed(proj_seed, d, proj_dim))
+            cached = torch.randperm(d, generator=gen)[:proj_dim].sort().values.to(device)
+            self._cache.put(key, cached)
+        return cached
 
     def clear(self) -> None:
         self._cache.clear()
@@ -281,6 +311,107 @@ def capture_projected(a_p: torch.Tensor, g: torch.Tensor, p_out: ProjectionMatri
     return fused_outer(a_p.to(p_out.dtype), g.to(p_out.dtype), ident, p_out)
 
 
+def project_materialized_factors(a, g, layer_type: str, projector, module_kwargs: dict | None = None,
+                                 include_bias: bool = True, *, proj_dim: int, proj_seed: int = 0,
+                                 **proj_kwargs) -> torch.Tensor:
+    """TRAK style (projection.py:396-420): the per-sample gradient (dW or norm
+    kernel), then one projection of it to ``(B, proj_dim)``."""
+    dense = materialize_factors(a, g, layer_type, module_kwargs, include_bias)
+    return apply_projection(projector, dense, proj_dim=proj_dim, proj_seed=proj_seed, **proj_kwargs)
+
+
+def project_materialized(f, layer_type: str, projector, *, proj_dim: int, include_bias: bool = True,
+                         proj_seed: int = 0, **proj_kwargs) -> torch.Tensor:
+    """:func:`project_materialized_factors` on a :class:`Factorized`, or the
+    projection of an already dense ``(B, D)`` block (projection.py:563-596)."""
+    if isinstance(f, torch.Tensor):
+        return apply_projection(projector, f.reshape(f.shape[0], -1), proj_dim=proj_dim, proj_seed=proj_seed,
+                                **proj_kwargs)
+    bf = f.as_batch_first()
+    return project_materialized_factors(bf.activation, bf.pre_activation_grad, layer_type, projector,
+                                        bf.module_kwargs, include_bias, proj_dim=proj_dim, proj_seed=proj_seed,
+                                        **proj_kwargs)
+
+
+def _mask_options(proj_kwargs: dict, default_device) -> torch.device:
+    unknown = set(proj_kwargs) - MASK_KEYS
+    if unknown:
+        raise ValueError(
+            "style 'mask' keeps coordinates rather than projecting, so it takes only "
+            f"{sorted(MASK_KEYS - {'style'})}; got unexpected {sorted(unknown)}."
+        )
+    return torch.device(proj_kwargs.get("device", default_device))
+
+
+def mask_coordinates(projection: dict | None, layer_name: str, width: int, projector,
+                     device="cpu") -> torch.Tensor | None:
+    """The coordinates a ``"mask"`` capture of ``layer_name`` kept
+    (projection.py:628-659), from the capture's projection config; None when
+    the layer is not masked.  Any other style raises: a projected gradient's
+    entries are not coordinates."""
+    if projection is None:
+        return None
+    kw = projection.get(layer_name, projection.get("__default__"))
+    if kw is None:
+        return None
+    style = kw.get("style", "logra")
+    if style != "mask":
+        raise ValueError(
+            f"layer {layer_name!r} is captured with style {style!r}; coordinate-wise maps need exact gradient "
+            "entries, i.e. no projection or style 'mask'."
+        )
+    return DattriProjector.coerce(projector).mask_indices(width, proj_dim=kw["proj_dim"],
+                                                          proj_seed=kw.get("proj_seed", 0), device=torch.device(device))
+
+
+def mask_materialized(x: torch.Tensor, projector, *, proj_dim: int, proj_seed: int = 0,
+                      **proj_kwargs) -> torch.Tensor:
+    """``proj_dim`` fixed random coordinates of a dense ``(..., D)`` block
+    (projection.py:662-684)."""
+    device = _mask_options(proj_kwargs, x.device)
+    x = x.to(device)
+    idx = DattriProjector.coerce(projector).mask_indices(x.shape[-1], proj_dim=proj_dim, proj_seed=proj_seed,
+                                                         device=device)
+    return x.index_select(-1, idx)
+
+
+def mask_factors(a, g, layer_type: str, projector, module_kwargs: dict | None = None, include_bias: bool = True,
+                 *, proj_dim: int, proj_seed: int = 0, **proj_kwargs) -> torch.Tensor:
+    """``materialize_factors(...)[:, mask]`` without materializing
+    (projection.py:687-783): linear layers gather each kept entry
+    ``sum_t g[b,t,o] * a[b,t,i]`` straight from the factors (``da_gather_entries``,
+    flat index ``o*(K+bias) + i``); norm layers are small and are materialized
+    (norm kernel), then gathered.  Returns ``(B, proj_dim)``."""
+    device = _mask_options(proj_kwargs, g.device)
+    proj = DattriProjector.coerce(projector)
+    if is_norm(layer_type):
+        dense = materialize_factors(a, g, layer_type, module_kwargs, include_bias).to(device)
+        idx = proj.mask_indices(dense.shape[-1], proj_dim=proj_dim, proj_seed=proj_seed, device=device)
+        return dense.index_select(-1, idx)
+    if is_embedding(layer_type) or not is_linear(layer_type):
+        require_supported(layer_type, "mask_factors")
+    x, y, bias = final_linear(a, g, layer_type, module_kwargs, include_bias)
+    out_dtype = dtypes.resolve(x, y)
+    x, y = (t.to(device=device, dtype=dtypes.kernel_dtype(out_dtype)) for t in dtypes.align(to_3d(x), to_3d(y)))
+    if x.ndim == 4:
+        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
+    cols = x.shape[-1] + int(bias)
+    idx = proj.mask_indices(y.shape[-1] * cols, proj_dim=proj_dim, proj_seed=proj_seed, device=device)
+    return kernels.gather_entries(x, y, idx // cols, idx % cols, bias=bias).to(out_dtype)
+
+
+def mask_factorized(f, layer_type: str, projector, *, proj_dim: int, include_bias: bool = True,
+                    proj_seed: int = 0, **proj_kwargs) -> torch.Tensor:
+    """:func:`mask_factors` on a :class:`Factorized`, or
+    :func:`mask_materialized` of a dense ``(B, D)`` block (projection.py:814-843)."""
+    if isinstance(f, torch.Tensor):
+        return mask_materialized(f.reshape(f.shape[0], -1), projector, proj_dim=proj_dim, proj_seed=proj_seed,
+                                 **proj_kwargs)
+    bf = f.as_batch_first()
+    return mask_factors(bf.activation, bf.pre_activation_grad, layer_type, projector, bf.module_kwargs,
+                        include_bias, proj_dim=proj_dim, proj_seed=proj_seed, **proj_kwargs)
+
+
 def maybe_materialize_projected(seq_len: int, k_a: int, k_g: int, kappa: float = 1.0) -> bool:
     """Capture-time rule: materialize iff ``S >= kappa*k_a*k_g/(k_a+k_g)``
     (projection.py:846-874)."""
@@ -310,14 +441,19 @@ def project_factorized(f, layer_type: str, projector, *, proj_dim: int, include_
 
 def project_layer(f, layer_type: str, projector, *, style: str = "logra", capture_style: str = "factorized",
                   **proj_kwargs):
-    """Route one layer through a projection style (projection.py:902-944).
+    """Route one layer through a projection style (projection.py:902-944):
+    ``(payload, is_factorized)``.
 
     ``"logra"`` keeps ``(a_p, g_p)`` or -- when :func:`should_materialize`
-    says so -- returns the ``(B, k_g*k_a)`` block from the fused kernel."""
+    says so -- returns the ``(B, k_g*k_a)`` block from the fused kernel;
+    ``"dense"`` projects the per-sample gradient; ``"mask"`` keeps fixed
+    coordinates of it.  A dense input takes the ``"dense"`` path unless masked."""
     if style not in PROJECTION_STYLES:
         raise ValueError(f"style must be one of {PROJECTION_STYLES}, got {style!r}.")
-    if style != "logra" or isinstance(f, torch.Tensor):
-        raise NotImplementedError(f"projection style {style!r} is not on the MI355X path (use 'logra')")
+    if style == "mask":
+        return mask_factorized(f, layer_type, projector, **proj_kwargs), False
+    if style == "dense" or isinstance(f, torch.Tensor):
+        return project_materialized(f, layer_type, projector, **proj_kwargs), False
     bf = f.as_batch_first()
     a, g = bf.activation, bf.pre_activation_grad
     seq_len = a.shape[1] if a.ndim >= 3 else 1

@@ -792,6 +792,33 @@ def project_outer(a: torch.Tensor, g: torch.Tensor, pin_t: torch.Tensor, pout_t:
     return out
 
 
+def gather_entries(a: torch.Tensor, g: torch.Tensor, rows: torch.Tensor, cols: torch.Tensor, *,
+                   bias: bool = False) -> torch.Tensor:
+    """fp32 ``(B, n)``: entries ``(rows[k], cols[k])`` of every sample's linear
+    weight gradient ``sum_t g[b,t,:]^T [a[b,t,:], 1]``, gathered from the
+    factors (a (B, T, K), g (B, T, D); column K is the bias column)."""
+    dev = nat.require_device(a, g, rows, cols)
+    if a.dim() != 3 or g.dim() != 3 or a.shape[:2] != g.shape[:2]:
+        raise ValueError("gather_entries expects a (B, T, K) and g (B, T, D)")
+    if a.dtype != g.dtype:
+        raise ValueError("gather_entries factors must share one dtype")
+    if rows.shape != cols.shape or rows.dim() != 1:
+        raise ValueError("rows and cols must be matching 1-D index tensors")
+    if a.stride(-1) != 1 or g.stride(-1) != 1:
+        a, g = a.contiguous(), g.contiguous()
+    rows, cols = rows.to(torch.int64).contiguous(), cols.to(torch.int64).contiguous()
+    b, t, k = a.shape
+    n = rows.numel()
+    out = torch.empty(b, n, dtype=torch.float32, device=dev)
+    if b == 0 or n == 0:
+        return out
+    _run(dev, "gather_entries", nat.load().da_gather_entries,
+         a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, g.shape[-1], a.stride(0), a.stride(1),
+         g.stride(0), g.stride(1), int(bias), rows.data_ptr(), cols.data_ptr(), n, out.data_ptr(), out.stride(0),
+         nat.stream_ptr(dev))
+    return out
+
+
 def moe_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Router top-k of softmax(logits) -> (weights (N, k) fp32, indices (N, k) int64)."""
     dev = nat.require_device(logits)

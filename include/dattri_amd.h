@@ -389,6 +389,24 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
                      size_t workspace_bytes, void* stream);
 
 /*
+ * A coordinate subset of per-sample linear weight gradients (the "mask"
+ * projection style), gathered from the factors without forming the gradient:
+ *
+ *   out[b*out_ld + k] = sum_t g[b, t, rows[k]] * A[b, t, cols[k]],   k < n,
+ *
+ * fp32, where A is a (B, T, K) with, when has_bias, an implicit ones column at
+ * index K.  rows/cols (int64, device) are the coordinates' output and input
+ * indices (flat index o*(K+bias) + i of the materialized gradient); entries
+ * outside the layer contribute 0.  Replaces mask_factors for linear layers,
+ * dattri_llm/gradient/ops/projection.py:687-783 (_gather_pairs,
+ * projection.py:786-811).
+ */
+int da_gather_entries(const void* a, const void* g, int dtype, int64_t batch, int64_t tokens, int64_t K, int64_t D,
+                      int64_t a_bstride, int64_t a_tstride, int64_t g_bstride, int64_t g_tstride, int has_bias,
+                      const int64_t* rows, const int64_t* cols, int64_t n, float* out, int64_t out_ld,
+                      void* stream);
+
+/*
  * MoE router: per token, top-k of softmax(logits) (fp32, a NaN or +inf logit
  * or an all -inf row gives NaN probabilities as torch's softmax does), weights
  * renormalised over the k, indices in the order torch.topk returns on the CPU,

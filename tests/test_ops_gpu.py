@@ -310,6 +310,45 @@ def test_capture_projected_and_routing(device, ops):
     assert not is_fact and payload.shape == (2, 32 * 32)  # T=70 >= H=16: materialized
 
 
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mask_and_dense_projection_styles(device, ops, bias, dtype):
+    """project_layer's "mask" style gathers the kept entries of the per-sample
+    gradient straight from the factors (equal to indexing the oracle's
+    materialized gradient); "dense" projects the materialized gradient with
+    the projector's own matrix."""
+    gen = torch.Generator().manual_seed(15)
+    a, g = _rand(gen, 3, 50, 40, dtype=dtype), _rand(gen, 3, 50, 24, dtype=dtype)
+    mk = {"has_bias": bias}
+    from dattri_llm_amd.gradient import Factorized
+
+    f = Factorized(a.to(device), g.to(device), module_kwargs=mk)
+    proj = ops.DattriProjector()
+    width = 24 * (40 + int(bias))
+    dense_ref = oracle.materialize_linear(_np(a), _np(g), bias=bias)
+    masked, is_fact = ops.project_layer(f, "nn.Linear", proj, style="mask", proj_dim=100, proj_seed=2)
+    assert not is_fact and masked.shape == (3, 100) and masked.dtype == dtype
+    idx = proj.mask_indices(width, proj_dim=100, proj_seed=2, device="cpu").numpy()
+    assert_parity(masked, dense_ref[:, idx], dtype, label="mask")
+    projected, is_fact = ops.project_layer(f, "nn.Linear", proj, style="dense", proj_dim=16, proj_seed=5)
+    assert not is_fact and projected.shape == (3, 16)
+    p = ops.projection.gaussian_matrix(width, 16, 5).double().numpy()
+    # the dense gradient, the matrix and the result are held in the compute dtype
+    tight = None if dtype == torch.float32 else roundings(3)
+    assert_parity(projected, dense_ref @ p, dtype, tight=tight, label="dense")
+    # a dense block takes the same two styles
+    block = ops.materialize(f, "nn.Linear")
+    assert torch.equal(ops.mask_factorized(block, "nn.Linear", proj, proj_dim=100, proj_seed=2),
+                       block[:, torch.from_numpy(idx).to(device)])
+    norm = Factorized(a.to(device), a.to(device), module_kwargs={"has_bias": False, "eps": 1e-5,
+                                                                  "normalized_shape": (40,)})
+    got = ops.mask_factors(norm.activation, norm.pre_activation_grad, "nn.RMSNorm", proj, norm.module_kwargs,
+                           proj_dim=7, proj_seed=1)
+    nidx = proj.mask_indices(40, proj_dim=7, proj_seed=1, device="cpu").numpy()
+    want = oracle.norm_weight_grad(_np(a), _np(a), "nn.RMSNorm", 1e-5)[:, nidx]
+    assert_parity(got, want, dtype, tight=None if dtype == torch.float32 else roundings(1), label="norm mask")
+
+
 def test_project_outer_c3_geometry_subset(device):
     """C3 shapes (down_proj 11008 -> 4096, T=128, proj 64) on 4 samples."""
     from dattri_llm_amd import kernels
