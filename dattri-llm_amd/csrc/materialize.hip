@@ -18,6 +18,8 @@
 // their rows 8 apart and folds them onto two bank groups.  A workgroup owns a 128 (o) x 128 (k) output tile of one
 // sample; the fp32 accumulators are converted to the output dtype and staged
 // through LDS so the tile leaves as coalesced 16-byte row stores.
+#include <atomic>
+
 #include "common.h"
 
 namespace da {
@@ -442,9 +444,22 @@ __global__ __launch_bounds__(kThreads, 1) void materialize_tiles_tr(MatArgs m) {
     }
     tn = tm + r;
   } else {
+    // When every sample's tile count divides by 8, XCD x takes the x-th
+    // eighth of each sample in turn, so all XCDs stream one sample's factors
+    // at a time (a working set the MALL keeps); otherwise XCD x takes the
+    // x-th eighth of all tiles.  Within an XCD, the tiles running together
+    // are consecutive in the grouped order below.
     const int64_t per_sample = m.tiles_m * m.tiles_n;
-    b = logical / per_sample;
-    const int64_t rem = logical - b * per_sample;
+    int64_t rem;
+    if (per_sample % kXcds == 0) {
+      const int64_t chunk = per_sample / kXcds;
+      const int64_t xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
+      b = local / chunk;
+      rem = xcd * chunk + local % chunk;
+    } else {
+      b = logical / per_sample;
+      rem = logical - b * per_sample;
+    }
     const int64_t per_group = (int64_t)trk::kGroup * m.tiles_n;
     const int64_t group = rem / per_group;
     const int64_t first = group * trk::kGroup;
@@ -761,11 +776,13 @@ int launch(const MatArgs& m, int has_bias, hipStream_t st) {
     mb.tiles_n = (m.k + big::kBN - 1) / big::kBN;
     const int64_t nb = m.batch * mb.tiles_m * mb.tiles_n;
     const size_t lds = 2 * (size_t)big::kStageBytes;
-    static bool attr_set = false;  // idempotent; per template instance
-    if (!attr_set) {
-      hipFuncSetAttribute((const void*)materialize_tiles_big<DT, OT>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      attr_set = true;
+    // Idempotent, so racing first calls are harmless; per template instance.
+    static std::atomic<bool> attr_set{false};
+    if (!attr_set.load(std::memory_order_relaxed)) {
+      if (hipFuncSetAttribute((const void*)materialize_tiles_big<DT, OT>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return set_error(DA_ERR_HIP, "da_materialize_linear: hipFuncSetAttribute failed");
+      attr_set.store(true, std::memory_order_relaxed);
     }
     materialize_tiles_big<DT, OT><<<(unsigned)nb, kThreads, lds, st>>>(mb);
     int rc = check_launch("da_materialize_linear(big tiles)");
