@@ -16,6 +16,8 @@
 // wave accumulates x_hat*g (and g) for its lanes' features across the rows it
 // visits.  The four waves of a workgroup combine through LDS and write one fp32
 // partial per (sample, token chunk); a second kernel sums the chunks in order.
+// Rows of up to 8 KB stream through a per-wave LDS ring (norm_grad_ring);
+// longer rows are loaded straight into registers (norm_grad_chunks).
 #include "common.h"
 
 namespace da {
@@ -156,31 +158,242 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
   }
 }
 
-// out[b, f] = sum over the sample's chunk partials, in chunk order within
-// eight interleaved accumulators that are added in a fixed tree: the same
-// order on every call.  A thread owns four consecutive features (16-byte
-// loads); eight chunks' loads are in flight per thread.
+// The same per-chunk partials with the rows streamed into LDS: each wave owns
+// a private ring of two slots (one token row of x and of g per slot) filled
+// by non-temporal buffer loads with the LDS-direct bit, so the next row is in
+// flight while the current one is reduced and no VGPRs hold data in flight.
+// A slot holds the row's bytes as they are (instruction j of an operand
+// carries 16-byte chunks 64j .. 64j+63), so lane l reads chunk l + 64q with
+// one conflict-free 16-byte LDS read.  No barriers in the row loop: only
+// wave w touches its slots.  Rows past the chunk and chunks past the width
+// load zeros from no memory, so every row issues the same 2*kQ instructions
+// and one vmcnt count holds.  At 8 KB rows the ring takes 128 KB (4 waves x
+// 2 slots x 16 KB); three waves with three slots each measured 5% slower.
+// acc + lo^2 + hi^2 of a packed pair of 16-bit values (v_dot2_f32_bf16 / _f16).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <int DT>
+__device__ __forceinline__ float dot2_sq(uint32_t w, float acc) {
+  if constexpr (DT == DA_BF16) {
+    const bf16x2_t v = __builtin_bit_cast(bf16x2_t, w);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  } else {
+    const f16x2_t v = __builtin_bit_cast(f16x2_t, w);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  }
+}
+
+constexpr int kRingRowsPerWG = 64;  // token rows per workgroup for the ring form
+constexpr int kRingSlots = 2;
+constexpr int ring_waves(int) { return 4; }
+
+template <int DT, int kQ, bool kBias>
+__global__ __launch_bounds__(ring_waves(kQ) * kWave, 1) void norm_grad_ring(NormArgs a) {
+  static_assert(kQ <= 8, "ring slots are sized for at most 8 KB rows");
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int NW = ring_waves(kQ);
+  constexpr int kRowBytes = kQ * kWave * 16;          // one operand's row, padded to kQ KB
+  constexpr int kSlot = 2 * kRowBytes;                // x row, then g row
+  __shared__ __attribute__((aligned(1024))) char ring[NW * kRingSlots * kSlot];
+  // After the rows, the waves combine through the ring's first bytes.
+  static_assert((kBias ? 2 : 1) * kQ * kWave * VEC * 4 <= NW * kRingSlots * kSlot, "combine buffer");
+  float* const comb = (float*)ring;
+
+  const int64_t b = blockIdx.y, chunk = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int uwave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t nchunk16 = a.d / VEC;
+  const float inv_d = 1.f / (float)a.d;
+  const u32x4 rx = make_rsrc(a.x + b * a.x_bstride, (uint32_t)(a.tokens * a.x_tstride));
+  const u32x4 rg = make_rsrc(a.g + b * a.g_bstride, (uint32_t)(a.tokens * a.g_tstride));
+  const uint32_t xts = (uint32_t)a.x_tstride, gts = (uint32_t)a.g_tstride;
+  const uint32_t lds_w = (uint32_t)(uintptr_t)(ring + uwave * kRingSlots * kSlot);
+  const lds_char* const slot_ptr = (const lds_char*)(ring + uwave * kRingSlots * kSlot);
+
+  const int64_t t_begin = chunk * kRingRowsPerWG;
+  const int64_t t_end = min(t_begin + kRingRowsPerWG, a.tokens);
+  const int nrows = (int)((t_end - t_begin - uwave + NW - 1) / NW);  // this wave's rows (may be <= 0)
+
+  // Row i of this wave is token t_begin + uwave + NW*i, in slot i % 2.
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    const bool live = i < nrows;
+    const uint32_t t = (uint32_t)(t_begin + uwave + (int64_t)NW * i);
+    const uint32_t lbase = lds_w + (uint32_t)((i % kRingSlots) * kSlot);
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+      const bool in = live && lane + (int64_t)j * kWave < nchunk16;
+      const uint32_t col = (uint32_t)((lane + j * kWave) * 16);
+      dma16_nt(rx, lbase + (uint32_t)(j * kWave * 16), in ? t * xts + col : 0x80000000u);
+    }
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+      const bool in = live && lane + (int64_t)j * kWave < nchunk16;
+      const uint32_t col = (uint32_t)((lane + j * kWave) * 16);
+      dma16_nt(rg, lbase + (uint32_t)(kRowBytes + j * kWave * 16), in ? t * gts + col : 0x80000000u);
+    }
+  };
+
+  float dg[kQ][VEC], db[kBias ? kQ : 1][VEC];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dg[q][e] = 0.f;
+#pragma unroll
+  for (int q = 0; q < (kBias ? kQ : 1); ++q)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) db[q][e] = 0.f;
+
+  issue(0);
+  for (int i = 0; i < nrows; ++i) {
+    // The slot row i + 1 fills held row i - 1, whose reads have returned
+    // (lgkmcnt); then row i is awaited, row i + 1's 2*kQ instructions
+    // staying in flight.
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    issue(i + 1);
+    if constexpr (kQ == 1) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if constexpr (kQ == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if constexpr (kQ == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    const lds_char* sx = slot_ptr + (i % kRingSlots) * kSlot;
+    u32x4 vx[kQ], vg[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      vx[q] = *(const __attribute__((address_space(3))) u32x4*)(sx + (lane + q * kWave) * 16);
+      vg[q] = *(const __attribute__((address_space(3))) u32x4*)(sx + kRowBytes + (lane + q * kWave) * 16);
+    }
+    if (DT != DA_F32 && a.kind != 1) {
+      // Zero mean (RMSNorm, or as given): the mean square comes from 16-bit
+      // pairs through v_dot2 (both products exact in fp32), and the padding
+      // lanes read zeros.
+      float ss = 0.f;
+      if (a.kind == 0) {
+#pragma unroll
+        for (int q = 0; q < kQ; ++q)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) ss = dot2_sq<DT>(vx[q][w], ss);
+      }
+      const float rstd = a.kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + a.eps);
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float gv = elem_of<DT>(vg[q], e);
+          dg[q][e] += (elem_of<DT>(vx[q], e) * rstd) * gv;
+          if constexpr (kBias) db[q][e] += gv;
+        }
+      continue;
+    }
+    float mean = 0.f;
+    if (a.kind == 1) {
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += elem_of<DT>(vx[q], e);
+      mean = wave_sum(s) * inv_d;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const bool in = lane + (int64_t)q * kWave < nchunk16;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float c = in ? elem_of<DT>(vx[q], e) - mean : 0.f;
+        ss += c * c;
+      }
+    }
+    const float rstd = a.kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + a.eps);
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float gv = elem_of<DT>(vg[q], e);
+        dg[q][e] += (elem_of<DT>(vx[q], e) - mean) * rstd * gv;
+        if constexpr (kBias) db[q][e] += gv;
+      }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zero-fill loads past the last row
+  __syncthreads();  // every wave is done with its slots before they hold the combine buffer
+
+  // Combine the waves in order 0 + 1 + ... through LDS, then wave 0 writes.
+  const int64_t width = (1 + a.has_bias) * a.d;
+  for (int w = 1; w < NW; ++w) {
+    if (uwave == w) {
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          comb[(q * kWave + lane) * VEC + e] = dg[q][e];
+          if constexpr (kBias) comb[(kQ * kWave + q * kWave + lane) * VEC + e] = db[q][e];
+        }
+    }
+    __syncthreads();
+    if (uwave == 0) {
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          dg[q][e] += comb[(q * kWave + lane) * VEC + e];
+          if constexpr (kBias) db[q][e] += comb[(kQ * kWave + q * kWave + lane) * VEC + e];
+        }
+    }
+    __syncthreads();
+  }
+  if (uwave == 0) {
+    float* dst = a.partial + (b * a.chunks + chunk) * width;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int64_t c = lane + (int64_t)q * kWave;
+      if (c < nchunk16) {
+        *(f32x4*)(dst + c * VEC) = f32x4{dg[q][0], dg[q][1], dg[q][2], dg[q][3]};
+        if constexpr (VEC == 8) *(f32x4*)(dst + c * VEC + 4) = f32x4{dg[q][4], dg[q][5], dg[q][6], dg[q][7]};
+        if constexpr (kBias) {
+          *(f32x4*)(dst + a.d + c * VEC) = f32x4{db[q][0], db[q][1], db[q][2], db[q][3]};
+          if constexpr (VEC == 8)
+            *(f32x4*)(dst + a.d + c * VEC + 4) = f32x4{db[q][4], db[q][5], db[q][6], db[q][7]};
+        }
+      }
+    }
+  }
+}
+
+// out[b, f] = sum over the sample's chunk partials in a fixed order: the
+// chunks are split into four consecutive groups, one per wave; within a group
+// eight interleaved accumulators run in chunk order and are added in a fixed
+// tree, and the four group sums are added as (g0 + g1) + (g2 + g3).  The same
+// order on every call.  A lane owns four consecutive features (16-byte loads);
+// a workgroup covers 64 feature quads of one sample.
 template <int OT>
 __global__ __launch_bounds__(256) void norm_grad_reduce(const float* __restrict__ partial, int64_t batch,
                                                         int64_t chunks, int64_t width, char* out,
                                                         int64_t out_bstride) {
-  const int64_t f = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  __shared__ f32x4 red[3][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t f = ((int64_t)blockIdx.x * 64 + lane) * 4;
   const int64_t b = blockIdx.y;
-  if (f >= width) return;
-  const float* p = partial + b * chunks * width + f;
+  const int64_t per = (chunks + 3) / 4;
+  const int64_t c0 = min(chunks, grp * per), c1 = min(chunks, c0 + per);
   f32x4 acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int64_t c = 0;
-  for (; c + 8 <= chunks; c += 8)
+  if (f < width) {
+    const float* p = partial + b * chunks * width + f;
+    int64_t c = c0;
+    for (; c + 8 <= c1; c += 8)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[u] += *(const f32x4*)(p + (c + u) * width);
+      for (int u = 0; u < 8; ++u) acc[u] += *(const f32x4*)(p + (c + u) * width);
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
-    if (c + u < chunks) acc[u] += *(const f32x4*)(p + (c + u) * width);
+    for (int u = 0; u < 8; ++u)
+      if (c + u < c1) acc[u] += *(const f32x4*)(p + (c + u) * width);
+  }
   const f32x4 s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  if (grp > 0) red[grp - 1][lane] = s;
+  __syncthreads();
+  if (grp == 0 && f < width) {
+    const f32x4 t = (s + red[0][lane]) + (red[1][lane] + red[2][lane]);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) Elem<OT>::store(out, b * out_bstride + f + e, s[e]);
+    for (int e = 0; e < 4; ++e) Elem<OT>::store(out, b * out_bstride + f + e, t[e]);
+  }
 }
 
 // x_hat rows for the preprocess API: one wave per row, same math as above.
@@ -244,24 +457,43 @@ int pick_q(int64_t d, int64_t vec) {
 template <int DT, int OT>
 int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t st) {
   const int64_t width = (1 + a.has_bias) * a.d;
-  const size_t lds = (size_t)width * sizeof(float);
-  dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
+  // The ring form addresses a sample's rows with 32-bit buffer offsets.
+  const int64_t max_ts = a.x_tstride > a.g_tstride ? a.x_tstride : a.g_tstride;
+  if (q <= 8 && a.tokens * max_ts < (1LL << 31)) {
+    a.chunks = (a.tokens + kRingRowsPerWG - 1) / kRingRowsPerWG;
+    dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
+#define DA_NORM_RING(Q)                                       \
+  if (a.has_bias)                                             \
+    norm_grad_ring<DT, Q, true><<<grid, ring_waves(Q) * kWave, 0, st>>>(a); \
+  else                                                                      \
+    norm_grad_ring<DT, Q, false><<<grid, ring_waves(Q) * kWave, 0, st>>>(a)
+    switch (q) {
+      case 1: DA_NORM_RING(1); break;
+      case 2: DA_NORM_RING(2); break;
+      case 4: DA_NORM_RING(4); break;
+      default: DA_NORM_RING(8); break;
+    }
+#undef DA_NORM_RING
+  } else {
+    const size_t lds = (size_t)width * sizeof(float);
+    dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
 #define DA_NORM_Q(Q)                                              \
   if (a.has_bias)                                                 \
     norm_grad_chunks<DT, Q, true><<<grid, kThreads, lds, st>>>(a); \
   else                                                            \
     norm_grad_chunks<DT, Q, false><<<grid, kThreads, lds, st>>>(a)
-  switch (q) {
-    case 1: DA_NORM_Q(1); break;
-    case 2: DA_NORM_Q(2); break;
-    case 4: DA_NORM_Q(4); break;
-    case 8: DA_NORM_Q(8); break;
-    default: DA_NORM_Q(16); break;
-  }
+    switch (q) {
+      case 1: DA_NORM_Q(1); break;
+      case 2: DA_NORM_Q(2); break;
+      case 4: DA_NORM_Q(4); break;
+      case 8: DA_NORM_Q(8); break;
+      default: DA_NORM_Q(16); break;
+    }
 #undef DA_NORM_Q
+  }
   int rc = check_launch("da_norm_weight_grad(chunks)");
   if (rc) return rc;
-  dim3 g2((unsigned)((width / 4 + 255) / 256), (unsigned)a.batch);
+  dim3 g2((unsigned)((width / 4 + 63) / 64), (unsigned)a.batch);
   norm_grad_reduce<OT><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, (char*)out,
                                            out_bstride);
   return check_launch("da_norm_weight_grad(reduce)");
