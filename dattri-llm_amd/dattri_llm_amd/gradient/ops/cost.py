@@ -9,9 +9,10 @@ time model prices each term at the rate its kernel actually achieves:
 
     t_F = 2*B1*B2*S1*S2*(K+D) / R_ghost                               + 1 launch
     t_M = 2*(B1*S1 + B2*S2)*D*K / R_mat
-          + (B1+B2)*D*K*e / R_stream   (dW written once and read once)  + 3 launches
+          + 2*(B1+B2)*D*K*e / R_stream (dW written once and read once)  + 3 launches
 
-with ``e`` the element size.  The rates come from :func:`calibrate` (timed
+with ``e`` the element size, and each extent rounded up to the kernel's tile
+(ghost: 256 x 128 tokens; dW: 256 x 256 outputs, 32-token stages).  The rates come from :func:`calibrate` (timed
 kernels on the current GPU) or the committed MI355X measurement.
 
 ``set_routing_policy("calibrated")`` makes ``maybe_use_materialized_gram`` use
@@ -56,12 +57,21 @@ class CostModel:
     elem_bytes: int = 2
     source: str = ""
 
+    # The kernels run whole tiles: the ghost tile is 256 (side-1 tokens) x 128
+    # (side-2 tokens), the dW tile 256 x 256 outputs over 32-token stages.  The
+    # rates are measured on whole tiles, so each term is priced on the padded
+    # work its kernel actually does.
+    @staticmethod
+    def _up(n, m):
+        return -(-n // m) * m
+
     def time_factorized(self, b1, b2, s1, s2, k, d) -> float:
-        flops = 2.0 * b1 * b2 * s1 * s2 * (k + d)
+        flops = 2.0 * b1 * b2 * self._up(s1, 256) * self._up(s2, 128) * (k + d)
         return flops / (self.ghost_tflops * 1e12) + self.launch_us * 1e-6
 
     def time_materialized(self, b1, b2, s1, s2, k, d) -> float:
-        flops = 2.0 * (b1 * s1 + b2 * s2) * d * k
+        tiles = self._up(d, 256) * self._up(k, 256)
+        flops = 2.0 * (b1 * self._up(s1, 32) + b2 * self._up(s2, 32)) * tiles
         stream = 2.0 * (b1 + b2) * d * k * self.elem_bytes
         return (flops / (self.materialize_tflops * 1e12) + stream / (self.stream_gbs * 1e9)
                 + 3 * self.launch_us * 1e-6)
@@ -91,8 +101,17 @@ def use_model(model: CostModel) -> None:
 
 
 def calibrate(device=None, repeats: int = 3) -> CostModel:
-    """Time the three kernels on the current GPU at mid-size shapes and return
-    the rates (TFLOP/s for the MFMA kernels, GB/s for the score stream)."""
+    """Time the three kernels on the current GPU at the shapes the routes run
+    at and return the rates (TFLOP/s for the MFMA kernels, GB/s for the score
+    stream):
+
+    * ghost: 32 x 16 sample pairs of a d = 4096 linear at T = 512 (a slice of
+      the 256 x 64 ghost workload);
+    * dW: 8 samples x 2048 tokens of a 4096 -> 14336 linear (the Llama-3-8B
+      block's gate projection);
+    * score stream: 8 train x 64 query rows of the same layer's dense
+      gradients (58.7 M weights, k-blocked as the dW kernel writes them).
+    """
     import torch
 
     from dattri_llm_amd import kernels
@@ -117,16 +136,22 @@ def calibrate(device=None, repeats: int = 3) -> CostModel:
             best = min(best, s.elapsed_time(e) * 1e-3)
         return best
 
-    b, t, k = 32, 512, 4096
-    a1, g1 = rnd(b, t, k), rnd(b, t, k)
-    a2, g2 = rnd(8, t, k), rnd(8, t, k)
+    b1, b2, t, k = 32, 16, 512, 4096
+    a1, g1 = rnd(b1, t, k), rnd(b1, t, k)
+    a2, g2 = rnd(b2, t, k), rnd(b2, t, k)
     t_ghost = timed(lambda: kernels.ghost_gram(a1, g1, a2, g2))
-    ghost = 2.0 * b * 8 * t * t * 2 * k / t_ghost / 1e12
-    t_mat = timed(lambda: kernels.materialize_linear(a1[:8], g1[:8]))
-    mat = 2.0 * 8 * t * k * k / t_mat / 1e12
-    m1 = rnd(8, k * k)
-    m2 = rnd(64, k * k)
+    ghost = 2.0 * b1 * b2 * t * t * 2 * k / t_ghost / 1e12
+    del a1, g1, a2, g2
+    bm, tm, km, dm = 8, 2048, 4096, 14336
+    a, g = rnd(bm, tm, km), rnd(bm, tm, dm)
+    t_mat = timed(lambda: kernels.materialize_linear(a, g, blocked=True))
+    mat = 2.0 * bm * tm * km * dm / t_mat / 1e12
+    m1 = kernels.materialize_linear(a, g, blocked=True)
+    del a, g
+    m2 = rnd(km * dm // 64, 64, 64).permute(1, 0, 2)  # k-blocked (64, W/64, 64) view
     t_score = timed(lambda: kernels.score_gemm([(m1, m2)]))
-    stream = (8 + 64) * k * k * 2 / t_score / 1e9
+    stream = (8 + 64) * km * dm * 2 / t_score / 1e9
     name = torch.cuda.get_device_name(dev)
-    return CostModel(round(ghost, 1), round(mat, 1), round(stream, 1), source=f"calibrate() on {name}")
+    return CostModel(round(ghost, 1), round(mat, 1), round(stream, 1),
+                     source=f"calibrate(repeats={repeats}) on {name}: ghost 32x16 pairs T=512 d=4096; "
+                            f"dW 8 x 2048 tokens 4096->14336; score 8x64 rows of the k-blocked 4096x14336 layer")
