@@ -249,6 +249,160 @@ class Gradient:
         data = {n: v.to(device=device, dtype=dtype, non_blocking=non_blocking) for n, v in self.data.items()}
         return Gradient(dict(self.representation), data, self.layer_types, dict(self.indexing))
 
+    def pin_memory(self) -> Gradient:
+        """Every host payload in page-locked memory (gradient.py:516-537): what
+        asynchronous host-to-device copies of whole blocks need.  Idempotent;
+        device payloads pass through."""
+
+        def pin(v):
+            if isinstance(v, Factorized):
+                return v.pin_memory()
+            return v if v.device.type != "cpu" or v.is_pinned() else v.pin_memory()
+
+        return Gradient(dict(self.representation), {n: pin(v) for n, v in self.data.items()}, self.layer_types,
+                        dict(self.indexing))
+
+    # -- batch / token reshaping (gradient.py:698-961) ---------------------------
+    def _sample_axis(self, value: GradientData, dim: str) -> int:
+        """Axis of ``dim`` ("batch" or "token") in a layer's payload."""
+        batch_first = value.batch_first if isinstance(value, Factorized) else True
+        return (0 if batch_first else 1) if dim == "batch" else (1 if batch_first else 0)
+
+    @staticmethod
+    def _rows(value: GradientData) -> int:
+        if isinstance(value, Factorized):
+            return value.activation.shape[0 if value.batch_first else 1]
+        return value.shape[0]
+
+    def _check_compatible(self, other: Gradient, require_same_batch: bool) -> None:
+        """The two blocks describe the same layers the same way (gradient.py:1150-1191)."""
+        if self.layer_names != other.layer_names:
+            raise ValueError("Layer sets differ")
+        for what, mine, theirs in (("representations", self.representation, other.representation),
+                                   ("indexing", self.indexing, other.indexing)):
+            bad = sorted(n for n in self.layer_names if mine.get(n) != theirs.get(n))
+            if bad:
+                raise ValueError(f"Layers have differing {what}: {bad}")
+        if self.layer_types != other.layer_types:
+            raise ValueError(f"Layer types differ: {self.layer_types} vs {other.layer_types}")
+        if require_same_batch:
+            if self.batch_size != other.batch_size:
+                raise ValueError("Batch sizes differ")
+            mine, theirs = self.token_dim, other.token_dim
+            bad = sorted(n for n in self.layer_names if mine[n] != theirs[n])
+            if bad:
+                raise ValueError(f"Token dimensions differ for layers: {bad}")
+
+    def _require_token_axis(self, what: str) -> None:
+        bad = sorted(n for n in self.layer_names if self.indexing[n] != "batch_token")
+        if bad:
+            raise ValueError(f"Token {what} requires all layers to have indexing='batch_token'. "
+                             f"Non-conforming: {bad}")
+
+    def concatenate(self, other: Gradient, dim: Literal["batch", "token"] = "batch") -> Gradient:
+        """Join two blocks along the batch or token axis (gradient.py:698-836).
+
+        * Batch joins accept different token counts on ``"batch_token"``
+          layers: the shorter side gets extra positions with an exactly-zero
+          output gradient (integer activations, i.e. token ids, take the
+          layer's ``padding_idx`` or 0), which contribute nothing downstream.
+        * A layer broadcast on both sides (one shared row while the block holds
+          several samples) becomes one shared row, the two rows averaged with
+          the blocks' sample counts as weights: on the output-gradient factor
+          when the two activations are identical, else on the materialized
+          gradients (the layer then turns ``"materialized"``).
+        """
+        if dim not in ("batch", "token"):
+            raise ValueError("dim must be 'batch' or 'token'")
+        self._check_compatible(other, require_same_batch=False)
+        if dim == "token":
+            self._require_token_axis("concatenation")
+            if self.batch_size != other.batch_size:
+                raise ValueError("Token concatenation requires the same batch size")
+        n_self, n_other = self.batch_size, other.batch_size
+        data, rep, index = {}, dict(self.representation), dict(self.indexing)
+        for name in self.layer_names:
+            mine, theirs = self.data[name], other.data[name]
+            if type(mine) is not type(theirs):
+                raise TypeError(f"{name} has mismatched data types")
+            shared = (self._rows(mine) == 1 < n_self, self._rows(theirs) == 1 < n_other)
+            if dim == "batch" and any(shared):
+                if not all(shared):
+                    raise ValueError(f"{name} is a broadcast (batch-collapsed) gradient on one side but "
+                                     "per-sample on the other; the two cannot be concatenated along the "
+                                     "batch axis.")
+                data[name], merged_dense = _merge_shared_rows(mine, theirs, n_self, n_other,
+                                                              self.layer_types[name])
+                if merged_dense:
+                    rep[name], index[name] = "materialized", "batch"
+                continue
+            if isinstance(mine, Factorized):
+                if mine.batch_first != theirs.batch_first:
+                    raise ValueError(f"{name} has mismatched batch_first layout between gradients")
+                if dim == "batch" and self.indexing[name] == "batch_token":
+                    mine, theirs = _pad_factor_tokens(mine, theirs)
+                ax = self._sample_axis(mine, dim)
+                data[name] = Factorized(torch.cat([mine.activation, theirs.activation], dim=ax),
+                                        torch.cat([mine.pre_activation_grad, theirs.pre_activation_grad], dim=ax),
+                                        module_kwargs=mine.module_kwargs, batch_first=mine.batch_first)
+            else:
+                if dim == "batch" and self.indexing[name] == "batch_token":
+                    t = max(mine.shape[1], theirs.shape[1])
+                    mine, theirs = _pad_axis(mine, t, 1), _pad_axis(theirs, t, 1)
+                data[name] = torch.cat([mine, theirs], dim=self._sample_axis(mine, dim))
+        return Gradient(rep, data, self.layer_types, index)
+
+    def aggregate(self, dim: Literal["token"] = "token") -> Gradient:
+        """Sum the token axis out of every ``"batch_token"`` layer
+        (gradient.py:838-886); ``"batch"`` layers pass through.  A sum, not a
+        mean: dL/dW = sum_t g_t a_t^T for any loss, so the per-token
+        gradients already carry the loss's own normalization."""
+        if dim != "token":
+            raise NotImplementedError("Only token aggregation is supported")
+        data, rep = {}, {}
+        for name, value in self.data.items():
+            if self.indexing[name] != "batch_token":
+                data[name], rep[name] = value, self.representation[name]
+            elif isinstance(value, Factorized):
+                data[name], rep[name] = ops.materialize(value, self.layer_types[name]), "materialized"
+            else:
+                data[name], rep[name] = value.sum(dim=1), self.representation[name]
+        return Gradient(rep, data, self.layer_types, {})
+
+    def slice(self, dim: Literal["batch", "token"], index) -> Gradient:
+        """Select samples or token positions of every layer (gradient.py:888-961).
+
+        An int index keeps the axis (length 1).  A layer broadcast along the
+        batch (one shared row for several samples) serves every requested
+        sample with that row; batch-level parameter gradients pass through."""
+        if dim not in ("batch", "token"):
+            raise ValueError("dim must be 'batch' or 'token'")
+        if dim == "token":
+            self._require_token_axis("slicing")
+
+        def take(x: torch.Tensor, ax: int) -> torch.Tensor:
+            sel = index
+            if dim == "batch" and x.shape[ax] == 1:
+                count = 1 if isinstance(index, int) else (index.numel() if torch.is_tensor(index) else len(index))
+                sel = 0 if isinstance(index, int) else torch.zeros(count, dtype=torch.long, device=x.device)
+            if isinstance(sel, int):
+                return x.narrow(ax, sel, 1)
+            if not torch.is_tensor(sel):
+                sel = torch.as_tensor(list(sel), dtype=torch.long)
+            return x.index_select(ax, sel.to(device=x.device, dtype=torch.long))
+
+        data = {}
+        for name, value in self.data.items():
+            if self.layer_types[name] == ops.PARAM_GRAD_TYPES:
+                data[name] = value
+            elif isinstance(value, Factorized):
+                ax = self._sample_axis(value, dim)
+                data[name] = Factorized(take(value.activation, ax), take(value.pre_activation_grad, ax),
+                                        module_kwargs=value.module_kwargs, batch_first=value.batch_first)
+            else:
+                data[name] = take(value, self._sample_axis(value, dim))
+        return Gradient(dict(self.representation), data, self.layer_types, dict(self.indexing))
+
     # -- arithmetic -------------------------------------------------------------
     def materialize(self) -> Gradient:
         """Every factorized layer as its dense per-sample gradient (gradient.py:539-567)."""
@@ -321,8 +475,78 @@ class Gradient:
             total = total / (ns.sqrt()[:, None] * no.sqrt()[None, :] + eps)
         return total
 
+    def similarity_per_token(self, other: Gradient, reduce: Literal["none", "all"] = "all"):
+        """Each token position's share of the per-sample similarity
+        (gradient.py:1072-1133): ``K[i, t, j]`` over this block's factorized
+        ``"batch_token"`` layers (the only ones that still carry a token axis),
+        so summing over ``t`` gives :meth:`similarity`'s ``(B_self, B_other)``.
+        ``other``'s layer may be factorized or dense.  ``reduce="none"`` gives
+        ``{layer: (B_self, T_self, B_other)}``, ``"all"`` their sum."""
+        if reduce not in {"none", "all"}:
+            raise ValueError("reduce must be 'none' or 'all'")
+        per_layer = {}
+        for name in sorted(self.layer_names & other.layer_names):
+            mine = self.data[name]
+            if isinstance(mine, Factorized) and self.indexing[name] == "batch_token":
+                per_layer[name] = ops.cross_dot_per_token(mine, other.data[name], self.layer_types[name])
+        if reduce == "none":
+            return per_layer
+        if not per_layer:
+            raise ValueError("No shared factorized batch_token layers for per-token similarity")
+        total = None
+        for k in per_layer.values():
+            total = k.clone() if total is None else total.add_(k)
+        return total
+
     def __repr__(self) -> str:
         return f"Gradient(layers={sorted(self.data)}, batch={self.batch_size})"
+
+
+def _pad_axis(t: torch.Tensor, length: int, axis: int, value=0) -> torch.Tensor:
+    """``t`` extended to ``length`` along ``axis`` with ``value``."""
+    extra = length - t.shape[axis]
+    if extra <= 0:
+        return t
+    shape = list(t.shape)
+    shape[axis] = extra
+    return torch.cat([t, t.new_full(shape, value)], dim=axis)
+
+
+def _pad_factor_tokens(x: Factorized, y: Factorized) -> tuple[Factorized, Factorized]:
+    """Both factor pairs at the longer token count: extra positions carry an
+    exactly-zero output gradient; an integer activation (token ids) is filled
+    with the layer's ``padding_idx`` when it has one, else 0 (the zero gradient
+    row keeps either inert)."""
+    axis = 1 if x.batch_first else 0
+    length = max(x.activation.shape[axis], y.activation.shape[axis])
+
+    def extend(f: Factorized) -> Factorized:
+        if f.activation.shape[axis] == length:
+            return f
+        fill = 0
+        if not f.activation.is_floating_point():
+            pad_idx = (f.module_kwargs or {}).get("padding_idx")
+            fill = 0 if pad_idx is None else pad_idx
+        return Factorized(_pad_axis(f.activation, length, axis, fill), _pad_axis(f.pre_activation_grad, length, axis),
+                          module_kwargs=f.module_kwargs, batch_first=f.batch_first)
+
+    return extend(x), extend(y)
+
+
+def _merge_shared_rows(x: GradientData, y: GradientData, n_x: int, n_y: int, layer_type: str):
+    """One shared row from two broadcast rows, weighted by the blocks' sample
+    counts; returns (row, became_dense).  Identical activations let the
+    factorized form average the output-gradient factor alone (the gradient is
+    linear in it); otherwise the rows are averaged as materialized gradients."""
+    wx, wy = float(n_x), float(n_y)
+    if isinstance(x, Factorized):
+        xb, yb = x.as_batch_first(), y.as_batch_first()
+        if xb.activation.shape == yb.activation.shape and torch.equal(xb.activation, yb.activation):
+            g = (wx * xb.pre_activation_grad + wy * yb.pre_activation_grad) / (wx + wy)
+            return Factorized(xb.activation, g, module_kwargs=xb.module_kwargs, batch_first=True), False
+        mx, my = ops.materialize(x, layer_type), ops.materialize(y, layer_type)
+        return (wx * mx + wy * my) / (wx + wy), True
+    return (wx * x + wy * y) / (wx + wy), False
 
 
 @dataclass
