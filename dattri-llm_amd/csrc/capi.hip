@@ -90,7 +90,7 @@ __global__ __launch_bounds__(64) void selftest_mfma16_kernel(const char* a, cons
 
 extern "C" {
 
-int da_abi_version(void) { return 12; }
+int da_abi_version(void) { return 13; }
 
 const char* da_last_error(void) { return da::g_error; }
 

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdattri_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 DA_F32, DA_F16, DA_BF16 = 0, 1, 2
 DA_OK, DA_ERR_INVALID, DA_ERR_UNSUPPORTED, DA_ERR_HIP, DA_ERR_WORKSPACE = 0, 1, 2, 3, 4
@@ -68,6 +68,14 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "da_ghost_gram_per_token_workspace": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
     "da_ghost_gram_per_token": (
         _I32, [_SIDE, _SIDE, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P]),
+    "da_ghost_gram_embedding_workspace": (_I32, [_SIDE, _SIDE, _I64, _I32, _I32, ctypes.POINTER(_SZ)]),
+    "da_ghost_gram_embedding": (_I32, [_SIDE, _SIDE, _I64, _I32, _I32, _P, _I64, _I32, _P, _SZ, _P]),
+    "da_ghost_gram_embedding_per_token_workspace": (_I32, [_SIDE, _SIDE, _I64, _I32, ctypes.POINTER(_SZ)]),
+    "da_ghost_gram_embedding_per_token": (
+        _I32, [_SIDE, _SIDE, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P]),
+    "da_dense_per_token_embedding": (
+        _I32, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64,
+               _I32, _P]),
     "da_dense_per_token_workspace": (_I32, [_SIDE, _I64, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
     "da_dense_per_token": (
         _I32, [_SIDE, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P]),
@@ -94,6 +102,9 @@ SIGNATURES.update(
             _I32,
             [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P],
         ),
+        "da_materialize_embedding_workspace": (_I32, [_I64, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
+        "da_materialize_embedding": (
+            _I32, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P]),
         "da_row_gram": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P, _SZ, _P]),
         "da_row_gram_workspace": (_I32, [_I64, _I64, _I32, ctypes.POINTER(_SZ)]),
         "da_nonzero_rows": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P]),

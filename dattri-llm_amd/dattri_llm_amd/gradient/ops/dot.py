@@ -28,6 +28,7 @@ import torch
 
 from dattri_llm_amd import kernels
 from dattri_llm_amd.gradient.ops import cost, dtypes
+from dattri_llm_amd.gradient.ops import embedding as emb
 from dattri_llm_amd.gradient.ops.materialize import (
     linear_dense,
     materialize,
@@ -158,9 +159,11 @@ def _ghost_pairs(pairs, out: torch.Tensor) -> None:
 def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Tensor:
     """Cross-gram ``K[i, j] = <dW1_i, dW2_j>`` on already-preprocessed factors
     (dot.py:36-118)."""
-    if is_embedding(layer_type):
-        require_supported(layer_type, "cross_gram")
     out_dtype = dtypes.resolve(a1, g1, a2, g2)
+    if is_embedding(layer_type):
+        # K[i,j] = sum over equal ids of g1_it . g2_js (dot.py:58-74)
+        emb.check_ids(a1, a2)
+        return emb.gram32(emb.side(a1, g1, layer_type, None), emb.side(a2, g2, layer_type, None)).to(out_dtype)
     if is_norm(layer_type):
         if layer_type not in TOKEN_NORM_TYPES:
             require_supported(layer_type, "cross_gram")
@@ -173,7 +176,10 @@ def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Ten
 
 
 def _side(a, g, layer_type, module_kwargs, include_bias):
-    """('norm', (B, d) dense) | ('linear', (a, g, bias)) for one raw side."""
+    """('norm', (B, d) dense) | ('linear', (a, g, bias)) | ('embedding', (ids, g))
+    for one raw side."""
+    if is_embedding(layer_type):
+        return "embedding", emb.side(a, g, layer_type, module_kwargs)
     if layer_type in TOKEN_NORM_TYPES:
         if module_kwargs is not None:
             return "norm", norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
@@ -184,8 +190,12 @@ def _side(a, g, layer_type, module_kwargs, include_bias):
 
 
 def _cross_factors32(a1, g1, a2, g2, layer_type, mk1, mk2, include_bias, mode, out=None, accumulate=False):
+    if is_embedding(layer_type):
+        emb.check_ids(a1, a2)
     kind, s1 = _side(a1, g1, layer_type, mk1, include_bias)
     _, s2 = _side(a2, g2, layer_type, mk2, include_bias)
+    if kind == "embedding":
+        return emb.gram32(s1, s2, out=out, accumulate=accumulate)
     if kind == "norm":
         return _dense_gram(s1, s2, out=out, accumulate=accumulate)
     return _linear_gram32(*s1, *s2, mode, out=out, accumulate=accumulate)
@@ -214,8 +224,12 @@ def dot_factors(a1, g1, a2, g2, layer_type: str, module_kwargs1: dict | None = N
     out_dtype = dtypes.resolve(a1, g1, a2, g2)
     if a1.shape[0] != g2.shape[0]:
         raise ValueError("dot_factors needs two blocks of one batch size")
+    if is_embedding(layer_type):
+        emb.check_ids(a1, a2)
     kind, s1 = _side(a1, g1, layer_type, module_kwargs1, include_bias)
     _, s2 = _side(a2, g2, layer_type, module_kwargs2, include_bias)
+    if kind == "embedding":
+        return emb.diag32(s1, s2).to(out_dtype)
     if kind == "norm":
         (m1, m2), _ = _kernel_operands(_rows(s1), _rows(s2))
         return kernels.row_dots([(m1, m2)]).to(out_dtype)
@@ -240,7 +254,11 @@ def grad_norm_sq_factors(a, g, layer_type: str, module_kwargs: dict | None = Non
     (factorized), or the row-dot kernel on the per-sample gradients
     (materialized, and norm layers)."""
     out_dtype = dtypes.resolve(a, g)
+    if is_embedding(layer_type):
+        emb.check_ids(a)
     kind, side = _side(a, g, layer_type, module_kwargs, include_bias)
+    if kind == "embedding":  # the diagonal of the pairwise gram (dot.py:383-384)
+        return emb.diag32(side, side).to(out_dtype)
     if kind == "norm":
         return _sq_row_norms(side).to(out_dtype)
     x, y, bias = side
@@ -444,9 +462,10 @@ def cross_gram_per_token(a1, g1, a2, g2, layer_type: str) -> torch.Tensor:
     """Per-token cross-gram ``K[i, t, j]`` on preprocessed factors
     (dot.py:171-222): side 1's token t against side 2's whole per-sample
     gradient; summing over t gives :func:`cross_gram`.  ``(B1, T1, B2)``."""
-    if is_embedding(layer_type):
-        require_supported(layer_type, "cross_gram_per_token")
     out_dtype = dtypes.resolve(a1, g1, a2, g2)
+    if is_embedding(layer_type):
+        emb.check_ids(a1, a2)
+        return emb.per_token32(emb.side(a1, g1, layer_type, None), emb.side(a2, g2, layer_type, None)).to(out_dtype)
     if is_norm(layer_type):
         if layer_type not in TOKEN_NORM_TYPES:
             require_supported(layer_type, "cross_gram_per_token")
@@ -461,9 +480,10 @@ def cross_gram_per_token(a1, g1, a2, g2, layer_type: str) -> torch.Tensor:
 def cross_gram_per_token_dense(a1, g1, m2, layer_type: str) -> torch.Tensor:
     """:func:`cross_gram_per_token` with side 2 dense (dot.py:225-263): ``m2`` is
     the (B2, D) per-sample gradient block in materialize's layout."""
-    if is_embedding(layer_type):
-        require_supported(layer_type, "cross_gram_per_token_dense")
     out_dtype = dtypes.resolve(a1, g1, m2)
+    if is_embedding(layer_type):
+        emb.check_ids(a1)
+        return emb.dense_per_token32(emb.side(a1, g1, layer_type, None), m2).to(out_dtype)
     m2 = m2.reshape(m2.shape[0], -1)
     if is_norm(layer_type):
         if layer_type not in TOKEN_NORM_TYPES:
@@ -488,7 +508,15 @@ def cross_dot_per_token(f1, f2, layer_type: str, include_bias: bool = True) -> t
         rows1 = norm_token_rows(a1, g1, layer_type, mk1, include_bias)
         m2 = f2.reshape(f2.shape[0], -1) if dense2 else materialize(f2, layer_type, include_bias)
         return _norm_per_token32(rows1, m2).to(out_dtype)
-    if is_embedding(layer_type) or not is_linear(layer_type):
+    if is_embedding(layer_type):
+        emb.check_ids(a1, None if dense2 else f2.as_batch_first().activation)
+        s1 = emb.side(a1, g1, layer_type, mk1)
+        if dense2:
+            return emb.dense_per_token32(s1, f2).to(out_dtype)
+        b2 = f2.as_batch_first()
+        s2 = emb.side(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs)
+        return emb.per_token32(s1, s2).to(out_dtype)
+    if not is_linear(layer_type):
         require_supported(layer_type, "cross_dot_per_token")
     x1, y1, bias1 = final_linear(a1, g1, layer_type, mk1, include_bias)
     if dense2:

@@ -1,9 +1,10 @@
 """Per-sample weight gradients of factorized captures (materialized form).
 
-Mirrors ``dattri_llm/gradient/ops/materialize.py:56-146`` for linear layers
+Mirrors ``dattri_llm/gradient/ops/materialize.py:22-146`` for linear layers
 (``bmm(g^T, a)`` flattened to ``(B, out*in)``, index ``o*K + i``, with the bias
-column last) and token norms (``sum_t x_hat * g``, and ``[dgamma, dbeta]`` with
-a bias).  The linear case runs the ``da_materialize_linear`` MFMA kernel; the
+column last), token norms (``sum_t x_hat * g``, and ``[dgamma, dbeta]`` with
+a bias) and embeddings (the scatter-add into ``(B, vocab*E)``, run by
+``da_materialize_embedding``).  The linear case runs the ``da_materialize_linear`` MFMA kernel; the
 norm case runs ``da_norm_weight_grad``, which normalises in registers and never
 forms x_hat.  Results are in the resolved compute dtype with fp32 accumulation.
 """
@@ -14,6 +15,7 @@ import torch
 
 from dattri_llm_amd import kernels
 from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops import embedding as emb
 from dattri_llm_amd.gradient.ops.preprocess import (
     final_linear,
     fold_norm_rows,
@@ -95,7 +97,9 @@ def materialize_factors(
                 "Materializing an embedding gradient requires module_kwargs with 'num_embeddings' "
                 "(the weight's vocab size cannot be inferred from the captured factors)."
             )
-        require_supported(layer_type, "materialize_factors")
+        vocab = int(module_kwargs["num_embeddings"])
+        emb.check_ids(a, vocab=vocab)
+        return emb.materialize(emb.side(a, g, layer_type, module_kwargs), vocab)
     if layer_type in TOKEN_NORM_TYPES:
         if per_token:
             return norm_token_rows(a, g, layer_type, module_kwargs, include_bias).flatten(1)

@@ -3,8 +3,10 @@
 Mirrors ``dattri_llm/gradient/ops/preprocess.py`` for the layer families of the
 scoring path: linear layers (bias folded as a ones column, :436-437) and token
 norms (RMSNorm / LayerNorm x_hat, :366-384, computed by the ``da_norm_xhat``
-kernel, with the bias augmentation of ``norm.py:95-110``).  Conv, embedding and
-channel-norm layers raise ``NotImplementedError``.
+kernel, with the bias augmentation of ``norm.py:95-110``) and embeddings
+(``nn.Embedding`` padding positions, ``nn.EmbeddingBag`` bags spread over their
+tokens, :403-416 and :126-169).  Conv and channel-norm layers raise
+``NotImplementedError``.
 
 The public ``preprocess_factors`` returns exactly the reference's tensors.  The
 scoring kernels never need them: :func:`final_linear` and :func:`norm_spec`
@@ -127,14 +129,61 @@ def preprocess_factors(
         if has_bias:
             return torch.cat([x_hat, torch.ones_like(x_hat)], dim=-1), torch.cat([g, g], dim=-1)
         return x_hat, g
+    if layer_type == "nn.Embedding":
+        pad = module_kwargs.get("padding_idx")
+        if pad is not None:
+            g = g.masked_fill((a == pad).unsqueeze(-1), 0)
+        return a, g
+    if layer_type == "nn.EmbeddingBag":
+        ids, rows = _bag_rows(a, g, module_kwargs["mode"], module_kwargs.get("padding_idx"))
+        if module_kwargs.get("padding_idx") is not None:
+            rows = rows.masked_fill((a == module_kwargs["padding_idx"]).unsqueeze(-1), 0)
+        return a, rows.contiguous()
     if is_norm(layer_type) or not is_linear(layer_type):
         raise NotImplementedError(
             f"preprocess_factors: {layer_type!r} is outside the MI355X scoring path "
-            "(linear layers and RMSNorm/LayerNorm)."
+            "(linear, embedding and RMSNorm/LayerNorm layers)."
         )
     if has_bias:
         return torch.cat([a, torch.ones_like(a[..., :1])], dim=-1), g
     return a, g
+
+
+def _bag_rows(a: torch.Tensor, g: torch.Tensor, mode: str, padding_idx):
+    """An EmbeddingBag's per-bag gradient ``g (N, E)`` spread over its ``T``
+    tokens (preprocess.py:126-169): the returned rows are a stride-0 ``(N, T, E)``
+    view of ``g`` scaled by ``1/T`` for ``mode='mean'`` (``1/(non-pad count)``,
+    at least 1, with a ``padding_idx``), and the ids have padding positions set
+    to -1 (they then add nothing).  The scaling is the reference's division in
+    g's dtype, done once per bag instead of once per token."""
+    if mode == "max":
+        raise NotImplementedError("EmbeddingBag mode='max' is not supported for factorized gradients.")
+    if a.ndim != 2 or g.ndim != 2:
+        raise NotImplementedError("EmbeddingBag factorization supports only 2-D inputs (N, T) without offsets.")
+    t = a.shape[1]
+    ids = a
+    if padding_idx is not None:
+        pad = a == padding_idx
+        ids = a.masked_fill(pad, -1)
+        if mode == "mean":
+            g = g / (~pad).sum(dim=1).clamp_min(1).view(-1, 1).to(g.dtype)
+    elif mode == "mean":
+        g = g / t
+    return ids, g.unsqueeze(1).expand(-1, t, -1)
+
+
+def final_embedding(a, g, layer_type: str, module_kwargs: dict | None):
+    """An embedding layer's kernel operands ``(ids, g)``: ``g`` the per-token
+    gradient rows (an EmbeddingBag's per-bag rows spread as a stride-0 view),
+    ``ids`` int64 with padding positions set to -1.  A negative id matches and
+    scatters nothing, which is what the reference's zeroed gradient at those
+    positions contributes (preprocess.py:403-408)."""
+    if module_kwargs is None:
+        return a, g
+    if layer_type == "nn.EmbeddingBag":
+        return _bag_rows(a, g, module_kwargs["mode"], module_kwargs.get("padding_idx"))
+    pad = module_kwargs.get("padding_idx")
+    return (a if pad is None else a.masked_fill(a == pad, -1)), g
 
 
 def preprocess_factorized(f, layer_type: str, include_bias: bool = True):
@@ -150,6 +199,7 @@ def flat_width(shape) -> int:
 __all__ = [
     "NormSpec",
     "extract_module_kwargs",
+    "final_embedding",
     "final_linear",
     "fold_norm_rows",
     "norm_spec",

@@ -196,6 +196,83 @@ def ghost_gram_diag(
     return out
 
 
+def _token_ids(tok: torch.Tensor) -> torch.Tensor:
+    """int64 (B, T) token ids, 8-byte aligned (a copy only when they are not)."""
+    if tok.dtype != torch.int64 or tok.data_ptr() % 8:
+        tok = tok.to(torch.int64).contiguous() if tok.dtype != torch.int64 else tok.clone()
+    return tok
+
+
+def ghost_gram_embedding(
+    tok1: torch.Tensor,
+    g1: torch.Tensor,
+    tok2: torch.Tensor,
+    g2: torch.Tensor,
+    *,
+    diag: bool = False,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Ghost inner product of one embedding layer, fp32 ``(B1, B2)``:
+    ``sum over (t, s) with tok1[i,t] == tok2[j,s] of g1[i,t] . g2[j,s]``.
+
+    ``tok*`` are integer (B, T) ids (negative ids match nothing), ``g*`` the
+    (B, T, E) gradient rows in one of fp32/fp16/bf16.  With ``diag`` only the
+    pairs (i, i) are formed and the result is ``(B,)``."""
+    dev = nat.require_device(tok1, g1, tok2, g2)
+    if diag and tok1.shape[0] != tok2.shape[0]:
+        raise ValueError("ghost_gram_embedding(diag=True) needs two blocks of one batch size")
+    tok1, g1, tok2, g2, e = _embedding_sides("ghost_gram_embedding", tok1, g1, tok2, g2)
+    code = nat.dtype_code(g1.dtype)
+    b1, b2 = tok1.shape[0], tok2.shape[0]
+    shape = (b1,) if diag else (b1, b2)
+    if out is None:
+        out = torch.empty(*shape, dtype=torch.float32, device=dev)
+        accumulate = False
+    elif out.dtype != torch.float32 or tuple(out.shape) != shape or out.stride(-1) != 1:
+        raise ValueError(f"out must be a float32 {shape} tensor with unit column stride")
+    s1, s2 = _side(tok1, g1, False), _side(tok2, g2, False)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_ghost_gram_embedding_workspace(s1, s2, e, code, int(diag), ctypes.byref(nbytes)),
+              "ghost_gram_embedding")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "ghost_gram_embedding", lib.da_ghost_gram_embedding,
+         s1, s2, e, code, int(diag), out.data_ptr(), out.stride(0), int(accumulate), ws.data_ptr(), ws.numel(),
+         nat.stream_ptr(dev))
+    return out
+
+
+def materialize_embedding(tok: torch.Tensor, g: torch.Tensor, vocab: int) -> torch.Tensor:
+    """Per-sample embedding weight gradient ``(B, vocab*E)`` in g's dtype:
+    row v of sample b is the sum of the gradient rows whose id is v, in fp32
+    in ascending token order, rounded once.  Ids must lie in ``[0, vocab)``
+    (the caller checks); a negative id adds nothing."""
+    dev = nat.require_device(tok, g)
+    if tok.dim() != 2 or g.dim() != 3 or tok.shape != g.shape[:2]:
+        raise ValueError("materialize_embedding expects (B, T) ids and (B, T, E) gradients")
+    b, t = tok.shape
+    e = g.shape[-1]
+    out = torch.empty(b, vocab * e, dtype=g.dtype, device=dev)
+    if b == 0 or e == 0 or vocab == 0:
+        return out
+    ep = -(-e // _chunk_elems(g.dtype)) * _chunk_elems(g.dtype)
+    if ep != e:  # padded width: scatter into a padded table, then drop the padding
+        full = materialize_embedding(tok, prepare_rows(g, ep), vocab)
+        out.view(b, vocab, e).copy_(full.view(b, vocab, ep)[:, :, :e])
+        return out
+    tok, g = _token_ids(tok), prepare_rows(g, e)
+    code = nat.dtype_code(g.dtype)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_materialize_embedding_workspace(b, t, e, code, ctypes.byref(nbytes)), "materialize_embedding")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "materialize_embedding", lib.da_materialize_embedding,
+         tok.data_ptr(), g.data_ptr(), code, b, t, e, vocab, tok.stride(0), tok.stride(1),
+         g.stride(0), g.stride(1), out.data_ptr(), vocab * e, ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    return out
+
+
 def _per_token_out(out, b1, t1, b2, dev, accumulate):
     if out is None:
         return torch.empty(b1, t1, b2, dtype=torch.float32, device=dev), False
@@ -244,6 +321,90 @@ def ghost_gram_per_token(
     _run(dev, "ghost_gram_per_token", lib.da_ghost_gram_per_token,
          s1, s2, k, d, code, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
          ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    return out
+
+
+def _embedding_sides(name, tok1, g1, tok2, g2):
+    if tok1.dim() != 2 or tok2.dim() != 2 or g1.dim() != 3 or g2.dim() != 3:
+        raise ValueError(f"{name} expects (B, T) ids and (B, T, E) gradients")
+    if tok1.shape != g1.shape[:2] or tok2.shape != g2.shape[:2]:
+        raise ValueError("ids and gradients disagree on (B, T)")
+    if g1.dtype != g2.dtype:
+        raise ValueError(f"{name} gradients must share one dtype")
+    if g1.shape[-1] != g2.shape[-1]:
+        raise ValueError("the two sides disagree on the embedding width")
+    e = -(-g1.shape[-1] // _chunk_elems(g1.dtype)) * _chunk_elems(g1.dtype)
+    same = tok1 is tok2 and g1 is g2
+    tok1, g1 = _token_ids(tok1), prepare_rows(g1, e)
+    tok2, g2 = (tok1, g1) if same else (_token_ids(tok2), prepare_rows(g2, e))
+    return tok1, g1, tok2, g2, e
+
+
+def ghost_gram_embedding_per_token(
+    tok1: torch.Tensor,
+    g1: torch.Tensor,
+    tok2: torch.Tensor,
+    g2: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Per-token embedding cross-gram, fp32 ``(B1, T1, B2)``: side 1's token t
+    against side 2's whole per-sample gradient, ``sum over s with
+    tok2[j,s] == tok1[i,t] of g1[i,t] . g2[j,s]``."""
+    dev = nat.require_device(tok1, g1, tok2, g2)
+    tok1, g1, tok2, g2, e = _embedding_sides("ghost_gram_embedding_per_token", tok1, g1, tok2, g2)
+    code = nat.dtype_code(g1.dtype)
+    b1, t1, b2 = tok1.shape[0], tok1.shape[1], tok2.shape[0]
+    out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
+    s1, s2 = _side(tok1, g1, False), _side(tok2, g2, False)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_ghost_gram_embedding_per_token_workspace(s1, s2, e, code, ctypes.byref(nbytes)),
+              "ghost_gram_embedding_per_token")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "ghost_gram_embedding_per_token", lib.da_ghost_gram_embedding_per_token,
+         s1, s2, e, code, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
+         ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    return out
+
+
+def dense_per_token_embedding(
+    tok1: torch.Tensor,
+    g1: torch.Tensor,
+    m2: torch.Tensor,
+    vocab: int,
+    *,
+    out: torch.Tensor | None = None,
+    accumulate: bool = False,
+) -> torch.Tensor:
+    """Per-token product of an embedding side against dense per-sample
+    gradients ``m2 (B2, vocab*E)``, fp32 ``(B1, T1, B2)``:
+    ``sum_e g1[i,t,e] * m2[j, tok1[i,t]*E + e]`` (0 for a negative id; ids
+    must be below ``vocab``)."""
+    dev = nat.require_device(tok1, g1, m2)
+    if tok1.dim() != 2 or g1.dim() != 3 or tok1.shape != g1.shape[:2]:
+        raise ValueError("dense_per_token_embedding expects (B, T) ids and (B, T, E) gradients")
+    if m2.dtype != g1.dtype:
+        raise ValueError("dense_per_token_embedding operands must share one dtype")
+    b1, t1, e = g1.shape
+    b2 = m2.shape[0]
+    if m2.reshape(b2, -1).shape[1] != vocab * e:
+        raise ValueError(f"m2 rows hold {m2.reshape(b2, -1).shape[1]} values, expected vocab*E = {vocab * e}")
+    vec = _chunk_elems(g1.dtype)
+    ep = -(-e // vec) * vec
+    m2 = m2.reshape(b2, vocab, e)
+    if ep != e:
+        m2 = prepare_rows(m2, ep)
+    m2 = m2.reshape(b2, vocab * ep)
+    if m2.stride(1) != 1 or m2.data_ptr() % 16 or (m2.stride(0) * m2.element_size()) % 16:
+        m2 = m2.contiguous()
+    tok1, g1 = _token_ids(tok1), prepare_rows(g1, ep)
+    out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
+    _run(dev, "dense_per_token_embedding", nat.load().da_dense_per_token_embedding,
+         tok1.data_ptr(), g1.data_ptr(), nat.dtype_code(g1.dtype), b1, t1, ep, vocab, tok1.stride(0),
+         tok1.stride(1), g1.stride(0), g1.stride(1), m2.data_ptr(), m2.stride(0), b2, out.data_ptr(),
+         out.stride(0), out.stride(1), out.stride(2), int(accumulate), nat.stream_ptr(dev))
     return out
 
 

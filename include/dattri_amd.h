@@ -117,6 +117,64 @@ int da_ghost_gram_diag(const da_factor_side* s1, const da_factor_side* s2, int64
                        void* stream);
 
 /*
+ * Ghost inner product of one embedding layer (nn.Embedding, and
+ * nn.EmbeddingBag once its per-bag gradient is spread over its tokens):
+ *
+ *   out[i*ld_out + j] (+)= sum_{t,s : tok1[i,t] == tok2[j,s]} g1[i,t,:] . g2[j,s,:]
+ *
+ * (the weight gradient is sum_t e_{tok_t} g_t^T, so the activation Gram of
+ * the linear ghost product is the token-equality indicator).  side->act holds
+ * int64 token ids (B, T) with element strides (act_bstride, act_tstride);
+ * side->grad the (B, T, D) gradient rows.  A negative id matches nothing (a
+ * padding position).  No segments, row index or bias column.  diag = 1 takes
+ * the pairs (i, i) only, into out[i*ld_out] (both batches equal): the
+ * per-sample dots, or squared norms when both sides are one block.  fp32,
+ * deterministic.  Replaces the embedding branches of cross_gram,
+ * dattri_llm/gradient/ops/dot.py:58-74 (a scatter_add_ into a (vocab, E)
+ * table per side-2 sample, then a gather), of dot_factors, dot.py:325-337,
+ * and of grad_norm_sq_factors, dot.py:383-384.
+ */
+int da_ghost_gram_embedding_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype,
+                                      int diag, size_t* bytes);
+int da_ghost_gram_embedding(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype, int diag,
+                            float* out, int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/*
+ * Per-token embedding cross-gram: side 1's token axis kept, side 2's summed,
+ *
+ *   out[i*ld_b1 + t*ld_t + j*ld_b2] (+)= sum_{s : tok2[j,s] == tok1[i,t]} g1[i,t,:] . g2[j,s,:]
+ *
+ * fp32 (B1, T1, B2), sides as for da_ghost_gram_embedding (a negative id
+ * matches nothing; a gradient token stride of 0 is allowed, for a bag's one
+ * gradient row spread over its tokens).  Summing over t gives
+ * da_ghost_gram_embedding's (B1, B2).  Replaces the embedding branch of
+ * cross_gram_per_token, dattri_llm/gradient/ops/dot.py:189-203.
+ */
+int da_ghost_gram_embedding_per_token_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t D,
+                                                int dtype, size_t* bytes);
+int da_ghost_gram_embedding_per_token(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype,
+                                      float* out, int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Per-token product of an embedding side against dense per-sample gradients,
+ *
+ *   out[i*ld_b1 + t*ld_t + j*ld_b2] (+)= sum_e g[i,t,e] * m2[j*m2_bstride + tok[i,t]*E + e]
+ *
+ * fp32; m2 holds each sample's (vocab, E) block (da_materialize_embedding's
+ * layout) in dtype.  tok int64 (B1, T1), g (B1, T1, E), element strides as
+ * for da_materialize_embedding; a negative id gives 0, ids must be < vocab.
+ * Replaces the embedding branch of cross_gram_per_token_dense,
+ * dattri_llm/gradient/ops/dot.py:239-245 (a gather of m2's rows, then an
+ * einsum).
+ */
+int da_dense_per_token_embedding(const int64_t* tok, const void* g, int dtype, int64_t b1, int64_t len1, int64_t E,
+                                 int64_t vocab, int64_t tok_bstride, int64_t tok_tstride, int64_t g_bstride,
+                                 int64_t g_tstride, const void* m2, int64_t m2_bstride, int64_t b2, float* out,
+                                 int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate, void* stream);
+
+/*
  * Per-token cross-gram of two factorized sides: side 1's token axis kept,
  * side 2's summed out,
  *
@@ -207,6 +265,30 @@ int da_materialize_linear(const void* a, const void* g, int dtype, int64_t batch
                           int64_t g_bstride, int64_t g_tstride, int has_bias, void* out,
                           int out_dtype, int64_t out_bstride, int64_t out_rstride,
                           int64_t out_blk, void* stream);
+
+/*
+ * Per-sample embedding weight gradient (scatter-add):
+ *
+ *   out[b*out_bstride + v*E + e] = sum over t with tok[b,t] == v of g[b,t,e]
+ *
+ * for v < vocab, in dtype: each row summed in fp32 in ascending t and rounded
+ * once (what the reference's scatter_add_ gives on the CPU, where the
+ * reduced-precision path accumulates in fp32; deterministic).  tok is int64
+ * (B, T) with element strides (tok_bstride, tok_tstride); g is (B, T, E) with
+ * element strides (g_bstride, g_tstride), rows 16-byte aligned, E a multiple
+ * of 16 bytes / element size.  Every block is zeroed first; ids outside
+ * [0, vocab) add nothing (callers reject them beforehand; a negative id is a
+ * padding position).  vocab, T < 2^31; B <= 65535.  The workspace (size from
+ * da_materialize_embedding_workspace, 256-byte aligned) holds each token's
+ * first occurrence and, for 2-byte dtypes, the fp32 (B, T, E) sums.
+ * Replaces _materialize_embedding, dattri_llm/gradient/ops/materialize.py:22-48
+ * (result.scatter_add_ into (B, vocab, E), flattened to (B, vocab*E)).
+ */
+int da_materialize_embedding_workspace(int64_t batch, int64_t tokens, int64_t E, int dtype, size_t* bytes);
+int da_materialize_embedding(const int64_t* tok, const void* g, int dtype, int64_t batch, int64_t tokens,
+                             int64_t E, int64_t vocab, int64_t tok_bstride, int64_t tok_tstride,
+                             int64_t g_bstride, int64_t g_tstride, void* out, int64_t out_bstride,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Row Gram: out (+)= x^T x, fp32 (width, width) with row stride ld_out, of the

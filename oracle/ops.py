@@ -51,6 +51,17 @@ ekfac_precondition             gradient/ops/kronecker.py:413-458              la
                                                                               score == vec(dW1)^T (U (x) U) diag(1/lam)
                                                                               (U (x) U)^T vec(dW2), matrices formed
 kfac_precondition_materialized gradient/ops/kronecker.py:386-410              kron(G^-1, A^-1) @ vec(dW)
+embedding_materialize          gradient/ops/materialize.py:22-48              torch autograd weight.grad of nn.Embedding
+                                                                              (f64); torch's CPU scatter_add_ in bf16 /
+                                                                              fp16 / fp32, bit for bit (per-add rounding)
+embedding_bag_expand           gradient/ops/preprocess.py:126-169             materialized: autograd of nn.EmbeddingBag
+                                                                              (sum / mean, with and without padding_idx)
+embedding_cross_gram           gradient/ops/dot.py:58-74                      brute-force loops; M1 @ M2^T of autograd
+                                                                              per-sample weight grads
+embedding_cross_gram_per_token gradient/ops/dot.py:189-203                    brute-force loops; the sum over t equals
+                                                                              embedding_cross_gram
+embedding_per_token_dense      gradient/ops/dot.py:239-245                    equals embedding_cross_gram_per_token with
+                                                                              m2 = embedding_materialize of side 2
 =============================  =============================================  ===========================================
 """
 
@@ -65,6 +76,11 @@ __all__ = [
     "cross_gram_per_token",
     "cross_gram_per_token_dense",
     "ekfac_materialize_factors",
+    "embedding_bag_expand",
+    "embedding_cross_gram",
+    "embedding_cross_gram_per_token",
+    "embedding_materialize",
+    "embedding_per_token_dense",
     "ekfac_precondition",
     "ekfac_rotate_materialized",
     "fim_factors",
@@ -615,3 +631,111 @@ def kfac_precondition_materialized(block, a_inv, g_inv):
     a_inv, g_inv = np.asarray(a_inv, np.float64), np.asarray(g_inv, np.float64)
     d_w = np.asarray(block, np.float64).reshape(len(block), g_inv.shape[0], a_inv.shape[0])
     return (g_inv @ d_w @ a_inv).reshape(len(block), -1)
+
+
+# ---------------------------------------------------------------------------
+# embedding layers
+# ---------------------------------------------------------------------------
+
+
+def _round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """fp32 values rounded to ``dtype`` ("bf16", "f16", "f32") with
+    round-to-nearest-even, returned as float32 (NaN stays NaN)."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "f32":
+        return x
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), x, out)
+
+
+def embedding_materialize(tok, g, vocab: int, dtype: str = "f64") -> np.ndarray:
+    """Per-sample embedding weight gradient (materialize.py:22-48): a zero
+    (B, vocab, E) table, ``scatter_add_`` of the (B, T, E) gradient rows at the
+    token ids along the vocab axis, flattened to (B, vocab*E).
+
+    ``dtype`` "f64" sums exactly (float64); "f32", "bf16" and "f16" restate the
+    CPU scatter_add_ in that dtype: rows are summed in fp32 in ascending t and
+    the sum is rounded once to the dtype (torch's reduced-precision scatter
+    accumulates in fp32).  Ids must lie in [0, vocab) (the reference raises
+    ValueError above it)."""
+    tok = np.asarray(tok, dtype=np.int64)
+    g = np.asarray(g)
+    b, t = tok.shape
+    e = g.shape[-1]
+    if tok.size and (tok.min() < 0 or tok.max() >= vocab):
+        raise ValueError("token id out of range")
+    rows = np.arange(b)
+    if dtype == "f64":
+        out = np.zeros((b, vocab, e), dtype=np.float64)
+        for s in range(t):
+            np.add.at(out, (rows, tok[:, s]), g[:, s].astype(np.float64))
+        return out.reshape(b, -1)
+    out = np.zeros((b, vocab, e), dtype=np.float32)
+    g32 = _round_to(g.astype(np.float32), dtype)
+    for s in range(t):  # one (b, id) pair per sample and step: no index collides
+        out[rows, tok[:, s]] = out[rows, tok[:, s]] + g32[:, s]
+    return _round_to(out, dtype).reshape(b, -1)
+
+
+def embedding_bag_expand(a, g, mode: str, padding_idx=None):
+    """EmbeddingBag per-bag gradients spread over the bag's tokens
+    (preprocess.py:126-169): g (N, E) -> (N, T, E), divided by T for 'mean';
+    with a padding_idx the pad positions get zero and the 'mean' divisor is the
+    bag's non-pad count (at least 1)."""
+    a = np.asarray(a, dtype=np.int64)
+    g = np.asarray(g)
+    n, t = a.shape
+    rows = np.repeat(g[:, None, :], t, axis=1).astype(g.dtype)
+    if padding_idx is not None:
+        pad = a == padding_idx
+        rows = np.where(pad[..., None], 0, rows)
+        if mode == "mean":
+            rows = rows / np.maximum((~pad).sum(axis=1), 1)[:, None, None]
+    elif mode == "mean":
+        rows = rows / t
+    return a, rows
+
+
+def embedding_cross_gram(tok1, g1, tok2, g2) -> np.ndarray:
+    """Embedding branch of cross_gram (dot.py:58-74), (B1, B2):
+    K[i, j] = sum_t g1_i[t] . G2_sum_j[tok1_i[t]] with
+    G2_sum_j[v] = sum over s with tok2_j[s] == v of g2_j[s], i.e. the sum over
+    token pairs with equal ids of g1_it . g2_js."""
+    tok1, tok2 = np.asarray(tok1, dtype=np.int64), np.asarray(tok2, dtype=np.int64)
+    b1, b2 = tok1.shape[0], tok2.shape[0]
+    out = np.zeros((b1, b2), dtype=np.result_type(g1, g2))
+    for i in range(b1):
+        for j in range(b2):
+            eq = tok1[i][:, None] == tok2[j][None, :]
+            out[i, j] = ((g1[i] @ g2[j].T) * eq).sum()
+    return out
+
+
+def embedding_cross_gram_per_token(tok1, g1, tok2, g2) -> np.ndarray:
+    """Embedding branch of cross_gram_per_token (dot.py:189-203), (B1, T1, B2):
+    out[i, t, j] = g1_i[t] . G2_sum_j[tok1_i[t]]."""
+    tok1, tok2 = np.asarray(tok1, dtype=np.int64), np.asarray(tok2, dtype=np.int64)
+    b1, t1 = tok1.shape
+    b2 = tok2.shape[0]
+    out = np.zeros((b1, t1, b2), dtype=np.result_type(g1, g2))
+    for i in range(b1):
+        for j in range(b2):
+            eq = tok1[i][:, None] == tok2[j][None, :]
+            out[i, :, j] = ((g1[i] @ g2[j].T) * eq).sum(axis=1)
+    return out
+
+
+def embedding_per_token_dense(tok1, g1, m2, vocab: int) -> np.ndarray:
+    """Embedding branch of cross_gram_per_token_dense (dot.py:239-245): the rows
+    of side 2's (B2, vocab, E) dense gradients at side 1's ids, dotted with
+    side 1's gradient rows, (B1, T1, B2)."""
+    tok1 = np.asarray(tok1, dtype=np.int64)
+    e = g1.shape[-1]
+    m2 = np.asarray(m2).reshape(m2.shape[0], vocab, e)
+    rows = m2[:, tok1.reshape(-1)].reshape(m2.shape[0], *tok1.shape, e)
+    return np.einsum("bte,cbte->btc", g1, rows)
+

@@ -259,3 +259,47 @@ def test_mask_indices_are_a_seeded_sorted_subset():
     assert torch.equal(ops.mask_materialized(dense, proj, proj_dim=37, proj_seed=3), dense[:, idx])
     with pytest.raises(ValueError, match="style 'mask'"):
         ops.mask_materialized(dense, proj, proj_dim=37, proj_seed=3, ensemble=2)
+
+
+# ---------------------------------------------------------------------------
+# embedding preprocessing (host side, no kernels)
+# ---------------------------------------------------------------------------
+
+
+def test_embedding_preprocess_matches_oracle():
+    import numpy as np
+
+    import oracle
+    from dattri_llm_amd.gradient.ops import embedding as emb
+    from dattri_llm_amd.gradient.ops import preprocess_factors
+    from dattri_llm_amd.gradient.ops.preprocess import final_embedding
+
+    gen = torch.Generator().manual_seed(3)
+    ids = torch.randint(1, 20, (4, 7), generator=gen)
+    ids[:, -2:] = 0
+    g = torch.randn(4, 7, 5, generator=gen)
+    mk = {"has_bias": False, "num_embeddings": 20, "padding_idx": 0}
+    a_p, g_p = preprocess_factors(ids, g, "nn.Embedding", mk)
+    assert torch.equal(a_p, ids) and torch.equal(g_p[:, -2:], torch.zeros(4, 2, 5))
+    assert torch.equal(g_p[:, :-2], g[:, :-2])
+    # the kernels' operands: ids -1 at the pads, g untouched
+    k_ids, k_g = final_embedding(ids, g, "nn.Embedding", mk)
+    assert torch.equal(k_ids[:, -2:], torch.full((4, 2), -1)) and k_g is g
+    for mode in ("sum", "mean"):
+        for pad in (None, 0):
+            bag = torch.randn(4, 5, generator=gen)
+            mkb = {"has_bias": False, "num_embeddings": 20, "mode": mode, "padding_idx": pad}
+            _, rows = preprocess_factors(ids, bag, "nn.EmbeddingBag", mkb)
+            _, ref = oracle.embedding_bag_expand(ids.numpy(), bag.double().numpy(), mode, pad)
+            np.testing.assert_allclose(rows.double().numpy(), ref, rtol=1e-6, atol=1e-7)
+            k_ids, k_rows = final_embedding(ids, bag, "nn.EmbeddingBag", mkb)
+            assert k_rows.stride(1) == 0  # the bag row is spread as a view, not copied
+            live = (k_ids >= 0).unsqueeze(-1).numpy()
+            np.testing.assert_allclose(np.where(live, k_rows.double().numpy(), 0.0), ref, rtol=1e-6, atol=1e-7)
+    with pytest.raises(NotImplementedError, match="max"):
+        final_embedding(ids, bag, "nn.EmbeddingBag", dict(mkb, mode="max"))
+    emb.check_ids(ids, vocab=20)
+    with pytest.raises(ValueError, match="out of range"):
+        emb.check_ids(ids, vocab=10)
+    with pytest.raises(ValueError, match="negative"):
+        emb.check_ids(ids - 5)

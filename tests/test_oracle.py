@@ -519,3 +519,119 @@ def test_ekfac_rotation_and_precondition():
     score = dw.reshape(b, -1) @ oracle.ekfac_precondition(
         oracle.ekfac_rotate_materialized(dw2, u_a, u_g), u_a, u_g, lam).T
     assert rel_err(score, dw.reshape(b, -1) @ u @ np.diag(1 / lam) @ u.T @ dw2.T) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# embedding layers
+# ---------------------------------------------------------------------------
+
+
+def _autograd_embedding_grads(ids, g, vocab, padding_idx=None, bag_mode=None):
+    """Per-sample weight.grad of nn.Embedding / nn.EmbeddingBag (float64, CPU)
+    for output gradients g, flattened to (B, vocab*E)."""
+    e = g.shape[-1]
+    torch.manual_seed(0)
+    if bag_mode is None:
+        layer = torch.nn.Embedding(vocab, e, padding_idx=padding_idx).double()
+    else:
+        layer = torch.nn.EmbeddingBag(vocab, e, mode=bag_mode, padding_idx=padding_idx).double()
+    ids_t, g_t = torch.from_numpy(ids), torch.from_numpy(g)
+    out = []
+    for i in range(ids.shape[0]):
+        layer.weight.grad = None
+        (layer(ids_t[i:i + 1]) * g_t[i:i + 1]).sum().backward()
+        out.append(layer.weight.grad.flatten().numpy().copy())
+    return np.stack(out)
+
+
+def test_embedding_materialize_against_autograd():
+    r = _rng(40)
+    vocab, b, t, e = 13, 3, 9, 5
+    ids = r.integers(0, vocab, (b, t))
+    ids[0, :4] = 7  # repeated ids accumulate into one row
+    g = r.standard_normal((b, t, e))
+    np.testing.assert_allclose(oracle.embedding_materialize(ids, g, vocab),
+                               _autograd_embedding_grads(ids, g, vocab), rtol=1e-12, atol=1e-12)
+    # padding_idx: the reference zeroes g at the pad positions (preprocess.py:403-408)
+    pad = 2
+    ids[:, -2:] = pad
+    g_pad = np.where((ids == pad)[..., None], 0.0, g)
+    np.testing.assert_allclose(oracle.embedding_materialize(ids, g_pad, vocab),
+                               _autograd_embedding_grads(ids, g, vocab, padding_idx=pad), rtol=1e-12, atol=1e-12)
+    with pytest.raises(ValueError):
+        oracle.embedding_materialize(ids, g, 5)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_embedding_materialize_rounds_like_torch_scatter_add(dtype):
+    """torch's CPU scatter_add_ (the reference's call, expanded index) sums in
+    fp32 in ascending token order and rounds once to the dtype; the oracle
+    agrees bit for bit (many repeats of few ids make the order and the
+    accumulation dtype matter)."""
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    r = _rng(41)
+    vocab, b, t, e = 6, 4, 200, 16
+    ids = r.integers(0, vocab, (b, t))
+    g = torch.from_numpy(r.standard_normal((b, t, e)) * 3).to(tdt)
+    ref = torch.zeros(b, vocab, e, dtype=tdt)
+    ref.scatter_add_(1, torch.from_numpy(ids).unsqueeze(-1).expand(b, t, e), g)
+    got = oracle.embedding_materialize(ids, g.float().numpy(), vocab, dtype=dtype)
+    assert np.array_equal(got.reshape(b, vocab, e), ref.float().numpy())
+    # the accumulation dtype is visible: rounding after every add differs
+    if dtype != "f32":
+        per_add = torch.zeros(b, vocab, e, dtype=tdt)
+        for s in range(t):
+            per_add[torch.arange(b), torch.from_numpy(ids[:, s])] += g[:, s]
+        assert not torch.equal(per_add, ref)
+
+
+@pytest.mark.parametrize("mode", ["sum", "mean"])
+@pytest.mark.parametrize("pad", [None, 0])
+def test_embedding_bag_expand_against_autograd(mode, pad):
+    r = _rng(42)
+    vocab, n, t, e = 11, 4, 6, 3
+    ids = r.integers(1, vocab, (n, t))
+    if pad is not None:
+        ids[:, -2:] = pad
+        ids[1, -3] = pad  # a bag with another non-pad count
+        ids[3, :] = pad  # an all-pad bag: zero gradient
+    g = r.standard_normal((n, e))
+    a, rows = oracle.embedding_bag_expand(ids, g, mode, pad)
+    np.testing.assert_allclose(oracle.embedding_materialize(a, rows, vocab),
+                               _autograd_embedding_grads(ids, g, vocab, padding_idx=pad, bag_mode=mode),
+                               rtol=1e-12, atol=1e-12)
+
+
+def _brute_embedding_gram(tok1, g1, tok2, g2):
+    out = np.zeros((tok1.shape[0], tok1.shape[1], tok2.shape[0]))
+    for i in range(tok1.shape[0]):
+        for t in range(tok1.shape[1]):
+            for j in range(tok2.shape[0]):
+                out[i, t, j] = sum(float(g1[i, t] @ g2[j, s]) for s in range(tok2.shape[1])
+                                   if tok1[i, t] == tok2[j, s])
+    return out
+
+
+def test_embedding_cross_gram_against_loops_and_autograd():
+    r = _rng(43)
+    vocab, e = 7, 4
+    tok1, tok2 = r.integers(0, vocab, (3, 5)), r.integers(0, vocab, (2, 8))
+    g1, g2 = r.standard_normal((3, 5, e)), r.standard_normal((2, 8, e))
+    brute = _brute_embedding_gram(tok1, g1, tok2, g2)
+    np.testing.assert_allclose(oracle.embedding_cross_gram(tok1, g1, tok2, g2), brute.sum(1), rtol=1e-12)
+    m1 = _autograd_embedding_grads(tok1, g1, vocab)
+    m2 = _autograd_embedding_grads(tok2, g2, vocab)
+    np.testing.assert_allclose(oracle.embedding_cross_gram(tok1, g1, tok2, g2), m1 @ m2.T, rtol=1e-12, atol=1e-12)
+
+
+def test_embedding_per_token_against_loops_and_dense_form():
+    r = _rng(44)
+    vocab, e = 6, 3
+    tok1, tok2 = r.integers(0, vocab, (2, 7)), r.integers(0, vocab, (3, 4))
+    g1, g2 = r.standard_normal((2, 7, e)), r.standard_normal((3, 4, e))
+    per_tok = oracle.embedding_cross_gram_per_token(tok1, g1, tok2, g2)
+    np.testing.assert_allclose(per_tok, _brute_embedding_gram(tok1, g1, tok2, g2), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(per_tok.sum(1), oracle.embedding_cross_gram(tok1, g1, tok2, g2), rtol=1e-12)
+    m2 = oracle.embedding_materialize(tok2, g2, vocab)
+    np.testing.assert_allclose(oracle.embedding_per_token_dense(tok1, g1, m2, vocab), per_tok,
+                               rtol=1e-12, atol=1e-12)
