@@ -27,9 +27,10 @@ from typing import TYPE_CHECKING
 import torch
 
 from dattri_llm_amd import kernels
-from dattri_llm_amd.gradient.ops import cost, dtypes
+from dattri_llm_amd.gradient.ops import conv, cost, dtypes
 from dattri_llm_amd.gradient.ops import embedding as emb
 from dattri_llm_amd.gradient.ops.materialize import (
+    conv_dense,
     linear_dense,
     materialize,
     materialize_blocked,
@@ -156,6 +157,123 @@ def _ghost_pairs(pairs, out: torch.Tensor) -> None:
         kernels.ghost_gram_grouped(g_1, g_2, bias=flags, out=out, accumulate=True)
 
 
+# ---------------------------------------------------------------------------
+# Convolutions and grouped (4-D) factors: the linear kernels, per group
+# ---------------------------------------------------------------------------
+
+
+def _is_conv_family(layer_type: str, a) -> bool:
+    """Conv / ConvTranspose layers, and any factors with a group axis."""
+    return is_conv(layer_type) or is_conv_transpose(layer_type) or to_3d(a).ndim == 4
+
+
+def _conv_pair(c1, c2):
+    if c1.bias != c2.bias:
+        raise ValueError("the two sides disagree on the bias column")
+    if c1.groups != c2.groups or c1.a.dim() != c2.a.dim():
+        raise ValueError(f"the two sides disagree on the group count ({c1.groups} vs {c2.groups})")
+    if c1.a.shape[-1] != c2.a.shape[-1] or c1.g.shape[-1] != c2.g.shape[-1]:
+        raise ValueError("the two sides disagree on the layer widths")
+
+
+def _conv_operands(c):
+    (a, g), _ = _kernel_operands(c.a, c.g)
+    return conv.ConvFactors(a, g, c.bias, c.transpose)
+
+
+def _group_rows(c, e: int):
+    """Group e of a side as the grouped kernel's (rows, width) operands: all
+    B*L rows, sample b's rows b*L .. b*L+L-1."""
+    a, g = c.group(e)
+    b, length = a.shape[:2]
+    seg = torch.arange(0, b * length + 1, max(length, 1), dtype=torch.int32, device=a.device)[: b + 1]
+    return a.reshape(b * length, a.shape[-1]), g.reshape(b * length, g.shape[-1]), seg, None
+
+
+def _conv_gram32(c1, c2, mode, out=None, accumulate=False):
+    """fp32 (B1, B2) cross-gram of two convolution sides (dot.py:88-118): the
+    ungrouped case is the linear layer's; groups pair with their own group
+    only -- one grouped ghost launch over all groups, or each group's dW."""
+    _conv_pair(c1, c2)
+    if c1.groups == 1 and c1.a.dim() == 3:
+        return _linear_gram32(c1.a, c1.g, c1.bias, c2.a, c2.g, c2.bias, mode, out=out, accumulate=accumulate)
+    c1, c2 = _conv_operands(c1), _conv_operands(c2)
+    b1, s, _g, k = c1.a.shape
+    b2, d = c2.a.shape[0], c1.g.shape[-1]
+    if mode == "auto":  # per-group widths: the group count scales both costs alike
+        mode = _route(b1, b2, s, k + int(c1.bias), d)
+    if mode == "materialized":
+        return kernels.score_gemm([(conv_dense(c1), conv_dense(c2))], out=out, accumulate=accumulate)
+    if mode != "factorized":
+        raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
+    if out is None:
+        out = torch.zeros(b1, b2, dtype=torch.float32, device=c1.a.device)
+    elif not accumulate:
+        out.zero_()
+    groups1 = [_group_rows(c1, e) for e in range(c1.groups)]
+    groups2 = [_group_rows(c2, e) for e in range(c2.groups)]
+    return kernels.ghost_gram_grouped(groups1, groups2, bias=c1.bias, out=out, accumulate=True)
+
+
+def _conv_diag32(c1, c2) -> torch.Tensor:
+    """fp32 (B,) per-sample dots (squared norms for one side with itself)."""
+    _conv_pair(c1, c2)
+    if c1.a.shape[0] != c2.a.shape[0]:
+        raise ValueError("per-sample dots need two blocks of one batch size")
+    same = c1 is c2
+    c1 = _conv_operands(c1)
+    c2 = c1 if same else _conv_operands(c2)
+    out = torch.zeros(c1.a.shape[0], dtype=torch.float32, device=c1.a.device)
+    for e in range(c1.groups):
+        (x1, y1), (x2, y2) = c1.group(e), c2.group(e)
+        if same:
+            x2, y2 = x1, y1
+        kernels.ghost_gram_diag(x1, y1, x2, y2, bias=c1.bias, out=out, accumulate=True)
+    return out
+
+
+def _conv_norm32(c, mode) -> torch.Tensor:
+    """fp32 (B,) squared norms, routed by the norm rule on per-group widths
+    (dot.py:386-405)."""
+    s, k, d = c.a.shape[1], c.a.shape[-1] + int(c.bias), c.g.shape[-1]
+    if mode == "auto":
+        mode = "materialized" if maybe_use_materialized_norm(s, k, d) else "factorized"
+    if mode == "materialized":
+        return _sq_row_norms(conv_dense(_conv_operands(c)))
+    if mode != "factorized":
+        raise ValueError("mode must be 'factorized', 'materialized', or 'auto'")
+    return _conv_diag32(c, c)
+
+
+def _conv_per_token32(c1, c2) -> torch.Tensor:
+    """fp32 (B1, T1, B2): side 1's location t against side 2's whole gradient,
+    summed over the groups (dot.py:216-222)."""
+    _conv_pair(c1, c2)
+    c1, c2 = _conv_operands(c1), _conv_operands(c2)
+    out = None
+    for e in range(c1.groups):
+        (x1, y1), (x2, y2) = c1.group(e), c2.group(e)
+        out = kernels.ghost_gram_per_token(x1, y1, x2, y2, bias=c1.bias, out=out, accumulate=out is not None)
+    return out
+
+
+def _conv_dense_per_token32(c1, m2: torch.Tensor) -> torch.Tensor:
+    """fp32 (B1, T1, B2) against dense per-sample gradients in materialize's
+    layout (dot.py:248-263): per group, (Wg, Wa) blocks -- (Wa, Wg) for a
+    transposed convolution, whose roles the kernel then swaps."""
+    c1 = _conv_operands(c1)
+    (m2,), _ = _kernel_operands(m2.reshape(m2.shape[0], -1))
+    groups = c1.groups
+    per = m2.reshape(m2.shape[0], groups, -1)
+    out = None
+    for e in range(groups):
+        x1, y1 = c1.group(e)
+        if c1.transpose:  # block (Wa, Wg): sum_c a[c] (M g)[c]
+            x1, y1 = y1, x1
+        out = kernels.dense_per_token(x1, y1, per[:, e], bias=c1.bias, out=out, accumulate=out is not None)
+    return out
+
+
 def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Tensor:
     """Cross-gram ``K[i, j] = <dW1_i, dW2_j>`` on already-preprocessed factors
     (dot.py:36-118)."""
@@ -168,10 +286,11 @@ def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Ten
         if layer_type not in TOKEN_NORM_TYPES:
             require_supported(layer_type, "cross_gram")
         return _dense_gram(norm_grad_from_final(a1, g1), norm_grad_from_final(a2, g2)).to(out_dtype)
-    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+    if _is_conv_family(layer_type, a1):
+        c1, c2 = conv.final(a1, g1, layer_type, None, False), conv.final(a2, g2, layer_type, None, False)
+        return _conv_gram32(c1, c2, mode).to(out_dtype)
+    if not is_linear(layer_type):
         require_supported(layer_type, "cross_gram")
-    if to_3d(a1).ndim == 4:
-        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
     return _linear_gram32(a1, g1, False, a2, g2, False, mode).to(out_dtype)
 
 
@@ -180,6 +299,8 @@ def _side(a, g, layer_type, module_kwargs, include_bias):
     for one raw side."""
     if is_embedding(layer_type):
         return "embedding", emb.side(a, g, layer_type, module_kwargs)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or (module_kwargs is None and a.ndim == 4):
+        return "conv", conv.final(a, g, layer_type, module_kwargs, include_bias)
     if layer_type in TOKEN_NORM_TYPES:
         if module_kwargs is not None:
             return "norm", norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
@@ -196,6 +317,8 @@ def _cross_factors32(a1, g1, a2, g2, layer_type, mk1, mk2, include_bias, mode, o
     _, s2 = _side(a2, g2, layer_type, mk2, include_bias)
     if kind == "embedding":
         return emb.gram32(s1, s2, out=out, accumulate=accumulate)
+    if kind == "conv":
+        return _conv_gram32(s1, s2, mode, out=out, accumulate=accumulate)
     if kind == "norm":
         return _dense_gram(s1, s2, out=out, accumulate=accumulate)
     return _linear_gram32(*s1, *s2, mode, out=out, accumulate=accumulate)
@@ -230,6 +353,8 @@ def dot_factors(a1, g1, a2, g2, layer_type: str, module_kwargs1: dict | None = N
     _, s2 = _side(a2, g2, layer_type, module_kwargs2, include_bias)
     if kind == "embedding":
         return emb.diag32(s1, s2).to(out_dtype)
+    if kind == "conv":
+        return _conv_diag32(s1, s2).to(out_dtype)
     if kind == "norm":
         (m1, m2), _ = _kernel_operands(_rows(s1), _rows(s2))
         return kernels.row_dots([(m1, m2)]).to(out_dtype)
@@ -259,6 +384,8 @@ def grad_norm_sq_factors(a, g, layer_type: str, module_kwargs: dict | None = Non
     kind, side = _side(a, g, layer_type, module_kwargs, include_bias)
     if kind == "embedding":  # the diagonal of the pairwise gram (dot.py:383-384)
         return emb.diag32(side, side).to(out_dtype)
+    if kind == "conv":
+        return _conv_norm32(side, mode).to(out_dtype)
     if kind == "norm":
         return _sq_row_norms(side).to(out_dtype)
     x, y, bias = side
@@ -471,7 +598,10 @@ def cross_gram_per_token(a1, g1, a2, g2, layer_type: str) -> torch.Tensor:
             require_supported(layer_type, "cross_gram_per_token")
         x1, y1, x2, y2 = dtypes.align(to_3d(a1), to_3d(g1), to_3d(a2), to_3d(g2))
         return _norm_per_token32(x1 * y1, norm_grad_from_final(x2, y2)).to(out_dtype)
-    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+    if _is_conv_family(layer_type, a1):
+        c1, c2 = conv.final(a1, g1, layer_type, None, False), conv.final(a2, g2, layer_type, None, False)
+        return _conv_per_token32(c1, c2).to(out_dtype)
+    if not is_linear(layer_type):
         require_supported(layer_type, "cross_gram_per_token")
     a1, g1, a2, g2 = _linear_operands(a1, g1, a2, g2)
     return kernels.ghost_gram_per_token(a1, g1, a2, g2).to(out_dtype)
@@ -490,7 +620,9 @@ def cross_gram_per_token_dense(a1, g1, m2, layer_type: str) -> torch.Tensor:
             require_supported(layer_type, "cross_gram_per_token_dense")
         x1, y1 = dtypes.align(to_3d(a1), to_3d(g1))
         return _norm_per_token32(x1 * y1, m2).to(out_dtype)
-    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+    if _is_conv_family(layer_type, a1):
+        return _conv_dense_per_token32(conv.final(a1, g1, layer_type, None, False), m2).to(out_dtype)
+    if not is_linear(layer_type):
         require_supported(layer_type, "cross_gram_per_token_dense")
     a1, g1, m2 = _linear_operands(a1, g1, m2)
     return kernels.dense_per_token(a1, g1, m2.reshape(m2.shape[0], -1)).to(out_dtype)
@@ -516,6 +648,13 @@ def cross_dot_per_token(f1, f2, layer_type: str, include_bias: bool = True) -> t
         b2 = f2.as_batch_first()
         s2 = emb.side(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs)
         return emb.per_token32(s1, s2).to(out_dtype)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or (mk1 is None and a1.ndim == 4):
+        c1 = conv.final(a1, g1, layer_type, mk1, include_bias)
+        if dense2:
+            return _conv_dense_per_token32(c1, f2).to(out_dtype)
+        b2 = f2.as_batch_first()
+        c2 = conv.final(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs, include_bias)
+        return _conv_per_token32(c1, c2).to(out_dtype)
     if not is_linear(layer_type):
         require_supported(layer_type, "cross_dot_per_token")
     x1, y1, bias1 = final_linear(a1, g1, layer_type, mk1, include_bias)

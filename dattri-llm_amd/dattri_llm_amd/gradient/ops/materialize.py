@@ -2,7 +2,8 @@
 
 Mirrors ``dattri_llm/gradient/ops/materialize.py:22-146`` for linear layers
 (``bmm(g^T, a)`` flattened to ``(B, out*in)``, index ``o*K + i``, with the bias
-column last), token norms (``sum_t x_hat * g``, and ``[dgamma, dbeta]`` with
+column last), convolutions (per group, the transposed layout for
+ConvTranspose, :100-114), token norms (``sum_t x_hat * g``, and ``[dgamma, dbeta]`` with
 a bias) and embeddings (the scatter-add into ``(B, vocab*E)``, run by
 ``da_materialize_embedding``).  The linear case runs the ``da_materialize_linear`` MFMA kernel; the
 norm case runs ``da_norm_weight_grad``, which normalises in registers and never
@@ -14,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from dattri_llm_amd import kernels
-from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops import conv, dtypes
 from dattri_llm_amd.gradient.ops import embedding as emb
 from dattri_llm_amd.gradient.ops.preprocess import (
     final_linear,
@@ -24,6 +25,8 @@ from dattri_llm_amd.gradient.ops.preprocess import (
 )
 from dattri_llm_amd.gradient.ops.types import (
     TOKEN_NORM_TYPES,
+    is_conv,
+    is_conv_transpose,
     is_embedding,
     is_linear,
     is_norm,
@@ -63,6 +66,23 @@ def linear_dense(a, g, bias: bool) -> torch.Tensor:
     (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
     out = kernels.materialize_linear(ao, go, bias=bias, out_dtype=dtypes.kernel_dtype(out_dtype))
     return out.to(out_dtype)
+
+
+def conv_dense(c) -> torch.Tensor:
+    """(B, d) per-sample weight gradient of convolution factors in the kernel
+    dtype of their operands (materialize.py:100-114): per group a (Wg, Wa(+1))
+    block -- (Wa, Wg) for a transposed convolution -- groups in order."""
+    b = c.a.shape[0]
+    if c.a.dim() == 3:
+        if c.transpose:
+            return kernels.materialize_linear(c.g, c.a)
+        return kernels.materialize_linear(c.a, c.g, bias=c.bias)
+    wa, wg = c.a.shape[-1] + int(c.bias), c.g.shape[-1]
+    out = torch.empty(b, c.groups, wa * wg, dtype=c.a.dtype, device=c.a.device)
+    for e in range(c.groups):
+        x, y = c.group(e)
+        out[:, e] = kernels.materialize_linear(y, x) if c.transpose else kernels.materialize_linear(x, y, bias=c.bias)
+    return out.reshape(b, -1)
 
 
 def norm_token_rows(a, g, layer_type: str, module_kwargs: dict | None = None,
@@ -106,10 +126,12 @@ def materialize_factors(
         if module_kwargs is not None:
             return norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
         return norm_grad_from_final(a, g)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or (module_kwargs is None and a.ndim == 4):
+        c = conv.final(a, g, layer_type, module_kwargs, include_bias)
+        (x, y), out_dtype = _operands(c.a, c.g)
+        return conv_dense(conv.ConvFactors(x, y, c.bias, c.transpose)).to(out_dtype)
     if is_norm(layer_type) or not is_linear(layer_type):
         require_supported(layer_type, "materialize_factors")
-    if a.ndim == 4:
-        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
     a, g, bias = final_linear(a, g, layer_type, module_kwargs, include_bias)
     return linear_dense(a, g, bias)
 

@@ -5,8 +5,8 @@ scoring path: linear layers (bias folded as a ones column, :436-437) and token
 norms (RMSNorm / LayerNorm x_hat, :366-384, computed by the ``da_norm_xhat``
 kernel, with the bias augmentation of ``norm.py:95-110``) and embeddings
 (``nn.Embedding`` padding positions, ``nn.EmbeddingBag`` bags spread over their
-tokens, :403-416 and :126-169).  Conv and channel-norm layers raise
-``NotImplementedError``.
+tokens, :403-416 and :126-169) and convolutions (the unfolding of
+``conv.py``).  Channel-norm layers raise ``NotImplementedError``.
 
 The public ``preprocess_factors`` returns exactly the reference's tensors.  The
 scoring kernels never need them: :func:`final_linear` and :func:`norm_spec`
@@ -22,7 +22,7 @@ from dataclasses import dataclass
 import torch
 
 from dattri_llm_amd import kernels
-from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops import conv, dtypes
 from dattri_llm_amd.gradient.ops.types import (
     CONV_TRANSPOSE_TYPES,
     CONV_TYPES,
@@ -139,10 +139,12 @@ def preprocess_factors(
         if module_kwargs.get("padding_idx") is not None:
             rows = rows.masked_fill((a == module_kwargs["padding_idx"]).unsqueeze(-1), 0)
         return a, rows.contiguous()
+    if layer_type in CONV_TYPES or layer_type in CONV_TRANSPOSE_TYPES:
+        return conv.preprocess(a, g, layer_type, module_kwargs, include_bias)
     if is_norm(layer_type) or not is_linear(layer_type):
         raise NotImplementedError(
             f"preprocess_factors: {layer_type!r} is outside the MI355X scoring path "
-            "(linear, embedding and RMSNorm/LayerNorm layers)."
+            "(linear, convolution, embedding and RMSNorm/LayerNorm layers)."
         )
     if has_bias:
         return torch.cat([a, torch.ones_like(a[..., :1])], dim=-1), g

@@ -62,7 +62,7 @@ def require_supported(layer_type: str, what: str) -> None:
     if is_linear(layer_type) or layer_type in TOKEN_NORM_TYPES:
         return
     raise NotImplementedError(
-        f"{what}: layer type {layer_type!r} is outside the MI355X scoring path for this operation "
-        "(linear layers and RMSNorm/LayerNorm everywhere, embeddings in the inner products and "
-        "materialization); conv and channel-norm layers are not implemented."
+        f"{what}: layer type {layer_type!r} is not covered by this operation on the MI355X kernels "
+        "(the inner products and materialization cover linear, convolution, embedding and "
+        "RMSNorm/LayerNorm layers; channel norms are not implemented)."
     )

@@ -51,6 +51,12 @@ ekfac_precondition             gradient/ops/kronecker.py:413-458              la
                                                                               score == vec(dW1)^T (U (x) U) diag(1/lam)
                                                                               (U (x) U)^T vec(dW2), matrices formed
 kfac_precondition_materialized gradient/ops/kronecker.py:386-410              kron(G^-1, A^-1) @ vec(dW)
+conv_unfold                    gradient/ops/preprocess.py:33-106 (im2col)     materialized through conv_preprocess:
+conv_preprocess                gradient/ops/preprocess.py:171-228, :417-433   autograd weight.grad (+ bias.grad) of
+conv_materialize               gradient/ops/materialize.py:100-114            nn.Conv1d/2d/3d and nn.ConvTranspose1d/2d
+                                                                              (stride, padding, dilation, groups, bias)
+grouped_cross_gram             gradient/ops/dot.py:100-109                    equals conv_materialize M1 @ M2^T
+grouped_cross_gram_per_token   gradient/ops/dot.py:216-218                    sums over t to grouped_cross_gram; brute force
 embedding_materialize          gradient/ops/materialize.py:22-48              torch autograd weight.grad of nn.Embedding
                                                                               (f64); torch's CPU scatter_add_ in bf16 /
                                                                               fp16 / fp32, bit for bit (per-add rounding)
@@ -75,6 +81,11 @@ __all__ = [
     "cross_gram_materialized",
     "cross_gram_per_token",
     "cross_gram_per_token_dense",
+    "conv_materialize",
+    "conv_preprocess",
+    "conv_unfold",
+    "grouped_cross_gram",
+    "grouped_cross_gram_per_token",
     "ekfac_materialize_factors",
     "embedding_bag_expand",
     "embedding_cross_gram",
@@ -738,4 +749,94 @@ def embedding_per_token_dense(tok1, g1, m2, vocab: int) -> np.ndarray:
     m2 = np.asarray(m2).reshape(m2.shape[0], vocab, e)
     rows = m2[:, tok1.reshape(-1)].reshape(m2.shape[0], *tok1.shape, e)
     return np.einsum("bte,cbte->btc", g1, rows)
+
+
+# ---------------------------------------------------------------------------
+# convolutions and grouped factors
+# ---------------------------------------------------------------------------
+
+
+def conv_unfold(x, kernel_size, stride, padding, dilation) -> np.ndarray:
+    """im2col of preprocess.py:33-106, one output location at a time:
+    (N, C, *spatial) -> (N, L, C*prod(k)), zero padding, features ordered
+    (channel, taps) and locations row-major over the output grid."""
+    import itertools
+
+    x = np.asarray(x)
+    rank = x.ndim - 2
+    ks, ss, ps, ds = (tuple(v) for v in (kernel_size, stride, padding, dilation))
+    xp = np.pad(x, [(0, 0), (0, 0)] + [(p, p) for p in ps])
+    outs = [(xp.shape[2 + i] - ds[i] * (ks[i] - 1) - 1) // ss[i] + 1 for i in range(rank)]
+    n, c = x.shape[:2]
+    cols = []
+    for loc in itertools.product(*(range(o) for o in outs)):
+        pos = [loc[i] * ss[i] + np.arange(ks[i]) * ds[i] for i in range(rank)]
+        patch = xp[(slice(None), slice(None)) + np.ix_(*pos)]  # (N, C, k_1, ..., k_r)
+        cols.append(patch.reshape(n, -1))
+    return np.stack(cols, axis=1)
+
+
+def conv_preprocess(a, g, transpose: bool, kernel_size, stride, padding, dilation, groups: int = 1,
+                    has_bias: bool = False):
+    """The preprocessed factors of a convolution (preprocess.py:417-433) or a
+    transposed convolution (:171-228): 3-D, or 4-D (N, L, G, W/G) with groups;
+    the conv bias a ones column per group, the transposed conv's bias an extra
+    location and feature block."""
+    a, g = np.asarray(a), np.asarray(g)
+    n = a.shape[0]
+    win = (kernel_size, stride, padding, dilation)
+
+    def split(x):
+        return x if groups == 1 else x.reshape(*x.shape[:-1], groups, x.shape[-1] // groups)
+
+    if not transpose:
+        a_f = split(conv_unfold(a, *win))
+        g_f = split(g.reshape(n, g.shape[1], -1).transpose(0, 2, 1))
+        if has_bias:
+            a_f = np.concatenate([a_f, np.ones(a_f.shape[:-1] + (1,), dtype=a_f.dtype)], axis=-1)
+        return a_f, g_f
+    a_f = split(a.reshape(n, a.shape[1], -1).transpose(0, 2, 1))
+    g_f = split(conv_unfold(g, *win))
+    if not has_bias:
+        return a_f, g_f
+    c_out = g.shape[1]
+    cg = c_out // groups
+    bias_grad = g.reshape(n, c_out, -1).sum(axis=2)
+    if groups > 1:
+        bias_grad = bias_grad.reshape(n, groups, cg)
+    zeros_a = np.zeros(a_f.shape[:-1] + (1,), dtype=a_f.dtype)
+    a_pad = np.concatenate([a_f, zeros_a], axis=-1)
+    a_row = np.zeros_like(a_pad[:, :1])
+    a_row[..., -1] = 1.0
+    g_pad = np.concatenate([g_f, np.zeros(g_f.shape[:-1] + (cg,), dtype=g_f.dtype)], axis=-1)
+    g_row = np.zeros_like(g_pad[:, :1])
+    g_row[:, 0, ..., -cg:] = bias_grad
+    return np.concatenate([a_pad, a_row], axis=1), np.concatenate([g_pad, g_row], axis=1)
+
+
+def conv_materialize(a, g, transpose: bool = False) -> np.ndarray:
+    """Per-sample weight gradient of preprocessed convolution factors
+    (materialize.py:100-114): per group (D, K) = g^T a, or (C, P) = a^T g for a
+    transposed convolution, groups in order, flattened to (B, d)."""
+    a, g = np.asarray(a), np.asarray(g)
+    if a.ndim == 3:
+        a, g = a[:, :, None], g[:, :, None]
+    if transpose:
+        return np.einsum("btgc,btgp->bgcp", a, g).reshape(a.shape[0], -1)
+    return np.einsum("btgk,btgd->bgdk", a, g).reshape(a.shape[0], -1)
+
+
+def grouped_cross_gram(a1, g1, a2, g2) -> np.ndarray:
+    """Grouped factorized cross_gram (dot.py:100-109): the group axis is a batch
+    axis aligned on both sides, K[i, j] = sum_{g,t,s} (a1 . a2)(g1 . g2)."""
+    ka = np.einsum("btgk,csgk->bcgts", a1, a2)
+    kg = np.einsum("btgd,csgd->bcgts", g1, g2)
+    return (ka * kg).sum(axis=(2, 3, 4))
+
+
+def grouped_cross_gram_per_token(a1, g1, a2, g2) -> np.ndarray:
+    """Grouped cross_gram_per_token (dot.py:216-218): side 2's per-group weight
+    gradients, then each side-1 token's per-group rank-1 term against them."""
+    m2 = np.einsum("csgk,csgd->cgkd", a2, g2)
+    return np.einsum("btgk,btgd,cgkd->btc", a1, g1, m2)
 

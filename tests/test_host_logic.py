@@ -92,7 +92,9 @@ def test_unsupported_layers_raise(ops):
     with pytest.raises(NotImplementedError):
         ops.kfac_cross_factors(a, a, a, a, "nn.Embedding", torch.eye(8), torch.eye(8))
     with pytest.raises(NotImplementedError):
-        ops.preprocess_factors(a, a, "nn.Conv2d", {"has_bias": False})
+        ops.preprocess_factors(a, a, "nn.GroupNorm", {"has_bias": False, "num_groups": 1, "eps": 1e-5})
+    with pytest.raises(NotImplementedError):
+        ops.project_factors(a, a, "nn.Conv2d", None, None, proj_dim=4)
     with pytest.raises(ValueError, match="factorized projection is undefined"):
         ops.project_factors(a, a, "nn.LayerNorm", None, None, proj_dim=4)
 
@@ -303,3 +305,38 @@ def test_embedding_preprocess_matches_oracle():
         emb.check_ids(ids, vocab=10)
     with pytest.raises(ValueError, match="negative"):
         emb.check_ids(ids - 5)
+
+
+# ---------------------------------------------------------------------------
+# convolution unfolding (host side, no kernels)
+# ---------------------------------------------------------------------------
+
+
+def test_conv_preprocess_matches_oracle():
+    import numpy as np
+
+    import oracle
+    from dattri_llm_amd.gradient.ops import conv, preprocess_factors
+    from test_oracle import CONV_CASES, conv_inputs
+
+    names = {(False, 1): "nn.Conv1d", (False, 2): "nn.Conv2d", (False, 3): "nn.Conv3d",
+             (True, 1): "nn.ConvTranspose1d", (True, 2): "nn.ConvTranspose2d"}
+    for case in CONV_CASES:
+        transpose, rank, _ci, _co, k, s, p, d, groups, bias, _sp = case
+        x, gout = conv_inputs(case)
+        mk = {"has_bias": bias, "kernel_size": k, "stride": s, "padding": p, "dilation": d, "groups": groups}
+        lt = names[(transpose, rank)]
+        a, g = preprocess_factors(torch.from_numpy(x), torch.from_numpy(gout), lt, mk)
+        ra, rg = oracle.conv_preprocess(x, gout, transpose, k, s, p, d, groups, bias)
+        np.testing.assert_array_equal(a.numpy(), ra)
+        np.testing.assert_allclose(g.numpy(), rg, rtol=1e-12, atol=1e-12)  # the bias sums' order differs
+        # the kernels' operands: views, the conv bias left implicit
+        f = conv.final(torch.from_numpy(x), torch.from_numpy(gout), lt, mk, True)
+        assert f.transpose == transpose and f.groups == groups and f.bias == (bias and not transpose)
+        if f.bias:
+            np.testing.assert_array_equal(f.a.numpy(), ra[..., :-1])
+    # 'same' and 'valid' padding strings
+    x = torch.randn(2, 3, 9)
+    assert conv.unfold_patches(x, 3, 1, "same", 1).shape == (2, 9, 9)
+    assert conv.unfold_patches(x, 4, 1, "same", 2).shape == (2, 9, 12)
+    assert torch.equal(conv.unfold_patches(x, 3, 1, "valid", 1), conv.unfold_patches(x, 3, 1, 0, 1))

@@ -635,3 +635,102 @@ def test_embedding_per_token_against_loops_and_dense_form():
     m2 = oracle.embedding_materialize(tok2, g2, vocab)
     np.testing.assert_allclose(oracle.embedding_per_token_dense(tok1, g1, m2, vocab), per_tok,
                                rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# convolutions and grouped factors
+# ---------------------------------------------------------------------------
+
+# (transpose, rank, c_in, c_out, kernel, stride, padding, dilation, groups, bias, spatial)
+CONV_CASES = [
+    (False, 1, 3, 4, (3,), (2,), (1,), (1,), 1, True, (9,)),
+    (False, 2, 4, 6, (3, 2), (1, 2), (1, 0), (2, 1), 2, True, (7, 6)),
+    (False, 2, 4, 4, (3, 3), (1, 1), (1, 1), (1, 1), 4, False, (5, 5)),   # depthwise
+    (False, 3, 2, 4, (2, 2, 2), (1, 2, 1), (1, 0, 1), (1, 1, 1), 2, True, (4, 4, 3)),
+    (True, 1, 4, 3, (3,), (2,), (1,), (1,), 1, True, (5,)),
+    (True, 2, 4, 6, (3, 3), (2, 1), (1, 1), (1, 2), 2, True, (3, 4)),
+    (True, 2, 3, 2, (2, 2), (1, 1), (0, 0), (1, 1), 1, False, (3, 3)),
+]
+
+
+def conv_autograd_grads(case, x, gout):
+    """Per-sample [weight.grad | bias.grad] of the layer in the reference's
+    materialized layout, float64."""
+    transpose, rank, c_in, c_out, k, s, p, d, groups, bias, _sp = case
+    nn = torch.nn
+    cls = {(False, 1): nn.Conv1d, (False, 2): nn.Conv2d, (False, 3): nn.Conv3d,
+           (True, 1): nn.ConvTranspose1d, (True, 2): nn.ConvTranspose2d, (True, 3): nn.ConvTranspose3d}
+    torch.manual_seed(0)
+    layer = cls[(transpose, rank)](c_in, c_out, k, stride=s, padding=p, dilation=d, groups=groups,
+                                   bias=bias).double()
+    rows = []
+    for i in range(x.shape[0]):
+        layer.zero_grad()
+        (layer(torch.from_numpy(x[i:i + 1])) * torch.from_numpy(gout[i:i + 1])).sum().backward()
+        w = layer.weight.grad.numpy()
+        if not transpose:
+            m = w.reshape(c_out, -1)
+            if bias:
+                m = np.concatenate([m, layer.bias.grad.numpy()[:, None]], axis=1)
+            rows.append(m.reshape(-1))
+            continue
+        cg_in, cg_out = c_in // groups, c_out // groups
+        blocks = []
+        for e in range(groups):
+            wb = w[e * cg_in:(e + 1) * cg_in].reshape(cg_in, -1)
+            if bias:
+                full = np.zeros((cg_in + 1, wb.shape[1] + cg_out))
+                full[:cg_in, :wb.shape[1]] = wb
+                full[cg_in, wb.shape[1]:] = layer.bias.grad.numpy()[e * cg_out:(e + 1) * cg_out]
+                wb = full
+            blocks.append(wb.reshape(-1))
+        rows.append(np.concatenate(blocks))
+    return np.stack(rows)
+
+
+def conv_inputs(case, n=3, seed=50):
+    transpose, rank, c_in, c_out, k, s, p, d, groups, bias, sp = case
+    r = _rng(seed)
+    x = r.standard_normal((n, c_in) + sp)
+    nn = torch.nn
+    cls = {1: (nn.Conv1d, nn.ConvTranspose1d), 2: (nn.Conv2d, nn.ConvTranspose2d),
+           3: (nn.Conv3d, nn.ConvTranspose3d)}[rank][int(transpose)]
+    out_shape = cls(c_in, c_out, k, stride=s, padding=p, dilation=d, groups=groups).double()(
+        torch.from_numpy(x)).shape
+    gout = r.standard_normal(tuple(out_shape))
+    return x, gout
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_preprocess_and_materialize_against_autograd(case):
+    transpose, _rank, _ci, _co, k, s, p, d, groups, bias, _sp = case
+    x, gout = conv_inputs(case)
+    a, g = oracle.conv_preprocess(x, gout, transpose, k, s, p, d, groups, bias)
+    assert a.ndim == (4 if groups > 1 else 3)
+    np.testing.assert_allclose(oracle.conv_materialize(a, g, transpose), conv_autograd_grads(case, x, gout),
+                               rtol=1e-10, atol=1e-10)
+    # the unfolding itself for a 1-D conv, by hand: location l reads padded
+    # positions l*s + j*d for taps j, channel-major
+    if not transpose and len(k) == 1:
+        xp = np.pad(x, [(0, 0), (0, 0), (p[0], p[0])])
+        unf = oracle.conv_unfold(x, k, s, p, d)
+        for loc in range(unf.shape[1]):
+            want = [xp[:, c, loc * s[0] + j * d[0]] for c in range(x.shape[1]) for j in range(k[0])]
+            np.testing.assert_array_equal(unf[:, loc], np.stack(want, axis=1))
+
+
+def test_grouped_cross_gram_and_per_token():
+    r = _rng(51)
+    a1, g1 = r.standard_normal((3, 5, 2, 4)), r.standard_normal((3, 5, 2, 3))
+    a2, g2 = r.standard_normal((2, 4, 2, 4)), r.standard_normal((2, 4, 2, 3))
+    m1, m2 = oracle.conv_materialize(a1, g1), oracle.conv_materialize(a2, g2)
+    np.testing.assert_allclose(oracle.grouped_cross_gram(a1, g1, a2, g2), m1 @ m2.T, rtol=1e-12)
+    pt = oracle.grouped_cross_gram_per_token(a1, g1, a2, g2)
+    np.testing.assert_allclose(pt.sum(1), m1 @ m2.T, rtol=1e-12)
+    brute = np.zeros_like(pt)
+    for i in range(3):
+        for t in range(5):
+            for j in range(2):
+                brute[i, t, j] = sum(float(a1[i, t, e] @ a2[j, s, e]) * float(g1[i, t, e] @ g2[j, s, e])
+                                     for e in range(2) for s in range(4))
+    np.testing.assert_allclose(pt, brute, rtol=1e-12, atol=1e-12)
