@@ -208,6 +208,43 @@ __global__ __launch_bounds__(256) void embed_dense_per_token(const int64_t* __re
   }
 }
 
+
+// Entries of the per-sample embedding gradient without forming it
+// (projection.py:718-735, the "mask" capture of an embedding):
+//
+//   out[b, q] = sum over t with tok[b, t] == rows[q] of g[b, t, cols[q]]
+//
+// fp32, the tokens in ascending order.  One thread per kept entry, the
+// sample's ids staged through LDS in runs; a column outside [0, E) or a
+// negative id adds nothing.
+template <int DT>
+__global__ __launch_bounds__(256) void embed_gather_entries(const int64_t* __restrict__ tok, int64_t tok_bs,
+                                                            int64_t tok_ts, const char* __restrict__ g,
+                                                            int64_t g_bs, int64_t g_ts, int64_t tokens, int64_t E,
+                                                            const int64_t* __restrict__ rows,
+                                                            const int64_t* __restrict__ cols, int64_t k,
+                                                            float* __restrict__ out, int64_t ld_out) {
+  __shared__ int64_t ids[kEmbedIds];
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const bool live = q < k;
+  const int64_t v = live ? rows[q] : -1, e = live ? cols[q] : -1;
+  const bool use = live && v >= 0 && e >= 0 && e < E;
+  const int64_t* tb = tok + b * tok_bs;
+  const char* gb = g + b * g_bs;
+  float acc = 0.f;
+  for (int64_t t0 = 0; t0 < tokens; t0 += kEmbedIds) {
+    const int n = (int)(tokens - t0 < kEmbedIds ? tokens - t0 : kEmbedIds);
+    __syncthreads();  // the previous run is consumed
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ids[i] = tb[(t0 + i) * tok_ts];
+    __syncthreads();
+    if (!use) continue;
+    for (int i = 0; i < n; ++i)
+      if (ids[i] == v) acc += Elem<DT>::load(gb + (t0 + i) * g_ts, e);
+  }
+  if (live) out[b * ld_out + q] = acc;
+}
+
 }  // namespace
 }  // namespace da
 
@@ -332,3 +369,32 @@ extern "C" int da_dense_per_token_embedding(const int64_t* tok, const void* g, i
 #undef DA_EDPT
   return check_launch(who);
 }
+
+extern "C" int da_gather_embedding_entries(const int64_t* tok, const void* g, int dtype, int64_t batch,
+                                           int64_t tokens, int64_t E, int64_t tok_bstride, int64_t tok_tstride,
+                                           int64_t g_bstride, int64_t g_tstride, const int64_t* rows,
+                                           const int64_t* cols, int64_t k, float* out, int64_t ld_out,
+                                           void* stream) {
+  using namespace da;
+  const char* who = "da_gather_embedding_entries";
+  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype", who);
+  if (batch < 0 || tokens < 0 || E < 0 || k < 0) return set_error(DA_ERR_INVALID, "%s: negative size", who);
+  if (batch == 0 || k == 0) return DA_OK;
+  if (!out || !rows || !cols || (tokens > 0 && (!tok || !g))) return set_error(DA_ERR_INVALID, "%s: NULL pointer", who);
+  if (ld_out < k) return set_error(DA_ERR_INVALID, "%s: ld_out below k", who);
+  if (batch > 65535 || (k + 255) / 256 > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
+  const int64_t es = (int64_t)elem_bytes(dtype);
+  dim3 grid((unsigned)((k + 255) / 256), (unsigned)batch);
+  hipStream_t st = (hipStream_t)stream;
+#define DA_EGE(DT)                                                                                             \
+  embed_gather_entries<DT><<<grid, 256, 0, st>>>(tok, tok_bstride, tok_tstride, (const char*)g, g_bstride * es, \
+                                                 g_tstride * es, tokens, E, rows, cols, k, out, ld_out)
+  switch (dtype) {
+    case DA_BF16: DA_EGE(DA_BF16); break;
+    case DA_F16: DA_EGE(DA_F16); break;
+    default: DA_EGE(DA_F32); break;
+  }
+#undef DA_EGE
+  return check_launch(who);
+}
+

@@ -102,6 +102,8 @@ SIGNATURES.update(
             _I32,
             [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _I32, _I64, _I64, _I64, _P],
         ),
+        "da_gather_embedding_entries": (
+            _I32, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
         "da_materialize_embedding_workspace": (_I32, [_I64, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
         "da_materialize_embedding": (
             _I32, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P]),

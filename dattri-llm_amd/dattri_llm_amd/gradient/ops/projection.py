@@ -28,6 +28,13 @@ The other two styles of ``project_layer`` (projection.py:902-944):
   the ``da_gather_entries`` kernel without forming the gradient; the subset is
   drawn as the reference draws it (a CPU generator seeded from ``(proj_seed,
   width, proj_dim)``), so masked captures interchange.
+
+Layer families (projection.py:440-489, :718-775): linear layers, convolutions
+(the unfolded factors, a grouped one per group with shared matrices; masks in
+the per-group (rows, columns) layout, transposed for ConvTranspose) and
+embeddings (the input-side projection of a token is a row of the
+``(num_embeddings, proj_dim)`` matrix; a mask entry (v, e) sums the gradient
+column e over the tokens with id v, ``da_gather_embedding_entries``).
 """
 
 from __future__ import annotations
@@ -37,10 +44,18 @@ import math
 import torch
 
 from dattri_llm_amd import kernels
-from dattri_llm_amd.gradient.ops import dtypes
+from dattri_llm_amd.gradient.ops import conv, dtypes
+from dattri_llm_amd.gradient.ops import embedding as emb
 from dattri_llm_amd.gradient.ops.materialize import linear_dense, materialize_factors
-from dattri_llm_amd.gradient.ops.preprocess import final_linear, to_3d
-from dattri_llm_amd.gradient.ops.types import is_embedding, is_linear, is_norm, require_supported
+from dattri_llm_amd.gradient.ops.preprocess import final_linear, preprocess_factors, to_3d
+from dattri_llm_amd.gradient.ops.types import (
+    is_conv,
+    is_conv_transpose,
+    is_embedding,
+    is_linear,
+    is_norm,
+    require_supported,
+)
 from dattri_llm_amd.utils.cache import TensorCache
 
 PROJECTION_STYLES = ("logra", "dense", "mask")
@@ -225,8 +240,46 @@ def _linear_only(layer_type: str, what: str) -> None:
             f"factorized projection is undefined for {layer_type!r}: its gradient is not an outer "
             "product of the factors -- use materialized projection"
         )
-    if is_embedding(layer_type) or not is_linear(layer_type):
+    if not (is_linear(layer_type) or is_embedding(layer_type) or is_conv(layer_type)
+            or is_conv_transpose(layer_type)):
         require_supported(layer_type, what)
+
+
+def _embedding_vocab(module_kwargs, what: str) -> int:
+    if module_kwargs is None:
+        raise ValueError(
+            f"{what} of an embedding requires module_kwargs with 'num_embeddings' (the one-hot width "
+            "cannot be inferred from the captured factors)."
+        )
+    return int(module_kwargs["num_embeddings"])
+
+
+def _outer_sides(a, g, layer_type, projector, module_kwargs, include_bias, proj_dim, proj_seed, proj_kwargs):
+    """Projected ``(a_p, g_p)`` of an embedding or convolution (projection.py:457-489).
+
+    Embedding: a linear layer over one-hot ids, so the input-side projection of
+    token v is row v of the ``(num_embeddings, proj_dim)`` matrix -- gathered
+    instead of multiplying a one-hot tensor (the same values: one 1.0 times each
+    entry).  The one-hot is integer, so that side resolves its dtype alone
+    (fp32 under "auto"), as the reference's one-hot projection does.
+    Convolution: the unfolded factors (a grouped one keeps its group axis and
+    every group uses the same matrices), the conv bias an implicit ones column
+    (the matrix's last row)."""
+    if is_embedding(layer_type):
+        vocab = _embedding_vocab(module_kwargs, "Factorized projection")
+        ids, g = preprocess_factors(a, g, layer_type, module_kwargs, include_bias)
+        emb.check_ids(ids, vocab=vocab)
+        (g_f,) = dtypes.align(to_3d(g))
+        g_p = apply_projection(projector, g_f, proj_dim=proj_dim, proj_seed=proj_seed, **proj_kwargs)
+        kw = dict(proj_kwargs)
+        device = torch.device(kw.pop("device", g_f.device))
+        m = DattriProjector.coerce(projector).matrix(vocab, proj_dim=proj_dim, proj_seed=proj_seed + 1,
+                                                     device=device, dtype=dtypes.resolve(ids), **kw)
+        return m[ids.to(device)], g_p
+    c = conv.final(a, g, layer_type, module_kwargs, include_bias)
+    x, y = dtypes.align(c.a, c.g)
+    p_in, p_out = _resolve_pair(projector, x, y, c.bias, proj_dim, proj_seed, proj_kwargs)
+    return p_in(x.to(p_in.device)), p_out(y.to(p_out.device))
 
 
 def _resolve_pair(projector, a, g, bias, proj_dim, proj_seed, proj_kwargs):
@@ -246,6 +299,9 @@ def project_factors(a, g, layer_type: str, projector, module_kwargs: dict | None
     """LoGRA: project both factors, keeping the outer-product structure
     (projection.py:423-489).  Returns ``(a_p, g_p)``."""
     _linear_only(layer_type, "project_factors")
+    if not is_linear(layer_type):
+        return _outer_sides(a, g, layer_type, projector, module_kwargs, include_bias, proj_dim, proj_seed,
+                            proj_kwargs)
     bias = bool(module_kwargs is not None and module_kwargs["has_bias"] and include_bias)
     a, g = dtypes.align(to_3d(a), to_3d(g))
     p_in, p_out = _resolve_pair(projector, a, g, bias, proj_dim, proj_seed, proj_kwargs)
@@ -279,6 +335,10 @@ def project_outer_factors(a, g, layer_type: str, projector, module_kwargs: dict 
     the fused projection + per-sample outer-product kernel.  Returns
     ``(B, k_g * k_a)``, index ``o * k_a + i``."""
     _linear_only(layer_type, "project_outer_factors")
+    if not is_linear(layer_type):  # the projected pair, then the dW kernel ("nn.Linear" layout, per group)
+        a_p, g_p = _outer_sides(a, g, layer_type, projector, module_kwargs, include_bias, proj_dim, proj_seed,
+                                proj_kwargs)
+        return materialize_factors(a_p, g_p, "nn.Linear")
     bias = bool(module_kwargs is not None and module_kwargs["has_bias"] and include_bias)
     a, g = dtypes.align(to_3d(a), to_3d(g))
     p_in, p_out = _resolve_pair(projector, a, g, bias, proj_dim, proj_seed, proj_kwargs)
@@ -388,7 +448,20 @@ def mask_factors(a, g, layer_type: str, projector, module_kwargs: dict | None = 
         dense = materialize_factors(a, g, layer_type, module_kwargs, include_bias).to(device)
         idx = proj.mask_indices(dense.shape[-1], proj_dim=proj_dim, proj_seed=proj_seed, device=device)
         return dense.index_select(-1, idx)
-    if is_embedding(layer_type) or not is_linear(layer_type):
+    if is_embedding(layer_type):  # entry (v, e): the gradient column e summed over the tokens with id v
+        vocab = _embedding_vocab(module_kwargs, "Subsetting")
+        ids, rows_g = emb.side(a, g, layer_type, module_kwargs)
+        emb.check_ids(a, vocab=vocab)
+        (rows_g,) = dtypes.align(rows_g)
+        out_dtype = rows_g.dtype
+        e = rows_g.shape[-1]
+        idx = proj.mask_indices(vocab * e, proj_dim=proj_dim, proj_seed=proj_seed, device=device)
+        got = kernels.gather_embedding_entries(ids.to(device), rows_g.to(device=device,
+                                               dtype=dtypes.kernel_dtype(out_dtype)), idx // e, idx % e)
+        return got.to(out_dtype)
+    if is_conv(layer_type) or is_conv_transpose(layer_type) or (module_kwargs is None and to_3d(a).ndim == 4):
+        return _mask_conv(a, g, layer_type, proj, module_kwargs, include_bias, proj_dim, proj_seed, device)
+    if not is_linear(layer_type):
         require_supported(layer_type, "mask_factors")
     x, y, bias = final_linear(a, g, layer_type, module_kwargs, include_bias)
     out_dtype = dtypes.resolve(x, y)
@@ -398,6 +471,30 @@ def mask_factors(a, g, layer_type: str, projector, module_kwargs: dict | None = 
     cols = x.shape[-1] + int(bias)
     idx = proj.mask_indices(y.shape[-1] * cols, proj_dim=proj_dim, proj_seed=proj_seed, device=device)
     return kernels.gather_entries(x, y, idx // cols, idx % cols, bias=bias).to(out_dtype)
+
+
+def _mask_conv(a, g, layer_type, proj, module_kwargs, include_bias, proj_dim, proj_seed, device):
+    """Kept entries of a convolution's gradient in materialize's layout
+    (projection.py:737-775): ``o * K + i`` (conv), ``c * P + p`` (transposed),
+    per group for grouped factors -- whose groups fold into the feature axes,
+    so an entry's row and column come from the same group."""
+    c = conv.final(a, g, layer_type, module_kwargs, include_bias)
+    x, y = c.a, c.g
+    if c.bias:  # an explicit ones column keeps the per-group index arithmetic plain
+        x = torch.cat([x, torch.ones_like(x[..., :1])], dim=-1)
+    out_dtype = dtypes.resolve(x, y)
+    x, y = (t.to(device=device, dtype=dtypes.kernel_dtype(out_dtype)) for t in dtypes.align(x, y))
+    groups = c.groups if x.dim() == 4 else 1
+    wa, wg = x.shape[-1], y.shape[-1]
+    if x.dim() == 4:
+        x, y = x.reshape(*x.shape[:2], groups * wa), y.reshape(*y.shape[:2], groups * wg)
+    idx = proj.mask_indices(groups * wa * wg, proj_dim=proj_dim, proj_seed=proj_seed, device=device)
+    grp, rem = idx // (wa * wg), idx % (wa * wg)
+    if c.transpose:  # blocks (Wa, Wg): rows from a, columns from g
+        got = kernels.gather_entries(y, x, grp * wa + rem // wg, grp * wg + rem % wg)
+    else:  # blocks (Wg, Wa): rows from g, columns from a
+        got = kernels.gather_entries(x, y, grp * wg + rem // wa, grp * wa + rem % wa)
+    return got.to(out_dtype)
 
 
 def mask_factorized(f, layer_type: str, projector, *, proj_dim: int, include_bias: bool = True,

@@ -408,6 +408,32 @@ def dense_per_token_embedding(
     return out
 
 
+def gather_embedding_entries(tok: torch.Tensor, g: torch.Tensor, rows: torch.Tensor,
+                             cols: torch.Tensor) -> torch.Tensor:
+    """fp32 ``(B, k)``: entry q of sample b is the sum of ``g[b, t, cols[q]]``
+    over the tokens whose id is ``rows[q]`` (ascending t) -- the kept
+    coordinates of the per-sample embedding gradient."""
+    dev = nat.require_device(tok, g, rows, cols)
+    if tok.dim() != 2 or g.dim() != 3 or tok.shape != g.shape[:2]:
+        raise ValueError("gather_embedding_entries expects (B, T) ids and (B, T, E) gradients")
+    if rows.shape != cols.shape or rows.dim() != 1:
+        raise ValueError("rows and cols must be matching 1-D index tensors")
+    b, t, e = g.shape
+    k = rows.numel()
+    out = torch.empty(b, k, dtype=torch.float32, device=dev)
+    if b == 0 or k == 0:
+        return out
+    tok = _token_ids(tok)
+    if g.stride(-1) != 1:
+        g = g.contiguous()
+    rows, cols = rows.to(torch.int64).contiguous(), cols.to(torch.int64).contiguous()
+    _run(dev, "gather_embedding_entries", nat.load().da_gather_embedding_entries,
+         tok.data_ptr(), g.data_ptr(), nat.dtype_code(g.dtype), b, t, e, tok.stride(0), tok.stride(1),
+         g.stride(0), g.stride(1), rows.data_ptr(), cols.data_ptr(), k, out.data_ptr(), out.stride(0),
+         nat.stream_ptr(dev))
+    return out
+
+
 def dense_per_token(
     a1: torch.Tensor,
     g1: torch.Tensor,

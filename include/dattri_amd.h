@@ -291,6 +291,23 @@ int da_materialize_embedding(const int64_t* tok, const void* g, int dtype, int64
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Kept entries of the per-sample embedding gradient, without forming it:
+ *
+ *   out[b*ld_out + q] = sum over t with tok[b,t] == rows[q] of g[b,t,cols[q]],  q < k,
+ *
+ * fp32, tokens in ascending order.  tok int64 (B, T) and g (B, T, E) with
+ * element strides as for da_materialize_embedding (no alignment needed);
+ * rows / cols int64 (k,).  A negative id or a column outside [0, E) adds
+ * nothing.  Replaces the embedding branch of mask_factors,
+ * dattri_llm/gradient/ops/projection.py:718-735 (a one-hot indicator times
+ * the gathered gradient columns, summed over tokens).
+ */
+int da_gather_embedding_entries(const int64_t* tok, const void* g, int dtype, int64_t batch, int64_t tokens,
+                                int64_t E, int64_t tok_bstride, int64_t tok_tstride, int64_t g_bstride,
+                                int64_t g_tstride, const int64_t* rows, const int64_t* cols, int64_t k, float* out,
+                                int64_t ld_out, void* stream);
+
+/*
  * Row Gram: out (+)= x^T x, fp32 (width, width) with row stride ld_out, of the
  * bf16/fp16 rows x (rows, width) with row stride x_stride (elements; width and
  * x_stride multiples of 8, rows 16-byte aligned).  accumulate = 0 overwrites,

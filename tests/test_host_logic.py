@@ -94,7 +94,7 @@ def test_unsupported_layers_raise(ops):
     with pytest.raises(NotImplementedError):
         ops.preprocess_factors(a, a, "nn.GroupNorm", {"has_bias": False, "num_groups": 1, "eps": 1e-5})
     with pytest.raises(NotImplementedError):
-        ops.project_factors(a, a, "nn.Conv2d", None, None, proj_dim=4)
+        ops.project_factors(a, a, "nn.PixelShuffle", None, None, proj_dim=4)
     with pytest.raises(ValueError, match="factorized projection is undefined"):
         ops.project_factors(a, a, "nn.LayerNorm", None, None, proj_dim=4)
 
