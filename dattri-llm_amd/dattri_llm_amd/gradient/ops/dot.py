@@ -41,7 +41,6 @@ from dattri_llm_amd.gradient.ops.materialize import (
 from dattri_llm_amd.gradient.ops.preprocess import final_linear, to_3d
 from dattri_llm_amd.gradient.ops.types import (
     PARAM_GRAD_TYPES,
-    TOKEN_NORM_TYPES,
     is_conv,
     is_conv_transpose,
     is_embedding,
@@ -282,10 +281,9 @@ def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Ten
         # K[i,j] = sum over equal ids of g1_it . g2_js (dot.py:58-74)
         emb.check_ids(a1, a2)
         return emb.gram32(emb.side(a1, g1, layer_type, None), emb.side(a2, g2, layer_type, None)).to(out_dtype)
-    if is_norm(layer_type):
-        if layer_type not in TOKEN_NORM_TYPES:
-            require_supported(layer_type, "cross_gram")
-        return _dense_gram(norm_grad_from_final(a1, g1), norm_grad_from_final(a2, g2)).to(out_dtype)
+    if is_norm(layer_type):  # final factors: the token sum of a * g, whatever the norm
+        return _dense_gram(norm_grad_from_final(a1, g1, fp32=True), norm_grad_from_final(a2, g2, fp32=True)).to(
+            out_dtype)
     if _is_conv_family(layer_type, a1):
         c1, c2 = conv.final(a1, g1, layer_type, None, False), conv.final(a2, g2, layer_type, None, False)
         return _conv_gram32(c1, c2, mode).to(out_dtype)
@@ -295,16 +293,17 @@ def cross_gram(a1, g1, a2, g2, layer_type: str, mode: str = "auto") -> torch.Ten
 
 
 def _side(a, g, layer_type, module_kwargs, include_bias):
-    """('norm', (B, d) dense) | ('linear', (a, g, bias)) | ('embedding', (ids, g))
-    for one raw side."""
+    """('norm', (B, d) fp32 dense) | ('linear', (a, g, bias)) | ('embedding', (ids, g))
+    | ('conv', ConvFactors) for one raw side.  A norm layer's per-sample
+    gradient stays in fp32 on its way into the inner product."""
     if is_embedding(layer_type):
         return "embedding", emb.side(a, g, layer_type, module_kwargs)
     if is_conv(layer_type) or is_conv_transpose(layer_type) or (module_kwargs is None and a.ndim == 4):
         return "conv", conv.final(a, g, layer_type, module_kwargs, include_bias)
-    if layer_type in TOKEN_NORM_TYPES:
+    if is_norm(layer_type):
         if module_kwargs is not None:
-            return "norm", norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias)
-        return "norm", norm_grad_from_final(a, g)
+            return "norm", norm_grad_from_raw(a, g, layer_type, module_kwargs, include_bias, fp32=True)
+        return "norm", norm_grad_from_final(a, g, fp32=True)
     if not is_linear(layer_type):
         require_supported(layer_type, "cross_dot")
     return "linear", final_linear(a, g, layer_type, module_kwargs, include_bias)
@@ -593,11 +592,9 @@ def cross_gram_per_token(a1, g1, a2, g2, layer_type: str) -> torch.Tensor:
     if is_embedding(layer_type):
         emb.check_ids(a1, a2)
         return emb.per_token32(emb.side(a1, g1, layer_type, None), emb.side(a2, g2, layer_type, None)).to(out_dtype)
-    if is_norm(layer_type):
-        if layer_type not in TOKEN_NORM_TYPES:
-            require_supported(layer_type, "cross_gram_per_token")
+    if is_norm(layer_type):  # final factors: the token sum of a * g, whatever the norm
         x1, y1, x2, y2 = dtypes.align(to_3d(a1), to_3d(g1), to_3d(a2), to_3d(g2))
-        return _norm_per_token32(x1 * y1, norm_grad_from_final(x2, y2)).to(out_dtype)
+        return _norm_per_token32(x1 * y1, norm_grad_from_final(x2, y2, fp32=True)).to(out_dtype)
     if _is_conv_family(layer_type, a1):
         c1, c2 = conv.final(a1, g1, layer_type, None, False), conv.final(a2, g2, layer_type, None, False)
         return _conv_per_token32(c1, c2).to(out_dtype)
@@ -615,9 +612,7 @@ def cross_gram_per_token_dense(a1, g1, m2, layer_type: str) -> torch.Tensor:
         emb.check_ids(a1)
         return emb.dense_per_token32(emb.side(a1, g1, layer_type, None), m2).to(out_dtype)
     m2 = m2.reshape(m2.shape[0], -1)
-    if is_norm(layer_type):
-        if layer_type not in TOKEN_NORM_TYPES:
-            require_supported(layer_type, "cross_gram_per_token_dense")
+    if is_norm(layer_type):  # final factors: the token sum of a * g, whatever the norm
         x1, y1 = dtypes.align(to_3d(a1), to_3d(g1))
         return _norm_per_token32(x1 * y1, m2).to(out_dtype)
     if _is_conv_family(layer_type, a1):
@@ -636,7 +631,7 @@ def cross_dot_per_token(f1, f2, layer_type: str, include_bias: bool = True) -> t
     a1, g1, mk1 = b1.activation, b1.pre_activation_grad, b1.module_kwargs
     dense2 = isinstance(f2, torch.Tensor)
     out_dtype = dtypes.resolve(a1, g1, f2) if dense2 else dtypes.resolve(a1, g1, f2.activation, f2.pre_activation_grad)
-    if layer_type in TOKEN_NORM_TYPES:
+    if is_norm(layer_type):
         rows1 = norm_token_rows(a1, g1, layer_type, mk1, include_bias)
         m2 = f2.reshape(f2.shape[0], -1) if dense2 else materialize(f2, layer_type, include_bias)
         return _norm_per_token32(rows1, m2).to(out_dtype)

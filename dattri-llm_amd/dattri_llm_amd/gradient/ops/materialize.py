@@ -18,6 +18,8 @@ from dattri_llm_amd import kernels
 from dattri_llm_amd.gradient.ops import conv, dtypes
 from dattri_llm_amd.gradient.ops import embedding as emb
 from dattri_llm_amd.gradient.ops.preprocess import (
+    channel_norm_factors,
+    channel_norm_spec,
     final_linear,
     fold_norm_rows,
     norm_spec,
@@ -42,23 +44,35 @@ def _operands(*tensors):
     return tuple(t.to(kd) for t in aligned), out_dtype
 
 
-def norm_grad_from_raw(x, g, layer_type: str, module_kwargs: dict, include_bias: bool = True):
-    """Fused preprocess + token sum of a raw token-norm capture -> (B, d[*2])."""
+def norm_grad_from_raw(x, g, layer_type: str, module_kwargs: dict, include_bias: bool = True, fp32: bool = False):
+    """Fused preprocess + token sum of a raw norm capture -> (B, d[*2]):
+    token norms normalise each row in registers (``da_norm_weight_grad``);
+    channel norms take their (sample, group) statistics first
+    (``da_channel_norm_weight_grad``).  ``fp32`` keeps the sums in fp32 (for
+    an inner product that follows) instead of the compute dtype."""
+    if layer_type not in TOKEN_NORM_TYPES:
+        groups, eps = channel_norm_spec(layer_type, module_kwargs)
+        bias = bool(module_kwargs["has_bias"] and include_bias)
+        (xo, go), out_dtype = _operands(x, g)
+        out = kernels.channel_norm_weight_grad(xo, go, groups=groups, eps=eps, bias=bias,
+                                               out_dtype=torch.float32 if fp32 else dtypes.kernel_dtype(out_dtype))
+        return out if fp32 else out.to(out_dtype)
     spec = norm_spec(x, layer_type, module_kwargs, include_bias)
     x3 = fold_norm_rows(x, spec.width)
     g3 = fold_norm_rows(g, spec.width)
     (xo, go), out_dtype = _operands(x3, g3)
     out = kernels.norm_weight_grad(xo, go, kind=spec.kind, eps=spec.eps, bias=spec.has_bias,
-                                   out_dtype=dtypes.kernel_dtype(out_dtype))
-    return out.to(out_dtype)
+                                   out_dtype=torch.float32 if fp32 else dtypes.kernel_dtype(out_dtype))
+    return out if fp32 else out.to(out_dtype)
 
 
-def norm_grad_from_final(a, g):
-    """Token sum ``(a * g).sum(1)`` of already-preprocessed norm factors."""
+def norm_grad_from_final(a, g, fp32: bool = False):
+    """Token sum ``(a * g).sum(1)`` of already-preprocessed norm factors
+    (kept in fp32 with ``fp32``)."""
     (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
     out = kernels.norm_weight_grad(ao, go, kind=2, eps=0.0, bias=False,
-                                   out_dtype=dtypes.kernel_dtype(out_dtype))
-    return out.to(out_dtype)
+                                   out_dtype=torch.float32 if fp32 else dtypes.kernel_dtype(out_dtype))
+    return out if fp32 else out.to(out_dtype)
 
 
 def linear_dense(a, g, bias: bool) -> torch.Tensor:
@@ -88,8 +102,11 @@ def conv_dense(c) -> torch.Tensor:
 def norm_token_rows(a, g, layer_type: str, module_kwargs: dict | None = None,
                     include_bias: bool = True) -> torch.Tensor:
     """(B, T, d') per-token norm gradients x_hat * g (with a bias, [x_hat * g, g]):
-    the terms whose token sum is the norm weight gradient (materialize.py:96-98)."""
-    if module_kwargs is not None:
+    the terms whose token sum is the norm weight gradient (materialize.py:96-98).
+    A channel norm's rows are its spatial positions, (B, S, C)."""
+    if module_kwargs is not None and layer_type not in TOKEN_NORM_TYPES:
+        x3, g3 = channel_norm_factors(a, g, layer_type, module_kwargs, include_bias)
+    elif module_kwargs is not None:
         spec = norm_spec(a, layer_type, module_kwargs, include_bias)
         x_hat = kernels.norm_xhat(a, kind=spec.kind, eps=spec.eps)
         x3, g3 = fold_norm_rows(x_hat, spec.width), fold_norm_rows(g, spec.width)
@@ -120,7 +137,7 @@ def materialize_factors(
         vocab = int(module_kwargs["num_embeddings"])
         emb.check_ids(a, vocab=vocab)
         return emb.materialize(emb.side(a, g, layer_type, module_kwargs), vocab)
-    if layer_type in TOKEN_NORM_TYPES:
+    if is_norm(layer_type):
         if per_token:
             return norm_token_rows(a, g, layer_type, module_kwargs, include_bias).flatten(1)
         if module_kwargs is not None:
@@ -130,7 +147,7 @@ def materialize_factors(
         c = conv.final(a, g, layer_type, module_kwargs, include_bias)
         (x, y), out_dtype = _operands(c.a, c.g)
         return conv_dense(conv.ConvFactors(x, y, c.bias, c.transpose)).to(out_dtype)
-    if is_norm(layer_type) or not is_linear(layer_type):
+    if not is_linear(layer_type):
         require_supported(layer_type, "materialize_factors")
     a, g, bias = final_linear(a, g, layer_type, module_kwargs, include_bias)
     return linear_dense(a, g, bias)

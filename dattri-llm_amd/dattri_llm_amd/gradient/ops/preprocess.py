@@ -5,8 +5,9 @@ scoring path: linear layers (bias folded as a ones column, :436-437) and token
 norms (RMSNorm / LayerNorm x_hat, :366-384, computed by the ``da_norm_xhat``
 kernel, with the bias augmentation of ``norm.py:95-110``) and embeddings
 (``nn.Embedding`` padding positions, ``nn.EmbeddingBag`` bags spread over their
-tokens, :403-416 and :126-169) and convolutions (the unfolding of
-``conv.py``).  Channel-norm layers raise ``NotImplementedError``.
+tokens, :403-416 and :126-169), convolutions (the unfolding of
+``conv.py``) and channel norms (GroupNorm / InstanceNorm x_hat laid out
+(B, S, C), :386-401, by the ``da_channel_norm_xhat`` kernel).
 
 The public ``preprocess_factors`` returns exactly the reference's tensors.  The
 scoring kernels never need them: :func:`final_linear` and :func:`norm_spec`
@@ -100,6 +101,28 @@ def fold_norm_rows(x: torch.Tensor, width: int) -> torch.Tensor:
     return x.reshape(x.shape[0], -1, width)
 
 
+def channel_norm_spec(layer_type: str, module_kwargs: dict) -> tuple[int, float]:
+    """(groups, eps) of a GroupNorm / InstanceNorm (preprocess.py:386-401):
+    InstanceNorm normalises each channel alone."""
+    if layer_type == "nn.GroupNorm":
+        return int(module_kwargs["num_groups"]), float(module_kwargs["eps"])
+    return int(module_kwargs["num_features"]), float(module_kwargs["eps"])
+
+
+def channel_norm_factors(a, g, layer_type: str, module_kwargs: dict, include_bias: bool = True):
+    """A channel norm's preprocessed factors (norm.py:120-141): x_hat and g as
+    (B, S, C), with a bias ``[x_hat, 1]`` and ``[g, g]``.  x_hat comes from
+    ``da_channel_norm_xhat`` in a's dtype; the rest is layout."""
+    groups, eps = channel_norm_spec(layer_type, module_kwargs)
+    x_hat = kernels.channel_norm_xhat(a, groups=groups, eps=eps, out_dtype=a.dtype)
+    n, c = a.shape[:2]
+    x_sc = x_hat.reshape(n, c, -1).transpose(1, 2).contiguous()
+    g_sc = g.reshape(n, c, -1).transpose(1, 2).contiguous()
+    if module_kwargs["has_bias"] and include_bias:
+        return torch.cat([x_sc, torch.ones_like(x_sc)], dim=-1), torch.cat([g_sc, g_sc], dim=-1)
+    return x_sc, g_sc
+
+
 def final_linear(a, g, layer_type: str, module_kwargs: dict | None, include_bias: bool):
     """A linear layer's final factors without forming the ones column:
     ``(a, g, bias)`` where ``bias`` says an implicit ones column follows ``a``."""
@@ -116,7 +139,7 @@ def preprocess_factors(
     include_bias: bool = True,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Transform raw captures into the reference's ``(a, g)`` form
-    (preprocess.py:301-439) for linear and token-norm layers."""
+    (preprocess.py:301-439)."""
     if module_kwargs is None:
         return a, g
     has_bias = module_kwargs["has_bias"] and include_bias
@@ -139,6 +162,8 @@ def preprocess_factors(
         if module_kwargs.get("padding_idx") is not None:
             rows = rows.masked_fill((a == module_kwargs["padding_idx"]).unsqueeze(-1), 0)
         return a, rows.contiguous()
+    if is_norm(layer_type):  # GroupNorm / InstanceNorm (preprocess.py:386-401)
+        return channel_norm_factors(a, g, layer_type, module_kwargs, include_bias)
     if layer_type in CONV_TYPES or layer_type in CONV_TRANSPOSE_TYPES:
         return conv.preprocess(a, g, layer_type, module_kwargs, include_bias)
     if is_norm(layer_type) or not is_linear(layer_type):
@@ -201,6 +226,8 @@ def flat_width(shape) -> int:
 __all__ = [
     "NormSpec",
     "extract_module_kwargs",
+    "channel_norm_factors",
+    "channel_norm_spec",
     "final_embedding",
     "final_linear",
     "fold_norm_rows",

@@ -897,6 +897,57 @@ def norm_xhat(x: torch.Tensor, *, kind: int, eps: float, out_dtype: torch.dtype 
     return out
 
 
+def _channel_rows(x: torch.Tensor):
+    n, c = x.shape[:2]
+    s = x.numel() // max(n * c, 1) if n * c else 0
+    return x.contiguous(), n, c, s
+
+
+def channel_norm_weight_grad(x: torch.Tensor, g: torch.Tensor, *, groups: int, eps: float, bias: bool = False,
+                             out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Per-sample weight gradient of a channel norm, ``(N, C)`` or with
+    ``bias`` ``(N, 2C)`` = ``[dgamma | dbeta]``: the x_hat of each (sample,
+    group) block times g, summed over the spatial positions (fp32)."""
+    dev = nat.require_device(x, g)
+    if x.shape != g.shape or x.dim() < 2:
+        raise ValueError("channel_norm_weight_grad expects x and g of one (N, C, *spatial) shape")
+    if x.dtype != g.dtype:
+        raise ValueError("channel_norm_weight_grad operands must share one dtype")
+    out_dtype = out_dtype or x.dtype
+    x, n, c, s = _channel_rows(x)
+    g = g.contiguous()
+    width = c * (2 if bias else 1)
+    if s == 0 or n == 0:
+        return torch.zeros(n, width, dtype=out_dtype, device=dev)
+    out = torch.empty(n, width, dtype=out_dtype, device=dev)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_channel_norm_workspace(n, groups, ctypes.byref(nbytes)), "channel_norm_weight_grad")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "channel_norm_weight_grad", lib.da_channel_norm_weight_grad,
+         x.data_ptr(), g.data_ptr(), nat.dtype_code(x.dtype), n, c, s, groups, float(eps), int(bias),
+         out.data_ptr(), nat.dtype_code(out_dtype), width, ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    return out
+
+
+def channel_norm_xhat(x: torch.Tensor, *, groups: int, eps: float, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """A channel norm's normalised input, in x's (N, C, *spatial) layout."""
+    dev = nat.require_device(x)
+    out_dtype = out_dtype or x.dtype
+    x, n, c, s = _channel_rows(x)
+    out = torch.empty(x.shape, dtype=out_dtype, device=dev)
+    if n * c * s == 0:
+        return out
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_channel_norm_workspace(n, groups, ctypes.byref(nbytes)), "channel_norm_xhat")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "channel_norm_xhat", lib.da_channel_norm_xhat,
+         x.data_ptr(), nat.dtype_code(x.dtype), n, c, s, groups, float(eps), out.data_ptr(),
+         nat.dtype_code(out_dtype), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    return out
+
+
 def selftest_mfma(dtype: torch.dtype, a: torch.Tensor, b: torch.Tensor, shape: int = 32) -> torch.Tensor:
     """Raw accumulator dump of one MFMA block (see da_selftest_mfma)."""
     dev = nat.require_device(a, b)

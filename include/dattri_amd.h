@@ -452,6 +452,29 @@ int da_norm_xhat(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rs
                  float eps, void* out, int out_dtype, int64_t out_rstride, void* stream);
 
 /*
+ * Channel norms (GroupNorm; InstanceNorm is one group per channel).  x and g
+ * are contiguous (N, C, S) (S = the flattened spatial axes), G groups of C/G
+ * consecutive channels; x_hat = (x - mean) / sqrt(var + eps) over each
+ * (sample, group) block of C/G x S values (biased variance), as
+ * dattri_llm/gradient/ops/norm.py:44-62 computes it.
+ *
+ * da_channel_norm_weight_grad: out[n*out_ld + c] = sum_s x_hat[n,c,s] g[n,c,s]
+ * and, with has_bias, out[n*out_ld + C + c] = sum_s g[n,c,s] (fp32 sums, out in
+ * out_dtype) -- the token sum of the (N, S, C) factors of
+ * _augment_channel_norm, norm.py:120-141, that materialize_factors forms
+ * (materialize.py:96-98).  S > 0.
+ * da_channel_norm_xhat: x_hat in x's layout, in out_dtype (the normalisation
+ * preprocess_factors applies, preprocess.py:386-401).
+ * Both need a workspace of da_channel_norm_workspace bytes (the statistics).
+ */
+int da_channel_norm_workspace(int64_t N, int64_t G, size_t* bytes);
+int da_channel_norm_weight_grad(const void* x, const void* g, int dtype, int64_t N, int64_t C, int64_t S, int64_t G,
+                                float eps, int has_bias, void* out, int out_dtype, int64_t out_ld, void* workspace,
+                                size_t workspace_bytes, void* stream);
+int da_channel_norm_xhat(const void* x, int dtype, int64_t N, int64_t C, int64_t S, int64_t G, float eps, void* out,
+                         int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Random projection of factor rows (ProjectionMatrix.__call__,
  * dattri_llm/gradient/ops/projection.py:363-370):
  *

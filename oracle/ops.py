@@ -57,6 +57,11 @@ conv_materialize               gradient/ops/materialize.py:100-114            nn
                                                                               (stride, padding, dilation, groups, bias)
 grouped_cross_gram             gradient/ops/dot.py:100-109                    equals conv_materialize M1 @ M2^T
 grouped_cross_gram_per_token   gradient/ops/dot.py:216-218                    sums over t to grouped_cross_gram; brute force
+group_norm_x_hat               gradient/ops/norm.py:44-62                     torch.nn.functional.group_norm (no affine),
+                                                                              InstanceNorm as one group per channel
+channel_norm_preprocess        gradient/ops/norm.py:120-141,                  token sum of a * g equals autograd
+                               preprocess.py:386-401                          [weight.grad, bias.grad] of nn.GroupNorm /
+                                                                              nn.InstanceNorm2d(affine=True) per sample
 embedding_materialize          gradient/ops/materialize.py:22-48              torch autograd weight.grad of nn.Embedding
                                                                               (f64); torch's CPU scatter_add_ in bf16 /
                                                                               fp16 / fp32, bit for bit (per-add rounding)
@@ -84,6 +89,8 @@ __all__ = [
     "conv_materialize",
     "conv_preprocess",
     "conv_unfold",
+    "channel_norm_preprocess",
+    "group_norm_x_hat",
     "grouped_cross_gram",
     "grouped_cross_gram_per_token",
     "ekfac_materialize_factors",
@@ -839,4 +846,34 @@ def grouped_cross_gram_per_token(a1, g1, a2, g2) -> np.ndarray:
     gradients, then each side-1 token's per-group rank-1 term against them."""
     m2 = np.einsum("csgk,csgd->cgkd", a2, g2)
     return np.einsum("btgk,btgd,cgkd->btc", a1, g1, m2)
+
+
+# ---------------------------------------------------------------------------
+# channel norms
+# ---------------------------------------------------------------------------
+
+
+def group_norm_x_hat(x, groups: int, eps: float) -> np.ndarray:
+    """GroupNorm x_hat (norm.py:44-62): x (N, C, *spatial) split into `groups`
+    blocks of consecutive channels, each normalised over its channels and
+    positions with the biased variance; groups == C is InstanceNorm."""
+    x = np.asarray(x)
+    n, c = x.shape[:2]
+    blk = x.reshape(n, groups, -1)
+    mean = blk.mean(axis=2, keepdims=True)
+    var = ((blk - mean) ** 2).mean(axis=2, keepdims=True)
+    return ((blk - mean) / np.sqrt(var + eps)).reshape(x.shape)
+
+
+def channel_norm_preprocess(x, g, groups: int, eps: float, has_bias: bool = False):
+    """A channel norm's factors (norm.py:120-141, preprocess.py:386-401): x_hat
+    and g laid out (N, S, C) with the positions as tokens; with a bias,
+    [x_hat, 1] and [g, g] so that a * g summed over S is [dgamma, dbeta]."""
+    x_hat = group_norm_x_hat(x, groups, eps)
+    n, c = x_hat.shape[:2]
+    a = x_hat.reshape(n, c, -1).transpose(0, 2, 1)
+    gg = np.asarray(g).reshape(n, c, -1).transpose(0, 2, 1)
+    if has_bias:
+        return np.concatenate([a, np.ones_like(a)], axis=-1), np.concatenate([gg, gg], axis=-1)
+    return a, gg
 

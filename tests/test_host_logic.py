@@ -92,7 +92,7 @@ def test_unsupported_layers_raise(ops):
     with pytest.raises(NotImplementedError):
         ops.kfac_cross_factors(a, a, a, a, "nn.Embedding", torch.eye(8), torch.eye(8))
     with pytest.raises(NotImplementedError):
-        ops.preprocess_factors(a, a, "nn.GroupNorm", {"has_bias": False, "num_groups": 1, "eps": 1e-5})
+        ops.preprocess_factors(a, a, "nn.PixelShuffle", {"has_bias": False})
     with pytest.raises(NotImplementedError):
         ops.project_factors(a, a, "nn.PixelShuffle", None, None, proj_dim=4)
     with pytest.raises(ValueError, match="factorized projection is undefined"):

@@ -734,3 +734,31 @@ def test_grouped_cross_gram_and_per_token():
                 brute[i, t, j] = sum(float(a1[i, t, e] @ a2[j, s, e]) * float(g1[i, t, e] @ g2[j, s, e])
                                      for e in range(2) for s in range(4))
     np.testing.assert_allclose(pt, brute, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# channel norms
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("kind", ["group", "instance"])
+def test_channel_norm_oracle_against_torch(kind):
+    r = _rng(90)
+    n, c, h, w = 3, 6, 4, 5
+    groups = 3 if kind == "group" else c
+    x, gout = r.standard_normal((n, c, h, w)) * 2 + 1, r.standard_normal((n, c, h, w))
+    eps = 1e-5
+    want = torch.nn.functional.group_norm(torch.from_numpy(x), groups, eps=eps).numpy()
+    np.testing.assert_allclose(oracle.group_norm_x_hat(x, groups, eps), want, rtol=1e-10, atol=1e-10)
+    if kind == "group":
+        layer = torch.nn.GroupNorm(groups, c, eps=eps).double()
+    else:
+        layer = torch.nn.InstanceNorm2d(c, eps=eps, affine=True).double()
+    rows = []
+    for i in range(n):
+        layer.zero_grad()
+        (layer(torch.from_numpy(x[i:i + 1])) * torch.from_numpy(gout[i:i + 1])).sum().backward()
+        rows.append(np.concatenate([layer.weight.grad.numpy(), layer.bias.grad.numpy()]))
+    a, g = oracle.channel_norm_preprocess(x, gout, groups, eps, has_bias=True)
+    assert a.shape == (n, h * w, 2 * c)
+    np.testing.assert_allclose((a * g).sum(axis=1), np.stack(rows), rtol=1e-10, atol=1e-10)
