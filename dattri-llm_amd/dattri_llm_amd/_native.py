@@ -124,6 +124,8 @@ SIGNATURES.update(
             [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, ctypes.c_float, _I32,
              _P, _I32, _I64, _P, _SZ, _P],
         ),
+        "da_match_rows_workspace": (_I32, [_I64, _I64, ctypes.POINTER(_SZ)]),
+        "da_match_rows": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I32, _P, _P, _P, _SZ, _P]),
         "da_channel_norm_workspace": (_I32, [_I64, _I64, ctypes.POINTER(_SZ)]),
         "da_channel_norm_weight_grad": (
             _I32, [_P, _P, _I32, _I64, _I64, _I64, _I64, ctypes.c_float, _I32, _P, _I32, _I64, _P, _SZ, _P]),

@@ -948,6 +948,35 @@ def channel_norm_xhat(x: torch.Tensor, *, groups: int, eps: float, out_dtype: to
     return out
 
 
+def match_rows(src: torch.Tensor, x: torch.Tensor) -> torch.Tensor | None:
+    """int64 ``(n_x,)``: the row of ``src (n_src, d)`` each row of ``x (n_x, d)``
+    was gathered from -- the k-th occurrence of a value in x takes the k-th
+    (ascending) src row holding it, verified by float equality -- or None when
+    some row cannot be placed (one host read of the status word)."""
+    dev = nat.require_device(src, x)
+    if src.dim() != 2 or x.dim() != 2 or src.shape[1] != x.shape[1]:
+        raise ValueError("match_rows expects (n_src, d) and (n_x, d) rows of one width")
+    if src.dtype != x.dtype:
+        raise ValueError("match_rows operands must share one dtype")
+    n_src, n_x = src.shape[0], x.shape[0]
+    token = torch.empty(n_x, dtype=torch.int64, device=dev)
+    if n_x == 0:
+        return token
+    if n_src == 0:
+        return None
+    d = -(-src.shape[1] // _chunk_elems(src.dtype)) * _chunk_elems(src.dtype)
+    src, x = prepare_rows(src, d), prepare_rows(x, d)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check(lib.da_match_rows_workspace(n_src, n_x, ctypes.byref(nbytes)), "match_rows")
+    ws = nat.workspace(nbytes.value, dev)
+    _run(dev, "match_rows", lib.da_match_rows,
+         src.data_ptr(), n_src, src.stride(0), x.data_ptr(), n_x, x.stride(0), d, nat.dtype_code(src.dtype),
+         token.data_ptr(), status.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
+    return None if int(status.item()) else token
+
+
 def selftest_mfma(dtype: torch.dtype, a: torch.Tensor, b: torch.Tensor, shape: int = 32) -> torch.Tensor:
     """Raw accumulator dump of one MFMA block (see da_selftest_mfma)."""
     dev = nat.require_device(a, b)

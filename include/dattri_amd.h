@@ -595,6 +595,25 @@ int da_compact_rows(const uint8_t* mask, int64_t batch, int64_t tokens, int32_t*
                     void* stream);
 
 /*
+ * Exact location of routed token rows: x (n_x, width) holds rows gathered
+ * from the block input src (n_src, width) (row strides in elements, rows
+ * 16-byte aligned, width * element size a multiple of 16).  The k-th
+ * occurrence of a row value among x's rows is matched to the k-th token, in
+ * ascending order, of src holding the same value, and verified element by
+ * element (float equality: -0 == +0, NaN equals nothing):
+ * token[r] (int64) = the matched src row of x row r, or -1.  *status (device
+ * int32) is set to 0, then to 1 when any row fails (a value absent from src,
+ * more copies than src holds, or a fingerprint collision).  Workspace from
+ * da_match_rows_workspace.  Replaces RoutedTokenTracker._match,
+ * dattri_llm/gradient/hooks/routing.py:300-333 (fingerprints, a stable sort,
+ * searchsorted, torch.equal).
+ */
+int da_match_rows_workspace(int64_t n_src, int64_t n_x, size_t* bytes);
+int da_match_rows(const void* src, int64_t n_src, int64_t src_rstride, const void* x, int64_t n_x, int64_t x_rstride,
+                  int64_t width, int dtype, int64_t* token, int32_t* status, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/*
  * Lane-layout self test of the MFMA conventions every kernel relies on.
  * shape 32: a and b are (32 x k) row-major with k = 16 (bf16/f16) or 8 (f32),
  *           one 16-byte chunk per lane half; out receives 64 lanes x 16

@@ -38,6 +38,9 @@ moe_segment_ghost              dense-with-zeros cross_gram (routing.py:17-23) eq
                                                                               zero-filled (B, T, d) factors
 moe_segment_ghost_compact      the same without the zero rows                 equals moe_segment_ghost (empty experts,
                                                                               bias, one sample); brute force
+match_rows                     gradient/hooks/routing.py:300-333              a gather by torch.where(mask) is recovered;
+                                                                              repeated rows in ascending order; absent
+                                                                              rows, surplus copies and NaN rows fail
 kfac_factors                   gradient/ops/kronecker.py:65-118               brute-force sums of row outer products over
                                                                               the rows with a non-zero gradient
 fim_factors                    gradient/ops/kronecker.py:121-141              brute-force sum of per-sample outer products
@@ -108,6 +111,7 @@ __all__ = [
     "sym_inverse",
     "layer_norm_x_hat",
     "materialize_linear",
+    "match_rows",
     "maybe_materialize_projected",
     "maybe_use_materialized_gram",
     "maybe_use_materialized_norm",
@@ -876,4 +880,34 @@ def channel_norm_preprocess(x, g, groups: int, eps: float, has_bias: bool = Fals
     if has_bias:
         return np.concatenate([a, np.ones_like(a)], axis=-1), np.concatenate([gg, gg], axis=-1)
     return a, gg
+
+
+# ---------------------------------------------------------------------------
+# routed-row location
+# ---------------------------------------------------------------------------
+
+
+def match_rows(x, src):
+    """RoutedTokenTracker._match (routing.py:300-333) by exact grouping: the
+    k-th occurrence of a row value in x takes the k-th token (ascending) of src
+    whose row has the same bits, then the pair must compare equal as floats
+    (torch.equal: a NaN fails).  Returns the int64 tokens, or None."""
+    x, src = np.asarray(x), np.asarray(src)
+    groups: dict[bytes, list[int]] = {}
+    for t in range(src.shape[0]):
+        groups.setdefault(src[t].tobytes(), []).append(t)
+    used: dict[bytes, int] = {}
+    out = np.empty(x.shape[0], dtype=np.int64)
+    for r in range(x.shape[0]):
+        key = x[r].tobytes()
+        k = used.get(key, 0)
+        cand = groups.get(key, [])
+        if k >= len(cand):
+            return None
+        used[key] = k + 1
+        t = cand[k]
+        if not np.array_equal(x[r].astype(np.float64), src[t].astype(np.float64)):
+            return None
+        out[r] = t
+    return out
 

@@ -762,3 +762,32 @@ def test_channel_norm_oracle_against_torch(kind):
     a, g = oracle.channel_norm_preprocess(x, gout, groups, eps, has_bias=True)
     assert a.shape == (n, h * w, 2 * c)
     np.testing.assert_allclose((a * g).sum(axis=1), np.stack(rows), rtol=1e-10, atol=1e-10)
+
+
+# ---------------------------------------------------------------------------
+# routed-row location
+# ---------------------------------------------------------------------------
+
+
+def test_match_rows_known_cases():
+    r = _rng(95)
+    src = r.standard_normal((24, 5)).astype(np.float32)
+    src[7] = src[3]  # a repeated token (a repeated sample or shared prefix)
+    src[19] = src[3]
+    # an expert's rows as fused_experts gathers them: torch.where over a mask, ascending
+    mask = np.zeros(24, dtype=bool)
+    mask[[1, 3, 7, 8, 19, 22]] = True
+    idx = torch.where(torch.from_numpy(mask))[0].numpy()
+    assert np.array_equal(oracle.match_rows(src[idx], src), idx)
+    # the same value three times in x: ascending tokens in order of appearance
+    assert np.array_equal(oracle.match_rows(src[[3, 5, 3, 3]], src), [3, 5, 7, 19])
+    # identity
+    assert np.array_equal(oracle.match_rows(src, src), np.arange(24))
+    # a row that is not a block row, and more copies than the block holds
+    assert oracle.match_rows(r.standard_normal((1, 5)).astype(np.float32), src) is None
+    assert oracle.match_rows(src[[3, 3, 3, 3]], src) is None
+    # a NaN row has matching bits but is not equal to itself (torch.equal)
+    nan_src = src.copy()
+    nan_src[2, 1] = np.nan
+    assert oracle.match_rows(nan_src[[2]], nan_src) is None
+    assert not torch.equal(torch.from_numpy(nan_src[[2]]), torch.from_numpy(nan_src[[2]]))
