@@ -98,7 +98,18 @@ from dattri_llm_amd.gradient.ops.types import (
     is_norm,
 )
 
+from dattri_llm_amd.gradient.ops.optimizer import (  # noqa: E402  (names only: outside the scoring path)
+    OPTIMIZER_STATE_KEYS,
+    adam_preconditioner,
+    adamw_influence_coupling,
+    adamw_influence_push,
+    adamw_influence_transition,
+    precondition,
+)
+
 __all__ = [
+    "OPTIMIZER_STATE_KEYS", "adam_preconditioner", "adamw_influence_coupling", "adamw_influence_push",
+    "adamw_influence_transition", "precondition",
     "FisherAccumulator", "KroneckerAccumulator", "LayerFisherAccumulator", "LayerKroneckerAccumulator",
     "dense_inverse", "ekfac_materialize", "ekfac_materialize_factors", "ekfac_precondition", "fim",
     "fim_factors", "kfac", "kfac_cross", "kfac_cross_factors", "kfac_eigh", "kfac_factors",

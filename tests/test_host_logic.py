@@ -340,3 +340,15 @@ def test_conv_preprocess_matches_oracle():
     assert conv.unfold_patches(x, 3, 1, "same", 1).shape == (2, 9, 9)
     assert conv.unfold_patches(x, 4, 1, "same", 2).shape == (2, 9, 12)
     assert torch.equal(conv.unfold_patches(x, 3, 1, "valid", 1), conv.unfold_patches(x, 3, 1, 0, 1))
+
+
+def test_ops_namespace_holds_every_reference_name(ops):
+    """Every name of the reference's ops namespace (its ``__all__``) imports
+    from ours; the optimizer maps of the out-of-scope attributors raise."""
+    names = ["OPTIMIZER_STATE_KEYS", "adam_preconditioner", "adamw_influence_coupling", "adamw_influence_push",
+             "adamw_influence_transition", "precondition", "cross_gram", "mask_factors", "project_materialized"]
+    for n in names:
+        assert hasattr(ops, n) and n in ops.__all__, n
+    assert ops.OPTIMIZER_STATE_KEYS["AdamW"] == ("exp_avg", "exp_avg_sq", "max_exp_avg_sq")
+    with pytest.raises(NotImplementedError, match="outside"):
+        ops.precondition(torch.zeros(2, 3), {}, optimizer_type="Adam", step=1)
