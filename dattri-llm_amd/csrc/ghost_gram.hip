@@ -779,83 +779,6 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
 }
 
 // ---------------------------------------------------------------------------
-// Embedding cross-gram on the 256 x 128 engine (dot.py:58-74):
-//
-//   out[i, j] = sum_{t, s : tok1[i,t] == tok2[j,s]} g1[i,t,:] . g2[j,s,:]
-//
-// An embedding's weight gradient is sum_t e_{tok_t} g_t^T, so the ghost
-// product's activation Gram is the token-equality indicator.  The tile runs
-// the engine's gradient product alone (K_g in registers) and the epilogue
-// keeps the entries whose two token ids agree.  Token ids are int64 (B, T)
-// rows; a negative id (a padding position) matches nothing, and rows past a
-// sample's length get negative sentinels.
-template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void ghost_embed_tiles_v2(GhostArgs g, const int64_t* __restrict__ tok1,
-                                                                     int64_t tok1_bs, int64_t tok1_ts,
-                                                                     const int64_t* __restrict__ tok2,
-                                                                     int64_t tok2_bs, int64_t tok2_ts) {
-  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
-  __shared__ float red[kThreads / kWave];
-  constexpr int64_t kRowGroup = 4;  // as ghost_gram_tiles_v2
-  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t per_group = kRowGroup * g.n_c;
-  const int64_t group = logical / per_group;
-  const int64_t first_r = group * kRowGroup;
-  const int64_t gsize = min(g.n_r - first_r, kRowGroup);
-  const int64_t in_group = logical - group * per_group;
-  const int64_t R = first_r + in_group % gsize;
-  const int64_t C = in_group / gsize;
-  const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
-  const int64_t j = pair_col_sample(g, i, C), ss = C % g.tiles_c;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t len1 = g.s1.tokens, len2 = g.s2.tokens;
-  const int64_t t0 = tt * v2::kBM, s0 = ss * v2::kBN;
-  float* dst = g.partial + (pair_slot(g, i, j) * g.tiles_r + tt) * g.tiles_c + ss;
-  TileSrc S;
-  const char* bg1 = g.s1.grad + i * g.s1.grad_bstride;
-  const char* bg2 = g.s2.grad + j * g.s2.grad_bstride;
-  S.ra1 = S.rg1 = make_rsrc(bg1, 0x7fffffffu);
-  S.ra2 = S.rg2 = make_rsrc(bg2, 0x7fffffffu);
-  S.kbytes_a = 0;
-  S.kbytes_g = g.kbytes_g;
-#pragma unroll
-  for (int q = 0; q < v2::kDma; ++q) {
-    const int row = dma_row(wave, q, lane);
-    const bool side1 = row < v2::kBM;
-    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
-    const bool live = t < (side1 ? len1 : len2);
-    S.roff_a[q] = v2::kOob;
-    S.roff_g[q] = live ? (uint32_t)(t * (side1 ? g.s1.grad_tstride : g.s2.grad_tstride)) : v2::kOob;
-  }
-  f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT, false>(S, smem, ka, kg);
-  // The ring is free: stage the tile's token ids (sentinels past the ends).
-  int64_t* ids = (int64_t*)smem;
-  for (int r = tid; r < v2::kRows; r += kThreads) {
-    const bool side1 = r < v2::kBM;
-    const int64_t t = side1 ? t0 + r : s0 + r - v2::kBM;
-    ids[r] = side1 ? (t < len1 ? tok1[i * tok1_bs + t * tok1_ts] : -1)
-                   : (t < len2 ? tok2[j * tok2_bs + t * tok2_ts] : -2);
-  }
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int64_t id2 = ids[v2::kBM + 64 * wn + 32 * y + acc_col(lane)];
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (id2 >= 0 && ids[128 * wm + 32 * x + acc_row(r, lane)] == id2) s += kg[x][y][r];
-    }
-  s = wave_sum(s);
-  if (lane == 0) red[wave] = s;
-  __syncthreads();
-  if (tid == 0) *dst = (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-// ---------------------------------------------------------------------------
 // Per-token cross-gram on the 256 x 128 engine: K[i, t, j] keeps side 1's
 // token t and sums side 2 out (the token decomposition of the score).
 //
@@ -946,84 +869,6 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) 
       }
   __syncthreads();
   // one thread per row: the row's 128 columns in order (zero past side 2's end)
-  const int64_t t = t0 + tid;
-  if (t < len1) {
-    const float* pr = P + tid * v2::kPRow;
-    float sum = 0.f;
-    for (int c = 0; c < v2::kBN; ++c) sum += pr[c];
-    g.partial[((i * g.s2.batch + j) * g.tpad + t) * g.tiles_c + ss] = sum;
-  }
-}
-
-// Per-token embedding cross-gram (dot.py:189-203):
-//
-//   out[i, t, j] = sum_{s : tok2[j,s] == tok1[i,t]} g1[i,t,:] . g2[j,s,:]
-//
-// The embedding tile above with the per-token epilogue: the kept entries of
-// the (256 x 128) gradient products are parked in LDS and each row is summed
-// over its 128 columns; per_token_reduce adds the column tiles in order.
-template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void ghost_embed_per_token_v2(PerTokArgs g, const int64_t* __restrict__ tok1,
-                                                                         int64_t tok1_bs, int64_t tok1_ts,
-                                                                         const int64_t* __restrict__ tok2,
-                                                                         int64_t tok2_bs, int64_t tok2_ts) {
-  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
-  __shared__ int64_t ids[v2::kRows];
-  constexpr int64_t kRowGroup = 4;
-  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t per_group = kRowGroup * g.n_c;
-  const int64_t group = logical / per_group;
-  const int64_t first_r = group * kRowGroup;
-  const int64_t gsize = min(g.n_r - first_r, kRowGroup);
-  const int64_t in_group = logical - group * per_group;
-  const int64_t R = first_r + in_group % gsize;
-  const int64_t C = in_group / gsize;
-  const int64_t i = R / g.tiles_r, tt = R % g.tiles_r;
-  const int64_t j = C / g.tiles_c, ss = C % g.tiles_c;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t len1 = g.s1.tokens, len2 = g.s2.tokens;
-  const int64_t t0 = tt * v2::kBM, s0 = ss * v2::kBN;
-  if (t0 >= len1) return;  // uniform: no row of this tile is read back
-  for (int r = tid; r < v2::kRows; r += kThreads) {
-    const bool side1 = r < v2::kBM;
-    const int64_t t = side1 ? t0 + r : s0 + r - v2::kBM;
-    ids[r] = side1 ? (t < len1 ? tok1[i * tok1_bs + t * tok1_ts] : -1)
-                   : (t < len2 ? tok2[j * tok2_bs + t * tok2_ts] : -2);
-  }
-  __syncthreads();
-  TileSrc S;
-  const char* bg1 = g.s1.grad + i * g.s1.grad_bstride;
-  const char* bg2 = g.s2.grad + j * g.s2.grad_bstride;
-  S.ra1 = S.rg1 = make_rsrc(bg1, 0x7fffffffu);
-  S.ra2 = S.rg2 = make_rsrc(bg2, 0x7fffffffu);
-  S.kbytes_a = 0;
-  S.kbytes_g = g.kbytes_g;
-#pragma unroll
-  for (int q = 0; q < v2::kDma; ++q) {
-    const int row = dma_row(wave, q, lane);
-    const bool side1 = row < v2::kBM;
-    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
-    const bool live = t < (side1 ? len1 : len2);
-    S.roff_a[q] = v2::kOob;
-    S.roff_g[q] = live ? (uint32_t)(t * (side1 ? g.s1.grad_tstride : g.s2.grad_tstride)) : v2::kOob;
-  }
-  f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT, false>(S, smem, ka, kg);
-  float* P = (float*)smem;
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int col = 64 * wn + 32 * y + acc_col(lane);
-      const int64_t id2 = ids[v2::kBM + col];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 128 * wm + 32 * x + acc_row(r, lane);
-        P[row * v2::kPRow + col] = (id2 >= 0 && ids[row] == id2) ? kg[x][y][r] : 0.f;
-      }
-    }
-  __syncthreads();
   const int64_t t = t0 + tid;
   if (t < len1) {
     const float* pr = P + tid * v2::kPRow;
@@ -1558,192 +1403,6 @@ int da_dense_per_token(const da_factor_side* s1, const void* m2, int64_t b2, int
   g.tpad = p.tpad;
   g.partial = (float*)workspace;
   return per_token_launch(g, true, dtype, s1->tokens, out, ld_b1, ld_t, ld_b2, accumulate, (hipStream_t)stream, who);
-}
-
-}  // extern "C"
-
-namespace da {
-namespace {
-
-// Embedding sides: act holds int64 token ids (B, T) with strides in ids,
-// grad the (B, T, D) output gradients; dense rows only, no bias column.
-int embed_plan(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype, bool diag, Plan* plan) {
-  const char* who = "da_ghost_gram_embedding";
-  if (diag && s1 && s2 && s1->batch != s2->batch)
-    return set_error(DA_ERR_INVALID, "%s: diag needs one batch size on both sides (%lld vs %lld)", who,
-                     (long long)s1->batch, (long long)s2->batch);
-  if (!valid_dtype(dtype)) return set_error(DA_ERR_INVALID, "%s: bad dtype %d", who, dtype);
-  if (!s1 || !s2) return set_error(DA_ERR_INVALID, "%s: NULL side", who);
-  const int64_t es = (int64_t)elem_bytes(dtype);
-  if (D <= 0 || (D * es) % 16)
-    return set_error(DA_ERR_INVALID, "%s: D=%lld must be a positive multiple of %lld elements", who, (long long)D,
-                     (long long)(16 / es));
-  const da_factor_side* sd[2] = {s1, s2};
-  for (int q = 0; q < 2; ++q) {
-    const da_factor_side* s = sd[q];
-    if (s->batch < 0 || s->tokens < 0) return set_error(DA_ERR_INVALID, "%s: negative batch/tokens", who);
-    if (s->seg_offsets || s->row_index || s->has_bias)
-      return set_error(DA_ERR_INVALID, "%s: embedding sides are dense, without a bias column", who);
-    if (s->batch == 0 || s->tokens == 0) continue;
-    if (!s->act || !s->grad) return set_error(DA_ERR_INVALID, "%s: NULL factor", who);
-    if (((uintptr_t)s->act & 7) || ((uintptr_t)s->grad & 15) || (s->grad_tstride * es) % 16 ||
-        (s->grad_bstride * es) % 16)
-      return set_error(DA_ERR_INVALID, "%s: gradient rows must be 16-byte aligned", who);
-    if ((s->grad_tstride != 0 && s->grad_tstride < D) || s->tokens * s->grad_tstride * es >= (1LL << 31) - (1LL << 20))
-      return set_error(DA_ERR_UNSUPPORTED, "%s: a sample's gradient rows must span under 2 GiB", who);
-  }
-  plan->v2 = true;
-  plan->tiles_r = (s1->tokens + v2::kBM - 1) / v2::kBM;
-  plan->tiles_c = (s2->tokens + v2::kBN - 1) / v2::kBN;
-  plan->n_r = s1->batch * plan->tiles_r;
-  plan->n_c = (diag ? 1 : s2->batch) * plan->tiles_c;
-  plan->per_pair = plan->tiles_r * plan->tiles_c;
-  plan->ws = (size_t)(s1->batch * (diag ? 1 : s2->batch) * plan->per_pair) * sizeof(float);
-  return DA_OK;
-}
-
-int run_embed(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype, bool diag, float* out,
-              int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  Plan plan;
-  int rc = embed_plan(s1, s2, D, dtype, diag, &plan);
-  if (rc) return rc;
-  const int64_t b1 = s1->batch, b2 = diag ? 1 : s2->batch;
-  if (b1 == 0 || s2->batch == 0) return DA_OK;
-  if (!out || ld_out < b2) return set_error(DA_ERR_INVALID, "da_ghost_gram_embedding: bad out / ld_out");
-  if (s1->tokens == 0 || s2->tokens == 0) return accumulate ? DA_OK : zero_f32_2d(out, b1, b2, ld_out, st);
-  if (!workspace || workspace_bytes < plan.ws)
-    return set_error(DA_ERR_WORKSPACE, "da_ghost_gram_embedding: workspace needs %zu bytes, got %zu", plan.ws,
-                     workspace_bytes);
-  const int64_t es = (int64_t)elem_bytes(dtype);
-  GhostArgs args;
-  args.s1 = to_dev(s1, es);
-  args.s2 = to_dev(s2, es);
-  args.kbytes_a = 0;
-  args.kbytes_g = D * es;
-  args.tiles_r = plan.tiles_r;
-  args.tiles_c = plan.tiles_c;
-  args.n_r = plan.n_r;
-  args.n_c = plan.n_c;
-  args.bias = 0.f;
-  args.diag = diag ? 1 : 0;
-  args.partial = (float*)workspace;
-  const int64_t ntiles = plan.n_r * plan.n_c;
-  if (ntiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_ghost_gram_embedding: too many tiles");
-  const int64_t* t1 = (const int64_t*)s1->act;
-  const int64_t* t2 = (const int64_t*)s2->act;
-  switch (dtype) {
-    case DA_BF16:
-      ghost_embed_tiles_v2<DA_BF16><<<(unsigned)ntiles, kThreads, 0, st>>>(args, t1, s1->act_bstride, s1->act_tstride,
-                                                                          t2, s2->act_bstride, s2->act_tstride);
-      break;
-    case DA_F16:
-      ghost_embed_tiles_v2<DA_F16><<<(unsigned)ntiles, kThreads, 0, st>>>(args, t1, s1->act_bstride, s1->act_tstride,
-                                                                         t2, s2->act_bstride, s2->act_tstride);
-      break;
-    default:
-      ghost_embed_tiles_v2<DA_F32><<<(unsigned)ntiles, kThreads, 0, st>>>(args, t1, s1->act_bstride, s1->act_tstride,
-                                                                         t2, s2->act_bstride, s2->act_tstride);
-      break;
-  }
-  rc = check_launch("da_ghost_gram_embedding(tiles)");
-  if (rc) return rc;
-  ghost_gram_reduce<<<(unsigned)((b1 * b2 + 255) / 256), 256, 0, st>>>((const float*)workspace, b1, b2,
-                                                                       plan.per_pair, out, ld_out, accumulate);
-  return check_launch("da_ghost_gram_embedding(reduce)");
-}
-
-}  // namespace
-}  // namespace da
-
-extern "C" {
-
-int da_ghost_gram_embedding_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype,
-                                      int diag, size_t* bytes) {
-  da::Plan plan;
-  int rc = da::embed_plan(s1, s2, D, dtype, diag != 0, &plan);
-  if (rc) return rc;
-  if (!bytes) return da::set_error(DA_ERR_INVALID, "da_ghost_gram_embedding_workspace: bytes is NULL");
-  *bytes = plan.ws;
-  return DA_OK;
-}
-
-int da_ghost_gram_embedding(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype, int diag,
-                            float* out, int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes,
-                            void* stream) {
-  return da::run_embed(s1, s2, D, dtype, diag != 0, out, ld_out, accumulate, workspace, workspace_bytes,
-                       (hipStream_t)stream);
-}
-
-int da_ghost_gram_embedding_per_token_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t D,
-                                                int dtype, size_t* bytes) {
-  using namespace da;
-  const char* who = "da_ghost_gram_embedding_per_token";
-  if (!bytes || !s1 || !s2) return set_error(DA_ERR_INVALID, "%s_workspace: NULL argument", who);
-  Plan plan;
-  int rc = embed_plan(s1, s2, D, dtype, false, &plan);
-  if (rc) return rc;
-  PerTokPlan p;
-  rc = per_token_plan(s1, s2->batch, s2->tokens, 0, D, dtype, who, &p);
-  if (rc) return rc;
-  *bytes = p.ws;
-  return DA_OK;
-}
-
-int da_ghost_gram_embedding_per_token(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype,
-                                      float* out, int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
-  using namespace da;
-  const char* who = "da_ghost_gram_embedding_per_token";
-  if (!s1 || !s2) return set_error(DA_ERR_INVALID, "%s: NULL side", who);
-  Plan plan;
-  int rc = embed_plan(s1, s2, D, dtype, false, &plan);
-  if (rc) return rc;
-  PerTokPlan p;
-  rc = per_token_plan(s1, s2->batch, s2->tokens, 0, D, dtype, who, &p);
-  if (rc) return rc;
-  if (s1->batch == 0 || s1->tokens == 0 || s2->batch == 0) return DA_OK;
-  if (!out) return set_error(DA_ERR_INVALID, "%s: out is NULL", who);
-  if (!workspace || workspace_bytes < p.ws)
-    return set_error(DA_ERR_WORKSPACE, "%s: workspace needs %zu bytes", who, p.ws);
-  const int64_t es = (int64_t)elem_bytes(dtype);
-  PerTokArgs g;
-  g.s1 = to_dev(s1, es);
-  g.s2 = to_dev(s2, es);
-  g.kbytes_a = 0;
-  g.kbytes_g = D * es;
-  g.tiles_r = p.tiles_r;
-  g.tiles_c = p.tiles_c;
-  g.n_r = s1->batch * p.tiles_r;
-  g.n_c = s2->batch * p.tiles_c;
-  g.bias = 0.f;
-  g.m2bias = nullptr;
-  g.m2bias_ld = 0;
-  g.tpad = p.tpad;
-  g.partial = (float*)workspace;
-  hipStream_t st = (hipStream_t)stream;
-  if (s2->tokens > 0) {
-    const int64_t tiles = g.n_r * g.n_c;
-    if (tiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
-    const int64_t* t1 = (const int64_t*)s1->act;
-    const int64_t* t2 = (const int64_t*)s2->act;
-#define DA_EPT(DT)                                                                                        \
-  ghost_embed_per_token_v2<DT><<<(unsigned)tiles, kThreads, 0, st>>>(g, t1, s1->act_bstride, s1->act_tstride, \
-                                                                     t2, s2->act_bstride, s2->act_tstride)
-    switch (dtype) {
-      case DA_BF16: DA_EPT(DA_BF16); break;
-      case DA_F16: DA_EPT(DA_F16); break;
-      default: DA_EPT(DA_F32); break;
-    }
-#undef DA_EPT
-    rc = check_launch(who);
-    if (rc) return rc;
-  } else {
-    g.tiles_c = 0;  // nothing on side 2: the sums are zero
-  }
-  const int64_t n = s1->batch * s1->tokens * s2->batch;
-  per_token_reduce<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(g.partial, s1->batch, s1->tokens, s2->batch, g.tpad,
-                                                                g.tiles_c, out, ld_b1, ld_t, ld_b2, accumulate);
-  return check_launch(who);
 }
 
 }  // extern "C"

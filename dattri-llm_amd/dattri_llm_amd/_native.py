@@ -68,10 +68,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "da_ghost_gram_per_token_workspace": (_I32, [_SIDE, _SIDE, _I64, _I64, _I32, ctypes.POINTER(_SZ)]),
     "da_ghost_gram_per_token": (
         _I32, [_SIDE, _SIDE, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P]),
-    "da_ghost_gram_embedding_workspace": (_I32, [_SIDE, _SIDE, _I64, _I32, _I32, ctypes.POINTER(_SZ)]),
-    "da_ghost_gram_embedding": (_I32, [_SIDE, _SIDE, _I64, _I32, _I32, _P, _I64, _I32, _P, _SZ, _P]),
-    "da_ghost_gram_embedding_per_token_workspace": (_I32, [_SIDE, _SIDE, _I64, _I32, ctypes.POINTER(_SZ)]),
-    "da_ghost_gram_embedding_per_token": (
+    "da_embedding_cross_gram_workspace": (_I32, [_SIDE, _SIDE, _I64, _I32, _I32, ctypes.POINTER(_SZ)]),
+    "da_embedding_cross_gram": (_I32, [_SIDE, _SIDE, _I64, _I32, _I32, _P, _I64, _I32, _P, _SZ, _P]),
+    "da_embedding_cross_gram_per_token_workspace": (_I32, [_SIDE, _SIDE, _I64, _I32, ctypes.POINTER(_SZ)]),
+    "da_embedding_cross_gram_per_token": (
         _I32, [_SIDE, _SIDE, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P]),
     "da_dense_per_token_embedding": (
         _I32, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64,

@@ -5,12 +5,13 @@ activation factor is a one-hot row per token, so every product of two such
 gradients only pairs tokens with equal ids.  The reference builds a
 ``(vocab, E)`` scatter-add table per side-2 sample and gathers from it
 (``dattri_llm/gradient/ops/dot.py:58-74``, ``:189-203``, ``:325-337``); here
-the ghost engine computes the gradient rows' products and keeps the pairs
-whose ids agree, so no table is formed:
+side 2 is compacted to each sample's distinct ids (fp32 row sums, sorted ids)
+and every side-1 token is looked up in it, so no vocabulary-sized table is
+formed and no token pair is multiplied:
 
-* :func:`gram32` / :func:`diag32` -- ``da_ghost_gram_embedding`` (all pairs, or
+* :func:`gram32` / :func:`diag32` -- ``da_embedding_cross_gram`` (all pairs, or
   the diagonal pairs for per-sample dots and squared norms);
-* :func:`per_token32` -- ``da_ghost_gram_embedding_per_token``;
+* :func:`per_token32` -- ``da_embedding_cross_gram_per_token``;
 * :func:`dense_per_token32` -- ``da_dense_per_token_embedding``, side 2 dense;
 * :func:`materialize` -- ``da_materialize_embedding``, the deterministic
   scatter-add of ``materialize.py:22-48``.
@@ -72,9 +73,9 @@ def gram32(s1, s2, out=None, accumulate=False) -> torch.Tensor:
     (ids1, g1), (ids2, g2) = s1, s2
     if s1 is s2:
         (g1,) = _rows(g1)
-        return kernels.ghost_gram_embedding(ids1, g1, ids1, g1, out=out, accumulate=accumulate)
+        return kernels.embedding_cross_gram(ids1, g1, ids1, g1, out=out, accumulate=accumulate)
     g1, g2 = _rows(g1, g2)
-    return kernels.ghost_gram_embedding(ids1, g1, ids2, g2, out=out, accumulate=accumulate)
+    return kernels.embedding_cross_gram(ids1, g1, ids2, g2, out=out, accumulate=accumulate)
 
 
 def diag32(s1, s2) -> torch.Tensor:
@@ -83,16 +84,16 @@ def diag32(s1, s2) -> torch.Tensor:
     (ids1, g1), (ids2, g2) = s1, s2
     if s1 is s2:
         (g1,) = _rows(g1)
-        return kernels.ghost_gram_embedding(ids1, g1, ids1, g1, diag=True)
+        return kernels.embedding_cross_gram(ids1, g1, ids1, g1, diag=True)
     g1, g2 = _rows(g1, g2)
-    return kernels.ghost_gram_embedding(ids1, g1, ids2, g2, diag=True)
+    return kernels.embedding_cross_gram(ids1, g1, ids2, g2, diag=True)
 
 
 def per_token32(s1, s2) -> torch.Tensor:
     """fp32 (B1, T1, B2): side 1's token t against side 2's whole gradient."""
     (ids1, g1), (ids2, g2) = s1, s2
     g1, g2 = _rows(g1, g2)
-    return kernels.ghost_gram_embedding_per_token(ids1, g1, ids2, g2)
+    return kernels.embedding_cross_gram_per_token(ids1, g1, ids2, g2)
 
 
 def dense_per_token32(s1, m2: torch.Tensor) -> torch.Tensor:

@@ -203,7 +203,7 @@ def _token_ids(tok: torch.Tensor) -> torch.Tensor:
     return tok
 
 
-def ghost_gram_embedding(
+def embedding_cross_gram(
     tok1: torch.Tensor,
     g1: torch.Tensor,
     tok2: torch.Tensor,
@@ -213,16 +213,17 @@ def ghost_gram_embedding(
     out: torch.Tensor | None = None,
     accumulate: bool = False,
 ) -> torch.Tensor:
-    """Ghost inner product of one embedding layer, fp32 ``(B1, B2)``:
-    ``sum over (t, s) with tok1[i,t] == tok2[j,s] of g1[i,t] . g2[j,s]``.
+    """Cross-gram of one embedding layer, fp32 ``(B1, B2)``:
+    ``sum over (t, s) with tok1[i,t] == tok2[j,s] of g1[i,t] . g2[j,s]`` --
+    side 2 compacted to its distinct ids, each side-1 token looked up.
 
     ``tok*`` are integer (B, T) ids (negative ids match nothing), ``g*`` the
     (B, T, E) gradient rows in one of fp32/fp16/bf16.  With ``diag`` only the
     pairs (i, i) are formed and the result is ``(B,)``."""
     dev = nat.require_device(tok1, g1, tok2, g2)
     if diag and tok1.shape[0] != tok2.shape[0]:
-        raise ValueError("ghost_gram_embedding(diag=True) needs two blocks of one batch size")
-    tok1, g1, tok2, g2, e = _embedding_sides("ghost_gram_embedding", tok1, g1, tok2, g2)
+        raise ValueError("embedding_cross_gram(diag=True) needs two blocks of one batch size")
+    tok1, g1, tok2, g2, e = _embedding_sides("embedding_cross_gram", tok1, g1, tok2, g2)
     code = nat.dtype_code(g1.dtype)
     b1, b2 = tok1.shape[0], tok2.shape[0]
     shape = (b1,) if diag else (b1, b2)
@@ -234,10 +235,10 @@ def ghost_gram_embedding(
     s1, s2 = _side(tok1, g1, False), _side(tok2, g2, False)
     lib = nat.load()
     nbytes = ctypes.c_size_t(0)
-    nat.check(lib.da_ghost_gram_embedding_workspace(s1, s2, e, code, int(diag), ctypes.byref(nbytes)),
-              "ghost_gram_embedding")
+    nat.check(lib.da_embedding_cross_gram_workspace(s1, s2, e, code, int(diag), ctypes.byref(nbytes)),
+              "embedding_cross_gram")
     ws = nat.workspace(nbytes.value, dev)
-    _run(dev, "ghost_gram_embedding", lib.da_ghost_gram_embedding,
+    _run(dev, "embedding_cross_gram", lib.da_embedding_cross_gram,
          s1, s2, e, code, int(diag), out.data_ptr(), out.stride(0), int(accumulate), ws.data_ptr(), ws.numel(),
          nat.stream_ptr(dev))
     return out
@@ -340,7 +341,7 @@ def _embedding_sides(name, tok1, g1, tok2, g2):
     return tok1, g1, tok2, g2, e
 
 
-def ghost_gram_embedding_per_token(
+def embedding_cross_gram_per_token(
     tok1: torch.Tensor,
     g1: torch.Tensor,
     tok2: torch.Tensor,
@@ -353,17 +354,17 @@ def ghost_gram_embedding_per_token(
     against side 2's whole per-sample gradient, ``sum over s with
     tok2[j,s] == tok1[i,t] of g1[i,t] . g2[j,s]``."""
     dev = nat.require_device(tok1, g1, tok2, g2)
-    tok1, g1, tok2, g2, e = _embedding_sides("ghost_gram_embedding_per_token", tok1, g1, tok2, g2)
+    tok1, g1, tok2, g2, e = _embedding_sides("embedding_cross_gram_per_token", tok1, g1, tok2, g2)
     code = nat.dtype_code(g1.dtype)
     b1, t1, b2 = tok1.shape[0], tok1.shape[1], tok2.shape[0]
     out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
     s1, s2 = _side(tok1, g1, False), _side(tok2, g2, False)
     lib = nat.load()
     nbytes = ctypes.c_size_t(0)
-    nat.check(lib.da_ghost_gram_embedding_per_token_workspace(s1, s2, e, code, ctypes.byref(nbytes)),
-              "ghost_gram_embedding_per_token")
+    nat.check(lib.da_embedding_cross_gram_per_token_workspace(s1, s2, e, code, ctypes.byref(nbytes)),
+              "embedding_cross_gram_per_token")
     ws = nat.workspace(nbytes.value, dev)
-    _run(dev, "ghost_gram_embedding_per_token", lib.da_ghost_gram_embedding_per_token,
+    _run(dev, "embedding_cross_gram_per_token", lib.da_embedding_cross_gram_per_token,
          s1, s2, e, code, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
          ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out

@@ -117,43 +117,42 @@ int da_ghost_gram_diag(const da_factor_side* s1, const da_factor_side* s2, int64
                        void* stream);
 
 /*
- * Ghost inner product of one embedding layer (nn.Embedding, and
- * nn.EmbeddingBag once its per-bag gradient is spread over its tokens):
+ * Cross-gram of two embedding sides (nn.Embedding, and nn.EmbeddingBag once
+ * its per-bag gradient is spread over its tokens).  The weight gradient is
+ * sum_t e_{tok_t} g_t^T, so
  *
- *   out[i*ld_out + j] (+)= sum_{t,s : tok1[i,t] == tok2[j,s]} g1[i,t,:] . g2[j,s,:]
+ *   out[i*ld_out + j] (+)= sum_t g1[i,t,:] . G2_j[tok1[i,t], :],
+ *   G2_j[v] = sum over s with tok2[j,s] == v of g2[j,s,:]
  *
- * (the weight gradient is sum_t e_{tok_t} g_t^T, so the activation Gram of
- * the linear ghost product is the token-equality indicator).  side->act holds
- * int64 token ids (B, T) with element strides (act_bstride, act_tstride);
- * side->grad the (B, T, D) gradient rows.  A negative id matches nothing (a
- * padding position).  No segments, row index or bias column.  diag = 1 takes
- * the pairs (i, i) only, into out[i*ld_out] (both batches equal): the
- * per-sample dots, or squared norms when both sides are one block.  fp32,
+ * side->act holds int64 token ids (B, T) with element strides (act_bstride,
+ * act_tstride); side->grad the (B, T, E) gradient rows (16-byte aligned).  A
+ * negative id matches nothing (a padding position).  No segments, row index
+ * or bias column.  diag = 1 takes the pairs (i, i) only, into out[i*ld_out]
+ * (both batches equal): per-sample dots, or squared norms when both sides are
+ * one block.  Side 2 is compacted to its samples' distinct ids (fp32 row sums,
+ * sorted ids), and every side-1 token is looked up in every side-2 sample:
+ * O(B1 T1 B2 log T2) searches plus one E-long dot per match.  fp32,
  * deterministic.  Replaces the embedding branches of cross_gram,
  * dattri_llm/gradient/ops/dot.py:58-74 (a scatter_add_ into a (vocab, E)
  * table per side-2 sample, then a gather), of dot_factors, dot.py:325-337,
  * and of grad_norm_sq_factors, dot.py:383-384.
  */
-int da_ghost_gram_embedding_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype,
+int da_embedding_cross_gram_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t E, int dtype,
                                       int diag, size_t* bytes);
-int da_ghost_gram_embedding(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype, int diag,
+int da_embedding_cross_gram(const da_factor_side* s1, const da_factor_side* s2, int64_t E, int dtype, int diag,
                             float* out, int64_t ld_out, int accumulate, void* workspace, size_t workspace_bytes,
                             void* stream);
 
 /*
- * Per-token embedding cross-gram: side 1's token axis kept, side 2's summed,
- *
- *   out[i*ld_b1 + t*ld_t + j*ld_b2] (+)= sum_{s : tok2[j,s] == tok1[i,t]} g1[i,t,:] . g2[j,s,:]
- *
- * fp32 (B1, T1, B2), sides as for da_ghost_gram_embedding (a negative id
- * matches nothing; a gradient token stride of 0 is allowed, for a bag's one
- * gradient row spread over its tokens).  Summing over t gives
- * da_ghost_gram_embedding's (B1, B2).  Replaces the embedding branch of
+ * The same products kept per side-1 token: out[i*ld_b1 + t*ld_t + j*ld_b2]
+ * (+)= g1[i,t,:] . G2_j[tok1[i,t], :], fp32 (B1, T1, B2); summing over t gives
+ * da_embedding_cross_gram.  A gradient token stride of 0 is allowed (a bag's
+ * one gradient row spread over its tokens).  Replaces the embedding branch of
  * cross_gram_per_token, dattri_llm/gradient/ops/dot.py:189-203.
  */
-int da_ghost_gram_embedding_per_token_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t D,
+int da_embedding_cross_gram_per_token_workspace(const da_factor_side* s1, const da_factor_side* s2, int64_t E,
                                                 int dtype, size_t* bytes);
-int da_ghost_gram_embedding_per_token(const da_factor_side* s1, const da_factor_side* s2, int64_t D, int dtype,
+int da_embedding_cross_gram_per_token(const da_factor_side* s1, const da_factor_side* s2, int64_t E, int dtype,
                                       float* out, int64_t ld_b1, int64_t ld_t, int64_t ld_b2, int accumulate,
                                       void* workspace, size_t workspace_bytes, void* stream);
 

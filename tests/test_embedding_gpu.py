@@ -3,7 +3,7 @@
 * ``da_materialize_embedding`` (materialize.py:22-48) is bit-exact against the
   oracle's restatement of the CPU scatter_add_ (fp32 sums in ascending token
   order, one rounding), in bf16, fp16 and fp32;
-* the ghost embedding kernels (dot.py:58-74, :189-203, :325-337, :383-384)
+* the embedding cross-gram kernels (dot.py:58-74, :189-203, :325-337, :383-384)
   and the dense per-token product (dot.py:239-245) meet the two parity bars
   of conftest.assert_parity against the float64 oracle;
 * the ops entry points (padding_idx, EmbeddingBag sum/mean) route there.
@@ -138,40 +138,40 @@ def _oracle_ids(tok, side):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("case", GRAM_CASES)
-def test_ghost_gram_embedding_matches_oracle(device, dtype, case):
+def test_embedding_cross_gram_matches_oracle(device, dtype, case):
     from dattri_llm_amd import kernels
 
     tok1, g1, tok2, g2 = _gram_inputs(case, dtype)
-    print(f"ghost_gram_embedding case={case} dtype={dtype}", flush=True)
+    print(f"embedding_cross_gram case={case} dtype={dtype}", flush=True)
     d = [x.to(device) for x in (tok1, g1, tok2, g2)]
     t1, t2 = _oracle_ids(tok1, 1), _oracle_ids(tok2, 2)
-    got = kernels.ghost_gram_embedding(*d)
+    got = kernels.embedding_cross_gram(*d)
     ref = oracle.embedding_cross_gram(t1, g1.double().numpy(), t2, g2.double().numpy())
     assert_parity(got, ref, dtype, label="gram")
-    per_tok = kernels.ghost_gram_embedding_per_token(*d)
+    per_tok = kernels.embedding_cross_gram_per_token(*d)
     ref_pt = oracle.embedding_cross_gram_per_token(t1, g1.double().numpy(), t2, g2.double().numpy())
     assert per_tok.shape == ref_pt.shape
     assert_parity(per_tok, ref_pt, dtype, label="per_token")
     # accumulate adds into out
     out = torch.ones_like(got)
-    kernels.ghost_gram_embedding(*d, out=out, accumulate=True)
+    kernels.embedding_cross_gram(*d, out=out, accumulate=True)
     assert_parity(out, ref + 1.0, dtype, label="accumulate")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("case", [(4, 300, 4, 200, 40, 30), (3, 77, 3, 77, 64, 5)])
-def test_ghost_gram_embedding_diag(device, dtype, case):
+def test_embedding_cross_gram_diag(device, dtype, case):
     from dattri_llm_amd import kernels
 
     tok1, g1, tok2, g2 = _gram_inputs(case, dtype)
     d = [x.to(device) for x in (tok1, g1, tok2, g2)]
-    got = kernels.ghost_gram_embedding(*d, diag=True)
+    got = kernels.embedding_cross_gram(*d, diag=True)
     full = oracle.embedding_cross_gram(_oracle_ids(tok1, 1), g1.double().numpy(), _oracle_ids(tok2, 2),
                                        g2.double().numpy())
     assert got.shape == (case[0],)
     assert_parity(got, np.diagonal(full).copy(), dtype, label="diag")
     # one block with itself: the squared norms of the materialized gradients
-    sq = kernels.ghost_gram_embedding(d[0], d[1], d[0], d[1], diag=True)
+    sq = kernels.embedding_cross_gram(d[0], d[1], d[0], d[1], diag=True)
     m = oracle.embedding_materialize(tok1.clamp_min(0).numpy(), np.where((tok1 < 0)[..., None].numpy(), 0.0,
                                      g1.double().numpy()), case[5])
     assert_parity(sq, (m * m).sum(-1), dtype, label="norm")
@@ -308,3 +308,32 @@ def test_ops_embedding_width_and_range(device):
         ops.materialize_factors(hi, g_hi, "nn.Embedding")
     with pytest.raises(ValueError, match="negative"):
         ops.cross_gram(lo - 3, g_lo, hi, g_hi, "nn.Embedding")
+
+
+def test_embedding_cross_gram_at_scale(device):
+    """Long sequences with a Zipf-like id distribution (8 x 2048 against 16 x 512
+    tokens, E = 1024, vocab 32000): the cross-gram, its diagonal and the
+    per-token sums against the product of the materialized gradients, an fp32
+    torch matmul of this build's bit-exact scatter."""
+    from dattri_llm_amd import kernels
+
+    vocab, e = 32000, 1024
+    gen = torch.Generator().manual_seed(21)
+    ranks = torch.arange(1, vocab + 1, dtype=torch.float64)
+    probs = (1.0 / ranks) / (1.0 / ranks).sum()
+    tok1 = torch.multinomial(probs, 8 * 2048, replacement=True, generator=gen).view(8, 2048)
+    tok2 = torch.multinomial(probs, 16 * 512, replacement=True, generator=gen).view(16, 512)
+    g1 = torch.randn(8, 2048, e, generator=gen) * 0.1
+    g2 = torch.randn(16, 512, e, generator=gen) * 0.1
+    d = [x.to(device) for x in (tok1, g1, tok2, g2)]
+    print("embedding cross-gram at scale", flush=True)
+    m1 = kernels.materialize_embedding(d[0], d[1], vocab)
+    m2 = kernels.materialize_embedding(d[2], d[3], vocab)
+    ref = (m1.double() @ m2.double().T).cpu().numpy()
+    got = kernels.embedding_cross_gram(*d)
+    assert_parity(got, ref, torch.float32, label="gram")
+    per_tok = kernels.embedding_cross_gram_per_token(*d)
+    assert_parity(per_tok.double().sum(1), ref, torch.float32, label="per-token sum")
+    sq = kernels.embedding_cross_gram(d[0], d[1], d[0], d[1], diag=True)
+    assert_parity(sq, (m1.double() ** 2).sum(-1).cpu().numpy(), torch.float32, label="norms")
+    del m1, m2
