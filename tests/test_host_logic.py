@@ -352,3 +352,24 @@ def test_ops_namespace_holds_every_reference_name(ops):
     assert ops.OPTIMIZER_STATE_KEYS["AdamW"] == ("exp_avg", "exp_avg_sq", "max_exp_avg_sq")
     with pytest.raises(NotImplementedError, match="outside"):
         ops.precondition(torch.zeros(2, 3), {}, optimizer_type="Adam", step=1)
+
+
+def test_locate_rows_identity_and_regroup_on_host():
+    """The block's own rows in order take the identity layout without a kernel
+    (routing.py:303-304); RowLayout.regroup scatters routed rows back to
+    (B, T, ...) with zeros elsewhere (routing.py:71-86)."""
+    from dattri_llm_amd.gradient.routing import RowLayout, locate_rows
+
+    x = torch.randn(6, 4)
+    lay = locate_rows(x, x.clone(), 2, 3)
+    assert lay == RowLayout(2, 3, 6)
+    assert torch.equal(lay.regroup(x), x.reshape(2, 3, 4))
+    with pytest.raises(ValueError):
+        lay.regroup(x[:5])
+    with pytest.raises(ValueError):
+        locate_rows(x, x[:5], 2, 3)
+    sparse = RowLayout(2, 3, 2, torch.tensor([1, 0]), torch.tensor([2, 0]))
+    dense = sparse.regroup(torch.tensor([[1.0], [2.0]]))
+    want = torch.zeros(2, 3, 1)
+    want[1, 2, 0], want[0, 0, 0] = 1.0, 2.0
+    assert torch.equal(dense, want)

@@ -76,3 +76,21 @@ def test_match_rows_mixtral_block(device):
         assert np.array_equal(dense, ref)
     ident = locate_rows(flat_d, flat_d, b, t)
     assert ident is not None and ident.sample is None
+
+
+def test_locate_rows_signed_zero(device):
+    """The block's own rows match by float equality (routing.py:303-304);
+    gathered rows match by their bits (routing.py:335-340), so a zero of the
+    other sign finds no token."""
+    from dattri_llm_amd.gradient.routing import locate_rows
+
+    gen = torch.Generator().manual_seed(8)
+    src = torch.randn(4 * 8, 16, generator=gen).to(torch.bfloat16)
+    src[5, 3] = 0.0
+    x = src.clone()
+    x[5, 3] = -0.0
+    ident = locate_rows(x.to(device), src.to(device), 4, 8)
+    assert ident is not None and ident.sample is None
+    assert locate_rows(x[[5, 2]].to(device), src.to(device), 4, 8) is None
+    part = locate_rows(src[[5, 2]].to(device), src.to(device), 4, 8)
+    assert part is not None and part.sample.tolist() == [0, 0] and part.position.tolist() == [5, 2]
