@@ -1,13 +1,15 @@
 """K-FAC / EK-FAC preconditioning and empirical-Fisher ops on the MI355X kernels.
 
 Same names, signatures and errors as ``dattri_llm/gradient/ops/kronecker.py``
-for linear layers (the K-FAC-eligible family on this path; conv layers are
-outside it and raise ``NotImplementedError``).  Where the arithmetic lives:
+for the K-FAC-eligible families: linear, convolution and transposed
+convolution layers, a grouped convolution with one covariance per group
+(``(G, K, K)`` factors).  Where the arithmetic lives:
 
 * token-axis contractions -- the K-FAC covariances ``a^T a`` / ``g^T g`` over
   every token row, the empirical Fisher ``grad^T grad`` over samples, the
-  EK-FAC eigenbasis coordinates -- run the per-sample dW kernel
-  (``da_materialize_linear``) with the whole row set as one sample, fp32 out;
+  EK-FAC eigenbasis coordinates -- run the symmetric row-Gram kernel or the
+  per-sample dW kernel (``da_materialize_linear``) with the whole row set as
+  one sample (a grouped convolution: each group as one sample), fp32 out;
 * the whitened cross-gram runs ``cross_gram`` (ghost / materialized kernels);
 * right-multiplications by a ``(K, K)`` inverse or eigenbasis are plain
   library GEMMs (``torch.matmul``), eigendecompositions and Cholesky factors
@@ -44,28 +46,40 @@ if TYPE_CHECKING:
 _GRAM_BYTES = 1 << 30
 
 
-def _require_kfac_linear(layer_type: str) -> None:
+def _require_kfac_eligible(layer_type: str) -> None:
     if is_norm(layer_type):
         raise NotImplementedError("K-FAC is not defined for normalization layers")
     if is_embedding(layer_type):
         raise NotImplementedError("K-FAC is not defined for embedding layers")
-    if is_conv(layer_type) or is_conv_transpose(layer_type) or not is_linear(layer_type):
+    if not (is_linear(layer_type) or is_conv(layer_type) or is_conv_transpose(layer_type)):
         require_supported(layer_type, "K-FAC")
 
 
 def _flatten_for_kfac(a: torch.Tensor, g: torch.Tensor, layer_type: str):
-    """kronecker.py:33-53: token rows ``(N, K)``, ``(N, D)`` in the aligned dtype."""
-    _require_kfac_linear(layer_type)
+    """kronecker.py:33-53: token rows ``(N, K)``, ``(N, D)`` in the aligned
+    dtype; a grouped convolution's ``(B, L, G, K)`` factors give ``(G, N, K)``
+    rows, one row set per group."""
+    _require_kfac_eligible(layer_type)
     a, g = dtypes.align(a, g)
     if a.ndim == 4:
-        raise NotImplementedError("grouped (4-D) factors are conv-only and outside this path")
+        groups = a.shape[2]
+        return (a.permute(2, 0, 1, 3).reshape(groups, -1, a.shape[-1]).contiguous(),
+                g.permute(2, 0, 1, 3).reshape(groups, -1, g.shape[-1]).contiguous())
     return a.reshape(-1, a.shape[-1]), g.reshape(-1, g.shape[-1])
 
 
+def _sequence_rows(layer_type: str) -> bool:
+    """Gradient-free rows are padding only for sequence layers; a convolution's
+    zero-gradient positions are architectural and stay (kronecker.py:104-108)."""
+    return not (is_conv(layer_type) or is_conv_transpose(layer_type))
+
+
 def _right_multiply(x: torch.Tensor, matrix: torch.Tensor) -> torch.Tensor:
-    """kronecker.py:56-62: ``x @ matrix`` on the feature axis (a plain GEMM)."""
+    """kronecker.py:56-62: ``x @ matrix`` on the feature axis (a plain GEMM);
+    per group when *matrix* is a ``(G, K, J)`` stack and *x* a grouped
+    ``(..., G, K)`` factor."""
     if matrix.ndim == 3:
-        raise NotImplementedError("per-group K-FAC factors are conv-only and outside this path")
+        return torch.matmul(x.unsqueeze(-2), matrix).squeeze(-2)
     return x @ matrix
 
 
@@ -108,6 +122,25 @@ def row_gram(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
     return out.t()
 
 
+def _grams(x: torch.Tensor) -> torch.Tensor:
+    """fp32 ``x^T x`` of ``(N, p)`` rows, or per group of ``(G, N, p)`` rows
+    -> ``(G, p, p)``: the dW kernel with each group as one sample, in row
+    chunks below 1 GiB added in fp32."""
+    if x.ndim == 2:
+        return row_gram(x)
+    kd = dtypes.kernel_dtype(x.dtype)
+    x = x.to(kd)
+    groups, n, p = x.shape
+    out = torch.zeros(groups, p * p, dtype=torch.float32, device=x.device)
+    if n == 0 or p == 0:
+        return out.view(groups, p, p)
+    rows = max(1, _GRAM_BYTES // max(1, groups * p * x.element_size()))
+    for r0 in range(0, n, rows):
+        xs = x[:, r0:r0 + rows]
+        out += kernels.materialize_linear(xs, xs, out_dtype=torch.float32)
+    return out.view(groups, p, p)
+
+
 def kfac_factors(
     a: torch.Tensor,
     g: torch.Tensor,
@@ -119,14 +152,15 @@ def kfac_factors(
     ``a^T a / N`` and ``g^T g / N`` over the token rows that carry a gradient."""
     a, g = preprocess_factors(a, g, layer_type, module_kwargs, include_bias)
     a_f, g_f = _flatten_for_kfac(a, g, layer_type)
-    a_f, g_f = _drop_gradient_free_rows(a_f, g_f)
+    if _sequence_rows(layer_type):
+        a_f, g_f = _drop_gradient_free_rows(a_f, g_f)
     n = a_f.shape[-2]
     if n == 0:
         raise ValueError(
             "K-FAC factors are undefined: every token row carries a zero "
             "gradient (fully padded / masked input).",
         )
-    return row_gram(a_f) / n, row_gram(g_f) / n
+    return _grams(a_f) / n, _grams(g_f) / n
 
 
 def fim_factors(
@@ -173,7 +207,7 @@ def kfac_cross_factors(
 ) -> torch.Tensor:
     """``K[i, j] = vec(dW1_i)^T (A^-1 (x) G^-1) vec(dW2_j)`` (kronecker.py:178-202):
     side 1's factors whitened by the inverses, then :func:`cross_gram`."""
-    _require_kfac_linear(layer_type)
+    _require_kfac_eligible(layer_type)
     a1, g1 = preprocess_factors(a1, g1, layer_type, module_kwargs1, include_bias)
     a2, g2 = preprocess_factors(a2, g2, layer_type, module_kwargs2, include_bias)
     a1 = _right_multiply(a1.float(), A_inv.float())
@@ -199,7 +233,7 @@ def ekfac_materialize_factors(
 ) -> torch.Tensor:
     """``(B, d_out*d_in)`` of ``U_G^T dW U_A``: the factors rotated into the
     eigenbasis, then the per-sample dW kernel (kronecker.py:215-233)."""
-    _require_kfac_linear(layer_type)
+    _require_kfac_eligible(layer_type)
     a, g = preprocess_factors(a, g, layer_type, module_kwargs, include_bias)
     a = _right_multiply(a.float(), U_A.float())
     g = _right_multiply(g.float(), U_G.float())
@@ -252,16 +286,31 @@ def ekfac_materialize(
     )
 
 
-def _ekfac_rotate_materialized(block, layer_type, U_A, U_G):  # noqa: N803
-    """``vec(U_G^T dW U_A)`` per row of a linear ``(B, d_out*d_in)`` block
-    (kronecker.py:323-354), as two fp32 GEMMs."""
-    if U_A.ndim == 3 or is_conv_transpose(layer_type):
-        raise NotImplementedError("grouped / conv-transpose bases are conv-only and outside this path")
+def _t(u: torch.Tensor) -> torch.Tensor:
+    """fp32 transpose of the last two axes, as a contiguous operand."""
+    return u.float().transpose(-1, -2).contiguous()
+
+
+def _layout(block: torch.Tensor, layer_type: str, U_A: torch.Tensor, U_G: torch.Tensor):  # noqa: N803
+    """The rows of a materialized block as matrices, and the bases on their
+    left and right: linear and conv blocks are ``(d_out, d_in)``-major (U_G on
+    the left), conv-transpose blocks ``(C_in, P)``-major (U_A on the left); a
+    grouped block holds one such matrix per group (materialize.py:100-114)."""
+    left, right = (U_A, U_G) if is_conv_transpose(layer_type) else (U_G, U_A)
     batch = block.shape[0]
-    d_out, d_in = U_G.shape[0], U_A.shape[0]
-    d_w = block.reshape(batch, d_out, d_in).float()
-    m = torch.matmul(U_G.float().t().contiguous(), d_w) @ U_A.float()
-    return m.reshape(batch, d_out * d_in)
+    if U_A.ndim == 3:
+        shape = (batch, U_A.shape[0], left.shape[-2], right.shape[-2])
+    else:
+        shape = (batch, left.shape[-2], right.shape[-2])
+    return block.reshape(shape).float(), left.float(), right.float()
+
+
+def _ekfac_rotate_materialized(block, layer_type, U_A, U_G):  # noqa: N803
+    """``vec(U_G^T dW U_A)`` per row of a materialized ``(B, D)`` block
+    (kronecker.py:323-354; ``U_A^T dW U_G`` for a conv-transpose block, per
+    group for a grouped one), as two fp32 GEMMs."""
+    d_w, left, right = _layout(block, layer_type, U_A, U_G)
+    return (torch.matmul(_t(left), d_w) @ right).reshape(block.shape[0], -1)
 
 
 def kfac_precondition(
@@ -274,7 +323,7 @@ def kfac_precondition(
     """The preprocessed ``(a @ A^-1, g @ G^-1)`` of one side (kronecker.py:357-383):
     a cross-gram of these against a raw side equals :func:`kfac_cross`."""
     bf = f.as_batch_first()
-    _require_kfac_linear(layer_type)
+    _require_kfac_eligible(layer_type)
     a, g = preprocess_factors(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
                               include_bias)
     return _right_multiply(a.float(), A_inv.float()), _right_multiply(g.float(), G_inv.float())
@@ -282,24 +331,19 @@ def kfac_precondition(
 
 def kfac_precondition_materialized(block, A_inv, G_inv):  # noqa: N803
     """``vec(G^-1 dW A^-1)`` per row of a ``(B, k_g*k_a)`` block (kronecker.py:386-410)."""
-    if A_inv.ndim == 3:
-        raise NotImplementedError("per-group inverses are conv-only and outside this path")
     batch = block.shape[0]
     k_g, k_a = G_inv.shape[-1], A_inv.shape[-1]
-    d_w = block.reshape(batch, k_g, k_a).float()
-    return (torch.matmul(G_inv.float(), d_w) @ A_inv.float()).reshape(batch, k_g * k_a)
+    shape = (batch, A_inv.shape[0], k_g, k_a) if A_inv.ndim == 3 else (batch, k_g, k_a)
+    d_w = block.reshape(shape).float()
+    return (torch.matmul(G_inv.float(), d_w) @ A_inv.float()).reshape(batch, -1)
 
 
 def ekfac_precondition(M, U_A, U_G, lam, layer_type: str):  # noqa: N803
     """``U_G (M / lam) U_A^T`` back in the original basis, flattened like
-    :func:`materialize_factors` (kronecker.py:413-458)."""
-    if U_A.ndim == 3 or is_conv_transpose(layer_type):
-        raise NotImplementedError("grouped / conv-transpose bases are conv-only and outside this path")
-    md = M / lam
-    d_out, d_in = U_G.shape[0], U_A.shape[0]
-    m3 = md.reshape(M.shape[0], d_out, d_in).float()
-    r = torch.matmul(U_G.float(), m3) @ U_A.float().t().contiguous()
-    return r.reshape(M.shape[0], d_out * d_in)
+    :func:`materialize_factors` (kronecker.py:413-458; ``U_A (M / lam) U_G^T``
+    for a conv-transpose block, per group for a grouped one)."""
+    m3, left, right = _layout(M / lam, layer_type, U_A, U_G)
+    return (torch.matmul(left, m3) @ _t(right)).reshape(M.shape[0], -1)
 
 
 def _all_reduce_sum(t: torch.Tensor) -> torch.Tensor:
@@ -321,7 +365,10 @@ def _accumulate_gram(acc: torch.Tensor | None, x: torch.Tensor) -> torch.Tensor:
     zero fill), else added into ``acc`` -- in the kernel's epilogue for 16-bit
     rows."""
     if acc is None:
-        return row_gram(x)
+        return _grams(x)
+    if x.ndim == 3:
+        acc += _grams(x)
+        return acc
     if x.dtype in (torch.bfloat16, torch.float16) and acc.dtype == torch.float32 and acc.is_contiguous():
         kernels.row_gram(x, out=acc, accumulate=True)
     else:
@@ -340,7 +387,8 @@ class LayerKroneckerAccumulator:
     def update(self, a, g, layer_type: str, module_kwargs: dict | None = None, include_bias: bool = True):
         a, g = preprocess_factors(a, g, layer_type, module_kwargs, include_bias)
         a_f, g_f = _flatten_for_kfac(a, g, layer_type)
-        a_f, g_f = _drop_gradient_free_rows(a_f, g_f)
+        if _sequence_rows(layer_type):
+            a_f, g_f = _drop_gradient_free_rows(a_f, g_f)
         self._A = _accumulate_gram(self._A, a_f)
         self._G = _accumulate_gram(self._G, g_f)
         self._n += a_f.shape[-2]

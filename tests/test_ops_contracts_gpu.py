@@ -1,6 +1,8 @@
-"""The reference's op-contract tests (tests/gradient/test_ops.py:428-524,
+"""The reference's op-contract tests (tests/gradient/test_ops.py:340-524,
 :778-1080) on the MI355X path, at its shapes (B=4, T=6, D_IN=8, D_OUT=12) and
-tolerances: streaming accumulators equal one-shot K-FAC / Fisher factors,
+tolerances: K-FAC / Fisher shapes (linear and convolution layers), the
+norm / embedding refusals and the gradient-free rows (dropped for sequence
+layers, kept for convolutions), streaming accumulators equal one-shot K-FAC / Fisher factors,
 token collapse of norm gradients, the multi-layer accumulators and the
 Fisher size cap, the Factorized wrappers (and sequence-first captures), the
 damped inverses, per-token cross-grams summing to the full one, the outer
@@ -276,3 +278,65 @@ def test_projection_matrix_matches_apply(device, include_bias):
     assert resolved(x).shape == (2, 5, 8)
     assert not resolved.matches(torch.randn(2, 5, 13, device=device))
     assert not resolved.matches(torch.randn(2, 5, 12, dtype=torch.float64, device=device))
+
+
+# -- K-FAC shapes and gradient-free rows (test_ops.py:340-425) ----------------------------------
+
+
+@pytest.mark.parametrize("lt,shape", [("nn.Linear", "2d"), ("nn.Linear", "3d"), ("nn.Conv1d", "3d"),
+                                      ("nn.ConvTranspose1d", "3d")])
+def test_kfac_and_fim_shapes(device, gen, lt, shape):
+    from dattri_llm_amd.gradient import ops
+
+    a, g = (_linear_2d if shape == "2d" else _linear_3d)(gen, device)
+    A, G = ops.kfac_factors(a, g, lt)
+    assert A.shape == (D_IN, D_IN) and G.shape == (D_OUT, D_OUT)
+    F = ops.fim_factors(a, g, lt)
+    assert F.dim() == 2 and F.shape[0] == F.shape[1] == D_IN * D_OUT
+
+
+@pytest.mark.parametrize("lt", ["nn.LayerNorm", "nn.Embedding"])
+def test_kfac_not_implemented(device, gen, lt):
+    from dattri_llm_amd.gradient import ops
+
+    a, g = _norm_3d(gen, device) if "Norm" in lt else _embedding(gen, device)
+    with pytest.raises(NotImplementedError):
+        ops.kfac_factors(a, g, lt)
+
+
+def _padded(device):
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn(B, 5, D_IN, generator=gen)
+    g = torch.randn(B, 5, D_OUT, generator=gen)
+    g[:, 3:] = 0.0
+    return _on(device, a, g)
+
+
+def test_kfac_gradient_free_rows(device):
+    """Sequence layers drop rows with an all-zero gradient from the factors and
+    the count; a convolution keeps them (its zeros are architectural)."""
+    from dattri_llm_amd.gradient import ops
+
+    a, g = _padded(device)
+    A_pad, G_pad = ops.kfac_factors(a, g, "nn.Linear")
+    A_ref, G_ref = ops.kfac_factors(a[:, :3].contiguous(), g[:, :3].contiguous(), "nn.Linear")
+    assert torch.allclose(A_pad, A_ref, atol=1e-6) and torch.allclose(G_pad, G_ref, atol=1e-6)
+    acc = ops.LayerKroneckerAccumulator()
+    acc.update(a, g, "nn.Linear")
+    A_s, G_s = acc.result()
+    assert torch.allclose(A_s, A_pad, atol=1e-6) and torch.allclose(G_s, G_pad, atol=1e-6)
+    a_long = torch.cat([a, torch.randn(B, 4, D_IN, device=device)], dim=1)
+    g_long = torch.cat([g, torch.zeros(B, 4, D_OUT, device=device)], dim=1)
+    A2, G2 = ops.kfac_factors(a_long, g_long, "nn.Linear")
+    assert torch.allclose(A_pad, A2, atol=1e-6) and torch.allclose(G_pad, G2, atol=1e-6)
+    # a convolution's rows all count
+    A_c, _G_c = ops.kfac_factors(a, g, "nn.Conv1d")
+    a64 = a.double().reshape(-1, D_IN)
+    assert torch.allclose(A_c.double(), a64.T @ a64 / a64.shape[0], atol=1e-5)
+    zeros = torch.zeros(B, 3, D_OUT, device=device)
+    with pytest.raises(ValueError, match="zero"):
+        ops.kfac_factors(a[:, :3].contiguous(), zeros, "nn.Linear")
+    acc = ops.LayerKroneckerAccumulator()
+    acc.update(a[:, :3].contiguous(), zeros, "nn.Linear")
+    with pytest.raises(RuntimeError, match="gradient-carrying"):
+        acc.result()
