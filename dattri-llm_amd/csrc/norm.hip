@@ -31,12 +31,13 @@ struct NormArgs {
   const char* x;
   const char* g;
   int64_t batch, tokens, d;
+  int64_t dp;                                          // d rounded up to whole 16-byte chunks
   int64_t x_bstride, x_tstride, g_bstride, g_tstride;  // bytes
   int kind;                                            // 0 RMSNorm, 1 LayerNorm, 2 as given
   float eps;
   int has_bias;
   int64_t chunks;                                      // token chunks per sample
-  float* partial;                                      // [batch][chunks][(1+bias)*d]
+  float* partial;                                      // [batch][chunks][(1+bias)*dp]
 };
 
 template <int DT>
@@ -52,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
 
   const int64_t b = blockIdx.y, chunk = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t nchunk16 = a.d / VEC;  // 16-byte chunks per row
+  const int64_t nchunk16 = a.dp / VEC;  // 16-byte chunks per row; elements past d are masked
   const float inv_d = 1.f / (float)a.d;
 
   float dg[kQ][VEC], db[kBias ? kQ : 1][VEC];
@@ -84,15 +85,18 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
 #pragma unroll
       for (int q = 0; q < kQ; ++q)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) s += elem_of<DT>(vx[q], e);
+        for (int e = 0; e < VEC; ++e) {
+          const bool in = (lane + (int64_t)q * kWave) * VEC + e < a.d;
+          s += in ? elem_of<DT>(vx[q], e) : 0.f;
+        }
       mean = wave_sum(s) * inv_d;
     }
     float ss = 0.f;
 #pragma unroll
     for (int q = 0; q < kQ; ++q) {
-      const bool in = lane + (int64_t)q * kWave < nchunk16;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
+        const bool in = (lane + (int64_t)q * kWave) * VEC + e < a.d;
         const float c = in ? elem_of<DT>(vx[q], e) - mean : 0.f;
         ss += c * c;
       }
@@ -106,7 +110,8 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
     for (int q = 0; q < kQ; ++q)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const float gv = elem_of<DT>(vg[q], e);
+        const bool in = (lane + (int64_t)q * kWave) * VEC + e < a.d;
+        const float gv = in ? elem_of<DT>(vg[q], e) : 0.f;
         dg[q][e] += (elem_of<DT>(vx[q], e) - mean) * rstd * gv;
         if constexpr (kBias) db[q][e] += gv;
       }
@@ -114,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
 
   // Combine waves one at a time through LDS (one wave's sums fit), then wave 0
   // writes the workgroup's partial.
-  const int64_t width = (1 + a.has_bias) * a.d;
+  const int64_t width = (1 + a.has_bias) * a.dp;
   for (int w = 1; w < kWaves; ++w) {
     if (wave == w) {
 #pragma unroll
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
             lds[c * VEC + e] = dg[q][e];
-            if constexpr (kBias) lds[a.d + c * VEC + e] = db[q][e];
+            if constexpr (kBias) lds[a.dp + c * VEC + e] = db[q][e];
           }
       }
     }
@@ -137,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
             dg[q][e] += lds[c * VEC + e];
-            if constexpr (kBias) db[q][e] += lds[a.d + c * VEC + e];
+            if constexpr (kBias) db[q][e] += lds[a.dp + c * VEC + e];
           }
       }
     }
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void norm_grad_chunks(NormArgs a) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
           dst[c * VEC + e] = dg[q][e];
-          if constexpr (kBias) dst[a.d + c * VEC + e] = db[q][e];
+          if constexpr (kBias) dst[a.dp + c * VEC + e] = db[q][e];
         }
     }
   }
@@ -202,7 +207,7 @@ __global__ __launch_bounds__(ring_waves(kQ) * kWave, 1) void norm_grad_ring(Norm
   const int64_t b = blockIdx.y, chunk = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int uwave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t nchunk16 = a.d / VEC;
+  const int64_t nchunk16 = a.d / VEC;  // the host sends only widths of whole chunks here (dp == d)
   const float inv_d = 1.f / (float)a.d;
   const u32x4 rx = make_rsrc(a.x + b * a.x_bstride, (uint32_t)(a.tokens * a.x_tstride));
   const u32x4 rg = make_rsrc(a.g + b * a.g_bstride, (uint32_t)(a.tokens * a.g_tstride));
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(ring_waves(kQ) * kWave, 1) void norm_grad_ring(Norm
   __syncthreads();  // every wave is done with its slots before they hold the combine buffer
 
   // Combine the waves in order 0 + 1 + ... through LDS, then wave 0 writes.
-  const int64_t width = (1 + a.has_bias) * a.d;
+  const int64_t width = (1 + a.has_bias) * a.dp;
   for (int w = 1; w < NW; ++w) {
     if (uwave == w) {
 #pragma unroll
@@ -362,11 +367,13 @@ __global__ __launch_bounds__(ring_waves(kQ) * kWave, 1) void norm_grad_ring(Norm
 // eight interleaved accumulators run in chunk order and are added in a fixed
 // tree, and the four group sums are added as (g0 + g1) + (g2 + g3).  The same
 // order on every call.  A lane owns four consecutive features (16-byte loads);
-// a workgroup covers 64 feature quads of one sample.
+// a workgroup covers 64 feature quads of one sample.  The partials hold each
+// block of d features at a pitch of dp (a multiple of 4): feature f of block
+// k = f / dp lands at out index k * d + f % dp when f % dp < d.
 template <int OT>
 __global__ __launch_bounds__(256) void norm_grad_reduce(const float* __restrict__ partial, int64_t batch,
-                                                        int64_t chunks, int64_t width, char* out,
-                                                        int64_t out_bstride) {
+                                                        int64_t chunks, int64_t width, int64_t d, int64_t dp,
+                                                        char* out, int64_t out_bstride) {
   __shared__ f32x4 red[3][64];
   const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int64_t f = ((int64_t)blockIdx.x * 64 + lane) * 4;
@@ -391,8 +398,10 @@ __global__ __launch_bounds__(256) void norm_grad_reduce(const float* __restrict_
   __syncthreads();
   if (grp == 0 && f < width) {
     const f32x4 t = (s + red[0][lane]) + (red[1][lane] + red[2][lane]);
+    const int64_t k = f / dp, j = f - k * dp;  // dp % 4 == 0: the quad stays in one block
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Elem<OT>::store(out, b * out_bstride + f + e, t[e]);
+    for (int e = 0; e < 4; ++e)
+      if (j + e < d) Elem<OT>::store(out, b * out_bstride + k * d + j + e, t[e]);
   }
 }
 
@@ -405,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int64_t nchunk16 = d / VEC;
+  const int64_t nchunk16 = (d + VEC - 1) / VEC;  // whole chunks are read; elements past d are masked
   const float inv_d = 1.f / (float)d;
   float xv[kQ][VEC];
 #pragma unroll
@@ -420,15 +429,15 @@ __global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_
 #pragma unroll
     for (int q = 0; q < kQ; ++q)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) s += xv[q][e];
+      for (int e = 0; e < VEC; ++e) s += (lane + (int64_t)q * kWave) * VEC + e < d ? xv[q][e] : 0.f;
     mean = wave_sum(s) * inv_d;
   }
   float ss = 0.f;
 #pragma unroll
   for (int q = 0; q < kQ; ++q) {
-    const bool in = lane + (int64_t)q * kWave < nchunk16;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
+      const bool in = (lane + (int64_t)q * kWave) * VEC + e < d;
       const float c = in ? xv[q][e] - mean : 0.f;
       ss += c * c;
     }
@@ -437,29 +446,127 @@ __global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_
 #pragma unroll
   for (int q = 0; q < kQ; ++q) {
     const int64_t c = lane + (int64_t)q * kWave;
-    if (c < nchunk16)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e)
-        Elem<OT>::store(out, row * out_rstride + c * VEC + e, (xv[q][e] - mean) * rstd);
+    for (int e = 0; e < VEC; ++e)
+      if (c * VEC + e < d) Elem<OT>::store(out, row * out_rstride + c * VEC + e, (xv[q][e] - mean) * rstd);
+  }
+}
+
+// Rows wider than the register forms hold (more than 16 chunks per lane): one
+// wave per 32-row token chunk walks each row three times from L2 -- the sum,
+// the squared deviations, then x_hat * g added into the chunk's partial row,
+// which this wave alone owns (its first row writes it, later rows add), so no
+// barrier and no zero fill.  Same fixed orders as the register forms.
+template <int DT, bool kBias>
+__global__ __launch_bounds__(kWave) void norm_grad_wide(NormArgs a) {
+  constexpr int VEC = Elem<DT>::kVec;
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.y, chunk = blockIdx.x;
+  const int64_t nchunk16 = a.dp / VEC;
+  const float inv_d = 1.f / (float)a.d;
+  float* dst = a.partial + (b * a.chunks + chunk) * (1 + a.has_bias) * a.dp;
+  const int64_t t_begin = chunk * kRowsPerWG;
+  const int64_t t_end = min(t_begin + kRowsPerWG, a.tokens);
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    const char* xr = a.x + b * a.x_bstride + t * a.x_tstride;
+    const char* gr = a.g + b * a.g_bstride + t * a.g_tstride;
+    float mean = 0.f;
+    if (a.kind == 1) {
+      float s = 0.f;
+      for (int64_t c = lane; c < nchunk16; c += kWave) {
+        const u32x4 v = ld16(xr + c * 16);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += c * VEC + e < a.d ? elem_of<DT>(v, e) : 0.f;
+      }
+      mean = wave_sum(s) * inv_d;
+    }
+    float ss = 0.f;
+    for (int64_t c = lane; c < nchunk16; c += kWave) {
+      const u32x4 v = ld16(xr + c * 16);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float dv = c * VEC + e < a.d ? elem_of<DT>(v, e) - mean : 0.f;
+        ss += dv * dv;
+      }
+    }
+    const float rstd = a.kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + a.eps);
+    const bool first = t == t_begin;
+    for (int64_t c = lane; c < nchunk16; c += kWave) {
+      const u32x4 vx = ld16(xr + c * 16), vg = ld16(gr + c * 16);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t f = c * VEC + e;
+        const float gv = f < a.d ? elem_of<DT>(vg, e) : 0.f;
+        const float dg = (elem_of<DT>(vx, e) - mean) * rstd * gv;
+        dst[f] = first ? dg : dst[f] + dg;
+        if constexpr (kBias) dst[a.dp + f] = first ? gv : dst[a.dp + f] + gv;
+      }
+    }
+  }
+}
+
+// x_hat of rows wider than the register form holds: one wave per row, three
+// passes from L2.
+template <int DT, int OT>
+__global__ __launch_bounds__(kThreads) void norm_xhat_wide(const char* x, int64_t rows, int64_t d,
+                                                           int64_t x_rstride, int kind, float eps,
+                                                           char* out, int64_t out_rstride) {
+  constexpr int VEC = Elem<DT>::kVec;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t nchunk16 = (d + VEC - 1) / VEC;
+  const float inv_d = 1.f / (float)d;
+  const char* xr = x + row * x_rstride;
+  float mean = 0.f;
+  if (kind == 1) {
+    float s = 0.f;
+    for (int64_t c = lane; c < nchunk16; c += kWave) {
+      const u32x4 v = ld16(xr + c * 16);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += c * VEC + e < d ? elem_of<DT>(v, e) : 0.f;
+    }
+    mean = wave_sum(s) * inv_d;
+  }
+  float ss = 0.f;
+  for (int64_t c = lane; c < nchunk16; c += kWave) {
+    const u32x4 v = ld16(xr + c * 16);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float dv = c * VEC + e < d ? elem_of<DT>(v, e) - mean : 0.f;
+      ss += dv * dv;
+    }
+  }
+  const float rstd = kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
+  for (int64_t c = lane; c < nchunk16; c += kWave) {
+    const u32x4 v = ld16(xr + c * 16);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e)
+      if (c * VEC + e < d) Elem<OT>::store(out, row * out_rstride + c * VEC + e, (elem_of<DT>(v, e) - mean) * rstd);
   }
 }
 
 int pick_q(int64_t d, int64_t vec) {
-  const int64_t per_lane = (d / vec + kWave - 1) / kWave;
+  const int64_t per_lane = ((d + vec - 1) / vec + kWave - 1) / kWave;
   if (per_lane <= 1) return 1;
   if (per_lane <= 2) return 2;
   if (per_lane <= 4) return 4;
   if (per_lane <= 8) return 8;
   if (per_lane <= 16) return 16;
-  return -1;
+  return 0;  // the wide form
 }
 
 template <int DT, int OT>
 int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t st) {
-  const int64_t width = (1 + a.has_bias) * a.d;
-  // The ring form addresses a sample's rows with 32-bit buffer offsets.
+  const int64_t width = (1 + a.has_bias) * a.dp;
+  // The ring form addresses a sample's rows with 32-bit buffer offsets and
+  // takes rows of whole 16-byte chunks.
   const int64_t max_ts = a.x_tstride > a.g_tstride ? a.x_tstride : a.g_tstride;
-  if (q <= 8 && a.tokens * max_ts < (1LL << 31)) {
+  if (q == 0) {
+    dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
+    if (a.has_bias) norm_grad_wide<DT, true><<<grid, kWave, 0, st>>>(a);
+    else norm_grad_wide<DT, false><<<grid, kWave, 0, st>>>(a);
+  } else if (q <= 8 && a.tokens * max_ts < (1LL << 31) && a.dp == a.d) {
     a.chunks = (a.tokens + kRingRowsPerWG - 1) / kRingRowsPerWG;
     dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
 #define DA_NORM_RING(Q)                                       \
@@ -494,7 +601,7 @@ int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t 
   int rc = check_launch("da_norm_weight_grad(chunks)");
   if (rc) return rc;
   dim3 g2((unsigned)((width / 4 + 63) / 64), (unsigned)a.batch);
-  norm_grad_reduce<OT><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, (char*)out,
+  norm_grad_reduce<OT><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, a.d, a.dp, (char*)out,
                                            out_bstride);
   return check_launch("da_norm_weight_grad(reduce)");
 }
@@ -504,6 +611,11 @@ int launch_xhat(const void* x, int64_t rows, int64_t d, int64_t x_rstride, int k
                 void* out, int64_t out_rstride, int q, hipStream_t st) {
   const unsigned blocks = (unsigned)((rows + kWaves - 1) / kWaves);
   const int64_t xs = x_rstride * Elem<DT>::kBytes;
+  if (q == 0) {
+    norm_xhat_wide<DT, OT><<<blocks, kThreads, 0, st>>>((const char*)x, rows, d, xs, kind, eps, (char*)out,
+                                                        out_rstride);
+    return check_launch("da_norm_xhat");
+  }
 #define DA_XHAT_Q(Q)                                                                       \
   norm_xhat_rows<DT, OT, Q><<<blocks, kThreads, 0, st>>>((const char*)x, rows, d, xs, kind, \
                                                          eps, (char*)out, out_rstride)
@@ -524,13 +636,8 @@ int check_common(const char* who, int dtype, int out_dtype, int64_t d, int kind,
   if (kind < 0 || kind > 2)
     return set_error(DA_ERR_INVALID, "%s: kind must be 0 (RMSNorm), 1 (LayerNorm) or 2 (normalised)", who);
   const int64_t vec = 16 / (int64_t)elem_bytes(dtype);
-  if (d <= 0 || d % vec)
-    return set_error(DA_ERR_INVALID, "%s: d=%lld must be a positive multiple of %lld", who,
-                     (long long)d, (long long)vec);
+  if (d <= 0) return set_error(DA_ERR_INVALID, "%s: d=%lld must be positive", who, (long long)d);
   *q = pick_q(d, vec);
-  if (*q < 0)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: d=%lld exceeds %lld features per row", who,
-                     (long long)d, (long long)(vec * kWave * 16));
   return DA_OK;
 }
 
@@ -544,7 +651,8 @@ int da_norm_weight_grad_workspace(int64_t batch, int64_t tokens, int64_t d, int 
   if (batch < 0 || tokens < 0 || d < 0 || !bytes)
     return da::set_error(DA_ERR_INVALID, "da_norm_weight_grad_workspace: bad arguments");
   const int64_t chunks = (tokens + da::kRowsPerWG - 1) / da::kRowsPerWG;
-  *bytes = (size_t)(batch * chunks * (1 + (has_bias ? 1 : 0)) * d) * sizeof(float);
+  const int64_t dp = (d + 7) / 8 * 8;  // whole 16-byte chunks of the narrowest element (2 bytes)
+  *bytes = (size_t)(batch * chunks * (1 + (has_bias ? 1 : 0)) * dp) * sizeof(float);
   return DA_OK;
 }
 
@@ -578,6 +686,7 @@ int da_norm_weight_grad(const void* x, const void* g, int dtype, int64_t batch, 
   a.batch = batch;
   a.tokens = tokens;
   a.d = d;
+  a.dp = (d + 16 / es - 1) / (16 / es) * (16 / es);
   a.x_bstride = x_bstride * es;
   a.x_tstride = x_tstride * es;
   a.g_bstride = g_bstride * es;

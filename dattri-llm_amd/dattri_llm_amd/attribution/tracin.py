@@ -110,11 +110,12 @@ class TracInAttributor:
         return dot if self._metric == "dot" else self._cosine(dot, train_rep, test_rep, layers)
 
     def attribute_sources(self, train_source, test_source, *, normalized_grad: bool = False,
-                          batch_size: int | None = None,
+                          batch_size: int | None = None, loop_over_test: bool = False,
                           attribution_granularity: str = "instance") -> AttributionScore:
         """Score two ``(step, Gradient, hashes)`` sources (base.py:704-770);
-        ``attribution_granularity="token"`` gives one row per training token
-        position (:meth:`inner_product_per_token`)."""
+        ``loop_over_test`` re-streams a reusable test source per train block
+        instead of caching it; ``attribution_granularity="token"`` gives one row
+        per training token position (:meth:`inner_product_per_token`)."""
         self._set_metric(normalized_grad)
         # The loop allocates many small objects per block; with the cyclic
         # collector running it rescans the whole heap over and over (measured:
@@ -126,7 +127,7 @@ class TracInAttributor:
             scores, row_ids, row_steps, test_ids, row_tokens = score_sources(
                 train_source, test_source, self.device, inner_product=self.inner_product,
                 transform_test=self.route_test_rep, batch_size=batch_size or self.train_batch_size,
-                granularity=attribution_granularity, inner_product_per_token=self.inner_product_per_token,
+                loop_over_test=loop_over_test, granularity=attribution_granularity, inner_product_per_token=self.inner_product_per_token,
             )
             return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
                                     algorithm=self.algorithm,

@@ -29,12 +29,15 @@ def finalize_factors(rep: Gradient, *, budget: CacheBudget | None = None, held: 
 
     Linear layers need no rewrite here: their bias column is applied inside
     the kernels (an implicit ones column), so the raw capture *is* the final
-    form and keeping ``module_kwargs`` costs nothing.  Token-norm layers are
-    replaced by their final factors (x_hat, with the bias block) exactly as
-    the reference does, under the same budget rule."""
+    form and keeping ``module_kwargs`` costs nothing.  Norm layers (x_hat,
+    with the bias block) and convolutions (the unfolded patches, with the ones
+    column) are replaced by their final factors exactly as the reference does,
+    under the same budget rule; embeddings stay raw."""
     names = [
         n for n, v in rep.data.items()
-        if isinstance(v, Factorized) and v.module_kwargs is not None and ops.is_norm(rep.layer_types[n])
+        if isinstance(v, Factorized) and v.module_kwargs is not None
+        and (ops.is_norm(rep.layer_types[n]) or ops.is_conv(rep.layer_types[n])
+             or ops.is_conv_transpose(rep.layer_types[n]))
     ]
     if not names:
         return rep
@@ -108,12 +111,21 @@ def score_sources(
     transform_train: Callable | None = None,
     transform_test: Callable | None = None,
     batch_size: int = 1,
+    loop_over_test: bool = False,
     cache_budget: CacheBudget | None = None,
     granularity: str = "instance",
     inner_product_per_token: Callable | None = None,
 ):
-    """Score every train block against every cached test block
-    (utils.py:239-440, cached test side).
+    """Score every train block against every test block (utils.py:239-440).
+
+    The test source is iterated once to fix the column order (first-seen
+    hashes) and, by default, to cache the transformed test blocks, merged
+    into one block when they are all dense.  With ``loop_over_test`` nothing
+    is cached: the test source (which must be ``reusable``) is re-streamed
+    and re-transformed for every train block, and train blocks are scored one
+    at a time.  The dense cache handed to ``inner_product`` lives for one
+    train block; it is ``None`` when a cached train block meets a single
+    test block.
 
     ``granularity="instance"`` gives one row per training sample;
     ``"token"`` one row per training token position, scored by
@@ -122,6 +134,10 @@ def score_sources(
 
     Returns ``(scores (rows, num_test) fp32 CPU, row_train_ids, row_steps,
     test_ids, row_token_ids or None)``."""
+    if loop_over_test and not getattr(test_source, "reusable", False):
+        raise ValueError(
+            "loop_over_test=True requires a re-iterable test source (reusable=True); got a single-shot source.",
+        )
     if granularity not in {"instance", "token"}:
         raise ValueError(f"granularity must be 'instance' or 'token', got {granularity!r}.")
     per_token = granularity == "token"
@@ -140,12 +156,28 @@ def score_sources(
                 index[h] = len(test_ids)
                 test_ids.append(h)
             cols.append(index[h])
-        cached.append((transform_test(test_g.to(device)), cols))
+        if not loop_over_test:
+            cached.append((transform_test(test_g.to(device)), cols))
+    test_g = None  # the last raw test block is not kept beside its transformed copy
     cached = _merge_dense_test(cached)
     num_test = len(test_ids)
     # a dense copy of the train block pays off only against several test blocks,
     # and only the instance-level kernel materializes the train side
-    reuse = len(cached) > 1 and not per_token
+    reuse = loop_over_test or (len(cached) > 1 and not per_token)
+
+    def test_blocks():
+        if not loop_over_test:
+            yield from cached
+            return
+        for _s, tg, hashes in test_source:
+            yield transform_test(tg.to(device)), [index[h] for h in hashes]
+
+    def train_blocks():
+        if not loop_over_test:
+            yield from rebatch_blocks(train_source, batch_size)
+            return
+        for step, block, hashes in train_source:
+            yield [step] * block.batch_size, block, list(hashes)
 
     def n_rows(train_rep) -> int:
         if not per_token:
@@ -155,11 +187,11 @@ def score_sources(
 
     rows_out = _HostRows()
     row_ids, row_steps, row_tokens = [], [], []
-    for steps, train_g, ids in rebatch_blocks(train_source, batch_size):
+    for steps, train_g, ids in train_blocks():
         train_rep = transform_train(train_g.to(device))
         row = torch.zeros(n_rows(train_rep), num_test, dtype=torch.float32, device=device)
         cache = TensorCache("memory", budget=budget) if reuse else None
-        for test_rep, cols in cached:
+        for test_rep, cols in test_blocks():
             if per_token:
                 block = inner_product_per_token(train_rep, test_rep).to(torch.float32)
                 block = block.reshape(-1, block.shape[-1])

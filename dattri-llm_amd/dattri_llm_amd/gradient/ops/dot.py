@@ -77,10 +77,26 @@ def _route(b1: int, b2: int, s: int, k: int, d: int) -> str:
     return "materialized" if maybe_use_materialized_gram(b1, b2, s, k, d) else "factorized"
 
 
+def _explicit_bias(x: torch.Tensor) -> torch.Tensor:
+    """``x`` with its ones column appended (the preprocessed form of a bias)."""
+    return torch.cat([x, torch.ones_like(x[..., :1])], dim=-1)
+
+
+def _agree_bias(x1, bias1, x2, bias2):
+    """One layer's activation factors where one side still applies its bias
+    column implicitly (a raw capture) and the other holds it explicitly
+    (already preprocessed, utils.py:180-236): the implicit one is appended, so
+    both sides read the same K + 1 columns."""
+    if bias1 == bias2:
+        return x1, bias1, x2, bias2
+    if bias1:
+        return _explicit_bias(x1), False, x2, False
+    return x1, False, _explicit_bias(x2), False
+
+
 def _linear_gram32(a1, g1, bias1, a2, g2, bias2, mode, out=None, accumulate=False):
     """fp32 (B1, B2) cross-gram of linear factors with implicit bias columns."""
-    if bias1 != bias2:
-        raise ValueError("the two sides disagree on the bias column")
+    a1, bias1, a2, bias2 = _agree_bias(a1, bias1, a2, bias2)
     (a1, g1, a2, g2), _ = _kernel_operands(to_3d(a1), to_3d(g1), to_3d(a2), to_3d(g2))
     if a1.shape[-1] != a2.shape[-1] or g1.shape[-1] != g2.shape[-1]:
         raise ValueError("the two sides disagree on the layer widths")
@@ -167,12 +183,19 @@ def _is_conv_family(layer_type: str, a) -> bool:
 
 
 def _conv_pair(c1, c2):
+    """The two sides of one convolution, checked and with one bias form (a
+    raw side's implicit ones column made explicit against a preprocessed
+    side's)."""
     if c1.bias != c2.bias:
-        raise ValueError("the two sides disagree on the bias column")
+        if c1.bias:
+            c1 = conv.ConvFactors(_explicit_bias(c1.a), c1.g, False, c1.transpose)
+        else:
+            c2 = conv.ConvFactors(_explicit_bias(c2.a), c2.g, False, c2.transpose)
     if c1.groups != c2.groups or c1.a.dim() != c2.a.dim():
         raise ValueError(f"the two sides disagree on the group count ({c1.groups} vs {c2.groups})")
     if c1.a.shape[-1] != c2.a.shape[-1] or c1.g.shape[-1] != c2.g.shape[-1]:
         raise ValueError("the two sides disagree on the layer widths")
+    return c1, c2
 
 
 def _conv_operands(c):
@@ -193,7 +216,7 @@ def _conv_gram32(c1, c2, mode, out=None, accumulate=False):
     """fp32 (B1, B2) cross-gram of two convolution sides (dot.py:88-118): the
     ungrouped case is the linear layer's; groups pair with their own group
     only -- one grouped ghost launch over all groups, or each group's dW."""
-    _conv_pair(c1, c2)
+    c1, c2 = _conv_pair(c1, c2)
     if c1.groups == 1 and c1.a.dim() == 3:
         return _linear_gram32(c1.a, c1.g, c1.bias, c2.a, c2.g, c2.bias, mode, out=out, accumulate=accumulate)
     c1, c2 = _conv_operands(c1), _conv_operands(c2)
@@ -216,10 +239,10 @@ def _conv_gram32(c1, c2, mode, out=None, accumulate=False):
 
 def _conv_diag32(c1, c2) -> torch.Tensor:
     """fp32 (B,) per-sample dots (squared norms for one side with itself)."""
-    _conv_pair(c1, c2)
+    same = c1 is c2
+    c1, c2 = _conv_pair(c1, c2)
     if c1.a.shape[0] != c2.a.shape[0]:
         raise ValueError("per-sample dots need two blocks of one batch size")
-    same = c1 is c2
     c1 = _conv_operands(c1)
     c2 = c1 if same else _conv_operands(c2)
     out = torch.zeros(c1.a.shape[0], dtype=torch.float32, device=c1.a.device)
@@ -247,7 +270,7 @@ def _conv_norm32(c, mode) -> torch.Tensor:
 def _conv_per_token32(c1, c2) -> torch.Tensor:
     """fp32 (B1, T1, B2): side 1's location t against side 2's whole gradient,
     summed over the groups (dot.py:216-222)."""
-    _conv_pair(c1, c2)
+    c1, c2 = _conv_pair(c1, c2)
     c1, c2 = _conv_operands(c1), _conv_operands(c2)
     out = None
     for e in range(c1.groups):
@@ -358,8 +381,7 @@ def dot_factors(a1, g1, a2, g2, layer_type: str, module_kwargs1: dict | None = N
         (m1, m2), _ = _kernel_operands(_rows(s1), _rows(s2))
         return kernels.row_dots([(m1, m2)]).to(out_dtype)
     (x1, y1, bias1), (x2, y2, bias2) = s1, s2
-    if bias1 != bias2:
-        raise ValueError("the two sides disagree on the bias column")
+    x1, bias1, x2, bias2 = _agree_bias(x1, bias1, x2, bias2)
     (x1, y1, x2, y2), _ = _kernel_operands(to_3d(x1), to_3d(y1), to_3d(x2), to_3d(y2))
     return kernels.ghost_gram_diag(x1, y1, x2, y2, bias=bias1).to(out_dtype)
 
@@ -553,8 +575,7 @@ def _factorized_linear_pair(f1, f2, layer_type: str, mode: str, include_bias: bo
     x2, y2, bias2 = final_linear(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs, include_bias)
     if any(to_3d(t).ndim == 4 for t in (x1, y1, x2, y2)):
         return None
-    if bias1 != bias2:
-        raise ValueError("the two sides disagree on the bias column")
+    x1, bias1, x2, bias2 = _agree_bias(x1, bias1, x2, bias2)
     (x1, y1, x2, y2), _ = _kernel_operands(to_3d(x1), to_3d(y1), to_3d(x2), to_3d(y2))
     if x1.shape[-1] != x2.shape[-1] or y1.shape[-1] != y2.shape[-1]:
         raise ValueError("the two sides disagree on the layer widths")
@@ -658,8 +679,7 @@ def cross_dot_per_token(f1, f2, layer_type: str, include_bias: bool = True) -> t
         return kernels.dense_per_token(x1, y1, m2.reshape(m2.shape[0], -1), bias=bias1).to(out_dtype)
     b2 = f2.as_batch_first()
     x2, y2, bias2 = final_linear(b2.activation, b2.pre_activation_grad, layer_type, b2.module_kwargs, include_bias)
-    if bias1 != bias2:
-        raise ValueError("the two sides disagree on the bias column")
+    x1, bias1, x2, bias2 = _agree_bias(x1, bias1, x2, bias2)
     x1, y1, x2, y2 = _linear_operands(x1, y1, x2, y2)
     return kernels.ghost_gram_per_token(x1, y1, x2, y2, bias=bias1).to(out_dtype)
 

@@ -70,7 +70,7 @@ def norm_grad_from_final(a, g, fp32: bool = False):
     """Token sum ``(a * g).sum(1)`` of already-preprocessed norm factors
     (kept in fp32 with ``fp32``)."""
     (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
-    out = kernels.norm_weight_grad(ao, go, kind=2, eps=0.0, bias=False,
+    out = kernels.norm_weight_grad(ao, go, kind=kernels.NORM_KIND_GIVEN, eps=0.0, bias=False,
                                    out_dtype=torch.float32 if fp32 else dtypes.kernel_dtype(out_dtype))
     return out if fp32 else out.to(out_dtype)
 

@@ -836,6 +836,7 @@ def row_dots(layers: list, *, out: torch.Tensor | None = None, accumulate: bool 
 
 
 NORM_KIND = {"nn.RMSNorm": 0, "nn.LayerNorm": 1}
+NORM_KIND_GIVEN = 2  # x is already normalised: x_hat = x
 
 
 def norm_weight_grad(
@@ -862,11 +863,8 @@ def norm_weight_grad(
     if t == 0:
         return out.zero_()
     if d % _chunk_elems(x.dtype) or not (_aligned(x) and _aligned(g)):
-        x, g = x.contiguous(), g.contiguous()
-        if d % _chunk_elems(x.dtype) or not (_aligned(x) and _aligned(g)):
-            raise NotImplementedError(
-                f"norm_weight_grad: width {d} is not a multiple of {_chunk_elems(x.dtype)} elements"
-            )
+        # rows of whole 16-byte chunks; the kernels mask the padding
+        x, g = prepare_rows(x), prepare_rows(g)
     lib = nat.load()
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_norm_weight_grad_workspace(b, t, d, int(bias), ctypes.byref(nbytes)), "norm_weight_grad")
@@ -889,9 +887,7 @@ def norm_xhat(x: torch.Tensor, *, kind: int, eps: float, out_dtype: torch.dtype 
         return out
     flat = x.reshape(rows, d)
     if d % _chunk_elems(x.dtype) or not _aligned(flat):
-        flat = flat.contiguous()
-        if d % _chunk_elems(x.dtype) or not _aligned(flat):
-            raise NotImplementedError(f"norm_xhat: width {d} is not a multiple of {_chunk_elems(x.dtype)}")
+        flat = prepare_rows(flat)  # rows of whole 16-byte chunks; the kernel masks the padding
     _run(dev, "norm_xhat", nat.load().da_norm_xhat,
          flat.data_ptr(), nat.dtype_code(x.dtype), rows, d, flat.stride(0), int(kind), float(eps),
          out.data_ptr(), nat.dtype_code(out_dtype), d, nat.stream_ptr(dev))

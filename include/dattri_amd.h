@@ -429,7 +429,10 @@ int da_score_gemm_noalloc(int64_t b1, int64_t b2, const da_dense_layer* layers, 
  *   out[b*out_bstride + d + f] = sum_t g[b,t,f]                     (has_bias)
  *
  * eps is the caller's resolved epsilon (the reference's eps=None means the
- * activation dtype's machine epsilon, gradient/ops/norm.py:38-39).
+ * activation dtype's machine epsilon, gradient/ops/norm.py:38-39).  Rows start
+ * 16-byte aligned and are read in whole 16-byte chunks: when d is not a
+ * multiple of a chunk, the row stride must leave room for the last chunk,
+ * whose elements past d are read and ignored.
  * Replaces preprocess_factors' norm branches (dattri_llm/gradient/ops/preprocess.py:366-384,
  * norm.py:25-41, :95-110) followed by materialize_factors' token sum
  * (materialize.py:96-98).
@@ -446,6 +449,7 @@ int da_norm_weight_grad(const void* x, const void* g, int dtype, int64_t batch, 
  * Normalised rows x_hat of a token norm layer (the activation factor
  * preprocess_factors returns, dattri_llm/gradient/ops/norm.py:10-41):
  * x is (rows, d) with row stride x_rstride, out (rows, d) in out_dtype.
+ * Rows are read in whole 16-byte chunks, as for da_norm_weight_grad.
  */
 int da_norm_xhat(const void* x, int dtype, int64_t rows, int64_t d, int64_t x_rstride, int kind,
                  float eps, void* out, int out_dtype, int64_t out_rstride, void* stream);

@@ -84,6 +84,8 @@ CASES = [
     ("layernorm-bias", lambda: nn.LayerNorm(D_IN), _x(B, T, D_IN), None, "nn.LayerNorm", _flat_param),
     ("layernorm-2d", lambda: nn.LayerNorm(D_IN), _x(B, D_IN), None, "nn.LayerNorm", _flat_param),
     ("rmsnorm", lambda: nn.RMSNorm(D_IN), _x(B, T, D_IN), None, "nn.RMSNorm", _flat_param),
+    ("layernorm-width6", lambda: nn.LayerNorm(6), _x(B, T, 6), None, "nn.LayerNorm", _flat_param),
+    ("rmsnorm-width5", lambda: nn.RMSNorm(5), _x(B, 5), None, "nn.RMSNorm", _flat_param),
     ("qk-norm", _QKNorm, _x(B, T, 8), "ln", "nn.RMSNorm", _flat_param),
     ("groupnorm", lambda: nn.GroupNorm(2, 4), _x(B, 4, 3, 3), None, "nn.GroupNorm", _flat_param),
     ("instancenorm2d", lambda: nn.InstanceNorm2d(4, affine=True), _x(B, 4, 3, 3), None, "nn.InstanceNorm2d",

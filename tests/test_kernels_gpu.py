@@ -123,6 +123,11 @@ NORM_CASES = [
     (2, 64, 136, "nn.LayerNorm", True, 1e-5),
     (4, 1, 64, "nn.LayerNorm", False, 1e-5),
     (1, 300, 1024, "nn.RMSNorm", False, 1e-5),
+    # widths that end inside a 16-byte chunk: zero-padded rows, masked in the kernels
+    (3, 40, 6, "nn.LayerNorm", True, 1e-5),
+    (2, 33, 101, "nn.RMSNorm", False, 1e-6),
+    (2, 70, 4099, "nn.LayerNorm", False, 1e-5),  # fp32: past the register form, the wide form
+    (2, 37, 9000, "nn.LayerNorm", True, 1e-5),   # both dtypes in the wide form
 ]
 
 
@@ -146,11 +151,12 @@ def test_norm_weight_grad(device, dtype, case):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("lt", ["nn.RMSNorm", "nn.LayerNorm"])
-def test_norm_xhat(device, dtype, lt):
+@pytest.mark.parametrize("d", [256, 6, 203, 9001])
+def test_norm_xhat(device, dtype, lt, d):
     from dattri_llm_amd import kernels
 
     gen = torch.Generator().manual_seed(3)
-    x = _rand(gen, 3, 17, 256, dtype=dtype, scale=3.0)
+    x = _rand(gen, 3, 17, d, dtype=dtype, scale=3.0)
     fn = oracle.rms_x_hat if lt == "nn.RMSNorm" else oracle.layer_norm_x_hat
     got = kernels.norm_xhat(x.to(device), kind=kernels.NORM_KIND[lt], eps=1e-5, out_dtype=torch.float32)
     assert_parity(got, fn(_np(x), 1e-5), dtype)

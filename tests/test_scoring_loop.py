@@ -1,0 +1,240 @@
+"""The scoring loop's host logic on the CPU (the reference's
+tests/attribution/test_utils.py:229-556): score_sources over in-memory
+sources with an injected inner product -- column order by first-seen hash,
+row ids and steps, invariance to the train batch size, mixed dense /
+factorized streams, empty sources, the loop_over_test mode and its source
+requirement, the transforms, merged dense test blocks and the dense cache's
+scope -- and rebatch_blocks."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from dattri_llm_amd.attribution.utils import rebatch_blocks, score_sources
+from dattri_llm_amd.gradient.gradient import Factorized, Gradient
+from dattri_llm_amd.utils.cache import TensorCache
+
+B, T, D_IN, D_OUT = 2, 4, 3, 5
+
+
+def dense_block(seed=0, b=B):
+    g = torch.Generator().manual_seed(seed)
+    return Gradient({"l1": "materialized"}, {"l1": torch.randn(b, D_IN * D_OUT, generator=g)}, {"l1": "nn.Linear"})
+
+
+def factorized_block(seed=0, b=B):
+    g = torch.Generator().manual_seed(seed)
+    return Gradient({"l1": "factorized"},
+                    {"l1": Factorized(torch.randn(b, T, D_IN, generator=g), torch.randn(b, T, D_OUT, generator=g))},
+                    {"l1": "nn.Linear"}, {"l1": "batch_token"})
+
+
+def stream(n=4, factory=dense_block):
+    return [(i, factory(seed=i), [f"h{i}-{j}" for j in range(B)]) for i in range(n)]
+
+
+class Source:
+    """An in-memory (step, Gradient, hashes) source."""
+
+    def __init__(self, blocks, reusable=True):
+        self.blocks, self._reusable, self.passes = blocks, reusable, 0
+
+    def __iter__(self):
+        self.passes += 1
+        return iter(self.blocks)
+
+    @property
+    def reusable(self):
+        return self._reusable
+
+
+def flat(g):
+    v = g.data["l1"]
+    if isinstance(v, Factorized):
+        bf = v.as_batch_first()
+        return torch.einsum("bti,bto->boi", bf.activation, bf.pre_activation_grad).flatten(1)
+    return v
+
+
+def dot(train_rep, test_rep, *, dense_cache=None):
+    return flat(train_rep) @ flat(test_rep).T
+
+
+def sources(n_train=3, n_test=2, reusable=True):
+    train = Source(stream(n_train))
+    test = Source([(0, dense_block(seed=100 + i), [f"t{i}-0", f"t{i}-1"]) for i in range(n_test)], reusable=reusable)
+    return train, test
+
+
+def expected(train, test):
+    return torch.cat([flat(g) for _, g, _ in train.blocks]) @ torch.cat([flat(g) for _, g, _ in test.blocks]).T
+
+
+def test_scores_rows_and_columns():
+    train, test = sources()
+    scores, ids, steps, test_ids, tokens = score_sources(train, test, "cpu", inner_product=dot)
+    assert torch.allclose(scores, expected(train, test), atol=1e-6)
+    assert ids == [h for _, _, hs in train.blocks for h in hs]
+    assert test_ids == [h for _, _, hs in test.blocks for h in hs]
+    assert steps == [s for s, _g, _ in train.blocks for _ in range(B)]
+    assert tokens is None
+
+
+def test_columns_land_by_first_seen_hash():
+    train = Source([(0, dense_block(seed=0), ["r0", "r1"])])
+    a, b = dense_block(seed=1), dense_block(seed=2)
+    test = Source([(0, a, ["a0", "a1"]), (0, b, ["b0", "b1"])])
+    scores, _, _, test_ids, _ = score_sources(train, test, "cpu", inner_product=dot)
+    assert test_ids == ["a0", "a1", "b0", "b1"]
+    tg = train.blocks[0][1]
+    assert torch.allclose(scores[:, :2], flat(tg) @ flat(a).T)
+    assert torch.allclose(scores[:, 2:], flat(tg) @ flat(b).T)
+    # a hash seen again lands in its first column
+    test = Source([(0, a, ["a0", "a1"]), (0, b, ["a1", "b1"])])
+    scores, _, _, test_ids, _ = score_sources(train, test, "cpu", inner_product=dot)
+    assert test_ids == ["a0", "a1", "b1"]
+    assert torch.allclose(scores[:, 1], (flat(tg) @ flat(b).T)[:, 0])
+
+
+@pytest.mark.parametrize("batch_size", [1, 3, 100])
+def test_scores_and_rows_invariant_to_batch_size(batch_size):
+    train, test = sources(n_train=4, n_test=1)
+    scores, ids, steps, _, _ = score_sources(train, test, "cpu", inner_product=dot, batch_size=batch_size)
+    assert ids == [h for _, _, hs in train.blocks for h in hs]
+    assert steps == [s for s, g, _ in train.blocks for _ in range(g.batch_size)]
+    assert torch.allclose(scores, expected(train, test), atol=1e-6)
+
+
+def test_mixed_stream_stays_ordered():
+    train = Source([(0, dense_block(seed=0), ["m0-a", "m0-b"]), (1, factorized_block(seed=1), ["f1-a", "f1-b"]),
+                    (2, dense_block(seed=2), ["m2-a", "m2-b"])])
+    test = Source([(0, dense_block(seed=99, b=3), ["t0", "t1", "t2"])])
+    scores, ids, steps, _, _ = score_sources(train, test, "cpu", inner_product=dot, batch_size=100)
+    assert ids == ["m0-a", "m0-b", "f1-a", "f1-b", "m2-a", "m2-b"]
+    assert steps == [0, 0, 1, 1, 2, 2]
+    assert scores.shape == (6, 3)
+    assert torch.allclose(scores, expected(train, test), atol=1e-5)
+
+
+def test_empty_train_source():
+    train, test = sources(n_train=0, n_test=1)
+    scores, ids, steps, test_ids, _ = score_sources(train, test, "cpu", inner_product=dot)
+    assert scores.shape == (0, 2) and ids == [] and steps == [] and len(test_ids) == 2
+
+
+def test_loop_over_test_matches_cached():
+    train_a, test_a = sources()
+    cached = score_sources(train_a, test_a, "cpu", inner_product=dot)
+    train_b, test_b = sources()
+    looped = score_sources(train_b, test_b, "cpu", inner_product=dot, loop_over_test=True)
+    for got, want in zip(looped, cached, strict=True):
+        if isinstance(got, torch.Tensor):
+            assert torch.allclose(got, want, atol=1e-6)
+        else:
+            assert got == want
+    # cached: one pass over the test source; looping: the column pass plus one per train block
+    assert test_a.passes == 1
+    assert test_b.passes == 1 + len(train_b.blocks)
+
+
+def test_loop_over_test_requires_reusable_source():
+    train, test = sources(reusable=False)
+    with pytest.raises(ValueError, match="reusable"):
+        score_sources(train, test, "cpu", inner_product=dot, loop_over_test=True)
+
+
+def test_transforms_feed_inner_product():
+    train, test = sources(n_train=1, n_test=1)
+    seen = []
+    train_marker, test_marker = dense_block(seed=7), dense_block(seed=8)
+
+    def inner(train_rep, test_rep, *, dense_cache=None):
+        seen.append((train_rep, test_rep))
+        return torch.zeros(train_rep.batch_size, test_rep.batch_size)
+
+    score_sources(train, test, "cpu", inner_product=inner, transform_train=lambda g: train_marker,
+                  transform_test=lambda g: test_marker)
+    assert seen == [(train_marker, test_marker)]
+
+
+def test_dense_test_blocks_are_merged_into_one():
+    seen = []
+
+    def inner(train_rep, test_rep, *, dense_cache=None):
+        seen.append((test_rep.batch_size, dense_cache))
+        return dot(train_rep, test_rep)
+
+    train, test = sources(n_train=2, n_test=3)
+    scores, _, _, test_ids, _ = score_sources(train, test, "cpu", inner_product=inner)
+    assert seen == [(6, None), (6, None)]  # one merged 6-column block per train block
+    assert test_ids == [h for _, _, hs in test.blocks for h in hs]
+    assert torch.allclose(scores, expected(train, test), atol=1e-6)
+
+
+def test_dense_cache_is_scoped_to_the_train_block():
+    caches = []
+
+    def inner(train_rep, test_rep, *, dense_cache=None):
+        caches.append(dense_cache)
+        if dense_cache is not None:
+            dense_cache.get_or_compute("l1", lambda: flat(train_rep))
+        return dot(train_rep, test_rep)
+
+    train = Source(stream(2))
+    test = Source([(0, factorized_block(seed=100 + i), [f"t{i}-0", f"t{i}-1"]) for i in range(3)])
+    score_sources(train, test, "cpu", inner_product=inner)
+    assert all(isinstance(c, TensorCache) for c in caches)
+    assert len({id(c) for c in caches}) == 2
+    assert caches[0] is caches[1] is caches[2] and caches[3] is not caches[0]
+    caches.clear()
+    train, test = sources(n_train=2, n_test=1)
+    score_sources(train, test, "cpu", inner_product=inner)
+    assert caches == [None, None]
+
+
+def test_token_granularity_rows():
+    train = Source([(0, factorized_block(seed=0), ["r0", "r1"]), (1, factorized_block(seed=1), ["r2", "r3"])])
+    test = Source([(0, dense_block(seed=5), ["q0", "q1"])])
+
+    def per_token(train_rep, test_rep):
+        bf = train_rep.data["l1"].as_batch_first()
+        rows = torch.einsum("bti,bto->btoi", bf.activation, bf.pre_activation_grad).flatten(2)
+        return rows @ flat(test_rep).T
+
+    scores, ids, steps, _, tokens = score_sources(train, test, "cpu", inner_product=dot, granularity="token",
+                                                  inner_product_per_token=per_token)
+    assert scores.shape == (4 * T, 2)
+    assert ids == [h for h in ["r0", "r1", "r2", "r3"] for _ in range(T)]
+    assert steps == [0] * (2 * T) + [1] * (2 * T)
+    assert tokens == list(range(T)) * 4
+    # the token rows of a sample sum to its instance score
+    inst, *_ = score_sources(train, test, "cpu", inner_product=dot)
+    assert torch.allclose(scores.view(4, T, 2).sum(1), inst, atol=1e-5)
+    with pytest.raises(ValueError, match="inner_product_per_token"):
+        score_sources(train, test, "cpu", inner_product=dot, granularity="token")
+    with pytest.raises(ValueError, match="granularity"):
+        score_sources(train, test, "cpu", inner_product=dot, granularity="sentence")
+
+
+# -- rebatch_blocks (test_utils.py:229-272) ----------------------------------------------------
+
+
+def test_rebatch_at_boundary_and_remainder():
+    out = list(rebatch_blocks(stream(5), batch_size=4))
+    assert [len(ids) for _s, _g, ids in out] == [4, 4, 2]
+    assert [g.batch_size for _s, g, _ in out] == [4, 4, 2]
+    assert [s for steps, _g, _ids in out for s in steps] == [0, 0, 1, 1, 2, 2, 3, 3, 4, 4]
+
+
+def test_rebatch_preserves_values_and_passes_factorized_through():
+    blocks = stream(3)
+    (steps, g, ids), = list(rebatch_blocks(blocks, batch_size=100))
+    assert torch.equal(g.data["l1"], torch.cat([b.data["l1"] for _s, b, _h in blocks]))
+    mixed = [blocks[0], (9, factorized_block(seed=9), ["f-a", "f-b"]), blocks[1]]
+    out = list(rebatch_blocks(mixed, batch_size=100))
+    assert [ids for _s, _g, ids in out] == [["h0-0", "h0-1"], ["f-a", "f-b"], ["h1-0", "h1-1"]]
+    assert out[1][1] is mixed[1][1]
+    assert list(rebatch_blocks([], batch_size=3)) == []
+    with pytest.raises(ValueError):
+        list(rebatch_blocks(stream(1), batch_size=0))
