@@ -4,7 +4,8 @@ sources with an injected inner product -- column order by first-seen hash,
 row ids and steps, invariance to the train batch size, mixed dense /
 factorized streams, empty sources, the loop_over_test mode and its source
 requirement, the transforms, merged dense test blocks and the dense cache's
-scope -- and rebatch_blocks."""
+scope -- rebatch_blocks, and the token-level AttributionScore read through its
+instance accessors (tests/attribution/test_token_granularity.py:135-166)."""
 
 from __future__ import annotations
 
@@ -238,3 +239,52 @@ def test_rebatch_preserves_values_and_passes_factorized_through():
     assert list(rebatch_blocks([], batch_size=3)) == []
     with pytest.raises(ValueError):
         list(rebatch_blocks(stream(1), batch_size=0))
+
+
+# -- token scores (test_token_granularity.py:135-166) ------------------------------------------
+
+
+def test_token_score_accessors_agree_with_the_instance_score(tmp_path):
+    """A token-level AttributionScore read through the instance accessors is
+    the instance score; token_scores gives each sample's positions; the round
+    trip through disk keeps the token axis."""
+    from dattri_llm_amd.attribution.score import AttributionScore
+
+    train = Source([(0, factorized_block(seed=0), ["r0", "r1"]), (0, factorized_block(seed=1), ["r2", "r3"])])
+    test = Source([(0, dense_block(seed=5), ["q0", "q1"])])
+
+    def per_token(train_rep, test_rep):
+        bf = train_rep.data["l1"].as_batch_first()
+        rows = torch.einsum("bti,bto->btoi", bf.activation, bf.pre_activation_grad).flatten(2)
+        return rows @ flat(test_rep).T
+
+    s_t = score_sources(train, test, "cpu", inner_product=dot, granularity="token",
+                        inner_product_per_token=per_token)
+    s_i = score_sources(train, test, "cpu", inner_product=dot)
+    token = AttributionScore(scores=s_t[0], row_train_ids=s_t[1], row_steps=s_t[2], test_ids=s_t[3],
+                             algorithm="tracin", algorithm_meta={"attribution_granularity": "token"},
+                             layer_name=None, row_token_ids=s_t[4])
+    inst = AttributionScore(scores=s_i[0], row_train_ids=s_i[1], row_steps=s_i[2], test_ids=s_i[3],
+                            algorithm="tracin", algorithm_meta={}, layer_name=None)
+    assert token.granularity == "token" and inst.granularity == "instance"
+    assert token.num_rows == 4 * T and token.row_token_ids == list(range(T)) * 4
+    ids_t, m_t = token.agnostic_matrix()
+    ids_i, m_i = inst.agnostic_matrix()
+    assert ids_t == ids_i
+    torch.testing.assert_close(m_t, m_i, atol=1e-4, rtol=1e-4)
+    for h in ids_t:
+        positions, block = token.token_scores(h)
+        assert positions == list(range(T))
+        torch.testing.assert_close(block.sum(0), inst.trajectory_agnostic(h), atol=1e-4, rtol=1e-4)
+        steps, rows = token.trajectory_aware(h)
+        assert steps == [0]
+        torch.testing.assert_close(rows[0], block.sum(0), atol=1e-4, rtol=1e-4)
+    t_ids, t_m = token.step_matrix(0)
+    assert t_ids == ids_i
+    torch.testing.assert_close(t_m, m_i, atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(token.score_at("r0", 0, "q1"), inst.score_at("r0", 0, "q1"), atol=1e-4, rtol=1e-4)
+    with pytest.raises(ValueError, match="token"):
+        inst.token_scores("r0")
+    back = AttributionScore.load(token.save(tmp_path / "tok"))
+    assert back.granularity == "token" and back.row_token_ids == token.row_token_ids
+    assert torch.equal(back.scores, token.scores)
