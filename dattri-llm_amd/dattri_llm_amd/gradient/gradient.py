@@ -63,6 +63,13 @@ class Factorized:
 GradientData = torch.Tensor | Factorized
 
 
+def base_layer_name(name: str) -> str:
+    """The module path of a layer name: a module invoked several times in one
+    step is recorded as ``"name"``, ``"name@2"``, ... and module paths hold
+    no ``@`` (gradient.py:122-131)."""
+    return name.split("@", 1)[0]
+
+
 @dataclass(frozen=True, eq=False)
 class Gradient:
     """A per-step, multi-layer container of per-sample gradients (gradient.py:183-1191)."""
@@ -231,8 +238,18 @@ class Gradient:
         return Gradient(new_repr, new_data, {k: v for k, v in self.layer_types.items() if k in new_data},
                         new_index, validate_on_init=False)
 
-    def select_layers(self, names: Iterable[str]) -> Gradient:
-        keep = [n for n in names if n in self.data]
+    def select_layers(self, names: Iterable[str], include_derived: bool = False) -> Gradient:
+        """A copy holding only *names* (gradient.py:664-698); with
+        ``include_derived`` a name also selects its invocation layers
+        (``"lin"`` pulls in ``"lin@2"``, ...).  Raises ``KeyError`` for an
+        unknown name."""
+        wanted = set(names)
+        if include_derived:
+            wanted |= {n for n in self.data if base_layer_name(n) in wanted}
+        missing = wanted - set(self.data)
+        if missing:
+            raise KeyError(f"Unknown layers: {sorted(missing)}")
+        keep = [n for n in self.data if n in wanted]
         return Gradient({n: self.representation[n] for n in keep}, {n: self.data[n] for n in keep},
                         {n: self.layer_types[n] for n in keep}, {n: self.indexing[n] for n in keep},
                         validate_on_init=False)
@@ -382,9 +399,11 @@ class Gradient:
 
         def take(x: torch.Tensor, ax: int) -> torch.Tensor:
             sel = index
+            if isinstance(sel, slice):  # explicit positions along this axis (a broadcast row spans the batch)
+                sel = torch.arange(self.batch_size if dim == "batch" and x.shape[ax] == 1 else x.shape[ax])[sel]
             if dim == "batch" and x.shape[ax] == 1:
-                count = 1 if isinstance(index, int) else (index.numel() if torch.is_tensor(index) else len(index))
-                sel = 0 if isinstance(index, int) else torch.zeros(count, dtype=torch.long, device=x.device)
+                count = 1 if isinstance(sel, int) else (sel.numel() if torch.is_tensor(sel) else len(sel))
+                sel = 0 if isinstance(sel, int) else torch.zeros(count, dtype=torch.long, device=x.device)
             if isinstance(sel, int):
                 return x.narrow(ax, sel, 1)
             if not torch.is_tensor(sel):
