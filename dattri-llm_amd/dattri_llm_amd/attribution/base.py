@@ -1,0 +1,107 @@
+"""The inner-product attributor workflow shared by TracIn and the K-FAC family.
+
+Follows ``dattri_llm/attribution/base.py``: an attributor scores
+``<T_train(g_train), T_test(g_test)>`` (base.py:206-214).  Before the loop,
+:meth:`prepare_scoring` fits whatever the transforms need from the sources
+(base.py:555-566).  Each query block is transformed once
+(:meth:`transform_test_rep`, base.py:576-584) and then routed once
+(:meth:`route_test_rep`, base.py:586-655).  The scoring loop
+(:func:`~dattri_llm_amd.attribution.utils.score_sources`, base.py:704-745)
+pairs every train block with every query block through :meth:`inner_product`,
+the layerwise cross-gram (base.py:657-675).
+"""
+
+from __future__ import annotations
+
+import gc
+from typing import ClassVar
+
+import torch
+
+from dattri_llm_amd.attribution.routing import apply_plan, plan_query
+from dattri_llm_amd.attribution.score import AttributionScore
+from dattri_llm_amd.attribution.utils import score_sources
+from dattri_llm_amd.gradient import ops
+from dattri_llm_amd.gradient.gradient import Gradient
+from dattri_llm_amd.utils.cache import CacheBudget
+
+
+class InnerProductAttributor:
+    """Scores of train blocks against query blocks by the layerwise cross-gram.
+
+    Args:
+        train_batch_size: train samples per scoring block (the reference's
+            ``per_device_train_batch_size``), used by the query routing rule.
+        device: where scoring runs.
+        cache_budget: budget factory ``device -> CacheBudget`` for the dense query cache.
+    """
+
+    algorithm: ClassVar[str] = "InnerProduct"
+
+    def __init__(self, train_batch_size: int = 1, device="cuda", *, cache_budget=None) -> None:
+        self.train_batch_size = train_batch_size
+        self.device = torch.device(device)
+        self._budget = cache_budget or (lambda dev: CacheBudget(dev))
+
+    # -- hooks ----------------------------------------------------------------
+
+    def prepare_scoring(self, train_source, test_source) -> None:  # noqa: ARG002
+        """One-time work before a scoring pass (base.py:555-566); none by default."""
+
+    def transform_test_rep(self, test_rep: Gradient) -> Gradient:  # noqa: PLR6301
+        """``T_test`` of one device-resident query block (base.py:576-584); identity by default."""
+        return test_rep
+
+    def route_test_rep(self, test_rep: Gradient) -> Gradient:
+        """The query block in the representation it is scored in (base.py:586-655)."""
+        budget = self._budget(test_rep.device)
+        return apply_plan(test_rep, plan_query(test_rep, self.train_batch_size or 1, budget), budget)
+
+    @staticmethod
+    def _shared(train_rep: Gradient, test_rep: Gradient) -> list[str]:
+        return [name for name in train_rep.data if name in test_rep.data]
+
+    def inner_product(self, train_rep: Gradient, test_rep: Gradient, *, dense_cache=None) -> torch.Tensor:
+        """``(B_train, B_test)`` layerwise cross-gram of one block pair (base.py:657-675)."""
+        if not self._shared(train_rep, test_rep):
+            return torch.zeros(train_rep.batch_size, test_rep.batch_size, device=self.device)
+        return ops.layerwise_cross_dot(train_rep, test_rep, dense_cache=dense_cache)
+
+    def _zeros_per_token(self, train_rep: Gradient, test_rep: Gradient) -> torch.Tensor:
+        tokens = [t for t in train_rep.token_dim.values() if t is not None]
+        return torch.zeros(train_rep.batch_size, max(tokens) if tokens else 1, test_rep.batch_size,
+                           device=self.device)
+
+    def inner_product_per_token(self, train_rep: Gradient, test_rep: Gradient) -> torch.Tensor:
+        """``(B_train, T_train, B_test)`` decomposition of :meth:`inner_product`
+        over the train side's token positions (base.py:677-698)."""
+        if not self._shared(train_rep, test_rep):
+            return self._zeros_per_token(train_rep, test_rep)
+        return ops.layerwise_cross_dot_per_token(train_rep, test_rep)
+
+    # -- the scoring pass -----------------------------------------------------
+
+    def _score(self, train_source, test_source, *, batch_size: int | None, loop_over_test: bool,
+               attribution_granularity: str, algorithm_meta: dict) -> AttributionScore:
+        """Fit, then run the scoring loop with each query block transformed and
+        routed once; the result in the reference's score format."""
+        self.prepare_scoring(train_source, test_source)
+        # The loop allocates many small objects per block; with the cyclic
+        # collector running it rescans the whole heap over and over (measured:
+        # 50 ms vs 8 ms for 32768 train rows x 128 queries).  Nothing made here
+        # needs collecting before the call returns.
+        gc_was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            scores, row_ids, row_steps, test_ids, row_tokens = score_sources(
+                train_source, test_source, self.device, inner_product=self.inner_product,
+                transform_test=lambda block: self.route_test_rep(self.transform_test_rep(block)),
+                batch_size=batch_size or self.train_batch_size, loop_over_test=loop_over_test,
+                granularity=attribution_granularity, inner_product_per_token=self.inner_product_per_token,
+            )
+            return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
+                                    algorithm=self.algorithm, algorithm_meta=algorithm_meta, layer_name=None,
+                                    row_token_ids=row_tokens)
+        finally:
+            if gc_was_enabled:
+                gc.enable()

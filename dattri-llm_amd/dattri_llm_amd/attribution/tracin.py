@@ -16,23 +16,20 @@ diagonal pairs).
 
 from __future__ import annotations
 
-import gc
 import weakref
 from typing import ClassVar
 
 import torch
 
-from dattri_llm_amd.attribution.routing import apply_plan, plan_query
+from dattri_llm_amd.attribution.base import InnerProductAttributor
 from dattri_llm_amd.attribution.score import AttributionScore
-from dattri_llm_amd.attribution.utils import score_sources
 from dattri_llm_amd.gradient import ops
 from dattri_llm_amd.gradient.gradient import Gradient
-from dattri_llm_amd.utils.cache import CacheBudget
 
 _EPS = 1e-8  # added to the product of the norms (tracin.py:108)
 
 
-class TracInAttributor:
+class TracInAttributor(InnerProductAttributor):
     """Gradient-dot (TracIn) or cosine (GradCos) attribution over gradient sources.
 
     Args:
@@ -45,9 +42,7 @@ class TracInAttributor:
     algorithm: ClassVar[str] = "TracIn"
 
     def __init__(self, train_batch_size: int = 1, device="cuda", *, cache_budget=None) -> None:
-        self.train_batch_size = train_batch_size
-        self.device = torch.device(device)
-        self._budget = cache_budget or (lambda dev: CacheBudget(dev))
+        super().__init__(train_batch_size, device, cache_budget=cache_budget)
         self._metric = "dot"
         # query block -> {shared layers: (B,) whole-model norms}; entries die with the block
         self._query_norms: weakref.WeakKeyDictionary = weakref.WeakKeyDictionary()
@@ -56,18 +51,7 @@ class TracInAttributor:
         self._metric = "cosine" if normalized_grad else "dot"
         self.algorithm = "GradCos" if normalized_grad else "TracIn"
 
-    # -- query routing ------------------------------------------------------
-
-    def route_test_rep(self, test_rep: Gradient) -> Gradient:
-        """The query block in the representation it is scored in (base.py:586-655)."""
-        budget = self._budget(test_rep.device)
-        return apply_plan(test_rep, plan_query(test_rep, self.train_batch_size or 1, budget), budget)
-
     # -- scores -------------------------------------------------------------
-
-    @staticmethod
-    def _shared(train_rep: Gradient, test_rep: Gradient) -> list[str]:
-        return [name for name in train_rep.data if name in test_rep.data]
 
     def _norms(self, rep: Gradient, layers: list[str], dense_cache=None) -> torch.Tensor:
         return ops.block_grad_norm_sq(rep, layers, dense_cache).clamp_min(0).sqrt()
@@ -103,9 +87,7 @@ class TracInAttributor:
         two whole-sample norms)."""
         layers = self._shared(train_rep, test_rep)
         if not layers:
-            tokens = [t for t in train_rep.token_dim.values() if t is not None]
-            return torch.zeros(train_rep.batch_size, max(tokens) if tokens else 1, test_rep.batch_size,
-                               device=self.device)
+            return self._zeros_per_token(train_rep, test_rep)
         dot = ops.layerwise_cross_dot_per_token(train_rep, test_rep)
         return dot if self._metric == "dot" else self._cosine(dot, train_rep, test_rep, layers)
 
@@ -117,22 +99,6 @@ class TracInAttributor:
         instead of caching it; ``attribution_granularity="token"`` gives one row
         per training token position (:meth:`inner_product_per_token`)."""
         self._set_metric(normalized_grad)
-        # The loop allocates many small objects per block; with the cyclic
-        # collector running it rescans the whole heap over and over (measured:
-        # 50 ms vs 8 ms for 32768 train rows x 128 queries).  Nothing made here
-        # needs collecting before the call returns.
-        gc_was_enabled = gc.isenabled()
-        gc.disable()
-        try:
-            scores, row_ids, row_steps, test_ids, row_tokens = score_sources(
-                train_source, test_source, self.device, inner_product=self.inner_product,
-                transform_test=self.route_test_rep, batch_size=batch_size or self.train_batch_size,
-                loop_over_test=loop_over_test, granularity=attribution_granularity, inner_product_per_token=self.inner_product_per_token,
-            )
-            return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
-                                    algorithm=self.algorithm,
-                                    algorithm_meta={"normalized_grad": normalized_grad}, layer_name=None,
-                                    row_token_ids=row_tokens)
-        finally:
-            if gc_was_enabled:
-                gc.enable()
+        return self._score(train_source, test_source, batch_size=batch_size, loop_over_test=loop_over_test,
+                           attribution_granularity=attribution_granularity,
+                           algorithm_meta={"normalized_grad": normalized_grad})
