@@ -219,3 +219,61 @@ def test_fit_reuse_and_token_rows(device):
     assert_parity(summed, _kfac_want(cat, q, 0.1), torch.float32, tight=TIGHT, label="token rows")
     looped = attr.attribute_sources(train, test, damping=0.1, raw_fit=raw, loop_over_test=True)
     assert_parity(looped.scores, _kfac_want(cat, q, 0.1), torch.float32, tight=TIGHT, label="loop_over_test")
+
+
+def test_dense_query_matches_factorized_query(device):
+    """A query stored materialized takes the two-sided dense product and scores
+    as the factorized query does (test_kronecker.py:395-419)."""
+    from dattri_llm_amd.attribution import EKFACAttributor, KFACAttributor
+
+    print("kfac/ekfac attributors, dense query side", flush=True)
+    train, test, _cat, _q = _setup(device)
+    _tr, dense_test, _c, _qq = _setup(device, dense=("up", "down"))
+    for cls in (KFACAttributor, EKFACAttributor):
+        attr = cls(train_batch_size=6, device=device)
+        raw = attr.fit(train)
+        fact = attr.attribute_sources(train, test, damping=0.1, raw_fit=raw)
+        dense = attr.attribute_sources(train, dense_test, damping=0.1, raw_fit=raw)
+        assert_parity(dense.scores, fact.scores, torch.float32, tight=TIGHT, label=cls.__name__)
+
+
+def test_fisher_cap_skips_a_layer_with_a_warning(device):
+    from dattri_llm_amd.attribution import KFACAttributor
+
+    print("kfac attributor, direct Fisher cap", flush=True)
+    train, test, cat, q = _setup(device)
+    with pytest.warns(UserWarning, match="direct_fim_max_params=4"):
+        score = KFACAttributor(train_batch_size=6, device=device).attribute_sources(
+            train, test, damping=0.1, non_kfac_strategy="direct", direct_fim_max_params=4)
+    assert score.algorithm_meta["direct_fim_layers"] == []
+    assert_parity(score.scores, _kfac_want(cat, q, 0.1), torch.float32, tight=TIGHT)
+
+
+def test_norm_only_scores_the_direct_fisher(device):
+    from dattri_llm_amd.attribution import EKFACAttributor, KFACAttributor
+
+    print("kfac/ekfac attributors, norm layer only", flush=True)
+    train, test, cat, q = _setup(device)
+    only = lambda src: Source([(s, b.select_layers(["ln"]), h) for s, b, h in src.blocks])  # noqa: E731
+    m_tr, m_q = _norm_dense(*cat["ln"]), _norm_dense(*q["ln"])
+    fisher = oracle.fim_factors(m_tr)
+    want = m_tr @ np.linalg.inv(fisher + 0.1 * np.eye(len(fisher))) @ m_q.T
+    for cls in (KFACAttributor, EKFACAttributor):
+        score = cls(train_batch_size=6, device=device).attribute_sources(
+            only(train), only(test), damping=0.1, non_kfac_strategy="direct")
+        assert_parity(score.scores, want, torch.float32, tight=TIGHT, label=cls.__name__)
+
+
+def test_ekfac_heavy_damping_is_the_gradient_dot(device):
+    """(lambda_raw + lam)^-1 = 1/lam (1 - lambda_raw/lam + ...)
+    (test_kronecker.py:252-286)."""
+    from dattri_llm_amd.attribution import EKFACAttributor, TracInAttributor
+
+    print("ekfac attributor, damping 1e4", flush=True)
+    train, test, _cat, _q = _setup(device)
+    lam = 1e4
+    ek = EKFACAttributor(train_batch_size=6, device=device).attribute_sources(train, test, damping=lam)
+    lin = lambda src: Source([(s, b.select_layers(["up", "down"]), h) for s, b, h in src.blocks])  # noqa: E731
+    dot = TracInAttributor(train_batch_size=6, device=device).attribute_sources(lin(train), lin(test))
+    got, want = _np(ek.scores) * lam, _np(dot.scores)
+    assert np.linalg.norm(got - want) <= 5e-3 * np.linalg.norm(want)
