@@ -277,3 +277,64 @@ def test_ekfac_heavy_damping_is_the_gradient_dot(device):
     dot = TracInAttributor(train_batch_size=6, device=device).attribute_sources(lin(train), lin(test))
     got, want = _np(ek.scores) * lam, _np(dot.scores)
     assert np.linalg.norm(got - want) <= 5e-3 * np.linalg.norm(want)
+
+
+def _conv_expected(case, train_in, query_in, kind, damping):
+    """K-FAC / EK-FAC scores of one convolution layer from the oracle's
+    preprocessed factors, group by group.  Both are symmetric in the two
+    factors' roles, so one rule covers convolutions and transposed ones."""
+    transpose, _rank, _ci, _co, k, s, p, d, groups, bias, _sp = case
+    pre = [oracle.conv_preprocess(x, g, transpose, k, s, p, d, groups, bias) for x, g in train_in]
+    a, f = np.concatenate([x for x, _ in pre]), np.concatenate([g for _, g in pre])
+    qa, qf = oracle.conv_preprocess(*query_in, transpose, k, s, p, d, groups, bias)
+    assert not (f == 0).all(-1).any()  # no gradient-free rows: the oracle's drop rule is moot
+    parts = ([(a[:, :, i], f[:, :, i], qa[:, :, i], qf[:, :, i]) for i in range(groups)] if a.ndim == 4
+             else [(a, f, qa, qf)])
+    total = 0.0
+    for pa, pf, pqa, pqf in parts:
+        big_a, big_g = oracle.kfac_factors(pa, pf)
+        if kind == "kfac":
+            total = total + oracle.kfac_cross_factors(pqa, pqf, pa, pf, oracle.sym_inverse(big_a, damping),
+                                                      oracle.sym_inverse(big_g, damping)).T
+        else:
+            u_a, u_g = np.linalg.eigh(big_a)[1], np.linalg.eigh(big_g)[1]
+            lam = (oracle.ekfac_materialize_factors(pa, pf, u_a, u_g) ** 2).mean(axis=0)
+            pre_q = oracle.ekfac_precondition(oracle.ekfac_materialize_factors(pqa, pqf, u_a, u_g), u_a, u_g,
+                                              lam + damping)
+            total = total + oracle.materialize_linear(pa, pf) @ pre_q.T
+    return total
+
+
+@pytest.mark.parametrize("kind", ["kfac", "ekfac"])
+@pytest.mark.parametrize("case", range(7))
+def test_convolution_layers(device, case, kind):
+    """Convolutions, transposed convolutions, grouped and depthwise ones
+    (the K-FAC family's conv support, kronecker.py:638-659 via ops)."""
+    from test_oracle import CONV_CASES, conv_inputs
+
+    from dattri_llm_amd.attribution import EKFACAttributor, KFACAttributor
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    conv = CONV_CASES[case]
+    transpose, rank, _ci, _co, k, s, p, d, groups, bias, _sp = conv
+    print(f"{kind} attributor, conv case {conv}", flush=True)
+    lt = {(False, 1): "nn.Conv1d", (False, 2): "nn.Conv2d", (False, 3): "nn.Conv3d",
+          (True, 1): "nn.ConvTranspose1d", (True, 2): "nn.ConvTranspose2d"}[(transpose, rank)]
+    mk = {"has_bias": bias, "kernel_size": k, "stride": s, "padding": p, "dilation": d, "groups": groups}
+    train_in = [conv_inputs(conv, n=3, seed=60), conv_inputs(conv, n=3, seed=62)]
+    query_in = conv_inputs(conv, n=2, seed=61)
+
+    def block(x, g):
+        data = {"conv": Factorized(torch.from_numpy(x).float().to(device), torch.from_numpy(g).float().to(device),
+                                   module_kwargs=mk)}
+        return Gradient({"conv": "factorized"}, data, {"conv": lt}, {"conv": "batch_token"})
+
+    # the oracle sees the fp32-rounded inputs the kernels read
+    rounded = lambda xg: tuple(v.astype(np.float32).astype(np.float64) for v in xg)  # noqa: E731
+    train = Source([(0, block(*xg), [f"r{i}-{j}" for j in range(3)]) for i, xg in enumerate(train_in)])
+    test = Source([(0, block(*query_in), ["q0", "q1"])])
+    cls = KFACAttributor if kind == "kfac" else EKFACAttributor
+    score = cls(train_batch_size=3, device=device).attribute_sources(train, test, damping=0.1)
+    want = _conv_expected(conv, [rounded(xg) for xg in train_in], rounded(query_in), kind, 0.1)
+    assert score.scores.shape == (6, 2)
+    assert_parity(score.scores, want, torch.float32, tight=TIGHT)
