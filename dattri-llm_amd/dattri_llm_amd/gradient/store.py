@@ -39,13 +39,15 @@ import json
 import os
 import queue
 import threading
+import warnings
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import numpy as np
 import torch
 
-from dattri_llm_amd.gradient.gradient import Factorized, Gradient, GradientRecord
+from dattri_llm_amd.gradient.gradient import Factorized, Gradient, GradientRecord, base_layer_name
+from dattri_llm_amd.gradient.ops.types import PARAM_GRAD_TYPES
 
 MEMMAP_FORMAT = 2
 INDEX_FORMAT = 2
@@ -327,8 +329,10 @@ def _cat_layer(values):
 
 def records_to_block(records, idxs, layer_name=None):
     """One ``(Gradient, hashes)`` block from the records ``idxs`` of a group
-    (datasets.py:40-97)."""
-    grads, hashes = [], []
+    (datasets.py:40-97).  A requested layer name also selects its invocation
+    layers (``"lin"`` pulls in ``"lin@2"``); batch-level ``param_grad`` layers
+    have no per-sample rows and are left out with a warning."""
+    grads, hashes, dropped = [], [], set()
     for i in idxs:
         rec = records[i]
         g = rec.gradient
@@ -336,9 +340,20 @@ def records_to_block(records, idxs, layer_name=None):
         missing = names - g.layer_names
         if missing:
             raise KeyError(f"Unknown layers: {sorted(missing)}")
+        if layer_name is not None:
+            names = names | {n for n in g.layer_names if base_layer_name(n) in names}
+        batch_level = {n for n in names if g.layer_types[n] == PARAM_GRAD_TYPES}
+        dropped |= batch_level
+        names = names - batch_level
+        if not names:
+            raise ValueError("No per-sample gradient layers remain once the batch-level param_grad layers "
+                             f"{sorted(batch_level)} are left out.")
         grads.append((g, sorted(names)))
         h = rec.input_hash
         hashes.extend(h if isinstance(h, list) else [h])
+    if dropped:
+        warnings.warn(f"Skipping batch-level param_grad layers during per-sample attribution: {sorted(dropped)}.",
+                      stacklevel=3)
     if not grads:
         raise RuntimeError("no records selected")
     g0, names = grads[0]

@@ -288,3 +288,22 @@ def test_token_score_accessors_agree_with_the_instance_score(tmp_path):
     back = AttributionScore.load(token.save(tmp_path / "tok"))
     assert back.granularity == "token" and back.row_token_ids == token.row_token_ids
     assert torch.equal(back.scores, token.scores)
+
+
+@pytest.mark.parametrize("loop_over_test", [False, True])
+def test_duplicate_test_samples_share_a_column(loop_over_test):
+    """Identical test samples (one content hash, inside a block and across
+    blocks) collapse to one column, and no column stays zero
+    (test_tracin.py:607-628)."""
+    a, b = dense_block(seed=100), dense_block(seed=101)
+    a.data["l1"][1] = a.data["l1"][0]          # sample 1 repeats sample 0
+    b.data["l1"][0] = a.data["l1"][0]          # and so does the next block's first sample
+    test = Source([(0, a, ["q0", "q0"]), (0, b, ["q0", "q1"])])
+    train = Source(stream(2))
+    scores, _ids, _steps, test_ids, _tok = score_sources(train, test, "cpu", inner_product=dot,
+                                                         loop_over_test=loop_over_test)
+    assert test_ids == ["q0", "q1"] and scores.shape == (2 * B, 2)
+    tr = torch.cat([flat(g) for _, g, _ in train.blocks])
+    want = tr @ torch.stack([a.data["l1"][0], b.data["l1"][1]]).T
+    assert torch.allclose(scores, want, atol=1e-5)
+    assert int((scores.abs().sum(0) == 0).sum()) == 0

@@ -188,3 +188,39 @@ def test_reader_thread_never_blocks_after_stop(tmp_path):
         out = queue.Queue(maxsize=1)
         src._host_files(out, threading.Event())
         assert isinstance(out.get_nowait(), BaseException)
+
+
+def _record(step, hashes, extra_layers):
+    """An in-memory record: one dense linear layer "fc" plus *extra_layers*
+    ``{name: (layer_type, tensor)}``."""
+    from dattri_llm_amd.gradient import Gradient
+    from dattri_llm_amd.gradient.gradient import GradientRecord
+
+    n = len(hashes)
+    data = {"fc": torch.randn(n, 6)}
+    types = {"fc": "nn.Linear"}
+    for name, (lt, t) in extra_layers.items():
+        data[name], types[name] = t, lt
+    g = Gradient(dict.fromkeys(data, "materialized"), data, types, dict.fromkeys(data, "batch"))
+    return GradientRecord(step, hashes, g)
+
+
+def test_param_grad_layers_are_skipped_with_a_warning():
+    """Batch-level param_grad layers are left out of per-sample blocks
+    (datasets.py:62-84, test_tracin.py:406-433)."""
+    recs = [_record(0, ["a", "b"], {"custom.weight": ("param_grad_layers", torch.ones(3, 2))}),
+            _record(0, ["c"], {"custom.weight": ("param_grad_layers", torch.ones(3, 2))})]
+    with pytest.warns(UserWarning, match="Skipping batch-level param_grad layers"):
+        block, hashes = records_to_block(recs, [0, 1])
+    assert block.layer_names == {"fc"} and block.batch_size == 3 and hashes == ["a", "b", "c"]
+    with pytest.raises(ValueError, match="No per-sample gradient layers remain"):
+        records_to_block(recs, [0], ["custom.weight"])
+
+
+def test_layer_name_pulls_in_invocation_layers():
+    """A requested layer also selects its ``@k`` invocation layers (datasets.py:57-63)."""
+    recs = [_record(0, ["a", "b"], {"fc@2": ("nn.Linear", torch.randn(2, 6)), "other": ("nn.Linear", torch.randn(2, 6))})]
+    block, _ = records_to_block(recs, [0], ["fc"])
+    assert block.layer_names == {"fc", "fc@2"}
+    with pytest.raises(KeyError, match="Unknown layers"):
+        records_to_block(recs, [0], ["fc@3"])
