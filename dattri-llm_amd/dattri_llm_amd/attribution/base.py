@@ -79,12 +79,24 @@ class InnerProductAttributor:
             return self._zeros_per_token(train_rep, test_rep)
         return ops.layerwise_cross_dot_per_token(train_rep, test_rep)
 
+    def dense_train_group(self, reps: list[Gradient]) -> Gradient:
+        """Several train blocks as one dense block, stacked along the batch
+        (linear layers straight into one k-blocked buffer); the layers all the
+        blocks hold."""
+        names = [n for n in reps[0].data if all(n in r.data for r in reps[1:])]
+        data = {n: ops.materialize_group([r.data[n] for r in reps], reps[0].layer_types[n]) for n in names}
+        return Gradient(dict.fromkeys(names, "materialized"), data, {n: reps[0].layer_types[n] for n in names},
+                        dict.fromkeys(names, "batch"), validate_on_init=False)
+
     # -- the scoring pass -----------------------------------------------------
 
     def _score(self, train_source, test_source, *, batch_size: int | None, loop_over_test: bool,
-               attribution_granularity: str, algorithm_meta: dict) -> AttributionScore:
+               attribution_granularity: str, algorithm_meta: dict,
+               train_blocks_per_pass: int = 1) -> AttributionScore:
         """Fit, then run the scoring loop with each query block transformed and
-        routed once; the result in the reference's score format."""
+        routed once; the result in the reference's score format.
+        ``train_blocks_per_pass`` > 1 scores that many dense train blocks per
+        pass over a dense query block (:meth:`dense_train_group`)."""
         self.prepare_scoring(train_source, test_source)
         # The loop allocates many small objects per block; with the cyclic
         # collector running it rescans the whole heap over and over (measured:
@@ -98,6 +110,7 @@ class InnerProductAttributor:
                 transform_test=lambda block: self.route_test_rep(self.transform_test_rep(block)),
                 batch_size=batch_size or self.train_batch_size, loop_over_test=loop_over_test,
                 granularity=attribution_granularity, inner_product_per_token=self.inner_product_per_token,
+                train_blocks_per_pass=train_blocks_per_pass, dense_group=self.dense_train_group,
             )
             return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
                                     algorithm=self.algorithm, algorithm_meta=algorithm_meta, layer_name=None,

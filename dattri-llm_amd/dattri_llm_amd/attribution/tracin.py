@@ -93,12 +93,16 @@ class TracInAttributor(InnerProductAttributor):
 
     def attribute_sources(self, train_source, test_source, *, normalized_grad: bool = False,
                           batch_size: int | None = None, loop_over_test: bool = False,
-                          attribution_granularity: str = "instance") -> AttributionScore:
+                          attribution_granularity: str = "instance",
+                          train_blocks_per_pass: int = 1) -> AttributionScore:
         """Score two ``(step, Gradient, hashes)`` sources (base.py:704-770);
         ``loop_over_test`` re-streams a reusable test source per train block
         instead of caching it; ``attribution_granularity="token"`` gives one row
-        per training token position (:meth:`inner_product_per_token`)."""
+        per training token position (:meth:`inner_product_per_token`);
+        ``train_blocks_per_pass`` > 1 reads a dense query block once per that
+        many train blocks, with the same scores."""
         self._set_metric(normalized_grad)
         return self._score(train_source, test_source, batch_size=batch_size, loop_over_test=loop_over_test,
                            attribution_granularity=attribution_granularity,
-                           algorithm_meta={"normalized_grad": normalized_grad})
+                           algorithm_meta={"normalized_grad": normalized_grad},
+                           train_blocks_per_pass=train_blocks_per_pass)

@@ -115,6 +115,8 @@ def score_sources(
     cache_budget: CacheBudget | None = None,
     granularity: str = "instance",
     inner_product_per_token: Callable | None = None,
+    train_blocks_per_pass: int = 1,
+    dense_group: Callable | None = None,
 ):
     """Score every train block against every test block (utils.py:239-440).
 
@@ -132,6 +134,12 @@ def score_sources(
     ``inner_product_per_token(train_rep, test_rep) -> (B_train, T, B_test)``
     (a sample of T positions contributes T consecutive rows).
 
+    ``train_blocks_per_pass`` > 1 (instance level, cached test side held as
+    one dense block): that many train blocks are made dense together by
+    ``dense_group(reps) -> Gradient`` and scored in one pass over the test
+    block, which is then read once per group instead of once per train block.
+    The scores are those of the block-by-block loop.
+
     Returns ``(scores (rows, num_test) fp32 CPU, row_train_ids, row_steps,
     test_ids, row_token_ids or None)``."""
     if loop_over_test and not getattr(test_source, "reusable", False):
@@ -141,6 +149,10 @@ def score_sources(
     if granularity not in {"instance", "token"}:
         raise ValueError(f"granularity must be 'instance' or 'token', got {granularity!r}.")
     per_token = granularity == "token"
+    if train_blocks_per_pass < 1:
+        raise ValueError(f"train_blocks_per_pass must be >= 1, got {train_blocks_per_pass}.")
+    if train_blocks_per_pass > 1 and dense_group is None:
+        raise ValueError("train_blocks_per_pass > 1 needs dense_group.")
     if per_token and inner_product_per_token is None:
         raise ValueError("granularity='token' needs inner_product_per_token.")
     transform_train = transform_train or (lambda g: g)
@@ -164,6 +176,8 @@ def score_sources(
     # a dense copy of the train block pays off only against several test blocks,
     # and only the instance-level kernel materializes the train side
     reuse = loop_over_test or (len(cached) > 1 and not per_token)
+    grouped = (train_blocks_per_pass > 1 and not loop_over_test and not per_token and len(cached) == 1
+               and all(isinstance(v, torch.Tensor) for v in cached[0][0].data.values()))
 
     def test_blocks():
         if not loop_over_test:
@@ -187,8 +201,28 @@ def score_sources(
 
     rows_out = _HostRows()
     row_ids, row_steps, row_tokens = [], [], []
-    for steps, train_g, ids in train_blocks():
-        train_rep = transform_train(train_g.to(device))
+
+    def scored_blocks():
+        if not grouped:
+            for steps, train_g, ids in train_blocks():
+                yield steps, transform_train(train_g.to(device)), ids
+            return
+        group: list = []
+
+        def dense(group):
+            reps = [transform_train(g.to(device)) for _s, g, _i in group]
+            return ([s for st, _g, _i in group for s in st], dense_group(reps),
+                    [h for _s, _g, ids in group for h in ids])
+
+        for item in train_blocks():
+            group.append(item)
+            if len(group) == train_blocks_per_pass:
+                yield dense(group)
+                group = []
+        if group:
+            yield dense(group)
+
+    for steps, train_rep, ids in scored_blocks():
         row = torch.zeros(n_rows(train_rep), num_test, dtype=torch.float32, device=device)
         cache = TensorCache("memory", budget=budget) if reuse else None
         for test_rep, cols in test_blocks():

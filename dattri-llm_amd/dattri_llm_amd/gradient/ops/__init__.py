@@ -50,7 +50,12 @@ from dattri_llm_amd.gradient.ops.kronecker import (
     kfac_precondition_materialized,
     sym_inverse,
 )
-from dattri_llm_amd.gradient.ops.materialize import materialize, materialize_blocked, materialize_factors
+from dattri_llm_amd.gradient.ops.materialize import (
+    materialize,
+    materialize_blocked,
+    materialize_factors,
+    materialize_group,
+)
 from dattri_llm_amd.gradient.ops.preprocess import (
     extract_module_kwargs,
     preprocess_factorized,
@@ -124,7 +129,7 @@ __all__ = [
     "grad_norm_sq", "grad_norm_sq_factors", "is_conv", "is_conv_transpose", "is_embedding",
     "is_kfac_eligible", "is_linear", "is_norm", "layerwise_cross_dot", "layerwise_cross_dot_per_token",
     "mask_coordinates", "mask_factorized", "mask_factors", "mask_materialized",
-    "materialize", "materialize_blocked", "materialize_factors", "maybe_materialize_projected", "maybe_use_materialized_gram",
+    "materialize", "materialize_blocked", "materialize_factors", "materialize_group", "maybe_materialize_projected", "maybe_use_materialized_gram",
     "maybe_use_materialized_norm", "moe", "pairwise_dot", "pairwise_dot_factors", "preprocess_factorized",
     "preprocess_factors", "project_activation", "project_factorized", "project_factors",
     "project_gradient", "project_layer", "project_materialized", "project_materialized_factors",

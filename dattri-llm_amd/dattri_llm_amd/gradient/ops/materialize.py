@@ -173,6 +173,45 @@ def materialize_blocked(f, layer_type: str, include_bias: bool = True) -> torch.
     return out.to(out_dtype)
 
 
+def materialize_group(values: list, layer_type: str, include_bias: bool = True) -> torch.Tensor:
+    """The dense form of one layer over several train blocks, stacked along the batch.
+
+    Linear layers that :func:`materialize_blocked` writes k-blocked go block
+    by block into row slices of one k-blocked buffer, so the score GEMM reads
+    the stacked rows as one block with no copy; other layers are materialized
+    and concatenated."""
+    if len(values) == 1:
+        return materialize_blocked(values[0], layer_type, include_bias)
+    prepared = []
+    if is_linear(layer_type):
+        for f in values:
+            if isinstance(f, torch.Tensor):
+                break
+            bf = f.as_batch_first()
+            a, g, bias = final_linear(bf.activation, bf.pre_activation_grad, layer_type, bf.module_kwargs,
+                                      include_bias)
+            if bias or a.ndim == 4:
+                break
+            (ao, go), out_dtype = _operands(to_3d(a), to_3d(g))
+            b, t, k = ao.shape
+            d = go.shape[-1]
+            if (k % 64 or d % (16 // ao.element_size()) or b == 0 or t == 0
+                    or dtypes.kernel_dtype(out_dtype) != out_dtype):
+                break
+            prepared.append((ao, go, out_dtype))
+    shapes = {(ao.shape[-1], go.shape[-1], ao.dtype, od) for ao, go, od in prepared}
+    if len(prepared) != len(values) or len(shapes) != 1:
+        return torch.cat([materialize(f, layer_type, include_bias) for f in values])
+    k, d, _dt, out_dtype = shapes.pop()
+    rows = sum(ao.shape[0] for ao, _go, _od in prepared)
+    buf = kernels.blocked_storage(rows, d * k, out_dtype, prepared[0][0].device)
+    r = 0
+    for ao, go, _od in prepared:
+        kernels.materialize_linear(ao, go, out_dtype=out_dtype, blocked=True, out=buf[r:r + ao.shape[0]])
+        r += ao.shape[0]
+    return buf
+
+
 def materialize(f, layer_type: str, include_bias: bool = True, per_token: bool = False) -> torch.Tensor:
     """Per-sample weight gradient of one layer, whatever its form (materialize.py:119-146)."""
     if isinstance(f, torch.Tensor):

@@ -572,12 +572,15 @@ def materialize_linear(
     bias: bool = False,
     out_dtype: torch.dtype | None = None,
     blocked: bool = False,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Per-sample linear weight gradient ``(B, D*(K+bias))``, index o*(K+bias)+k.
 
     With ``blocked`` (and K a multiple of 64, no bias) the result is written in
     the k-blocked layout and returned as its ``(B, D*K/64, 64)`` view (see
-    :func:`is_blocked`); otherwise ``blocked`` is ignored."""
+    :func:`is_blocked`); otherwise ``blocked`` is ignored.  ``out`` (blocked
+    only) is a row slice ``view[b0:b0+B]`` of a larger :func:`blocked_storage`
+    buffer, so several blocks can be written into one."""
     dev = nat.require_device(a, g)
     if a.dim() != 3 or g.dim() != 3 or a.shape[:2] != g.shape[:2]:
         raise ValueError("materialize_linear expects a (B, T, K) and g (B, T, D)")
@@ -588,13 +591,20 @@ def materialize_linear(
     d = g.shape[-1]
     kb = k + int(bias)
     if blocked and not bias and k % 64 == 0 and d % _chunk_elems(a.dtype) == 0 and b > 0 and t > 0:
-        out = blocked_storage(b, d * k, out_dtype, dev)
+        if out is None:
+            out = blocked_storage(b, d * k, out_dtype, dev)
+        elif not (is_blocked(out) and out.shape == (b, d * k // 64, 64) and out.stride(0) == 64
+                  and out.stride(1) >= b * 64 and out.dtype == out_dtype and out.device == dev):
+            raise ValueError("materialize_linear out must be a (B, D*K/64, 64) row slice of a blocked buffer "
+                             "in out_dtype")
         a, g = prepare_rows(a, k), prepare_rows(g, d)
         _run(dev, "materialize_linear", nat.load().da_materialize_linear,
              a.data_ptr(), g.data_ptr(), nat.dtype_code(a.dtype), b, t, k, d, a.stride(0), a.stride(1),
-             g.stride(0), g.stride(1), 0, out.data_ptr(), nat.dtype_code(out_dtype), 64, k, b * 64,
+             g.stride(0), g.stride(1), 0, out.data_ptr(), nat.dtype_code(out_dtype), 64, k, out.stride(1),
              nat.stream_ptr(dev))
         return out
+    if out is not None:
+        raise ValueError("materialize_linear out is for the blocked layout only")
     out = torch.empty(b, d * kb, dtype=out_dtype, device=dev)
     if b == 0 or d == 0 or kb == 0:
         return out

@@ -1,0 +1,55 @@
+"""Several train blocks scored in one pass over a dense query block
+(score_sources' train_blocks_per_pass): materialize_group writes the linear
+layers of every block into row slices of one k-blocked buffer, and the scores
+equal the block-by-block loop's (the query side is read once per group)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from conftest import assert_parity, roundings
+
+pytestmark = pytest.mark.gpu
+
+
+def _block(gen, b, device, t=24):
+    from dattri_llm_amd.gradient import Factorized, Gradient
+
+    r = lambda *s: torch.randn(*s, generator=gen).to(torch.bfloat16).to(device)  # noqa: E731
+    data = {"up": Factorized(r(b, t, 128), r(b, t, 40)),            # k-blocked (K % 64 == 0)
+            "out": Factorized(r(b, t, 40), r(b, t, 64), module_kwargs={"has_bias": True}),  # plain
+            "ln": Factorized(r(b, t, 32), r(b, t, 32))}
+    lts = {"up": "nn.Linear", "out": "nn.Linear", "ln": "nn.RMSNorm"}
+    return Gradient(dict.fromkeys(data, "factorized"), data, lts, dict.fromkeys(data, "batch_token"))
+
+
+def test_materialize_group_matches_materialize(device):
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.gradient import ops
+
+    print("materialize_group: 3 blocks of 2, 3, 1 samples", flush=True)
+    gen = torch.Generator().manual_seed(3)
+    blocks = [_block(gen, b, device) for b in (2, 3, 1)]
+    for name, lt in (("up", "nn.Linear"), ("out", "nn.Linear"), ("ln", "nn.RMSNorm")):
+        got = ops.materialize_group([bl.data[name] for bl in blocks], lt)
+        want = torch.cat([ops.materialize(bl.data[name], lt) for bl in blocks])
+        assert kernels.is_blocked(got) == (name == "up"), name
+        assert torch.equal(got.reshape(6, -1), want), name
+
+
+@pytest.mark.parametrize("normalized", [False, True])
+def test_grouped_passes_give_the_block_scores(device, normalized):
+    from dattri_llm_amd.attribution import TracInAttributor
+
+    print(f"train_blocks_per_pass=3 over 7 blocks, normalized={normalized}", flush=True)
+    gen = torch.Generator().manual_seed(4)
+    train = [(s, _block(gen, 4, device), [f"r{s}-{i}" for i in range(4)]) for s in range(7)]
+    attr = TracInAttributor(train_batch_size=4, device=device)
+    query = attr.route_test_rep(_block(gen, 16, device, t=16))
+    assert all(isinstance(v, torch.Tensor) for v in query.data.values())
+    test = [(0, query, [f"q{j}" for j in range(16)])]
+    one = attr.attribute_sources(train, test, normalized_grad=normalized)
+    grouped = attr.attribute_sources(train, test, normalized_grad=normalized, train_blocks_per_pass=3)
+    assert grouped.row_train_ids == one.row_train_ids and grouped.row_steps == one.row_steps
+    # one bf16 rounding of each score apart at most, should the kernel split its sums differently
+    assert_parity(grouped.scores, one.scores, torch.bfloat16, tight=roundings(1))

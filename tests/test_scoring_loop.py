@@ -307,3 +307,32 @@ def test_duplicate_test_samples_share_a_column(loop_over_test):
     want = tr @ torch.stack([a.data["l1"][0], b.data["l1"][1]]).T
     assert torch.allclose(scores, want, atol=1e-5)
     assert int((scores.abs().sum(0) == 0).sum()) == 0
+
+
+@pytest.mark.parametrize("per_pass", [2, 3, 8])
+def test_train_blocks_per_pass_groups_dense_passes(per_pass):
+    """Grouped train blocks give the block-by-block scores, rows and steps; the
+    hook sees groups of ``per_pass`` blocks (the last one shorter)."""
+    train, test = Source(stream(5)), Source([(0, dense_block(seed=100), ["t0", "t1"])])
+    seen = []
+
+    def group(reps):
+        seen.append(len(reps))
+        data = torch.cat([flat(r) for r in reps])
+        return Gradient({"l1": "materialized"}, {"l1": data}, {"l1": "nn.Linear"})
+
+    want = score_sources(train, test, "cpu", inner_product=dot)
+    got = score_sources(train, test, "cpu", inner_product=dot, train_blocks_per_pass=per_pass, dense_group=group)
+    assert torch.allclose(got[0], want[0], atol=1e-5) and got[1:4] == want[1:4]
+    assert seen == [per_pass] * (5 // per_pass) + ([5 % per_pass] if 5 % per_pass else [])
+    with pytest.raises(ValueError, match="dense_group"):
+        score_sources(train, test, "cpu", inner_product=dot, train_blocks_per_pass=2)
+
+
+def test_train_blocks_per_pass_needs_one_dense_test_block():
+    """A factorized or multi-block test side keeps the block-by-block loop."""
+    train, test = Source(stream(3)), Source([(0, factorized_block(seed=100), ["t0", "t1"])])
+    calls = []
+    score_sources(train, test, "cpu", inner_product=dot, train_blocks_per_pass=2,
+                  dense_group=lambda reps: calls.append(reps))
+    assert calls == []
