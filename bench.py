@@ -48,6 +48,9 @@ for _p in (os.path.join(REPO, "dattri-llm_amd"), REPO):
 
 METRIC = "train×query pair-scores/sec (Llama-8B-shaped block, bf16); MFMA util % of peak"
 PEAK_BF16_TFLOPS = 2500.0
+# C4: train blocks scored per pass over the dense query block (score_sources' train_blocks_per_pass);
+# 4 x 8 rows fill the score kernel's 32-row side.
+PASS = 4
 PEAK_HBM_GBS = 8000.0
 
 D_MODEL, D_KV, D_FFN = 4096, 1024, 14336
@@ -104,6 +107,28 @@ def dense_block(acts, grads, norms, timers=None):
         ev = _ev(timers, f"materialize:{name}")
         out[name] = kernels.materialize_linear(acts[act], grads[name], blocked=True)
         _ev_end(ev)
+    return out
+
+
+def dense_group(acts, grads, norms, n_blocks):
+    """``dense_block`` of ``n_blocks`` train blocks stacked along the batch: each
+    linear layer's blocks written into row slices of one k-blocked buffer (the
+    layout one score pass reads for all of them)."""
+    import torch
+
+    from dattri_llm_amd import kernels
+
+    out = {}
+    for name, _d in NORMS:
+        x, g = norms[name]
+        out[name] = torch.cat([kernels.norm_weight_grad(x, g, kind=0, eps=RMS_EPS, out_dtype=torch.bfloat16)
+                               for _ in range(n_blocks)])
+    for name, act, din, dout in LINEARS:
+        b = acts[act].shape[0]
+        buf = kernels.blocked_storage(n_blocks * b, din * dout, torch.bfloat16, acts[act].device)
+        for i in range(n_blocks):
+            kernels.materialize_linear(acts[act], grads[name], blocked=True, out=buf[i * b:(i + 1) * b])
+        out[name] = buf
     return out
 
 
@@ -260,7 +285,8 @@ def bench_block(args):
     test_source = [(0, routed, [f"query{j}" for j in range(n_query)])]
 
     def attribute(k):
-        return attr.attribute_sources(((step, train, train_ids) for step in range(k)), test_source)
+        return attr.attribute_sources(((step, train, train_ids) for step in range(k)), test_source,
+                                      train_blocks_per_pass=PASS)
 
     attribute(args.warmup)
     torch.cuda.synchronize()
@@ -272,33 +298,39 @@ def bench_block(args):
     assert score.scores.shape == (n_train * args.steps, n_query)
 
     def event_ms(name):
-        return sum(s.elapsed_time(e) for s, e in log.get(name, [])) / args.steps, len(log.get(name, [])) // args.steps
+        launches = log.get(name, [])
+        return sum(s.elapsed_time(e) for s, e in launches) / args.steps, round(len(launches) / args.steps, 4)
 
-    # The same step as raw kernel calls (no boundary): dW of the 7 linears, 2 norm grads, one score GEMM.
+    # The same steps as raw kernel calls (no boundary), grouped alike: per group of
+    # PASS train blocks, dW of the 7 linears and 2 norm grads per block, one score GEMM.
     q_dense = {n: routed.data[n] for n in routed.data}
     names = list(train.data)  # the order layerwise_cross_dot sums the layers in
-    raw_scores = torch.empty(n_train, n_query, dtype=torch.float32, device="cuda")
+    raw_scores = torch.empty(PASS * n_train, n_query, dtype=torch.float32, device="cuda")
 
-    def raw_step():
-        tr = dense_block(*train_fac)
-        kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=raw_scores)
+    def raw_steps(k):
+        for first in range(0, k, PASS):
+            nb = min(PASS, k - first)
+            tr = dense_group(*train_fac, nb)
+            kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=raw_scores[:nb * n_train])
+        return nb
 
-    for _ in range(args.warmup):
-        raw_step()
+    raw_steps(args.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        raw_step()
+    last = raw_steps(args.steps)
     torch.cuda.synchronize()
     raw_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    # the drop-in scores are the raw ones rounded to the compute dtype (bf16)
-    same = bool(torch.equal(score.scores[-n_train:], raw_scores.to(torch.bfloat16).float().cpu()))
+    # the drop-in scores are the raw ones rounded to the compute dtype (bf16); compare the last group
+    rows = last * n_train
+    same = bool(torch.equal(score.scores[-rows:], raw_scores[:rows].to(torch.bfloat16).float().cpu()))
 
     # Algorithmic work.
     dk = {n: din * dout for n, _a, din, dout in LINEARS}
     width = sum(dk.values()) + sum(d for _, d in NORMS)
     mat_flops = sum(2.0 * n_train * t_train * v for v in dk.values())
-    score_bytes = (n_train + n_query) * width * 2.0
+    # one score launch reads PASS train blocks and the queries once
+    score_bytes_launch = (PASS * n_train + n_query) * width * 2.0
+    score_bytes = score_bytes_launch / PASS  # per step
     norm_bytes = 2.0 * n_train * t_train * D_MODEL * 2
     t_mat, n_mat = event_ms("materialize_linear")
     t_score, n_score = event_ms("score_gemm")
@@ -322,7 +354,7 @@ def bench_block(args):
         gbs = score_bytes / t_score / 1e6
         roof = {"bound": "hbm", "kernel": big, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                "work_per_launch": f"{score_bytes:.4g} B (72 rows x {width} weights x 2 B)",
+                "work_per_launch": f"{score_bytes_launch:.4g} B ({PASS * n_train + n_query} rows x {width} weights x 2 B)",
                 "launches_per_step": n_score}
     elif big == "materialize_tiles_tr":
         tf = mat_flops / (t_mat * 1e9)
@@ -356,8 +388,10 @@ def bench_block(args):
         "data": "synthetic",
         "config": {
             "workload": "llama3-8b-block: 8 train x 2048 tok vs 64 query x 512 tok, 7 linears + 2 RMSNorm, "
-                        "TracInAttributor.attribute_sources (cost-rule routing per layer)",
+                        "TracInAttributor.attribute_sources (cost-rule routing per layer; 4 train blocks "
+                        "per pass over the dense queries)",
             "train_block": [n_train, t_train],
+            "train_blocks_per_query_pass": PASS,
             "query_block": [n_query, t_query],
             "score_width_per_sample": width,
             "routes": routes,
