@@ -2,7 +2,7 @@
 
     python dattri-llm_amd/build.py          # or __graft_entry__.build()
 
-Compiles every ``csrc/*.hip`` into one shared library next to the Python
+Compiles every ``csrc/*.hip`` (in parallel, objects under ``_build/``) into one shared library next to the Python
 package (``dattri_llm_amd/libdattri_amd.so``).  Always recompiles.
 """
 
@@ -13,12 +13,14 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "dattri_llm_amd", "libdattri_amd.so")
+OBJ_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 FLAGS = [
@@ -29,6 +31,10 @@ FLAGS = [
     "-shared",
     "-Wall",
     "-Wno-unused-function",
+    # Inline assembly must declare every register it touches as an operand:
+    # a clobber the compiler cannot honour (a reserved register such as M0)
+    # fails the build instead of warning.
+    "-Werror=inline-asm",
     # Packed fp32 VALU forms are kept out of the generated code.
     "-Xclang",
     "-target-feature",
@@ -46,12 +52,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build the HIP kernels)")
 
 
-def build(verbose: bool = False) -> str:
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    if not sources:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *FLAGS, *sources, "-o", tmp]
+def _run(cmd: list, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -61,6 +62,29 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{stderr}")
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile each source to an object in parallel, then link the library.
+
+    Every ``.hip`` file is a self-contained translation unit (its kernels and
+    their ``extern "C"`` launchers), so the objects link without relocatable
+    device code.
+    """
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objects = [os.path.join(OBJ_DIR, os.path.basename(s)[:-4] + ".o") for s in sources]
+    jobs = jobs or min(len(sources), os.cpu_count() or 1, 16)
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        futures = [pool.submit(_run, [hipcc(), *compile_flags, "-c", s, "-o", o], verbose)
+                   for s, o in zip(sources, objects)]
+        for f in futures:
+            f.result()
+    tmp = OUT + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp], verbose)
     os.replace(tmp, OUT)
     return OUT
 

@@ -199,22 +199,25 @@ typedef __attribute__((address_space(3))) char lds_char;
 // One 16-byte-per-lane buffer load into LDS at lds_addr + 16 * lane (M0 holds
 // the wave-uniform LDS byte address).  Inline assembly, so the compiler does
 // not wait for every outstanding load before each LDS read (it cannot tell a
-// ring's stages apart); callers wait with explicit vmcnt counts.  An offset
-// at or past the resource's range reads zeros and touches no memory.
+// ring's stages apart); callers wait with explicit vmcnt counts.  The LDS
+// address is an operand bound to M0 ("{m0}"), so the compiler writes M0
+// itself and knows the statement reads it: nothing it keeps in M0 (LDS
+// bounds, other DMA addresses) is overwritten behind its back.  An offset at
+// or past the resource's range reads zeros and touches no memory.
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
+               : "v"(voff), "s"(rsrc), "{m0}"(lds_addr)
+               : "memory");
 }
 
 // The same with the non-temporal hint: for data read once (streamed factor
 // rows), so that it does not push data that is read again out of L2.
 __device__ __forceinline__ void dma16_nt(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds"
                :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
+               : "v"(voff), "s"(rsrc), "{m0}"(lds_addr)
+               : "memory");
 }
 
 // Raw buffer resource over [base, base + bytes) (stride 0: byte offsets).
