@@ -14,6 +14,7 @@ the layerwise cross-gram (base.py:657-675).
 from __future__ import annotations
 
 import gc
+import os
 from typing import ClassVar
 
 import torch
@@ -23,7 +24,16 @@ from dattri_llm_amd.attribution.score import AttributionScore
 from dattri_llm_amd.attribution.utils import score_sources
 from dattri_llm_amd.gradient import ops
 from dattri_llm_amd.gradient.gradient import Gradient
+from dattri_llm_amd.gradient.store import GradientStore, PinnedBlockSource
 from dattri_llm_amd.utils.cache import CacheBudget
+
+
+def normalize_layer_names(layer_name) -> list[str] | None:
+    """``None`` (every stored layer), one name, or several, as a list or None
+    (attribution/utils.py:38-51)."""
+    if layer_name is None:
+        return None
+    return [layer_name] if isinstance(layer_name, str) else list(layer_name)
 
 
 class InnerProductAttributor:
@@ -90,9 +100,58 @@ class InnerProductAttributor:
 
     # -- the scoring pass -----------------------------------------------------
 
+    @staticmethod
+    def resolve_store(source) -> GradientStore:
+        """The store behind a directory, an open :class:`GradientStore`, or a
+        :class:`PinnedBlockSource` over one (base.py:1058-1071)."""
+        if isinstance(source, GradientStore):
+            return source
+        if isinstance(source, PinnedBlockSource):
+            return source.store
+        if isinstance(source, (str, os.PathLike)):
+            if not os.path.isdir(source):
+                raise FileNotFoundError(f"no gradient store at {os.fspath(source)!r}")
+            return GradientStore(source)
+        raise TypeError("expected a store directory, a GradientStore, or a PinnedBlockSource, "
+                        f"got {type(source).__name__}.")
+
+    def attribute_from_cache(self, train_source, test_source, *, selected_training_steps=None, layer_name=None,
+                             verbose: bool = False, loop_over_test: bool = False, algorithm_meta: dict | None = None,
+                             attribution_granularity: str = "instance", train_blocks_per_pass: int = 1,
+                             **attribution_kwargs) -> AttributionScore:
+        """Score stored gradients: every train record against every test
+        record (the store-then-attribute path, base.py:1073-1152).
+
+        The sources may be store directories, open stores or block sources
+        over them; rows and columns are the train / test ids in store order,
+        each row stamped with its recorded step.  ``selected_training_steps``
+        keeps the stored steps among these (at least one must be present);
+        ``layer_name`` scores a subset of the stored layers; ``loop_over_test``
+        re-reads the test store per train block instead of caching it once.
+        ``verbose`` is accepted for the reference's signature (this path draws
+        no progress bars).  ``algorithm_meta`` and any further keyword
+        arguments are recorded in the score's metadata, beside the selected
+        steps, each store's sample-id scheme and the granularity.
+        ``train_blocks_per_pass`` is :meth:`score`'s grouping of dense train
+        blocks (the scores do not depend on it)."""
+        if attribution_granularity not in {"instance", "token"}:
+            raise ValueError(f"attribution_granularity must be 'instance' or 'token', "
+                             f"got {attribution_granularity!r}.")
+        train_store, test_store = self.resolve_store(train_source), self.resolve_store(test_source)
+        layers = normalize_layer_names(layer_name)
+        train = PinnedBlockSource(train_store, device=self.device, steps=selected_training_steps, layer_name=layers)
+        test = PinnedBlockSource(test_store, device=self.device, layer_name=layers)
+        meta = {"selected_training_steps": list(train.steps),
+                "sample_id_key": {"train": train_store.sample_id_key, "test": test_store.sample_id_key},
+                "attribution_granularity": attribution_granularity,
+                **(algorithm_meta or {}), **attribution_kwargs}
+        return self._score(train, test, batch_size=None, loop_over_test=loop_over_test,
+                           attribution_granularity=attribution_granularity, algorithm_meta=meta,
+                           train_blocks_per_pass=train_blocks_per_pass, layer_name=layers)
+
     def _score(self, train_source, test_source, *, batch_size: int | None, loop_over_test: bool,
                attribution_granularity: str, algorithm_meta: dict,
-               train_blocks_per_pass: int = 1) -> AttributionScore:
+               train_blocks_per_pass: int = 1, layer_name: list[str] | None = None) -> AttributionScore:
         """Fit, then run the scoring loop with each query block transformed and
         routed once; the result in the reference's score format.
         ``train_blocks_per_pass`` > 1 scores that many dense train blocks per
@@ -113,7 +172,7 @@ class InnerProductAttributor:
                 train_blocks_per_pass=train_blocks_per_pass, dense_group=self.dense_train_group,
             )
             return AttributionScore(scores=scores, row_train_ids=row_ids, row_steps=row_steps, test_ids=test_ids,
-                                    algorithm=self.algorithm, algorithm_meta=algorithm_meta, layer_name=None,
+                                    algorithm=self.algorithm, algorithm_meta=algorithm_meta, layer_name=layer_name,
                                     row_token_ids=row_tokens)
         finally:
             if gc_was_enabled:

@@ -128,15 +128,24 @@ class AttributionScore:
         return self.scores[:, self._require_test(test_hash)]
 
     def step_matrix(self, step: int) -> tuple[list[str], torch.Tensor]:
+        """The rows recorded at ``step`` (score.py:278-304): instance rows as
+        stored, in row order (a sample stored twice at one step keeps both
+        rows); token rows summed per sample, in first-seen order."""
         rows = [i for i, s in enumerate(self.row_steps) if s == step]
         if not rows:
             raise KeyError(f"step {step} not present in scores.")
+        if self.row_token_ids is None:
+            return [self.row_train_ids[i] for i in rows], self.scores[rows]
         ids = list(dict.fromkeys(self.row_train_ids[i] for i in rows))
         pos = {h: i for i, h in enumerate(ids)}
         out = self.scores.new_zeros(len(ids), self.num_test)
         for i in rows:
             out[pos[self.row_train_ids[i]]] += self.scores[i]
         return ids, out
+
+    def step_matrices(self) -> dict[int, tuple[list[str], torch.Tensor]]:
+        """``{step: step_matrix(step)}`` for every recorded step, ascending (score.py:306-318)."""
+        return {step: self.step_matrix(step) for step in sorted(set(self.row_steps))}
 
     def score_at(self, train_hash: str, step: int, test_hash: str) -> torch.Tensor:
         col = self._require_test(test_hash)

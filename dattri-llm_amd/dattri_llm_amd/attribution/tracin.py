@@ -91,6 +91,20 @@ class TracInAttributor(InnerProductAttributor):
         dot = ops.layerwise_cross_dot_per_token(train_rep, test_rep)
         return dot if self._metric == "dot" else self._cosine(dot, train_rep, test_rep, layers)
 
+    def attribute_from_cache(self, train_source, test_source, *, selected_training_steps=None, layer_name=None,
+                             verbose: bool = False, loop_over_test: bool = False, algorithm_meta: dict | None = None,
+                             attribution_granularity: str = "instance", normalized_grad: bool = False,
+                             train_blocks_per_pass: int = 1) -> AttributionScore:
+        """Score stored gradients (tracin.py:186-215); ``normalized_grad``
+        selects GradCos and is recorded in the metadata.  The other arguments
+        are :meth:`InnerProductAttributor.attribute_from_cache`'s."""
+        self._set_metric(normalized_grad)
+        return super().attribute_from_cache(
+            train_source, test_source, selected_training_steps=selected_training_steps, layer_name=layer_name,
+            verbose=verbose, loop_over_test=loop_over_test, algorithm_meta=algorithm_meta,
+            attribution_granularity=attribution_granularity, train_blocks_per_pass=train_blocks_per_pass,
+            normalized_grad=normalized_grad)
+
     def attribute_sources(self, train_source, test_source, *, normalized_grad: bool = False,
                           batch_size: int | None = None, loop_over_test: bool = False,
                           attribution_granularity: str = "instance",

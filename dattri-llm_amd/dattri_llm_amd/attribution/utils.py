@@ -138,7 +138,11 @@ def score_sources(
     one dense block): that many train blocks are made dense together by
     ``dense_group(reps) -> Gradient`` and scored in one pass over the test
     block, which is then read once per group instead of once per train block.
-    The scores are those of the block-by-block loop.
+    The scores are those of the block-by-block loop.  A group holds no more
+    blocks than ``cache_budget`` has room for (their dense rows, re-read at
+    the start of every group), and blocks that cannot be stacked with the
+    same scores (:func:`groupable`: differing layers, broadcast or batch-level
+    layers) are scored one at a time.
 
     Returns ``(scores (rows, num_test) fp32 CPU, row_train_ids, row_steps,
     test_ids, row_token_ids or None)``."""
@@ -208,19 +212,28 @@ def score_sources(
                 yield steps, transform_train(train_g.to(device)), ids
             return
         group: list = []
+        limit = train_blocks_per_pass
 
-        def dense(group):
+        def flush(group):
             reps = [transform_train(g.to(device)) for _s, g, _i in group]
-            return ([s for st, _g, _i in group for s in st], dense_group(reps),
-                    [h for _s, _g, ids in group for h in ids])
+            if groupable(reps):
+                yield ([s for st, _g, _i in group for s in st], dense_group(reps),
+                       [h for _s, _g, ids in group for h in ids])
+                return
+            for (steps, _g, ids), rep in zip(group, reps, strict=True):
+                yield steps, rep, ids
 
         for item in train_blocks():
+            if not group:
+                # the group's dense rows must fit the budget beside what is
+                # already resident: re-read at the start of every group
+                limit = group_limit(item[1], train_blocks_per_pass, budget)
             group.append(item)
-            if len(group) == train_blocks_per_pass:
-                yield dense(group)
+            if len(group) >= limit:
+                yield from flush(group)
                 group = []
         if group:
-            yield dense(group)
+            yield from flush(group)
 
     for steps, train_rep, ids in scored_blocks():
         row = torch.zeros(n_rows(train_rep), num_test, dtype=torch.float32, device=device)
@@ -249,6 +262,40 @@ def score_sources(
             row_steps.extend(steps)
     scores = rows_out.result(num_test)
     return scores, row_ids, row_steps, test_ids, (row_tokens if per_token else None)
+
+
+def _layer_rows(value) -> int:
+    if isinstance(value, Factorized):
+        return value.as_batch_first().activation.shape[0]
+    return value.shape[0]
+
+
+def groupable(reps: list[Gradient]) -> bool:
+    """Whether train blocks can be stacked into one dense block with the
+    scores of the block-by-block loop: the same layers with the same types in
+    every block, each layer holding one row per sample (no broadcast row, no
+    batch-level ``param_grad`` layer, which the per-block loop treats apart)."""
+    first = reps[0]
+    names = list(first.data)
+    for rep in reps:
+        if list(rep.data) != names:
+            return False
+        for name in names:
+            layer_type = rep.layer_types.get(name)
+            if layer_type != first.layer_types.get(name) or layer_type == ops.PARAM_GRAD_TYPES:
+                return False
+            if _layer_rows(rep.data[name]) != rep.batch_size:
+                return False
+    return True
+
+
+def group_limit(block: Gradient, blocks_per_pass: int, budget: CacheBudget) -> int:
+    """How many train blocks like ``block`` to make dense together: at most
+    ``blocks_per_pass``, and no more than the budget holds (at least one)."""
+    per_block = block.materialized_nbytes
+    if per_block <= 0:
+        return blocks_per_pass
+    return max(1, min(blocks_per_pass, budget.room() // per_block))
 
 
 class _HostRows:

@@ -12,6 +12,8 @@ forms x_hat.  Results are in the resolved compute dtype with fp32 accumulation.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from dattri_llm_amd import kernels
@@ -173,6 +175,19 @@ def materialize_blocked(f, layer_type: str, include_bias: bool = True) -> torch.
     return out.to(out_dtype)
 
 
+_UNBLOCKED_GROUP_WARNED = False
+
+
+def _warn_unblocked_group() -> None:
+    global _UNBLOCKED_GROUP_WARNED
+    if not _UNBLOCKED_GROUP_WARNED:
+        _UNBLOCKED_GROUP_WARNED = True
+        warnings.warn("materialize_group: the blocks of a linear layer differ in form (a dense block, a bias "
+                      "column, other widths or dtypes), so the group is concatenated row-major instead of "
+                      "written k-blocked; scores are unchanged, the score GEMM reads it more slowly",
+                      RuntimeWarning, stacklevel=3)
+
+
 def materialize_group(values: list, layer_type: str, include_bias: bool = True) -> torch.Tensor:
     """The dense form of one layer over several train blocks, stacked along the batch.
 
@@ -201,6 +216,8 @@ def materialize_group(values: list, layer_type: str, include_bias: bool = True) 
             prepared.append((ao, go, out_dtype))
     shapes = {(ao.shape[-1], go.shape[-1], ao.dtype, od) for ao, go, od in prepared}
     if len(prepared) != len(values) or len(shapes) != 1:
+        if is_linear(layer_type):
+            _warn_unblocked_group()
         return torch.cat([materialize(f, layer_type, include_bias) for f in values])
     k, d, _dt, out_dtype = shapes.pop()
     rows = sum(ao.shape[0] for ao, _go, _od in prepared)

@@ -378,7 +378,9 @@ def _map_tensors(block: Gradient, fn) -> Gradient:
 
 
 class PinnedBlockSource:
-    """``(step, Gradient, hashes)`` blocks of a store, delivered on ``device``.
+    """``(step, Gradient, hashes)`` blocks of a store, delivered on ``device``
+    (a ROCm device through pinned buffers and a copy stream; the host, as
+    plain host tensors).
 
     ``steps``: the stored steps to read (``None``: all); ``layer_name``: a layer
     filter; ``prefetch``: host blocks the reader thread keeps ready."""
@@ -435,9 +437,23 @@ class PinnedBlockSource:
         except BaseException as exc:  # noqa: BLE001 - handed to the consumer
             self._put(out, exc, stop)
 
+    def _host_blocks(self):
+        """The blocks in host memory, one file at a time with no reader thread
+        or copy stream: the same records, for a source whose device is the
+        host."""
+        for file_rel, by_step in self.store.iter_steps(self.steps):
+            payload = self.store.read_meta(file_rel)
+            host = torch.empty(self.store.bin_nbytes(file_rel), dtype=torch.uint8)
+            self.store.read_bin_into(file_rel, host)
+            records = self.store.records_from(payload, host, file_rel)
+            for step, idxs in by_step.items():
+                block, hashes = records_to_block(records, idxs, self.layer_name)
+                yield step, block, hashes
+
     def __iter__(self):
         if self.device.type != "cuda":
-            raise ValueError("PinnedBlockSource delivers blocks to a ROCm device")
+            yield from self._host_blocks()
+            return
         q: queue.Queue = queue.Queue(maxsize=self.prefetch)
         stop = threading.Event()
         reader = threading.Thread(target=self._host_files, args=(q, stop), daemon=True)

@@ -10,6 +10,8 @@ provide.
 
 from __future__ import annotations
 
+import os
+import re
 from collections import OrderedDict
 from typing import Callable
 
@@ -17,43 +19,59 @@ import torch
 
 DEFAULT_CACHE_FRACTION = 0.35
 
+_MEM_AVAILABLE = re.compile(r"^MemAvailable:\s+(\d+)\s+kB", re.MULTILINE)
 
-def available_host_bytes() -> int:
+
+def host_free_bytes() -> int:
+    """Host memory a new allocation can take now: the kernel's MemAvailable
+    estimate (free plus reclaimable page cache), else the free physical pages."""
     try:
-        with open("/proc/meminfo", encoding="utf-8") as f:
-            for line in f:
-                if line.startswith("MemAvailable:"):
-                    return int(line.split()[1]) * 1024
-    except (OSError, ValueError, IndexError):
+        with open("/proc/meminfo", encoding="ascii") as f:
+            found = _MEM_AVAILABLE.search(f.read())
+        if found:
+            return int(found.group(1)) << 10
+    except OSError:
         pass
-    return 16 * 2**30
+    return os.sysconf("SC_AVPHYS_PAGES") * os.sysconf("SC_PAGE_SIZE")
+
+
+def device_free_bytes(device) -> int:
+    """Free bytes on ``device`` now (``None`` or a CPU device: the host)."""
+    if device is not None and device.type == "cuda":
+        return int(torch.cuda.mem_get_info(device)[0])
+    return host_free_bytes()
 
 
 class CacheBudget:
-    """Byte budget a cache may occupy on a device (``None`` = host)."""
+    """How many bytes a cache may hold on one device (``None``: the host).
+
+    A budget is a rule evaluated on demand, not a reservation: either the
+    fixed ``limit_bytes``, or ``fraction`` of what is free on the device at
+    the moment of asking, so a cache shrinks its claims as the rest of the
+    run allocates (the reference's ``utils/cache.py:89-131`` contract).
+    """
+
+    __slots__ = ("device", "fraction", "limit_bytes")
 
     def __init__(self, device=None, *, fraction: float = DEFAULT_CACHE_FRACTION,
                  limit_bytes: int | None = None) -> None:
-        self._device = torch.device(device) if device is not None else None
-        self._fraction = fraction
-        self._limit = limit_bytes
-
-    @property
-    def device(self):
-        return self._device
+        self.device = None if device is None else torch.device(device)
+        self.fraction = fraction
+        self.limit_bytes = limit_bytes
 
     def total(self) -> int:
-        """Bytes the cache may hold in total, right now."""
-        if self._limit is not None:
-            return self._limit
-        if self._device is not None and self._device.type == "cuda":
-            free, _total = torch.cuda.mem_get_info(self._device)
-            return int(free * self._fraction)
-        return int(available_host_bytes() * self._fraction)
+        """The budget's size in bytes, evaluated now."""
+        if self.limit_bytes is None:
+            return int(self.fraction * device_free_bytes(self.device))
+        return int(self.limit_bytes)
+
+    def room(self, held: int = 0) -> int:
+        """Bytes that may still be added on top of ``held`` (never negative)."""
+        return max(self.total() - held, 0)
 
     def fits(self, nbytes: int, held: int = 0) -> bool:
-        """Whether *nbytes* more may be cached given *held* bytes already are."""
-        return held + nbytes <= self.total()
+        """True when ``nbytes`` more fit on top of ``held``."""
+        return nbytes <= self.room(held)
 
 
 def _nbytes(value) -> int:

@@ -91,3 +91,41 @@ def assert_parity(got, ref, in_dtype, *, out_dtype=None, tight=None, label=""):
         return err
     assert err <= bound, f"{label} normwise error {err:.3e} above the tight bound {bound:.1e}"
     return err
+
+
+def _bf16_keys(bits):
+    """Monotone integer keys of bf16 bit patterns (int16 view): adjacent
+    representable values differ by 1, and +0 and -0 share key 0."""
+    import numpy as np
+
+    b = np.asarray(bits, dtype=np.int32) & 0xFFFF
+    mag = b & 0x7FFF
+    return np.where(b & 0x8000, -mag, mag)
+
+
+def assert_bf16_rounded(got, ref, *, max_ulps=1, max_frac=2e-3, label=""):
+    """Assert that the bf16 tensor ``got`` is the float64 ``ref`` rounded to
+    bf16, up to what fp32 accumulation in another order can leave: at most
+    ``max_frac`` of the entries off round-to-nearest-even(ref) at all, and none
+    more than ``max_ulps`` bf16 ulps off it unless its absolute error is
+    within TIGHT_FP32 of max|ref| (an entry summed down to near zero by
+    cancellation carries fp32's absolute error over a tiny ulp).  A systematic
+    relative error of a fraction of an ulp (a dropped term, a wrong scale)
+    moves a large share of the entries across a rounding boundary and fails
+    the first test; fp32 accumulation moves only entries within ~1e-6 of one."""
+    import numpy as np
+    import torch
+
+    assert got.dtype == torch.bfloat16, got.dtype
+    ref = np.asarray(ref, dtype=np.float64)
+    want = torch.from_numpy(ref.astype(np.float32)).to(torch.bfloat16)
+    got = got.detach().cpu().reshape(want.shape).contiguous()
+    dist = np.abs(_bf16_keys(got.view(torch.int16).numpy()) - _bf16_keys(want.view(torch.int16).numpy()))
+    frac = float(np.count_nonzero(dist)) / max(dist.size, 1)
+    scale = float(np.abs(ref).max()) if ref.size else 0.0
+    abs_err = np.abs(got.double().numpy() - ref)
+    far = (dist > max_ulps) & (abs_err > TIGHT_FP32 * scale)
+    worst = int(dist[far].max()) if far.any() else 0
+    assert not far.any(), f"{label}: {int(far.sum())} entries up to {worst} bf16 ulps from the rounded oracle"
+    assert frac <= max_frac, f"{label}: {frac:.2e} of entries off the rounded oracle (limit {max_frac:g})"
+    return frac

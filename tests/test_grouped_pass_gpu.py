@@ -53,3 +53,29 @@ def test_grouped_passes_give_the_block_scores(device, normalized):
     assert grouped.row_train_ids == one.row_train_ids and grouped.row_steps == one.row_steps
     # one bf16 rounding of each score apart at most, should the kernel split its sums differently
     assert_parity(grouped.scores, one.scores, torch.bfloat16, tight=roundings(1))
+
+
+def test_mixed_group_falls_back_to_row_major(device):
+    """A group mixing a dense block with factorized ones cannot be written
+    k-blocked: it is concatenated row-major (a plain (B, W) tensor) with the
+    same values, and says so once."""
+    import warnings
+
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.gradient import ops
+    from dattri_llm_amd.gradient.ops import materialize as mat
+
+    print("materialize_group: dense + factorized blocks", flush=True)
+    gen = torch.Generator().manual_seed(5)
+    blocks = [_block(gen, b, device) for b in (2, 3)]
+    dense_first = ops.materialize(blocks[0].data["up"], "nn.Linear")
+    values = [dense_first, blocks[1].data["up"]]
+    mat._UNBLOCKED_GROUP_WARNED = False
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        got = ops.materialize_group(values, "nn.Linear")
+        ops.materialize_group(values, "nn.Linear")
+    assert sum("k-blocked" in str(w.message) for w in caught) == 1
+    assert not kernels.is_blocked(got) and got.shape == (5, 40 * 128)
+    want = torch.cat([dense_first, ops.materialize(blocks[1].data["up"], "nn.Linear")])
+    assert torch.equal(got, want)

@@ -336,3 +336,73 @@ def test_train_blocks_per_pass_needs_one_dense_test_block():
     score_sources(train, test, "cpu", inner_product=dot, train_blocks_per_pass=2,
                   dense_group=lambda reps: calls.append(reps))
     assert calls == []
+
+
+def _two_layer_block(seed, b=B, layers=("l1", "l2"), broadcast=()):
+    g = torch.Generator().manual_seed(seed)
+    data = {n: torch.randn(1 if n in broadcast else b, D_IN * D_OUT, generator=g) for n in layers}
+    return Gradient(dict.fromkeys(data, "materialized"), data, dict.fromkeys(data, "nn.Linear"))
+
+
+def _layer_dot(train_rep, test_rep, *, dense_cache=None):
+    """Sum over the layers both sides hold; a one-row train layer is the
+    whole block's (broadcast) gradient."""
+    total = torch.zeros(train_rep.batch_size, test_rep.batch_size)
+    for name, m1 in train_rep.data.items():
+        if name in test_rep.data:
+            total += (m1 @ test_rep.data[name].T).expand(train_rep.batch_size, -1)
+    return total
+
+
+def _stack(reps):
+    data = {n: torch.cat([r.data[n] for r in reps]) for n in reps[0].data}
+    return Gradient(dict.fromkeys(data, "materialized"), data, dict.fromkeys(data, "nn.Linear"))
+
+
+@pytest.mark.parametrize("odd", ["missing_layer", "broadcast_layer", "other_type"])
+def test_train_blocks_per_pass_keeps_unstackable_blocks_apart(odd):
+    """A group whose blocks differ in their layers, or hold a broadcast
+    (one-row) layer, is scored block by block: the scores stay those of the
+    per-block loop and the stacking hook never sees such a group."""
+    blocks = [_two_layer_block(i) for i in range(4)]
+    if odd == "missing_layer":
+        blocks[1] = _two_layer_block(1, layers=("l1",))
+    elif odd == "broadcast_layer":
+        blocks[1] = _two_layer_block(1, broadcast=("l2",))
+    else:
+        blocks[1].layer_types["l2"] = "nn.Conv2d"
+    train = Source([(i, g, [f"h{i}-{j}" for j in range(B)]) for i, g in enumerate(blocks)])
+    test = Source([(0, _two_layer_block(100), ["t0", "t1"])])
+    seen = []
+
+    def group(reps):
+        seen.append(len(reps))
+        return _stack(reps)
+
+    want = score_sources(train, test, "cpu", inner_product=_layer_dot)
+    got = score_sources(train, test, "cpu", inner_product=_layer_dot, train_blocks_per_pass=2, dense_group=group)
+    assert torch.allclose(got[0], want[0], atol=1e-5) and got[1:4] == want[1:4]
+    assert seen == [2]  # blocks 0-1 are not stacked, blocks 2-3 are
+
+
+def test_train_blocks_per_pass_is_capped_by_the_budget():
+    """A group holds no more blocks than the cache budget has room for (their
+    dense rows), and at least one."""
+    from dattri_llm_amd.utils.cache import CacheBudget
+
+    blocks = [_two_layer_block(i) for i in range(5)]
+    per_block = blocks[0].materialized_nbytes
+    train = Source([(i, g, [f"h{i}-{j}" for j in range(B)]) for i, g in enumerate(blocks)])
+    test = Source([(0, _two_layer_block(100), ["t0", "t1"])])
+    want = score_sources(train, test, "cpu", inner_product=_layer_dot)
+    for room, sizes in ((2 * per_block + 1, [2, 2, 1]), (per_block - 1, [1, 1, 1, 1, 1]), (1 << 40, [4, 1])):
+        seen = []
+
+        def group(reps):
+            seen.append(len(reps))
+            return _stack(reps)
+
+        got = score_sources(train, test, "cpu", inner_product=_layer_dot, train_blocks_per_pass=4,
+                            dense_group=group, cache_budget=CacheBudget(limit_bytes=room))
+        assert torch.allclose(got[0], want[0], atol=1e-5) and got[1:4] == want[1:4]
+        assert seen == sizes, (room, seen)

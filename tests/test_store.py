@@ -224,3 +224,114 @@ def test_layer_name_pulls_in_invocation_layers():
     assert block.layer_names == {"fc", "fc@2"}
     with pytest.raises(KeyError, match="Unknown layers"):
         records_to_block(recs, [0], ["fc@3"])
+
+
+# ---------------------------------------------------------------------------
+# attribute_from_cache: the store-then-attribute entry point's host logic
+# ---------------------------------------------------------------------------
+
+
+def _dense_store(root, steps, per_step, seed, widths=(("a", 6), ("b", 4))):
+    """A store of dense per-sample layers: ``per_step`` records of one sample
+    at every step of ``steps``."""
+    store = GradientStore(root)
+    gen = torch.Generator().manual_seed(seed)
+    for step in steps:
+        recs = []
+        for i in range(per_step):
+            data = {n: torch.randn(1, w, generator=gen) for n, w in widths}
+            g = Gradient(dict.fromkeys(data, "materialized"), data, dict.fromkeys(data, "nn.Linear"))
+            recs.append(GradientRecord(step, [f"s{seed}-{step}-{i}"], g))
+        store.save_bulk(recs)
+    return store
+
+
+def _rows(store, steps=None, layers=None):
+    """(ids, steps, (n, width) matrix) of a store's records in store order."""
+    ids, st, rows = [], [], []
+    for file_rel, by_step in store.iter_steps(steps or store.available_steps()):
+        recs = store.load_records(file_rel)
+        for step, idxs in by_step.items():
+            block, hashes = records_to_block(recs, idxs, layers)
+            ids += hashes
+            st += [step] * len(hashes)
+            rows.append(torch.cat([block.data[n] for n in sorted(block.data)], 1))
+    return ids, st, torch.cat(rows)
+
+
+class _HostTracIn:
+    """A TracIn attributor whose block products run on the host (the kernels
+    are exercised on the GPU): dense layers only, no query routing."""
+
+    def __new__(cls, **kw):
+        from dattri_llm_amd.attribution import TracInAttributor
+
+        class Host(TracInAttributor):
+            def route_test_rep(self, test_rep):
+                return test_rep
+
+            def inner_product(self, train_rep, test_rep, *, dense_cache=None):
+                names = sorted(n for n in train_rep.data if n in test_rep.data)
+                m1 = torch.cat([train_rep.data[n] for n in names], 1)
+                m2 = torch.cat([test_rep.data[n] for n in names], 1)
+                return m1 @ m2.T
+
+        return Host(device="cpu", **kw)
+
+
+def test_attribute_from_cache_reads_stores_in_order(tmp_path):
+    from dattri_llm_amd.gradient.store import PinnedBlockSource
+
+    train = _dense_store(tmp_path / "train", [1, 2, 3], 2, 10)
+    test = _dense_store(tmp_path / "test", [0], 3, 20)
+    ids, steps, m1 = _rows(train)
+    test_ids, _s, m2 = _rows(test)
+    attr = _HostTracIn(train_batch_size=2)
+    for tr, te in ((tmp_path / "train", str(tmp_path / "test")), (train, test),
+                   (PinnedBlockSource(train, device="cpu"), PinnedBlockSource(test, device="cpu"))):
+        got = attr.attribute_from_cache(tr, te)
+        assert got.row_train_ids == ids and got.row_steps == steps and got.test_ids == test_ids
+        torch.testing.assert_close(got.scores, m1 @ m2.T)
+        assert got.algorithm == "TracIn" and got.layer_name is None
+        assert got.algorithm_meta["selected_training_steps"] == [1, 2, 3]
+        assert got.algorithm_meta["sample_id_key"] == {"train": None, "test": None}
+        assert got.algorithm_meta["attribution_granularity"] == "instance"
+        assert got.algorithm_meta["normalized_grad"] is False
+    # the per-step view of the result
+    mats = got.step_matrices()
+    assert list(mats) == [1, 2, 3]
+    for step, (step_ids, mat) in mats.items():
+        rows = [i for i, s in enumerate(steps) if s == step]
+        assert step_ids == [ids[i] for i in rows] and torch.equal(mat, got.scores[rows])
+
+
+def test_attribute_from_cache_selection_and_options(tmp_path):
+    train = _dense_store(tmp_path / "train", [1, 2, 3], 2, 11)
+    test = _dense_store(tmp_path / "test", [0], 2, 21)
+    attr = _HostTracIn(train_batch_size=4)
+    # over-specified steps are intersected with the stored ones
+    got = attr.attribute_from_cache(train, test, selected_training_steps=[2, 9], algorithm_meta={"run": "x"})
+    ids, steps, m1 = _rows(train, [2])
+    _t, _s, m2 = _rows(test)
+    assert got.row_train_ids == ids and set(got.row_steps) == {2}
+    torch.testing.assert_close(got.scores, m1 @ m2.T)
+    assert got.algorithm_meta["selected_training_steps"] == [2] and got.algorithm_meta["run"] == "x"
+    with pytest.raises(ValueError, match="requested steps"):
+        attr.attribute_from_cache(train, test, selected_training_steps=[7])
+    # a layer subset, given as one name
+    got = attr.attribute_from_cache(train, test, layer_name="b")
+    _i, _s, m1b = _rows(train, layers=["b"])
+    _t, _s, m2b = _rows(test, layers=["b"])
+    torch.testing.assert_close(got.scores, m1b @ m2b.T)
+    assert got.layer_name == ["b"]
+    # re-reading the test store per train block gives the same scores
+    again = attr.attribute_from_cache(train, test, loop_over_test=True)
+    torch.testing.assert_close(again.scores, attr.attribute_from_cache(train, test).scores)
+    cos = attr.attribute_from_cache(train, test, normalized_grad=True)
+    assert cos.algorithm == "GradCos" and cos.algorithm_meta["normalized_grad"] is True
+    with pytest.raises(ValueError, match="granularity"):
+        attr.attribute_from_cache(train, test, attribution_granularity="sample")
+    with pytest.raises(FileNotFoundError):
+        attr.attribute_from_cache(tmp_path / "absent", test)
+    with pytest.raises(TypeError, match="store directory"):
+        attr.attribute_from_cache(42, test)

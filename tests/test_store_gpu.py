@@ -87,3 +87,30 @@ def test_async_writer_from_device(device, tmp_path):
     for a, b in zip(loaded, recs):
         assert torch.equal(a.gradient.data["proj"], b.gradient.data["proj"])
         assert torch.equal(a.gradient.data["mlp"].activation, b.gradient.data["mlp"].activation)
+
+
+@pytest.mark.parametrize("normalized", [False, True])
+def test_attribute_from_cache_equals_attribute_sources(device, tmp_path, normalized):
+    """The store-then-attribute entry point on two store directories gives the
+    scores, rows and columns of attribute_sources over block sources of the
+    same stores."""
+    from dattri_llm_amd.attribution import TracInAttributor
+
+    print(f"attribute_from_cache vs attribute_sources, normalized={normalized}", flush=True)
+    train = _fill(tmp_path / "train", 3, 2, 500)
+    test = _fill(tmp_path / "test", 1, 2, 600)
+    ref = TracInAttributor(train_batch_size=4, device=device).attribute_sources(
+        PinnedBlockSource(train, device=device), PinnedBlockSource(test, device=device), normalized_grad=normalized)
+    got = TracInAttributor(train_batch_size=4, device=device).attribute_from_cache(
+        tmp_path / "train", str(tmp_path / "test"), normalized_grad=normalized)
+    assert got.row_train_ids == ref.row_train_ids and got.row_steps == ref.row_steps
+    assert got.test_ids == ref.test_ids and torch.equal(got.scores, ref.scores)
+    assert got.algorithm == ("GradCos" if normalized else "TracIn")
+    assert got.algorithm_meta["selected_training_steps"] == train.available_steps()
+    one_step = TracInAttributor(train_batch_size=4, device=device).attribute_from_cache(
+        train, test, selected_training_steps=[1], layer_name="proj", normalized_grad=normalized)
+    ref1 = TracInAttributor(train_batch_size=4, device=device).attribute_sources(
+        PinnedBlockSource(train, device=device, steps=[1], layer_name="proj"),
+        PinnedBlockSource(test, device=device, layer_name="proj"), normalized_grad=normalized)
+    assert one_step.row_train_ids == ref1.row_train_ids and torch.equal(one_step.scores, ref1.scores)
+    assert set(one_step.row_steps) == {1} and one_step.layer_name == ["proj"]
