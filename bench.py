@@ -110,23 +110,23 @@ def dense_block(acts, grads, norms, timers=None):
     return out
 
 
-def dense_group(acts, grads, norms, n_blocks):
-    """``dense_block`` of ``n_blocks`` train blocks stacked along the batch: each
-    linear layer's blocks written into row slices of one k-blocked buffer (the
-    layout one score pass reads for all of them)."""
+def dense_group(blocks):
+    """``dense_block`` of several train blocks (``(acts, grads, norms)`` each)
+    stacked along the batch: each linear layer's blocks written into row
+    slices of one k-blocked buffer (the layout one score pass reads for all of
+    them)."""
     import torch
 
     from dattri_llm_amd import kernels
 
     out = {}
     for name, _d in NORMS:
-        x, g = norms[name]
-        out[name] = torch.cat([kernels.norm_weight_grad(x, g, kind=0, eps=RMS_EPS, out_dtype=torch.bfloat16)
-                               for _ in range(n_blocks)])
+        out[name] = torch.cat([kernels.norm_weight_grad(*norms[name], kind=0, eps=RMS_EPS, out_dtype=torch.bfloat16)
+                               for _a, _g, norms in blocks])
     for name, act, din, dout in LINEARS:
-        b = acts[act].shape[0]
-        buf = kernels.blocked_storage(n_blocks * b, din * dout, torch.bfloat16, acts[act].device)
-        for i in range(n_blocks):
+        b = blocks[0][0][act].shape[0]
+        buf = kernels.blocked_storage(len(blocks) * b, din * dout, torch.bfloat16, blocks[0][0][act].device)
+        for i, (acts, grads, _n) in enumerate(blocks):
             kernels.materialize_linear(acts[act], grads[name], blocked=True, out=buf[i * b:(i + 1) * b])
         out[name] = buf
     return out
@@ -270,9 +270,11 @@ def bench_block(args):
     from dattri_llm_amd.attribution import TracInAttributor
 
     n_train, t_train, n_query, t_query = 8, 2048, 64, 512
-    train_fac = make_block(n_train, t_train, seed=0)
+    # PASS distinct train blocks, cycled: the blocks of one group are
+    # different tensors, as a real source's are
+    train_facs = [make_block(n_train, t_train, seed=10 + i) for i in range(PASS)]
     query_fac = make_block(n_query, t_query, seed=1)
-    train = block_gradient(*train_fac)
+    trains = [block_gradient(*fac) for fac in train_facs]
     attr = TracInAttributor(train_batch_size=n_train, device="cuda")
     torch.cuda.synchronize()
 
@@ -284,9 +286,9 @@ def bench_block(args):
     train_ids = [f"train{i}" for i in range(n_train)]
     test_source = [(0, routed, [f"query{j}" for j in range(n_query)])]
 
-    def attribute(k):
-        return attr.attribute_sources(((step, train, train_ids) for step in range(k)), test_source,
-                                      train_blocks_per_pass=PASS)
+    def attribute(k, per_pass=PASS):
+        return attr.attribute_sources(((step, trains[step % PASS], train_ids) for step in range(k)), test_source,
+                                      train_blocks_per_pass=per_pass)
 
     attribute(args.warmup)
     torch.cuda.synchronize()
@@ -296,6 +298,13 @@ def bench_block(args):
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
     assert score.scores.shape == (n_train * args.steps, n_query)
+    # the same steps with the reference's schedule, one query pass per train block
+    attribute(args.warmup, per_pass=1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    attribute(args.steps, per_pass=1)
+    torch.cuda.synchronize()
+    ms_one = (time.perf_counter() - t0) * 1e3 / args.steps
 
     def event_ms(name):
         launches = log.get(name, [])
@@ -304,13 +313,14 @@ def bench_block(args):
     # The same steps as raw kernel calls (no boundary), grouped alike: per group of
     # PASS train blocks, dW of the 7 linears and 2 norm grads per block, one score GEMM.
     q_dense = {n: routed.data[n] for n in routed.data}
-    names = list(train.data)  # the order layerwise_cross_dot sums the layers in
     raw_scores = torch.empty(PASS * n_train, n_query, dtype=torch.float32, device="cuda")
+
+    names = list(trains[0].data)  # the order layerwise_cross_dot sums the layers in
 
     def raw_steps(k):
         for first in range(0, k, PASS):
             nb = min(PASS, k - first)
-            tr = dense_group(*train_fac, nb)
+            tr = dense_group([train_facs[(first + i) % PASS] for i in range(nb)])
             kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=raw_scores[:nb * n_train])
         return nb
 
@@ -343,7 +353,11 @@ def bench_block(args):
         "norm_weight_grad": {"ms_per_step": round(t_norm, 4), "launches_per_step": n_norm,
                              "gbs": round(2 * norm_bytes / t_norm / 1e6, 1)},
     }
-    mfma_util = mat_flops / (t_mat * 1e9) / PEAK_BF16_TFLOPS
+    dw_mfma_util = mat_flops / (t_mat * 1e9) / PEAK_BF16_TFLOPS
+    # the whole step's matrix work (dW of the 7 linears and the score GEMM)
+    # over the step's wall time: the MFMA utilisation of the step
+    step_flops = mat_flops + 2.0 * n_train * n_query * width
+    step_mfma_util = step_flops / (ms * 1e9) / PEAK_BF16_TFLOPS
 
     # Dominant kernel: the one taking most of the step (summed over its launches).
     # Its roofline is the step's algorithmic work over the summed event time,
@@ -396,7 +410,12 @@ def bench_block(args):
             "score_width_per_sample": width,
             "routes": routes,
         },
-        "mfma_util": round(mfma_util, 4),
+        "mfma_util": round(step_mfma_util, 4),
+        "mfma_util_basis": f"{step_flops:.4g} flop per step (dW + score GEMM) / step time / 2.5 PF/s bf16 peak",
+        "dw_mfma_util": round(dw_mfma_util, 4),
+        "one_block_per_pass": {"value": round(n_train * n_query / (ms_one / 1e3), 1), "ms_per_step": round(ms_one, 4),
+                               "schedule": "train_blocks_per_pass=1 (the reference's loop: one query pass per "
+                                           "train block)"},
         "query_prep_ms": round(query_prep_ms, 2),
         "kernels_only_ms": round(raw_ms, 4),
         "boundary_overhead": round(ms / raw_ms - 1.0, 4),
@@ -405,7 +424,8 @@ def bench_block(args):
         "kernels": kern,
     }
     if args.cpu_baseline:
-        result["cpu_baseline"], result["parity"] = cpu_baseline_block(train_fac, query_fac, score.scores[-n_train:])
+        last = train_facs[(args.steps - 1) % PASS]
+        result["cpu_baseline"], result["parity"] = cpu_baseline_block(last, query_fac, score.scores[-n_train:])
     return result
 
 

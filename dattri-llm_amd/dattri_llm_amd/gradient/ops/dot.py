@@ -22,6 +22,7 @@ compute dtype (the reference's contract).
 from __future__ import annotations
 
 import math
+import weakref
 from typing import TYPE_CHECKING
 
 import torch
@@ -123,10 +124,10 @@ def _linear_gram32(a1, g1, bias1, a2, g2, bias2, mode, out=None, accumulate=Fals
 # The factorized route over packed rows when most rows carry no gradient
 # ---------------------------------------------------------------------------
 
-# Take the packed route when the live rows' pairs are under this share of the
-# dense ghost's (B1*T1) x (B2*T2) rows: the packed kernel bins its products by
-# sample pair and runs at ~3/4 of the dense engine's rate, so it pays from
-# about half the work down.
+# Take the packed route when side 2's live rows are under this share of its
+# B2*T2 rows (so the live pairs are under it of the dense ghost's (B1*T1) x
+# (B2*T2)): the packed kernel bins its products by sample pair and runs at
+# ~3/4 of the dense engine's rate, so it pays from about half the work down.
 _PACKED_SHARE = 0.5
 
 
@@ -138,30 +139,59 @@ def _live_rows(x3: torch.Tensor, y3: torch.Tensor):
     return kernels.compact_rows(kernels.nonzero_rows(y3.reshape(b * t, y3.shape[-1])), b, t)
 
 
+# Live-row probes per gradient factor (keyed on the tensor a factor is a view
+# of, checked against the view's address, shape, strides and version): a
+# query block scored against every train block is read and counted once.
+_PROBES: weakref.WeakKeyDictionary = weakref.WeakKeyDictionary()
+
+
+def _probe_key(y3: torch.Tensor):
+    root = y3._base if y3._base is not None else y3
+    return root, (y3.data_ptr(), tuple(y3.shape), y3.stride(), y3._version)
+
+
 def _ghost_pairs(pairs, out: torch.Tensor) -> None:
     """Add the factorized cross-gram of every ``(a1, g1, a2, g2, bias)`` kernel
     operand pair (3-D, one dtype per pair) into ``out`` (fp32, (B1, B2)).
 
-    Each side's gradient-carrying rows are found on the device (one read of
-    its gradient factor) and packed per sample; one host read of the counts
-    for all pairs decides, per pair, between the dense ghost kernel and the
-    packed grouped kernel, which runs every packed pair of a dtype in ONE
-    launch.  Both give the same sums -- zero rows contribute nothing -- so the
-    choice changes speed only.  The packed kernel's grid is sized for all
-    B*T rows; tiles past the live rows return at once."""
+    Side 2 (the query side, scored against every train block) decides the
+    route: its gradient-carrying rows are found on the device and counted on
+    the host once per tensor.  When under ``_PACKED_SHARE`` of its rows live,
+    the pair's products are under that share of the dense ghost's for any
+    side 1, so side 1 is packed on the device too (no host read) and the
+    packed grouped kernel runs every such pair of a dtype in ONE launch;
+    otherwise the dense ghost kernel runs and side 1 is never probed, so a
+    dense train block costs no extra read and no host sync.  Both kernels give
+    the same sums -- zero rows contribute nothing -- so the choice changes
+    speed only.  The packed kernel's grid is sized for all B*T rows; tiles
+    past the live rows return at once."""
     probed, plain = [], []
     for pair in pairs:
         a1, _g1, a2, _g2, _bias = pair
         (plain if a1.shape[1] <= 1 and a2.shape[1] <= 1 else probed).append(pair)
-    live = [(_live_rows(a1, g1), _live_rows(a2, g2)) for a1, g1, a2, g2, _b in probed]
-    counts = torch.stack([torch.stack([s1[0][-1], s2[0][-1]]) for s1, s2 in live]).tolist() if live else []
+    side2, misses = [], []
+    for _a1, _g1, a2, g2, _b in probed:
+        root, sig = _probe_key(g2)
+        hit = _PROBES.get(root)
+        if hit is not None and hit[0] == sig:
+            side2.append(hit[1])
+        else:
+            seg, rows = _live_rows(a2, g2)
+            side2.append([seg, rows, None])
+            misses.append((root, sig, side2[-1]))
+    if misses:  # one host read for every newly probed side
+        counts = torch.stack([entry[0][-1] for _r, _s, entry in misses]).tolist()
+        for (root, sig, entry), n in zip(misses, counts):
+            entry[2] = int(n)
+            _PROBES[root] = (sig, entry)
     packed: dict[torch.dtype, tuple[list, list, list]] = {}
-    for pair, ((seg1, rows1), (seg2, rows2)), (n1, n2) in zip(probed, live, counts):
+    for pair, (seg2, rows2, n2) in zip(probed, side2):
         a1, g1, a2, g2, bias = pair
         rows_1, rows_2 = a1.shape[0] * a1.shape[1], a2.shape[0] * a2.shape[1]
-        if n1 * n2 >= _PACKED_SHARE * rows_1 * rows_2:
+        if n2 >= _PACKED_SHARE * rows_2:
             plain.append(pair)
             continue
+        seg1, rows1 = _live_rows(a1, g1)
         g_1, g_2, flags = packed.setdefault(a1.dtype, ([], [], []))
         g_1.append((a1.reshape(rows_1, -1), g1.reshape(rows_1, -1), seg1, rows1))
         g_2.append((a2.reshape(rows_2, -1), g2.reshape(rows_2, -1), seg2, rows2))

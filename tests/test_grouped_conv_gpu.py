@@ -32,29 +32,55 @@ def _cases():
     ]
 
 
-class _Capture:
-    """Raw captures (float64 on the CPU, fp32 on the device) and per-sample
-    autograd gradients of one module."""
+def _dense_layout(wg, bg, transposed, groups):
+    """One sample's (weight, bias) gradient placed where materialize puts it.
 
-    def __init__(self, factory, shape, device, seed=0, module=None):
+    Convolution: a row per output channel -- its kernel weights, then its
+    bias.  Transposed convolution (weight ``(C_in, C_out/g, *k)``): per group,
+    a row per input channel holding its weights to the group's output
+    channels, and with a bias one extra row carrying the group's output-channel
+    biases past those weight columns, zero before them."""
+    if not transposed:
+        rows = wg.flatten(1)
+        return (rows if bg is None else torch.column_stack([rows, bg])).flatten()
+    per_group = wg.flatten(1).unflatten(0, (groups, -1))  # (g, C_in/g, C_out/g * prod(k))
+    if bg is None:
+        return per_group.flatten()
+    bias = bg.unflatten(0, (groups, -1))  # (g, C_out/g)
+    width = per_group.shape[-1]
+    weights = nn.functional.pad(per_group, (0, bias.shape[-1]))
+    bias_row = nn.functional.pad(bias, (width, 0)).unsqueeze(1)
+    return torch.cat([weights, bias_row], dim=1).flatten()
+
+
+class _ConvCase:
+    """One module's raw captures (float64 on the host, fp32 on the device) and
+    its per-sample gradients from torch.func (a vmap over samples of the
+    gradient of sum(out * w))."""
+
+    def __init__(self, module, shape, device, seed):
+        from torch.func import functional_call, grad, vmap
+
         from dattri_llm_amd.gradient import ops
 
-        torch.manual_seed(seed)
-        self.module = module if module is not None else factory().double()
-        self.layer_type = f"nn.{type(self.module).__name__}"
-        self.kwargs = ops.extract_module_kwargs(self.module, self.layer_type)
-        self.x = torch.randn(B, *shape, dtype=torch.float64)
-        out = self.module(self.x)
-        self.w = torch.randn_like(out)
-        self.a, self.g = self.x.float().to(device), self.w.float().to(device)
-        self.ref = []
-        for i in range(B):
-            self.module.zero_grad()
-            (self.module(self.x[i:i + 1]) * self.w[i:i + 1]).sum().backward()
-            bias = self.module.bias
-            self.ref.append((self.module.weight.grad.detach().clone(),
-                             None if bias is None else bias.grad.detach().clone()))
-        self.module.zero_grad()
+        gen = torch.Generator().manual_seed(seed)
+        self.module = module
+        self.layer_type = "nn." + type(module).__name__
+        self.kwargs = ops.extract_module_kwargs(module, self.layer_type)
+        self.x = torch.randn(B, *shape, dtype=torch.float64, generator=gen)
+        with torch.no_grad():
+            w = torch.randn(module(self.x).shape, dtype=torch.float64, generator=gen)
+        self.a, self.g = self.x.float().to(device), w.float().to(device)
+        params = {n: p.detach() for n, p in module.named_parameters()}
+
+        def weighted_out(p, xi, wi):
+            return (functional_call(module, p, (xi[None],)) * wi[None]).sum()
+
+        per_sample = vmap(grad(weighted_out), in_dims=(None, 0, 0))(params, self.x, w)
+        bias = per_sample.get("bias")
+        self._flat = torch.stack([
+            _dense_layout(per_sample["weight"][i], None if bias is None else bias[i], self.transposed, self.groups)
+            for i in range(B)])
 
     @property
     def groups(self):
@@ -62,31 +88,11 @@ class _Capture:
 
     @property
     def transposed(self):
-        return "Transpose" in self.layer_type
+        return isinstance(self.module, nn.modules.conv._ConvTransposeNd)
 
     def ref_flat(self):
         """Per-sample gradients in the materialized layout (float64)."""
-        rows = []
-        for wg, bg in self.ref:
-            if self.transposed:
-                c_in = wg.shape[0]
-                g_, c_in_g = self.groups, c_in // self.groups
-                p_g = wg[0].numel()
-                blocks = wg.reshape(g_, c_in_g, p_g)
-                if bg is None:
-                    rows.append(blocks.reshape(-1))
-                    continue
-                c_out_g = bg.numel() // g_
-                full = torch.zeros(g_, c_in_g + 1, p_g + c_out_g, dtype=wg.dtype)
-                full[:, :c_in_g, :p_g] = blocks
-                full[:, -1, p_g:] = bg.reshape(g_, c_out_g)
-                rows.append(full.reshape(-1))
-            else:
-                block = wg.reshape(wg.shape[0], -1)
-                if bg is not None:
-                    block = torch.cat([block, bg.unsqueeze(-1)], dim=-1)
-                rows.append(block.reshape(-1))
-        return torch.stack(rows)
+        return self._flat
 
     def pre(self):
         from dattri_llm_amd.gradient import ops
@@ -98,11 +104,13 @@ class _Capture:
 def cap(request, device):
     _, factory, shape = request.param
     print(f"grouped conv case {request.param[0]}", flush=True)
-    return _Capture(factory, shape, device)
+    torch.manual_seed(0)
+    return _ConvCase(factory().double(), shape, device, seed=0)
 
 
 def _second(cap_, device):
-    return _Capture(None, tuple(cap_.x.shape[1:]), device, seed=1, module=cap_.module)
+    """Other samples through the same module."""
+    return _ConvCase(cap_.module, tuple(cap_.x.shape[1:]), device, seed=1)
 
 
 def _close(got, want, **tol):
