@@ -139,15 +139,31 @@ def _live_rows(x3: torch.Tensor, y3: torch.Tensor):
     return kernels.compact_rows(kernels.nonzero_rows(y3.reshape(b * t, y3.shape[-1])), b, t)
 
 
-# Live-row probes per gradient factor (keyed on the tensor a factor is a view
-# of, checked against the view's address, shape, strides and version): a
-# query block scored against every train block is read and counted once.
-_PROBES: weakref.WeakKeyDictionary = weakref.WeakKeyDictionary()
+# Live-row probes per gradient factor, keyed by the identity of the tensor a
+# factor is a view of (an entry leaves with that tensor) and checked against
+# the view's address, shape, strides and version: a query block scored
+# against every train block is read and counted once.
+_PROBES: dict[int, tuple] = {}
 
 
 def _probe_key(y3: torch.Tensor):
     root = y3._base if y3._base is not None else y3
     return root, (y3.data_ptr(), tuple(y3.shape), y3.stride(), y3._version)
+
+
+def _probe_get(root: torch.Tensor, sig):
+    hit = _PROBES.get(id(root))
+    return hit[2] if hit is not None and hit[0]() is root and hit[1] == sig else None
+
+
+def _probe_put(root: torch.Tensor, sig, entry) -> None:
+    key = id(root)
+
+    def drop(ref, key=key):
+        if _PROBES.get(key, (None,))[0] is ref:
+            del _PROBES[key]
+
+    _PROBES[key] = (weakref.ref(root, drop), sig, entry)
 
 
 def _ghost_pairs(pairs, out: torch.Tensor) -> None:
@@ -172,9 +188,9 @@ def _ghost_pairs(pairs, out: torch.Tensor) -> None:
     side2, misses = [], []
     for _a1, _g1, a2, g2, _b in probed:
         root, sig = _probe_key(g2)
-        hit = _PROBES.get(root)
-        if hit is not None and hit[0] == sig:
-            side2.append(hit[1])
+        hit = _probe_get(root, sig)
+        if hit is not None:
+            side2.append(hit)
         else:
             seg, rows = _live_rows(a2, g2)
             side2.append([seg, rows, None])
@@ -183,7 +199,7 @@ def _ghost_pairs(pairs, out: torch.Tensor) -> None:
         counts = torch.stack([entry[0][-1] for _r, _s, entry in misses]).tolist()
         for (root, sig, entry), n in zip(misses, counts):
             entry[2] = int(n)
-            _PROBES[root] = (sig, entry)
+            _probe_put(root, sig, entry)
     packed: dict[torch.dtype, tuple[list, list, list]] = {}
     for pair, (seg2, rows2, n2) in zip(probed, side2):
         a1, g1, a2, g2, bias = pair

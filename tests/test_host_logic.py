@@ -373,3 +373,25 @@ def test_locate_rows_identity_and_regroup_on_host():
     want = torch.zeros(2, 3, 1)
     want[1, 2, 0], want[0, 0, 0] = 1.0, 2.0
     assert torch.equal(dense, want)
+
+
+def test_ghost_probe_cache_follows_tensor_identity_and_version():
+    """The live-row probe cache of the factorized route: an entry is found
+    through any view of the same tensor, is stale once the tensor is written
+    in place, and leaves with the tensor."""
+    import gc
+    import importlib
+
+    dot = importlib.import_module("dattri_llm_amd.gradient.ops.dot")
+    g = torch.randn(3, 4, 5)
+    root, sig = dot._probe_key(g[:, :, :])
+    assert root is g
+    dot._probe_put(root, sig, ["seg", "rows", 7])
+    assert dot._probe_get(*dot._probe_key(g[:, :, :])) == ["seg", "rows", 7]
+    assert dot._probe_get(*dot._probe_key(g[:2])) is None  # another view: another shape
+    g.mul_(2.0)
+    assert dot._probe_get(*dot._probe_key(g[:, :, :])) is None
+    n = len(dot._PROBES)
+    del g, root
+    gc.collect()
+    assert len(dot._PROBES) == n - 1
