@@ -14,10 +14,11 @@
 // second tiny kernel sums the per-tile partials of each pair in a fixed order,
 // so results are deterministic.
 //
-// Two tile engines: the 256 x 128 engine (ghost_gram_tiles_v2 and the grouped
-// MoE form ghost_grouped_tiles_v2, below) takes dense and grouped launches
-// whose rows it can address with 32-bit offsets; the 128 x 128 kernels first
-// in this file take per-sample segmented sides and the rest.  Tile order:
+// Tile engines: the 256 x 128 tile on 8 waves (ghost_gram_tiles_v3 and the
+// grouped MoE form ghost_grouped_tiles_v3, below) takes dense and grouped
+// launches whose rows it can address with 32-bit offsets; the same tile on 4
+// waves runs the per-token form; the 128 x 128 kernels first in this file
+// take per-sample segmented sides and the rest.  Tile order:
 // workgroups are remapped so each XCD owns a contiguous run of tiles, grouped
 // a few row tiles wide, so the concurrently running tiles on one XCD share
 // their operand row blocks through that XCD's L2.
@@ -638,76 +639,178 @@ __device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, 
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Grouped (MoE) mode on the 256 x 128 engine: tiles over each group's packed
-// rows, the tile's products parked in LDS and binned by sample pair.
-template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void ghost_grouped_tiles_v2(GroupedArgs ga) {
-  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
-  // Tiles go to the XCDs round-robin in launch order (no XCD remap): the host
-  // orders the groups longest reduction first, so every XCD gets the same mix
-  // of tile lengths, longest first.  A contiguous range per XCD would hand the
-  // long groups' tiles to some XCDs and the short ones to the rest.
-  const int64_t logical = blockIdx.x;
-  int e = 0;
-  while (e + 1 < ga.n_groups && ga.grp[e + 1].tile0 <= logical) ++e;
-  const GroupDev& G = ga.grp[e];
-  const int64_t local = logical - G.tile0;
-  constexpr int64_t kRowGroup = 4;
-  const int64_t per_group = kRowGroup * G.tiles_c;
-  const int64_t grp = local / per_group;
-  const int64_t first_r = grp * kRowGroup;
-  const int64_t gsize = min(G.tiles_r - first_r, kRowGroup);
-  const int64_t in_group = local - grp * per_group;
-  const int64_t m = first_r + in_group % gsize;
-  const int64_t n = in_group / gsize;
+// ---------------------------------------------------------------------------
+// The same 256 x 128 tile on 8 waves (two per SIMD).  Wave w owns the 64 x 64
+// block at side-1 rows 64 (w / 2) and side-2 rows 64 (w % 2) of both Grams
+// (2 x 2 MFMA blocks each, 128 accumulators), so two waves fit one SIMD's
+// registers and one keeps the MFMA pipe busy while the other waits at a
+// barrier, for a load or on LDS.  A 32-byte K slice costs 4 fragment reads per
+// 4 MFMAs (8 reads per 8 with the 4-wave blocks of 128 x 64: 6); the stage,
+// ring, swizzle and row layout are the 4-wave engine's, with 6 DMA
+// instructions per wave and stage (wave w loads tile rows 48w .. 48w+47).
+// ---------------------------------------------------------------------------
+namespace v3 {
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kDma = v2::kRows * (v2::kSB / 16) / (kWave * kWaves);  // 6 per wave and stage
+static_assert(kDma == 6, "the vmcnt wait and the quarter split assume 6 DMA instructions per stage");
+// instructions [kLo[q], kLo[q + 1]) of a stage go out in quarter q
+__device__ __forceinline__ constexpr int lo(int q) { return q == 0 ? 0 : q == 1 ? 2 : q == 2 ? 3 : q == 3 ? 5 : 6; }
+}  // namespace v3
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t t0 = m * v2::kBM, s0 = n * v2::kBN;
-  // Rows at or past seg[B] belong to no sample (and may have no row_index entry).
-  const int64_t n1 = min(G.rows1, (int64_t)G.seg1[ga.b1]), n2 = min(G.rows2, (int64_t)G.seg2[ga.b2]);
-  // A tile wholly past the packed rows of a side owns no bin (the row count a
-  // caller passes may only bound seg[B]): nothing to compute.
-  if (t0 >= n1 || s0 >= n2) return;
-  TileSrc S;
-  S.ra1 = make_rsrc(G.a1, 0x7fffffffu);
-  S.rg1 = make_rsrc(G.g1, 0x7fffffffu);
-  S.ra2 = make_rsrc(G.a2, 0x7fffffffu);
-  S.rg2 = make_rsrc(G.g2, 0x7fffffffu);
-  S.kbytes_a = G.kbytes_a;
-  S.kbytes_g = G.kbytes_g;
+struct TileSrc8 {
+  u32x4 ra1, rg1, ra2, rg2;
+  uint32_t roff_a[v3::kDma], roff_g[v3::kDma];
+  int64_t kbytes_a, kbytes_g;
+};
+
+__device__ __forceinline__ int dma_row8(int w, int j, int lane) { return 8 * (v3::kDma * w + j) + (lane >> 3); }
+
+struct DmaState8 {
+  u32x4 ra1, rg1, ra2, rg2;
+  uint32_t roa[v3::kDma], rog[v3::kDma];
+  uint32_t cbyte, lds0;
+  int uwave, na, nst;
+  int64_t kba, kbg;
+};
+
+// Instructions [j0, j1) of stage st's loads for this wave (the 4-wave
+// engine's dma_quarter, 6 instructions per wave and stage).
+__device__ __forceinline__ void dma_part8(const DmaState8& D, int st, int j0, int j1) {
+  const bool act = st < D.na;
+  const uint32_t koff = (uint32_t)(act ? st : st - D.na) * v2::kSB;
+  const int64_t kb = act ? D.kba : D.kbg;
+  const bool kin = st < D.nst && (int64_t)(koff + D.cbyte) < kb;
+  const uint32_t base = D.lds0 + (uint32_t)((st % v2::kNBuf) * v2::kStage + v3::kDma * D.uwave * 8 * v2::kSB);
 #pragma unroll
-  for (int q = 0; q < v2::kDma; ++q) {
-    const int row = dma_row(wave, q, lane);
-    const bool side1 = row < v2::kBM;
-    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
-    const bool live = t < (side1 ? n1 : n2);
-    const int32_t* idx = side1 ? G.idx1 : G.idx2;
-    const int64_t r = live ? (idx ? (int64_t)idx[t] : t) : 0;
-    S.roff_a[q] = live ? (uint32_t)(r * (side1 ? G.a1_ts : G.a2_ts)) : v2::kOob;
-    S.roff_g[q] = live ? (uint32_t)(r * (side1 ? G.g1_ts : G.g2_ts)) : v2::kOob;
+  for (int j = j0; j < j1; ++j) {
+    const bool side1 = v3::kDma * D.uwave + j < v2::kBM / 8;  // uniform
+    const uint32_t m = act ? 0xffffffffu : 0u;
+    const uint32_t roff = (D.roa[j] & m) | (D.rog[j] & ~m);
+    const uint32_t ms = side1 ? 0xffffffffu : 0u;
+    u32x4 rs;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      rs[c] = (((D.ra1[c] & m) | (D.rg1[c] & ~m)) & ms) | (((D.ra2[c] & m) | (D.rg2[c] & ~m)) & ~ms);
+    dma16(rs, base + (uint32_t)(j * 8 * v2::kSB), (kin && roff != v2::kOob) ? roff + koff + D.cbyte : v2::kOob);
   }
-  f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT, true>(S, smem, ka, kg);
-  float* P = (float*)smem;
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 128 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
-        P[row * v2::kPRow + col] = (ka[x][y][r] + G.bias) * kg[x][y][r];
-      }
-  __syncthreads();
-  grouped_bins(P, v2::kPRow, v2::kBM, v2::kBN, t0, s0, n1, n2, m, n, G, ga);
 }
 
-// Dense / per-sample segmented mode: a 256 x 128 tile inside one sample pair.
+// One slice: the 4 MFMAs of (ua, ub) into acc, with rd the 4 fragment reads
+// of the slice two ahead (stage base sb, chunk offset coff) into (na, nb), and
+// with qd >= 0 quarter qd's share of stage dst's loads (after MFMAs 1 and 3).
 template <int DT>
-__global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
-  __shared__ float red[kThreads / kWave];
+__device__ __forceinline__ void ghost_quarter8(f32x16 (&acc)[2][2], const u32x4 (&ua)[2], const u32x4 (&ub)[2],
+                                               bool rd, const lds_char* sb, int coff, int wm, int wn,
+                                               u32x4 (&na)[2], u32x4 (&nb)[2], const DmaState8& D, int qd, int dst) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (rd) {
+      if (i < 2) na[i] = *(const u32x4*)(sb + (64 * wm + 32 * i) * v2::kSB + coff);
+      else nb[i - 2] = *(const u32x4*)(sb + (v2::kBM + 64 * wn + 32 * (i - 2)) * v2::kSB + coff);
+    }
+    Mfma32<DT>::mma(acc[i >> 1][i & 1], ua[i >> 1], ub[i & 1]);
+    if (qd >= 0 && i == 1) dma_part8(D, dst, v3::lo(qd), v3::lo(qd) + 1);
+    if (qd >= 0 && i == 3 && v3::lo(qd + 1) - v3::lo(qd) > 1) dma_part8(D, dst, v3::lo(qd) + 1, v3::lo(qd + 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__device__ __forceinline__ void ghost_stage_sync8() {
+  static_assert(v2::kNBuf == 3, "vmcnt below is one stage of 6 instructions");
+  asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// The 4-wave engine's schedule (see ghost_tile_engine) on 8 waves.
+template <int DT, bool kHasA>
+__device__ __forceinline__ void ghost_tile_engine8(const TileSrc8& S, char* smem, f32x16 (&ka)[2][2],
+                                                   f32x16 (&kg)[2][2]) {
+  lds_char* const L = (lds_char*)smem;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  DmaState8 D;
+  D.uwave = __builtin_amdgcn_readfirstlane(wave);
+  D.na = (int)((S.kbytes_a + v2::kSB - 1) / v2::kSB);
+  D.nst = D.na + (int)((S.kbytes_g + v2::kSB - 1) / v2::kSB);
+  D.ra1 = uniform4(S.ra1);
+  D.rg1 = uniform4(S.rg1);
+  D.ra2 = uniform4(S.ra2);
+  D.rg2 = uniform4(S.rg2);
+  D.kba = S.kbytes_a;
+  D.kbg = S.kbytes_g;
+  D.lds0 = (uint32_t)(uintptr_t)L;
+  D.cbyte = 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
+#pragma unroll
+  for (int j = 0; j < v3::kDma; ++j) {
+    D.roa[j] = S.roff_a[j];
+    D.rog[j] = S.roff_g[j];
+  }
+  const int na = D.na, nst = D.nst;
+
+  const int lrow = lane & 31, hh = lane >> 5;
+  const int c0 = lrow * v2::kSB + (((0 + hh) ^ (lane & 7)) << 4), c1 = lrow * v2::kSB + (((2 + hh) ^ (lane & 7)) << 4);
+  const int c2 = lrow * v2::kSB + (((4 + hh) ^ (lane & 7)) << 4), c3 = lrow * v2::kSB + (((6 + hh) ^ (lane & 7)) << 4);
+  u32x4 fa[4][2], fb[4][2];
+
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      ka[x][y] = f32x16{};
+      kg[x][y] = f32x16{};
+    }
+
+#pragma unroll
+  for (int s0 = 0; s0 < v2::kNBuf - 1; ++s0) dma_part8(D, s0, 0, v3::kDma);
+  ghost_stage_sync8();
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int co = kk == 0 ? c0 : c1;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) fa[kk][x] = *(const u32x4*)(L + (64 * wm + 32 * x) * v2::kSB + co);
+#pragma unroll
+    for (int y = 0; y < 2; ++y) fb[kk][y] = *(const u32x4*)(L + (v2::kBM + 64 * wn + 32 * y) * v2::kSB + co);
+  }
+  dma_part8(D, v2::kNBuf - 1, v3::lo(0), v3::lo(2));
+  {
+    f32x16(&acc0)[2][2] = kHasA ? ka : kg;
+    ghost_quarter8<DT>(acc0, fa[0], fb[0], true, L, c2, wm, wn, fa[2], fb[2], D, 2, v2::kNBuf - 1);
+    ghost_quarter8<DT>(acc0, fa[1], fb[1], true, L, c3, wm, wn, fa[3], fb[3], D, 3, v2::kNBuf - 1);
+  }
+  ghost_stage_sync8();
+
+#define DA_GHOST_BODY8(A1, A2)                                                                        \
+  {                                                                                                   \
+    const lds_char* nxt = L + ((st + 1) % v2::kNBuf) * v2::kStage;                                    \
+    ghost_quarter8<DT>(A1, fa[2], fb[2], true, nxt, c0, wm, wn, fa[0], fb[0], D, 0, st + 3);          \
+    ghost_quarter8<DT>(A1, fa[3], fb[3], true, nxt, c1, wm, wn, fa[1], fb[1], D, 1, st + 3);          \
+    ghost_quarter8<DT>(A2, fa[0], fb[0], true, nxt, c2, wm, wn, fa[2], fb[2], D, 2, st + 3);          \
+    ghost_quarter8<DT>(A2, fa[1], fb[1], true, nxt, c3, wm, wn, fa[3], fb[3], D, 3, st + 3);          \
+    ghost_stage_sync8();                                                                              \
+  }
+  if constexpr (kHasA) {
+    for (int st = 0; st + 1 < na; ++st) DA_GHOST_BODY8(ka, ka)
+    {
+      const int st = na - 1;
+      DA_GHOST_BODY8(ka, kg)
+    }
+  }
+  for (int st = kHasA ? na : 0; st + 1 < nst; ++st) DA_GHOST_BODY8(kg, kg)
+#undef DA_GHOST_BODY8
+  ghost_quarter8<DT>(kg, fa[2], fb[2], false, L, c0, wm, wn, fa[0], fb[0], D, -1, 0);
+  ghost_quarter8<DT>(kg, fa[3], fb[3], false, L, c1, wm, wn, fa[1], fb[1], D, -1, 0);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Dense / per-sample segmented mode: a 256 x 128 tile inside one sample pair on
+// the 8-wave engine.  Its fp32 partial (the 8 waves' shares summed in a fixed
+// order) goes to the pair's slot; ghost_gram_reduce adds a pair's tiles.
+template <int DT>
+__global__ __launch_bounds__(v3::kThreads, 1) void ghost_gram_tiles_v3(GhostArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[v2::kRing];
+  __shared__ float red[v3::kWaves];
   // Each XCD runs 32 tiles at once; grouping 4 row tiles (4 MB of operand rows
   // each at d = 4096) with 8 column tiles (2 MB each) minimises the rows its L2
   // streams per block of concurrent tiles (measured: groups of 4 rows beat 8,
@@ -739,7 +842,7 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
   const char* bg1 = g.s1.seg ? g.s1.grad : g.s1.grad + i * g.s1.grad_bstride;
   const char* ba2 = g.s2.seg ? g.s2.act : g.s2.act + j * g.s2.act_bstride;
   const char* bg2 = g.s2.seg ? g.s2.grad : g.s2.grad + j * g.s2.grad_bstride;
-  TileSrc S;
+  TileSrc8 S;
   S.ra1 = make_rsrc(ba1, 0x7fffffffu);
   S.rg1 = make_rsrc(bg1, 0x7fffffffu);
   S.ra2 = make_rsrc(ba2, 0x7fffffffu);
@@ -747,8 +850,8 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
   S.kbytes_a = g.kbytes_a;
   S.kbytes_g = g.kbytes_g;
 #pragma unroll
-  for (int q = 0; q < v2::kDma; ++q) {
-    const int row = dma_row(wave, q, lane);
+  for (int q = 0; q < v3::kDma; ++q) {
+    const int row = dma_row8(wave, q, lane);
     const bool side1 = row < v2::kBM;
     const SideDev& sd = side1 ? g.s1 : g.s2;
     const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
@@ -763,11 +866,11 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
       S.roff_g[q] = v2::kOob;
     }
   }
-  f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT, true>(S, smem, ka, kg);
+  f32x16 ka[2][2], kg[2][2];
+  ghost_tile_engine8<DT, true>(S, smem, ka, kg);
   float s = 0.f;
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int y = 0; y < 2; ++y)
 #pragma unroll
@@ -775,8 +878,75 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_gram_tiles_v2(GhostArgs g) 
   s = wave_sum(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  if (tid == 0) *dst = (red[0] + red[1]) + (red[2] + red[3]);
+  if (tid == 0) *dst = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
 }
+
+// Grouped (MoE) mode on the 8-wave engine: tiles over each group's packed
+// rows, the tile's products parked in LDS and binned by sample pair.  Each
+// K_a / K_g entry is the same MFMA chain as on the 4-wave engine, so the
+// parked products, and the bins summed from them, are bit-identical to it.
+template <int DT>
+__global__ __launch_bounds__(v3::kThreads, 1) void ghost_grouped_tiles_v3(GroupedArgs ga) {
+  __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
+  // Tiles go to the XCDs round-robin in launch order (no XCD remap): the host
+  // orders the groups longest reduction first, so every XCD gets the same mix
+  // of tile lengths, longest first.  A contiguous range per XCD would hand the
+  // long groups' tiles to some XCDs and the short ones to the rest.
+  const int64_t logical = blockIdx.x;
+  int e = 0;
+  while (e + 1 < ga.n_groups && ga.grp[e + 1].tile0 <= logical) ++e;
+  const GroupDev& G = ga.grp[e];
+  const int64_t local = logical - G.tile0;
+  constexpr int64_t kRowGroup = 4;
+  const int64_t per_group = kRowGroup * G.tiles_c;
+  const int64_t grp = local / per_group;
+  const int64_t first_r = grp * kRowGroup;
+  const int64_t gsize = min(G.tiles_r - first_r, kRowGroup);
+  const int64_t in_group = local - grp * per_group;
+  const int64_t m = first_r + in_group % gsize;
+  const int64_t n = in_group / gsize;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t t0 = m * v2::kBM, s0 = n * v2::kBN;
+  // Rows at or past seg[B] belong to no sample (and may have no row_index
+  // entry); a tile wholly past the packed rows of a side owns no bin.
+  const int64_t n1 = min(G.rows1, (int64_t)G.seg1[ga.b1]), n2 = min(G.rows2, (int64_t)G.seg2[ga.b2]);
+  if (t0 >= n1 || s0 >= n2) return;
+  TileSrc8 S;
+  S.ra1 = make_rsrc(G.a1, 0x7fffffffu);
+  S.rg1 = make_rsrc(G.g1, 0x7fffffffu);
+  S.ra2 = make_rsrc(G.a2, 0x7fffffffu);
+  S.rg2 = make_rsrc(G.g2, 0x7fffffffu);
+  S.kbytes_a = G.kbytes_a;
+  S.kbytes_g = G.kbytes_g;
+#pragma unroll
+  for (int q = 0; q < v3::kDma; ++q) {
+    const int row = dma_row8(wave, q, lane);
+    const bool side1 = row < v2::kBM;
+    const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
+    const bool live = t < (side1 ? n1 : n2);
+    const int32_t* idx = side1 ? G.idx1 : G.idx2;
+    const int64_t r = live ? (idx ? (int64_t)idx[t] : t) : 0;
+    S.roff_a[q] = live ? (uint32_t)(r * (side1 ? G.a1_ts : G.a2_ts)) : v2::kOob;
+    S.roff_g[q] = live ? (uint32_t)(r * (side1 ? G.g1_ts : G.g2_ts)) : v2::kOob;
+  }
+  f32x16 ka[2][2], kg[2][2];
+  ghost_tile_engine8<DT, true>(S, smem, ka, kg);
+  float* P = (float*)smem;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 64 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
+        P[row * v2::kPRow + col] = (ka[x][y][r] + G.bias) * kg[x][y][r];
+      }
+  __syncthreads();
+  grouped_bins(P, v2::kPRow, v2::kBM, v2::kBN, t0, s0, n1, n2, m, n, G, ga);
+}
+
 
 // ---------------------------------------------------------------------------
 // Per-token cross-gram on the 256 x 128 engine: K[i, t, j] keeps side 1's
@@ -1118,9 +1288,9 @@ int run_ghost(const da_factor_side* s1, const da_factor_side* s2, int64_t K, int
   dim3 grid((unsigned)ntiles);
   if (plan.v2) {
     switch (dtype) {
-      case DA_BF16: ghost_gram_tiles_v2<DA_BF16><<<grid, kThreads, 0, st>>>(args); break;
-      case DA_F16: ghost_gram_tiles_v2<DA_F16><<<grid, kThreads, 0, st>>>(args); break;
-      default: ghost_gram_tiles_v2<DA_F32><<<grid, kThreads, 0, st>>>(args); break;
+      case DA_BF16: ghost_gram_tiles_v3<DA_BF16><<<grid, v3::kThreads, 0, st>>>(args); break;
+      case DA_F16: ghost_gram_tiles_v3<DA_F16><<<grid, v3::kThreads, 0, st>>>(args); break;
+      default: ghost_gram_tiles_v3<DA_F32><<<grid, v3::kThreads, 0, st>>>(args); break;
     }
   } else {
     switch (dtype) {
@@ -1265,9 +1435,9 @@ int da_ghost_gram_grouped(const da_factor_side* s1, const da_factor_side* s2, in
     if (tiles > 0) {
       if (plan.v2) {
         switch (dtype) {
-          case DA_BF16: ghost_grouped_tiles_v2<DA_BF16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
-          case DA_F16: ghost_grouped_tiles_v2<DA_F16><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
-          default: ghost_grouped_tiles_v2<DA_F32><<<(unsigned)tiles, kThreads, 0, st>>>(ga); break;
+          case DA_BF16: ghost_grouped_tiles_v3<DA_BF16><<<(unsigned)tiles, v3::kThreads, 0, st>>>(ga); break;
+          case DA_F16: ghost_grouped_tiles_v3<DA_F16><<<(unsigned)tiles, v3::kThreads, 0, st>>>(ga); break;
+          default: ghost_grouped_tiles_v3<DA_F32><<<(unsigned)tiles, v3::kThreads, 0, st>>>(ga); break;
         }
       } else {
         switch (dtype) {
