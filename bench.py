@@ -362,7 +362,7 @@ def bench_block(args):
     # Dominant kernel: the one taking most of the step (summed over its launches).
     # Its roofline is the step's algorithmic work over the summed event time,
     # i.e. per-launch work over the average launch duration.
-    totals = {"materialize_tiles_tr": t_mat, "score_ring": t_score, "norm_grad_chunks": t_norm}
+    totals = {"materialize_tiles_tr8": t_mat, "score_ring": t_score, "norm_grad_chunks": t_norm}
     big = max(totals, key=totals.get)
     if big == "score_ring":
         gbs = score_bytes / t_score / 1e6
@@ -370,7 +370,7 @@ def bench_block(args):
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": f"{score_bytes_launch:.4g} B ({PASS * n_train + n_query} rows x {width} weights x 2 B)",
                 "launches_per_step": n_score}
-    elif big == "materialize_tiles_tr":
+    elif big == "materialize_tiles_tr8":
         tf = mat_flops / (t_mat * 1e9)
         roof = {"bound": "mfma", "kernel": big, "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
@@ -537,10 +537,10 @@ def bench_ghost(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "ghost cross-gram 256 train x 64 query, T=512, d_in=d_out=4096"},
-        "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles_v2", "achieved": round(tflops, 1),
+        "roofline": {"bound": "mfma", "kernel": "ghost_gram_tiles_v3", "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic("ghost_gram_tiles_v2", GHOST_TRAFFIC),
+                     "traffic": profiled_traffic("ghost_gram_tiles_v3", GHOST_TRAFFIC),
                      "traffic_source": os.path.relpath(GHOST_TRAFFIC, REPO),
                      "work_per_launch": f"{flops:.4g} flop = 2 x 256 x 64 pairs x 512^2 x (4096 + 4096)"},
     }
@@ -806,9 +806,9 @@ def bench_moe(args):
         "config": {"workload": "mixtral moe layer: 16 train x 256 tok vs 16 query x 256 tok, 8 experts top-2, "
                                "gate_up 4096->28672, down 14336->4096, grouped packed ghost route",
                    "rows_per_expert": rows},
-        "roofline": {"bound": "mfma", "kernel": "ghost_grouped_tiles_v2", "achieved": round(tf, 1),
+        "roofline": {"bound": "mfma", "kernel": "ghost_grouped_tiles_v3", "achieved": round(tf, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic("ghost_grouped_tiles_v2", MOE_TRAFFIC),
+                     "traffic": profiled_traffic("ghost_grouped_tiles_v3", MOE_TRAFFIC),
                      "traffic_source": os.path.relpath(MOE_TRAFFIC, REPO),
                      "work_per_step": f"{flops:.4g} flop = sum over experts and both linears "
                                                        "of 2 x rows1 x rows2 x (d_in + d_out)",
