@@ -48,9 +48,11 @@ for _p in (os.path.join(REPO, "dattri-llm_amd"), REPO):
 
 METRIC = "train×query pair-scores/sec (Llama-8B-shaped block, bf16); MFMA util % of peak"
 PEAK_BF16_TFLOPS = 2500.0
-# C4: train blocks scored per pass over the dense query block (score_sources' train_blocks_per_pass);
-# 4 x 8 rows fill the score kernel's 32-row side.
-PASS = 4
+# C4: train blocks scored per pass over the dense query block (score_sources' train_blocks_per_pass).
+# The 64 query rows are read once per 8 blocks (64 train rows, four 16-row tiles of the score ring
+# sharing them through L2): 1.26-1.32 ms of score per block against 1.56-1.58 with 4 blocks per
+# pass; groups of 10 or 20 blocks measured slower (1.96 ms).
+PASS = 8
 PEAK_HBM_GBS = 8000.0
 
 D_MODEL, D_KV, D_FFN = 4096, 1024, 14336
@@ -402,7 +404,7 @@ def bench_block(args):
         "data": "synthetic",
         "config": {
             "workload": "llama3-8b-block: 8 train x 2048 tok vs 64 query x 512 tok, 7 linears + 2 RMSNorm, "
-                        "TracInAttributor.attribute_sources (cost-rule routing per layer; 4 train blocks "
+                        "TracInAttributor.attribute_sources (cost-rule routing per layer; 8 train blocks "
                         "per pass over the dense queries)",
             "train_block": [n_train, t_train],
             "train_blocks_per_query_pass": PASS,
