@@ -295,6 +295,146 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring(RingArgs a) {
   }
 }
 
+// The same stream-K ring with a 64 x 64 output tile, for side 1 taller than
+// one 16-row tile.  With 16-row tiles every tile stages the same side-2 rows
+// again (64 train x 64 query rows: 4 tiles of 80 rows, 2.5 times the rows
+// read from HBM, through the L2 -> LDS path, which caps the launch near 5 TB/s);
+// here each unit's 128 rows are staged once.  A unit is 256 bytes of width (two
+// 128-byte blocks), a stage one unit of the 128 rows (32 KB), four stages in
+// the ring.  Wave w loads LDS rows 64 (w % 2) .. +63 of block w / 2 (side 1
+// for w even, side 2 for w odd: 8 instructions of 8 rows) and multiplies
+// output rows 32 (w % 2) .. +31 of block w / 2 against all 64 side-2 rows
+// (2 x 4 16x16x32 MFMAs per k-step, two k-steps per block); the two blocks'
+// partial tiles are added in block order at the end.  Block rows keep the
+// swizzle c ^ ((row/2) % 8).
+namespace sr64 {
+constexpr int kTM = 64, kTN = 64;
+constexpr int kRows = kTM + kTN;            // 128 LDS rows per block
+constexpr int kBlkB = 128;
+constexpr int kUnitB = 2 * kBlkB;           // 256 bytes of width per unit
+constexpr int kStage = 2 * kRows * kBlkB;   // 32 KB
+constexpr int kNBuf = 4;                    // three stages in flight
+constexpr int kDma = kRows / 2 / 8;         // 8 instructions per wave and stage
+constexpr uint32_t kOob = 0x80000000u;
+static_assert(kNBuf * kStage + 0 <= 160 * 1024, "LDS");
+static_assert(kDma == 8 && kNBuf == 4, "the vmcnt wait below is 8 * (kNBuf - 2) = 16");
+}  // namespace sr64
+
+template <int DT>
+__global__ __launch_bounds__(kThreads, 1) void score_ring64(RingArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[sr64::kNBuf * sr64::kStage];
+  lds_char* const Ls = (lds_char*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)Ls;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+  const int bw = uwave >> 1, hw = uwave & 1;  // block and half of this wave (uniform)
+  const int64_t tile = blockIdx.x / a.nwg, w = blockIdx.x % a.nwg;
+  const int64_t tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  const int64_t ub = uniform64(ring_first(w, a));
+  const int nloc = __builtin_amdgcn_readfirstlane((int)(ring_first(w + 1, a) - ub));
+
+  // DMA instruction i: LDS rows 64 hw + 8i .. +7 of block bw; lane l -> row
+  // 64 hw + 8i + l/8 (side 1 row tm*64 + r, or side 2 row tn*64 + r - 64),
+  // slot l%8 holding chunk (l%8) ^ ((row/2) % 8).
+  int rowv[sr64::kDma];
+  uint32_t cbo[sr64::kDma];
+#pragma unroll
+  for (int i = 0; i < sr64::kDma; ++i) {
+    const int r = 64 * hw + 8 * i + (lane >> 3);
+    cbo[i] = 16u * (uint32_t)((lane & 7) ^ ((r >> 1) & 7));
+    const int rl = r - 64 * hw;  // row within its side's tile
+    const int64_t row = hw == 0 ? tm * sr64::kTM + rl : tn * sr64::kTN + rl;
+    rowv[i] = row < (hw == 0 ? a.b1 : a.b2) ? rl : -1;
+  }
+  const bool nt = hw == 0 ? a.nt1 : a.nt2;  // uniform
+  int il = 0;
+  while (il + 1 < a.n_layers && a.layers[il + 1].u0 <= ub) ++il;
+  int64_t iu = uniform64(ub - a.layers[il].u0);
+  uint32_t roff[sr64::kDma];
+  uint32_t lbytes = 0;
+  int64_t lunits = 0, blk = 0;
+  const char* mb = nullptr;  // this wave's side: the tile's first row
+  auto set_layer = [&]() __attribute__((always_inline)) {
+    const RingLayer& Ly = a.layers[il];
+    const int64_t ld = hw == 0 ? Ly.ld1 : Ly.ld2;
+    blk = hw == 0 ? Ly.blk1 : Ly.blk2;
+    mb = hw == 0 ? Ly.m1 + tm * sr64::kTM * Ly.ld1 : Ly.m2 + tn * sr64::kTN * Ly.ld2;
+    lbytes = (uint32_t)min(Ly.bytes, (int64_t)0x7fffffff);
+    lunits = Ly.units;
+#pragma unroll
+    for (int i = 0; i < sr64::kDma; ++i)
+      roff[i] = rowv[i] < 0 ? sr64::kOob : (uint32_t)(rowv[i] * ld + bw * blk) + cbo[i];
+  };
+  auto issue = [&](int slot, bool live, bool more) __attribute__((always_inline)) {
+    const u32x4 rs = uniform4(make_rsrc(mb + iu * 2 * blk, 0x7fffffffu));
+    const uint32_t kin = (uint32_t)iu * sr64::kUnitB + (uint32_t)bw * sr64::kBlkB;
+    const uint32_t dst0 = lds0 + (uint32_t)(slot * sr64::kStage + bw * sr64::kRows * sr64::kBlkB +
+                                            64 * hw * sr64::kBlkB);
+#pragma unroll
+    for (int i = 0; i < sr64::kDma; ++i) {
+      const bool en = live & (roff[i] != sr64::kOob) & (kin + cbo[i] < lbytes);
+      if (nt)
+        dma16_nt(rs, dst0 + (uint32_t)(8 * i * sr64::kBlkB), en ? roff[i] : sr64::kOob);
+      else
+        dma16(rs, dst0 + (uint32_t)(8 * i * sr64::kBlkB), en ? roff[i] : sr64::kOob);
+    }
+    if (live && ++iu == lunits) {
+      iu = 0;
+      do {
+        ++il;
+      } while (il < a.n_layers && a.layers[il].units == 0);
+      if (more) set_layer();
+    }
+  };
+
+  set_layer();
+  int ix = 0;
+#pragma unroll
+  for (int p = 0; p < sr64::kNBuf - 1; ++p, ++ix) issue(p, ix < nloc, ix + 1 < nloc);
+
+  const int r16 = lane & 15, q = lane >> 4;
+  const int sw = (r16 >> 1) & 7;
+  f32x4 acc[2][4] = {};
+  int slot = 0;
+  for (int x = 0; x < nloc; ++x, ++ix) {
+    asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(slot == 0 ? sr64::kNBuf - 1 : slot - 1, ix < nloc, ix + 1 < nloc);
+    const lds_char* bb = Ls + slot * sr64::kStage + bw * sr64::kRows * sr64::kBlkB;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int so = (((4 * ks + q) ^ sw) << 4);
+      u32x4 va[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) va[rb] = *(const u32x4*)(bb + (32 * hw + 16 * rb + r16) * sr64::kBlkB + so);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const u32x4 vb = *(const u32x4*)(bb + (sr64::kTM + 16 * cb + r16) * sr64::kBlkB + so);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) Mfma16<DT>::mma(acc[rb][cb], va[rb], vb);
+      }
+    }
+    slot = slot + 1 == sr64::kNBuf ? 0 : slot + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // the two blocks' partial tiles through LDS (64 x 64 fp32 each), summed in block order
+  float* red = (float*)smem;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        red[(bw * sr64::kTM + 32 * hw + 16 * rb + acc16_row(e, lane)) * sr64::kTN + 16 * cb + acc16_col(lane)] =
+            acc[rb][cb][e];
+  __syncthreads();
+  for (int x = tid; x < sr64::kTM * sr64::kTN; x += kThreads) {
+    const int row = x / sr64::kTN, col = x % sr64::kTN;
+    const float v = red[x] + red[sr64::kTM * sr64::kTN + x];
+    const int64_t oi = tm * sr64::kTM + row, oj = tn * sr64::kTN + col;
+    if (oi < a.b1 && oj < a.b2) a.partial[(oi * a.b2 + oj) * a.nwg + w] = v;
+  }
+}
+
 // One workgroup per output: its n_chunks partials are contiguous; each thread
 // sums a fixed strided subset, then a fixed tree combines the threads.
 __global__ __launch_bounds__(256) void score_gemm_reduce(const float* __restrict__ partial,
@@ -350,6 +490,7 @@ struct Plan {
   int64_t chunk_bytes, n_chunks;
   size_t ws;
   bool ring;              // streaming form (2-byte dtypes, offsets within a tile fit 32 bits)
+  bool tall;              // its 64 x 64 tile (side 1 taller than one 16-row tile), else 16 x 64
   int64_t units, nwg;     // its units and workgroups per tile
 };
 
@@ -389,19 +530,22 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
   // per-lane offsets within one tile and the row widths fit 32 bits.
   const int64_t lim = (1LL << 31) - (1LL << 20);
   p->ring = es == 2 && b1 > 0 && b2 > 0;
+  p->tall = b1 > kTileM;
+  const int64_t unit_b = p->tall ? sr64::kUnitB : sr::kUnitB;
+  const int64_t tile_m = p->tall ? sr64::kTM : kTileM;
   int64_t units = 0;
   for (int l = 0; l < n_layers && p->ring; ++l) {
     const da_dense_layer& L = layers[l];
     const int64_t bytes = L.width * es, ld1 = L.ld1 * es, ld2 = L.ld2 * es;
     const int64_t bk1 = (L.blk1 ? L.blk1 : 64) * es, bk2 = (L.blk2 ? L.blk2 : 64) * es;
     if (bytes >= lim || (kTileN - 1) * ld1 + 4 * bk1 >= lim || (kTileN - 1) * ld2 + 4 * bk2 >= lim) p->ring = false;
-    units += (bytes + sr::kUnitB - 1) / sr::kUnitB;
+    units += (bytes + unit_b - 1) / unit_b;
   }
   if (p->ring && units > 0) {
     int64_t slots = 0;
     const int rc = device_cu_count(&slots);
     if (rc) return rc;
-    const int64_t tiles = ((b1 + kTileM - 1) / kTileM) * ((b2 + kTileN - 1) / kTileN);
+    const int64_t tiles = ((b1 + tile_m - 1) / tile_m) * ((b2 + kTileN - 1) / kTileN);
     int64_t nwg = slots / tiles;
     if (nwg < 1) nwg = 1;
     if (nwg > units) nwg = units;
@@ -443,10 +587,12 @@ int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers
       Ly.ld2 = layers[l].ld2 * es;
       Ly.blk1 = (layers[l].blk1 ? layers[l].blk1 : 64) * es;
       Ly.blk2 = (layers[l].blk2 ? layers[l].blk2 : 64) * es;
-      Ly.units = (Ly.bytes + sr::kUnitB - 1) / sr::kUnitB;
+      const int64_t unit_b = p.tall ? sr64::kUnitB : sr::kUnitB;
+      Ly.units = (Ly.bytes + unit_b - 1) / unit_b;
       Ly.u0 = u;
       u += Ly.units;
     }
+    const int64_t tile_m = p.tall ? sr64::kTM : kTileM;
     r.units = p.units;
     r.nwg = p.nwg;
     r.b1 = b1;
@@ -454,12 +600,19 @@ int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers
     r.tiles_n = (b2 + kTileN - 1) / kTileN;
     r.partial = (float*)workspace;
     r.nt1 = r.tiles_n == 1;                     // side-1 rows meet one side-2 tile
-    r.nt2 = (b1 + kTileM - 1) / kTileM == 1;    // side-2 rows meet one side-1 tile
-    const int64_t tiles = ((b1 + kTileM - 1) / kTileM) * r.tiles_n;
+    r.nt2 = (b1 + tile_m - 1) / tile_m == 1;    // side-2 rows meet one side-1 tile
+    const int64_t tiles = ((b1 + tile_m - 1) / tile_m) * r.tiles_n;
     const unsigned grid = (unsigned)(tiles * p.nwg);
-    switch (dtype) {
-      case DA_BF16: score_ring<DA_BF16><<<grid, kThreads, 0, st>>>(r); break;
-      default: score_ring<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+    if (p.tall) {
+      switch (dtype) {
+        case DA_BF16: score_ring64<DA_BF16><<<grid, kThreads, 0, st>>>(r); break;
+        default: score_ring64<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+      }
+    } else {
+      switch (dtype) {
+        case DA_BF16: score_ring<DA_BF16><<<grid, kThreads, 0, st>>>(r); break;
+        default: score_ring<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+      }
     }
     rc = check_launch("da_score_gemm(ring)");
     if (rc) return rc;

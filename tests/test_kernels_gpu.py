@@ -179,13 +179,18 @@ def test_blocked_materialize_equals_plain(device, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_score_gemm_blocked_operands(device, dtype):
+@pytest.mark.parametrize("b1", [8, 17, 64, 100])
+def test_score_gemm_blocked_operands(device, dtype, b1):
+    """k-blocked and row-major layers mixed in one launch.  b1 <= 16 takes the
+    16 x 64 ring tile; taller side-1 blocks the 64 x 64 tile (one tile at 17
+    and 64 rows, two row tiles at 100, whose side-2 rows then keep the default
+    load policy)."""
     from dattri_llm_amd import kernels
 
-    gen = torch.Generator().manual_seed(21)
+    gen = torch.Generator().manual_seed(21 + b1)
     pairs, m1s, m2s = [], [], []
     for w, (bl1, bl2) in [(4096, (True, True)), (1024, (False, True)), (192, (True, False)), (136, (False, False))]:
-        m1, m2 = _rand(gen, 8, w, dtype=dtype), _rand(gen, 64, w, dtype=dtype)
+        m1, m2 = _rand(gen, b1, w, dtype=dtype), _rand(gen, 64, w, dtype=dtype)
         m1s.append(_np(m1))
         m2s.append(_np(m2))
 
