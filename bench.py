@@ -364,9 +364,9 @@ def bench_block(args):
     # Dominant kernel: the one taking most of the step (summed over its launches).
     # Its roofline is the step's algorithmic work over the summed event time,
     # i.e. per-launch work over the average launch duration.
-    totals = {"materialize_tiles_tr8": t_mat, "score_ring": t_score, "norm_grad_chunks": t_norm}
+    totals = {"materialize_tiles_tr8": t_mat, "score_ring64": t_score, "norm_grad_ring": t_norm}
     big = max(totals, key=totals.get)
-    if big == "score_ring":
+    if big == "score_ring64":
         gbs = score_bytes / t_score / 1e6
         roof = {"bound": "hbm", "kernel": big, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
