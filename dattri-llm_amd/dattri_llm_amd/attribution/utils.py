@@ -260,6 +260,11 @@ def score_sources(
         else:
             row_ids.extend(ids)
             row_steps.extend(steps)
+        # Drop this block before the next one is built: a dense group of 8 C4
+        # blocks is 28 GB, and holding it while the next one materializes
+        # doubles the peak and can make the caching allocator free and map
+        # tens of GB again (a 1-2 s stall).
+        del train_rep
     scores = rows_out.result(num_test)
     return scores, row_ids, row_steps, test_ids, (row_tokens if per_token else None)
 
