@@ -292,6 +292,12 @@ def bench_block(args):
         return attr.attribute_sources(((step, trains[step % PASS], train_ids) for step in range(k)), test_source,
                                       train_blocks_per_pass=per_pass)
 
+    # Setup: reserve one full group's dense buffers in the caching allocator (allocated and
+    # released here), so that no multi-GB device allocation falls inside a timed region, whatever
+    # the warmup's group size (a 5-step warmup builds a group of 5).
+    reserve = [kernels.blocked_storage(PASS * n_train, din * dout, torch.bfloat16, "cuda")
+               for _n, _a, din, dout in LINEARS]
+    del reserve
     attribute(args.warmup)
     torch.cuda.synchronize()
     with kernels.launch_events() as log:
@@ -324,6 +330,7 @@ def bench_block(args):
             nb = min(PASS, k - first)
             tr = dense_group([train_facs[(first + i) % PASS] for i in range(nb)])
             kernels.score_gemm([(tr[n], q_dense[n]) for n in names], out=raw_scores[:nb * n_train])
+            del tr  # before the next group is built, as score_sources does
         return nb
 
     raw_steps(args.warmup)
