@@ -347,9 +347,11 @@ def bench_block(args):
     dk = {n: din * dout for n, _a, din, dout in LINEARS}
     width = sum(dk.values()) + sum(d for _, d in NORMS)
     mat_flops = sum(2.0 * n_train * t_train * v for v in dk.values())
-    # one score launch reads PASS train blocks and the queries once
+    # one score launch reads a group's train blocks (PASS, the last group of the timed steps
+    # possibly fewer) and the queries once
     score_bytes_launch = (PASS * n_train + n_query) * width * 2.0
-    score_bytes = score_bytes_launch / PASS  # per step
+    groups = [min(PASS, args.steps - f) for f in range(0, args.steps, PASS)]
+    score_bytes = sum((nb * n_train + n_query) * width * 2.0 for nb in groups) / args.steps  # per step
     norm_bytes = 2.0 * n_train * t_train * D_MODEL * 2
     t_mat, n_mat = event_ms("materialize_linear")
     t_score, n_score = event_ms("score_gemm")
