@@ -1323,8 +1323,9 @@ def bench_copy(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 32 timed steps after 8 warmup: whole groups of the block workload's 8 train blocks per query pass
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "kfac", "capture",
                                            "store", "copy"],
                     default="block")
