@@ -27,6 +27,23 @@ import json
 import os
 from dataclasses import asdict, dataclass
 
+# The packed (segmented) ghost kernel over fully live rows runs at about this
+# share of the dense engine's rate (measured at K = D = 4096, bf16: 895-910
+# against 1121-1139 TFLOP/s at T = 256 and 512), with no padding but the last
+# tile's.  The factorized route packs a pair whose dense 256 x 128-token tiles
+# hold a smaller share of live row pairs than this (every T up to about 200
+# tokens on both sides, and single-token rows).
+PACKED_RELATIVE_RATE = 0.8
+
+
+def ghost_tile_share(s1: int, s2: int) -> float:
+    """Share of the dense ghost engine's tile work (256 side-1 x 128 side-2
+    tokens per sample pair) that falls on real token pairs."""
+    if s1 <= 0 or s2 <= 0:
+        return 1.0
+    return (s1 / (-(-s1 // 256) * 256)) * (s2 / (-(-s2 // 128) * 128))
+
+
 _POLICIES = ("flops", "calibrated")
 _policy = "flops"
 _model = None
@@ -66,8 +83,10 @@ class CostModel:
         return -(-n // m) * m
 
     def time_factorized(self, b1, b2, s1, s2, k, d) -> float:
-        flops = 2.0 * b1 * b2 * self._up(s1, 256) * self._up(s2, 128) * (k + d)
-        return flops / (self.ghost_tflops * 1e12) + self.launch_us * 1e-6
+        # the dense tiles' padded work, or the packed kernel's at its lower rate
+        dense = 2.0 * b1 * b2 * self._up(s1, 256) * self._up(s2, 128) * (k + d)
+        packed = 2.0 * b1 * b2 * s1 * s2 * (k + d) / PACKED_RELATIVE_RATE
+        return min(dense, packed) / (self.ghost_tflops * 1e12) + self.launch_us * 1e-6
 
     def time_materialized(self, b1, b2, s1, s2, k, d) -> float:
         tiles = self._up(d, 256) * self._up(k, 256)

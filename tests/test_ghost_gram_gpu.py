@@ -263,3 +263,50 @@ def test_dense_per_token(device, case):
     want = oracle.cross_gram_per_token_dense(_np(a1), _np(g1), _np(m2), bias=bias)
     assert got.shape == (b1, t1, b2)
     assert_parity(got, want, dtype)
+
+
+# (b1, s1, b2, s2, k, d, bias, dtype): short sequences, where the dense engine's
+# 256 x 128-token tiles would be mostly padding, including single-token rows
+SHORT_CASES = [
+    (40, 64, 24, 64, 256, 128, False, torch.bfloat16),
+    (9, 40, 7, 24, 72, 40, True, torch.bfloat16),
+    (300, 1, 70, 1, 128, 96, True, torch.bfloat16),
+    (6, 100, 5, 33, 64, 48, False, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", SHORT_CASES)
+def test_short_sequences_take_the_packed_kernel(device, case, monkeypatch):
+    """cross_gram's factorized route packs several samples into each tile when
+    the dense tiles would hold few live token pairs: the packed (grouped)
+    kernel runs, the dense one does not, and the scores match the oracle and
+    the dense kernel.  A bias is the preprocessed form: a ones column."""
+    from dattri_llm_amd import kernels
+    from dattri_llm_amd.gradient import ops
+
+    b1, s1, b2, s2, k, d, bias, dtype = case
+    print(f"short-sequence packed route case={case}", flush=True)
+    a1, g1, a2, g2 = (x.to(device) for x in _inputs(5, b1, s1, b2, s2, k, d, dtype))
+    if bias:
+        a1, a2 = (torch.cat([x, torch.ones_like(x[..., :1])], dim=-1) for x in (a1, a2))
+    dense = kernels.ghost_gram(a1, g1, a2, g2)
+    calls = {"dense": 0, "packed": 0}
+    real_dense, real_packed = kernels.ghost_gram, kernels.ghost_gram_grouped
+
+    def spy_dense(*a, **kw):
+        calls["dense"] += 1
+        return real_dense(*a, **kw)
+
+    def spy_packed(*a, **kw):
+        calls["packed"] += 1
+        return real_packed(*a, **kw)
+
+    monkeypatch.setattr(kernels, "ghost_gram", spy_dense)
+    monkeypatch.setattr(kernels, "ghost_gram_grouped", spy_packed)
+    got = ops.cross_gram(a1, g1, a2, g2, "nn.Linear", mode="factorized")  # in the inputs' dtype
+    torch.cuda.synchronize()
+    assert calls == {"dense": 0, "packed": 1}, calls
+    assert got.dtype == dtype
+    want = oracle.cross_gram(*(x.double().cpu().numpy() for x in (a1, g1, a2, g2)), "nn.Linear", mode="factorized")
+    assert_parity(got, want, dtype, label=f"{case} packed")
+    assert_parity(got, dense.double().cpu().numpy(), dtype, label=f"{case} vs dense")

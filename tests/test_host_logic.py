@@ -395,3 +395,28 @@ def test_ghost_probe_cache_follows_tensor_identity_and_version():
     del g, root
     gc.collect()
     assert len(dot._PROBES) == n - 1
+
+
+def test_ghost_tile_share_and_packed_pricing():
+    """The share of the dense ghost engine's 256 x 128-token tiles that holds
+    real token pairs decides the packed route; the calibrated cost model
+    prices the factorized route at the cheaper of the two kernels."""
+    from dattri_llm_amd.gradient.ops import cost
+
+    assert cost.ghost_tile_share(512, 512) == 1.0
+    assert cost.ghost_tile_share(256, 128) == 1.0
+    assert cost.ghost_tile_share(64, 64) == pytest.approx(0.25 * 0.5)
+    assert cost.ghost_tile_share(1, 1) == pytest.approx(1 / (256 * 128))
+    assert cost.ghost_tile_share(200, 200) == pytest.approx((200 / 256) ** 2)
+    assert cost.ghost_tile_share(2048, 512) == 1.0
+    # packed below the relative rate, dense at or above it
+    for s1, s2, packed in ((64, 64, True), (128, 128, True), (200, 200, True), (256, 256, False), (512, 512, False),
+                           (1000, 1000, False)):
+        assert (cost.ghost_tile_share(s1, s2) < cost.PACKED_RELATIVE_RATE) == packed, (s1, s2)
+    m = cost.CostModel(ghost_tflops=1000.0, materialize_tflops=1200.0, stream_gbs=6000.0)
+    k = d = 4096
+    flops = 2.0 * 256 * 64 * 64 * 64 * (k + d)
+    assert m.time_factorized(256, 64, 64, 64, k, d) == pytest.approx(
+        flops / cost.PACKED_RELATIVE_RATE / 1e15 + m.launch_us * 1e-6)
+    dense512 = 2.0 * 8 * 8 * 512 * 512 * (k + d)
+    assert m.time_factorized(8, 8, 512, 512, k, d) == pytest.approx(dense512 / 1e15 + m.launch_us * 1e-6)
