@@ -313,6 +313,13 @@ def ghost_gram_per_token(
     g1, g2 = prepare_rows(g1, d), prepare_rows(g2, d)
     b1, t1, b2 = a1.shape[0], a1.shape[1], a2.shape[0]
     out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
+    o0 = out.stride(0)
+    if _flatten_side1(a1, g1, out):
+        # Side 1's token rows are independent outputs: as one sample of
+        # B1*T1 tokens they fill the kernel's 256-row tiles instead of padding
+        # each short sample to a tile (out row i*T1 + t is token t of sample i).
+        a1, g1 = a1.reshape(1, b1 * t1, k), g1.reshape(1, b1 * t1, d)
+        o0 = b1 * t1 * out.stride(1)
     s1, s2 = _side(a1, g1, bias), _side(a2, g2, bias)
     lib = nat.load()
     nbytes = ctypes.c_size_t(0)
@@ -320,9 +327,24 @@ def ghost_gram_per_token(
               "ghost_gram_per_token")
     ws = nat.workspace(nbytes.value, dev)
     _run(dev, "ghost_gram_per_token", lib.da_ghost_gram_per_token,
-         s1, s2, k, d, code, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), int(accumulate),
+         s1, s2, k, d, code, out.data_ptr(), o0, out.stride(1), out.stride(2), int(accumulate),
          ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out
+
+
+def _flatten_side1(a1: torch.Tensor, g1: torch.Tensor, out: torch.Tensor) -> bool:
+    """Whether the per-token kernel should see side 1 as one sample of B1*T1
+    tokens: several samples shorter than the 256-row tile, whose rows (and out
+    rows) lie at one stride, within the kernel's 32-bit row offsets."""
+    b1, t1 = a1.shape[:2]
+    if b1 < 2 or t1 >= 256:
+        return False
+    if a1.stride(0) != t1 * a1.stride(1) or g1.stride(0) != t1 * g1.stride(1):
+        return False
+    if out.stride(0) != t1 * out.stride(1):
+        return False
+    row_bytes = max(a1.stride(1), g1.stride(1)) * a1.element_size()
+    return b1 * t1 * row_bytes + max(a1.shape[-1], g1.shape[-1]) * a1.element_size() < (1 << 31) - (1 << 20)
 
 
 def _embedding_sides(name, tok1, g1, tok2, g2):
