@@ -497,6 +497,10 @@ def dense_per_token(
         bias_grad = torch.nn.functional.pad(bias_grad, (0, d - dd))
     b1, t1, b2 = a1.shape[0], a1.shape[1], w.shape[0]
     out, accumulate = _per_token_out(out, b1, t1, b2, dev, accumulate)
+    o0 = out.stride(0)
+    if _flatten_side1(a1, g1, out):  # short samples as one long one (see ghost_gram_per_token)
+        a1, g1 = a1.reshape(1, b1 * t1, k), g1.reshape(1, b1 * t1, d)
+        o0 = b1 * t1 * out.stride(1)
     s1 = _side(a1, g1, bias)
     lib = nat.load()
     nbytes = ctypes.c_size_t(0)
@@ -505,7 +509,7 @@ def dense_per_token(
     _run(dev, "dense_per_token", lib.da_dense_per_token,
          s1, w.data_ptr(), b2, w.stride(0), w.stride(1),
          bias_grad.data_ptr() if bias_grad is not None else None,
-         bias_grad.stride(0) if bias_grad is not None else 0, k, d, code, out.data_ptr(), out.stride(0),
+         bias_grad.stride(0) if bias_grad is not None else 0, k, d, code, out.data_ptr(), o0,
          out.stride(1), out.stride(2), int(accumulate), ws.data_ptr(), ws.numel(), nat.stream_ptr(dev))
     return out
 
