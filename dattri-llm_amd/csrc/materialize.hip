@@ -885,6 +885,125 @@ __global__ __launch_bounds__(tr8::kThreads, 1) void materialize_tiles_tr8(MatArg
   }
 }
 
+// Narrow layers: one side at most 64 wide (LoRA adapters, small heads).  The
+// wide-tile kernels pad such a side to their 128 or 256 rows and leave few
+// tiles per sample (16 of 256 x 256 for 4096 -> 16), so the GPU idles and the
+// bytes, which bound this shape, stream slowly.  Here a workgroup owns the
+// whole narrow side (up to 64 columns) against 64 columns of the wide side:
+// 64 tiles per sample at width 4096.  The tile's two 64-column operand slices
+// go HBM -> LDS by buffer loads with the LDS-direct bit, 32 tokens per stage
+// (8 KB), through a ring of four stages, three in flight, one DMA instruction
+// per operand, wave and stage.  Wave w multiplies all (up to four) 16-row
+// blocks of the narrow side against wide columns 16w .. 16w+15 with
+// 16x16x32 MFMAs, fragments read with transposing LDS reads (16-byte chunk c
+// of token row r stored at slot c ^ 2(r % 4), so the four rows of a read's
+// 16-lane phase use distinct 32-byte bank groups).  The wide operand is read
+// once (non-temporal); the narrow one, shared by the sample's tiles, through
+// L2, each XCD owning a contiguous run of tiles.
+namespace nw {
+constexpr int kCols = 64;            // columns per operand and tile
+constexpr int kTS = 32;              // tokens per stage
+constexpr int kRow = kCols * 2;      // 128 bytes per token row and operand
+constexpr int kSide = kTS * kRow;    // 4 KB
+constexpr int kStage = 2 * kSide;    // narrow operand, then wide operand
+constexpr int kNBuf = 4;             // three stages in flight (eight measured slower)
+constexpr uint32_t kOob = 0x80000000u;
+__device__ __forceinline__ int swz(int r) { return (r & 3) << 1; }
+static_assert(kNBuf == 4, "the vmcnt wait below is 2 * (kNBuf - 2) = 4");
+}  // namespace nw
+
+template <int DT, int OT>
+__global__ __launch_bounds__(256) void materialize_narrow(MatArgs m, int narrow_is_d) {
+  static_assert(Elem<DT>::kBytes == 2, "transposing reads are 16-bit");
+  __shared__ __attribute__((aligned(1024))) char smem[nw::kNBuf * nw::kStage];
+  lds_char* const L = (lds_char*)smem;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)L;
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t b = logical / m.tiles_n, tw = logical - b * m.tiles_n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);
+
+  // the narrow operand (width N) and the wide one (width W) of sample b
+  const char* xn = narrow_is_d ? m.g + b * m.g_bstride : m.a + b * m.a_bstride;
+  const char* xw = narrow_is_d ? m.a + b * m.a_bstride : m.g + b * m.g_bstride;
+  const uint32_t tsn = (uint32_t)(narrow_is_d ? m.g_tstride : m.a_tstride);
+  const uint32_t tsw = (uint32_t)(narrow_is_d ? m.a_tstride : m.g_tstride);
+  const int64_t n_cols = narrow_is_d ? m.d : m.k, w_cols = narrow_is_d ? m.k : m.d;
+  const int64_t w0 = tw * nw::kCols;
+  const u32x4 rn = uniform4(make_rsrc(xn, (uint32_t)(m.tokens * tsn)));
+  const u32x4 rw = uniform4(make_rsrc(xw, (uint32_t)(m.tokens * tsw)));
+  const int nst = (int)((m.tokens + nw::kTS - 1) / nw::kTS);
+
+  // DMA: wave w loads token rows 8w .. 8w+7 of both operands; lane l takes
+  // row 8w + l/8 and LDS slot l%8, which holds chunk (l%8) ^ swz(row).
+  const int r = 8 * wave + (lane >> 3);
+  const int c = (lane & 7) ^ nw::swz(r);
+  const uint32_t offn = 8 * c < n_cols ? r * tsn + 16u * (uint32_t)c : nw::kOob;
+  const uint32_t offw = w0 + 8 * c < w_cols ? r * tsw + (uint32_t)(w0 + 8 * c) * 2u : nw::kOob;
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const bool en = st < nst;
+    const uint32_t base = lds0 + (uint32_t)((st % nw::kNBuf) * nw::kStage + 8 * uwave * nw::kRow);
+    dma16(rn, base, en && offn != nw::kOob ? offn + (uint32_t)st * (nw::kTS * tsn) : nw::kOob);
+    dma16_nt(rw, base + nw::kSide, en && offw != nw::kOob ? offw + (uint32_t)st * (nw::kTS * tsw) : nw::kOob);
+  };
+
+  // Fragment of the 16 columns c0 .. c0+15 of one operand over the stage's 32
+  // tokens: lane l gets tokens 8(l/16) .. +7 of column c0 + l%16 (two
+  // transposing reads of 4 tokens; lane j of a 16-lane phase addresses token
+  // row t0 + j/4, columns c0 + 4(j%4) .. +3).
+  const int g4 = lane >> 4, i16 = lane & 15;
+  auto frag = [&](const lds_char* side, int c0) __attribute__((always_inline)) {
+    u32x2 h[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int t = 8 * g4 + 4 * k + (i16 >> 2);
+      const int col = c0 + 4 * (i16 & 3);
+      const lds_char* p = side + t * nw::kRow + (((col >> 3) ^ nw::swz(t)) << 4) + (col & 7) * 2;
+      h[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                           (__attribute__((address_space(3))) s16x4*)p));
+    }
+    return u32x4{h[0][0], h[0][1], h[1][0], h[1][1]};
+  };
+
+  const int nblk = (int)((n_cols + 15) / 16);  // 16-row blocks of the narrow side (<= 4)
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s0 = 0; s0 < nw::kNBuf - 1; ++s0) issue(s0);
+  for (int st = 0; st < nst; ++st) {
+    // this wave's loads of stage st are done (the two later stages' 4 may fly),
+    // its LDS reads of stage st - 1 have returned; then every wave's
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+    issue(st + nw::kNBuf - 1);  // into the slot stage st - 1 used
+    const lds_char* sb = L + (st % nw::kNBuf) * nw::kStage;
+    const u32x4 fw = frag(sb + nw::kSide, 16 * wave);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < nblk) Mfma16<DT>::mma(acc[j], frag(sb, 16 * j), fw);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the zero-fill loads past the last stage
+
+  // lane l holds narrow rows 16j + 4(l/16) + e against wide column 16w + l%16
+  const int64_t wc = w0 + 16 * wave + i16;
+  if (wc >= w_cols) return;
+  const int64_t base = b * m.out_bstride;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j >= nblk) break;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t n = 16 * j + 4 * g4 + e;
+      if (n < n_cols) {
+        const int64_t o = narrow_is_d ? n : wc, k = narrow_is_d ? wc : n;
+        Elem<OT>::store(m.out, base + out_index(m, o, k), acc[j][e]);
+      }
+    }
+  }
+}
+
 // Row Gram with token splits: for the triangle tiles tile0 .. tile0 + count - 1
 // (row by row over T tiles per side), out (+)= the sum over splits s, in order,
 // of the compact partial tiles ws[s][t] (256 x 256 fp32 each).  Block (t, y):
@@ -986,7 +1105,22 @@ int launch(const MatArgs& m, int has_bias, hipStream_t st) {
   const int64_t max_ts = m.g_tstride > m.a_tstride ? m.g_tstride : m.a_tstride;
   const bool use_tr = Elem<DT>::kBytes == 2 && use_big && (m.tokens + trk::kTS) * max_ts < (1LL << 31) &&
                       m.g_tstride >= m.d * 2 && m.a_tstride >= m.k * 2;
-  if (use_tr) {
+  // one side at most 64 wide: the narrow-layer kernel (rows addressed by
+  // 32-bit buffer offsets, disjoint rows)
+  const bool use_narrow = Elem<DT>::kBytes == 2 && (m.d <= nw::kCols || m.k <= nw::kCols) &&
+                          (m.tokens + nw::kTS) * max_ts < (1LL << 31) && m.g_tstride >= m.d * 2 &&
+                          m.a_tstride >= m.k * 2;
+  if (use_narrow) {
+    MatArgs mn = m;
+    const int narrow_is_d = m.d <= nw::kCols ? 1 : 0;
+    mn.tiles_m = 1;
+    mn.tiles_n = ((narrow_is_d ? m.k : m.d) + nw::kCols - 1) / nw::kCols;
+    const int64_t nt = m.batch * mn.tiles_n;
+    if (nt > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "da_materialize_linear: too many tiles");
+    if constexpr (Elem<DT>::kBytes == 2) materialize_narrow<DT, OT><<<(unsigned)nt, 256, 0, st>>>(mn, narrow_is_d);
+    int rc = check_launch("da_materialize_linear(narrow)");
+    if (rc) return rc;
+  } else if (use_tr) {
     MatArgs mt = m;
     mt.tiles_m = (m.d + trk::kBM - 1) / trk::kBM;
     mt.tiles_n = (m.k + trk::kBN - 1) / trk::kBN;

@@ -41,6 +41,12 @@ MAT_CASES = [
     (1, 2048, 512, 768, False),   # 256x256-tile kernel, long token axis
     (3, 77, 512, 264, True),      # 256x256 tiles, ragged last stage, bias column
     (2, 31, 256, 256, False),     # 256x256 tiles, a single partial stage
+    # one side at most 64 wide (LoRA-like adapters): the narrow-layer kernel
+    (3, 77, 1024, 16, False),     # narrow d, ragged last stage
+    (2, 300, 16, 1000, True),     # narrow k, wide side past its last 64-column tile, bias column
+    (5, 64, 64, 520, False),      # narrow k at the 64-column limit
+    (4, 33, 48, 40, True),        # both sides narrow
+    (6, 130, 2048, 56, False),    # narrow d of four 16-row blocks, the last partial
 ]
 
 
