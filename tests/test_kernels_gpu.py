@@ -47,6 +47,9 @@ MAT_CASES = [
     (5, 64, 64, 520, False),      # narrow k at the 64-column limit
     (4, 33, 48, 40, True),        # both sides narrow
     (6, 130, 2048, 56, False),    # narrow d of four 16-row blocks, the last partial
+    (3, 77, 1024, 128, True),     # narrow d up to 128 (eight 16-row blocks)
+    (2, 100, 200, 1000, False),   # narrow k up to 256 (sixteen blocks, the last partial)
+    (4, 50, 136, 96, True),       # both under 256: the narrower side whole
 ]
 
 
