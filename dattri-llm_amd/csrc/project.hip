@@ -615,20 +615,27 @@ __global__ __launch_bounds__(kThreads, 1) void project_pieces(SkArgs args) {
 // sums are added in wave order.
 template <int OT>
 __global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int ka, int kg, char* out,
-                                                              int64_t out_bstride) {
+                                                              int64_t out_bstride, int64_t nb, int64_t tokens,
+                                                              int flat) {
   __shared__ f32x4 red[4][4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t id = blockIdx.x;
   const int64_t b = 8 * (id >> 5) + (id & 7);
   const int ob = (int)((id >> 3) & 3);
-  if (b >= args.batch || 16 * ob >= kg) return;  // uniform
+  if (b >= nb || 16 * ob >= kg) return;  // uniform
   const SkSide& SA = args.s[0];
   const SkSide& SG = args.s[1];
   f32x4 m[4];
 #pragma unroll
   for (int ib = 0; ib < 4; ++ib) m[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t ch = 0; ch < args.chunks; ++ch) {
-    const int64_t il = b * args.chunks + ch;
+  // Sample b's rows in the items' row space (128 rows per item): its own
+  // chunks, or, with short samples packed (flat), rows b*T .. of one run.
+  const int64_t r0 = flat ? b * tokens : b * args.chunks * ps::kTok;
+  const int64_t il0 = r0 / ps::kTok, il1 = (r0 + tokens - 1) / ps::kTok;
+  for (int64_t il = il0; il <= il1; ++il) {
+    // the item's rows [lo, hi) are this sample's
+    const int64_t lo = max(r0, il * ps::kTok) - il * ps::kTok;
+    const int64_t hi = min(r0 + tokens, (il + 1) * ps::kTok) - il * ps::kTok;
     const int64_t fa = SA.s0 + il * SA.nst, fg = SG.s0 + il * SG.nst;
     const int64_t a0 = sk_owner(fa, args), a1 = sk_owner(fa + SA.nst - 1, args);
     const int64_t g0 = sk_owner(fg, args), g1 = sk_owner(fg + SG.nst - 1, args);
@@ -658,6 +665,19 @@ __global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int k
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) vg[rb] += pg[(ob * 8 + rb) * 64];
     }
+    // rows outside [lo, hi): past the sample's last token (zero pieces) or
+    // another sample's (packed items) -- out of both products
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = 32 * wave + 16 * rb + 4 * (lane >> 4) + r;
+        if (row < lo || row >= hi) {
+          vg[rb][r] = 0.f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) va[rb][c][r] = 0.f;
+        }
+      }
     if (SA.bias) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -667,8 +687,8 @@ __global__ __launch_bounds__(kThreads) void outer_from_pieces(SkArgs args, int k
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int64_t t = ch * ps::kTok + 32 * wave + 16 * rb + 4 * (lane >> 4) + r;
-            if (t < args.tokens) va[rb][c][r] += bv;
+            const int64_t row = 32 * wave + 16 * rb + 4 * (lane >> 4) + r;
+            if (row >= lo && row < hi) va[rb][c][r] += bv;
           }
       }
     }
@@ -914,10 +934,17 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
   if (stream_ok) {
     // Stream-K projection of both sides into fp32 pieces, then the per-sample
     // contraction.
+    // Samples whose rows lie at one stride (batch stride = tokens x token
+    // stride on both sides) are packed: the items run over the B*T rows as
+    // one sample, so an item's 128 rows may hold several samples, and a
+    // sample's last rows share an item with the next sample's first instead
+    // of with zero rows.
+    const bool flat = batch > 1 && tokens % ps::kTok != 0 && o.a_bstride == tokens * o.a_tstride &&
+                      o.g_bstride == tokens * o.g_tstride;
     SkArgs sk;
-    sk.batch = batch;
-    sk.tokens = tokens;
-    sk.chunks = (tokens + ps::kTok - 1) / ps::kTok;
+    sk.batch = flat ? 1 : batch;
+    sk.tokens = flat ? batch * tokens : tokens;
+    sk.chunks = (sk.tokens + ps::kTok - 1) / ps::kTok;
     sk.pieces = (float*)workspace;
     int64_t s0 = 0;
     for (int side = 0; side < 2; ++side) {
@@ -931,7 +958,7 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
       S.pt_rstride = act ? o.pin_rstride : o.pout_rstride;
       S.ncols = act ? o.ka : o.kg;
       S.nst = (int)((S.wbytes + sk::kKB - 1) / sk::kKB);  // stream-K units (k-blocks) per item
-      S.items = batch * sk.chunks;
+      S.items = sk.batch * sk.chunks;
       S.s0 = s0;
       S.i0 = side * S.items;
       S.bias = act ? bias_in : nullptr;
@@ -955,9 +982,9 @@ int da_project_outer(const void* a, const void* g, int dtype, int64_t batch, int
     if (rc) return rc;
     const unsigned ob_blocks = (unsigned)(32 * ((batch + 7) / 8));  // 4 row blocks x 8 samples per 32 ids
     switch (out_dtype) {
-      case DA_F32: outer_from_pieces<DA_F32><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
-      case DA_BF16: outer_from_pieces<DA_BF16><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
-      default: outer_from_pieces<DA_F16><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride); break;
+      case DA_F32: outer_from_pieces<DA_F32><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride, batch, tokens, flat ? 1 : 0); break;
+      case DA_BF16: outer_from_pieces<DA_BF16><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride, batch, tokens, flat ? 1 : 0); break;
+      default: outer_from_pieces<DA_F16><<<ob_blocks, kThreads, 0, st>>>(sk, o.ka, o.kg, (char*)out, out_bstride, batch, tokens, flat ? 1 : 0); break;
     }
     return check_launch("da_project_outer(outer)");
   } else {

@@ -225,6 +225,13 @@ PROJ_CASES = [
     (3, 50, 512, 264, 32, 64, False, torch.bfloat16, True),    # sequence-first captures (token stride B*width)
     (9, 260, 2048, 4096, 64, 64, True, torch.float16, False),  # 3 chunks per sample, fp16
     (40, 128, 1024, 2752, 64, 48, False, torch.bfloat16, False),  # more stages than workgroups
+    # short samples packed into 128-row items (several samples per item)
+    (40, 16, 512, 264, 64, 48, True, torch.bfloat16, False),
+    (7, 100, 1024, 2752, 64, 64, True, torch.float16, False),  # samples straddle items
+    (33, 1, 256, 128, 32, 16, True, torch.float32, False),     # one token per sample
+    (9, 127, 2048, 512, 48, 64, False, torch.bfloat16, False),
+    (6, 40, 512, 264, 64, 32, True, torch.bfloat16, "slice"),  # batch stride above T rows: not packed
+    (12, 30, 256, 136, 24, 40, False, torch.bfloat16, True),   # sequence-first: not packed
 ]
 
 
@@ -235,7 +242,12 @@ def test_project_outer_kernel(device, case):
     b, t, k, d, ka, kg, bias, dtype, seq_first = case
     print(f"project_outer case={case}", flush=True)
     gen = torch.Generator().manual_seed(b * t + k)
-    if seq_first:
+    if seq_first == "slice":  # sliced on the device: a copy would be made dense
+        a_full, g_full = _rand(gen, b, t + 8, k, dtype=dtype), _rand(gen, b, t + 8, d, dtype=dtype)
+        a, g = a_full[:, 3:3 + t], g_full[:, 5:5 + t]
+        a_dev, g_dev = a_full.to(device)[:, 3:3 + t], g_full.to(device)[:, 5:5 + t]
+        assert a_dev.stride(0) != t * a_dev.stride(1)
+    elif seq_first:
         a = _rand(gen, t, b, k, dtype=dtype).transpose(0, 1)
         g = _rand(gen, t, b, d, dtype=dtype).transpose(0, 1)
     else:
@@ -243,7 +255,9 @@ def test_project_outer_kernel(device, case):
     p_in = _rand(gen, k, ka, dtype=dtype, scale=k**-0.5)
     p_out = _rand(gen, d, kg, dtype=dtype, scale=d**-0.5)
     bias_in = torch.randn(ka, generator=gen) if bias else None
-    got = kernels.project_outer(a.to(device), g.to(device), p_in.t().contiguous().to(device),
+    if seq_first != "slice":
+        a_dev, g_dev = a.to(device), g.to(device)
+    got = kernels.project_outer(a_dev, g_dev, p_in.t().contiguous().to(device),
                                 p_out.t().contiguous().to(device),
                                 bias_in=bias_in.to(device) if bias else None, out_dtype=torch.float32)
     p_in_np = _np(p_in)
