@@ -37,6 +37,7 @@ struct NormArgs {
   float eps;
   int has_bias;
   int64_t chunks;                                      // token chunks per sample
+  int64_t ring_rows;                                   // token rows per workgroup of the ring form
   float* partial;                                      // [batch][chunks][(1+bias)*dp]
 };
 
@@ -188,7 +189,9 @@ __device__ __forceinline__ float dot2_sq(uint32_t w, float acc) {
   }
 }
 
-constexpr int kRingRowsPerWG = 64;  // token rows per workgroup for the ring form
+// Token rows per workgroup of the ring form: 64, or 32 / 16 when fewer
+// workgroups would leave CUs idle (one long sample, a few short ones).
+constexpr int kRingRowsMax = 64, kRingRowsMin = 16;
 constexpr int kRingSlots = 2;
 constexpr int ring_waves(int) { return 4; }
 
@@ -215,8 +218,8 @@ __global__ __launch_bounds__(ring_waves(kQ) * kWave, 1) void norm_grad_ring(Norm
   const uint32_t lds_w = (uint32_t)(uintptr_t)(ring + uwave * kRingSlots * kSlot);
   const lds_char* const slot_ptr = (const lds_char*)(ring + uwave * kRingSlots * kSlot);
 
-  const int64_t t_begin = chunk * kRingRowsPerWG;
-  const int64_t t_end = min(t_begin + kRingRowsPerWG, a.tokens);
+  const int64_t t_begin = chunk * a.ring_rows;
+  const int64_t t_end = min(t_begin + a.ring_rows, a.tokens);
   const int nrows = (int)((t_end - t_begin - uwave + NW - 1) / NW);  // this wave's rows (may be <= 0)
 
   // Row i of this wave is token t_begin + uwave + NW*i, in slot i % 2.
@@ -363,22 +366,25 @@ __global__ __launch_bounds__(ring_waves(kQ) * kWave, 1) void norm_grad_ring(Norm
 }
 
 // out[b, f] = sum over the sample's chunk partials in a fixed order: the
-// chunks are split into four consecutive groups, one per wave; within a group
+// chunks are split into NG consecutive groups, one per wave; within a group
 // eight interleaved accumulators run in chunk order and are added in a fixed
-// tree, and the four group sums are added as (g0 + g1) + (g2 + g3).  The same
-// order on every call.  A lane owns four consecutive features (16-byte loads);
-// a workgroup covers 64 feature quads of one sample.  The partials hold each
-// block of d features at a pitch of dp (a multiple of 4): feature f of block
-// k = f / dp lands at out index k * d + f % dp when f % dp < d.
-template <int OT>
-__global__ __launch_bounds__(256) void norm_grad_reduce(const float* __restrict__ partial, int64_t batch,
-                                                        int64_t chunks, int64_t width, int64_t d, int64_t dp,
-                                                        char* out, int64_t out_bstride) {
-  __shared__ f32x4 red[3][64];
+// tree, and the group sums are added as (g0 + g1) + (g2 + g3) (NG = 4) or in
+// group order (NG = 16, for 128 or more chunks per sample -- one long sample
+// -- so that four times the loads are in flight).  The same order on every
+// call with the same chunk count.  A lane owns four consecutive features
+// (16-byte loads); a workgroup covers 64 feature quads of one sample.  The
+// partials hold each block of d features at a pitch of dp (a multiple of 4):
+// feature f of block k = f / dp lands at out index k * d + f % dp when
+// f % dp < d.
+template <int OT, int NG>
+__global__ __launch_bounds__(NG * 64) void norm_grad_reduce(const float* __restrict__ partial, int64_t batch,
+                                                            int64_t chunks, int64_t width, int64_t d, int64_t dp,
+                                                            char* out, int64_t out_bstride) {
+  __shared__ f32x4 red[NG - 1][64];
   const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int64_t f = ((int64_t)blockIdx.x * 64 + lane) * 4;
   const int64_t b = blockIdx.y;
-  const int64_t per = (chunks + 3) / 4;
+  const int64_t per = (chunks + NG - 1) / NG;
   const int64_t c0 = min(chunks, grp * per), c1 = min(chunks, c0 + per);
   f32x4 acc[8];
 #pragma unroll
@@ -397,7 +403,14 @@ __global__ __launch_bounds__(256) void norm_grad_reduce(const float* __restrict_
   if (grp > 0) red[grp - 1][lane] = s;
   __syncthreads();
   if (grp == 0 && f < width) {
-    const f32x4 t = (s + red[0][lane]) + (red[1][lane] + red[2][lane]);
+    f32x4 t;
+    if constexpr (NG == 4) {
+      t = (s + red[0][lane]) + (red[1][lane] + red[2][lane]);
+    } else {
+      t = s;
+#pragma unroll
+      for (int w = 0; w < NG - 1; ++w) t += red[w][lane];
+    }
     const int64_t k = f / dp, j = f - k * dp;  // dp % 4 == 0: the quad stays in one block
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -567,7 +580,16 @@ int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t 
     if (a.has_bias) norm_grad_wide<DT, true><<<grid, kWave, 0, st>>>(a);
     else norm_grad_wide<DT, false><<<grid, kWave, 0, st>>>(a);
   } else if (q <= 8 && a.tokens * max_ts < (1LL << 31) && a.dp == a.d) {
-    a.chunks = (a.tokens + kRingRowsPerWG - 1) / kRingRowsPerWG;
+    // At 8 KB rows a workgroup's ring takes most of a CU's LDS: aim for one
+    // workgroup per CU, else two.
+    int64_t cus = 0;
+    int rc = device_cu_count(&cus);
+    if (rc) return rc;
+    const int64_t want = cus * (q == 8 ? 1 : 2);
+    a.ring_rows = kRingRowsMax;
+    while (a.ring_rows > kRingRowsMin && a.batch * ((a.tokens + a.ring_rows - 1) / a.ring_rows) < want)
+      a.ring_rows /= 2;
+    a.chunks = (a.tokens + a.ring_rows - 1) / a.ring_rows;
     dim3 grid((unsigned)a.chunks, (unsigned)a.batch);
 #define DA_NORM_RING(Q)                                       \
   if (a.has_bias)                                             \
@@ -601,8 +623,12 @@ int launch_grad(NormArgs& a, int q, void* out, int64_t out_bstride, hipStream_t 
   int rc = check_launch("da_norm_weight_grad(chunks)");
   if (rc) return rc;
   dim3 g2((unsigned)((width / 4 + 63) / 64), (unsigned)a.batch);
-  norm_grad_reduce<OT><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, a.d, a.dp, (char*)out,
-                                           out_bstride);
+  if (a.chunks >= 128)
+    norm_grad_reduce<OT, 16><<<g2, 1024, 0, st>>>(a.partial, a.batch, a.chunks, width, a.d, a.dp, (char*)out,
+                                                  out_bstride);
+  else
+    norm_grad_reduce<OT, 4><<<g2, 256, 0, st>>>(a.partial, a.batch, a.chunks, width, a.d, a.dp, (char*)out,
+                                                out_bstride);
   return check_launch("da_norm_weight_grad(reduce)");
 }
 
@@ -650,7 +676,8 @@ int da_norm_weight_grad_workspace(int64_t batch, int64_t tokens, int64_t d, int 
                                   size_t* bytes) {
   if (batch < 0 || tokens < 0 || d < 0 || !bytes)
     return da::set_error(DA_ERR_INVALID, "da_norm_weight_grad_workspace: bad arguments");
-  const int64_t chunks = (tokens + da::kRowsPerWG - 1) / da::kRowsPerWG;
+  // chunks of the shortest token run any form gives a workgroup
+  const int64_t chunks = (tokens + da::kRingRowsMin - 1) / da::kRingRowsMin;
   const int64_t dp = (d + 7) / 8 * 8;  // whole 16-byte chunks of the narrowest element (2 bytes)
   *bytes = (size_t)(batch * chunks * (1 + (has_bias ? 1 : 0)) * dp) * sizeof(float);
   return DA_OK;
@@ -695,6 +722,7 @@ int da_norm_weight_grad(const void* x, const void* g, int dtype, int64_t batch, 
   a.eps = eps;
   a.has_bias = bias;
   a.chunks = (tokens + kRowsPerWG - 1) / kRowsPerWG;
+  a.ring_rows = 0;
   a.partial = (float*)workspace;
   hipStream_t st = (hipStream_t)stream;
 #define DA_NG(DT)                                                                  \

@@ -137,6 +137,10 @@ NORM_CASES = [
     (2, 33, 101, "nn.RMSNorm", False, 1e-6),
     (2, 70, 4099, "nn.LayerNorm", False, 1e-5),  # fp32: past the register form, the wide form
     (2, 37, 9000, "nn.LayerNorm", True, 1e-5),   # both dtypes in the wide form
+    # 16-bit rows of 8 KB in the LDS ring: 64, 32 and 16 token rows per workgroup on 256 CUs
+    (8, 2048, 4096, "nn.RMSNorm", False, 1e-6),
+    (1, 8192, 4096, "nn.RMSNorm", False, 1e-6),
+    (3, 1000, 4096, "nn.LayerNorm", True, 1e-5),
 ]
 
 
