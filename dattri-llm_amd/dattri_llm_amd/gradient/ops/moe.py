@@ -24,6 +24,8 @@ import torch
 from dattri_llm_amd import kernels
 from dattri_llm_amd.gradient.ops import dtypes
 
+_KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
 
 def router_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
     """``(weights, indices)`` of the top-k router; indices int64 (N, k)."""
@@ -104,14 +106,20 @@ def moe_layers_cross_gram(layers, segs1, segs2, *, out: torch.Tensor | None = No
     layers.  Groups are ordered widest layer first so the longest tiles are
     scheduled first."""
     groups1, groups2, biases, widths = [], [], [], []
+    auto = dtypes.get_compute_dtype() == "auto"
     for experts, bias in layers:
         if len(experts) != len(segs1) or len(experts) != len(segs2):
             raise ValueError("one (a1, g1, a2, g2) per expert, matching the segment lists")
         for e, (a1, g1, a2, g2) in enumerate(experts):
-            a1, g1, a2, g2 = dtypes.align(a1, g1, a2, g2)
-            kd = dtypes.kernel_dtype(a1.dtype)
-            groups1.append((a1.to(kd), g1.to(kd), *segs1[e]))
-            groups2.append((a2.to(kd), g2.to(kd), *segs2[e]))
+            dt = a1.dtype
+            # operands already in one kernel dtype under the "auto" policy
+            # pass as they are (a model's many experts: no per-expert casts)
+            if not (auto and g1.dtype == dt and a2.dtype == dt and g2.dtype == dt and dt in _KERNEL_DTYPES):
+                a1, g1, a2, g2 = dtypes.align(a1, g1, a2, g2)
+                kd = dtypes.kernel_dtype(a1.dtype)
+                a1, g1, a2, g2 = a1.to(kd), g1.to(kd), a2.to(kd), g2.to(kd)
+            groups1.append((a1, g1, *segs1[e]))
+            groups2.append((a2, g2, *segs2[e]))
             biases.append(bool(bias))
             widths.append(a1.shape[-1] + g1.shape[-1])
     if not groups1:

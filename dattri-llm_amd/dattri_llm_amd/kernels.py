@@ -13,6 +13,7 @@ import contextlib
 import ctypes
 import math
 
+import numpy as np
 import torch
 
 from dattri_llm_amd import _native as nat
@@ -514,6 +515,65 @@ def dense_per_token(
     return out
 
 
+# FactorSide as a numpy record, so a grouped launch's side arrays are filled
+# column by column instead of one ctypes structure per group (a launch may
+# carry hundreds of groups: the experts of an MoE layer, a depthwise conv).
+_SIDE_RECORD = np.dtype({"names": [f for f, _t in nat.FactorSide._fields_],
+                         "formats": ["<u8", "<u8", "<i8", "<i8", "<i8", "<i8", "<i8", "<i8", "<u8", "<u8", "<i4",
+                                     "<i4"],
+                         "offsets": [getattr(nat.FactorSide, f).offset for f, _t in nat.FactorSide._fields_],
+                         "itemsize": ctypes.sizeof(nat.FactorSide)})
+
+
+def _grouped_sides(groups, nb, ks, ds, biases, dev_index, dtype, vec, es, keep):
+    """One side's FactorSide array for :func:`ghost_gram_grouped`, checked."""
+    n = len(groups)
+    cols = {f: [0] * n for f in ("act", "grad", "tokens", "act_tstride", "grad_tstride", "seg_offsets",
+                                  "row_index")}
+    for e, (a, g, seg, idx) in enumerate(groups):
+        if a.dim() != 2 or g.dim() != 2:
+            raise ValueError("grouped factors must be (rows, width) with matching rows")
+        (ra, wa), (rg, wg) = a.shape, g.shape
+        if ra != rg:
+            raise ValueError("grouped factors must be (rows, width) with matching rows")
+        if a.dtype != dtype or g.dtype != dtype:
+            raise ValueError("grouped factors must share one dtype")
+        if seg.dtype != torch.int32 or seg.numel() != nb + 1 or (idx is not None and idx.dtype != torch.int32):
+            raise ValueError("segment offsets (B+1) and row indices must be int32, one batch per side")
+        for t in (a, g, seg, idx):
+            if t is not None and t.get_device() != dev_index:
+                nat.require_device(*[x for grp in groups for x in grp])  # raises with the reason
+                raise ValueError("grouped operands on different devices")
+        pa, pg = a.data_ptr(), g.data_ptr()
+        sa, sg = a.stride(), g.stride()
+        if not (wa == ks[e] and sa[1] == 1 and pa % 16 == 0 and (sa[0] * es) % 16 == 0):
+            a = prepare_rows(a, ks[e])
+            keep.append(a)
+            pa, sa = a.data_ptr(), a.stride()
+        if not (wg == ds[e] and sg[1] == 1 and pg % 16 == 0 and (sg[0] * es) % 16 == 0):
+            g = prepare_rows(g, ds[e])
+            keep.append(g)
+            pg, sg = g.data_ptr(), g.stride()
+        if not seg.is_contiguous():
+            seg = seg.contiguous()
+            keep.append(seg)
+        if idx is not None and not idx.is_contiguous():
+            idx = idx.contiguous()
+            keep.append(idx)
+        cols["act"][e], cols["grad"][e] = pa, pg
+        cols["tokens"][e] = ra
+        cols["act_tstride"][e], cols["grad_tstride"][e] = sa[0], sg[0]
+        cols["seg_offsets"][e] = seg.data_ptr()
+        cols["row_index"][e] = idx.data_ptr() if idx is not None else 0
+    rec = np.zeros(n, dtype=_SIDE_RECORD)
+    for f, v in cols.items():
+        rec[f] = v
+    rec["batch"] = nb
+    rec["has_bias"] = biases
+    keep.append(rec)
+    return (nat.FactorSide * n).from_buffer(rec)
+
+
 def ghost_gram_grouped(groups1, groups2, *, bias=False, out: torch.Tensor | None = None,
                        accumulate: bool = False) -> torch.Tensor:
     """Segment-summed ghost product over groups (experts of one or several
@@ -529,45 +589,32 @@ def ghost_gram_grouped(groups1, groups2, *, bias=False, out: torch.Tensor | None
     n = len(groups1)
     if len(groups2) != n or n == 0:
         raise ValueError("ghost_gram_grouped needs the same, non-zero number of groups on both sides")
-    biases = list(bias) if isinstance(bias, (list, tuple)) else [bias] * n
+    biases = [int(bool(x)) for x in bias] if isinstance(bias, (list, tuple)) else [int(bool(bias))] * n
     if len(biases) != n:
         raise ValueError("one bias flag per group")
-    flat = [t for grp in (*groups1, *groups2) for t in grp if t is not None]
-    dev = nat.require_device(*flat)
+    dev = nat.require_device(groups1[0][0])
+    dev_index = groups1[0][0].get_device()
     dtype = groups1[0][0].dtype
     b1, b2 = groups1[0][2].numel() - 1, groups2[0][2].numel() - 1
-    vec = _chunk_elems(dtype)
-    ks, ds = [], []
+    code = nat.dtype_code(dtype)  # raises for a dtype the kernels do not read
+    es = nat.ELEM_BYTES[dtype]
+    vec = 16 // es
+    ks, ds = [0] * n, [0] * n
     for e in range(n):
         kw, dw = groups1[e][0].shape[-1], groups1[e][1].shape[-1]
         if groups2[e][0].shape[-1] != kw or groups2[e][1].shape[-1] != dw:
             raise ValueError(f"group {e}: the two sides disagree on the layer widths")
-        ks.append(-(-kw // vec) * vec)
-        ds.append(-(-dw // vec) * vec)
-    sides = []
-    keep = []
-    for groups, nb in ((groups1, b1), (groups2, b2)):
-        row = []
-        for e, (a, g, seg, idx) in enumerate(groups):
-            if a.dim() != 2 or g.dim() != 2 or a.shape[0] != g.shape[0]:
-                raise ValueError("grouped factors must be (rows, width) with matching rows")
-            if a.dtype != dtype or g.dtype != dtype:
-                raise ValueError("grouped factors must share one dtype")
-            if seg.dtype != torch.int32 or seg.numel() != nb + 1 or (idx is not None and idx.dtype != torch.int32):
-                raise ValueError("segment offsets (B+1) and row indices must be int32, one batch per side")
-            a, g = prepare_rows(a, ks[e]), prepare_rows(g, ds[e])
-            seg = seg.contiguous()
-            idx = idx.contiguous() if idx is not None else None
-            keep += [a, g, seg, idx]
-            row.append(_side(a, g, biases[e], seg=seg, index=idx, tokens=a.shape[0]))
-        sides.append((nat.FactorSide * n)(*row))
+        ks[e] = -(-kw // vec) * vec
+        ds[e] = -(-dw // vec) * vec
+    keep: list = []
+    sides = [_grouped_sides(groups, nb, ks, ds, biases, dev_index, dtype, vec, es, keep)
+             for groups, nb in ((groups1, b1), (groups2, b2))]
     if out is None:
         out = torch.empty(b1, b2, dtype=torch.float32, device=dev)
         accumulate = False
     elif out.dtype != torch.float32 or tuple(out.shape) != (b1, b2) or out.stride(1) != 1:
         raise ValueError("out must be a float32 (B1, B2) tensor with unit column stride")
     karr, darr = (ctypes.c_int64 * n)(*ks), (ctypes.c_int64 * n)(*ds)
-    code = nat.dtype_code(dtype)
     lib = nat.load()
     nbytes = ctypes.c_size_t(0)
     nat.check(lib.da_ghost_gram_grouped_workspace(sides[0], sides[1], n, karr, darr, code, ctypes.byref(nbytes)),
