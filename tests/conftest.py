@@ -56,6 +56,14 @@ def roundings(n: int, dtype: str = "bfloat16") -> float:
     return TIGHT_FP32 + n * HALF_ULP[dtype]
 
 
+def stable_seed(case) -> int:
+    """A seed from a test case's parameters that is the same in every process
+    (``hash`` of a tuple holding strings is salted per process)."""
+    import zlib
+
+    return zlib.crc32(repr(case).encode()) % 1000
+
+
 def _dtype_name(dtype) -> str:
     return str(dtype).replace("torch.", "")
 

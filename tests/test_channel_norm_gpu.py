@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from conftest import assert_parity, roundings
+from conftest import HALF_ULP, SPEC_BAR, TIGHT_FP32, assert_parity, roundings, stable_seed
 
 pytestmark = pytest.mark.gpu
 
@@ -41,7 +41,7 @@ def test_channel_norm_ops(device, dtype, case):
 
     lt, n, c, sp, groups, bias = case
     mk = _mk(lt, c, groups, bias)
-    gen = torch.Generator().manual_seed(hash(case) % 1000)
+    gen = torch.Generator().manual_seed(stable_seed(case))
     raw = [(torch.randn(b, c, *sp, generator=gen) * 1.5 + 0.5).to(dtype) for b in (n, n - 1)]
     grads = [torch.randn(b, c, *sp, generator=gen).to(dtype) for b in (n, n - 1)]
     print(f"channel norm case={case} dtype={dtype}", flush=True)
@@ -62,8 +62,16 @@ def test_channel_norm_ops(device, dtype, case):
     assert_parity(gram, dense[0] @ dense[1].T, dtype, tight=tight, label="cross")
     assert_parity(ops.grad_norm_sq_factors(x1, g1, lt, mk), (dense[0] ** 2).sum(-1), dtype, tight=tight,
                   label="norm")
-    assert_parity(ops.dot_factors(x1[:n - 1], g1[:n - 1], x2, g2, lt, mk, mk), (dense[0][:n - 1] * dense[1]).sum(-1),
-                  dtype, tight=tight, label="dot")
+    # A per-sample dot of two C-wide rows may cancel: its error is measured
+    # against |row1| |row2| (the Cauchy-Schwarz scale of the sum), not |dot|.
+    dot = ops.dot_factors(x1[:n - 1], g1[:n - 1], x2, g2, lt, mk, mk)
+    assert dot.dtype == dtype
+    ref_dot = (dense[0][:n - 1] * dense[1]).sum(-1)
+    scale = np.linalg.norm(dense[0][:n - 1], axis=-1) * np.linalg.norm(dense[1], axis=-1)
+    dot_err = float(np.max(np.abs(dot.double().cpu().numpy() - ref_dot) / scale))
+    name = str(dtype).replace("torch.", "")
+    assert dot_err <= SPEC_BAR[name], f"dot error {dot_err:.3e} above the spec bar"
+    assert dot_err <= TIGHT_FP32 + HALF_ULP.get(name, 0.0), f"dot error {dot_err:.3e} above the tight bound"
     # per-token: positions of side 1 against side 2 (factorized, then dense)
     rows_ref = refs[0][0] * refs[0][1]
     pt_ref = np.einsum("bsd,cd->bsc", rows_ref, dense[1])
