@@ -3,7 +3,8 @@
 A numpy restatement of TRAIS-Lab/dattri-llm 0.1.0's ops on this path, each
 function citing the reference file:line it follows.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
-it, and only as the checker / the timed CPU baseline.  The product package
+it, and only as the reference results are compared with / the timed CPU
+baseline.  The product package
 (``dattri_llm_amd``) never imports it and has no CPU fallback.
 
 Every function computes in the dtype of its inputs (float64 for parity

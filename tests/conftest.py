@@ -38,7 +38,7 @@ def rel_err(got, ref) -> float:
     return float(np.abs(got - ref).max() / (denom if denom > 0 else 1.0)) if ref.size else 0.0
 
 
-# The north-star bar: normwise relative error for bf16/fp16 inputs with fp32
+# The spec bar: normwise relative error for bf16/fp16 inputs with fp32
 # accumulation, and for fp32 inputs.
 SPEC_BAR = {"bfloat16": 1e-2, "float16": 1e-2, "float32": 1e-3, "float64": 1e-3}
 # What fp32 accumulation against the float64 oracle on identical (already
@@ -73,7 +73,7 @@ def assert_parity(got, ref, in_dtype, *, out_dtype=None, tight=None, label=""):
 
     ``got`` is a tensor (its dtype is the output dtype unless ``out_dtype`` is
     given) or an array of fp32 results; ``in_dtype`` is the dtype of the
-    inputs the kernels read (picks the north-star bar).  The tight bound is
+    inputs the kernels read (picks the spec bar).  The tight bound is
     ``tight`` or TIGHT_FP32 plus the output rounding.  With DA_PARITY_LOG set,
     the tight bound is logged to that file instead of asserted (the spec bar
     still holds), to measure the errors the kernels leave."""
