@@ -236,6 +236,12 @@ PROJ_CASES = [
     (9, 127, 2048, 512, 48, 64, False, torch.bfloat16, False),
     (6, 40, 512, 264, 64, 32, True, torch.bfloat16, "slice"),  # batch stride above T rows: not packed
     (12, 30, 256, 136, 24, 40, False, torch.bfloat16, True),   # sequence-first: not packed
+    # samples over several items (partial blocks of M), contracted items and split ones
+    (4, 256, 512, 264, 64, 48, True, torch.bfloat16, False),
+    (5, 300, 256, 136, 32, 64, True, torch.bfloat16, "slice"),
+    (3, 4096, 4096, 1024, 64, 64, False, torch.bfloat16, False),
+    (1, 1000, 1024, 512, 64, 64, True, torch.float16, False),
+    (50, 10, 256, 128, 64, 64, False, torch.bfloat16, False),  # under 16 rows a sample: pieces only
 ]
 
 
