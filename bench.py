@@ -615,7 +615,7 @@ def bench_per_token(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "per-token cross-gram 256 train x 512 tok vs 64 query x 512 tok, d_in=d_out=4096"},
-        "roofline": {"bound": "mfma", "kernel": "ghost_per_token_v2", "achieved": round(tflops, 1),
+        "roofline": {"bound": "mfma", "kernel": "ghost_per_token_v3", "achieved": round(tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
                      "work_per_launch": f"{flops:.4g} flop = 2 x 256 x 64 pairs x 512^2 x (4096 + 4096)"},

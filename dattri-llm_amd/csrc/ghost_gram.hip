@@ -425,12 +425,14 @@ __global__ void grouped_reduce(GroupedArgs ga, float* __restrict__ out, int64_t 
 // of every operand row) through a ring of three LDS stages (48 KB each, two in
 // flight).  Operand rows go HBM -> LDS untouched by buffer loads with the
 // LDS-direct bit (16 bytes per lane); rows past a sample's end, and chunks past
-// the width, read as zero (offset past the buffer range).  The four waves each
-// own a 128 x 64 block (4 x 2 MFMA blocks of 32 x 32); K_a and K_g together
-// fill the 256 accumulator registers.  As in the dW kernel, the loads are
-// issued as inline assembly with explicit vmcnt waits, interleaved with the
-// MFMAs (a quarter stage of loads per quarter stage of MFMAs), and the last
-// quarter of each stage is multiplied after the barrier that opens the next.
+// the width, read as zero (offset past the buffer range).  Eight waves, two per
+// SIMD, each own a 64 x 64 block of both products (2 x 2 MFMA blocks of
+// 32 x 32, 128 accumulators), so one wave of a SIMD keeps the MFMA pipe busy
+// while the other waits at a barrier, for a load or on LDS.  As in the dW
+// kernel, the loads are issued as inline assembly with explicit vmcnt waits,
+// interleaved with the MFMAs (a quarter stage of loads per quarter stage of
+// MFMAs), and the last quarter of each stage is multiplied after the barrier
+// that opens the next.
 // ---------------------------------------------------------------------------
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -442,212 +444,21 @@ constexpr int kRows = kBM + kBN;         // LDS rows per stage
 constexpr int kSB = 128;                 // bytes of K per row and stage: one cache line, four 32-byte slices
 constexpr int kStage = kRows * kSB;      // 48 KB
 constexpr int kNBuf = 3;                 // ring: two stages in flight
-constexpr int kDma = kRows * (kSB / 16) / (kWave * 4);  // DMA instructions per wave and stage
 constexpr uint32_t kOob = 0x80000000u;
 constexpr int kPRow = kBN + 1;           // parked fp32 product row (grouped epilogue)
 constexpr int kRing = kNBuf * kStage;
 constexpr int kPark = kBM * kPRow * 4;
 constexpr int kSmem = kPark > kRing ? kPark : kRing;
-static_assert(kDma == 12, "three DMA instructions per quarter stage");
 static_assert(kSmem <= 160 * 1024, "LDS");
 // 16-byte chunk c of LDS row r sits in slot c ^ (r & 7): the 8 lanes one LDS
 // cycle serves (8 consecutive rows, one chunk) read 8 distinct bank groups.
 }  // namespace v2
 
-// Operand sources of one tile: buffer resources of the four factors and, per
-// lane, the byte offset of the row each of its 12 DMA instructions loads
-// (kOob for rows past an end), for the activation and the gradient.
-struct TileSrc {
-  u32x4 ra1, rg1, ra2, rg2;
-  uint32_t roff_a[v2::kDma], roff_g[v2::kDma];
-  int64_t kbytes_a, kbytes_g;
-};
-
-// Tile row loaded by lane `lane` of DMA instruction j of wave w.
-__device__ __forceinline__ int dma_row(int w, int j, int lane) { return 8 * (v2::kDma * w + j) + (lane >> 3); }
-
-// Load-issue state of one wave (plain locals after inlining).
-struct DmaState {
-  u32x4 ra1, rg1, ra2, rg2;            // wave-uniform
-  uint32_t roa[v2::kDma], rog[v2::kDma];
-  uint32_t cbyte, lds0;
-  int uwave, na, nst;
-  int64_t kba, kbg;
-};
-
-// Quarter q of stage st's loads = instructions 3q .. 3q+2 of every wave.
-// DMA instruction j of wave w loads tile rows 8*(12w + j) .. +7 (rows < 256 are
-// side 1); lane l -> row 8*(12w+j) + l/8, slot l%8 holding logical chunk
-// (l%8) ^ (l/8), which is cbyte / 16.
-__device__ __forceinline__ void dma_quarter(const DmaState& D, int q, int st, int x0 = 0, int x1 = 3) {
-  const bool act = st < D.na;
-  const uint32_t koff = (uint32_t)(act ? st : st - D.na) * v2::kSB;
-  const int64_t kb = act ? D.kba : D.kbg;
-  const bool kin = st < D.nst && (int64_t)(koff + D.cbyte) < kb;
-  const uint32_t base = D.lds0 + (uint32_t)((st % v2::kNBuf) * v2::kStage + v2::kDma * D.uwave * 8 * v2::kSB);
-#pragma unroll
-  for (int x = x0; x < x1; ++x) {
-    const int j = 3 * q + x;
-    const bool side1 = v2::kDma * D.uwave + j < v2::kBM / 8;  // uniform
-    const uint32_t m = act ? 0xffffffffu : 0u;
-    const uint32_t roff = (D.roa[j] & m) | (D.rog[j] & ~m);
-    // Mask arithmetic, not a select: a select between the four descriptors is
-    // turned into a pointer select over stack copies (a scratch load, and the
-    // compiler then waits for every outstanding load before using it).
-    const uint32_t ms = side1 ? 0xffffffffu : 0u;
-    u32x4 rs;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      rs[c] = (((D.ra1[c] & m) | (D.rg1[c] & ~m)) & ms) | (((D.ra2[c] & m) | (D.rg2[c] & ~m)) & ~ms);
-    dma16(rs, base + (uint32_t)(j * 8 * v2::kSB), (kin && roff != v2::kOob) ? roff + koff + D.cbyte : v2::kOob);
-  }
-}
-
-// One quarter of a stage: the 8 MFMAs of one slice held in (ua, ub) into acc;
-// with rd, the 6 fragment reads of the slice (stage base sb, slice kk) into
-// (na, nb) interleaved one per MFMA; with qd >= 0, quarter qd of stage dst's
-// loads, one instruction after each of MFMAs 1, 3 and 5 (spread out, so the
-// address unit never queues a wave's loads behind each other).
-template <int DT>
-__device__ __forceinline__ void ghost_quarter(f32x16 (&acc)[4][2], const u32x4 (&ua)[4], const u32x4 (&ub)[2],
-                                              bool rd, const lds_char* sb, int coff, int wm, int wn,
-                                              u32x4 (&na)[4], u32x4 (&nb)[2], const DmaState& D, int qd, int dst) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (rd) {
-      if (i < 4) na[i] = *(const u32x4*)(sb + (128 * wm + 32 * i) * v2::kSB + coff);
-      else if (i < 6) nb[i - 4] = *(const u32x4*)(sb + (v2::kBM + 64 * wn + 32 * (i - 4)) * v2::kSB + coff);
-    }
-    Mfma32<DT>::mma(acc[i >> 1][i & 1], ua[i >> 1], ub[i & 1]);
-    if (qd >= 0 && (i == 1 || i == 3 || i == 5)) dma_quarter(D, qd, dst, i / 2, i / 2 + 1);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// Wait for this wave's loads of the next stage (the 12 instructions of the
-// stage after it may stay in flight) and its own LDS reads, then barrier.  The
-// LDS wait is the compiler's own s_waitcnt (lgkmcnt(0), others at maximum) so
-// it knows the fragments in registers are complete.
-__device__ __forceinline__ void ghost_stage_sync() {
-  static_assert(v2::kNBuf == 3, "vmcnt below is one stage of 12 instructions");
-  asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  asm volatile("s_barrier" ::: "memory");
-}
-
-// Runs the tile's K stages; returns with every wave done reading the ring
-// (so the caller may reuse the LDS) and no load in flight.
-// kHasA: the tile has activation stages (K > 0), multiplied into ka before
-// the gradient stages into kg; otherwise every stage goes to kg and ka stays 0.
-template <int DT, bool kHasA>
-__device__ __forceinline__ void ghost_tile_engine(const TileSrc& S, char* smem, f32x16 (&ka)[4][2],
-                                                  f32x16 (&kg)[4][2]) {
-  lds_char* const L = (lds_char*)smem;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  DmaState D;
-  D.uwave = __builtin_amdgcn_readfirstlane(wave);
-  D.na = (int)((S.kbytes_a + v2::kSB - 1) / v2::kSB);
-  D.nst = D.na + (int)((S.kbytes_g + v2::kSB - 1) / v2::kSB);
-  D.ra1 = uniform4(S.ra1);
-  D.rg1 = uniform4(S.rg1);
-  D.ra2 = uniform4(S.ra2);
-  D.rg2 = uniform4(S.rg2);
-  D.kba = S.kbytes_a;
-  D.kbg = S.kbytes_g;
-  D.lds0 = (uint32_t)(uintptr_t)L;
-  D.cbyte = 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
-#pragma unroll
-  for (int j = 0; j < v2::kDma; ++j) {
-    D.roa[j] = S.roff_a[j];
-    D.rog[j] = S.roff_g[j];
-  }
-  const int na = D.na, nst = D.nst;
-
-  // Fragment offsets inside a stage: A fragment x = rows 128wm + 32x + l%32,
-  // B fragment y = rows 256 + 64wn + 32y + l%32; slice kk reads logical chunk
-  // 2kk + l/32, stored in slot (2kk + l/32) ^ (l%8).
-  const int lrow = lane & 31, hh = lane >> 5;
-  const int c0 = lrow * v2::kSB + (((0 + hh) ^ (lane & 7)) << 4), c1 = lrow * v2::kSB + (((2 + hh) ^ (lane & 7)) << 4);
-  const int c2 = lrow * v2::kSB + (((4 + hh) ^ (lane & 7)) << 4), c3 = lrow * v2::kSB + (((6 + hh) ^ (lane & 7)) << 4);
-  // Slice kk of every stage lives in fragment buffer kk.
-  u32x4 fa[4][4], fb[4][2];
-
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      ka[x][y] = f32x16{};
-      kg[x][y] = f32x16{};
-    }
-
-  // Fragments are read two slices ahead of their MFMAs, so a read has a whole
-  // quarter (8 MFMAs) to come back while the DMA writes share the LDS.  A loop
-  // body starts right after a barrier (no read in flight, so the loop header
-  // needs no wait): it multiplies slices 2 and 3 of stage st and slices 0 and
-  // 1 of st + 1 while reading slices 0..3 of st + 1, loads stage st + 3 into
-  // the buffer stage st left (its reads all ended before that barrier), then
-  // waits for stage st + 2.  Exactly the 12 instructions of the body's own
-  // loads follow the awaited stage's last one at every barrier.
-#pragma unroll
-  for (int s0 = 0; s0 < v2::kNBuf - 1; ++s0)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) dma_quarter(D, q, s0);
-  ghost_stage_sync();
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int co = kk == 0 ? c0 : c1;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) fa[kk][x] = *(const u32x4*)(L + (128 * wm + 32 * x) * v2::kSB + co);
-#pragma unroll
-    for (int y = 0; y < 2; ++y) fb[kk][y] = *(const u32x4*)(L + (v2::kBM + 64 * wn + 32 * y) * v2::kSB + co);
-  }
-  dma_quarter(D, 0, v2::kNBuf - 1);
-  dma_quarter(D, 1, v2::kNBuf - 1);
-  {
-    f32x16(&acc0)[4][2] = kHasA ? ka : kg;
-    ghost_quarter<DT>(acc0, fa[0], fb[0], true, L, c2, wm, wn, fa[2], fb[2], D, 2, v2::kNBuf - 1);
-    ghost_quarter<DT>(acc0, fa[1], fb[1], true, L, c3, wm, wn, fa[3], fb[3], D, 3, v2::kNBuf - 1);
-  }
-  ghost_stage_sync();
-
-  // The loops carry no branch around their MFMAs (a join there makes the
-  // register allocator shuffle accumulators): the activation loop, the body
-  // that crosses into the gradient stages and the gradient loop are separate,
-  // and the last stage's second half is peeled (nst > na, and na >= 1 when
-  // kHasA, because both widths are non-zero).
-#define DA_GHOST_BODY(A1, A2)                                                                         \
-  {                                                                                                   \
-    const lds_char* nxt = L + ((st + 1) % v2::kNBuf) * v2::kStage;                                    \
-    ghost_quarter<DT>(A1, fa[2], fb[2], true, nxt, c0, wm, wn, fa[0], fb[0], D, 0, st + 3);           \
-    ghost_quarter<DT>(A1, fa[3], fb[3], true, nxt, c1, wm, wn, fa[1], fb[1], D, 1, st + 3);           \
-    ghost_quarter<DT>(A2, fa[0], fb[0], true, nxt, c2, wm, wn, fa[2], fb[2], D, 2, st + 3);           \
-    ghost_quarter<DT>(A2, fa[1], fb[1], true, nxt, c3, wm, wn, fa[3], fb[3], D, 3, st + 3);           \
-    ghost_stage_sync();                                                                               \
-  }
-  if constexpr (kHasA) {
-    for (int st = 0; st + 1 < na; ++st) DA_GHOST_BODY(ka, ka)
-    {
-      const int st = na - 1;
-      DA_GHOST_BODY(ka, kg)
-    }
-  }
-  for (int st = kHasA ? na : 0; st + 1 < nst; ++st) DA_GHOST_BODY(kg, kg)
-#undef DA_GHOST_BODY
-  ghost_quarter<DT>(kg, fa[2], fb[2], false, L, c0, wm, wn, fa[0], fb[0], D, -1, 0);
-  ghost_quarter<DT>(kg, fa[3], fb[3], false, L, c1, wm, wn, fa[1], fb[1], D, -1, 0);
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // ---------------------------------------------------------------------------
-// The same 256 x 128 tile on 8 waves (two per SIMD).  Wave w owns the 64 x 64
-// block at side-1 rows 64 (w / 2) and side-2 rows 64 (w % 2) of both Grams
-// (2 x 2 MFMA blocks each, 128 accumulators), so two waves fit one SIMD's
-// registers and one keeps the MFMA pipe busy while the other waits at a
-// barrier, for a load or on LDS.  A 32-byte K slice costs 4 fragment reads per
-// 4 MFMAs (8 reads per 8 with the 4-wave blocks of 128 x 64: 6); the stage,
-// ring, swizzle and row layout are the 4-wave engine's, with 6 DMA
-// instructions per wave and stage (wave w loads tile rows 48w .. 48w+47).
+// The engine's per-wave layout: wave w owns the 64 x 64 block at side-1 rows
+// 64 (w / 2) and side-2 rows 64 (w % 2); a 32-byte K slice costs it 4 fragment
+// reads per 4 MFMAs.  Each wave issues 6 DMA instructions per stage (wave w
+// loads tile rows 48w .. 48w+47).
 // ---------------------------------------------------------------------------
 namespace v3 {
 constexpr int kWaves = 8;
@@ -674,8 +485,13 @@ struct DmaState8 {
   int64_t kba, kbg;
 };
 
-// Instructions [j0, j1) of stage st's loads for this wave (the 4-wave
-// engine's dma_quarter, 6 instructions per wave and stage).
+// Instructions [j0, j1) of stage st's loads for this wave (6 per wave and
+// stage).  Instruction j of wave w loads tile rows 8*(6w + j) .. +7 (rows <
+// 256 are side 1); lane l -> row 8*(6w+j) + l/8, slot l%8 holding logical
+// chunk (l%8) ^ (l/8), which is cbyte / 16.  A select between the four
+// descriptors would be turned into a pointer select over stack copies (a
+// scratch load, and the compiler then waits for every outstanding load before
+// using it), so the descriptor is picked by mask arithmetic.
 __device__ __forceinline__ void dma_part8(const DmaState8& D, int st, int j0, int j1) {
   const bool act = st < D.na;
   const uint32_t koff = (uint32_t)(act ? st : st - D.na) * v2::kSB;
@@ -723,7 +539,21 @@ __device__ __forceinline__ void ghost_stage_sync8() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-// The 4-wave engine's schedule (see ghost_tile_engine) on 8 waves.
+// Runs the tile's K stages; returns with every wave done reading the ring
+// (so the caller may reuse the LDS) and no load in flight.
+// kHasA: the tile has activation stages (K > 0), multiplied into ka before
+// the gradient stages into kg; otherwise every stage goes to kg and ka stays 0.
+// Fragment offsets inside a stage: A fragment x = rows 64wm + 32x + l%32, B
+// fragment y = rows 256 + 64wn + 32y + l%32; slice kk reads logical chunk
+// 2kk + l/32, stored in slot (2kk + l/32) ^ (l%8).  Fragments are read two
+// slices ahead of their MFMAs, so a read has a whole slice of MFMAs to come
+// back while the DMA writes share the LDS.  A loop body starts right after a
+// barrier (no read in flight, so the loop header needs no wait): it
+// multiplies slices 2 and 3 of stage st and slices 0 and 1 of st + 1 while
+// reading slices 0..3 of st + 1, loads stage st + 3 into the buffer stage st
+// left (its reads all ended before that barrier), then waits for stage st + 2.
+// Exactly the 6 instructions of the body's own loads follow the awaited
+// stage's last one at every barrier.
 template <int DT, bool kHasA>
 __device__ __forceinline__ void ghost_tile_engine8(const TileSrc8& S, char* smem, f32x16 (&ka)[2][2],
                                                    f32x16 (&kg)[2][2]) {
@@ -881,10 +711,8 @@ __global__ __launch_bounds__(v3::kThreads, 1) void ghost_gram_tiles_v3(GhostArgs
   if (tid == 0) *dst = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
 }
 
-// Grouped (MoE) mode on the 8-wave engine: tiles over each group's packed
-// rows, the tile's products parked in LDS and binned by sample pair.  Each
-// K_a / K_g entry is the same MFMA chain as on the 4-wave engine, so the
-// parked products, and the bins summed from them, are bit-identical to it.
+// Grouped (MoE) mode: tiles over each group's packed rows, the tile's
+// products parked in LDS and binned by sample pair.
 template <int DT>
 __global__ __launch_bounds__(v3::kThreads, 1) void ghost_grouped_tiles_v3(GroupedArgs ga) {
   __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
@@ -973,7 +801,7 @@ struct PerTokArgs {
 };
 
 template <int DT, bool kDense>
-__global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) {
+__global__ __launch_bounds__(v3::kThreads, 1) void ghost_per_token_v3(PerTokArgs g) {
   __shared__ __attribute__((aligned(1024))) char smem[v2::kSmem];
   constexpr int64_t kRowGroup = 4;
   const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -991,7 +819,7 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) 
   const int64_t len1 = g.s1.tokens, len2 = g.s2.tokens;
   const int64_t t0 = tt * v2::kBM, s0 = ss * v2::kBN;
   if (t0 >= len1) return;  // uniform: no row of this tile is read back
-  TileSrc S;
+  TileSrc8 S;
   S.ra1 = make_rsrc(g.s1.act + i * g.s1.act_bstride, 0x7fffffffu);
   S.rg1 = make_rsrc((kDense ? g.s1.act : g.s1.grad) + i * (kDense ? g.s1.act_bstride : g.s1.grad_bstride),
                     0x7fffffffu);
@@ -1001,8 +829,8 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) 
   S.kbytes_a = g.kbytes_a;
   S.kbytes_g = g.kbytes_g;
 #pragma unroll
-  for (int q = 0; q < v2::kDma; ++q) {
-    const int row = dma_row(wave, q, lane);
+  for (int q = 0; q < v3::kDma; ++q) {
+    const int row = dma_row8(wave, q, lane);
     const bool side1 = row < v2::kBM;
     const int64_t t = side1 ? t0 + row : s0 + row - v2::kBM;
     if (t < (side1 ? len1 : len2)) {
@@ -1015,16 +843,16 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) 
       S.roff_g[q] = v2::kOob;
     }
   }
-  f32x16 ka[4][2], kg[4][2];
-  ghost_tile_engine<DT, !kDense>(S, smem, ka, kg);
+  f32x16 ka[2][2], kg[2][2];
+  ghost_tile_engine8<DT, !kDense>(S, smem, ka, kg);
   float* P = (float*)smem;
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int y = 0; y < 2; ++y)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = 128 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
+        const int row = 64 * wm + 32 * x + acc_row(r, lane), col = 64 * wn + 32 * y + acc_col(lane);
         float v;
         if constexpr (kDense) {
           const int64_t t = t0 + row, o = s0 + col;
@@ -1040,7 +868,7 @@ __global__ __launch_bounds__(kThreads, 1) void ghost_per_token_v2(PerTokArgs g) 
   __syncthreads();
   // one thread per row: the row's 128 columns in order (zero past side 2's end)
   const int64_t t = t0 + tid;
-  if (t < len1) {
+  if (tid < v2::kBM && t < len1) {
     const float* pr = P + tid * v2::kPRow;
     float sum = 0.f;
     for (int c = 0; c < v2::kBN; ++c) sum += pr[c];
@@ -1168,7 +996,11 @@ int per_token_launch(const PerTokArgs& g, bool dense, int dtype, int64_t len1, f
                      int64_t ld_t, int64_t ld_b2, int accumulate, hipStream_t st, const char* who) {
   const int64_t tiles = g.n_r * g.n_c;
   if (tiles > 0x7fffffffLL) return set_error(DA_ERR_INVALID, "%s: problem too large", who);
-#define DA_PT(DT)                                                                                            if (dense) ghost_per_token_v2<DT, true><<<(unsigned)tiles, kThreads, 0, st>>>(g);                           else ghost_per_token_v2<DT, false><<<(unsigned)tiles, kThreads, 0, st>>>(g);
+#define DA_PT(DT)                                                                  \
+  if (dense)                                                                       \
+    ghost_per_token_v3<DT, true><<<(unsigned)tiles, v3::kThreads, 0, st>>>(g);     \
+  else                                                                             \
+    ghost_per_token_v3<DT, false><<<(unsigned)tiles, v3::kThreads, 0, st>>>(g);
   switch (dtype) {
     case DA_BF16: DA_PT(DA_BF16) break;
     case DA_F16: DA_PT(DA_F16) break;
