@@ -661,22 +661,26 @@ int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers
 // -- the per-sample squared gradient norms of GradCos and the per-sample dots
 // of two blocks, on the dense route.  HBM-bound: every weight is read once.
 // The rows are walked block-major in stages of S consecutive 64-element blocks
-// of R rows (R * S * C = 1024 16-byte chunks, 4 per thread), so in the
+// of R rows (R * S * C = kStage 16-byte chunks, kPer per thread), so in the
 // k-blocked layout a stage reads S contiguous runs and in the row-major one R
-// runs of S blocks.  A workgroup owns one row tile and one range of stages and
-// writes one fp32 partial per row; a second kernel adds a row's partials in
+// runs of S blocks.  Every layer starts a new stage (its blocks padded to whole
+// stages), so the layer of a stage is uniform across the workgroup and its
+// description comes through scalar loads.  A thread issues all its loads of a
+// stage before the first product (chunks past the data read the layer's first
+// chunk and are masked).  A workgroup owns one row tile and one range of stages
+// and writes one fp32 partial per row; a second kernel adds a row's partials in
 // range order (deterministic).
 // ---------------------------------------------------------------------------
 namespace rd {
 constexpr int kThreads = 256;
-constexpr int kPer = 4;                        // 16-byte chunks per thread and stage
+constexpr int kPer = 8;                        // 16-byte chunks per thread and stage
 constexpr int kStage = kThreads * kPer;        // chunks per stage
 struct Layer {
   const char* m1;
   const char* m2;                              // == m1 for a squared norm
   int64_t ld1, blk1, ld2, blk2;                // bytes
   int64_t bytes;                               // row width in bytes
-  int64_t blocks;                              // 64-element blocks per row
+  int64_t stage0;                              // the layer's first stage
 };
 struct Args {
   Layer layers[kMaxLayers];
@@ -697,41 +701,48 @@ __global__ __launch_bounds__(rd::kThreads) void row_dots_kernel(rd::Args a) {
   const int R = (int)a.tile_rows, S = (int)a.stage_blocks;
   const int64_t rt = blockIdx.x / a.ranges, w = blockIdx.x % a.ranges;
   const int64_t st0 = w * a.stages / a.ranges, st1 = (w + 1) * a.stages / a.ranges;
-  int row[rd::kPer], cb[rd::kPer], il[rd::kPer];
-  int64_t jb[rd::kPer];
+  int row[rd::kPer], cb[rd::kPer], bo[rd::kPer];
   float acc[rd::kPer];
 #pragma unroll
   for (int k = 0; k < rd::kPer; ++k) {
     const int q = tid + k * rd::kThreads;      // chunk q of a stage: block q / (R*C), row, chunk
     row[k] = (q % (R * C)) / C;
     cb[k] = q % C;
+    bo[k] = q / (R * C);
     acc[k] = 0.f;
-    il[k] = 0;
-    jb[k] = st0 * S + q / (R * C);             // global block index, then the layer cursor
-    while (il[k] < a.n_layers && jb[k] >= a.layers[il[k]].blocks) jb[k] -= a.layers[il[k]++].blocks;
   }
+  int l = 0;  // the stage's layer (uniform)
   for (int64_t st = st0; st < st1; ++st) {
+    while (l + 1 < a.n_layers && st >= a.layers[l + 1].stage0) ++l;
+    const rd::Layer& L = a.layers[l];
+    const int64_t jb0 = (st - L.stage0) * S;
+    u32x4 vx[rd::kPer], vy[rd::kPer];
+    bool live[rd::kPer];
 #pragma unroll
     for (int k = 0; k < rd::kPer; ++k) {
-      const int64_t r = rt * R + row[k];
-      if (il[k] < a.n_layers && r < a.rows) {
-        const rd::Layer& L = a.layers[il[k]];
-        const int64_t byte = jb[k] * 64 * Elem<DT>::kBytes + cb[k] * 16;
-        if (byte < L.bytes) {
-          float x[V], y[V];
-          unpack16<DT>(ld16(L.m1 + r * L.ld1 + jb[k] * L.blk1 + cb[k] * 16), x);
-          if (L.m2 == L.m1) {
+      const int64_t r = rt * R + row[k], jb = jb0 + bo[k];
+      live[k] = r < a.rows && jb * 64 * Elem<DT>::kBytes + cb[k] * 16 < L.bytes;
+      vx[k] = ld16(L.m1 + (live[k] ? r * L.ld1 + jb * L.blk1 + cb[k] * 16 : 0));
+    }
+    if (L.m2 != L.m1) {  // uniform
 #pragma unroll
-            for (int e = 0; e < V; ++e) acc[k] += x[e] * x[e];
-          } else {
-            unpack16<DT>(ld16(L.m2 + r * L.ld2 + jb[k] * L.blk2 + cb[k] * 16), y);
-#pragma unroll
-            for (int e = 0; e < V; ++e) acc[k] += x[e] * y[e];
-          }
-        }
+      for (int k = 0; k < rd::kPer; ++k) {
+        const int64_t r = rt * R + row[k], jb = jb0 + bo[k];
+        vy[k] = ld16(L.m2 + (live[k] ? r * L.ld2 + jb * L.blk2 + cb[k] * 16 : 0));
       }
-      jb[k] += S;
-      while (il[k] < a.n_layers && jb[k] >= a.layers[il[k]].blocks) jb[k] -= a.layers[il[k]++].blocks;
+    } else {
+#pragma unroll
+      for (int k = 0; k < rd::kPer; ++k) vy[k] = vx[k];
+    }
+#pragma unroll
+    for (int k = 0; k < rd::kPer; ++k) {
+      if (live[k]) {
+        float x[V], y[V];
+        unpack16<DT>(vx[k], x);
+        unpack16<DT>(vy[k], y);
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[k] += x[e] * y[e];
+      }
     }
   }
 #pragma unroll
@@ -762,9 +773,13 @@ int row_dots_plan(int64_t rows, const da_dense_layer* layers, int n_layers, int 
   if (n_layers < 0 || (n_layers > 0 && !layers)) return set_error(DA_ERR_INVALID, "%s: bad layer list", who);
   if (n_layers > kMaxLayers) return set_error(DA_ERR_INVALID, "%s: at most %d layers per call", who, kMaxLayers);
   const int64_t es = (int64_t)elem_bytes(dtype);
+  const int64_t C = 4 * es;                       // chunks per block
+  int64_t R = 1;
+  while (R < rows && R * C < rd::kStage) R *= 2;  // rows per tile, a power of two with R * C <= kStage
+  const int64_t S = rd::kStage / (R * C);         // blocks per stage
   rd::Args& a = p->args;
   a.n_layers = 0;
-  int64_t blocks = 0;
+  int64_t stages = 0;
   for (int l = 0; l < n_layers; ++l) {
     const da_dense_layer& L = layers[l];
     const bool sq = L.m2 == nullptr;
@@ -786,16 +801,13 @@ int row_dots_plan(int64_t rows, const da_dense_layer* layers, int n_layers, int 
     D.blk1 = blk1 * es;
     D.blk2 = blk2 * es;
     D.bytes = L.width * es;
-    D.blocks = (L.width + 63) / 64;
-    blocks += D.blocks;
+    D.stage0 = stages;
+    stages += ((L.width + 63) / 64 + S - 1) / S;  // the layer's blocks in whole stages
   }
-  const int64_t C = 4 * es;                       // chunks per block
-  int64_t R = 1;
-  while (R < rows && R * C < rd::kStage) R *= 2;  // rows per tile, a power of two with R * C <= 1024
   a.rows = rows;
   a.tile_rows = R;
-  a.stage_blocks = rd::kStage / (R * C);
-  a.stages = (blocks + a.stage_blocks - 1) / a.stage_blocks;
+  a.stage_blocks = S;
+  a.stages = stages;
   p->row_tiles = rows > 0 ? (rows + R - 1) / R : 0;
   a.ranges = 1;
   p->ws = 0;
@@ -804,7 +816,7 @@ int row_dots_plan(int64_t rows, const da_dense_layer* layers, int n_layers, int 
   const int rc = device_cu_count(&cus);
   if (rc) return rc;
   int64_t ranges = 4 * cus / p->row_tiles;         // ~4 workgroups per CU in all
-  const int64_t most = a.stages / 16 > 0 ? a.stages / 16 : 1;  // at least 16 stages per workgroup
+  const int64_t most = a.stages / 8 > 0 ? a.stages / 8 : 1;  // at least 8 stages per workgroup
   if (ranges > most) ranges = most;
   if (ranges < 1) ranges = 1;
   a.ranges = ranges;
