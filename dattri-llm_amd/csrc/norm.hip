@@ -418,6 +418,33 @@ __global__ __launch_bounds__(NG * 64) void norm_grad_reduce(const float* __restr
   }
 }
 
+// N consecutive outputs in the output dtype through 8- or 16-byte stores,
+// each value rounded as Elem<OT>::store rounds it.  dst is aligned to
+// min(N * bytes, 16).
+template <int OT, int N>
+__device__ __forceinline__ void store_chunk(char* dst, const float (&v)[N]) {
+  if constexpr (Elem<OT>::kBytes == 2) {
+    uint32_t w[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      uint16_t lo, hi;
+      if constexpr (OT == DA_BF16) {
+        lo = f32_to_bf16_bits(v[2 * i]);
+        hi = f32_to_bf16_bits(v[2 * i + 1]);
+      } else {
+        lo = f32_to_f16_bits(v[2 * i]);
+        hi = f32_to_f16_bits(v[2 * i + 1]);
+      }
+      w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    if constexpr (N == 8) *(u32x4*)dst = u32x4{w[0], w[1], w[2], w[3]};
+    else *(u32x2*)dst = u32x2{w[0], w[1]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) *(f32x4*)(dst + 4 * i) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+  }
+}
+
 // x_hat rows for the preprocess API: one wave per row, same math as above.
 template <int DT, int OT, int kQ>
 __global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_t rows, int64_t d,
@@ -456,12 +483,22 @@ __global__ __launch_bounds__(kThreads) void norm_xhat_rows(const char* x, int64_
     }
   }
   const float rstd = kind == 2 ? 1.f : 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
+  constexpr int OS = Elem<OT>::kBytes;
+  constexpr int kAlign = VEC * OS < 16 ? VEC * OS : 16;  // the widest store a chunk's outputs take
 #pragma unroll
   for (int q = 0; q < kQ; ++q) {
     const int64_t c = lane + (int64_t)q * kWave;
+    float y[VEC];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e)
-      if (c * VEC + e < d) Elem<OT>::store(out, row * out_rstride + c * VEC + e, (xv[q][e] - mean) * rstd);
+    for (int e = 0; e < VEC; ++e) y[e] = (xv[q][e] - mean) * rstd;
+    char* dst = out + (row * out_rstride + c * VEC) * OS;
+    if ((c + 1) * VEC <= d && ((uintptr_t)dst % kAlign) == 0) {
+      store_chunk<OT, VEC>(dst, y);  // the chunk's outputs in whole 8- or 16-byte stores
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if (c * VEC + e < d) Elem<OT>::store(out, row * out_rstride + c * VEC + e, y[e]);
+    }
   }
 }
 
