@@ -195,9 +195,13 @@ __global__ __launch_bounds__(256) void counting_sort_kernel(SortArgs a) {
 //   by e      -> entries[off[e] + r] = p for expert e's local row r (routed order);
 //   by e*B+b  -> rows[off2[e*B+b] + q] = r, expert e's local rows grouped by sample,
 // and seg[e*(B+1) + b] = off2[e*B+b] - off2[e*B] (per-expert relative offsets).
-// Histograms and scans use the whole workgroup; the order-dependent scatter is
-// one wave walking LDS-resident keys 64 at a time, each lane's rank among the
-// lanes of equal key coming from one ballot per distinct key in the wave.
+// Histograms and scans use the whole workgroup; the order-dependent scatter
+// splits each LDS-resident tile of keys into 16 consecutive segments, one per
+// wave, starting from per-wave counters (the cross-wave exclusive sums of
+// per-wave histograms), each lane's rank among the lanes of equal key coming
+// from one ballot per distinct key in the wave.  When E*B bins do not fit the
+// per-wave histograms, the workgroup sorts by e alone and moe_route_rows forms
+// the rows, one wave per expert.
 struct RouteArgs {
   const int64_t* index;  // (N, k)
   int64_t n, k, experts, batch, tokens;
@@ -269,6 +273,7 @@ __device__ __forceinline__ void route_ranks(bool ok, int key, uint64_t lt, int& 
 // The ordered scatter of one wave over keys[beg, end) of the tile starting at
 // entry t0, advancing the running counters n1 (by expert) and n2 (by expert
 // and sample).
+template <bool kRows>
 __device__ __forceinline__ void route_scatter(const RouteArgs& a, const int32_t* keys, uint32_t t0, uint32_t beg,
                                               uint32_t end, int32_t* n1, int32_t* n2, const int32_t* o1) {
   const int lane = threadIdx.x & 63;
@@ -278,21 +283,23 @@ __device__ __forceinline__ void route_scatter(const RouteArgs& a, const int32_t*
     const int32_t kk = i < end ? keys[i] : -1;
     const bool ok = kk >= 0;
     const int e = kk & 511, e2 = kk >> 9;
-    int r1, t1, r2, t2;
+    int r1, t1, r2 = 0, t2 = 0;
     route_ranks(ok, e, lt, r1, t1);
-    route_ranks(ok, e2, lt, r2, t2);
+    if constexpr (kRows) route_ranks(ok, e2, lt, r2, t2);
     int32_t s1 = 0, s2 = 0;
     if (ok) {
       s1 = n1[e] + r1;
-      s2 = n2[e2] + r2;
+      if constexpr (kRows) s2 = n2[e2] + r2;
     }
     // every lane has read the counters before the last lane of each key bumps them
     __builtin_amdgcn_wave_barrier();
     if (ok) {
       a.entries[s1] = (int32_t)(t0 + i);
-      a.rows[s2] = s1 - o1[e];  // expert-local routed row
       if (r1 == t1 - 1) n1[e] = s1 + 1;
-      if (r2 == t2 - 1) n2[e2] = s2 + 1;
+      if constexpr (kRows) {
+        a.rows[s2] = s1 - o1[e];  // expert-local routed row
+        if (r2 == t2 - 1) n2[e2] = s2 + 1;
+      }
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -370,18 +377,20 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
       for (int j = 0; j < 8; ++j)
         if (i0 + (uint32_t)(kRouteThreads * j) < nt) keys[i0 + kRouteThreads * j] = kk[j];
     }
-    if (per_wave) {
-      // wave w takes keys [w*seg, (w+1)*seg) of the tile, in order
+    {
+      // wave w takes keys [w*seg, (w+1)*seg) of the tile, in order; the
+      // (expert, sample) counters only when they fit (per_wave)
       const uint32_t segl = (nt + kRouteWaves - 1) / kRouteWaves;
       for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) (&h1[0][0])[(i / E) * kMaxExperts + i % E] = 0;
-      for (int i = tid; i < kRouteWaves * nb2; i += kRouteThreads) (&h2[0][0])[(i / nb2) * kRouteWaveBins + i % nb2] = 0;
+      if (per_wave)
+        for (int i = tid; i < kRouteWaves * nb2; i += kRouteThreads) (&h2[0][0])[(i / nb2) * kRouteWaveBins + i % nb2] = 0;
       __syncthreads();
       const uint32_t beg = min(nt, wave * segl), end = min(nt, beg + segl);
       for (uint32_t i = beg + (tid & 63); i < end; i += 64) {
         const int32_t kk = keys[i];
         if (kk >= 0) {
           atomicAdd(&h1[wave][kk & 511], 1);
-          atomicAdd(&h2[wave][kk >> 9], 1);
+          if (per_wave) atomicAdd(&h2[wave][kk >> 9], 1);
         }
       }
       __syncthreads();
@@ -395,22 +404,62 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(RouteArgs a) {
         }
         c1[e] = run;
       }
-      for (int q = tid; q < nb2; q += kRouteThreads) {
-        int32_t run = c2[q];
-        for (int w = 0; w < kRouteWaves; ++w) {
-          const int32_t c = h2[w][q];
-          h2[w][q] = run;
-          run += c;
+      if (per_wave)
+        for (int q = tid; q < nb2; q += kRouteThreads) {
+          int32_t run = c2[q];
+          for (int w = 0; w < kRouteWaves; ++w) {
+            const int32_t c = h2[w][q];
+            h2[w][q] = run;
+            run += c;
+          }
+          c2[q] = run;
         }
-        c2[q] = run;
-      }
       __syncthreads();
-      route_scatter(a, keys, t0, beg, end, h1[wave], h2[wave], o1);
-    } else {
-      __syncthreads();
-      if (tid < 64) route_scatter(a, keys, t0, 0, nt, c1, c2, o1);
+      if (per_wave) route_scatter<true>(a, keys, t0, beg, end, h1[wave], h2[wave], o1);
+      else route_scatter<false>(a, keys, t0, beg, end, h1[wave], nullptr, o1);
     }
     __syncthreads();
+  }
+}
+
+// The rows of moe_route when E*B bins do not fit its per-wave histograms:
+// wave w of the grid takes expert e = w and walks the expert's entries (the
+// by-expert sort, routed order) 64 at a time, so rows[off2[e*B+b] + q] = r for
+// expert-local row r runs in the same order as in the one-pass form; the
+// per-sample counters start at off2[e*B+b] = off[e] + seg[e*(B+1)+b] and sit
+// in LDS (B ints per wave; up to 4 waves per workgroup, as many as keep the
+// counters within 64 KB).
+constexpr int kRowsWaves = 4;
+__global__ __launch_bounds__(kRowsWaves * 64) void moe_route_rows(RouteArgs a) {
+  extern __shared__ int32_t cnt_all[];  // (blockDim / 64) * B
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * (int)(blockDim.x >> 6) + wave;
+  const int B = (int)a.batch;
+  if (e >= a.experts) return;  // uniform per wave; no barrier below
+  int32_t* cnt = cnt_all + wave * B;
+  const int32_t o = a.offsets[e], oend = a.offsets[e + 1];
+  for (int b = lane; b < B; b += 64) cnt[b] = o + a.seg[e * (B + 1) + b];
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));  // lanes below this one
+  const uint32_t n = (uint32_t)a.n, T = (uint32_t)a.tokens;
+  for (int32_t base = o; base < oend; base += 64) {
+    const int32_t i = base + lane;
+    const bool ok = i < oend;
+    int b = 0;
+    if (ok) {
+      const uint32_t p = (uint32_t)a.entries[i];
+      b = (int)((p - (p / n) * n) / T);  // token p % N, its sample
+    }
+    int r, t;
+    route_ranks(ok, b, lt, r, t);
+    const int32_t s2 = ok ? cnt[b] + r : 0;
+    // every lane has read the counters before the last lane of each sample bumps them
+    __builtin_amdgcn_wave_barrier();
+    if (ok) {
+      a.rows[s2] = i - o;  // expert-local routed row
+      if (r == t - 1) cnt[b] = s2 + 1;
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -503,7 +552,14 @@ int da_moe_route(const int64_t* index, int64_t n_tokens, int k, int n_experts, i
   a.entries = entries;
   a.seg = seg;
   a.rows = rows;
-  moe_route_kernel<<<1, kRouteThreads, 0, (hipStream_t)stream>>>(a);
+  hipStream_t st = (hipStream_t)stream;
+  moe_route_kernel<<<1, kRouteThreads, 0, st>>>(a);
+  const int rc = check_launch(who);
+  if (rc || (int64_t)n_experts * batch <= kRouteWaveBins) return rc;
+  // the rows, one wave per expert, when the (expert, sample) bins exceed the per-wave histograms
+  const int waves = batch <= 4096 ? kRowsWaves : 2;  // batch <= 8192: at most 64 KB of counters
+  const unsigned blocks = (unsigned)((n_experts + waves - 1) / waves);
+  moe_route_rows<<<blocks, waves * 64, (size_t)waves * batch * sizeof(int32_t), st>>>(a);
   return check_launch(who);
 }
 

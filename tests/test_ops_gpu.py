@@ -525,7 +525,10 @@ def test_c1_token_granularity(device, normalized):
 
 
 @pytest.mark.parametrize("batch,tokens,n_exp,k", [(16, 256, 8, 2), (3, 37, 5, 3), (1, 64, 4, 1),
-                                                    (64, 300, 64, 4), (8, 1024, 256, 2), (32, 512, 8, 2)])
+                                                    (64, 300, 64, 4), (8, 1024, 256, 2), (32, 512, 8, 2),
+                                                    # over 1024 (expert, sample) bins: rows one wave per expert
+                                                    (16, 256, 128, 8), (4, 64, 256, 8), (4096, 2, 2, 1),
+                                                    (8192, 1, 1, 1)])
 def test_route_segments_matches_per_expert_sorts(device, ops, batch, tokens, n_exp, k):
     """One-launch routing == router top-k -> per-expert torch.where order ->
     per-expert stable sort by sample, bit for bit."""
@@ -549,12 +552,12 @@ def test_route_segments_matches_per_expert_sorts(device, ops, batch, tokens, n_e
         assert torch.equal((ent // n).cpu(), slot.cpu()) and torch.equal((ent % n).cpu(), tok.cpu())
 
 
-def test_route_drops_out_of_range_experts(device):
+@pytest.mark.parametrize("batch,tokens,n_exp,k", [(5, 41, 6, 2), (40, 9, 30, 3)])
+def test_route_drops_out_of_range_experts(device, batch, tokens, n_exp, k):
     """Entries whose expert index is outside [0, n_experts) are dropped; the
     rest keep the slot-major, token-ascending order, grouped by sample."""
     from dattri_llm_amd import kernels
 
-    batch, tokens, n_exp, k = 5, 41, 6, 2
     n = batch * tokens
     gen = torch.Generator().manual_seed(7)
     idx = torch.randint(-2, n_exp + 2, (n, k), generator=gen, dtype=torch.int64)
