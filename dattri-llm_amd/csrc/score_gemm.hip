@@ -8,11 +8,13 @@
 // launch with fp32 accumulation throughout.
 //
 // The product is skinny (B1, B2 in the tens, widths up to 10^8) and bound by
-// streaming both operands from HBM once.  The flattened width of every layer
-// is cut into chunks; a workgroup owns one chunk of one layer for a 16-row x
-// 64-row (side-1 x side-2) output tile and runs 16x16x32 MFMAs straight from
-// registers (every element is used by exactly one MFMA of the tile, so there
-// is nothing to share through LDS).  In a 16x16 MFMA four lanes serve one
+// streaming both operands from HBM once.  Most launches take the streaming
+// form below (an LDS ring per output tile).  The register-fed form here takes
+// what the ring cannot address (k-blocked fp32 rows, rows past 2 GB): the
+// flattened width of every layer is cut into chunks; a workgroup owns one
+// chunk of one layer for a 16-row x 64-row (side-1 x side-2) output tile and
+// runs 16x16 MFMAs straight from registers (every element is used by exactly
+// one MFMA of the tile, so there is nothing to share through LDS).  In a 16x16 MFMA four lanes serve one
 // row; they read 64 contiguous bytes of it per load instruction, and the same
 // element-to-k assignment is used on both sides, so the sum is exact in any
 // order.  The four waves split the chunk, combine through LDS and write one
@@ -145,7 +147,11 @@ __global__ __launch_bounds__(kThreads) void score_gemm_chunks(ScoreArgs s) {
 // other tiles (a 4096 x 128 output re-reads each query row per 16-row tile)
 // keep the default policy, which leaves them in L2.
 // Rows past a side's end and bytes past a layer's width read as zero.  Wave w
-// loads block w of every stage and multiplies it: 2 x 4 16x16x32 MFMAs.  LDS
+// loads block w of every stage and multiplies it: 2 x 4 16x16 MFMA steps
+// (one 16x16x32 MFMA for 2-byte rows, four 16x16x4 for fp32 rows: the lane's
+// 16 bytes are four k-slots, paired the same way on both sides).  Each DMA
+// instruction's buffer base is the unit's first block of its own 8 rows, so
+// only 8 rows' offsets need fit the 32-bit per-lane offset.  LDS
 // row r of a block holds logical 16-byte chunk c in slot c ^ ((r/2) % 8): the
 // 16 rows of a fragment, 128 bytes apart, then hit 16 distinct bank groups.
 // ---------------------------------------------------------------------------
@@ -197,14 +203,14 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring(RingArgs a) {
   // DMA instruction i of wave w: LDS rows 8i .. 8i+7 of block w (rows < 16:
   // side 1, row tm*16 + r; else side 2, row tn*64 + r - 16); lane l -> row
   // 8i + l/8, slot l%8 holding chunk (l%8) ^ ((row/2) % 8).
-  int rowv[sr::kDma];
+  bool rlive[sr::kDma];
   uint32_t cbo[sr::kDma];
 #pragma unroll
   for (int i = 0; i < sr::kDma; ++i) {
     const int r = 8 * i + (lane >> 3);
     cbo[i] = 16u * (uint32_t)((lane & 7) ^ ((r >> 1) & 7));
     const int64_t row = i < 2 ? tm * kTileM + r : tn * kTileN + r - kTileM;  // row of its side
-    rowv[i] = row < (i < 2 ? a.b1 : a.b2) ? (i < 2 ? r : r - kTileM) : -1;      // row of the tile, or dead
+    rlive[i] = row < (i < 2 ? a.b1 : a.b2);
   }
   // issue cursor: layer il, unit iu of the layer, and the layer's per-lane offsets
   int il = 0;
@@ -212,35 +218,38 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring(RingArgs a) {
   int64_t iu = uniform64(ub - a.layers[il].u0);
   uint32_t roff[sr::kDma];
   uint32_t lbytes = 0;
-  int64_t lunits = 0, blk1 = 0, blk2 = 0;
+  int64_t lunits = 0, blk1 = 0, blk2 = 0, ld1 = 0, ld2 = 0;
   const char* m1 = nullptr;  // the tile's first row of each side
   const char* m2 = nullptr;
   auto set_layer = [&]() __attribute__((always_inline)) {
     const RingLayer& Ly = a.layers[il];
     m1 = Ly.m1 + tm * kTileM * Ly.ld1;
     m2 = Ly.m2 + tn * kTileN * Ly.ld2;
+    ld1 = Ly.ld1;
+    ld2 = Ly.ld2;
     blk1 = Ly.blk1;
     blk2 = Ly.blk2;
     lbytes = (uint32_t)min(Ly.bytes, (int64_t)0x7fffffff);
     lunits = Ly.units;
 #pragma unroll
     for (int i = 0; i < sr::kDma; ++i)
-      roff[i] = rowv[i] < 0 ? sr::kOob
-                            : (uint32_t)(rowv[i] * (i < 2 ? Ly.ld1 : Ly.ld2) + uwave * (i < 2 ? Ly.blk1 : Ly.blk2)) + cbo[i];
+      roff[i] = rlive[i] ? (uint32_t)((lane >> 3) * (i < 2 ? Ly.ld1 : Ly.ld2) + uwave * (i < 2 ? Ly.blk1 : Ly.blk2)) + cbo[i]
+                         : sr::kOob;
   };
   auto issue = [&](int slot, bool live, bool more) __attribute__((always_inline)) {
-    // the unit's first block of every row is the resource base; block w, chunk, row are per-lane offsets
-    const u32x4 r1 = uniform4(make_rsrc(m1 + iu * 4 * blk1, 0x7fffffffu));
-    const u32x4 r2 = uniform4(make_rsrc(m2 + iu * 4 * blk2, 0x7fffffffu));
+    // Each instruction's resource base is the unit's first block of its first
+    // row, so per-lane offsets (row within the 8, block w, chunk) span 8 rows.
     const uint32_t kin = (uint32_t)iu * sr::kUnitB + (uint32_t)uwave * sr::kBlkB;  // byte of the layer row
     const uint32_t dst0 = lds0 + (uint32_t)(slot * sr::kStage + uwave * sr::kRows * sr::kBlkB);
 #pragma unroll
     for (int i = 0; i < sr::kDma; ++i) {
+      const u32x4 rs = uniform4(make_rsrc(i < 2 ? m1 + 8 * i * ld1 + iu * 4 * blk1 : m2 + 8 * (i - 2) * ld2 + iu * 4 * blk2,
+                                          0x7fffffffu));
       const bool en = live & (roff[i] != sr::kOob) & (kin + cbo[i] < lbytes);
       if (i < 2 ? a.nt1 : a.nt2)
-        dma16_nt(i < 2 ? r1 : r2, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
+        dma16_nt(rs, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
       else
-        dma16(i < 2 ? r1 : r2, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
+        dma16(rs, dst0 + (uint32_t)(8 * i * sr::kBlkB), en ? roff[i] : sr::kOob);
     }
     if (live && ++iu == lunits) {
       iu = 0;
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring(RingArgs a) {
 // the ring.  Wave w loads LDS rows 64 (w % 2) .. +63 of block w / 2 (side 1
 // for w even, side 2 for w odd: 8 instructions of 8 rows) and multiplies
 // output rows 32 (w % 2) .. +31 of block w / 2 against all 64 side-2 rows
-// (2 x 4 16x16x32 MFMAs per k-step, two k-steps per block); the two blocks'
+// (2 x 4 16x16 MFMA steps per k-step, two k-steps per block); the two blocks'
 // partial tiles are added in block order at the end.  Block rows keep the
 // swizzle c ^ ((row/2) % 8).
 namespace sr64 {
@@ -336,7 +345,7 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring64(RingArgs a) {
   // DMA instruction i: LDS rows 64 hw + 8i .. +7 of block bw; lane l -> row
   // 64 hw + 8i + l/8 (side 1 row tm*64 + r, or side 2 row tn*64 + r - 64),
   // slot l%8 holding chunk (l%8) ^ ((row/2) % 8).
-  int rowv[sr64::kDma];
+  bool rlive[sr64::kDma];
   uint32_t cbo[sr64::kDma];
 #pragma unroll
   for (int i = 0; i < sr64::kDma; ++i) {
@@ -344,7 +353,7 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring64(RingArgs a) {
     cbo[i] = 16u * (uint32_t)((lane & 7) ^ ((r >> 1) & 7));
     const int rl = r - 64 * hw;  // row within its side's tile
     const int64_t row = hw == 0 ? tm * sr64::kTM + rl : tn * sr64::kTN + rl;
-    rowv[i] = row < (hw == 0 ? a.b1 : a.b2) ? rl : -1;
+    rlive[i] = row < (hw == 0 ? a.b1 : a.b2);
   }
   const bool nt = hw == 0 ? a.nt1 : a.nt2;  // uniform
   int il = 0;
@@ -352,26 +361,27 @@ __global__ __launch_bounds__(kThreads, 1) void score_ring64(RingArgs a) {
   int64_t iu = uniform64(ub - a.layers[il].u0);
   uint32_t roff[sr64::kDma];
   uint32_t lbytes = 0;
-  int64_t lunits = 0, blk = 0;
+  int64_t lunits = 0, blk = 0, ld = 0;
   const char* mb = nullptr;  // this wave's side: the tile's first row
   auto set_layer = [&]() __attribute__((always_inline)) {
     const RingLayer& Ly = a.layers[il];
-    const int64_t ld = hw == 0 ? Ly.ld1 : Ly.ld2;
+    ld = hw == 0 ? Ly.ld1 : Ly.ld2;
     blk = hw == 0 ? Ly.blk1 : Ly.blk2;
     mb = hw == 0 ? Ly.m1 + tm * sr64::kTM * Ly.ld1 : Ly.m2 + tn * sr64::kTN * Ly.ld2;
     lbytes = (uint32_t)min(Ly.bytes, (int64_t)0x7fffffff);
     lunits = Ly.units;
 #pragma unroll
     for (int i = 0; i < sr64::kDma; ++i)
-      roff[i] = rowv[i] < 0 ? sr64::kOob : (uint32_t)(rowv[i] * ld + bw * blk) + cbo[i];
+      roff[i] = rlive[i] ? (uint32_t)((lane >> 3) * ld + bw * blk) + cbo[i] : sr64::kOob;
   };
   auto issue = [&](int slot, bool live, bool more) __attribute__((always_inline)) {
-    const u32x4 rs = uniform4(make_rsrc(mb + iu * 2 * blk, 0x7fffffffu));
+    // instruction i's resource base: the unit's first block of row 8i (per-lane offsets span 8 rows)
     const uint32_t kin = (uint32_t)iu * sr64::kUnitB + (uint32_t)bw * sr64::kBlkB;
     const uint32_t dst0 = lds0 + (uint32_t)(slot * sr64::kStage + bw * sr64::kRows * sr64::kBlkB +
                                             64 * hw * sr64::kBlkB);
 #pragma unroll
     for (int i = 0; i < sr64::kDma; ++i) {
+      const u32x4 rs = uniform4(make_rsrc(mb + 8 * i * ld + iu * 2 * blk, 0x7fffffffu));
       const bool en = live & (roff[i] != sr64::kOob) & (kin + cbo[i] < lbytes);
       if (nt)
         dma16_nt(rs, dst0 + (uint32_t)(8 * i * sr64::kBlkB), en ? roff[i] : sr64::kOob);
@@ -486,10 +496,15 @@ int reduce_partials(const float* partial, int64_t n, int64_t b1, int64_t b2, flo
   return check_launch("da_score_gemm(reduce)");
 }
 
+// Stride between consecutive 128-byte blocks of a ring row, in bytes: a
+// 64-element block of a 2-byte row is one 128-byte run at block stride blk
+// (0: contiguous); 4-byte rows take the ring only when contiguous.
+int64_t ring_block_stride(int64_t blk, int64_t es) { return es == 4 ? 128 : (blk ? blk : 64) * es; }
+
 struct Plan {
   int64_t chunk_bytes, n_chunks;
   size_t ws;
-  bool ring;              // streaming form (2-byte dtypes, offsets within a tile fit 32 bits)
+  bool ring;              // streaming form (128-byte blocks at a fixed stride, offsets within 8 rows fit 32 bits)
   bool tall;              // its 64 x 64 tile (side 1 taller than one 16-row tile), else 16 x 64
   int64_t units, nwg;     // its units and workgroups per tile
 };
@@ -526,10 +541,12 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
   for (int l = 0; l < n_layers; ++l) n += (layers[l].width * es + cb - 1) / cb;
   p->n_chunks = n;
   p->ws = (size_t)(n * b1 * b2) * sizeof(float);
-  // Streaming form: 2-byte dtypes (a 64-element block is one 128-byte run);
-  // per-lane offsets within one tile and the row widths fit 32 bits.
+  // Streaming form: rows whose 128-byte blocks sit a fixed stride apart --
+  // every 2-byte layout (a 64-element block is one 128-byte run) and
+  // contiguous 4-byte rows; the per-lane offsets within 8 rows and the row
+  // widths fit 32 bits.
   const int64_t lim = (1LL << 31) - (1LL << 20);
-  p->ring = es == 2 && b1 > 0 && b2 > 0;
+  p->ring = (es == 2 || es == 4) && b1 > 0 && b2 > 0;
   p->tall = b1 > kTileM;
   const int64_t unit_b = p->tall ? sr64::kUnitB : sr::kUnitB;
   const int64_t tile_m = p->tall ? sr64::kTM : kTileM;
@@ -537,8 +554,9 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
   for (int l = 0; l < n_layers && p->ring; ++l) {
     const da_dense_layer& L = layers[l];
     const int64_t bytes = L.width * es, ld1 = L.ld1 * es, ld2 = L.ld2 * es;
-    const int64_t bk1 = (L.blk1 ? L.blk1 : 64) * es, bk2 = (L.blk2 ? L.blk2 : 64) * es;
-    if (bytes >= lim || (kTileN - 1) * ld1 + 4 * bk1 >= lim || (kTileN - 1) * ld2 + 4 * bk2 >= lim) p->ring = false;
+    if (es == 4 && ((L.blk1 && L.blk1 != 64) || (L.blk2 && L.blk2 != 64))) p->ring = false;
+    const int64_t bk1 = ring_block_stride(L.blk1, es), bk2 = ring_block_stride(L.blk2, es);
+    if (bytes >= lim || 7 * ld1 + 4 * bk1 >= lim || 7 * ld2 + 4 * bk2 >= lim) p->ring = false;
     units += (bytes + unit_b - 1) / unit_b;
   }
   if (p->ring && units > 0) {
@@ -585,8 +603,8 @@ int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers
       Ly.bytes = layers[l].width * es;
       Ly.ld1 = layers[l].ld1 * es;
       Ly.ld2 = layers[l].ld2 * es;
-      Ly.blk1 = (layers[l].blk1 ? layers[l].blk1 : 64) * es;
-      Ly.blk2 = (layers[l].blk2 ? layers[l].blk2 : 64) * es;
+      Ly.blk1 = ring_block_stride(layers[l].blk1, es);
+      Ly.blk2 = ring_block_stride(layers[l].blk2, es);
       const int64_t unit_b = p.tall ? sr64::kUnitB : sr::kUnitB;
       Ly.units = (Ly.bytes + unit_b - 1) / unit_b;
       Ly.u0 = u;
@@ -606,12 +624,14 @@ int run_plan(const Plan& p, int64_t b1, int64_t b2, const da_dense_layer* layers
     if (p.tall) {
       switch (dtype) {
         case DA_BF16: score_ring64<DA_BF16><<<grid, kThreads, 0, st>>>(r); break;
-        default: score_ring64<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+        case DA_F16: score_ring64<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+        default: score_ring64<DA_F32><<<grid, kThreads, 0, st>>>(r); break;
       }
     } else {
       switch (dtype) {
         case DA_BF16: score_ring<DA_BF16><<<grid, kThreads, 0, st>>>(r); break;
-        default: score_ring<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+        case DA_F16: score_ring<DA_F16><<<grid, kThreads, 0, st>>>(r); break;
+        default: score_ring<DA_F32><<<grid, kThreads, 0, st>>>(r); break;
       }
     }
     rc = check_launch("da_score_gemm(ring)");

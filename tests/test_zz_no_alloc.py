@@ -85,17 +85,19 @@ def test_noalloc_accumulates_like_workspace_entry(device):
 
 
 def test_noalloc_rejects_problems_beyond_its_scratch(device):
-    """fp32 operands keep one partial per 1 KB width chunk and output: 512 x 512
-    outputs of width 4096 need 16 MiB of partials, more than the scratch
-    holds.  The call fails before any launch and leaves out untouched."""
+    """Every output keeps at least one fp32 partial per workgroup of its tile:
+    2048 x 2048 outputs need 16 MiB of partials at one workgroup per tile,
+    more than the scratch holds.  The call fails before any launch and leaves
+    out untouched."""
     nat, lib = _lib()
-    pairs = _pairs(512, 512, [4096], torch.float32, device, seed=3)
+    n = 2048
+    pairs = _pairs(n, n, [64], torch.float32, device, seed=3)
     arr = _layer_array(nat, pairs)
     nbytes = ctypes.c_size_t(0)
-    nat.check(lib.da_score_gemm_workspace(512, 512, arr, 1, nat.DA_F32, ctypes.byref(nbytes)), "workspace")
+    nat.check(lib.da_score_gemm_workspace(n, n, arr, 1, nat.DA_F32, ctypes.byref(nbytes)), "workspace")
     assert nbytes.value > 8 << 20
-    out = torch.full((512, 512), 3.0, device=device)
-    status = lib.da_score_gemm_noalloc(512, 512, arr, 1, nat.DA_F32, out.data_ptr(), 512, 1, 0,
+    out = torch.full((n, n), 3.0, device=device)
+    status = lib.da_score_gemm_noalloc(n, n, arr, 1, nat.DA_F32, out.data_ptr(), n, 1, 0,
                                        torch.cuda.current_stream(device).cuda_stream)
     assert status == nat.DA_ERR_WORKSPACE
     assert b"scratch" in lib.da_last_error()
