@@ -221,6 +221,33 @@ def test_score_gemm_blocked_operands(device, dtype, b1):
     assert_parity(got_t, oracle.score_gemm(m2s, m1s), dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("b1", [8, 64])
+def test_score_gemm_wide_row_strides(device, dtype, b1):
+    """Layers sliced out of 64 MiB rows: 63 row strides exceed a 32-bit buffer
+    offset, so the rings give every DMA instruction its own base (8 rows of
+    offsets).  b1 = 8 takes the 16 x 64 tile, b1 = 64 the 64 x 64 tile."""
+    from dattri_llm_amd import kernels
+
+    ld = (64 << 20) // torch.tensor([], dtype=dtype).element_size()
+    gen = torch.Generator().manual_seed(31 + b1)
+    widths = [4096, 136]
+    m1s = [_rand(gen, b1, w, dtype=dtype) for w in widths]
+    m2s = [_rand(gen, 64, w, dtype=dtype) for w in widths]
+    buf1 = torch.empty(b1, ld, dtype=dtype, device=device)
+    buf2 = torch.empty(64, ld, dtype=dtype, device=device)
+    pairs, off = [], 0
+    for m1, m2, w in zip(m1s, m2s, widths):
+        buf1[:, off:off + w] = m1.to(device)
+        buf2[:, off:off + w] = m2.to(device)
+        pairs.append((buf1[:, off:off + w], buf2[:, off:off + w]))
+        off += w
+    print(f"score_gemm wide strides b1={b1} dtype={dtype} ld={ld}", flush=True)
+    got = kernels.score_gemm(pairs)
+    assert_parity(got, oracle.score_gemm([_np(m) for m in m1s], [_np(m) for m in m2s]), dtype)
+    del buf1, buf2
+
+
 PROJ_CASES = [
     # (b, t, k, d, ka, kg, bias, dtype, seq_first)
     (3, 300, 200, 136, 24, 40, True, torch.bfloat16, False),   # 3 chunks, ragged; widths not whole stages
