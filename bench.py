@@ -49,10 +49,11 @@ for _p in (os.path.join(REPO, "dattri-llm_amd"), REPO):
 METRIC = "train×query pair-scores/sec (Llama-8B-shaped block, bf16); MFMA util % of peak"
 PEAK_BF16_TFLOPS = 2500.0
 # C4: train blocks scored per pass over the dense query block (score_sources' train_blocks_per_pass).
-# The 64 query rows are read once per 8 blocks (64 train rows, four 16-row tiles of the score ring
-# sharing them through L2): 1.26-1.32 ms of score per block against 1.56-1.58 with 4 blocks per
-# pass; groups of 10 or 20 blocks measured slower (1.96 ms).
-PASS = 8
+# The 64 query rows are read once per 16 blocks: 128 train rows, two 64 x 64 tiles of the score ring
+# whose workgroups stream the query rows in step on the same XCDs. Score per block: 0.76-0.79 ms
+# against 1.01-1.10 with 8 blocks per pass (+3-5% pair-scores/s on the same box). 24 blocks need
+# more dense rows than the default cache budget holds beside the queries.
+PASS = 16
 PEAK_HBM_GBS = 8000.0
 
 D_MODEL, D_KV, D_FFN = 4096, 1024, 14336
@@ -413,7 +414,7 @@ def bench_block(args):
         "data": "synthetic",
         "config": {
             "workload": "llama3-8b-block: 8 train x 2048 tok vs 64 query x 512 tok, 7 linears + 2 RMSNorm, "
-                        "TracInAttributor.attribute_sources (cost-rule routing per layer; 8 train blocks "
+                        "TracInAttributor.attribute_sources (cost-rule routing per layer; 16 train blocks "
                         "per pass over the dense queries)",
             "train_block": [n_train, t_train],
             "train_blocks_per_query_pass": PASS,
@@ -1323,7 +1324,7 @@ def bench_copy(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # 32 timed steps after 8 warmup: whole groups of the block workload's 8 train blocks per query pass
+    # 32 timed steps after 8 warmup: whole groups of the block workload's 16 train blocks per query pass
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", choices=["block", "ghost", "per_token", "project", "moe", "kfac", "capture",

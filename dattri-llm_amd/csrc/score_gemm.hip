@@ -565,6 +565,12 @@ int make_plan(int64_t b1, int64_t b2, const da_dense_layer* layers, int n_layers
     if (rc) return rc;
     const int64_t tiles = ((b1 + tile_m - 1) / tile_m) * ((b2 + kTileN - 1) / kTileN);
     int64_t nwg = slots / tiles;
+    // Workgroup w of every tile takes the same units at the same time; with
+    // nwg a multiple of the 8 XCDs they also share an XCD (workgroups go to
+    // the XCDs round-robin), so the rows the tiles have in common come from
+    // that XCD's L2 once (3 tiles of 64 x 64 at 85 workgroups each read the
+    // shared side three times).
+    if (tiles > 1 && nwg > 8) nwg -= nwg % 8;
     if (nwg < 1) nwg = 1;
     if (nwg > units) nwg = units;
     p->units = units;

@@ -406,3 +406,21 @@ def test_train_blocks_per_pass_is_capped_by_the_budget():
                             dense_group=group, cache_budget=CacheBudget(limit_bytes=room))
         assert torch.allclose(got[0], want[0], atol=1e-5) and got[1:4] == want[1:4]
         assert seen == sizes, (room, seen)
+
+
+def test_budget_capped_groups_fill_whole_score_tiles():
+    """A group the budget cuts short is cut to whole 64-row score tiles (or to
+    one tile); a group the caller asked for is kept as asked."""
+    from types import SimpleNamespace
+
+    from dattri_llm_amd.attribution.utils import group_limit, whole_tile_group
+    from dattri_llm_amd.utils.cache import CacheBudget
+
+    assert [whole_tile_group(n, 8) for n in (1, 8, 9, 12, 17, 23, 24, 31)] == [1, 8, 8, 8, 16, 16, 24, 24]
+    assert whole_tile_group(30, 3) == 21          # 64 / gcd(3, 64) = 64 blocks per whole tile: one tile
+    assert whole_tile_group(5, 100) == 5          # a block taller than a tile
+    assert whole_tile_group(7, 16) == 4           # 4 blocks per tile
+    block = SimpleNamespace(materialized_nbytes=1000, batch_size=8)
+    assert group_limit(block, 32, CacheBudget(limit_bytes=17_500)) == 16
+    assert group_limit(block, 12, CacheBudget(limit_bytes=1 << 40)) == 12
+    assert group_limit(block, 32, CacheBudget(limit_bytes=500)) == 1
