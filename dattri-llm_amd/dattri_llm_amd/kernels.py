@@ -518,9 +518,10 @@ def dense_per_token(
 # FactorSide as a numpy record, so a grouped launch's side arrays are filled
 # column by column instead of one ctypes structure per group (a launch may
 # carry hundreds of groups: the experts of an MoE layer, a depthwise conv).
+# numpy record with FactorSide's layout (field names, offsets and size taken from the ctypes struct)
+_CTYPE_FORMAT = {ctypes.c_void_p: "<u8", ctypes.c_int64: "<i8", ctypes.c_int32: "<i4"}
 _SIDE_RECORD = np.dtype({"names": [f for f, _t in nat.FactorSide._fields_],
-                         "formats": ["<u8", "<u8", "<i8", "<i8", "<i8", "<i8", "<i8", "<i8", "<u8", "<u8", "<i4",
-                                     "<i4"],
+                         "formats": [_CTYPE_FORMAT[t] for _f, t in nat.FactorSide._fields_],
                          "offsets": [getattr(nat.FactorSide, f).offset for f, _t in nat.FactorSide._fields_],
                          "itemsize": ctypes.sizeof(nat.FactorSide)})
 

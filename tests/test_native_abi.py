@@ -97,3 +97,21 @@ def test_argument_checks_fail_before_any_gpu_work():
     st = lib.da_project_outer(X, X, bf, 2, 16, 64, 64, 1024, 64, 1024, 64, X, 65, 64, None, X, 64, 64,
                               OUT, f32, 65 * 64, None, 0, None)
     check(st, _native.DA_ERR_UNSUPPORTED, ["projected widths"])
+
+
+def test_grouped_side_record_has_the_struct_layout():
+    """The numpy records the grouped launches fill read back field for field
+    through the ctypes mirror of da_factor_side."""
+    import numpy as np
+
+    from dattri_llm_amd import _native as nat
+    from dattri_llm_amd import kernels
+
+    assert kernels._SIDE_RECORD.itemsize == ctypes.sizeof(nat.FactorSide)
+    rec = np.zeros(2, dtype=kernels._SIDE_RECORD)
+    for i, (name, _t) in enumerate(nat.FactorSide._fields_):
+        rec[name] = [1000 * (i + 1) + 1, 1000 * (i + 1) + 2]
+    sides = (nat.FactorSide * 2).from_buffer(rec)
+    for j in range(2):
+        for i, (name, _t) in enumerate(nat.FactorSide._fields_):
+            assert getattr(sides[j], name) == 1000 * (i + 1) + 1 + j, name
