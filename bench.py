@@ -1184,10 +1184,10 @@ def bench_store(args):
         "data": "synthetic",
         "config": {"workload": "attribute from a memmap store: 32768 train x 128 query, 3 layers x 4096 "
                                "(64x64 LoGRA blocks) bf16, 64 files of 512; store in the page cache"},
-        "roofline": {"bound": "hbm", "kernel": "da_score_gemm (score_ring + reduce), one 4096-row train batch",
+        "roofline": {"bound": "hbm", "kernel": "da_score_gemm (score_ring64 + reduce), one 4096-row train batch",
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": profiled_traffic("score_ring", STORE_TRAFFIC),
+                     "traffic": profiled_traffic("score_ring64", STORE_TRAFFIC),
                      "traffic_source": os.path.relpath(STORE_TRAFFIC, REPO),
                      "work_per_launch": f"{launch_bytes:.4g} B = (4096 + 128) x 3 x 4096 x 2 B",
                      "launch_ms": round(t_score, 4), "launches_per_step": files // 8},

@@ -43,12 +43,12 @@ def test_refuses_without_a_gpu():
 # figure is not byte-bound)
 TRAFFIC = [
     ("materialize_tiles_tr8", "TRAFFIC_PROFILE", None),  # MFMA-bound: the bytes the L2 side moves
-    ("score_ring64", "TRAFFIC_PROFILE", (64 + 64) * 218_112_000 * 2.0),
+    ("score_ring64", "TRAFFIC_PROFILE", (128 + 64) * 218_112_000 * 2.0),  # 16 train blocks of 8 per pass
     ("ghost_gram_tiles_v3", "GHOST_TRAFFIC", None),
     ("da_project_outer", "PROJECT_TRAFFIC", 640 * 128 * (4096 + 11008) * 2.0),
     ("ghost_grouped_tiles_v3", "MOE_TRAFFIC", None),
     ("da_project_outer", "CAPTURE_TRAFFIC", None),
-    ("score_ring", "STORE_TRAFFIC", None),
+    ("score_ring64", "STORE_TRAFFIC", (4096 + 128) * 3 * 4096 * 2.0),
     ("materialize_tiles_tr", "KFAC_TRAFFIC", None),
 ]
 
