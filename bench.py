@@ -13,7 +13,8 @@ kernels a step launches are
 
     RMSNorm per-sample weight grads  (norm kernel, x2)
     per-sample dW of the 7 linears   (materialize kernel, x7)
-    one multi-layer score GEMM       (score kernel: 9 layers, 8 x 64)
+    a share of one multi-layer score GEMM (score kernel: 9 layers; sixteen
+    train blocks share one pass over the queries, 128 x 64 per launch)
 
 and the block's (8, 64) scores are copied to pinned host memory.  Inputs are
 synthetic (seeded on the device) and already resident in HBM; the query block
