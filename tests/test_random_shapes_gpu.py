@@ -150,3 +150,79 @@ def test_project_outer_random_shapes(device, seed):
         ap, gp = a.double() @ pin.double().T, g.double() @ pout.double().T
         ref = torch.bmm(gp.transpose(1, 2).contiguous(), ap).reshape(b, -1)
         assert _rel(got, ref) <= TOL, (dt, b, t, k, d, ka, kg)
+
+
+@pytest.mark.parametrize("seed", [61, 62, 63])
+def test_ghost_per_token_random_shapes(device, seed):
+    """K[i, t, j] = sum_s (a1_it . a2_js + bias)(g1_it . g2_js), widths at any
+    element count (the wrapper pads rows to whole 16-byte chunks)."""
+    from dattri_llm_amd import kernels
+
+    for rng, dt in _cases(seed, 12):
+        b1, b2, t1, t2 = rng.randint(1, 6), rng.randint(1, 6), rng.randint(1, 300), rng.randint(1, 300)
+        k, d = rng.randint(1, 300), rng.randint(1, 300)
+        bias = rng.random() < 0.3
+        a1, g1 = _rnd(device, b1, t1, k, dt=dt), _rnd(device, b1, t1, d, dt=dt)
+        a2, g2 = _rnd(device, b2, t2, k, dt=dt), _rnd(device, b2, t2, d, dt=dt)
+        print(f"per-token seed={seed} {dt} {b1}x{b2} T={t1}/{t2} K={k} D={d} bias={bias}", flush=True)
+        got = kernels.ghost_gram_per_token(a1, g1, a2, g2, bias=bias)
+        ka = a1.double().reshape(b1 * t1, k) @ a2.double().reshape(b2 * t2, k).T
+        kg = g1.double().reshape(b1 * t1, d) @ g2.double().reshape(b2 * t2, d).T
+        ref = ((ka + float(bias)) * kg).reshape(b1, t1, b2, t2).sum(-1)
+        assert got.shape == (b1, t1, b2)
+        assert _rel(got, ref) <= TOL, (dt, b1, b2, t1, t2, k, d, bias)
+
+
+def _segments(rng, device, batch, rows):
+    """Random non-decreasing per-sample offsets over at most ``rows`` packed
+    rows (int32, B+1 entries) and, half the time, a random row index into
+    ``rows`` physical rows."""
+    cuts = sorted(rng.randint(0, rows) for _ in range(batch - 1))
+    end = rng.randint(cuts[-1] if cuts else 0, rows)
+    seg = torch.tensor([0, *cuts, end], dtype=torch.int32, device=device)
+    idx = None
+    if rng.random() < 0.5:
+        idx = torch.tensor(rng.sample(range(rows), rows), dtype=torch.int32, device=device)
+    return seg, idx
+
+
+@pytest.mark.parametrize("seed", [71, 72, 73])
+def test_grouped_ghost_random_segments(device, seed):
+    """Segment-summed ghost products over groups of different widths (the
+    experts of several routed layers), ragged and empty samples, with and
+    without a row index."""
+    from dattri_llm_amd import kernels
+
+    for rng, dt in _cases(seed, 6):
+        v = _vec(dt)
+        b1, b2 = rng.randint(1, 12), rng.randint(1, 12)
+        bias = rng.random() < 0.3
+        groups1, groups2, info = [], [], []
+        ref = torch.zeros(b1, b2, dtype=torch.float64, device=device)
+        for _ in range(rng.randint(1, 6)):
+            k, d = v * rng.randint(1, 40), v * rng.randint(1, 40)
+            sides = []
+            for b in (b1, b2):
+                rows = rng.randint(1, 400)
+                a, g = _rnd(device, rows, k, dt=dt), _rnd(device, rows, d, dt=dt)
+                seg, idx = _segments(rng, device, b, rows)
+                sides.append((a, g, seg, idx))
+            dws = []
+            for a, g, seg, idx in sides:
+                s = seg.tolist()
+                order = idx.long() if idx is not None else torch.arange(a.shape[0], device=device)
+                per = []
+                for i in range(len(s) - 1):
+                    r = order[s[i]:s[i + 1]]
+                    ar = a[r].double()
+                    if bias:
+                        ar = torch.cat([ar, torch.ones(ar.shape[0], 1, dtype=torch.float64, device=device)], -1)
+                    per.append((g[r].double().T @ ar).reshape(-1))
+                dws.append(torch.stack(per))
+            ref += dws[0] @ dws[1].T
+            groups1.append(sides[0])
+            groups2.append(sides[1])
+            info.append((k, d))
+        print(f"grouped seed={seed} {dt} {b1}x{b2} groups {info} bias={bias}", flush=True)
+        got = kernels.ghost_gram_grouped(groups1, groups2, bias=bias)
+        assert _rel(got, ref) <= TOL, (dt, b1, b2, info, bias)
