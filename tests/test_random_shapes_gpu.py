@@ -226,3 +226,36 @@ def test_grouped_ghost_random_segments(device, seed):
         print(f"grouped seed={seed} {dt} {b1}x{b2} groups {info} bias={bias}", flush=True)
         got = kernels.ghost_gram_grouped(groups1, groups2, bias=bias)
         assert _rel(got, ref) <= TOL, (dt, b1, b2, info, bias)
+
+
+@pytest.mark.parametrize("seed", [81, 82, 83])
+def test_route_segments_random_routings(device, seed):
+    """da_moe_route's per-expert segments against a torch CPU restatement of
+    the reference's enumeration: expert e's routed rows in slot-major, token
+    ascending order (torch.where over the one-hot mask permuted to (E, k, N)),
+    then grouped by sample, stably; random top-k sets over 1-256 experts."""
+    from dattri_llm_amd.gradient import ops
+
+    rng = random.Random(seed)
+    for _ in range(10):
+        n_exp = rng.choice([1, 2, 5, 8, 16, 60, 128, 256])
+        k = rng.randint(1, min(8, n_exp))
+        batch, tokens = rng.randint(1, min(64, 8192 // n_exp)), rng.randint(1, 128)  # E * B <= 8192 bins
+        n = batch * tokens
+        gen = torch.Generator().manual_seed(rng.randrange(1 << 30))
+        idx = torch.rand(n, n_exp, generator=gen).argsort(-1)[:, :k].contiguous()  # k distinct experts per token
+        print(f"route seed={seed} E={n_exp} k={k} B={batch} T={tokens}", flush=True)
+        got = ops.moe.route_segments(idx.to(device), n_exp, batch, tokens)
+        assert len(got) == n_exp
+        tok_all = torch.arange(n).unsqueeze(1).expand(n, k)
+        slot_all = torch.arange(k).unsqueeze(0).expand(n, k)
+        for e in range(n_exp):
+            hit = idx == e
+            p = (slot_all[hit] * n + tok_all[hit]).sort().values  # slot-major, token ascending
+            sample = (p % n) // tokens
+            seg = torch.zeros(batch + 1, dtype=torch.int64)
+            seg[1:] = torch.bincount(sample, minlength=batch).cumsum(0)
+            rows = torch.sort(sample, stable=True).indices
+            seg_g, rows_g = got[e]
+            assert torch.equal(seg_g.cpu().to(torch.int64), seg), (e, n_exp, k, batch, tokens)
+            assert torch.equal(rows_g.cpu().to(torch.int64), rows), (e, n_exp, k, batch, tokens)
