@@ -259,3 +259,54 @@ def test_route_segments_random_routings(device, seed):
             seg_g, rows_g = got[e]
             assert torch.equal(seg_g.cpu().to(torch.int64), seg), (e, n_exp, k, batch, tokens)
             assert torch.equal(rows_g.cpu().to(torch.int64), rows), (e, n_exp, k, batch, tokens)
+
+
+@pytest.mark.parametrize("seed", [91, 92])
+def test_row_dots_random_layers(device, seed):
+    """Per-row squared norms and dots summed over layers (row-major, sliced and
+    k-blocked layers mixed)."""
+    from dattri_llm_amd import kernels
+
+    for rng, dt in _cases(seed, 12):
+        v = _vec(dt)
+        b = rng.randint(1, 96)
+        layers, ref, info = [], torch.zeros(b, dtype=torch.float64, device=device), []
+        for _ in range(rng.randint(1, 5)):
+            w = v * rng.randint(1, 3000)
+            m1 = _rnd(device, b, w, dt=dt)
+            m2 = _rnd(device, b, w, dt=dt) if rng.random() < 0.5 else None
+            ref += (m1.double() * (m2 if m2 is not None else m1).double()).sum(-1)
+            if w % 64 == 0 and rng.random() < 0.4:
+                x = kernels.blocked_storage(b, w, dt, device)
+                x.copy_(m1.view(b, -1, 64))
+                m1 = x
+                if m2 is not None:
+                    y = kernels.blocked_storage(b, w, dt, device)
+                    y.copy_(m2.view(b, -1, 64))
+                    m2 = y
+            layers.append((m1, m2))
+            info.append((w, m2 is None))
+        print(f"row_dots seed={seed} {dt} B={b} {info}", flush=True)
+        assert _rel(kernels.row_dots(layers), ref) <= TOL, (dt, b, info)
+
+
+@pytest.mark.parametrize("seed", [101, 102])
+def test_embedding_cross_gram_random_ids(device, seed):
+    """sum over (t, s) with tok1[i,t] == tok2[j,s] of g1[i,t] . g2[j,s], ids
+    drawn from small and large vocabularies (many and few matches), with
+    negative (padding) ids that match nothing."""
+    from dattri_llm_amd import kernels
+
+    for rng, dt in _cases(seed, 8):
+        b1, b2, t1, t2 = rng.randint(1, 8), rng.randint(1, 8), rng.randint(1, 200), rng.randint(1, 200)
+        vocab, d = rng.choice([5, 50, 1000, 128256]), _vec(dt) * rng.randint(1, 100)
+        gen = torch.Generator().manual_seed(rng.randrange(1 << 30))
+        tok1 = torch.randint(-1, vocab, (b1, t1), generator=gen)
+        tok2 = torch.randint(-1, vocab, (b2, t2), generator=gen)
+        g1, g2 = _rnd(device, b1, t1, d, dt=dt), _rnd(device, b2, t2, d, dt=dt)
+        print(f"embedding seed={seed} {dt} {b1}x{b2} T={t1}/{t2} V={vocab} d={d}", flush=True)
+        got = kernels.embedding_cross_gram(tok1.to(device), g1, tok2.to(device), g2)
+        match = (tok1.reshape(-1, 1) == tok2.reshape(1, -1)) & (tok1.reshape(-1, 1) >= 0)
+        dots = g1.double().reshape(b1 * t1, d) @ g2.double().reshape(b2 * t2, d).T
+        ref = (dots * match.to(device)).reshape(b1, t1, b2, t2).sum((1, 3))
+        assert _rel(got, ref) <= TOL, (dt, b1, b2, t1, t2, vocab, d)
